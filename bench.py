@@ -1,0 +1,363 @@
+"""Throughput of libkk's op classes on one MI355X.
+
+A step is one pass of the reduction workload over one set of resident
+inputs: AdaIN (InstanceNorm over T, eps 1e-5, with the style Linear
+128 -> 1024 fused) on [1,512,1200] and on [1,512,9600], LayerNorm(768,
+eps 1e-12) on [1,256,768] and Softmax(last axis) on [1,12,256,256].  `value`
+is the algorithmic HBM bytes of a step divided by its time (GB/s).
+
+Timing: every step's kernels are recorded once into a HIP graph per input
+set; the timed region replays them with HIP events on libkk's stream.
+Inputs rotate over enough sets (> 512 MB) that the 256 MB Infinity Cache
+cannot serve them.  Per-op lines (elementwise set, reductions, dequant
+GEMM/conv, the decoder upsample stage) are measured the same way, one op
+per graph node.  The CPU baseline runs the numpy oracle on this host.
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = ("achieved HBM GB/s (% of peak) per op class; audio-sec per wall-sec on "
+          "Kokoro graph")
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 (vector and MFMA)
+ROTATE_BYTES = 640 << 20    # > 2x the 256 MB Infinity Cache
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Bench:
+    def __init__(self, kk):
+        self.kk = kk
+        self.lib = kk._lib
+        self.D = kk.to_device
+
+    def call(self, name, *args):
+        self.lib.call(name, *args)
+
+    def graph(self, fn):
+        """Record fn()'s launches into a HIP graph; returns its id."""
+        self.call("kk_graph_begin")
+        try:
+            fn()
+        except Exception:
+            gid = ctypes.c_int()
+            self.lib.load().kk_graph_end(ctypes.byref(gid))
+            raise
+        gid = ctypes.c_int()
+        self.call("kk_graph_end", ctypes.byref(gid))
+        return gid.value
+
+    def time_graphs(self, gids, reps):
+        """Average ms per replay of the list `gids` launched in turn."""
+        for g in gids:  # warm
+            self.call("kk_graph_launch", g)
+        self.kk.sync()
+        self.call("kk_event_record", 0)
+        for _ in range(reps):
+            for g in gids:
+                self.call("kk_graph_launch", g)
+        self.call("kk_event_record", 1)
+        ms = ctypes.c_float()
+        self.call("kk_event_elapsed", 0, 1, ctypes.byref(ms))
+        return ms.value / (reps * len(gids))
+
+    def replicate(self, t, n):
+        """n device copies of t (device-to-device)."""
+        out = [t]
+        for _ in range(n - 1):
+            c = self.kk.DeviceTensor.empty(t.shape, t.dtype)
+            self.kk.ops.copy_into(c, t)
+            out.append(c)
+        return out
+
+
+# ------------------------------------------------------------ workloads
+def reduction_inputs(seed=0):
+    """Seeded like the parity tests: x ~ N(0,1), style ~ N(0,0.1) [1,128],
+    W ~ N(0,0.05) [128,1024], b = 0; LN gamma = 1 + 0.1N, beta = 0.1N;
+    softmax input ~ N(0, std 2)."""
+    r = np.random.default_rng(seed)
+    return dict(
+        x1200=r.normal(0, 1, (1, 512, 1200)).astype(np.float32),
+        x9600=r.normal(0, 1, (1, 512, 9600)).astype(np.float32),
+        style=r.normal(0, 0.1, (1, 128)).astype(np.float32),
+        w=r.normal(0, 0.05, (128, 1024)).astype(np.float32),
+        b=np.zeros(1024, np.float32),
+        ln=r.normal(0, 1, (1, 256, 768)).astype(np.float32),
+        g=(1 + 0.1 * r.normal(0, 1, 768)).astype(np.float32),
+        beta=(0.1 * r.normal(0, 1, 768)).astype(np.float32),
+        sm=r.normal(0, 2, (1, 12, 256, 256)).astype(np.float32),
+    )
+
+
+def adain_bytes(c, t, s=128):
+    # read x, write y, read W [S,2C], style [S], bias [2C]
+    return 2 * c * t * 4 + s * 2 * c * 4 + s * 4 + 2 * c * 4
+
+
+BYTES = {
+    "adain_t1200": adain_bytes(512, 1200),
+    "adain_t9600": adain_bytes(512, 9600),
+    "layernorm_768": 2 * 256 * 768 * 4 + 2 * 768 * 4,
+    "softmax_12x256x256": 2 * 12 * 256 * 256 * 4,
+}
+STEP_BYTES = sum(BYTES.values())
+
+
+def run_gpu(args):
+    kk = importlib.import_module("best-tts-godot_amd")
+    kk.init(0)
+    B = Bench(kk)
+    D = B.D
+    host = reduction_inputs()
+    nsets = max(2, -(-ROTATE_BYTES // (2 * STEP_BYTES)))  # inputs + outputs per set
+    log(f"bench: {nsets} rotating sets x {2 * STEP_BYTES / 1e6:.1f} MB")
+    style, w, b = D(host["style"]), D(host["w"]), D(host["b"])
+    g, beta = D(host["g"]), D(host["beta"])
+    xs = {k: B.replicate(D(host[k]), nsets) for k in ("x1200", "x9600", "ln", "sm")}
+    outs = {k: [kk.DeviceTensor.empty(v[0].shape) for _ in range(nsets)] for k, v in xs.items()}
+    eps_in, eps_ln = 1e-5, 1e-12
+
+    def op_adain(k, i):
+        B.call("kk_adain", outs[k][i].desc(), xs[k][i].desc(), style.desc(), w.desc(), None, None,
+               b.desc(), eps_in)
+
+    def op_ln(i):
+        B.call("kk_layernorm", outs["ln"][i].desc(), xs["ln"][i].desc(), None, None, g.desc(),
+               beta.desc(), -1, eps_ln)
+
+    def op_sm(i):
+        B.call("kk_softmax", outs["sm"][i].desc(), xs["sm"][i].desc(), -1)
+
+    def step(i):
+        op_adain("x1200", i)
+        op_adain("x9600", i)
+        op_ln(i)
+        op_sm(i)
+
+    # One graph per input set (one step) and one graph for a whole rotation
+    # (nsets steps), so K steps cost K // nsets + K % nsets graph launches.
+    step_graphs = [B.graph(lambda i=i: step(i)) for i in range(nsets)]
+    rotation = B.graph(lambda: [step(i) for i in range(nsets)])
+
+    def run_steps(k_steps):
+        for _ in range(k_steps // nsets):
+            B.call("kk_graph_launch", rotation)
+        for k in range(k_steps % nsets):
+            B.call("kk_graph_launch", step_graphs[k])
+
+    run_steps(args.warmup)
+    kk.sync()
+    B.call("kk_event_record", 2)
+    run_steps(args.steps)
+    B.call("kk_event_record", 3)
+    kk.sync()
+    ms = ctypes.c_float()
+    B.call("kk_event_elapsed", 2, 3, ctypes.byref(ms))
+    ms_per_step = ms.value / args.steps
+    log(f"bench: step {ms_per_step * 1e3:.2f} us ({STEP_BYTES / ms_per_step / 1e6:.0f} GB/s)")
+
+    # ---- per-op lines: one graph per set, each with a single op node
+    ops_out = {}
+
+    def per_op(name, fn, nbytes=None, flops=None, reps=20, sets=nsets):
+        # one graph holding the op once per rotating set
+        gid = B.graph(lambda: [fn(i) for i in range(sets)])
+        t_ms = B.time_graphs([gid], reps) / sets
+        B.call("kk_graph_destroy", gid)
+        rec = {"us": round(t_ms * 1e3, 3)}
+        if nbytes:
+            gbs = nbytes / (t_ms * 1e-3) / 1e9
+            rec.update(bytes=nbytes, gbps=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4))
+        if flops:
+            tf = flops / (t_ms * 1e-3) / 1e12
+            rec.update(flops=flops, tflops=round(tf, 2), frac_fp32=round(tf / FP32_PEAK_TFLOPS, 4))
+        ops_out[name] = rec
+        log(f"bench: {name:<28} {json.dumps(rec)}")
+        return rec
+
+    per_op("adain_t1200", lambda i: op_adain("x1200", i), BYTES["adain_t1200"])
+    dom = per_op("adain_t9600", lambda i: op_adain("x9600", i), BYTES["adain_t9600"])
+    per_op("layernorm_768", op_ln, BYTES["layernorm_768"])
+    per_op("softmax_12x256x256", op_sm, BYTES["softmax_12x256x256"])
+
+    # elementwise set: x [1,512,2400], per-channel c, alpha
+    r = np.random.default_rng(0)
+    ex = D(r.normal(0, 1, (1, 512, 2400)).astype(np.float32))
+    ec = D(r.normal(0, 1, (1, 512, 1)).astype(np.float32))
+    ea = D(r.uniform(0.5, 2, (1, 512, 1)).astype(np.float32))
+    ne = max(2, -(-ROTATE_BYTES // (2 * 4915200)))
+    exs = B.replicate(ex, ne)
+    eos = [kk.DeviceTensor.empty(ex.shape) for _ in range(ne)]
+    ebytes = 2 * 4915200 + 2048
+    opc = kk._lib.OP
+    per_op("add_1x512x2400", lambda i: B.call("kk_binary", opc["Add"], eos[i].desc(), exs[i].desc(),
+                                               ec.desc()), ebytes, sets=ne)
+    per_op("mul_1x512x2400", lambda i: B.call("kk_binary", opc["Mul"], eos[i].desc(), exs[i].desc(),
+                                               ec.desc()), ebytes, sets=ne)
+    per_op("leakyrelu_1x512x2400", lambda i: B.call("kk_unary", opc["LeakyRelu"], eos[i].desc(),
+                                                     exs[i].desc(), 0.2), 2 * 4915200, sets=ne)
+    per_op("snake_1x512x2400", lambda i: B.call("kk_snake", eos[i].desc(), exs[i].desc(), ea.desc(),
+                                                 None), ebytes, sets=ne)
+    del exs, eos
+
+    # dequant contractions (fp32 semantics; TFLOP/s against the fp32 peak)
+    def gemm_case(name, m, k, n, wdt):
+        a = B.replicate(D(r.normal(0, 1, (m, k)).astype(np.float32)), 4)
+        if wdt == "i8":
+            wq = D(r.integers(-127, 128, (k, n)).astype(np.int8))
+            sc = D(np.array(r.uniform(1e-3, 1e-2), np.float32))
+        else:
+            wq = D(r.normal(0, 0.02, (k, n)).astype(np.float16))
+            sc = None
+        o = [kk.DeviceTensor.empty((m, n)) for _ in range(4)]
+        per_op(name, lambda i: B.call("kk_gemm", o[i].desc(), a[i].desc(), wq.desc(),
+                                      sc.desc() if sc else None, None, 1.0),
+               flops=2 * m * n * k, sets=4)
+
+    gemm_case("gemm_i8_256x768x2048", 256, 768, 2048, "i8")
+    gemm_case("gemm_i8_256x2048x768", 256, 2048, 768, "i8")
+    gemm_case("gemm_f16_256x768x768", 256, 768, 768, "f16")
+
+    def conv_case(name, cin, cout, k, L, pad, dil):
+        x = B.replicate(D(r.normal(0, 1, (1, cin, L)).astype(np.float32)), 4)
+        wq = D(r.integers(-127, 128, (cout, cin, k)).astype(np.int8))
+        sc = D(np.array(0.005, np.float32))
+        lout = L + 2 * pad - dil * (k - 1)
+        o = [kk.DeviceTensor.empty((1, cout, lout)) for _ in range(4)]
+        per_op(name, lambda i: B.call("kk_conv1d", o[i].desc(), x[i].desc(), wq.desc(), sc.desc(),
+                                      None, None, 1, dil, pad, pad, 1),
+               flops=2 * cout * cin * k * lout, sets=4)
+
+    conv_case("conv_i8_512x512_k3_L2400", 512, 512, 3, 2400, 1, 1)
+    conv_case("conv_i8_256x256_k3_d1_L2400", 256, 256, 3, 2400, 1, 1)
+    conv_case("conv_i8_256x256_k3_d3_L2400", 256, 256, 3, 2400, 3, 3)
+    xt = B.replicate(D(r.normal(0, 1, (1, 512, 240)).astype(np.float32)), 4)
+    wt = D(r.integers(-127, 128, (512, 256, 20)).astype(np.int8))
+    sct = D(np.array(0.005, np.float32))
+    ot = [kk.DeviceTensor.empty((1, 256, 2400)) for _ in range(4)]
+    per_op("convT_i8_512x256_k20_s10", lambda i: B.call(
+        "kk_conv_transpose1d", ot[i].desc(), xt[i].desc(), wt.desc(), sct.desc(), None, None, 10, 1,
+        5, 5, 1, 0), flops=2 * 512 * 256 * 2400 * 20 // 10, sets=4)
+
+    roofline = {
+        "kernel": "instnorm_kernel (AdaIN T=9600, style Linear fused)",
+        "bound": "hbm",
+        "achieved": dom["gbps"],
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(dom["gbps"] / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "algorithmic_bytes_per_launch": BYTES["adain_t9600"],
+        "avg_launch_us": dom["us"],
+    }
+    return ms_per_step, nsets, ops_out, roofline
+
+
+def run_cpu(seconds):
+    """The numpy oracle on this host, single-threaded, over the same step."""
+    from oracle import ref_ops as O
+    try:
+        from threadpoolctl import threadpool_limits
+        limiter = threadpool_limits(limits=1)
+    except Exception:  # pragma: no cover - threadpoolctl is installed here
+        limiter = None
+    h = reduction_inputs()
+
+    def step():
+        O.adain(h["x1200"], h["style"], h["w"], h["b"], 1e-5)
+        O.adain(h["x9600"], h["style"], h["w"], h["b"], 1e-5)
+        O.layernorm(h["ln"], h["g"], h["beta"], -1, 1e-12)
+        O.softmax(h["sm"], -1)
+
+    step()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+    t = float(np.median(times))
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(STEP_BYTES / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"numpy oracle, full step (AdaIN T=1200 and T=9600 with Linear, LayerNorm, "
+                   f"Softmax) x{len(times)} runs, median {t * 1e3:.1f} ms/step; 1 thread "
+                   f"(threadpoolctl); {model or platform.processor()}; "
+                   f"{len(os.sched_getaffinity(0))} cores visible; numpy {np.__version__}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the op layer shards by utterance with no collective)", file=sys.stderr)
+        return 2
+    ms_per_step, nsets, ops_out, roofline = run_gpu(args)
+    cpu = None if args.no_cpu else run_cpu(args.cpu_seconds)
+    value = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy draws; inputs resident in HBM)",
+        "config": {
+            "workload": ("reductions: AdaIN (InstanceNorm over T, eps 1e-5, style Linear "
+                         "128->1024 fused) on [1,512,1200] and [1,512,9600]; LayerNorm(768, "
+                         "eps 1e-12) on [1,256,768]; Softmax(last axis) on [1,12,256,256]"),
+            "bytes_per_step": STEP_BYTES,
+            "rotating_sets": nsets,
+            "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "ops": ops_out,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,134 @@
+// Internal declarations shared by the libkk translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "kk.h"
+
+namespace kk {
+
+// ---------------------------------------------------------------- context
+struct Context {
+  bool ready = false;
+  int device = -1;
+  hipStream_t stream = nullptr;
+  int num_cus = 0;
+  bool capturing = false;  // between kk_graph_begin and kk_graph_end
+};
+Context& ctx();
+
+// Thread-local last error; set_error returns `code` so call sites can
+// `return set_error(KK_E_ARG, "...")`.
+int set_error(int code, const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+int require_ready();
+
+#define KK_TRY(expr)            \
+  do {                          \
+    int _rc = (expr);           \
+    if (_rc != KK_OK) return _rc; \
+  } while (0)
+
+#define KK_HIP(expr) KK_TRY(::kk::check_hip((expr), #expr))
+
+// Checks the launch that was just enqueued.
+int check_launch(const char* kernel);
+
+// ------------------------------------------------------------ descriptors
+int dtype_size(int dtype);
+bool is_float(int dtype);
+bool is_int(int dtype);
+int64_t numel(const kk_tensor* t);
+bool is_contiguous(const kk_tensor* t);
+// Validates rank, dtype and non-negative extents; `name` goes in the error.
+int check_tensor(const kk_tensor* t, const char* name);
+
+// An elementwise plan: up to four operands (0 = output) walked over one
+// collapsed index space.  Strides are in elements, broadcast axes carry 0.
+constexpr int kMaxOperands = 4;
+struct Plan {
+  int rank = 0;
+  int64_t dims[KK_MAX_RANK];
+  int64_t st[kMaxOperands][KK_MAX_RANK];
+  int nops = 0;
+  int64_t n = 0;
+};
+// Broadcasts the inputs against out->shape (numpy right alignment), drops
+// unit axes and merges adjacent axes that every operand walks contiguously
+// (the same rule as runtime/ops.gd:85-129).  ins may hold NULL entries,
+// which are skipped (their strides stay 0).
+int make_plan(Plan* p, const kk_tensor* out, const kk_tensor* const* ins,
+              int nins);
+
+// -------------------------------------------------------- device helpers
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Loads element `i` of a buffer of dtype `dt` as fp32 (fp16 is storage only).
+__device__ __forceinline__ float load_as_f32(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case KK_F32: return static_cast<const float*>(p)[i];
+    case KK_F16: return __half2float(static_cast<const __half*>(p)[i]);
+    case KK_I8: return static_cast<float>(static_cast<const int8_t*>(p)[i]);
+    case KK_U8: return static_cast<float>(static_cast<const uint8_t*>(p)[i]);
+    case KK_I32: return static_cast<float>(static_cast<const int32_t*>(p)[i]);
+    case KK_I64: return static_cast<float>(static_cast<const int64_t*>(p)[i]);
+    case KK_BOOL: return static_cast<const uint8_t*>(p)[i] ? 1.0f : 0.0f;
+  }
+  return 0.0f;
+}
+
+__device__ __forceinline__ int64_t load_as_i64(const void* p, int dt, int64_t i) {
+  switch (dt) {
+    case KK_I8: return static_cast<const int8_t*>(p)[i];
+    case KK_U8: return static_cast<const uint8_t*>(p)[i];
+    case KK_I32: return static_cast<const int32_t*>(p)[i];
+    case KK_I64: return static_cast<const int64_t*>(p)[i];
+    case KK_BOOL: return static_cast<const uint8_t*>(p)[i] ? 1 : 0;
+    case KK_F32: return static_cast<int64_t>(static_cast<const float*>(p)[i]);
+    case KK_F16:
+      return static_cast<int64_t>(__half2float(static_cast<const __half*>(p)[i]));
+  }
+  return 0;
+}
+
+// Weight dequantisation parameters shared by gemm, conv and adain: a
+// per-tensor or per-column scale and zero point, read once on the host side
+// of the launch as device pointers.
+struct Dequant {
+  const void* scale = nullptr;  // fp32/fp16, 1 or `count` elements
+  int scale_dt = KK_F32;
+  int64_t scale_stride = 0;     // 0 = per tensor
+  const void* zp = nullptr;     // int8/uint8/int32, 1 or `count` elements
+  int zp_dt = KK_I8;
+  int64_t zp_stride = 0;
+  bool active = false;          // true for int8/uint8 weights
+};
+// Checks `w_scale`/`w_zp` against the weight dtype and the number of
+// columns (`count`) they may be indexed by.
+int make_dequant(Dequant* d, const kk_tensor* w, const kk_tensor* scale,
+                 const kk_tensor* zp, int64_t count, const char* who);
+
+__device__ __forceinline__ float dequant_value(float q, const Dequant& d,
+                                               int64_t col) {
+  float z = d.zp ? load_as_f32(d.zp, d.zp_dt, col * d.zp_stride) : 0.0f;
+  float s = load_as_f32(d.scale, d.scale_dt, col * d.scale_stride);
+  return (q - z) * s;
+}
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace kk

@@ -1,0 +1,743 @@
+// Row reductions and normalisations: ReduceMean/Sum/Max, InstanceNorm with
+// the AdaIN affine (optionally with the style Linear fused in), LayerNorm /
+// SkipLayerNorm and Softmax.
+//
+// Row kernels hold their row in registers: a GROUP of 64 (one wavefront) or
+// 256 (four wavefronts) threads owns one row, each thread NV vectors of VEC
+// floats, so the row is read from HBM once and written once.  Reductions
+// are wave butterflies (__shfl_xor) plus, for 256-thread groups, a 4-entry
+// LDS combine; the order is fixed, so results are identical run to run.
+// Statistics follow numpy: mean = sum / n in fp32, variance two-pass
+// mean((x - mean)^2), normalisation a true division by sqrt(var + eps).
+#include <algorithm>
+
+#include "kk_internal.h"
+
+namespace kk {
+
+constexpr int kRowBlock = 256;
+
+template <int GROUP>
+__device__ __forceinline__ float group_sum(float v, float* lds) {
+  v = wave_sum(v);
+  if constexpr (GROUP == 64) {
+    return v;
+  } else {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    return (lds[0] + lds[1]) + (lds[2] + lds[3]);
+  }
+}
+
+template <int GROUP>
+__device__ __forceinline__ float group_max(float v, float* lds) {
+  v = wave_max(v);
+  if constexpr (GROUP == 64) {
+    return v;
+  } else {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) lds[w] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(lds[0], lds[1]), fmaxf(lds[2], lds[3]));
+  }
+}
+
+// Loads this thread's share of a row of `n` floats into r[NV][VEC].
+// Element index of (j, e) is (j * GROUP + g) * VEC + e; missing ones are 0.
+template <int GROUP, int NV, int VEC>
+__device__ __forceinline__ void load_row(const float* __restrict__ row, int64_t n, int g,
+                                         float (&r)[NV][VEC]) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
+    if constexpr (VEC == 4) {
+      if (base < n) {
+        const float4 v = *reinterpret_cast<const float4*>(row + base);
+        r[j][0] = v.x; r[j][1] = v.y; r[j][2] = v.z; r[j][3] = v.w;
+      } else {
+        r[j][0] = r[j][1] = r[j][2] = r[j][3] = 0.0f;
+      }
+    } else {
+      r[j][0] = base < n ? row[base] : 0.0f;
+    }
+  }
+}
+
+template <int GROUP, int NV, int VEC>
+__device__ __forceinline__ void store_row(float* __restrict__ row, int64_t n, int g,
+                                          const float (&r)[NV][VEC]) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
+    if (base < n) {
+      if constexpr (VEC == 4) {
+        *reinterpret_cast<float4*>(row + base) = make_float4(r[j][0], r[j][1], r[j][2], r[j][3]);
+      } else {
+        row[base] = r[j][0];
+      }
+    }
+  }
+}
+
+// Two-pass mean and variance of the row held in r (n valid elements; the
+// padding lanes hold 0 and are masked out of the second pass).
+template <int GROUP, int NV, int VEC>
+__device__ __forceinline__ void row_stats(float (&r)[NV][VEC], int64_t n, int g, float* lds,
+                                          float& mean, float& var) {
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) s += r[j][e];
+  s = group_sum<GROUP>(s, lds);
+  mean = s / static_cast<float>(n);
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float d = r[j][e] - mean;
+      r[j][e] = d;  // keep x - mean for the output pass
+      if (base + e < n) q += d * d;
+    }
+  }
+  q = group_sum<GROUP>(q, lds);
+  var = q / static_cast<float>(n);
+}
+
+// ----------------------------------------------------- InstanceNorm / AdaIN
+// Style projection for channel c of C: h[j] = sum_k style[k] * W[k, j] + b[j]
+// for j = c (gamma) and j = C + c (beta).  W is any-strided, optionally
+// int8/uint8 with per-tensor/per-column dequantisation.
+struct StyleArgs {
+  const float* style;     // [S] fp32 (contiguous)
+  const void* w;          // [S, 2C]
+  int w_dt;
+  int64_t w_sk, w_sj;     // strides of W in elements
+  Dequant dq;
+  const float* bias;      // [2C] or NULL
+  int64_t S;
+};
+
+template <int GROUP>
+__device__ __forceinline__ void style_affine(const StyleArgs& sa, int64_t C, int64_t c, int g,
+                                             float* lds, float& gamma, float& beta) {
+  float ag = 0.0f, ab = 0.0f;
+  const int64_t jg = c, jb = C + c;
+  for (int64_t k = g; k < sa.S; k += GROUP) {
+    const float s = sa.style[k];
+    float wg = load_as_f32(sa.w, sa.w_dt, k * sa.w_sk + jg * sa.w_sj);
+    float wb = load_as_f32(sa.w, sa.w_dt, k * sa.w_sk + jb * sa.w_sj);
+    if (sa.dq.active) {
+      wg = dequant_value(wg, sa.dq, jg);
+      wb = dequant_value(wb, sa.dq, jb);
+    }
+    ag = __builtin_fmaf(s, wg, ag);
+    ab = __builtin_fmaf(s, wb, ab);
+  }
+  ag = group_sum<GROUP>(ag, lds);
+  ab = group_sum<GROUP>(ab, lds);
+  if (sa.bias) {
+    ag = ag + sa.bias[jg];
+    ab = ab + sa.bias[jb];
+  }
+  gamma = ag;
+  beta = ab;
+}
+
+// mode 0: no affine; 1: gamma/beta from `gb` ([2C]); 2: from the style Linear.
+template <int GROUP, int NV, int VEC>
+__global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__ out,
+                                                             const float* __restrict__ x,
+                                                             int64_t rows, int64_t C, int64_t T,
+                                                             float eps, int mode,
+                                                             const float* __restrict__ gb,
+                                                             StyleArgs sa) {
+  __shared__ float lds[4];
+  constexpr int RPB = kRowBlock / GROUP;
+  const int g = threadIdx.x % GROUP;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
+  // Every thread of the block takes part in the group reductions even when
+  // its row is past the end (RPB > 1 only for GROUP == 64, whose reductions
+  // are per wave, so the idle rows simply return).
+  if constexpr (GROUP == 64) {
+    if (row >= rows) return;
+  }
+  const int64_t c = row % C;
+  float gamma = 0.0f, beta = 0.0f;
+  if (mode == 2) style_affine<GROUP>(sa, C, c, g, lds, gamma, beta);
+  else if (mode == 1) { gamma = gb[c]; beta = gb[C + c]; }
+  const float* xr = x + row * T;
+  float r[NV][VEC];
+  load_row<GROUP, NV, VEC>(xr, T, g, r);
+  float mean, var;
+  row_stats<GROUP, NV, VEC>(r, T, g, lds, mean, var);
+  const float den = sqrtf(var + eps);
+  const float g1 = gamma + 1.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float q = r[j][e] / den;
+      r[j][e] = mode ? (q * g1) + beta : q;
+    }
+  store_row<GROUP, NV, VEC>(out + row * T, T, g, r);
+}
+
+// Rows too long for registers: three passes over global memory.
+__global__ void __launch_bounds__(kRowBlock) instnorm_long_kernel(float* __restrict__ out,
+                                                                  const float* __restrict__ x,
+                                                                  int64_t C, int64_t T, float eps,
+                                                                  int mode,
+                                                                  const float* __restrict__ gb,
+                                                                  StyleArgs sa) {
+  __shared__ float lds[4];
+  const int g = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t c = row % C;
+  float gamma = 0.0f, beta = 0.0f;
+  if (mode == 2) style_affine<kRowBlock>(sa, C, c, g, lds, gamma, beta);
+  else if (mode == 1) { gamma = gb[c]; beta = gb[C + c]; }
+  const float* xr = x + row * T;
+  float s = 0.0f;
+  for (int64_t i = g; i < T; i += kRowBlock) s += xr[i];
+  const float mean = group_sum<kRowBlock>(s, lds) / static_cast<float>(T);
+  float q = 0.0f;
+  for (int64_t i = g; i < T; i += kRowBlock) {
+    const float d = xr[i] - mean;
+    q += d * d;
+  }
+  const float var = group_sum<kRowBlock>(q, lds) / static_cast<float>(T);
+  const float den = sqrtf(var + eps);
+  const float g1 = gamma + 1.0f;
+  float* orow = out + row * T;
+  for (int64_t i = g; i < T; i += kRowBlock) {
+    const float v = (xr[i] - mean) / den;
+    orow[i] = mode ? (v * g1) + beta : v;
+  }
+}
+
+// -------------------------------------------------------------- LayerNorm
+struct LnArgs {
+  const float* skip;       // [rows, cols] or NULL
+  const float* skip_bias;  // [cols] or NULL
+  const float* scale;      // [cols]
+  const float* bias;       // [cols] or NULL
+};
+
+template <int GROUP, int NV, int VEC>
+__global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict__ out,
+                                                              const float* __restrict__ x,
+                                                              int64_t rows, int64_t cols, float eps,
+                                                              LnArgs la) {
+  __shared__ float lds[4];
+  constexpr int RPB = kRowBlock / GROUP;
+  const int g = threadIdx.x % GROUP;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
+  if constexpr (GROUP == 64) {
+    if (row >= rows) return;
+  }
+  float r[NV][VEC];
+  load_row<GROUP, NV, VEC>(x + row * cols, cols, g, r);
+  if (la.skip) {
+    // SkipLayerNormalization: s = x + skip (+ bias), ref_runtime.py:605-608.
+    float k[NV][VEC];
+    load_row<GROUP, NV, VEC>(la.skip + row * cols, cols, g, k);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] + k[j][e];
+    if (la.skip_bias) {
+      load_row<GROUP, NV, VEC>(la.skip_bias, cols, g, k);
+#pragma unroll
+      for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] + k[j][e];
+    }
+  }
+  float mean, var;
+  row_stats<GROUP, NV, VEC>(r, cols, g, lds, mean, var);
+  const float den = sqrtf(var + eps);
+  float sc[NV][VEC];
+  load_row<GROUP, NV, VEC>(la.scale, cols, g, sc);
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) r[j][e] = (r[j][e] / den) * sc[j][e];
+  if (la.bias) {
+    load_row<GROUP, NV, VEC>(la.bias, cols, g, sc);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] + sc[j][e];
+  }
+  store_row<GROUP, NV, VEC>(out + row * cols, cols, g, r);
+}
+
+__global__ void __launch_bounds__(kRowBlock) layernorm_long_kernel(float* __restrict__ out,
+                                                                   const float* __restrict__ x,
+                                                                   int64_t cols, float eps,
+                                                                   LnArgs la) {
+  __shared__ float lds[4];
+  const int g = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * cols;
+  const float* kr = la.skip ? la.skip + row * cols : nullptr;
+  auto val = [&](int64_t i) {
+    float v = xr[i];
+    if (kr) {
+      v = v + kr[i];
+      if (la.skip_bias) v = v + la.skip_bias[i];
+    }
+    return v;
+  };
+  float s = 0.0f;
+  for (int64_t i = g; i < cols; i += kRowBlock) s += val(i);
+  const float mean = group_sum<kRowBlock>(s, lds) / static_cast<float>(cols);
+  float q = 0.0f;
+  for (int64_t i = g; i < cols; i += kRowBlock) {
+    const float d = val(i) - mean;
+    q += d * d;
+  }
+  const float var = group_sum<kRowBlock>(q, lds) / static_cast<float>(cols);
+  const float den = sqrtf(var + eps);
+  float* orow = out + row * cols;
+  for (int64_t i = g; i < cols; i += kRowBlock) {
+    float v = ((val(i) - mean) / den) * la.scale[i];
+    if (la.bias) v = v + la.bias[i];
+    orow[i] = v;
+  }
+}
+
+// ---------------------------------------------------------------- Softmax
+template <int GROUP, int NV, int VEC>
+__global__ void __launch_bounds__(kRowBlock) softmax_kernel(float* __restrict__ out,
+                                                            const float* __restrict__ x,
+                                                            int64_t rows, int64_t cols) {
+  __shared__ float lds[4];
+  constexpr int RPB = kRowBlock / GROUP;
+  const int g = threadIdx.x % GROUP;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
+  if constexpr (GROUP == 64) {
+    if (row >= rows) return;
+  }
+  float r[NV][VEC];
+  load_row<GROUP, NV, VEC>(x + row * cols, cols, g, r);
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e)
+      if (base + e < cols) m = fmaxf(m, r[j][e]);
+  }
+  m = group_max<GROUP>(m, lds);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      const float v = expf(r[j][e] - m);
+      r[j][e] = v;
+      if (base + e < cols) s += v;
+    }
+  }
+  s = group_sum<GROUP>(s, lds);
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] / s;
+  store_row<GROUP, NV, VEC>(out + row * cols, cols, g, r);
+}
+
+// Softmax / reduce along an axis with inner extent > 1: one thread per
+// (outer, inner) column walks the axis (coalesced across inner).
+__global__ void softmax_cols_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                    int64_t outer, int64_t dim, int64_t inner) {
+  const int64_t n = outer * inner;
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < n;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t o = t / inner, i = t % inner;
+    const float* xc = x + o * dim * inner + i;
+    float* oc = out + o * dim * inner + i;
+    float m = -INFINITY;
+    for (int64_t d = 0; d < dim; ++d) m = fmaxf(m, xc[d * inner]);
+    double s = 0.0;
+    for (int64_t d = 0; d < dim; ++d) s += expf(xc[d * inner] - m);
+    const float sf = static_cast<float>(s);
+    for (int64_t d = 0; d < dim; ++d) oc[d * inner] = expf(xc[d * inner] - m) / sf;
+  }
+}
+
+// ------------------------------------------------------------- reductions
+template <int GROUP, int NV, int VEC>
+__global__ void __launch_bounds__(kRowBlock) reduce_rows_kernel(float* __restrict__ out,
+                                                                const float* __restrict__ x,
+                                                                int64_t rows, int64_t cols, int op) {
+  __shared__ float lds[4];
+  constexpr int RPB = kRowBlock / GROUP;
+  const int g = threadIdx.x % GROUP;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
+  if constexpr (GROUP == 64) {
+    if (row >= rows) return;
+  }
+  float r[NV][VEC];
+  load_row<GROUP, NV, VEC>(x + row * cols, cols, g, r);
+  float v;
+  if (op == KK_REDUCE_MAX) {
+    float m = -INFINITY;
+    bool nan = false;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        if (base + e < cols) { nan |= __builtin_isnan(r[j][e]); m = fmaxf(m, r[j][e]); }
+    }
+    m = group_max<GROUP>(m, lds);
+    const float anynan = group_max<GROUP>(nan ? 1.0f : 0.0f, lds);
+    v = anynan > 0.0f ? NAN : m;
+  } else {
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) s += r[j][e];
+    s = group_sum<GROUP>(s, lds);
+    v = op == KK_REDUCE_MEAN ? s / static_cast<float>(cols) : s;
+  }
+  if (g == 0) out[row] = v;
+}
+
+// General reduction: kept axes (kdims/kst) index the output in order,
+// reduced axes (rdims/rst) are walked by each thread; x is strided.
+struct RedArgs {
+  int kr, rr;
+  int64_t kdims[KK_MAX_RANK], kst[KK_MAX_RANK];
+  int64_t rdims[KK_MAX_RANK], rst[KK_MAX_RANK];
+  int64_t nout, nred;
+};
+
+__global__ void reduce_generic_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                      RedArgs R, int op) {
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < R.nout;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int64_t rem = t, base = 0;
+    for (int d = R.kr - 1; d >= 0; --d) {
+      base += (rem % R.kdims[d]) * R.kst[d];
+      rem /= R.kdims[d];
+    }
+    double s = 0.0;
+    float m = -INFINITY;
+    bool nan = false;
+    for (int64_t j = 0; j < R.nred; ++j) {
+      int64_t rj = j, off = base;
+      for (int d = R.rr - 1; d >= 0; --d) {
+        off += (rj % R.rdims[d]) * R.rst[d];
+        rj /= R.rdims[d];
+      }
+      const float v = x[off];
+      s += v;
+      nan |= __builtin_isnan(v);
+      m = fmaxf(m, v);
+    }
+    float v;
+    if (op == KK_REDUCE_MAX) v = nan ? NAN : m;
+    else if (op == KK_REDUCE_MEAN) v = static_cast<float>(s) / static_cast<float>(R.nred);
+    else v = static_cast<float>(s);
+    out[t] = v;
+  }
+}
+
+// ------------------------------------------------------------- launching
+// Picks (GROUP, NV, VEC) so that GROUP * NV * VEC covers the row; returns
+// false when the row is too long for registers.
+struct RowShape {
+  int group, nv, vec;
+};
+static bool pick_row_shape(int64_t n, bool vec_ok, RowShape* rs) {
+  const int vec = vec_ok ? 4 : 1;
+  const int64_t nvec = ceil_div(n, vec);
+  static const int nvs[] = {1, 2, 4, 8, 16};
+  // One wavefront per row while the row fits 64 * 4 vectors (keeps many
+  // rows in flight for short rows); 256 threads per row beyond that.
+  for (int nv : nvs) {
+    if (nv > 4) break;
+    if (nvec <= int64_t(64) * nv) { *rs = {64, nv, vec}; return true; }
+  }
+  for (int nv : nvs)
+    if (nvec <= int64_t(256) * nv) { *rs = {256, nv, vec}; return true; }
+  return false;
+}
+
+#define KK_ROW_DISPATCH(KERNEL, RS, GRID_ROWS, ...)                                          \
+  do {                                                                                         \
+    const int _rpb = kRowBlock / (RS).group;                                                   \
+    const dim3 _grid(static_cast<unsigned>(ceil_div((GRID_ROWS), _rpb)));                      \
+    hipStream_t _s = ctx().stream;                                                             \
+    if ((RS).group == 64) {                                                                    \
+      if ((RS).vec == 4) {                                                                     \
+        switch ((RS).nv) {                                                                     \
+          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<64, 4, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+        }                                                                                      \
+      } else {                                                                                 \
+        switch ((RS).nv) {                                                                     \
+          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<64, 4, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+        }                                                                                      \
+      }                                                                                        \
+    } else {                                                                                   \
+      if ((RS).vec == 4) {                                                                     \
+        switch ((RS).nv) {                                                                     \
+          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<256, 16, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+        }                                                                                      \
+      } else {                                                                                 \
+        switch ((RS).nv) {                                                                     \
+          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<256, 16, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+        }                                                                                      \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+static int check_f32_contig(const kk_tensor* t, const char* name) {
+  KK_TRY(check_tensor(t, name));
+  if (t->dtype != KK_F32) return set_error(KK_E_ARG, "%s must be fp32", name);
+  if (!is_contiguous(t)) return set_error(KK_E_ARG, "%s must be contiguous", name);
+  return KK_OK;
+}
+
+static bool same_shape(const kk_tensor* a, const kk_tensor* b) {
+  if (a->rank != b->rank) return false;
+  for (int i = 0; i < a->rank; ++i)
+    if (a->shape[i] != b->shape[i]) return false;
+  return true;
+}
+
+static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, int mode,
+                           const float* gb, const StyleArgs& sa) {
+  if (x->rank < 2) return set_error(KK_E_ARG, "instance norm: x must be [N, C, ...T]");
+  const int64_t T = x->shape[x->rank - 1];
+  const int64_t C = x->shape[x->rank - 2];
+  const int64_t rows = numel(x) / (T ? T : 1);
+  if (numel(x) == 0) return KK_OK;
+  RowShape rs;
+  const bool vec_ok = (T % 4 == 0) && aligned16(x->data) && aligned16(out->data);
+  if (pick_row_shape(T, vec_ok, &rs)) {
+    KK_ROW_DISPATCH(instnorm_kernel, rs, rows, static_cast<float*>(out->data),
+                    static_cast<const float*>(x->data), rows, C, T, eps, mode, gb, sa);
+  } else {
+    hipLaunchKernelGGL(instnorm_long_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
+                       ctx().stream, static_cast<float*>(out->data),
+                       static_cast<const float*>(x->data), C, T, eps, mode, gb, sa);
+  }
+  return check_launch("instnorm_kernel");
+}
+
+}  // namespace kk
+
+using namespace kk;
+
+extern "C" {
+
+int kk_instance_norm_affine(const kk_tensor* out, const kk_tensor* x, const kk_tensor* gamma_beta,
+                            float eps) {
+  KK_TRY(require_ready());
+  KK_TRY(check_f32_contig(x, "x"));
+  KK_TRY(check_f32_contig(out, "out"));
+  if (!same_shape(out, x)) return set_error(KK_E_ARG, "instance norm: out shape must equal x");
+  const float* gb = nullptr;
+  if (gamma_beta) {
+    KK_TRY(check_f32_contig(gamma_beta, "gamma_beta"));
+    const int64_t C = x->rank >= 2 ? x->shape[x->rank - 2] : 0;
+    if (numel(gamma_beta) != 2 * C)
+      return set_error(KK_E_ARG, "instance norm: gamma_beta needs 2C = %lld elements",
+                       (long long)(2 * C));
+    gb = static_cast<const float*>(gamma_beta->data);
+  }
+  StyleArgs sa{};
+  return instnorm_launch(out, x, eps, gb ? 1 : 0, gb, sa);
+}
+
+int kk_adain(const kk_tensor* out, const kk_tensor* x, const kk_tensor* style, const kk_tensor* w,
+             const kk_tensor* w_scale, const kk_tensor* w_zp, const kk_tensor* bias, float eps) {
+  KK_TRY(require_ready());
+  KK_TRY(check_f32_contig(x, "x"));
+  KK_TRY(check_f32_contig(out, "out"));
+  KK_TRY(check_f32_contig(style, "style"));
+  KK_TRY(check_tensor(w, "w"));
+  if (!same_shape(out, x)) return set_error(KK_E_ARG, "adain: out shape must equal x");
+  if (x->rank < 2) return set_error(KK_E_ARG, "adain: x must be [N, C, T]");
+  const int64_t C = x->shape[x->rank - 2];
+  const int64_t S = numel(style);
+  if (w->rank != 2 || w->shape[0] != S || w->shape[1] != 2 * C)
+    return set_error(KK_E_ARG, "adain: w must be [S=%lld, 2C=%lld]", (long long)S,
+                     (long long)(2 * C));
+  if (x->shape[0] != 1 && x->rank == 3)
+    return set_error(KK_E_UNSUPPORTED, "adain: one style row serves batch 1 only");
+  StyleArgs sa{};
+  sa.style = static_cast<const float*>(style->data);
+  sa.w = w->data;
+  sa.w_dt = w->dtype;
+  sa.w_sk = w->strides[0];
+  sa.w_sj = w->strides[1];
+  sa.S = S;
+  KK_TRY(make_dequant(&sa.dq, w, w_scale, w_zp, 2 * C, "adain"));
+  if (bias) {
+    KK_TRY(check_f32_contig(bias, "bias"));
+    if (numel(bias) != 2 * C) return set_error(KK_E_ARG, "adain: bias needs 2C elements");
+    sa.bias = static_cast<const float*>(bias->data);
+  }
+  return instnorm_launch(out, x, eps, 2, nullptr, sa);
+}
+
+int kk_layernorm(const kk_tensor* out, const kk_tensor* x, const kk_tensor* skip,
+                 const kk_tensor* skip_bias, const kk_tensor* scale, const kk_tensor* bias,
+                 int axis, float eps) {
+  KK_TRY(require_ready());
+  KK_TRY(check_f32_contig(x, "x"));
+  KK_TRY(check_f32_contig(out, "out"));
+  KK_TRY(check_f32_contig(scale, "scale"));
+  if (!same_shape(out, x)) return set_error(KK_E_ARG, "layernorm: out shape must equal x");
+  if (axis < 0) axis += x->rank;
+  if (axis < 0 || axis >= x->rank) return set_error(KK_E_ARG, "layernorm: axis out of range");
+  int64_t cols = 1;
+  for (int i = axis; i < x->rank; ++i) cols *= x->shape[i];
+  const int64_t n = numel(x);
+  if (n == 0) return KK_OK;
+  const int64_t rows = n / cols;
+  if (numel(scale) != cols) return set_error(KK_E_ARG, "layernorm: scale needs %lld elements", (long long)cols);
+  LnArgs la{};
+  la.scale = static_cast<const float*>(scale->data);
+  if (bias) {
+    KK_TRY(check_f32_contig(bias, "bias"));
+    if (numel(bias) != cols) return set_error(KK_E_ARG, "layernorm: bias needs %lld elements", (long long)cols);
+    la.bias = static_cast<const float*>(bias->data);
+  }
+  if (skip) {
+    KK_TRY(check_f32_contig(skip, "skip"));
+    if (!same_shape(skip, x)) return set_error(KK_E_ARG, "layernorm: skip shape must equal x");
+    la.skip = static_cast<const float*>(skip->data);
+    if (skip_bias) {
+      KK_TRY(check_f32_contig(skip_bias, "skip_bias"));
+      if (numel(skip_bias) != cols) return set_error(KK_E_ARG, "layernorm: skip bias needs %lld elements", (long long)cols);
+      la.skip_bias = static_cast<const float*>(skip_bias->data);
+    }
+  } else if (skip_bias) {
+    return set_error(KK_E_ARG, "layernorm: skip_bias without skip");
+  }
+  bool vec_ok = (cols % 4 == 0) && aligned16(x->data) && aligned16(out->data) &&
+                aligned16(la.scale) && (!la.bias || aligned16(la.bias)) &&
+                (!la.skip || aligned16(la.skip)) && (!la.skip_bias || aligned16(la.skip_bias));
+  RowShape rs;
+  if (pick_row_shape(cols, vec_ok, &rs)) {
+    KK_ROW_DISPATCH(layernorm_kernel, rs, rows, static_cast<float*>(out->data),
+                    static_cast<const float*>(x->data), rows, cols, eps, la);
+  } else {
+    hipLaunchKernelGGL(layernorm_long_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
+                       ctx().stream, static_cast<float*>(out->data),
+                       static_cast<const float*>(x->data), cols, eps, la);
+  }
+  return check_launch("layernorm_kernel");
+}
+
+int kk_softmax(const kk_tensor* out, const kk_tensor* x, int axis) {
+  KK_TRY(require_ready());
+  KK_TRY(check_f32_contig(x, "x"));
+  KK_TRY(check_f32_contig(out, "out"));
+  if (!same_shape(out, x)) return set_error(KK_E_ARG, "softmax: out shape must equal x");
+  if (x->rank == 0) return set_error(KK_E_ARG, "softmax: scalar input");
+  if (axis < 0) axis += x->rank;
+  if (axis < 0 || axis >= x->rank) return set_error(KK_E_ARG, "softmax: axis out of range");
+  int64_t outer = 1, inner = 1;
+  for (int i = 0; i < axis; ++i) outer *= x->shape[i];
+  for (int i = axis + 1; i < x->rank; ++i) inner *= x->shape[i];
+  const int64_t dim = x->shape[axis];
+  if (numel(x) == 0) return KK_OK;
+  RowShape rs;
+  const bool vec_ok = (dim % 4 == 0) && aligned16(x->data) && aligned16(out->data);
+  if (inner == 1 && pick_row_shape(dim, vec_ok, &rs)) {
+    KK_ROW_DISPATCH(softmax_kernel, rs, outer, static_cast<float*>(out->data),
+                    static_cast<const float*>(x->data), outer, dim);
+    return check_launch("softmax_kernel");
+  }
+  const int64_t cols = outer * inner;
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(cols, 256), 65535));
+  hipLaunchKernelGGL(softmax_cols_kernel, dim3(grid), dim3(256), 0, ctx().stream,
+                     static_cast<float*>(out->data), static_cast<const float*>(x->data), outer, dim,
+                     inner);
+  return check_launch("softmax_cols_kernel");
+}
+
+int kk_reduce(int op, const kk_tensor* out, const kk_tensor* x, uint32_t axes_mask) {
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(x, "x"));
+  KK_TRY(check_f32_contig(out, "out"));
+  if (x->dtype != KK_F32) return set_error(KK_E_ARG, "reduce: x must be fp32");
+  if (op != KK_REDUCE_SUM && op != KK_REDUCE_MEAN && op != KK_REDUCE_MAX)
+    return set_error(KK_E_ARG, "reduce: unknown op %d", op);
+  if (axes_mask >> x->rank) return set_error(KK_E_ARG, "reduce: axis beyond rank");
+  RedArgs R{};
+  int64_t nout = 1, nred = 1;
+  for (int i = 0; i < x->rank; ++i) {
+    if (axes_mask & (1u << i)) {
+      R.rdims[R.rr] = x->shape[i];
+      R.rst[R.rr++] = x->strides[i];
+      nred *= x->shape[i];
+    } else {
+      R.kdims[R.kr] = x->shape[i];
+      R.kst[R.kr++] = x->strides[i];
+      nout *= x->shape[i];
+    }
+  }
+  if (numel(out) != nout) return set_error(KK_E_ARG, "reduce: out has %lld elements, expected %lld",
+                                           (long long)numel(out), (long long)nout);
+  R.nout = nout;
+  R.nred = nred;
+  if (nout == 0) return KK_OK;
+  if (nred == 0) {
+    // numpy: sum of nothing is 0, mean of nothing is NaN, max raises.
+    if (op == KK_REDUCE_MAX) return set_error(KK_E_ARG, "reduce: max over an empty axis");
+    return kk_fill(out, op == KK_REDUCE_SUM ? 0.0 : NAN);
+  }
+  // Fast path: contiguous x whose reduced axes are exactly the trailing ones.
+  bool trailing = is_contiguous(x);
+  {
+    bool seen_red = false;
+    for (int i = 0; i < x->rank && trailing; ++i) {
+      const bool red = axes_mask & (1u << i);
+      if (red) seen_red = true;
+      else if (seen_red && x->shape[i] != 1) trailing = false;
+    }
+  }
+  RowShape rs;
+  const bool vec_ok = (nred % 4 == 0) && aligned16(x->data);
+  if (trailing && pick_row_shape(nred, vec_ok, &rs)) {
+    KK_ROW_DISPATCH(reduce_rows_kernel, rs, nout, static_cast<float*>(out->data),
+                    static_cast<const float*>(x->data), nout, nred, op);
+    return check_launch("reduce_rows_kernel");
+  }
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(nout, 256), 65535));
+  hipLaunchKernelGGL(reduce_generic_kernel, dim3(grid), dim3(256), 0, ctx().stream,
+                     static_cast<float*>(out->data), static_cast<const float*>(x->data), R, op);
+  return check_launch("reduce_generic_kernel");
+}
+
+}  // extern "C"

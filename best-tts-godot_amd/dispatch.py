@@ -1,0 +1,278 @@
+"""Drop-in op dispatch: ``dispatch(op, node_input, node_output, attrs, env)``.
+
+Same signature, op names, attribute names and defaults as the reference's
+``RefRuntime.dispatch`` (tools/ref_runtime.py:428-668): `env` maps tensor
+names to values, inputs are read by name (``""`` = absent), outputs are
+written by name.  Values are :class:`DeviceTensor` for tensor data on the
+GPU; numpy arrays are host values.
+
+Placement follows the reference's GPU executor: float tensors are computed
+on the device by libkk's HIP kernels; small integer/bool "shape-domain"
+tensors (shapes, axes, indices, sizes) live on the host and the ops that
+only touch them run there, as executor.gd places its 409 CPU shape nodes
+(executor.gd:483-518 -> cpu_ops.gd:66-140).  A float op given host data
+uploads it first; nothing float is ever computed on the host.
+
+fp16 is storage only (tools/NOTES.md:44-59): fp16 data is widened to fp32 on
+the device when it enters a device op, every float result is fp32, and
+Cast(to=float16) yields fp32.
+"""
+import numpy as np
+
+from . import ops
+from .tensor import DeviceTensor
+
+# ONNX TensorProto element types -> numpy (ref_runtime.py:24-28)
+ONNX_DTYPE = {
+    1: np.float32, 2: np.uint8, 3: np.int8, 4: np.uint16, 5: np.int16,
+    6: np.int32, 7: np.int64, 9: np.bool_, 10: np.float16, 11: np.float64,
+    12: np.uint32, 13: np.uint64,
+}
+
+# Ops whose integer/bool host inputs are shape-domain data computed on the
+# host (cpu_ops.gd:66-140 lists the same family).
+_HOST_OPS = {
+    "Shape", "Reshape", "Unsqueeze", "Squeeze", "Concat", "Slice", "Gather",
+    "Cast", "Equal", "Where", "Range", "Greater", "Less", "GreaterOrEqual",
+    "And", "Add", "Sub", "Mul", "Div", "Transpose", "NonZero", "Expand",
+    "ConstantOfShape", "Split", "CumSum",
+}
+
+
+def _is_dev(v):
+    return isinstance(v, DeviceTensor)
+
+
+def to_device(v):
+    """Device copy of a host value; fp16 data is widened to fp32 on the GPU."""
+    if v is None or _is_dev(v):
+        return v
+    arr = np.asarray(v)
+    if arr.dtype == np.float64:
+        raise TypeError("float64 host data has no device type (fp32 compute only)")
+    t = DeviceTensor.from_numpy(arr)
+    return t
+
+
+def _f32(t):
+    """_f32 of the reference (ref_runtime.py:49-51): widen fp16 storage."""
+    if t is not None and t.dtype == np.float16:
+        return t.astype(np.float32)
+    return t
+
+
+def to_host(v):
+    """Host array of a value (a device value is downloaded: a sync point)."""
+    if _is_dev(v):
+        return v.numpy()
+    return v
+
+
+def _host_int(v):
+    return v is not None and not _is_dev(v) and np.asarray(v).dtype.kind in "iub"
+
+
+def _slice_params(dim, s, e, st):
+    """Clamp like op_slice (ref_runtime.py:307-325) and resolve the python
+    slice to (start, stop, step) of the selected range."""
+    if st > 0:
+        s = min(max(s if s >= 0 else s + dim, 0), dim)
+        e = min(max(e if e >= 0 else e + dim, 0), dim)
+    else:
+        s = min(max(s if s >= 0 else s + dim, -1), dim - 1)
+        e = min(max(e if e >= 0 else e + dim, -1), dim - 1)
+    r = range(dim)[slice(s, e, st)]
+    return r.start, r.stop, r.step, len(r)
+
+
+def dispatch(op, node_input, node_output, at, env):
+    """Execute one node.  Mirrors tools/ref_runtime.py:428-668."""
+
+    def inp(i, default=None):
+        if i >= len(node_input) or not node_input[i]:
+            return default
+        return env[node_input[i]]
+
+    x = inp(0)
+    y = inp(1)
+
+    # ---------------------------------------------------- host shape domain
+    if op in _HOST_OPS:
+        vals = [inp(i) for i in range(len(node_input))]
+        present = [v for v in vals if v is not None]
+        if present and all(_host_int(v) for v in present) and op != "Shape":
+            from . import hostops
+            hostops.run(op, node_input, node_output, at, env)
+            return
+
+    out = None
+    # ------------------------------------------------ elementwise / math
+    if op in ("Add", "Sub", "Mul", "Div", "Pow"):
+        out = ops.binary(op, to_device(x), to_device(y))
+    elif op in ("Sqrt", "Exp", "Sin", "Cos", "Atan", "Tanh", "Sigmoid", "Floor", "Round", "Erf"):
+        out = ops.unary(op, to_device(x))
+    elif op == "LeakyRelu":
+        out = ops.unary(op, to_device(x), np.float32(at.get("alpha", 0.01)))
+    elif op == "Clip":
+        lo, hi = inp(1), inp(2)
+        out = ops.clip(to_device(x), to_device(lo), to_device(hi))
+
+    # --------------------------------------------- comparison / logic
+    elif op in ("Equal", "Greater", "Less", "GreaterOrEqual", "And"):
+        out = ops.binary(op, to_device(x), to_device(y))
+    elif op == "Where":
+        out = ops.where(to_device(x), to_device(y), to_device(inp(2)))
+
+    # --------------------------------------------------- shape / layout
+    elif op == "Shape":
+        s = np.array(x.shape, dtype=np.int64)
+        out = s[at.get("start", 0):at.get("end", len(s))]
+    elif op == "Reshape":
+        shape = [int(v) for v in np.asarray(to_host(y)).reshape(-1)]
+        if not at.get("allowzero", 0):
+            shape = [x.shape[i] if v == 0 else v for i, v in enumerate(shape)]
+        out = x.reshape(shape)
+    elif op == "Transpose":
+        out = x.transpose(at.get("perm"))
+    elif op == "Unsqueeze":
+        axes = inp(1) if len(node_input) > 1 else at.get("axes")
+        for a in sorted(int(v) for v in np.asarray(to_host(axes)).reshape(-1)):
+            x = x.expand_dims(a)
+        out = x
+    elif op == "Squeeze":
+        axes = inp(1) if len(node_input) > 1 else at.get("axes")
+        out = x.squeeze(None if axes is None else
+                        [int(v) for v in np.asarray(to_host(axes)).reshape(-1)])
+    elif op == "Concat":
+        vals = [to_device(env[i]) for i in node_input if i]
+        if any(v.dtype == np.float16 for v in vals):
+            vals = [_f32(v) for v in vals]
+        axis = int(at["axis"]) % vals[0].ndim
+        dt = np.result_type(*[v.dtype for v in vals])
+        shape = list(vals[0].shape)
+        shape[axis] = sum(v.shape[axis] for v in vals)
+        out = DeviceTensor.empty(shape, dt)
+        pos = 0
+        for v in vals:
+            n = v.shape[axis]
+            if n:
+                ops.copy_into(out.slice_axis(axis, pos, pos + n), v)
+            pos += n
+    elif op == "Split":
+        axis = int(at.get("axis", 0)) % x.ndim
+        split = inp(1)
+        dim = x.shape[axis]
+        if split is None:
+            n = len(node_output)
+            q, r = divmod(dim, n)
+            sizes = [q + 1] * r + [q] * (n - r)
+        else:
+            sizes = [int(v) for v in np.asarray(to_host(split)).reshape(-1)]
+        # np.split at the running sums: the last part runs to the end.
+        pos = 0
+        for k, (name, sz) in enumerate(zip(node_output, sizes)):
+            lo = min(pos, dim)
+            hi = dim if k == len(sizes) - 1 else min(max(pos + sz, lo), dim)
+            if name:
+                env[name] = x.slice_axis(axis, lo, hi)
+            pos += sz
+        return
+    elif op == "Slice":
+        starts = np.asarray(to_host(inp(1))).reshape(-1)
+        ends = np.asarray(to_host(inp(2))).reshape(-1)
+        axes = inp(3)
+        steps = inp(4)
+        axes = list(range(len(starts))) if axes is None else np.asarray(to_host(axes)).reshape(-1)
+        steps = [1] * len(starts) if steps is None else np.asarray(to_host(steps)).reshape(-1)
+        out = x
+        for s, e, a, st in zip(starts, ends, axes, steps):
+            a = int(a) % x.ndim
+            start, _, step, n = _slice_params(x.shape[a], int(s), int(e), int(st))
+            out = out.slice_axis(a, start, start + n * step, step) if n else \
+                out.slice_axis(a, 0, 0)
+    elif op == "Gather":
+        axis = int(at.get("axis", 0))
+        idx = y
+        if not _is_dev(idx):
+            idx = np.asarray(idx).astype(np.int64)
+            dim = x.shape[axis]
+            if idx.size and (idx.min() < -dim or idx.max() >= dim):
+                raise IndexError(f"index out of bounds for axis {axis} with size {dim}")
+        out = ops.gather(to_device(x), to_device(idx), axis)
+    elif op == "Expand":
+        shape = np.broadcast_shapes(x.shape, tuple(int(v) for v in to_host(y)))
+        out = to_device(x).broadcast_to(shape).contiguous()
+    elif op == "ConstantOfShape":
+        v = at.get("value", np.array([0], dtype=np.float32))
+        v = np.asarray(v)
+        dt = np.float32 if v.dtype == np.float16 else v.dtype
+        shape = [int(s) for s in to_host(x)]
+        out = ops.fill(shape, v.reshape(-1)[0], dt)
+    elif op == "Cast":
+        to = ONNX_DTYPE[at["to"]]
+        dt = np.float32 if to == np.float16 else to
+        if _is_dev(x) and x.dtype == dt:
+            out = x
+        else:
+            out = to_device(x).astype(dt)
+
+    # --------------------------------------------- reductions / norms
+    elif op in ("ReduceMean", "ReduceSum"):
+        axes = inp(1) if len(node_input) > 1 else at.get("axes")
+        keep = bool(at.get("keepdims", 1))
+        v = _f32(to_device(x))
+        if axes is None:
+            if at.get("noop_with_empty_axes", 0):
+                out = v
+            else:
+                out = ops.reduce(op, v, range(v.ndim), keep)
+        else:
+            axes_t = [int(a) for a in np.asarray(to_host(axes)).reshape(-1)]
+            out = v if not axes_t else ops.reduce(op, v, axes_t, keep)
+    elif op == "Softmax":
+        out = ops.softmax(_f32(to_device(x)), at.get("axis", -1))
+    elif op == "LayerNormalization":
+        out = ops.layernorm(_f32(to_device(x)), _f32(to_device(y)),
+                            _f32(to_device(inp(2))), at.get("axis", -1),
+                            at.get("epsilon", 1e-5))
+    elif op == "SkipLayerNormalization":
+        out = ops.layernorm(_f32(to_device(x)), _f32(to_device(inp(2))),
+                            _f32(to_device(inp(3))), -1, at.get("epsilon", 1e-12),
+                            skip=_f32(to_device(y)), skip_bias=_f32(to_device(inp(4))))
+    elif op == "FastGelu":
+        out = ops.fast_gelu(to_device(x), to_device(y))
+
+    # --------------------------------------------------- matmul / conv
+    elif op == "MatMul":
+        out = ops.matmul(to_device(x), to_device(y))
+    elif op == "FusedMatMul":
+        a, b = to_device(x), to_device(y)
+        if at.get("transA", 0):
+            a = a.transpose(list(range(a.ndim - 2)) + [a.ndim - 1, a.ndim - 2])
+        if at.get("transB", 0):
+            b = b.transpose(list(range(b.ndim - 2)) + [b.ndim - 1, b.ndim - 2])
+        out = ops.matmul(a, b, alpha=np.float32(at.get("alpha", 1.0)))
+    elif op == "DequantizeLinear":
+        out = ops.dequantize(to_device(x), to_device(y), to_device(inp(2)))
+    elif op == "Conv":
+        out = ops.conv1d(_f32(to_device(x)), to_device(y), _f32(to_device(inp(2))),
+                         at.get("pads", [0, 0]), at.get("strides", [1])[0],
+                         at.get("dilations", [1])[0], at.get("group", 1))
+    elif op == "ConvTranspose":
+        out = ops.conv_transpose1d(_f32(to_device(x)), to_device(y), _f32(to_device(inp(2))),
+                                   at.get("pads", [0, 0]), at.get("strides", [1])[0],
+                                   at.get("dilations", [1])[0], at.get("group", 1),
+                                   at.get("output_padding", [0])[0])
+
+    # -------------------------------------- fused composites (libkk only)
+    elif op == "Snake":
+        # x + recip * sin(alpha * x)^2: the Mul/Sin/Pow/Mul/Add chain fused.
+        out = ops.snake(to_device(x), to_device(y), to_device(inp(2)))
+    elif op == "AdaIN":
+        # inputs: x, style, W, bias; attribute epsilon.
+        out = ops.adain(to_device(x), to_device(y), to_device(inp(2)),
+                        to_device(inp(3)), at.get("epsilon", 1e-5))
+    else:
+        raise NotImplementedError(f"{op}")
+
+    env[node_output[0]] = out

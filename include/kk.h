@@ -1,0 +1,224 @@
+/*
+ * kk.h -- C ABI of libkk, the MI355X (gfx950) tensor-op layer for the
+ * quantized Kokoro-82M graph.
+ *
+ * libkk replaces the numpy op layer `RefRuntime.dispatch`
+ * (tools/ref_runtime.py:428-668) and the GLSL twin of that layer
+ * (addons/best-tts/runtime/executor.gd:733-843 over runtime/gpu.gd:233-249).
+ * A host-side `dispatch(op, node_input, node_output, attrs, env)` with the
+ * reference's signature calls these entry points through ctypes.
+ *
+ * Conventions
+ *  - Every entry point returns 0 on success and a negative KK_E* code on
+ *    failure; it never aborts.  kk_last_error() describes the last failure of
+ *    the calling thread.
+ *  - All work is enqueued on the library's one HIP stream, in call order.
+ *    kk_download() and kk_sync() wait for it; nothing else blocks.
+ *  - Tensors are described by kk_tensor: a device pointer to element
+ *    [0,...,0], a dtype code and up to KK_MAX_RANK extents and element
+ *    strides.  A stride of 0 marks a broadcast axis.  Shapes follow numpy:
+ *    inputs of an elementwise op are right-aligned against the output shape.
+ *  - Arithmetic is fp32 whatever the storage type (fp16 is storage only,
+ *    tools/NOTES.md:44-59).
+ */
+#ifndef KK_H
+#define KK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KK_MAX_RANK 8
+
+/* dtype codes: the KPK1 codes of tools/kpk_runtime.py:21-24
+ * (also tools/pack_model.py:38-44). */
+enum {
+  KK_F32 = 0, KK_I8 = 1, KK_U8 = 2, KK_I32 = 3, KK_I64 = 4, KK_BOOL = 5,
+  KK_F16 = 6
+};
+
+/* status codes */
+enum {
+  KK_OK = 0,
+  KK_E_ARG = -1,      /* invalid argument, shape or dtype */
+  KK_E_HIP = -2,      /* a HIP runtime call failed */
+  KK_E_NOMEM = -3,    /* device allocation failed */
+  KK_E_STATE = -4,    /* library not initialised, or double free */
+  KK_E_UNSUPPORTED = -5
+};
+
+typedef struct kk_tensor {
+  void*   data;                     /* device address of element [0,..,0] */
+  int32_t dtype;                    /* KK_F32 .. KK_F16 */
+  int32_t rank;                     /* 0 .. KK_MAX_RANK */
+  int64_t shape[KK_MAX_RANK];
+  int64_t strides[KK_MAX_RANK];     /* in elements; 0 = broadcast */
+} kk_tensor;
+
+/* ---------------------------------------------------------------- lifecycle
+ * Replaces KokoroGPU.initialize/cleanup/submit_and_wait
+ * (addons/best-tts/runtime/gpu.gd:35-41, 266-268): one device, one stream. */
+int         kk_init(int device);
+int         kk_shutdown(void);
+int         kk_sync(void);
+const char* kk_last_error(void);
+int         kk_device_count(int* count);
+
+/* --------------------------------------------------------------- buffer pool
+ * Replaces the executor's pool: _bucket/_alloc/_release/trim_memory
+ * (addons/best-tts/runtime/executor.gd:206-268, 400-425) and numpy's
+ * per-op allocation (tools/ref_runtime.py:668).  Sizes are rounded up to a
+ * bucket that keeps four significant bits (256 B minimum); freed buffers are
+ * kept per bucket and handed out again; a second free of one buffer is
+ * rejected with KK_E_STATE. */
+int kk_alloc(size_t bytes, void** dptr);
+int kk_free(void* dptr);
+int kk_pool_stats(size_t* live_bytes, size_t* pooled_bytes,
+                  size_t* peak_live_bytes);
+int kk_pool_trim(size_t budget_bytes);
+/* Host <-> device copies (gpu.gd:88-103 create_buffer / read_f32).
+ * Both return after the copy has completed. */
+int kk_upload(void* dst_device, const void* src_host, size_t bytes);
+int kk_download(void* dst_host, const void* src_device, size_t bytes);
+
+/* ------------------------------------------------------ elementwise family
+ * Broadcast elementwise ops, the Add/Sub/Mul/Div/Pow/... branches of
+ * tools/ref_runtime.py:446-503 and the GLSL twin elementwise.glsl:43-160
+ * with its broadcast indexer runtime/ops.gd:45-129.  `out` may be strided
+ * (writes into a view) but must not broadcast. */
+enum {
+  KK_OP_ADD = 0, KK_OP_SUB = 1, KK_OP_MUL = 2, KK_OP_DIV = 3, KK_OP_POW = 4,
+  KK_OP_SQRT = 5, KK_OP_EXP = 6, KK_OP_SIN = 7, KK_OP_COS = 8,
+  KK_OP_ATAN = 9, KK_OP_TANH = 10, KK_OP_SIGMOID = 11, KK_OP_FLOOR = 12,
+  KK_OP_ROUND = 13, KK_OP_LEAKYRELU = 14, KK_OP_EQUAL = 16,
+  KK_OP_GREATER = 17, KK_OP_LESS = 18, KK_OP_GEQ = 19, KK_OP_AND = 20,
+  KK_OP_NEG = 25, KK_OP_ABS = 26, KK_OP_LOG = 27, KK_OP_MIN = 28,
+  KK_OP_MAX = 29, KK_OP_ERF = 30, KK_OP_IDENTITY = 24
+};
+
+/* Add/Sub/Mul/Div/Pow/Min/Max and comparisons: ref_runtime.py:446-457,
+ * 492-501.  Float inputs (f32/f16) compute in fp32; two integer inputs
+ * compute in int64 with Div as floor division (:453-455). */
+int kk_binary(int op, const kk_tensor* out, const kk_tensor* a,
+              const kk_tensor* b);
+/* Sqrt/Exp/Sin/Cos/Atan/Tanh/Sigmoid/Floor/Round/LeakyRelu/Neg/Abs/Log/Erf:
+ * ref_runtime.py:458-479, 487-489.  `alpha` is LeakyRelu's slope. */
+int kk_unary(int op, const kk_tensor* out, const kk_tensor* x, float alpha);
+/* Where(cond, x, y): ref_runtime.py:502-503. */
+int kk_where(const kk_tensor* out, const kk_tensor* cond, const kk_tensor* x,
+             const kk_tensor* y);
+/* Clip(x, lo, hi), lo/hi may be NULL: ref_runtime.py:480-486. */
+int kk_clip(const kk_tensor* out, const kk_tensor* x, const kk_tensor* lo,
+            const kk_tensor* hi);
+/* Fused snake activation y = x + r * sin(alpha*x)^2, the five-node chain
+ * Mul -> Sin -> Pow(2) -> Mul(recip) -> Add of the graph (kpk #2853-2857,
+ * built from ref_runtime.py:446-463).  If `recip` is NULL, r = 1/alpha in
+ * fp32.  alpha/recip broadcast like any operand (normally [1,C,1]). */
+int kk_snake(const kk_tensor* out, const kk_tensor* x, const kk_tensor* alpha,
+             const kk_tensor* recip);
+/* FastGelu(x, bias): ref_runtime.py:288-293; bias may be NULL. */
+int kk_fast_gelu(const kk_tensor* out, const kk_tensor* x,
+                 const kk_tensor* bias);
+/* DequantizeLinear: (q - zp) * scale in fp32, ref_runtime.py:631-636;
+ * zp may be NULL. */
+int kk_dequantize(const kk_tensor* out, const kk_tensor* q,
+                  const kk_tensor* scale, const kk_tensor* zp);
+
+/* ------------------------------------------------------------ data movement
+ * Strided copy with dtype conversion.  Serves Cast (ref_runtime.py:572-578:
+ * fp16 targets store fp32, float->int truncates), Transpose/Expand/Concat
+ * materialisation (:517-518, :531-535, :553-555) and the copy.glsl twin.
+ * `x` may broadcast against `out`. */
+int kk_copy(const kk_tensor* out, const kk_tensor* x);
+/* ConstantOfShape / zero fill (ref_runtime.py:556-559). */
+int kk_fill(const kk_tensor* out, double value);
+/* Gather: np.take(data, indices, axis) (ref_runtime.py:550-552), the GLSL
+ * twin gather.glsl.  Negative indices count from the end; indices outside
+ * [-dim, dim) are clamped on the device (the host checks host-side ones). */
+int kk_gather(const kk_tensor* out, const kk_tensor* data,
+              const kk_tensor* indices, int axis);
+
+/* ------------------------------------------------------------- reductions
+ * ReduceMean/ReduceSum/ReduceMax over the axes in `axes_mask` (bit i =
+ * axis i of x): ref_runtime.py:589-598.  `out` holds the kept axes in
+ * order (keepdims is a view question for the caller). */
+enum { KK_REDUCE_SUM = 0, KK_REDUCE_MEAN = 1, KK_REDUCE_MAX = 2 };
+int kk_reduce(int op, const kk_tensor* out, const kk_tensor* x,
+              uint32_t axes_mask);
+/* Instance norm over the last axis of x [N,C,T] with the AdaIN affine:
+ *   y = (x - mean_T) / sqrt(var_T + eps) * (1 + gamma[c]) + beta[c]
+ * (graph kpk #2844-2852: ReduceMean, Sub, Mul, ReduceMean, Add, Sqrt, Div,
+ * Mul(1+gamma), Add(beta)).  gamma_beta is h = [gamma | beta] of 2C floats
+ * (the Split of kpk #80 -> #138); NULL gives gamma = beta = 0. */
+int kk_instance_norm_affine(const kk_tensor* out, const kk_tensor* x,
+                            const kk_tensor* gamma_beta, float eps);
+/* AdaIN with the style Linear fused: h = style . W + b with W [S, 2C]
+ * (any strides), then kk_instance_norm_affine on x [N,C,T].  bias may be
+ * NULL.  W may be f32, f16 or int8/uint8 with w_scale/w_zp (per tensor or
+ * per column, as kk_gemm). */
+int kk_adain(const kk_tensor* out, const kk_tensor* x, const kk_tensor* style,
+             const kk_tensor* w, const kk_tensor* w_scale,
+             const kk_tensor* w_zp, const kk_tensor* bias, float eps);
+/* LayerNormalization / SkipLayerNormalization: op_layernorm
+ * (ref_runtime.py:276-285) over axes [axis, rank), after s = x + skip
+ * (+ skip_bias) when skip is given (:604-609).  scale/bias broadcast over
+ * the normalised axes; bias may be NULL. */
+int kk_layernorm(const kk_tensor* out, const kk_tensor* x,
+                 const kk_tensor* skip, const kk_tensor* skip_bias,
+                 const kk_tensor* scale, const kk_tensor* bias, int axis,
+                 float eps);
+/* Softmax along `axis`: op_softmax (ref_runtime.py:269-273). */
+int kk_softmax(const kk_tensor* out, const kk_tensor* x, int axis);
+
+/* ----------------------------------------------------------- contractions
+ * Batched matmul out = alpha * a @ deq(w) with numpy batch broadcasting
+ * (MatMul ref_runtime.py:614-615, FusedMatMul :616-622 with transA/transB
+ * expressed as swapped strides).  deq(w) = (w - w_zp) * w_scale in fp32
+ * for int8/uint8 w (DequantizeLinear :631-636, op_lstm.deq :154-158);
+ * scale/zp are per tensor (one element) or per column (N elements).  f32
+ * and f16 w take no scale.  Accumulation is fp32. */
+int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w,
+            const kk_tensor* w_scale, const kk_tensor* w_zp, float alpha);
+/* Conv1d: op_conv1d forward (ref_runtime.py:58-82, 101-103).  x [N,Cin,L],
+ * w [Cout, Cin/group, K] (f32/f16, or int8/uint8 dequantized with a
+ * per-tensor or per-output-channel scale/zp), bias [Cout] or NULL. */
+int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+              const kk_tensor* w_scale, const kk_tensor* w_zp,
+              const kk_tensor* bias, int stride, int dilation, int pad0,
+              int pad1, int group);
+/* ConvTranspose1d: op_conv1d transposed (ref_runtime.py:83-99).
+ * w [Cin, Cout/group, K]. */
+int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x,
+                        const kk_tensor* w, const kk_tensor* w_scale,
+                        const kk_tensor* w_zp, const kk_tensor* bias,
+                        int stride, int dilation, int pad0, int pad1,
+                        int group, int output_padding);
+
+/* -------------------------------------------------------------- timing
+ * HIP events on the library stream, for measuring kernels where they run.
+ * Slots 0..KK_MAX_EVENTS-1.  No counterpart in the reference, which has no
+ * GPU timestamps (only Time.get_ticks_msec on the host). */
+#define KK_MAX_EVENTS 16
+int kk_event_record(int slot);
+int kk_event_elapsed(int start_slot, int stop_slot, float* ms);
+
+/* ---------------------------------------------------------- HIP graphs
+ * Records the ops called between kk_graph_begin and kk_graph_end on the
+ * library stream into a HIP graph that kk_graph_launch replays -- the
+ * replacement for the reference's recorded Vulkan compute list
+ * (addons/best-tts/runtime/gpu.gd:227-262) when a node sequence repeats.
+ * While recording, kk_alloc/kk_upload/kk_download/kk_sync fail: every
+ * buffer a graph touches must exist before kk_graph_begin and stay
+ * allocated while the graph may be launched. */
+int kk_graph_begin(void);
+int kk_graph_end(int* graph_id);
+int kk_graph_launch(int graph_id);
+int kk_graph_destroy(int graph_id);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KK_H */

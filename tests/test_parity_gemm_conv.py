@@ -1,0 +1,267 @@
+"""Parity of the contractions -- weight-dequant MatMul, Conv1d and
+ConvTranspose1d -- with the oracle, on the GPU through the C ABI.
+
+Bar: |got - ref| <= 1e-4*|ref| + 1e-5*max|ref|.  Both sides accumulate in
+fp32 but in different orders (numpy: OpenBLAS / einsum loops; libkk: MFMA
+tiles), so the absolute floor scales with the size of the terms: for K in
+the thousands an element whose exact value is near zero still carries
+~sqrt(K)*eps*|partial sums| of rounding on either side.  Each test also
+checks that the worst relative error over elements with |ref| >= 1% of
+max|ref| stays below 1e-4."""
+import numpy as np
+import pytest
+
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+RTOL, FLOOR = 1e-4, 1e-5
+
+
+def check(got, want, what):
+    assert_close(got, want, RTOL, floor_rel=FLOOR, what=what)
+    w = np.abs(np.asarray(want, np.float64))
+    big = w >= 0.01 * w.max()
+    rel = np.abs(np.asarray(got, np.float64) - want)[big] / w[big]
+    assert rel.max() < 1e-4, f"{what}: worst relative error {rel.max():.2e} on large elements"
+
+
+def int8_weight(r, shape):
+    q = r.integers(-127, 128, shape).astype(np.int8)
+    s = np.float32(r.uniform(1e-3, 1e-2))
+    return q, s
+
+
+# -------------------------------------------------- dequant GEMM workloads
+@pytest.mark.parametrize("m,k,n", [(256, 768, 2048), (256, 2048, 768)])
+def test_int8_matmul_config(gpu, oracle, m, k, n):
+    """A ~ N(0,1); W ~ U{-127..127} int8, per-tensor scale ~ U(1e-3,1e-2),
+    zero point 0: DequantizeLinear then MatMul."""
+    r = rng(0)
+    a = r.normal(0, 1, (m, k)).astype(np.float32)
+    q, s = int8_weight(r, (k, n))
+    zp = np.int8(0)
+    got = gpu.ops.matmul(gpu.to_device(a), gpu.to_device(q), gpu.to_device(np.array(s)),
+                         gpu.to_device(np.array(zp))).numpy()
+    want = oracle.matmul(a, oracle.dequantize(q, s, zp))
+    check(got, want, f"int8 matmul {m}x{k}x{n}")
+
+
+def test_fp16_matmul_config(gpu, oracle):
+    r = rng(0)
+    a = r.normal(0, 1, (256, 768)).astype(np.float32)
+    w = r.normal(0, 0.02, (768, 768)).astype(np.float16)
+    env = {"a": gpu.to_device(a), "w": gpu.to_device(w)}
+    gpu.dispatch("MatMul", ["a", "w"], ["y"], {}, env)
+    check(env["y"].numpy(), oracle.matmul(a, w), "fp16 matmul")
+
+
+def test_per_column_dequant_u8_and_i8(gpu, oracle):
+    r = rng(1)
+    a = r.normal(0, 1, (130, 128)).astype(np.float32)
+    q = r.integers(-127, 128, (128, 1028)).astype(np.int8)
+    sc = r.uniform(1e-3, 1e-2, 1028).astype(np.float32)
+    zp = r.integers(-3, 4, 1028).astype(np.int8)
+    got = gpu.ops.matmul(gpu.to_device(a), gpu.to_device(q), gpu.to_device(sc),
+                         gpu.to_device(zp)).numpy()
+    check(got, oracle.matmul(a, oracle.dequantize(q, sc, zp)), "int8 per-column")
+    u = r.integers(0, 256, (128, 96)).astype(np.uint8)
+    got = gpu.ops.matmul(gpu.to_device(a), gpu.to_device(u), gpu.to_device(np.float32(0.01)),
+                         gpu.to_device(np.uint8(128))).numpy()
+    check(got, oracle.matmul(a, oracle.dequantize(u, np.float32(0.01), np.uint8(128))), "uint8")
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 13, 5), (33, 65, 97), (130, 512, 50),
+                                   (64, 64, 64)])
+def test_matmul_odd_shapes(gpu, oracle, m, k, n):
+    r = rng(2)
+    a = r.normal(0, 1, (m, k)).astype(np.float32)
+    w = r.normal(0, 0.1, (k, n)).astype(np.float32)
+    check(gpu.ops.matmul(gpu.to_device(a), gpu.to_device(w)).numpy(), oracle.matmul(a, w),
+          f"matmul {m}x{k}x{n}")
+
+
+def test_attention_batched_and_fused(gpu, oracle):
+    """[1,12,T,64] x [1,12,64,T] with the right operand a transposed view,
+    FusedMatMul with transB and alpha, and vector operands."""
+    r = rng(3)
+    t = 130
+    q = r.normal(0, 1, (1, 12, t, 64)).astype(np.float32)
+    kx = r.normal(0, 1, (1, 12, t, 64)).astype(np.float32)
+    env = {"q": gpu.to_device(q), "k": gpu.to_device(kx)}
+    gpu.dispatch("Transpose", ["k"], ["kt"], {"perm": [0, 1, 3, 2]}, env)
+    gpu.dispatch("MatMul", ["q", "kt"], ["s"], {}, env)
+    check(env["s"].numpy(), oracle.matmul(q, np.transpose(kx, (0, 1, 3, 2))), "QK^T")
+    gpu.dispatch("FusedMatMul", ["q", "k"], ["f"], {"transB": 1, "alpha": 0.125}, env)
+    check(env["f"].numpy(), oracle.fused_matmul(q, kx, 0, 1, 0.125), "FusedMatMul")
+    gpu.dispatch("FusedMatMul", ["k", "q"], ["g"], {"transA": 1}, env)
+    check(env["g"].numpy(), oracle.fused_matmul(kx, q, 1, 0, 1.0), "FusedMatMul transA")
+    v = r.normal(0, 1, 64).astype(np.float32)
+    env["v"] = gpu.to_device(v)
+    gpu.dispatch("MatMul", ["q", "v"], ["qv"], {}, env)
+    check(env["qv"].numpy(), oracle.matmul(q, v), "matrix @ vector")
+    w = r.normal(0, 1, (64, 40)).astype(np.float32)
+    env["w"] = gpu.to_device(w)
+    gpu.dispatch("MatMul", ["q", "w"], ["qw"], {}, env)
+    check(env["qw"].numpy(), oracle.matmul(q, w), "batched @ broadcast weight")
+
+
+# --------------------------------------------------------------- conv1d
+def test_int8_conv1d_config(gpu, oracle):
+    """x ~ N(0,1) [1,512,2400]; W int8 [512,512,3], per-tensor scale; pad 1."""
+    r = rng(0)
+    x = r.normal(0, 1, (1, 512, 2400)).astype(np.float32)
+    q, s = int8_weight(r, (512, 512, 3))
+    got = gpu.ops.conv1d(gpu.to_device(x), gpu.to_device(q), None, (1, 1),
+                         w_scale=gpu.to_device(np.array(s))).numpy()
+    want = oracle.conv1d(x, oracle.dequantize(q, s), None, (1, 1))
+    check(got, want, "int8 conv1d 512->512 k3")
+
+
+CONV = [  # (n, cin, cout, k, L, p0, p1, s, d, g, wdt)
+    (1, 256, 256, 3, 2400, 1, 1, 1, 1, 1, "i8"),
+    (1, 256, 256, 3, 2400, 3, 3, 1, 3, 1, "i8"),
+    (1, 256, 256, 3, 2400, 5, 5, 1, 5, 1, "f32"),
+    (2, 22, 256, 12, 600, 3, 3, 6, 1, 1, "f16"),
+    (1, 128, 22, 7, 480, 3, 3, 1, 1, 1, "f16"),
+    (1, 512, 512, 5, 130, 2, 2, 1, 1, 1, "u8"),
+    (1, 64, 64, 3, 101, 1, 0, 2, 1, 64, "f16"),
+    (1, 1090, 1090, 3, 50, 1, 1, 1, 1, 1090, "f32"),
+    (1, 12, 6, 4, 33, 0, 2, 3, 2, 3, "f32"),
+    (1, 1, 1, 3, 40, 1, 1, 2, 1, 1, "f32"),
+]
+
+
+@pytest.mark.parametrize("case", CONV)
+def test_conv1d_cases(gpu, oracle, case):
+    n, cin, cout, k, L, p0, p1, s, d, g, wdt = case
+    r = rng(4)
+    x = r.normal(0, 1, (n, cin, L)).astype(np.float32)
+    b = r.normal(0, 0.1, cout).astype(np.float32)
+    shape = (cout, cin // g, k)
+    ws = wz = None
+    if wdt == "i8":
+        w, sc = int8_weight(r, shape)
+        ws = np.array(sc)
+        wdeq = oracle.dequantize(w, sc)
+    elif wdt == "u8":
+        w = r.integers(0, 256, shape).astype(np.uint8)
+        ws, wz = np.array(np.float32(0.004)), np.array(np.uint8(114))
+        wdeq = oracle.dequantize(w, ws, wz)
+    else:
+        w = (r.normal(0, 0.05, shape)).astype(np.float16 if wdt == "f16" else np.float32)
+        wdeq = w
+    got = gpu.ops.conv1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (p0, p1), s, d, g,
+                         w_scale=gpu.to_device(ws) if ws is not None else None,
+                         w_zp=gpu.to_device(wz) if wz is not None else None).numpy()
+    check(got, oracle.conv1d(x, wdeq, b, (p0, p1), s, d, g), f"conv1d {case}")
+
+
+def test_conv_dispatch_f16(gpu, oracle):
+    r = rng(5)
+    x = r.normal(0, 1, (1, 128, 240)).astype(np.float32)
+    w = r.normal(0, 0.05, (22, 128, 7)).astype(np.float16)
+    b = r.normal(0, 0.1, 22).astype(np.float16)
+    env = {"x": gpu.to_device(x), "w": gpu.to_device(w), "b": gpu.to_device(b)}
+    at = {"pads": [3, 3], "strides": [1], "dilations": [1], "group": 1}
+    gpu.dispatch("Conv", ["x", "w", "b"], ["y"], at, env)
+    oenv = {"x": x, "w": w, "b": b}
+    oracle.dispatch("Conv", ["x", "w", "b"], ["y"], at, oenv)
+    check(env["y"].numpy(), oenv["y"], "Conv dispatch")
+
+
+# ------------------------------------------------------ conv transpose
+def test_int8_conv_transpose_config(gpu, oracle):
+    """x ~ N(0,1) [1,512,240]; W int8 [512,256,20]; stride 10, pad 5."""
+    r = rng(0)
+    x = r.normal(0, 1, (1, 512, 240)).astype(np.float32)
+    q, s = int8_weight(r, (512, 256, 20))
+    got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(q), None, (5, 5), 10,
+                                   w_scale=gpu.to_device(np.array(s))).numpy()
+    assert got.shape == (1, 256, 2400)
+    want = oracle.conv_transpose1d(x, oracle.dequantize(q, s), None, (5, 5), 10)
+    check(got, want, "int8 convT 512->256 k20 s10 p5")
+
+
+CONVT = [  # (n, cin, cout_g, k, L, p0, p1, s, d, g, op, wdt)
+    (1, 256, 128, 12, 300, 3, 3, 6, 1, 1, 0, "f16"),
+    (1, 22, 1, 20, 101, 0, 0, 5, 1, 1, 0, "f32"),
+    (1, 512, 1, 3, 40, 1, 1, 2, 1, 512, 1, "f16"),
+    (2, 8, 3, 5, 17, 2, 1, 3, 1, 1, 2, "f32"),
+    (1, 6, 4, 3, 9, 1, 1, 2, 2, 1, 0, "f32"),
+    (1, 4, 4, 4, 10, 0, 0, 1, 1, 1, 0, "i8"),
+    (1, 3, 2, 2, 8, 0, 0, 4, 1, 1, 3, "f32"),
+]
+
+
+@pytest.mark.parametrize("case", CONVT)
+def test_conv_transpose_cases(gpu, oracle, case):
+    n, cin, cout_g, k, L, p0, p1, s, d, g, op, wdt = case
+    r = rng(6)
+    x = r.normal(0, 1, (n, cin, L)).astype(np.float32)
+    b = r.normal(0, 0.1, cout_g * g).astype(np.float32)
+    shape = (cin, cout_g, k)
+    ws = None
+    if wdt == "i8":
+        w, sc = int8_weight(r, shape)
+        ws = np.array(sc)
+        wdeq = oracle.dequantize(w, sc)
+    else:
+        w = r.normal(0, 0.1, shape).astype(np.float16 if wdt == "f16" else np.float32)
+        wdeq = w
+    got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (p0, p1),
+                                   s, d, g, op,
+                                   w_scale=gpu.to_device(ws) if ws is not None else None).numpy()
+    check(got, oracle.conv_transpose1d(x, wdeq, b, (p0, p1), s, d, g, op), f"convT {case}")
+
+
+# ---------------------------------------------------- decoder stage chain
+def test_decoder_upsample_stage(gpu, oracle):
+    """int8 ConvTranspose1d(512->256, k20, s10, p5) on [1,512,240], snake,
+    AdaIN with style [1,128], then two residual blocks
+    AdaIN -> snake -> conv(d) -> AdaIN -> snake -> conv(d1) -> + x with
+    dilations 1 and 3 (int8 weights, per-tensor scales)."""
+    r = rng(0)
+    x = r.normal(0, 1, (1, 512, 240)).astype(np.float32)
+    style = r.normal(0, 0.1, (1, 128)).astype(np.float32)
+    qt, st = int8_weight(r, (512, 256, 20))
+    alphas = [r.uniform(0.5, 2, (1, 256, 1)).astype(np.float32) for _ in range(5)]
+    fcs = [r.normal(0, 0.05, (128, 512)).astype(np.float32) for _ in range(5)]
+    convs = [int8_weight(r, (256, 256, 3)) for _ in range(4)]
+
+    def run(lib):
+        if lib is None:
+            h = oracle.conv_transpose1d(x, oracle.dequantize(qt, st), None, (5, 5), 10)
+            h = oracle.snake(h, alphas[0])
+            h = oracle.adain(h, style, fcs[0], None, 1e-5)
+            for blk, dil in enumerate((1, 3)):
+                y = oracle.adain(h, style, fcs[1 + 2 * blk], None, 1e-5)
+                y = oracle.snake(y, alphas[1 + 2 * blk])
+                q, s = convs[2 * blk]
+                y = oracle.conv1d(y, oracle.dequantize(q, s), None, (dil, dil), 1, dil)
+                y = oracle.adain(y, style, fcs[2 + 2 * blk], None, 1e-5)
+                y = oracle.snake(y, alphas[2 + 2 * blk])
+                q, s = convs[2 * blk + 1]
+                y = oracle.conv1d(y, oracle.dequantize(q, s), None, (1, 1))
+                h = oracle.binary("Add", h, y)
+            return h
+        D = lib.to_device
+        sty = D(style)
+        h = lib.ops.conv_transpose1d(D(x), D(qt), None, (5, 5), 10, w_scale=D(np.array(st)))
+        h = lib.ops.snake(h, D(alphas[0]))
+        h = lib.ops.adain(h, sty, D(fcs[0]), None, 1e-5)
+        for blk, dil in enumerate((1, 3)):
+            y = lib.ops.adain(h, sty, D(fcs[1 + 2 * blk]), None, 1e-5)
+            y = lib.ops.snake(y, D(alphas[1 + 2 * blk]))
+            q, s = convs[2 * blk]
+            y = lib.ops.conv1d(y, D(q), None, (dil, dil), 1, dil, w_scale=D(np.array(s)))
+            y = lib.ops.adain(y, sty, D(fcs[2 + 2 * blk]), None, 1e-5)
+            y = lib.ops.snake(y, D(alphas[2 + 2 * blk]))
+            q, s = convs[2 * blk + 1]
+            y = lib.ops.conv1d(y, D(q), None, (1, 1), w_scale=D(np.array(s)))
+            h = lib.ops.binary("Add", h, y)
+        return h.numpy()
+
+    got, want = run(gpu), run(None)
+    # Five normalisations in series amplify per-op rounding; the chain is
+    # held to 10x the single-op bar.
+    assert_close(got, want, 1e-3, floor_rel=1e-4, what="decoder stage")
