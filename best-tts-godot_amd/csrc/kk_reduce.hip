@@ -168,12 +168,14 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
     if (row >= rows) return;
   }
   const int64_t c = row % C;
-  float gamma = 0.0f, beta = 0.0f;
-  if (mode == 2) style_affine<GROUP>(sa, C, c, g, lds, gamma, beta);
-  else if (mode == 1) { gamma = gb[c]; beta = gb[C + c]; }
+  // Issue the row's loads first so the style projection's latency hides
+  // under them.
   const float* xr = x + row * T;
   float r[NV][VEC];
   load_row<GROUP, NV, VEC>(xr, T, g, r);
+  float gamma = 0.0f, beta = 0.0f;
+  if (mode == 2) style_affine<GROUP>(sa, C, c, g, lds, gamma, beta);
+  else if (mode == 1) { gamma = gb[c]; beta = gb[C + c]; }
   float mean, var;
   row_stats<GROUP, NV, VEC>(r, T, g, lds, mean, var);
   const float den = sqrtf(var + eps);

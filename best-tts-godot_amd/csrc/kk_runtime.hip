@@ -70,6 +70,7 @@ int64_t numel(const kk_tensor* t) {
 }
 
 bool is_contiguous(const kk_tensor* t) {
+  if (numel(t) == 0) return true;
   int64_t acc = 1;
   for (int i = t->rank - 1; i >= 0; --i) {
     if (t->shape[i] != 1 && t->strides[i] != acc) return false;
@@ -96,10 +97,11 @@ int make_plan(Plan* p, const kk_tensor* out, const kk_tensor* const* ins, int ni
   p->nops = nins + 1;
   int64_t dims[KK_MAX_RANK];
   int64_t st[kMaxOperands][KK_MAX_RANK];
+  const bool empty = numel(out) == 0;  // nothing is walked: strides are moot
   for (int i = 0; i < r; ++i) {
     dims[i] = out->shape[i];
     st[0][i] = out->strides[i];
-    if (out->shape[i] != 1 && out->strides[i] == 0)
+    if (!empty && out->shape[i] != 1 && out->strides[i] == 0)
       return set_error(KK_E_ARG, "output must not broadcast (axis %d has stride 0)", i);
   }
   for (int k = 0; k < nins; ++k) {

@@ -111,7 +111,9 @@ class DeviceTensor:
 
     @classmethod
     def from_numpy(cls, arr):
-        arr = np.ascontiguousarray(arr)
+        arr = np.asarray(arr)
+        if not arr.flags.c_contiguous:  # (np.ascontiguousarray would make 0-d arrays 1-d)
+            arr = arr.copy(order="C")
         if arr.dtype not in NP_TO_CODE:
             raise TypeError(f"unsupported dtype {arr.dtype}")
         t = cls.empty(arr.shape, arr.dtype)
@@ -138,6 +140,8 @@ class DeviceTensor:
         return NP_TO_CODE[self.dtype]
 
     def is_contiguous(self):
+        if self.size == 0:
+            return True
         acc = 1
         for d, s in zip(reversed(self.shape), reversed(self.strides)):
             if d != 1 and s != acc:
