@@ -2,15 +2,21 @@
 //
 // One engine serves every elementwise node: the host plans the launch
 // (broadcast strides, unit-axis removal, contiguous-axis merging) and picks
-//  * ew_inner<OP, NIN, VEC, Idx>: all operands fp32, the collapsed innermost
-//    axis is contiguous (stride 1) or broadcast (stride 0) for every operand.
-//    Each thread owns VEC consecutive elements of a row (128-bit loads when
-//    VEC == 4); the row offset of each operand comes from a div/mod walk over
-//    the outer axes, once per VEC elements.  This covers the hot shapes:
-//    x [1,C,L] op per-channel [1,C,1] collapses to rank 2 with strides
-//    (L,1) and (1,0).
+//  * fast paths, all operands fp32 with the collapsed innermost axis
+//    contiguous (stride 1) or broadcast (stride 0) for every operand; each
+//    thread owns VEC consecutive elements of a row (128-bit non-temporal
+//    loads and stores when VEC == 4):
+//      ew_rows<OP, NIN, VEC>      rank <= 2, rows on blockIdx.y.  The hot
+//                                 shapes land here: x [1,C,L] op [1,C,1]
+//                                 collapses to [C, L] with strides (L,1) and
+//                                 (1,0), so the per-channel value is one
+//                                 block-uniform load.
+//      ew_inner<OP, NIN, VEC, Idx> rank > 2, outer offsets from a div/mod
+//                                 walk once per VEC elements.
 //  * ew_generic: any dtype mix, any strides, one element per thread.
-// Both walk a grid-stride loop so any size fits any grid.
+// All walk grid-stride loops so any size fits any grid.
+#include <algorithm>
+
 #include "kk_internal.h"
 
 namespace kk {
@@ -126,6 +132,69 @@ __device__ __forceinline__ void outer_offsets(const EwArgs& A, Idx row, Idx (&of
   }
 }
 
+// Loads VEC consecutive floats of an operand whose innermost stride is 1
+// (streamed) or 0 (one value broadcast along the row).
+template <int VEC>
+__device__ __forceinline__ void load_operand(const float* __restrict__ p, bool contiguous,
+                                             float (&v)[VEC]) {
+  if constexpr (VEC == 4) {
+    if (contiguous) {
+      const float4 t = ld_stream4(p);
+      v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else {
+      v[0] = v[1] = v[2] = v[3] = *p;
+    }
+  } else {
+    v[0] = contiguous ? ld_stream(p) : *p;
+  }
+}
+
+template <int OP, int NIN, int VEC>
+__device__ __forceinline__ void ew_apply_store(float* __restrict__ out, const float (&a)[VEC],
+                                               const float (&b)[VEC], const float (&c)[VEC],
+                                               float alpha, int aux) {
+  float r[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i)
+    r[i] = apply_f32<OP>(a[i], NIN > 1 ? b[i] : 0.0f, NIN > 2 ? c[i] : 0.0f, alpha, aux);
+  if constexpr (VEC == 4) st_stream4(out, make_float4(r[0], r[1], r[2], r[3]));
+  else st_stream(out, r[0]);
+}
+
+// Plans of rank <= 2: [rows, L].  Rows run over blockIdx.y, so each operand's
+// row offset -- and a row-broadcast operand's value -- is uniform across the
+// block; columns run over blockIdx.x with one VEC-wide item per thread.
+template <int OP, int NIN, int VEC>
+__global__ void __launch_bounds__(256) ew_rows(EwArgs A) {
+  const int64_t L = A.dims[A.rank - 1];
+  const int64_t rows = A.rank == 2 ? A.dims[0] : 1;
+  const int64_t per_row = L / VEC;
+  float* __restrict__ out = static_cast<float*>(A.out);
+  const float* __restrict__ in0 = static_cast<const float*>(A.in[0]);
+  const float* __restrict__ in1 = NIN > 1 ? static_cast<const float*>(A.in[1]) : nullptr;
+  const float* __restrict__ in2 = NIN > 2 ? static_cast<const float*>(A.in[2]) : nullptr;
+  const int last = A.rank - 1;
+  const bool c0 = A.st[1][last] != 0, c1 = NIN > 1 && A.st[2][last] != 0,
+             c2 = NIN > 2 && A.st[3][last] != 0;
+  for (int64_t row = blockIdx.y; row < rows; row += gridDim.y) {
+    const int64_t ro = A.rank == 2 ? row * A.st[0][0] : 0;
+    const int64_t r0 = A.rank == 2 ? row * A.st[1][0] : 0;
+    const int64_t r1 = (NIN > 1 && A.rank == 2) ? row * A.st[2][0] : 0;
+    const int64_t r2 = (NIN > 2 && A.rank == 2) ? row * A.st[3][0] : 0;
+    for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; v < per_row;
+         v += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+      const int64_t col = v * VEC;
+      float a[VEC], b[VEC], c[VEC];
+      load_operand<VEC>(in0 + r0 + (c0 ? col : 0), c0, a);
+      if constexpr (NIN > 1) load_operand<VEC>(in1 + r1 + (c1 ? col : 0), c1, b);
+      if constexpr (NIN > 2) load_operand<VEC>(in2 + r2 + (c2 ? col : 0), c2, c);
+      ew_apply_store<OP, NIN, VEC>(out + ro + col, a, b, c, A.alpha, A.aux);
+    }
+  }
+}
+
+// Plans of rank > 2: flat index over VEC-wide items; the outer offsets come
+// from a div/mod walk over the outer axes.
 template <int OP, int NIN, int VEC, typename Idx>
 __global__ void __launch_bounds__(256) ew_inner(EwArgs A) {
   const Idx L = static_cast<Idx>(A.dims[A.rank - 1]);
@@ -135,37 +204,20 @@ __global__ void __launch_bounds__(256) ew_inner(EwArgs A) {
   const float* __restrict__ in0 = static_cast<const float*>(A.in[0]);
   const float* __restrict__ in1 = NIN > 1 ? static_cast<const float*>(A.in[1]) : nullptr;
   const float* __restrict__ in2 = NIN > 2 ? static_cast<const float*>(A.in[2]) : nullptr;
-  const Idx s0 = static_cast<Idx>(A.st[1][A.rank - 1]);
-  const Idx s1 = NIN > 1 ? static_cast<Idx>(A.st[2][A.rank - 1]) : 0;
-  const Idx s2 = NIN > 2 ? static_cast<Idx>(A.st[3][A.rank - 1]) : 0;
+  const bool c0 = A.st[1][A.rank - 1] != 0;
+  const bool c1 = NIN > 1 && A.st[2][A.rank - 1] != 0;
+  const bool c2 = NIN > 2 && A.st[3][A.rank - 1] != 0;
   for (Idx v = blockIdx.x * static_cast<Idx>(blockDim.x) + threadIdx.x; v < items;
        v += static_cast<Idx>(gridDim.x) * blockDim.x) {
     const Idx row = v / per_row;
     const Idx col = (v - row * per_row) * VEC;
     Idx off[kMaxOperands];
     outer_offsets<Idx>(A, row, off, NIN + 1);
-    float a[VEC], b[VEC], c[VEC], r[VEC];
-    if constexpr (VEC == 4) {
-      if (s0) *reinterpret_cast<float4*>(a) = *reinterpret_cast<const float4*>(in0 + off[1] + col);
-      else { a[0] = a[1] = a[2] = a[3] = in0[off[1]]; }
-      if constexpr (NIN > 1) {
-        if (s1) *reinterpret_cast<float4*>(b) = *reinterpret_cast<const float4*>(in1 + off[2] + col);
-        else { b[0] = b[1] = b[2] = b[3] = in1[off[2]]; }
-      }
-      if constexpr (NIN > 2) {
-        if (s2) *reinterpret_cast<float4*>(c) = *reinterpret_cast<const float4*>(in2 + off[3] + col);
-        else { c[0] = c[1] = c[2] = c[3] = in2[off[3]]; }
-      }
-    } else {
-      a[0] = in0[off[1] + col * s0];
-      if constexpr (NIN > 1) b[0] = in1[off[2] + col * s1];
-      if constexpr (NIN > 2) c[0] = in2[off[3] + col * s2];
-    }
-#pragma unroll
-    for (int i = 0; i < VEC; ++i)
-      r[i] = apply_f32<OP>(a[i], NIN > 1 ? b[i] : 0.0f, NIN > 2 ? c[i] : 0.0f, A.alpha, A.aux);
-    if constexpr (VEC == 4) *reinterpret_cast<float4*>(out + off[0] + col) = *reinterpret_cast<float4*>(r);
-    else out[off[0] + col] = r[0];
+    float a[VEC], b[VEC], c[VEC];
+    load_operand<VEC>(in0 + off[1] + (c0 ? col : 0), c0, a);
+    if constexpr (NIN > 1) load_operand<VEC>(in1 + off[2] + (c1 ? col : 0), c1, b);
+    if constexpr (NIN > 2) load_operand<VEC>(in2 + off[3] + (c2 ? col : 0), c2, c);
+    ew_apply_store<OP, NIN, VEC>(out + off[0] + col, a, b, c, A.alpha, A.aux);
   }
 }
 
@@ -327,8 +379,18 @@ static bool fits_u32(const Plan& p) {
 template <int OP, int NIN>
 static int launch_inner_op(const EwArgs& A, int vec, bool u32) {
   const int64_t items = A.n / vec;
-  const int grid = grid_for(items);
   hipStream_t s = ctx().stream;
+  const int64_t per_row = A.dims[A.rank - 1] / vec;
+  if (A.rank <= 2 && per_row >= 64) {
+    const int64_t rows = A.rank == 2 ? A.dims[0] : 1;
+    const int64_t gx = std::min<int64_t>(ceil_div(per_row, 256), 1 << 20);
+    const int64_t gy = std::min<int64_t>(rows, 65535);
+    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+    if (vec == 4) hipLaunchKernelGGL((ew_rows<OP, NIN, 4>), grid, dim3(256), 0, s, A);
+    else hipLaunchKernelGGL((ew_rows<OP, NIN, 1>), grid, dim3(256), 0, s, A);
+    return check_launch("ew_rows");
+  }
+  const int grid = grid_for(items);
   if (vec == 4) {
     if (u32) hipLaunchKernelGGL((ew_inner<OP, NIN, 4, uint32_t>), dim3(grid), dim3(256), 0, s, A);
     else hipLaunchKernelGGL((ew_inner<OP, NIN, 4, int64_t>), dim3(grid), dim3(256), 0, s, A);

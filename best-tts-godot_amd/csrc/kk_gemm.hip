@@ -3,13 +3,16 @@
 // on one fp32 MFMA core (v_mfma_f32_16x16x4_f32: fp32 operands, exact fp32
 // products, fp32 accumulation -- the fp32 semantics of the numpy reference).
 //
-// Core: a block computes a BM x BN tile of C = A . B with BK = 16 deep
-// K-steps.  Each wavefront owns a 32 x 32 sub-tile made of 2 x 2 MFMA
-// 16 x 16 tiles.  A and B tiles are fetched from global memory by loader
-// policies (dense strided, int8/uint8 dequant, im2col gather, transposed-conv
-// phase gather) into registers, dequantised to fp32 there, stored K-major in
-// LDS, and the next tile's fetch overlaps the current tile's MFMAs.
+// Core: a block of four wavefronts computes a BM x BN tile of C = A . B in
+// K-steps of 32.  Each wavefront owns a (16*WTM) x (16*WTN) sub-tile made of
+// WTM x WTN MFMA 16x16 tiles.  Tile loaders -- vectorised dense loaders for
+// fp32 activations and int8/uint8/fp16/fp32 weights, an im2col gather for
+// the convolution input, scalar gathers for everything else -- fetch the
+// next K-step from global memory into registers while the current one is
+// multiplied, dequantise there ((q - zp) * scale in fp32, with the scale and
+// zero point held in registers), and store it K-major in LDS.
 #include <algorithm>
+#include <type_traits>
 
 #include "kk_internal.h"
 
@@ -17,8 +20,21 @@ namespace kk {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 16;
-constexpr int kPad = 4;  // LDS row padding (floats) against bank conflicts
+constexpr int kBK = 32;   // K-step
+constexpr int kPad = 4;   // LDS row padding (floats)
+constexpr int kNT = 256;  // threads per block (4 wavefronts)
+
+template <int BM_, int BN_, int WTM_, int WTN_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, WTM = WTM_, WTN = WTN_;
+  static constexpr int WM = 16 * WTM, WN = 16 * WTN;
+  static constexpr int WAVES_N = BN / WN;
+  static constexpr int PA = BM + kPad, PB = BN + kPad;
+  static_assert((BM / WM) * (BN / WN) == 4, "four wavefronts per block");
+};
+using CfgL = Cfg<64, 64, 2, 2>;  // 32x32 per wave
+using CfgM = Cfg<64, 32, 1, 2>;  // 16x32 per wave
+using CfgS = Cfg<32, 32, 1, 1>;  // 16x16 per wave
 
 // Batch offsets: up to 6 batch axes with per-operand strides (0 = broadcast).
 struct BatchMap {
@@ -36,184 +52,314 @@ __device__ __forceinline__ int64_t batch_offset(const BatchMap& bm, int which, i
   return off;
 }
 
-// ----------------------------------------------------------- loader: dense
-// Element (i, j) of a strided matrix, i over `rows`, j over `cols`, with
-// optional dequantisation by column (`deq_by_col`) or by row.
-struct DenseLoader {
-  const void* p;
-  int dt;
-  int64_t si, sj;      // element strides
-  int64_t rows, cols;  // logical extents (for bounds)
-  Dequant dq;
-  int deq_by_col;      // 1: scale/zp index = j, 0: = i
-  int which;           // batch stride slot
-  __device__ __forceinline__ float get(int64_t boff, int64_t i, int64_t j) const {
-    if (i >= rows || j >= cols) return 0.0f;
-    const int64_t off = boff + i * si + j * sj;
-    float v;
-    if (dt == KK_F32) v = static_cast<const float*>(p)[off];
-    else v = load_as_f32(p, dt, off);
-    if (dq.active) v = dequant_value(v, dq, deq_by_col ? j : i);
-    return v;
-  }
-};
-
-// --------------------------------------------------------- loader: im2col
-// B[kk, l] = x[n, ci, l*s + k*d - p0] with kk = ci*K + k (zero padding).
-struct Im2colLoader {
-  const float* x;
-  int64_t cin, L, K, s, d, p0;
-  int64_t rows, cols;  // Cin*K, Lout
-  __device__ __forceinline__ float get(int64_t boff, int64_t kk, int64_t l) const {
-    if (kk >= rows || l >= cols) return 0.0f;
-    const int64_t ci = kk / K, k = kk - ci * K;
-    const int64_t pos = l * s + k * d - p0;
-    if (pos < 0 || pos >= L) return 0.0f;
-    return x[boff + ci * L + pos];
-  }
-};
-
-// ------------------------------------------- loaders: transposed-conv phase
-// For output phase r (positions j = q*s + r of the uncropped output):
-//   out[co, q*s + r] = sum_{ci, m} W[ci, co, r + s*m] * x[ci, q - m]
-// A[co, kk] = W[ci, co, r + s*m] and B[kk, q] = x[ci, q - m], kk = ci*MR + m.
-struct ConvTWLoader {
-  const void* w;
-  int dt;
-  Dequant dq;
-  int64_t cout_g, K, s, MR;
-  int64_t rows, cols;  // Cout, Cin*MR
-  __device__ __forceinline__ float get(int64_t r, int64_t co, int64_t kk) const {
-    if (co >= rows || kk >= cols) return 0.0f;
-    const int64_t ci = kk / MR, m = kk - ci * MR;
-    const int64_t k = r + s * m;
-    if (k >= K) return 0.0f;
-    float v = load_as_f32(w, dt, (ci * cout_g + co) * K + k);
-    if (dq.active) v = dequant_value(v, dq, co);
-    return v;
-  }
-};
-struct ConvTXLoader {
-  const float* x;
-  int64_t L, MR;
-  int64_t rows, cols;  // Cin*MR, number of q
-  int64_t q0;          // first q of this phase
-  __device__ __forceinline__ float get(int64_t boff, int64_t kk, int64_t qi) const {
-    if (kk >= rows || qi >= cols) return 0.0f;
-    const int64_t ci = kk / MR, m = kk - ci * MR;
-    const int64_t l = q0 + qi - m;
-    if (l < 0 || l >= L) return 0.0f;
-    return x[boff + ci * L + l];
-  }
-};
-
-// ------------------------------------------------------------ MFMA core
-// acc[2][2] are the wave's four 16x16 tiles.  Lane layout of
-// v_mfma_f32_16x16x4_f32: lane l supplies A[l%16][l/16] and B[l/16][l%16];
-// D element (i, j) lives in lane j + 16*(i/4), register i%4.
-template <int BM, int BN>
-struct Tile {
-  static constexpr int WN = BN / 32;
-  static constexpr int WAVES = (BM / 32) * (BN / 32);
-  static constexpr int NT = WAVES * 64;
-  static constexpr int AE = BM * kBK / NT;  // A elements per thread
-  static constexpr int BE = kBK * BN / NT;  // B elements per thread
-};
-
-template <int BM, int BN>
-__device__ __forceinline__ void mfma_tile(const float* As, const float* Bs, v4f (&acc)[2][2],
-                                          int wm, int wn, int lane) {
-#pragma unroll
-  for (int kk = 0; kk < kBK; kk += 4) {
-    const int k = kk + (lane >> 4);
-    float a[2], b[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) a[i] = As[k * (BM + kPad) + wm + i * 16 + (lane & 15)];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) b[j] = Bs[k * (BN + kPad) + wn + j * 16 + (lane & 15)];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
-  }
+// Scale and zero point of one weight row/column, read once per block.
+__device__ __forceinline__ void dq_params(const Dequant& dq, int64_t idx, float& s, float& z) {
+  s = load_as_f32(dq.scale, dq.scale_dt, idx * dq.scale_stride);
+  z = dq.zp ? load_as_f32(dq.zp, dq.zp_dt, idx * dq.zp_stride) : 0.0f;
 }
 
-// Element e of a tile with `fast` extent along the contiguous direction.
-// A tile is BM (m) x kBK (k); B tile is kBK (k) x BN (n).  `a_kfast`: A's
-// consecutive elements run along k (else along m); `b_nfast` likewise.
+// Four consecutive elements of type T starting at p (4-element aligned).
+template <typename T>
+__device__ __forceinline__ float4 load4(const T* p);
+template <>
+__device__ __forceinline__ float4 load4<float>(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+template <>
+__device__ __forceinline__ float4 load4<__half>(const __half* p) {
+  const uint2 u = *reinterpret_cast<const uint2*>(p);
+  const __half2 lo = *reinterpret_cast<const __half2*>(&u.x);
+  const __half2 hi = *reinterpret_cast<const __half2*>(&u.y);
+  return make_float4(__low2float(lo), __high2float(lo), __low2float(hi), __high2float(hi));
+}
+template <>
+__device__ __forceinline__ float4 load4<int8_t>(const int8_t* p) {
+  const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+  return make_float4(static_cast<float>(static_cast<int8_t>(u & 0xff)),
+                     static_cast<float>(static_cast<int8_t>((u >> 8) & 0xff)),
+                     static_cast<float>(static_cast<int8_t>((u >> 16) & 0xff)),
+                     static_cast<float>(static_cast<int8_t>(u >> 24)));
+}
+template <>
+__device__ __forceinline__ float4 load4<uint8_t>(const uint8_t* p) {
+  const uint32_t u = *reinterpret_cast<const uint32_t*>(p);
+  return make_float4(static_cast<float>(u & 0xff), static_cast<float>((u >> 8) & 0xff),
+                     static_cast<float>((u >> 16) & 0xff), static_cast<float>(u >> 24));
+}
 
-// Generic kernel body.  GetA(boffA/phase, m, k) and GetB(boffB, k, n) return
-// fp32 values; Store(m, n, value) writes the result.
-template <int BM, int BN, class FA, class FB, class FS>
-__device__ __forceinline__ void gemm_body(const FA& getA, const FB& getB, const FS& store,
-                                          int64_t M, int64_t N, int64_t K, bool a_kfast,
-                                          bool b_nfast) {
-  using T = Tile<BM, BN>;
-  __shared__ float As[2][kBK * (BM + kPad)];
-  __shared__ float Bs[2][kBK * (BN + kPad)];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = (wave / T::WN) * 32, wn = (wave % T::WN) * 32;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * BM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * BN;
+template <typename T>
+constexpr bool is_quant() {
+  return std::is_same<T, int8_t>::value || std::is_same<T, uint8_t>::value;
+}
 
-  v4f acc[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+// ---------------------------------------------------------------- loaders
+// A loaders fill As[k][m] (pitch PA), B loaders fill Bs[k][n] (pitch PB).
+// fetch(k0) reads the K-step starting at k0 into registers; stash() writes
+// them to LDS.  Out-of-range elements are zero.
 
-  float ra[T::AE], rb[T::BE];
-  auto fetch = [&](int64_t k0) {
+// A [M, K] with K contiguous, element type T, optional per-row (or
+// per-tensor) dequantisation; needs K % 4 == 0 and 4-element-aligned rows.
+template <class C, typename T>
+struct AQuad {
+  static constexpr int QPR = kBK / 4;
+  static constexpr int RPP = kNT / QPR;
+  static constexpr int P = (C::BM + RPP - 1) / RPP;
+  const T* ptr[P];
+  bool ok[P];
+  float s[P], z[P];
+  float4 v[P];
+  int kq, r0;
+  int64_t K;
+  __device__ __forceinline__ void init(const T* a, int64_t lda, int64_t M, int64_t K_, int64_t m0,
+                                       const Dequant& dq) {
+    kq = (threadIdx.x % QPR) * 4;
+    r0 = threadIdx.x / QPR;
+    K = K_;
 #pragma unroll
-    for (int t = 0; t < T::AE; ++t) {
-      const int e = tid + t * T::NT;
-      const int mi = a_kfast ? e / kBK : e % BM;
-      const int ki = a_kfast ? e % kBK : e / BM;
-      ra[t] = (k0 + ki < K) ? getA(m0 + mi, k0 + ki) : 0.0f;
+    for (int p = 0; p < P; ++p) {
+      const int row = r0 + p * RPP;
+      ok[p] = row < C::BM && m0 + row < M;
+      ptr[p] = a + (ok[p] ? (m0 + row) * lda : 0);
+      s[p] = 1.0f;
+      z[p] = 0.0f;
+      if (is_quant<T>() && ok[p]) dq_params(dq, m0 + row, s[p], z[p]);
     }
+  }
+  __device__ __forceinline__ void fetch(int64_t k0) {
 #pragma unroll
-    for (int t = 0; t < T::BE; ++t) {
-      const int e = tid + t * T::NT;
-      const int ni = b_nfast ? e % BN : e / kBK;
-      const int ki = b_nfast ? e / BN : e % kBK;
-      rb[t] = (k0 + ki < K) ? getB(k0 + ki, n0 + ni) : 0.0f;
+    for (int p = 0; p < P; ++p) {
+      if (ok[p] && k0 + kq < K) {
+        float4 t = load4<T>(ptr[p] + k0 + kq);
+        if (is_quant<T>()) {
+          t.x = (t.x - z[p]) * s[p];
+          t.y = (t.y - z[p]) * s[p];
+          t.z = (t.z - z[p]) * s[p];
+          t.w = (t.w - z[p]) * s[p];
+        }
+        v[p] = t;
+      } else {
+        v[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
-  };
-  auto stash = [&](int buf) {
+  }
+  __device__ __forceinline__ void stash(float* As) const {
 #pragma unroll
-    for (int t = 0; t < T::AE; ++t) {
-      const int e = tid + t * T::NT;
-      const int mi = a_kfast ? e / kBK : e % BM;
-      const int ki = a_kfast ? e % kBK : e / BM;
-      As[buf][ki * (BM + kPad) + mi] = ra[t];
+    for (int p = 0; p < P; ++p) {
+      const int row = r0 + p * RPP;
+      if (row < C::BM) {
+        As[(kq + 0) * C::PA + row] = v[p].x;
+        As[(kq + 1) * C::PA + row] = v[p].y;
+        As[(kq + 2) * C::PA + row] = v[p].z;
+        As[(kq + 3) * C::PA + row] = v[p].w;
+      }
     }
+  }
+};
+
+// B [K, N] with N contiguous, element type T, optional per-column (or
+// per-tensor) dequantisation; needs N % 4 == 0 and 4-element-aligned rows.
+template <class C, typename T>
+struct BQuad {
+  static constexpr int QPR = C::BN / 4;
+  static constexpr int RPP = kNT / QPR;
+  static constexpr int P = kBK / RPP;
+  const T* base;
+  int64_t ldb, K;
+  bool col_ok;
+  float s[4], z[4];
+  float4 v[P];
+  int nq, r0;
+  __device__ __forceinline__ void init(const T* b, int64_t ldb_, int64_t N, int64_t K_, int64_t n0,
+                                       const Dequant& dq) {
+    nq = (threadIdx.x % QPR) * 4;
+    r0 = threadIdx.x / QPR;
+    ldb = ldb_;
+    K = K_;
+    col_ok = n0 + nq < N;
+    base = b + (col_ok ? n0 + nq : 0);
 #pragma unroll
-    for (int t = 0; t < T::BE; ++t) {
-      const int e = tid + t * T::NT;
-      const int ni = b_nfast ? e % BN : e / kBK;
-      const int ki = b_nfast ? e / BN : e % kBK;
-      Bs[buf][ki * (BN + kPad) + ni] = rb[t];
+    for (int c = 0; c < 4; ++c) {
+      s[c] = 1.0f;
+      z[c] = 0.0f;
+      if (is_quant<T>() && col_ok) dq_params(dq, n0 + nq + c, s[c], z[c]);
     }
-  };
+  }
+  __device__ __forceinline__ void fetch(int64_t k0) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t k = k0 + r0 + p * RPP;
+      if (col_ok && k < K) {
+        float4 t = load4<T>(base + k * ldb);
+        if (is_quant<T>()) {
+          t.x = (t.x - z[0]) * s[0];
+          t.y = (t.y - z[1]) * s[1];
+          t.z = (t.z - z[2]) * s[2];
+          t.w = (t.w - z[3]) * s[3];
+        }
+        v[p] = t;
+      } else {
+        v[p] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
+    }
+  }
+  __device__ __forceinline__ void stash(float* Bs) const {
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      *reinterpret_cast<float4*>(Bs + (r0 + p * RPP) * C::PB + nq) = v[p];
+  }
+};
+
+// Scalar gathers through a functor get(i, j) (bounds-checked by the
+// functor).  The FAST flag selects which tile dimension consecutive threads
+// walk (the operand's unit-stride direction, for coalescing).
+template <class C, class Get, bool KFAST>
+struct AScalar {
+  static constexpr int E = C::BM * kBK / kNT;
+  Get get;
+  int64_t m0;
+  float v[E];
+  __device__ __forceinline__ void idx(int e, int& m, int& k) const {
+    if (KFAST) { m = e / kBK; k = e % kBK; } else { m = e % C::BM; k = e / C::BM; }
+  }
+  __device__ __forceinline__ void fetch(int64_t k0) {
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+      int m, k;
+      idx(threadIdx.x + t * kNT, m, k);
+      v[t] = get(m0 + m, k0 + k);
+    }
+  }
+  __device__ __forceinline__ void stash(float* As) const {
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+      int m, k;
+      idx(threadIdx.x + t * kNT, m, k);
+      As[k * C::PA + m] = v[t];
+    }
+  }
+};
+
+template <class C, class Get, bool NFAST>
+struct BScalar {
+  static constexpr int E = kBK * C::BN / kNT;
+  Get get;
+  int64_t n0;
+  float v[E];
+  __device__ __forceinline__ void idx(int e, int& k, int& n) const {
+    if (NFAST) { k = e / C::BN; n = e % C::BN; } else { n = e / kBK; k = e % kBK; }
+  }
+  __device__ __forceinline__ void fetch(int64_t k0) {
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+      int k, n;
+      idx(threadIdx.x + t * kNT, k, n);
+      v[t] = get(k0 + k, n0 + n);
+    }
+  }
+  __device__ __forceinline__ void stash(float* Bs) const {
+#pragma unroll
+    for (int t = 0; t < E; ++t) {
+      int k, n;
+      idx(threadIdx.x + t * kNT, k, n);
+      Bs[k * C::PB + n] = v[t];
+    }
+  }
+};
+
+// Conv1d input as the B operand: B[kk, l] = x[ci, l*s + k*d - p0] with
+// kk = ci*Kw + k; each thread gathers four consecutive l of one kk.
+template <class C>
+struct BIm2col {
+  static constexpr int QPR = C::BN / 4;
+  static constexpr int RPP = kNT / QPR;
+  static constexpr int P = kBK / RPP;
+  const float* x;  // this batch item's [Cin, L]
+  int64_t L, Kw, s, d, p0, Kdim, Lout;
+  int64_t l0;      // first output position of this thread's quad
+  float4 v[P];
+  int r0;
+  __device__ __forceinline__ void fetch(int64_t k0) {
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int64_t kk = k0 + r0 + p * RPP;
+      float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (kk < Kdim) {
+        const int64_t ci = kk / Kw, k = kk - ci * Kw;
+        const float* xr = x + ci * L;
+        const int64_t pos0 = l0 * s + k * d - p0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int64_t pos = pos0 + c * s;
+          if (l0 + c < Lout && pos >= 0 && pos < L) e[c] = xr[pos];
+        }
+      }
+      v[p] = make_float4(e[0], e[1], e[2], e[3]);
+    }
+  }
+  __device__ __forceinline__ void stash(float* Bs) const {
+    const int nq = (threadIdx.x % QPR) * 4;
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      *reinterpret_cast<float4*>(Bs + (r0 + p * RPP) * C::PB + nq) = v[p];
+  }
+};
+
+// ------------------------------------------------------------- MFMA core
+// Lane layout of v_mfma_f32_16x16x4_f32: lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; D element (i, j) lives in lane j + 16*(i/4), register i%4.
+template <class C, class LA, class LB, class ST>
+__device__ __forceinline__ void gemm_run(LA& la, LB& lb, const ST& store, int64_t M, int64_t N,
+                                         int64_t K, int64_t m0, int64_t n0) {
+  __shared__ __align__(16) float As[2][kBK * C::PA];
+  __shared__ __align__(16) float Bs[2][kBK * C::PB];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = (wave / C::WAVES_N) * C::WM, wn = (wave % C::WAVES_N) * C::WN;
+  v4f acc[C::WTM][C::WTN];
+#pragma unroll
+  for (int i = 0; i < C::WTM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::WTN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
   const int64_t nk = ceil_div(K, kBK);
-  fetch(0);
-  stash(0);
+  la.fetch(0);
+  lb.fetch(0);
+  la.stash(As[0]);
+  lb.stash(Bs[0]);
   __syncthreads();
   for (int64_t kt = 0; kt < nk; ++kt) {
     const int buf = static_cast<int>(kt & 1);
-    if (kt + 1 < nk) fetch((kt + 1) * kBK);
-    mfma_tile<BM, BN>(As[buf], Bs[buf], acc, wm, wn, lane);
-    if (kt + 1 < nk) stash(buf ^ 1);
+    const bool more = kt + 1 < nk;
+    if (more) {
+      la.fetch((kt + 1) * kBK);
+      lb.fetch((kt + 1) * kBK);
+    }
+    const float* as = As[buf];
+    const float* bs = Bs[buf];
+#pragma unroll
+    for (int kk = 0; kk < kBK; kk += 4) {
+      const int k = kk + (lane >> 4);
+      float a[C::WTM], b[C::WTN];
+#pragma unroll
+      for (int i = 0; i < C::WTM; ++i) a[i] = as[k * C::PA + wm + i * 16 + (lane & 15)];
+#pragma unroll
+      for (int j = 0; j < C::WTN; ++j) b[j] = bs[k * C::PB + wn + j * 16 + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < C::WTM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::WTN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      la.stash(As[buf ^ 1]);
+      lb.stash(Bs[buf ^ 1]);
+    }
     __syncthreads();
   }
 
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < C::WTM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < C::WTN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t m = m0 + wm + i * 16 + (lane >> 4) * 4 + r;
@@ -224,83 +370,184 @@ __device__ __forceinline__ void gemm_body(const FA& getA, const FB& getB, const 
 
 // ------------------------------------------------------------------ GEMM
 struct GemmArgs {
-  DenseLoader a, b;
+  const void* a;
+  int a_dt;
+  int64_t a_si, a_sj;  // element strides of A [M, K]
+  const void* b;
+  int b_dt;
+  int64_t b_si, b_sj;  // element strides of B [K, N]
+  Dequant dq;          // B's dequantisation (per column or per tensor)
   float* out;
   int64_t som, son;
   BatchMap bm;
   int64_t M, N, K;
   float alpha;
-  int a_kfast, b_nfast;
 };
 
-template <int BM, int BN>
-__global__ void __launch_bounds__((BM / 32) * (BN / 32) * 64) gemm_kernel(GemmArgs G) {
-  const int64_t b = blockIdx.z;
-  const int64_t oa = batch_offset(G.bm, 0, b), ob = batch_offset(G.bm, 1, b),
-                oo = batch_offset(G.bm, 2, b);
-  auto getA = [&](int64_t m, int64_t k) { return G.a.get(oa, m, k); };
-  auto getB = [&](int64_t k, int64_t n) { return G.b.get(ob, k, n); };
+// A kinds: 0 = fp32 K-contiguous quads, 1 = scalar gather.
+// B kinds: 0 = N-contiguous quads of TB, 1 = scalar gather.
+template <class C, int AK, int BK, typename TB>
+__global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
+  const int64_t bz = blockIdx.z;
+  const int64_t oa = batch_offset(G.bm, 0, bz), ob = batch_offset(G.bm, 1, bz),
+                oo = batch_offset(G.bm, 2, bz);
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * C::BN;
   float* out = G.out + oo;
   const float alpha = G.alpha;
+  const int64_t som = G.som, son = G.son;
   auto store = [&](int64_t m, int64_t n, float v) {
-    out[m * G.som + n * G.son] = alpha == 1.0f ? v : v * alpha;
+    out[m * som + n * son] = alpha == 1.0f ? v : v * alpha;
   };
-  gemm_body<BM, BN>(getA, getB, store, G.M, G.N, G.K, G.a_kfast, G.b_nfast);
+  const int64_t M = G.M, N = G.N, K = G.K;
+  auto getA = [&](int64_t m, int64_t k) -> float {
+    if (m >= M || k >= K) return 0.0f;
+    return load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
+  };
+  auto getB = [&](int64_t k, int64_t n) -> float {
+    if (k >= K || n >= N) return 0.0f;
+    const float q = load_as_f32(G.b, G.b_dt, ob + k * G.b_si + n * G.b_sj);
+    return G.dq.active ? dequant_value(q, G.dq, n) : q;
+  };
+  if constexpr (AK == 0 && BK == 0) {
+    AQuad<C, float> la;
+    la.init(static_cast<const float*>(G.a) + oa, G.a_si, M, K, m0, G.dq);
+    BQuad<C, TB> lb;
+    lb.init(static_cast<const TB*>(G.b) + ob, G.b_si, N, K, n0, G.dq);
+    gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+  } else if constexpr (AK == 0) {
+    AQuad<C, float> la;
+    la.init(static_cast<const float*>(G.a) + oa, G.a_si, M, K, m0, G.dq);
+    if (G.b_si == 1) {
+      BScalar<C, decltype(getB), false> lb{getB, n0};
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+    } else {
+      BScalar<C, decltype(getB), true> lb{getB, n0};
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+    }
+  } else if constexpr (BK == 0) {
+    BQuad<C, TB> lb;
+    lb.init(static_cast<const TB*>(G.b) + ob, G.b_si, N, K, n0, G.dq);
+    if (G.a_si == 1) {
+      AScalar<C, decltype(getA), false> la{getA, m0};
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+    } else {
+      AScalar<C, decltype(getA), true> la{getA, m0};
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+    }
+  } else {
+    // consecutive threads walk the unit-stride direction of each operand
+    if (G.a_si == 1) {
+      AScalar<C, decltype(getA), false> la{getA, m0};
+      if (G.b_si == 1) {
+        BScalar<C, decltype(getB), false> lb{getB, n0};
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      } else {
+        BScalar<C, decltype(getB), true> lb{getB, n0};
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      }
+    } else {
+      AScalar<C, decltype(getA), true> la{getA, m0};
+      if (G.b_si == 1) {
+        BScalar<C, decltype(getB), false> lb{getB, n0};
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      } else {
+        BScalar<C, decltype(getB), true> lb{getB, n0};
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ conv
 struct ConvArgs {
-  DenseLoader w;       // A = W as [Cout, Cin*K], dequant by row (co)
-  Im2colLoader x;      // B
+  const void* w;       // [Cout, Cin*Kw] (K contiguous)
+  int w_dt;
+  Dequant dq;          // per output channel (row) or per tensor
+  const float* x;      // [N, Cin, L]
   float* out;          // [N, Cout, Lout]
   const float* bias;   // [Cout] or NULL
-  int64_t x_bstride;   // Cin*L
-  int64_t o_bstride;   // Cout*Lout
-  int64_t M, N, K;
+  int64_t Cin, L, Kw, s, d, p0, Lout;
+  int64_t M, K;        // Cout, Cin*Kw
 };
 
-template <int BM, int BN>
-__global__ void __launch_bounds__((BM / 32) * (BN / 32) * 64) conv1d_kernel(ConvArgs C) {
-  const int64_t b = blockIdx.z;
-  const int64_t ox = b * C.x_bstride;
-  auto getA = [&](int64_t m, int64_t k) { return C.w.get(0, m, k); };
-  auto getB = [&](int64_t k, int64_t n) { return C.x.get(ox, k, n); };
-  float* out = C.out + b * C.o_bstride;
-  const int64_t N = C.N;
-  const float* bias = C.bias;
-  auto store = [&](int64_t m, int64_t n, float v) {
-    out[m * N + n] = bias ? v + bias[m] : v;
-  };
-  gemm_body<BM, BN>(getA, getB, store, C.M, C.N, C.K, true, true);
+// AK: 0 = quad loads of TW (K % 4 == 0), 1 = scalar gather.
+template <class C, int AK, typename TW>
+__global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
+  const int64_t bz = blockIdx.z;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * C::BN;
+  const int64_t M = A.M, N = A.Lout, K = A.K;
+  float* out = A.out + bz * M * N;
+  const float* bias = A.bias;
+  auto store = [&](int64_t m, int64_t n, float v) { out[m * N + n] = bias ? v + bias[m] : v; };
+  BIm2col<C> lb;
+  lb.x = A.x + bz * A.Cin * A.L;
+  lb.L = A.L; lb.Kw = A.Kw; lb.s = A.s; lb.d = A.d; lb.p0 = A.p0; lb.Kdim = K; lb.Lout = N;
+  lb.r0 = threadIdx.x / BIm2col<C>::QPR;
+  lb.l0 = n0 + (threadIdx.x % BIm2col<C>::QPR) * 4;
+  if constexpr (AK == 0) {
+    AQuad<C, TW> la;
+    la.init(static_cast<const TW*>(A.w), K, M, K, m0, A.dq);
+    gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+  } else {
+    auto getA = [&](int64_t m, int64_t k) -> float {
+      if (m >= M || k >= K) return 0.0f;
+      const float q = load_as_f32(A.w, A.w_dt, m * K + k);
+      return A.dq.active ? dequant_value(q, A.dq, m) : q;
+    };
+    AScalar<C, decltype(getA), true> la{getA, m0};
+    gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+  }
 }
 
+// ------------------------------------------------- transposed conv (phases)
+// For output phase r (uncropped positions j = q*s + r):
+//   out[co, q*s + r] = sum_{ci, m} W[ci, co, r + s*m] * x[ci, q - m]
+// A[co, kk] = W[ci, co, r + s*m] and B[kk, q] = x[ci, q - m], kk = ci*MR + m.
 struct ConvTArgs {
-  ConvTWLoader w;
-  ConvTXLoader x;
+  const void* w;       // [Cin, Cout, Kw]
+  int w_dt;
+  Dequant dq;          // per output channel or per tensor
+  const float* x;      // [N, Cin, L]
   float* out;          // [N, Cout, Lout]
   const float* bias;
-  int64_t x_bstride, o_bstride;
-  int64_t s, p0, Lout, lfull;
-  int64_t M, K;        // Cout, Cin*MR
-  int64_t nq;          // q values per phase (upper bound)
+  int64_t Cin, Cout, L, Kw, s, MR, p0, Lout, nq;
 };
 
-template <int BM, int BN>
-__global__ void __launch_bounds__((BM / 32) * (BN / 32) * 64) conv_transpose_kernel(ConvTArgs C) {
-  const int64_t r = blockIdx.z % C.s;
-  const int64_t b = blockIdx.z / C.s;
-  const int64_t ox = b * C.x_bstride;
-  ConvTXLoader xl = C.x;
-  auto getA = [&](int64_t m, int64_t k) { return C.w.get(r, m, k); };
-  auto getB = [&](int64_t k, int64_t n) { return xl.get(ox, k, n); };
-  float* out = C.out + b * C.o_bstride;
-  const int64_t s = C.s, p0 = C.p0, Lout = C.Lout;
-  const float* bias = C.bias;
+template <class C>
+__global__ void __launch_bounds__(kNT) conv_transpose_kernel(ConvTArgs A) {
+  const int64_t r = blockIdx.z % A.s;
+  const int64_t bz = blockIdx.z / A.s;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * C::BN;
+  const int64_t M = A.Cout, N = A.nq, K = A.Cin * A.MR;
+  const float* x = A.x + bz * A.Cin * A.L;
+  float* out = A.out + bz * A.Cout * A.Lout;
+  const int64_t s = A.s, p0 = A.p0, Lout = A.Lout, MR = A.MR, Kw = A.Kw, L = A.L;
+  const float* bias = A.bias;
   auto store = [&](int64_t m, int64_t q, float v) {
     const int64_t jo = q * s + r - p0;
     if (jo >= 0 && jo < Lout) out[m * Lout + jo] = bias ? v + bias[m] : v;
   };
-  gemm_body<BM, BN>(getA, getB, store, C.M, C.nq, C.K, false, true);
+  auto getA = [&](int64_t co, int64_t kk) -> float {
+    if (co >= M || kk >= K) return 0.0f;
+    const int64_t ci = kk / MR, mt = kk - ci * MR;
+    const int64_t k = r + s * mt;
+    if (k >= Kw) return 0.0f;
+    const float q = load_as_f32(A.w, A.w_dt, (ci * M + co) * Kw + k);
+    return A.dq.active ? dequant_value(q, A.dq, co) : q;
+  };
+  auto getB = [&](int64_t kk, int64_t q) -> float {
+    if (kk >= K || q >= N) return 0.0f;
+    const int64_t ci = kk / MR, mt = kk - ci * MR;
+    const int64_t l = q - mt;
+    if (l < 0 || l >= L) return 0.0f;
+    return x[ci * L + l];
+  };
+  AScalar<C, decltype(getA), false> la{getA, m0};
+  BScalar<C, decltype(getB), true> lb{getB, n0};
+  gemm_run<C>(la, lb, store, M, N, K, m0, n0);
 }
 
 // --------------------------------------------------- direct conv kernels
@@ -369,33 +616,43 @@ __global__ void conv_transpose_direct_kernel(DirectArgs D) {
 }
 
 // ------------------------------------------------------------- launching
-static int tiles_for(int64_t M, int64_t N, int64_t batch, int* bm, int* bn) {
-  // Prefer 64x64 tiles; drop to smaller tiles while the grid would leave
-  // most of the 256 CUs idle.
-  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
-  const int64_t b64 = ceil_div(M, 64) * ceil_div(N, 64) * batch;
-  if (b64 >= 2 * cus) { *bm = 64; *bn = 64; return KK_OK; }
-  const int64_t b3264 = ceil_div(M, 32) * ceil_div(N, 64) * batch;
-  if (b3264 >= 2 * cus) { *bm = 32; *bn = 64; return KK_OK; }
-  *bm = 32; *bn = 32;
+enum TileSize { TILE_L = 0, TILE_M = 1, TILE_S = 2 };
+
+// The largest tile that still gives every SIMD (4 per CU) a wavefront; the
+// smallest tile otherwise.
+static TileSize pick_tile(int64_t M, int64_t N, int64_t batch) {
+  const int64_t simds = 4 * static_cast<int64_t>(ctx().num_cus > 0 ? ctx().num_cus : 256);
+  const int64_t wl = ceil_div(M, 64) * ceil_div(N, 64) * batch * 4;
+  if (wl >= simds) return TILE_L;
+  const int64_t wm = ceil_div(M, 64) * ceil_div(N, 32) * batch * 4;
+  if (wm >= simds) return TILE_M;
+  return TILE_S;
+}
+
+static dim3 grid_of(TileSize t, int64_t M, int64_t N, int64_t z) {
+  const int bm = t == TILE_S ? 32 : 64, bn = t == TILE_L ? 64 : 32;
+  return dim3(static_cast<unsigned>(ceil_div(N, bn)), static_cast<unsigned>(ceil_div(M, bm)),
+              static_cast<unsigned>(z));
+}
+
+static int check_grid(const dim3& g, int64_t z) {
+  if (z > 65535 || g.y > 65535)
+    return set_error(KK_E_UNSUPPORTED, "grid %u x %u x %lld too large", g.x, g.y, (long long)z);
   return KK_OK;
 }
 
-#define KK_LAUNCH_TILED(KERNEL, BM, BN, GRID, ARGS)                                            \
+#define KK_TILED(KERNEL, TS, GRID, ...)                                                       \
   do {                                                                                          \
-    if ((BM) == 64 && (BN) == 64)                                                               \
-      hipLaunchKernelGGL((KERNEL<64, 64>), GRID, dim3(Tile<64, 64>::NT), 0, ctx().stream, ARGS); \
-    else if ((BM) == 32 && (BN) == 64)                                                          \
-      hipLaunchKernelGGL((KERNEL<32, 64>), GRID, dim3(Tile<32, 64>::NT), 0, ctx().stream, ARGS); \
+    if ((TS) == TILE_L)                                                                         \
+      hipLaunchKernelGGL((KERNEL<CfgL, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
+    else if ((TS) == TILE_M)                                                                    \
+      hipLaunchKernelGGL((KERNEL<CfgM, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
     else                                                                                        \
-      hipLaunchKernelGGL((KERNEL<32, 32>), GRID, dim3(Tile<32, 32>::NT), 0, ctx().stream, ARGS); \
+      hipLaunchKernelGGL((KERNEL<CfgS, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
   } while (0)
 
-static int check_grid(int64_t gx, int64_t gy, int64_t gz) {
-  if (gx > 0x7fffffff || gy > 65535 || gz > 65535)
-    return set_error(KK_E_UNSUPPORTED, "grid %lld x %lld x %lld too large", (long long)gx,
-                     (long long)gy, (long long)gz);
-  return KK_OK;
+static bool aligned(const void* p, int bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
 static int conv_common(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
@@ -416,6 +673,42 @@ static int conv_common(const kk_tensor* out, const kk_tensor* x, const kk_tensor
       return set_error(KK_E_ARG, "%s: bias must be contiguous fp32", who);
   }
   return KK_OK;
+}
+
+static int launch_gemm(const GemmArgs& args, int64_t batch) {
+  const TileSize ts = pick_tile(args.M, args.N, batch);
+  const dim3 grid = grid_of(ts, args.M, args.N, batch);
+  KK_TRY(check_grid(grid, batch));
+  // Vector paths: A fp32 with K contiguous; B with N contiguous; rows (and
+  // batch strides) whole 4-element groups, aligned to them.
+  const int bsz = dtype_size(args.b_dt);
+  bool a_quad = args.a_dt == KK_F32 && args.a_sj == 1 && args.K % 4 == 0 && args.a_si % 4 == 0 &&
+                aligned(args.a, 16);
+  bool b_quad = args.b_sj == 1 && args.N % 4 == 0 && args.b_si % 4 == 0 && aligned(args.b, 4 * bsz);
+  for (int d = 0; d < args.bm.nb; ++d) {
+    if (args.bm.st[0][d] % 4) a_quad = false;
+    if (args.bm.st[1][d] % 4) b_quad = false;
+  }
+  if (a_quad && b_quad) {
+    switch (args.b_dt) {
+      case KK_F32: KK_TILED(gemm_kernel, ts, grid, 0, 0, float); break;
+      case KK_F16: KK_TILED(gemm_kernel, ts, grid, 0, 0, __half); break;
+      case KK_I8: KK_TILED(gemm_kernel, ts, grid, 0, 0, int8_t); break;
+      default: KK_TILED(gemm_kernel, ts, grid, 0, 0, uint8_t); break;
+    }
+  } else if (a_quad) {
+    KK_TILED(gemm_kernel, ts, grid, 0, 1, float);
+  } else if (b_quad) {
+    switch (args.b_dt) {
+      case KK_F32: KK_TILED(gemm_kernel, ts, grid, 1, 0, float); break;
+      case KK_F16: KK_TILED(gemm_kernel, ts, grid, 1, 0, __half); break;
+      case KK_I8: KK_TILED(gemm_kernel, ts, grid, 1, 0, int8_t); break;
+      default: KK_TILED(gemm_kernel, ts, grid, 1, 0, uint8_t); break;
+    }
+  } else {
+    KK_TILED(gemm_kernel, ts, grid, 1, 1, float);
+  }
+  return check_launch("gemm_kernel");
 }
 
 }  // namespace kk
@@ -441,7 +734,7 @@ int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const 
   if (out->shape[out->rank - 2] != M || out->shape[out->rank - 1] != N)
     return set_error(KK_E_ARG, "kk_gemm: out must end in [%lld, %lld]", (long long)M, (long long)N);
   GemmArgs G{};
-  KK_TRY(make_dequant(&G.b.dq, w, w_scale, w_zp, N, "kk_gemm"));
+  KK_TRY(make_dequant(&G.dq, w, w_scale, w_zp, N, "kk_gemm"));
   // Batch axes: numpy broadcasting of a[:-2] and w[:-2] against out[:-2].
   const int nb = out->rank - 2;
   if (nb > 6) return set_error(KK_E_UNSUPPORTED, "kk_gemm: more than 6 batch axes");
@@ -465,28 +758,17 @@ int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const 
     }
   }
   if (M == 0 || N == 0 || batch == 0) return KK_OK;
-  G.a.p = a->data; G.a.dt = a->dtype;
-  G.a.si = a->strides[a->rank - 2]; G.a.sj = a->strides[a->rank - 1];
-  G.a.rows = M; G.a.cols = K;
-  G.b.p = w->data; G.b.dt = w->dtype;
-  G.b.si = w->strides[w->rank - 2]; G.b.sj = w->strides[w->rank - 1];
-  G.b.rows = K; G.b.cols = N; G.b.deq_by_col = 1;
+  if (K == 0) return kk_fill(out, 0.0);
+  G.a = a->data; G.a_dt = a->dtype;
+  G.a_si = a->strides[a->rank - 2]; G.a_sj = a->strides[a->rank - 1];
+  G.b = w->data; G.b_dt = w->dtype;
+  G.b_si = w->strides[w->rank - 2]; G.b_sj = w->strides[w->rank - 1];
   G.out = static_cast<float*>(out->data);
   G.som = out->strides[out->rank - 2];
   G.son = out->strides[out->rank - 1];
   G.M = M; G.N = N; G.K = K;
   G.alpha = alpha;
-  // Coalesce each fetch along the operand's unit-stride direction.
-  G.a_kfast = (G.a.sj == 1) || (G.a.si != 1);
-  G.b_nfast = (G.b.sj == 1) || (G.b.si != 1);
-  if (K == 0) return kk_fill(out, 0.0);
-  int bm, bn;
-  tiles_for(M, N, batch, &bm, &bn);
-  const int64_t gx = ceil_div(N, bn), gy = ceil_div(M, bm);
-  KK_TRY(check_grid(gx, gy, batch));
-  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(batch));
-  KK_LAUNCH_TILED(gemm_kernel, bm, bn, grid, G);
-  return check_launch("gemm_kernel");
+  return launch_gemm(G, batch);
 }
 
 int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* w_scale,
@@ -511,23 +793,27 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
   if (N * Cout * Lout == 0) return KK_OK;
   const float* bp = bias ? static_cast<const float*>(bias->data) : nullptr;
   if (group == 1) {
-    ConvArgs C{};
-    C.w.p = w->data; C.w.dt = w->dtype; C.w.si = cin_g * K; C.w.sj = 1;
-    C.w.rows = Cout; C.w.cols = Cin * K; C.w.dq = dq; C.w.deq_by_col = 0;
-    C.x.x = static_cast<const float*>(x->data);
-    C.x.cin = Cin; C.x.L = L; C.x.K = K; C.x.s = stride; C.x.d = dilation; C.x.p0 = pad0;
-    C.x.rows = Cin * K; C.x.cols = Lout;
-    C.out = static_cast<float*>(out->data);
-    C.bias = bp;
-    C.x_bstride = Cin * L;
-    C.o_bstride = Cout * Lout;
-    C.M = Cout; C.N = Lout; C.K = Cin * K;
-    int bm, bn;
-    tiles_for(Cout, Lout, N, &bm, &bn);
-    const int64_t gx = ceil_div(Lout, bn), gy = ceil_div(Cout, bm);
-    KK_TRY(check_grid(gx, gy, N));
-    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(N));
-    KK_LAUNCH_TILED(conv1d_kernel, bm, bn, grid, C);
+    ConvArgs args{};
+    args.w = w->data; args.w_dt = w->dtype; args.dq = dq;
+    args.x = static_cast<const float*>(x->data);
+    args.out = static_cast<float*>(out->data);
+    args.bias = bp;
+    args.Cin = Cin; args.L = L; args.Kw = K; args.s = stride; args.d = dilation; args.p0 = pad0;
+    args.Lout = Lout; args.M = Cout; args.K = Cin * K;
+    const TileSize ts = pick_tile(Cout, Lout, N);
+    const dim3 grid = grid_of(ts, Cout, Lout, N);
+    KK_TRY(check_grid(grid, N));
+    const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4 * dtype_size(w->dtype));
+    if (!quad) {
+      KK_TILED(conv1d_kernel, ts, grid, 1, float);
+    } else {
+      switch (w->dtype) {
+        case KK_F32: KK_TILED(conv1d_kernel, ts, grid, 0, float); break;
+        case KK_F16: KK_TILED(conv1d_kernel, ts, grid, 0, __half); break;
+        case KK_I8: KK_TILED(conv1d_kernel, ts, grid, 0, int8_t); break;
+        default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t); break;
+      }
+    }
     return check_launch("conv1d_kernel");
   }
   DirectArgs D{};
@@ -567,28 +853,26 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
   const float* bp = bias ? static_cast<const float*>(bias->data) : nullptr;
   if (group == 1 && dilation == 1) {
     // Phase decomposition: s sub-GEMMs of MR = ceil(K/s) taps each.  Output
-    // position jo maps to j = jo + p0 = q*s + r.  Positions j >= (L-1)s+K
-    // (output_padding tail) receive nothing but the bias, handled because
-    // every q up to the last j is enumerated and x reads are bounds-checked.
-    const int64_t MR = ceil_div(K, stride);
-    ConvTArgs C{};
-    C.w.w = w->data; C.w.dt = w->dtype; C.w.dq = dq; C.w.cout_g = cout_g; C.w.K = K;
-    C.w.s = stride; C.w.MR = MR; C.w.rows = Cout; C.w.cols = Cin * MR;
-    C.x.x = static_cast<const float*>(x->data); C.x.L = L; C.x.MR = MR; C.x.rows = Cin * MR;
+    // position jo maps to j = jo + p0 = q*s + r; every q up to the last
+    // needed j is enumerated (x reads are bounds-checked, so the
+    // output_padding tail gets the bias alone).
+    ConvTArgs args{};
+    args.w = w->data; args.w_dt = w->dtype; args.dq = dq;
+    args.x = static_cast<const float*>(x->data);
+    args.out = static_cast<float*>(out->data); args.bias = bp;
+    args.Cin = Cin; args.Cout = Cout; args.L = L; args.Kw = K; args.s = stride;
+    args.MR = ceil_div(K, stride); args.p0 = pad0; args.Lout = Lout;
     const int64_t jmax = lfull - pad1 - 1;  // last needed uncropped position
-    C.nq = jmax / stride + 1;
-    C.x.cols = C.nq; C.x.q0 = 0;
-    C.out = static_cast<float*>(out->data); C.bias = bp;
-    C.x_bstride = Cin * L; C.o_bstride = Cout * Lout;
-    C.s = stride; C.p0 = pad0; C.Lout = Lout; C.lfull = lfull;
-    C.M = Cout; C.K = Cin * MR;
-    int bm, bn;
-    tiles_for(Cout, C.nq, N * stride, &bm, &bn);
-    const int64_t gx = ceil_div(C.nq, bn), gy = ceil_div(Cout, bm);
-    KK_TRY(check_grid(gx, gy, N * stride));
-    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy),
-                    static_cast<unsigned>(N * stride));
-    KK_LAUNCH_TILED(conv_transpose_kernel, bm, bn, grid, C);
+    args.nq = jmax / stride + 1;
+    const TileSize ts = pick_tile(Cout, args.nq, N * stride);
+    const dim3 grid = grid_of(ts, Cout, args.nq, N * stride);
+    KK_TRY(check_grid(grid, N * stride));
+    if (ts == TILE_L)
+      hipLaunchKernelGGL(conv_transpose_kernel<CfgL>, grid, dim3(kNT), 0, ctx().stream, args);
+    else if (ts == TILE_M)
+      hipLaunchKernelGGL(conv_transpose_kernel<CfgM>, grid, dim3(kNT), 0, ctx().stream, args);
+    else
+      hipLaunchKernelGGL(conv_transpose_kernel<CfgS>, grid, dim3(kNT), 0, ctx().stream, args);
     return check_launch("conv_transpose_kernel");
   }
   DirectArgs D{};

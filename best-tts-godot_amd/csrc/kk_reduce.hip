@@ -47,7 +47,9 @@ __device__ __forceinline__ float group_max(float v, float* lds) {
 
 // Loads this thread's share of a row of `n` floats into r[NV][VEC].
 // Element index of (j, e) is (j * GROUP + g) * VEC + e; missing ones are 0.
-template <int GROUP, int NV, int VEC>
+// STREAM rows are read once (non-temporal); parameter vectors shared by
+// every row (scale, bias) use ordinary cached loads.
+template <int GROUP, int NV, int VEC, bool STREAM = true>
 __device__ __forceinline__ void load_row(const float* __restrict__ row, int64_t n, int g,
                                          float (&r)[NV][VEC]) {
 #pragma unroll
@@ -55,13 +57,14 @@ __device__ __forceinline__ void load_row(const float* __restrict__ row, int64_t 
     const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
     if constexpr (VEC == 4) {
       if (base < n) {
-        const float4 v = *reinterpret_cast<const float4*>(row + base);
+        const float4 v = STREAM ? ld_stream4(row + base)
+                                : *reinterpret_cast<const float4*>(row + base);
         r[j][0] = v.x; r[j][1] = v.y; r[j][2] = v.z; r[j][3] = v.w;
       } else {
         r[j][0] = r[j][1] = r[j][2] = r[j][3] = 0.0f;
       }
     } else {
-      r[j][0] = base < n ? row[base] : 0.0f;
+      r[j][0] = base < n ? (STREAM ? ld_stream(row + base) : row[base]) : 0.0f;
     }
   }
 }
@@ -74,9 +77,9 @@ __device__ __forceinline__ void store_row(float* __restrict__ row, int64_t n, in
     const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
     if (base < n) {
       if constexpr (VEC == 4) {
-        *reinterpret_cast<float4*>(row + base) = make_float4(r[j][0], r[j][1], r[j][2], r[j][3]);
+        st_stream4(row + base, make_float4(r[j][0], r[j][1], r[j][2], r[j][3]));
       } else {
-        row[base] = r[j][0];
+        st_stream(row + base, r[j][0]);
       }
     }
   }
@@ -254,7 +257,7 @@ __global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict_
 #pragma unroll
       for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] + k[j][e];
     if (la.skip_bias) {
-      load_row<GROUP, NV, VEC>(la.skip_bias, cols, g, k);
+      load_row<GROUP, NV, VEC, false>(la.skip_bias, cols, g, k);
 #pragma unroll
       for (int j = 0; j < NV; ++j)
 #pragma unroll
@@ -265,13 +268,13 @@ __global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict_
   row_stats<GROUP, NV, VEC>(r, cols, g, lds, mean, var);
   const float den = sqrtf(var + eps);
   float sc[NV][VEC];
-  load_row<GROUP, NV, VEC>(la.scale, cols, g, sc);
+  load_row<GROUP, NV, VEC, false>(la.scale, cols, g, sc);
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) r[j][e] = (r[j][e] / den) * sc[j][e];
   if (la.bias) {
-    load_row<GROUP, NV, VEC>(la.bias, cols, g, sc);
+    load_row<GROUP, NV, VEC, false>(la.bias, cols, g, sc);
 #pragma unroll
     for (int j = 0; j < NV; ++j)
 #pragma unroll
