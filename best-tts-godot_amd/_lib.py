@@ -82,6 +82,15 @@ PROTOTYPES = {
     "kk_conv_transpose1d": [_T, _T, _T, _T, _T, _T, _i, _i, _i, _i, _i, _i],
     "kk_event_record": [_i],
     "kk_event_elapsed": [_i, _i, ctypes.POINTER(_f)],
+    "kk_dynamic_quantize_linear": [_T, _T, _T, _T],
+    "kk_matmul_integer": [_T, _T, _T, _T, _T],
+    "kk_conv_integer": [_T, _T, _T, _T, _T, _i, _i, _i, _i, _i],
+    "kk_lstm": [_T] * 13 + [_i, _i],
+    "kk_stft": [_T, _T, _T, ctypes.c_int64, ctypes.c_int64, _i],
+    "kk_resize": [_T, _T, _i, _d],
+    "kk_pad": [_T, _T, ctypes.POINTER(ctypes.c_int64), _i, _f],
+    "kk_cumsum": [_T, _T, _i],
+    "kk_scatter_nd": [_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int64, ctypes.c_int64],
     "kk_graph_begin": [],
     "kk_graph_end": [ctypes.POINTER(_i)],
     "kk_graph_launch": [_i],

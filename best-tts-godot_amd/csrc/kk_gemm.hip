@@ -53,8 +53,9 @@ __device__ __forceinline__ int64_t batch_offset(const BatchMap& bm, int which, i
 }
 
 // Scale and zero point of one weight row/column, read once per block.
+// A NULL scale means 1 (the integer ops shift by their zero point only).
 __device__ __forceinline__ void dq_params(const Dequant& dq, int64_t idx, float& s, float& z) {
-  s = load_as_f32(dq.scale, dq.scale_dt, idx * dq.scale_stride);
+  s = dq.scale ? load_as_f32(dq.scale, dq.scale_dt, idx * dq.scale_stride) : 1.0f;
   z = dq.zp ? load_as_f32(dq.zp, dq.zp_dt, idx * dq.zp_stride) : 0.0f;
 }
 
@@ -267,13 +268,16 @@ struct BScalar {
 };
 
 // Conv1d input as the B operand: B[kk, l] = x[ci, l*s + k*d - p0] with
-// kk = ci*Kw + k; each thread gathers four consecutive l of one kk.
-template <class C>
+// kk = ci*Kw + k; each thread gathers four consecutive l of one kk.  For
+// ConvInteger, x is uint8 and in-range taps read x - x_zp while padding
+// reads 0 (the zero-point shift precedes the padding, ref_runtime.py:131-133).
+template <class C, typename TX = float>
 struct BIm2col {
   static constexpr int QPR = C::BN / 4;
   static constexpr int RPP = kNT / QPR;
   static constexpr int P = kBK / RPP;
-  const float* x;  // this batch item's [Cin, L]
+  const TX* x;     // this batch item's [Cin, L]
+  float xzp = 0.0f;
   int64_t L, Kw, s, d, p0, Kdim, Lout;
   int64_t l0;      // first output position of this thread's quad
   float4 v[P];
@@ -285,12 +289,15 @@ struct BIm2col {
       float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (kk < Kdim) {
         const int64_t ci = kk / Kw, k = kk - ci * Kw;
-        const float* xr = x + ci * L;
+        const TX* xr = x + ci * L;
         const int64_t pos0 = l0 * s + k * d - p0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int64_t pos = pos0 + c * s;
-          if (l0 + c < Lout && pos >= 0 && pos < L) e[c] = xr[pos];
+          if (l0 + c < Lout && pos >= 0 && pos < L) {
+            if constexpr (std::is_same<TX, float>::value) e[c] = xr[pos];
+            else e[c] = static_cast<float>(xr[pos]) - xzp;
+          }
         }
       }
       v[p] = make_float4(e[0], e[1], e[2], e[3]);
@@ -373,20 +380,22 @@ struct GemmArgs {
   const void* a;
   int a_dt;
   int64_t a_si, a_sj;  // element strides of A [M, K]
+  Dequant adq;         // A's zero-point shift (MatMulInteger), per tensor
   const void* b;
   int b_dt;
   int64_t b_si, b_sj;  // element strides of B [K, N]
   Dequant dq;          // B's dequantisation (per column or per tensor)
-  float* out;
+  float* out;          // fp32, or int32 when out_i32
+  int out_i32;         // store round-half-even(acc) as int32 (MatMulInteger)
   int64_t som, son;
   BatchMap bm;
   int64_t M, N, K;
   float alpha;
 };
 
-// A kinds: 0 = fp32 K-contiguous quads, 1 = scalar gather.
+// A kinds: 0 = K-contiguous quads of TA, 1 = scalar gather.
 // B kinds: 0 = N-contiguous quads of TB, 1 = scalar gather.
-template <class C, int AK, int BK, typename TB>
+template <class C, int AK, int BK, typename TA, typename TB>
 __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
   const int64_t bz = blockIdx.z;
   const int64_t oa = batch_offset(G.bm, 0, bz), ob = batch_offset(G.bm, 1, bz),
@@ -396,13 +405,16 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
   float* out = G.out + oo;
   const float alpha = G.alpha;
   const int64_t som = G.som, son = G.son;
+  const bool out_i32 = G.out_i32;
   auto store = [&](int64_t m, int64_t n, float v) {
-    out[m * som + n * son] = alpha == 1.0f ? v : v * alpha;
+    if (out_i32) reinterpret_cast<int32_t*>(out)[m * som + n * son] = __float2int_rn(v);
+    else out[m * som + n * son] = alpha == 1.0f ? v : v * alpha;
   };
   const int64_t M = G.M, N = G.N, K = G.K;
   auto getA = [&](int64_t m, int64_t k) -> float {
     if (m >= M || k >= K) return 0.0f;
-    return load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
+    const float q = load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
+    return G.adq.active ? dequant_value(q, G.adq, m) : q;
   };
   auto getB = [&](int64_t k, int64_t n) -> float {
     if (k >= K || n >= N) return 0.0f;
@@ -410,14 +422,14 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
     return G.dq.active ? dequant_value(q, G.dq, n) : q;
   };
   if constexpr (AK == 0 && BK == 0) {
-    AQuad<C, float> la;
-    la.init(static_cast<const float*>(G.a) + oa, G.a_si, M, K, m0, G.dq);
+    AQuad<C, TA> la;
+    la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, G.adq);
     BQuad<C, TB> lb;
     lb.init(static_cast<const TB*>(G.b) + ob, G.b_si, N, K, n0, G.dq);
     gemm_run<C>(la, lb, store, M, N, K, m0, n0);
   } else if constexpr (AK == 0) {
-    AQuad<C, float> la;
-    la.init(static_cast<const float*>(G.a) + oa, G.a_si, M, K, m0, G.dq);
+    AQuad<C, TA> la;
+    la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, G.adq);
     if (G.b_si == 1) {
       BScalar<C, decltype(getB), false> lb{getB, n0};
       gemm_run<C>(la, lb, store, M, N, K, m0, n0);
@@ -464,15 +476,17 @@ struct ConvArgs {
   const void* w;       // [Cout, Cin*Kw] (K contiguous)
   int w_dt;
   Dequant dq;          // per output channel (row) or per tensor
-  const float* x;      // [N, Cin, L]
-  float* out;          // [N, Cout, Lout]
+  const void* x;       // [N, Cin, L], fp32 (Conv) or uint8 (ConvInteger)
+  const void* xzp;     // ConvInteger: uint8 zero point of x, or NULL
+  float* out;          // [N, Cout, Lout], fp32 or int32 when out_i32
+  int out_i32;
   const float* bias;   // [Cout] or NULL
   int64_t Cin, L, Kw, s, d, p0, Lout;
   int64_t M, K;        // Cout, Cin*Kw
 };
 
-// AK: 0 = quad loads of TW (K % 4 == 0), 1 = scalar gather.
-template <class C, int AK, typename TW>
+// AK: 0 = quad loads of TW (K % 4 == 0), 1 = scalar gather.  TX: x's type.
+template <class C, int AK, typename TW, typename TX>
 __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
   const int64_t bz = blockIdx.z;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
@@ -480,12 +494,17 @@ __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
   const int64_t M = A.M, N = A.Lout, K = A.K;
   float* out = A.out + bz * M * N;
   const float* bias = A.bias;
-  auto store = [&](int64_t m, int64_t n, float v) { out[m * N + n] = bias ? v + bias[m] : v; };
-  BIm2col<C> lb;
-  lb.x = A.x + bz * A.Cin * A.L;
+  const bool out_i32 = A.out_i32;
+  auto store = [&](int64_t m, int64_t n, float v) {
+    if (out_i32) reinterpret_cast<int32_t*>(out)[m * N + n] = __float2int_rn(v);
+    else out[m * N + n] = bias ? v + bias[m] : v;
+  };
+  BIm2col<C, TX> lb;
+  lb.x = static_cast<const TX*>(A.x) + bz * A.Cin * A.L;
+  lb.xzp = A.xzp ? static_cast<float>(*static_cast<const uint8_t*>(A.xzp)) : 0.0f;
   lb.L = A.L; lb.Kw = A.Kw; lb.s = A.s; lb.d = A.d; lb.p0 = A.p0; lb.Kdim = K; lb.Lout = N;
-  lb.r0 = threadIdx.x / BIm2col<C>::QPR;
-  lb.l0 = n0 + (threadIdx.x % BIm2col<C>::QPR) * 4;
+  lb.r0 = threadIdx.x / BIm2col<C, TX>::QPR;
+  lb.l0 = n0 + (threadIdx.x % BIm2col<C, TX>::QPR) * 4;
   if constexpr (AK == 0) {
     AQuad<C, TW> la;
     la.init(static_cast<const TW*>(A.w), K, M, K, m0, A.dq);
@@ -682,33 +701,114 @@ static int launch_gemm(const GemmArgs& args, int64_t batch) {
   // Vector paths: A fp32 with K contiguous; B with N contiguous; rows (and
   // batch strides) whole 4-element groups, aligned to them.
   const int bsz = dtype_size(args.b_dt);
-  bool a_quad = args.a_dt == KK_F32 && args.a_sj == 1 && args.K % 4 == 0 && args.a_si % 4 == 0 &&
-                aligned(args.a, 16);
+  // (uint8 A -- MatMulInteger -- is vectorised only together with int8 B.)
+  const int asz = dtype_size(args.a_dt);
+  bool a_quad = (args.a_dt == KK_F32 || (args.a_dt == KK_U8 && args.b_dt == KK_I8)) &&
+                args.a_sj == 1 && args.K % 4 == 0 && args.a_si % 4 == 0 &&
+                aligned(args.a, 4 * asz);
   bool b_quad = args.b_sj == 1 && args.N % 4 == 0 && args.b_si % 4 == 0 && aligned(args.b, 4 * bsz);
   for (int d = 0; d < args.bm.nb; ++d) {
     if (args.bm.st[0][d] % 4) a_quad = false;
     if (args.bm.st[1][d] % 4) b_quad = false;
   }
   if (a_quad && b_quad) {
-    switch (args.b_dt) {
-      case KK_F32: KK_TILED(gemm_kernel, ts, grid, 0, 0, float); break;
-      case KK_F16: KK_TILED(gemm_kernel, ts, grid, 0, 0, __half); break;
-      case KK_I8: KK_TILED(gemm_kernel, ts, grid, 0, 0, int8_t); break;
-      default: KK_TILED(gemm_kernel, ts, grid, 0, 0, uint8_t); break;
+    if (args.a_dt == KK_U8) {  // MatMulInteger: uint8 activations, int8 weights
+      KK_TILED(gemm_kernel, ts, grid, 0, 0, uint8_t, int8_t);
+    } else {
+      switch (args.b_dt) {
+        case KK_F32: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, float); break;
+        case KK_F16: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, __half); break;
+        case KK_I8: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, int8_t); break;
+        default: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, uint8_t); break;
+      }
     }
-  } else if (a_quad) {
-    KK_TILED(gemm_kernel, ts, grid, 0, 1, float);
+  } else if (a_quad && args.a_dt == KK_F32) {
+    KK_TILED(gemm_kernel, ts, grid, 0, 1, float, float);
   } else if (b_quad) {
     switch (args.b_dt) {
-      case KK_F32: KK_TILED(gemm_kernel, ts, grid, 1, 0, float); break;
-      case KK_F16: KK_TILED(gemm_kernel, ts, grid, 1, 0, __half); break;
-      case KK_I8: KK_TILED(gemm_kernel, ts, grid, 1, 0, int8_t); break;
-      default: KK_TILED(gemm_kernel, ts, grid, 1, 0, uint8_t); break;
+      case KK_F32: KK_TILED(gemm_kernel, ts, grid, 1, 0, float, float); break;
+      case KK_F16: KK_TILED(gemm_kernel, ts, grid, 1, 0, float, __half); break;
+      case KK_I8: KK_TILED(gemm_kernel, ts, grid, 1, 0, float, int8_t); break;
+      default: KK_TILED(gemm_kernel, ts, grid, 1, 0, float, uint8_t); break;
     }
   } else {
-    KK_TILED(gemm_kernel, ts, grid, 1, 1, float);
+    KK_TILED(gemm_kernel, ts, grid, 1, 1, float, float);
   }
   return check_launch("gemm_kernel");
+}
+
+
+// Shapes, batch broadcasting and strides of out = a @ w (numpy matmul rules
+// for rank >= 2 operands).  Leaves the dequantisation to the caller.
+static int setup_gemm(GemmArgs* G, const kk_tensor* out, const kk_tensor* a, const kk_tensor* w,
+                      int64_t* batch_out, const char* who) {
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(out, "out"));
+  KK_TRY(check_tensor(a, "a"));
+  KK_TRY(check_tensor(w, "w"));
+  if (a->rank < 2 || w->rank < 2 || out->rank < 2)
+    return set_error(KK_E_ARG, "%s: operands need rank >= 2 (promote vectors first)", who);
+  const int64_t M = a->shape[a->rank - 2], K = a->shape[a->rank - 1];
+  const int64_t K2 = w->shape[w->rank - 2], N = w->shape[w->rank - 1];
+  if (K != K2)
+    return set_error(KK_E_ARG, "%s: inner extents differ (%lld vs %lld)", who, (long long)K,
+                     (long long)K2);
+  if (out->shape[out->rank - 2] != M || out->shape[out->rank - 1] != N)
+    return set_error(KK_E_ARG, "%s: out must end in [%lld, %lld]", who, (long long)M,
+                     (long long)N);
+  const int nb = out->rank - 2;
+  if (nb > 6) return set_error(KK_E_UNSUPPORTED, "%s: more than 6 batch axes", who);
+  if (a->rank - 2 > nb || w->rank - 2 > nb)
+    return set_error(KK_E_ARG, "%s: operand has more batch axes than out", who);
+  int64_t batch = 1;
+  G->bm.nb = nb;
+  for (int i = 0; i < nb; ++i) {
+    const int64_t od = out->shape[i];
+    G->bm.dims[i] = od;
+    G->bm.st[2][i] = out->strides[i];
+    batch *= od;
+    const kk_tensor* ops[2] = {a, w};
+    for (int k = 0; k < 2; ++k) {
+      const int pad = nb - (ops[k]->rank - 2);
+      if (i < pad) { G->bm.st[k][i] = 0; continue; }
+      const int64_t d = ops[k]->shape[i - pad];
+      if (d == od) G->bm.st[k][i] = ops[k]->strides[i - pad];
+      else if (d == 1) G->bm.st[k][i] = 0;
+      else return set_error(KK_E_ARG, "%s: batch axis %d does not broadcast", who, i);
+    }
+  }
+  G->a = a->data; G->a_dt = a->dtype;
+  G->a_si = a->strides[a->rank - 2]; G->a_sj = a->strides[a->rank - 1];
+  G->b = w->data; G->b_dt = w->dtype;
+  G->b_si = w->strides[w->rank - 2]; G->b_sj = w->strides[w->rank - 1];
+  G->out = static_cast<float*>(out->data);
+  G->som = out->strides[out->rank - 2];
+  G->son = out->strides[out->rank - 1];
+  G->M = M; G->N = N; G->K = K;
+  G->alpha = 1.0f;
+  *batch_out = batch;
+  return KK_OK;
+}
+
+// A zero-point-only shift (scale 1) for the integer ops: per tensor, or per
+// element of `count` when the zero point has that many elements.
+static int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* who) {
+  *d = Dequant();
+  if (!zp) return KK_OK;
+  KK_TRY(check_tensor(zp, "zero point"));
+  if (!(zp->dtype == KK_I8 || zp->dtype == KK_U8 || zp->dtype == KK_I32))
+    return set_error(KK_E_ARG, "%s: zero point must be int8/uint8/int32", who);
+  const int64_t n = numel(zp);
+  if (n != 1 && n != count)
+    return set_error(KK_E_ARG, "%s: zero point has %lld elements, expected 1 or %lld", who,
+                     (long long)n, (long long)count);
+  if (n > 1 && !is_contiguous(zp))
+    return set_error(KK_E_ARG, "%s: per-column zero point must be contiguous", who);
+  d->zp = zp->data;
+  d->zp_dt = zp->dtype;
+  d->zp_stride = n > 1 ? 1 : 0;
+  d->active = true;
+  return KK_OK;
 }
 
 }  // namespace kk
@@ -719,55 +819,31 @@ extern "C" {
 
 int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
             const kk_tensor* w_zp, float alpha) {
-  KK_TRY(require_ready());
-  KK_TRY(check_tensor(out, "out"));
-  KK_TRY(check_tensor(a, "a"));
-  KK_TRY(check_tensor(w, "w"));
-  if (a->rank < 2 || w->rank < 2 || out->rank < 2)
-    return set_error(KK_E_ARG, "kk_gemm: operands need rank >= 2 (promote vectors first)");
+  GemmArgs G{};
+  int64_t batch = 0;
+  KK_TRY(setup_gemm(&G, out, a, w, &batch, "kk_gemm"));
   if (!is_float(a->dtype)) return set_error(KK_E_ARG, "kk_gemm: a must be f32/f16");
   if (out->dtype != KK_F32) return set_error(KK_E_ARG, "kk_gemm: out must be fp32");
-  const int64_t M = a->shape[a->rank - 2], K = a->shape[a->rank - 1];
-  const int64_t K2 = w->shape[w->rank - 2], N = w->shape[w->rank - 1];
-  if (K != K2) return set_error(KK_E_ARG, "kk_gemm: inner extents differ (%lld vs %lld)",
-                                (long long)K, (long long)K2);
-  if (out->shape[out->rank - 2] != M || out->shape[out->rank - 1] != N)
-    return set_error(KK_E_ARG, "kk_gemm: out must end in [%lld, %lld]", (long long)M, (long long)N);
-  GemmArgs G{};
-  KK_TRY(make_dequant(&G.dq, w, w_scale, w_zp, N, "kk_gemm"));
-  // Batch axes: numpy broadcasting of a[:-2] and w[:-2] against out[:-2].
-  const int nb = out->rank - 2;
-  if (nb > 6) return set_error(KK_E_UNSUPPORTED, "kk_gemm: more than 6 batch axes");
-  if (a->rank - 2 > nb || w->rank - 2 > nb)
-    return set_error(KK_E_ARG, "kk_gemm: operand has more batch axes than out");
-  int64_t batch = 1;
-  G.bm.nb = nb;
-  for (int i = 0; i < nb; ++i) {
-    const int64_t od = out->shape[i];
-    G.bm.dims[i] = od;
-    G.bm.st[2][i] = out->strides[i];
-    batch *= od;
-    const kk_tensor* ops[2] = {a, w};
-    for (int k = 0; k < 2; ++k) {
-      const int pad = nb - (ops[k]->rank - 2);
-      if (i < pad) { G.bm.st[k][i] = 0; continue; }
-      const int64_t d = ops[k]->shape[i - pad];
-      if (d == od) G.bm.st[k][i] = ops[k]->strides[i - pad];
-      else if (d == 1) G.bm.st[k][i] = 0;
-      else return set_error(KK_E_ARG, "kk_gemm: batch axis %d does not broadcast", i);
-    }
-  }
-  if (M == 0 || N == 0 || batch == 0) return KK_OK;
-  if (K == 0) return kk_fill(out, 0.0);
-  G.a = a->data; G.a_dt = a->dtype;
-  G.a_si = a->strides[a->rank - 2]; G.a_sj = a->strides[a->rank - 1];
-  G.b = w->data; G.b_dt = w->dtype;
-  G.b_si = w->strides[w->rank - 2]; G.b_sj = w->strides[w->rank - 1];
-  G.out = static_cast<float*>(out->data);
-  G.som = out->strides[out->rank - 2];
-  G.son = out->strides[out->rank - 1];
-  G.M = M; G.N = N; G.K = K;
+  KK_TRY(make_dequant(&G.dq, w, w_scale, w_zp, G.N, "kk_gemm"));
   G.alpha = alpha;
+  if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
+  if (G.K == 0) return kk_fill(out, 0.0);
+  return launch_gemm(G, batch);
+}
+
+int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
+                      const kk_tensor* a_zp, const kk_tensor* b_zp) {
+  GemmArgs G{};
+  int64_t batch = 0;
+  KK_TRY(setup_gemm(&G, out, a, b, &batch, "kk_matmul_integer"));
+  if (!(a->dtype == KK_U8 || a->dtype == KK_I8) || !(b->dtype == KK_U8 || b->dtype == KK_I8))
+    return set_error(KK_E_ARG, "kk_matmul_integer: a and b must be uint8/int8");
+  if (out->dtype != KK_I32) return set_error(KK_E_ARG, "kk_matmul_integer: out must be int32");
+  KK_TRY(zp_shift(&G.adq, a_zp, 1, "kk_matmul_integer"));
+  KK_TRY(zp_shift(&G.dq, b_zp, G.N, "kk_matmul_integer"));
+  G.out_i32 = 1;
+  if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
+  if (G.K == 0) return kk_fill(out, 0.0);
   return launch_gemm(G, batch);
 }
 
@@ -795,7 +871,7 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
   if (group == 1) {
     ConvArgs args{};
     args.w = w->data; args.w_dt = w->dtype; args.dq = dq;
-    args.x = static_cast<const float*>(x->data);
+    args.x = x->data;
     args.out = static_cast<float*>(out->data);
     args.bias = bp;
     args.Cin = Cin; args.L = L; args.Kw = K; args.s = stride; args.d = dilation; args.p0 = pad0;
@@ -805,13 +881,13 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
     KK_TRY(check_grid(grid, N));
     const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4 * dtype_size(w->dtype));
     if (!quad) {
-      KK_TILED(conv1d_kernel, ts, grid, 1, float);
+      KK_TILED(conv1d_kernel, ts, grid, 1, float, float);
     } else {
       switch (w->dtype) {
-        case KK_F32: KK_TILED(conv1d_kernel, ts, grid, 0, float); break;
-        case KK_F16: KK_TILED(conv1d_kernel, ts, grid, 0, __half); break;
-        case KK_I8: KK_TILED(conv1d_kernel, ts, grid, 0, int8_t); break;
-        default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t); break;
+        case KK_F32: KK_TILED(conv1d_kernel, ts, grid, 0, float, float); break;
+        case KK_F16: KK_TILED(conv1d_kernel, ts, grid, 0, __half, float); break;
+        case KK_I8: KK_TILED(conv1d_kernel, ts, grid, 0, int8_t, float); break;
+        default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t, float); break;
       }
     }
     return check_launch("conv1d_kernel");
@@ -825,6 +901,60 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 1 << 20));
   hipLaunchKernelGGL(conv1d_direct_kernel, dim3(grid), dim3(256), 0, ctx().stream, D);
   return check_launch("conv1d_direct_kernel");
+}
+
+int kk_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                    const kk_tensor* x_zp, const kk_tensor* w_zp, int stride, int dilation,
+                    int pad0, int pad1, int group) {
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(out, "out"));
+  KK_TRY(check_tensor(x, "x"));
+  KK_TRY(check_tensor(w, "w"));
+  if (x->rank != 3 || w->rank != 3 || out->rank != 3)
+    return set_error(KK_E_ARG, "kk_conv_integer: x, w and out must be rank 3");
+  if (x->dtype != KK_U8 || !(w->dtype == KK_U8 || w->dtype == KK_I8) || out->dtype != KK_I32)
+    return set_error(KK_E_ARG, "kk_conv_integer: x uint8, w uint8/int8, out int32");
+  if (!is_contiguous(x) || !is_contiguous(out) || !is_contiguous(w))
+    return set_error(KK_E_ARG, "kk_conv_integer: x, w and out must be contiguous");
+  if (group != 1) return set_error(KK_E_UNSUPPORTED, "kk_conv_integer: group %d", group);
+  const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
+  const int64_t Cout = w->shape[0], K = w->shape[2];
+  if (w->shape[1] != Cin) return set_error(KK_E_ARG, "kk_conv_integer: w must be [Cout, Cin, K]");
+  if (stride < 1 || dilation < 1 || pad0 < 0 || pad1 < 0)
+    return set_error(KK_E_ARG, "kk_conv_integer: bad stride/dilation/pads");
+  const int64_t span = static_cast<int64_t>(dilation) * (K - 1) + 1;
+  const int64_t Lp = L + pad0 + pad1;
+  const int64_t Lout = Lp >= span ? (Lp - span) / stride + 1 : 0;
+  if (out->shape[0] != N || out->shape[1] != Cout || out->shape[2] != Lout)
+    return set_error(KK_E_ARG, "kk_conv_integer: out must be [%lld, %lld, %lld]", (long long)N,
+                     (long long)Cout, (long long)Lout);
+  ConvArgs args{};
+  KK_TRY(zp_shift(&args.dq, w_zp, Cout, "kk_conv_integer"));
+  if (x_zp) {
+    KK_TRY(check_tensor(x_zp, "x_zp"));
+    if (x_zp->dtype != KK_U8 || numel(x_zp) != 1)
+      return set_error(KK_E_ARG, "kk_conv_integer: x_zp must be one uint8");
+    args.xzp = x_zp->data;
+  }
+  if (N * Cout * Lout == 0) return KK_OK;
+  args.w = w->data; args.w_dt = w->dtype;
+  args.x = x->data;
+  args.out = static_cast<float*>(out->data);
+  args.out_i32 = 1;
+  args.Cin = Cin; args.L = L; args.Kw = K; args.s = stride; args.d = dilation; args.p0 = pad0;
+  args.Lout = Lout; args.M = Cout; args.K = Cin * K;
+  const TileSize ts = pick_tile(Cout, Lout, N);
+  const dim3 grid = grid_of(ts, Cout, Lout, N);
+  KK_TRY(check_grid(grid, N));
+  const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4);
+  if (!quad) {
+    KK_TILED(conv1d_kernel, ts, grid, 1, float, uint8_t);
+  } else if (w->dtype == KK_U8) {
+    KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t, uint8_t);
+  } else {
+    KK_TILED(conv1d_kernel, ts, grid, 0, int8_t, uint8_t);
+  }
+  return check_launch("conv1d_kernel");
 }
 
 int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,

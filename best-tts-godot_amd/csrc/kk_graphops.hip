@@ -1,0 +1,562 @@
+// The rest of the Kokoro graph's device ops: DynamicQuantizeLinear, the
+// DynamicQuantizeLSTM recurrence, STFT, Resize, Pad, CumSum and ScatterND.
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "kk_internal.h"
+
+namespace kk {
+
+// --------------------------------------------------- DynamicQuantizeLinear
+// Stage 1: per-block min/max.  Stage 2: every block folds the partials,
+// derives scale and zero point in double exactly as the reference does
+// (ref_runtime.py:106-116), and quantises its share.
+constexpr int kDqlBlocks = 512;
+
+__global__ void __launch_bounds__(256) dql_minmax(const float* __restrict__ x, int64_t n,
+                                                   float2* __restrict__ part) {
+  __shared__ float smin[4], smax[4];
+  float lo = INFINITY, hi = -INFINITY;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float v = x[i];
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) { smin[w] = lo; smax[w] = hi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    part[blockIdx.x] = make_float2(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
+                                   fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])));
+  }
+}
+
+__global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x, int64_t n,
+                                                     const float2* __restrict__ part, int npart,
+                                                     uint8_t* __restrict__ y,
+                                                     float* __restrict__ scale_out,
+                                                     uint8_t* __restrict__ zp_out) {
+  __shared__ float smin[4], smax[4];
+  __shared__ float s_scale, s_zp;
+  float lo = INFINITY, hi = -INFINITY;
+  for (int i = threadIdx.x; i < npart; i += blockDim.x) {
+    lo = fminf(lo, part[i].x);
+    hi = fmaxf(hi, part[i].y);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) { smin[w] = lo; smax[w] = hi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const double mn = fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3]));
+    const double mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    const double dlo = mn < 0.0 ? mn : 0.0;
+    const double dhi = mx > 0.0 ? mx : 0.0;
+    double scale = (dhi - dlo) / 255.0;
+    if (scale == 0.0) scale = 1.0;
+    double zp = rint(0.0 - dlo / scale);
+    zp = zp < 0.0 ? 0.0 : (zp > 255.0 ? 255.0 : zp);
+    s_scale = static_cast<float>(scale);
+    s_zp = static_cast<float>(zp);
+    if (blockIdx.x == 0) {
+      *scale_out = s_scale;
+      *zp_out = static_cast<uint8_t>(zp);
+    }
+  }
+  __syncthreads();
+  const float sc = s_scale, z = s_zp;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    float v = rintf(x[i] / sc) + z;  // exact integers: the sum is exact in fp32
+    v = v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v);
+    y[i] = static_cast<uint8_t>(v);
+  }
+}
+
+// ------------------------------------------------------------------- LSTM
+// One block per (direction, batch row) runs the whole recurrence: thread j
+// owns gate column j of g = (xw[t] + (wb + rb)) + h @ R, with R's column
+// dequantised on the fly ((q - zp) * scale, the value op_lstm.deq builds);
+// h and the gates live in LDS.  Gate order i, o, f, c (ref_runtime.py:194-208).
+struct LstmArgs {
+  const float* xw;       // [ndir][seq * batch][4H] input projections x @ deq(W)
+  const float* bias;     // [ndir][8H] or NULL
+  const int8_t* r;       // [ndir][H][4H]
+  const void* r_scale;   // [ndir] (or 1 element)
+  int r_scale_dt;
+  int64_t r_scale_n;
+  const void* r_zp;      // [ndir] int8 or NULL
+  int r_zp_dt;
+  int64_t r_zp_n;
+  const float* init_h;   // [ndir][batch][H] or NULL
+  const float* init_c;
+  float* ys;             // [seq][ndir][batch][H]
+  float* yh;             // [ndir][batch][H] or NULL
+  float* yc;
+  int64_t seq, batch, H, ndir;
+};
+
+__global__ void __launch_bounds__(1024) lstm_recurrence(LstmArgs A) {
+  extern __shared__ float lds[];
+  const int64_t H = A.H, G4 = 4 * H;
+  float* hs = lds;        // [H]
+  float* gs = lds + H;    // [4H]
+  const int64_t d = blockIdx.x / A.batch, b = blockIdx.x % A.batch;
+  const float rs = load_as_f32(A.r_scale, A.r_scale_dt, A.r_scale_n > 1 ? d : 0);
+  const float rz = A.r_zp ? load_as_f32(A.r_zp, A.r_zp_dt, A.r_zp_n > 1 ? d : 0) : 0.0f;
+  const int8_t* R = A.r + d * H * G4;
+  const float* xw = A.xw + d * A.seq * A.batch * G4;
+  // c for the units this thread updates (thread u < H)
+  float c = 0.0f;
+  for (int64_t u = threadIdx.x; u < H; u += blockDim.x) {
+    hs[u] = A.init_h ? A.init_h[(d * A.batch + b) * H + u] : 0.0f;
+    if (u == threadIdx.x) c = A.init_c ? A.init_c[(d * A.batch + b) * H + u] : 0.0f;
+  }
+  __syncthreads();
+  for (int64_t step = 0; step < A.seq; ++step) {
+    const int64_t t = d == 0 ? step : A.seq - 1 - step;
+    for (int64_t j = threadIdx.x; j < G4; j += blockDim.x) {
+      float acc = 0.0f;
+      for (int64_t k = 0; k < H; ++k) {
+        const float q = static_cast<float>(R[k * G4 + j]);
+        acc = __builtin_fmaf(hs[k], (q - rz) * rs, acc);
+      }
+      float xv = xw[(t * A.batch + b) * G4 + j];
+      if (A.bias) xv = xv + (A.bias[d * 2 * G4 + j] + A.bias[d * 2 * G4 + G4 + j]);
+      gs[j] = xv + acc;
+    }
+    __syncthreads();
+    if (threadIdx.x < H) {
+      const int64_t u = threadIdx.x;
+      const float ig = 1.0f / (1.0f + expf(-gs[u]));
+      const float og = 1.0f / (1.0f + expf(-gs[H + u]));
+      const float fg = 1.0f / (1.0f + expf(-gs[2 * H + u]));
+      const float cc = tanhf(gs[3 * H + u]);
+      c = fg * c + ig * cc;
+      const float h = og * tanhf(c);
+      hs[u] = h;
+      A.ys[((t * A.ndir + d) * A.batch + b) * H + u] = h;
+      if (step == A.seq - 1) {
+        if (A.yh) A.yh[(d * A.batch + b) * H + u] = h;
+        if (A.yc) A.yc[(d * A.batch + b) * H + u] = c;
+      }
+    }
+    __syncthreads();
+  }
+  if (A.seq == 0 && threadIdx.x < H) {
+    const int64_t u = threadIdx.x;
+    if (A.yh) A.yh[(d * A.batch + b) * H + u] = hs[u];
+    if (A.yc) A.yc[(d * A.batch + b) * H + u] = c;
+  }
+}
+
+// ------------------------------------------------------------------- STFT
+// out[b, f, k, 0/1] = sum_t (sig[b, f*step + t] * win[t]) * cos/sin(-2 pi k t / n),
+// the product in fp32 and the sum in fp64 (op_stft: float32 frames @ a
+// float64 basis), rounded to fp32.
+__global__ void stft_kernel(float* __restrict__ out, const float* __restrict__ sig,
+                            const void* __restrict__ win, int win_dt, int64_t batch,
+                            int64_t slen, int64_t nframes, int64_t nfreq, int64_t n,
+                            int64_t step) {
+  const int64_t total = batch * nframes * nfreq;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t k = i % nfreq;
+    const int64_t f = (i / nfreq) % nframes;
+    const int64_t bi = i / (nfreq * nframes);
+    const float* s = sig + bi * slen + f * step;
+    double re = 0.0, im = 0.0;
+    for (int64_t t = 0; t < n; ++t) {
+      const float fr = s[t] * load_as_f32(win, win_dt, t);
+      const double ang = -2.0 * M_PI * static_cast<double>(k) * static_cast<double>(t) /
+                         static_cast<double>(n);
+      re += static_cast<double>(fr) * cos(ang);
+      im += static_cast<double>(fr) * sin(ang);
+    }
+    out[i * 2 + 0] = static_cast<float>(re);
+    out[i * 2 + 1] = static_cast<float>(im);
+  }
+}
+
+// ----------------------------------------------------------------- Resize
+// Along the last axis (op_resize, ref_runtime.py:236-256): mode 0 nearest
+// (asymmetric, floor), mode 1 linear (half_pixel); positions in fp64.
+__global__ void resize_kernel(float* __restrict__ out, const float* __restrict__ x, int64_t rows,
+                              int64_t lin, int64_t lout, double scale, int mode) {
+  const int64_t total = rows * lout;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t o = i % lout, r = i / lout;
+    const float* xr = x + r * lin;
+    if (mode == 0) {
+      int64_t src = static_cast<int64_t>(floor(static_cast<double>(o) / scale));
+      src = src < 0 ? 0 : (src > lin - 1 ? lin - 1 : src);
+      out[i] = xr[src];
+    } else {
+      double pos = (static_cast<double>(o) + 0.5) / scale - 0.5;
+      pos = pos < 0.0 ? 0.0 : (pos > static_cast<double>(lin - 1) ? static_cast<double>(lin - 1) : pos);
+      const int64_t i0 = static_cast<int64_t>(floor(pos));
+      const int64_t i1 = i0 + 1 > lin - 1 ? lin - 1 : i0 + 1;
+      const float frac = static_cast<float>(pos - static_cast<double>(i0));
+      out[i] = xr[i0] * (1.0f - frac) + xr[i1] * frac;
+    }
+  }
+}
+
+// -------------------------------------------------------------------- Pad
+// numpy.pad semantics (op_pad): mode 0 constant, 1 reflect (mirror without
+// repeating the edge), 2 edge.
+struct PadArgs {
+  int rank;
+  int64_t in_dims[KK_MAX_RANK], out_dims[KK_MAX_RANK], begin[KK_MAX_RANK];
+  int64_t in_st[KK_MAX_RANK];
+  int mode;
+  float value;
+  int64_t n;
+};
+
+__device__ __forceinline__ int64_t reflect_index(int64_t i, int64_t dim) {
+  if (dim == 1) return 0;
+  const int64_t period = 2 * (dim - 1);
+  int64_t m = i % period;
+  if (m < 0) m += period;
+  return m < dim ? m : period - m;
+}
+
+__global__ void pad_kernel(float* __restrict__ out, const float* __restrict__ x, PadArgs P) {
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < P.n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    int64_t rem = i, off = 0;
+    bool inside = true;
+    for (int d = P.rank - 1; d >= 0; --d) {
+      const int64_t o = rem % P.out_dims[d];
+      rem /= P.out_dims[d];
+      int64_t s = o - P.begin[d];
+      const int64_t dim = P.in_dims[d];
+      if (s < 0 || s >= dim) {
+        if (P.mode == 0) inside = false;
+        else if (P.mode == 1) s = reflect_index(s, dim);
+        else s = s < 0 ? 0 : dim - 1;
+      }
+      off += s * P.in_st[d];
+    }
+    out[i] = inside ? x[off] : P.value;
+  }
+}
+
+// ----------------------------------------------------------------- CumSum
+// One thread per line, a sequential running sum in the input's type (numpy
+// cumsum accumulates in order, so fp32 results match bit for bit).
+template <typename T>
+__global__ void cumsum_kernel(T* __restrict__ out, const T* __restrict__ x, int64_t outer,
+                              int64_t dim, int64_t inner) {
+  const int64_t lines = outer * inner;
+  for (int64_t l = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; l < lines;
+       l += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t o = l / inner, in = l % inner;
+    const T* xs = x + o * dim * inner + in;
+    T* os = out + o * dim * inner + in;
+    T acc = 0;
+    for (int64_t d = 0; d < dim; ++d) {
+      acc = acc + xs[d * inner];
+      os[d * inner] = acc;
+    }
+  }
+}
+
+// -------------------------------------------------------------- ScatterND
+// out[idx[i]] = updates[i] for slices of `inner` elements; the host has
+// already removed duplicate indices (keeping the last, as the reference's
+// sequential loop does), so no two threads write one element.
+__global__ void scatter_kernel(uint8_t* __restrict__ out, const uint8_t* __restrict__ upd,
+                               const int64_t* __restrict__ offsets, int64_t nidx, int64_t inner,
+                               int elem) {
+  const int64_t total = nidx * inner;
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = t / inner, e = t % inner;
+    const int64_t dst = (offsets[i] + e) * elem, src = t * elem;
+    for (int k = 0; k < elem; ++k) out[dst + k] = upd[src + k];
+  }
+}
+
+static unsigned grid1d(int64_t n) {
+  return static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 1 << 16)));
+}
+
+static int f32_contig(const kk_tensor* t, const char* name) {
+  KK_TRY(check_tensor(t, name));
+  if (t->dtype != KK_F32) return set_error(KK_E_ARG, "%s must be fp32", name);
+  if (!is_contiguous(t)) return set_error(KK_E_ARG, "%s must be contiguous", name);
+  return KK_OK;
+}
+
+}  // namespace kk
+
+using namespace kk;
+
+extern "C" {
+
+int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const kk_tensor* zp,
+                               const kk_tensor* x) {
+  KK_TRY(require_ready());
+  KK_TRY(f32_contig(x, "x"));
+  KK_TRY(check_tensor(y, "y"));
+  KK_TRY(check_tensor(scale, "scale"));
+  KK_TRY(check_tensor(zp, "zp"));
+  if (y->dtype != KK_U8 || !is_contiguous(y) || numel(y) != numel(x))
+    return set_error(KK_E_ARG, "kk_dynamic_quantize_linear: y must be contiguous uint8 like x");
+  if (scale->dtype != KK_F32 || numel(scale) != 1 || zp->dtype != KK_U8 || numel(zp) != 1)
+    return set_error(KK_E_ARG, "kk_dynamic_quantize_linear: scale is one fp32, zp one uint8");
+  const int64_t n = numel(x);
+  if (n == 0) return set_error(KK_E_ARG, "kk_dynamic_quantize_linear: empty input");
+  const int nblk = static_cast<int>(std::min<int64_t>(kDqlBlocks, ceil_div(n, 256)));
+  void* part = nullptr;
+  KK_TRY(kk_alloc(sizeof(float2) * nblk, &part));
+  hipLaunchKernelGGL(dql_minmax, dim3(nblk), dim3(256), 0, ctx().stream,
+                     static_cast<const float*>(x->data), n, static_cast<float2*>(part));
+  int rc = check_launch("dql_minmax");
+  if (rc == KK_OK) {
+    const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 256), 2048));
+    hipLaunchKernelGGL(dql_quantize, dim3(g), dim3(256), 0, ctx().stream,
+                       static_cast<const float*>(x->data), n, static_cast<const float2*>(part),
+                       nblk, static_cast<uint8_t*>(y->data), static_cast<float*>(scale->data),
+                       static_cast<uint8_t*>(zp->data));
+    rc = check_launch("dql_quantize");
+  }
+  // Stream order keeps the partials alive until both kernels have read them.
+  kk_free(part);
+  return rc;
+}
+
+int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const kk_tensor* x,
+            const kk_tensor* w, const kk_tensor* r, const kk_tensor* b, const kk_tensor* init_h,
+            const kk_tensor* init_c, const kk_tensor* w_scale, const kk_tensor* w_zp,
+            const kk_tensor* r_scale, const kk_tensor* r_zp, int hidden_size, int bidirectional) {
+  KK_TRY(require_ready());
+  KK_TRY(f32_contig(x, "x"));
+  KK_TRY(f32_contig(ys, "ys"));
+  KK_TRY(check_tensor(w, "w"));
+  KK_TRY(check_tensor(r, "r"));
+  KK_TRY(check_tensor(w_scale, "w_scale"));
+  KK_TRY(check_tensor(r_scale, "r_scale"));
+  const int64_t H = hidden_size, ndir = bidirectional ? 2 : 1;
+  if (x->rank != 3) return set_error(KK_E_ARG, "kk_lstm: x must be [seq, batch, input]");
+  const int64_t seq = x->shape[0], batch = x->shape[1], in = x->shape[2];
+  if (w->dtype != KK_I8 || r->dtype != KK_I8 || !is_contiguous(w) || !is_contiguous(r))
+    return set_error(KK_E_ARG, "kk_lstm: W and R must be contiguous int8");
+  if (w->rank != 3 || w->shape[0] != ndir || w->shape[1] != in || w->shape[2] != 4 * H)
+    return set_error(KK_E_ARG, "kk_lstm: W must be [dir, input, 4H]");
+  if (r->rank != 3 || r->shape[0] != ndir || r->shape[1] != H || r->shape[2] != 4 * H)
+    return set_error(KK_E_ARG, "kk_lstm: R must be [dir, H, 4H]");
+  if (4 * H > 1024) return set_error(KK_E_UNSUPPORTED, "kk_lstm: 4H > 1024");
+  if (numel(ys) != seq * ndir * batch * H) return set_error(KK_E_ARG, "kk_lstm: ys shape");
+  const int64_t nws = numel(w_scale), nrs = numel(r_scale);
+  if ((nws != 1 && nws != ndir) || (nrs != 1 && nrs != ndir))
+    return set_error(KK_E_ARG, "kk_lstm: scales need 1 or dir elements");
+  if (b) {
+    KK_TRY(f32_contig(b, "b"));
+    if (numel(b) != ndir * 8 * H) return set_error(KK_E_ARG, "kk_lstm: B must be [dir, 8H]");
+  }
+  for (const kk_tensor* t : {init_h, init_c, yh, yc})
+    if (t) {
+      KK_TRY(f32_contig(t, "state"));
+      if (numel(t) != ndir * batch * H) return set_error(KK_E_ARG, "kk_lstm: state shape");
+    }
+  // Input projections xw[d] = x @ deq(W[d]) on the MFMA GEMM.
+  void* xw = nullptr;
+  const int64_t xw_n = ndir * seq * batch * 4 * H;
+  KK_TRY(kk_alloc(sizeof(float) * std::max<int64_t>(xw_n, 1), &xw));
+  int rc = KK_OK;
+  for (int64_t d = 0; d < ndir && rc == KK_OK && seq * batch > 0; ++d) {
+    kk_tensor a{}, wd{}, o{}, sc{}, zpt{};
+    a.data = x->data; a.dtype = KK_F32; a.rank = 2;
+    a.shape[0] = seq * batch; a.shape[1] = in; a.strides[0] = in; a.strides[1] = 1;
+    wd.data = static_cast<int8_t*>(w->data) + d * in * 4 * H; wd.dtype = KK_I8; wd.rank = 2;
+    wd.shape[0] = in; wd.shape[1] = 4 * H; wd.strides[0] = 4 * H; wd.strides[1] = 1;
+    o.data = static_cast<float*>(xw) + d * seq * batch * 4 * H; o.dtype = KK_F32; o.rank = 2;
+    o.shape[0] = seq * batch; o.shape[1] = 4 * H; o.strides[0] = 4 * H; o.strides[1] = 1;
+    sc.data = static_cast<char*>(w_scale->data) + (nws > 1 ? d * dtype_size(w_scale->dtype) : 0);
+    sc.dtype = w_scale->dtype; sc.rank = 0;
+    const kk_tensor* zptr = nullptr;
+    if (w_zp) {
+      zpt.data = static_cast<char*>(w_zp->data) + (numel(w_zp) > 1 ? d * dtype_size(w_zp->dtype) : 0);
+      zpt.dtype = w_zp->dtype; zpt.rank = 0;
+      zptr = &zpt;
+    }
+    rc = kk_gemm(&o, &a, &wd, &sc, zptr, 1.0f);
+  }
+  if (rc == KK_OK) {
+    LstmArgs A{};
+    A.xw = static_cast<const float*>(xw);
+    A.bias = b ? static_cast<const float*>(b->data) : nullptr;
+    A.r = static_cast<const int8_t*>(r->data);
+    A.r_scale = r_scale->data; A.r_scale_dt = r_scale->dtype; A.r_scale_n = nrs;
+    if (r_zp) { A.r_zp = r_zp->data; A.r_zp_dt = r_zp->dtype; A.r_zp_n = numel(r_zp); }
+    A.init_h = init_h ? static_cast<const float*>(init_h->data) : nullptr;
+    A.init_c = init_c ? static_cast<const float*>(init_c->data) : nullptr;
+    A.ys = static_cast<float*>(ys->data);
+    A.yh = yh ? static_cast<float*>(yh->data) : nullptr;
+    A.yc = yc ? static_cast<float*>(yc->data) : nullptr;
+    A.seq = seq; A.batch = batch; A.H = H; A.ndir = ndir;
+    const size_t lds = sizeof(float) * 5 * H;
+    hipLaunchKernelGGL(lstm_recurrence, dim3(static_cast<unsigned>(ndir * batch)), dim3(1024), lds,
+                       ctx().stream, A);
+    rc = check_launch("lstm_recurrence");
+  }
+  kk_free(xw);
+  return rc;
+}
+
+int kk_stft(const kk_tensor* out, const kk_tensor* signal, const kk_tensor* window,
+            int64_t frame_step, int64_t frame_length, int onesided) {
+  KK_TRY(require_ready());
+  KK_TRY(f32_contig(signal, "signal"));
+  KK_TRY(f32_contig(out, "out"));
+  KK_TRY(check_tensor(window, "window"));
+  if (!is_float(window->dtype) || numel(window) != frame_length)
+    return set_error(KK_E_ARG, "kk_stft: window must hold frame_length floats");
+  if (frame_step < 1 || frame_length < 1) return set_error(KK_E_ARG, "kk_stft: bad frame sizes");
+  const int64_t batch = signal->shape[0];
+  const int64_t slen = numel(signal) / std::max<int64_t>(batch, 1);
+  const int64_t nframes = slen >= frame_length ? (slen - frame_length) / frame_step + 1 : 0;
+  const int64_t nfreq = onesided ? frame_length / 2 + 1 : frame_length;
+  if (numel(out) != batch * nframes * nfreq * 2)
+    return set_error(KK_E_ARG, "kk_stft: out must be [batch, %lld, %lld, 2]", (long long)nframes,
+                     (long long)nfreq);
+  const int64_t total = batch * nframes * nfreq;
+  if (!total) return KK_OK;
+  hipLaunchKernelGGL(stft_kernel, dim3(grid1d(total)), dim3(256), 0, ctx().stream,
+                     static_cast<float*>(out->data), static_cast<const float*>(signal->data),
+                     window->data, window->dtype, batch, slen, nframes, nfreq, frame_length,
+                     frame_step);
+  return check_launch("stft_kernel");
+}
+
+int kk_resize(const kk_tensor* out, const kk_tensor* x, int mode, double scale) {
+  KK_TRY(require_ready());
+  KK_TRY(f32_contig(x, "x"));
+  KK_TRY(f32_contig(out, "out"));
+  if (mode != 0 && mode != 1) return set_error(KK_E_ARG, "kk_resize: mode 0 or 1");
+  if (x->rank < 1 || out->rank != x->rank) return set_error(KK_E_ARG, "kk_resize: ranks");
+  const int64_t lin = x->shape[x->rank - 1], lout = out->shape[out->rank - 1];
+  if (lout != static_cast<int64_t>(std::floor(lin * scale)))
+    return set_error(KK_E_ARG, "kk_resize: out length must be floor(L * scale)");
+  for (int i = 0; i < x->rank - 1; ++i)
+    if (x->shape[i] != out->shape[i]) return set_error(KK_E_ARG, "kk_resize: leading axes differ");
+  const int64_t rows = lin ? numel(x) / lin : 0;
+  if (!rows || !lout) return KK_OK;
+  hipLaunchKernelGGL(resize_kernel, dim3(grid1d(rows * lout)), dim3(256), 0, ctx().stream,
+                     static_cast<float*>(out->data), static_cast<const float*>(x->data), rows, lin,
+                     lout, scale, mode);
+  return check_launch("resize_kernel");
+}
+
+int kk_pad(const kk_tensor* out, const kk_tensor* x, const int64_t* pads, int mode, float value) {
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(x, "x"));
+  KK_TRY(f32_contig(out, "out"));
+  if (x->dtype != KK_F32) return set_error(KK_E_ARG, "kk_pad: x must be fp32");
+  if (!pads) return set_error(KK_E_ARG, "kk_pad: pads is NULL");
+  if (mode < 0 || mode > 2) return set_error(KK_E_ARG, "kk_pad: mode 0/1/2");
+  PadArgs P{};
+  P.rank = x->rank;
+  P.mode = mode;
+  P.value = value;
+  P.n = 1;
+  for (int d = 0; d < x->rank; ++d) {
+    const int64_t b0 = pads[d], b1 = pads[d + x->rank];
+    if (b0 < 0 || b1 < 0) return set_error(KK_E_UNSUPPORTED, "kk_pad: negative pads");
+    if (mode != 0 && (b0 || b1) && x->shape[d] == 0)
+      return set_error(KK_E_ARG, "kk_pad: cannot reflect or extend an empty axis");
+    P.in_dims[d] = x->shape[d];
+    P.in_st[d] = x->strides[d];
+    P.begin[d] = b0;
+    P.out_dims[d] = x->shape[d] + b0 + b1;
+    if (out->shape[d] != P.out_dims[d]) return set_error(KK_E_ARG, "kk_pad: out shape");
+    P.n *= P.out_dims[d];
+  }
+  if (out->rank != x->rank) return set_error(KK_E_ARG, "kk_pad: out rank");
+  if (!P.n) return KK_OK;
+  hipLaunchKernelGGL(pad_kernel, dim3(grid1d(P.n)), dim3(256), 0, ctx().stream,
+                     static_cast<float*>(out->data), static_cast<const float*>(x->data), P);
+  return check_launch("pad_kernel");
+}
+
+int kk_cumsum(const kk_tensor* out, const kk_tensor* x, int axis) {
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(x, "x"));
+  KK_TRY(check_tensor(out, "out"));
+  if (!is_contiguous(x) || !is_contiguous(out) || x->dtype != out->dtype || numel(x) != numel(out))
+    return set_error(KK_E_ARG, "kk_cumsum: contiguous x and out of one dtype and size");
+  if (x->rank == 0) return set_error(KK_E_ARG, "kk_cumsum: scalar input");
+  if (axis < 0) axis += x->rank;
+  if (axis < 0 || axis >= x->rank) return set_error(KK_E_ARG, "kk_cumsum: axis");
+  int64_t outer = 1, inner = 1;
+  for (int i = 0; i < axis; ++i) outer *= x->shape[i];
+  for (int i = axis + 1; i < x->rank; ++i) inner *= x->shape[i];
+  const int64_t dim = x->shape[axis];
+  if (!numel(x)) return KK_OK;
+  const dim3 g(grid1d(outer * inner));
+  switch (x->dtype) {
+    case KK_F32:
+      hipLaunchKernelGGL(cumsum_kernel<float>, g, dim3(256), 0, ctx().stream,
+                         static_cast<float*>(out->data), static_cast<const float*>(x->data), outer,
+                         dim, inner);
+      break;
+    case KK_I64:
+      hipLaunchKernelGGL(cumsum_kernel<int64_t>, g, dim3(256), 0, ctx().stream,
+                         static_cast<int64_t*>(out->data), static_cast<const int64_t*>(x->data),
+                         outer, dim, inner);
+      break;
+    case KK_I32:
+      hipLaunchKernelGGL(cumsum_kernel<int32_t>, g, dim3(256), 0, ctx().stream,
+                         static_cast<int32_t*>(out->data), static_cast<const int32_t*>(x->data),
+                         outer, dim, inner);
+      break;
+    default:
+      return set_error(KK_E_UNSUPPORTED, "kk_cumsum: dtype %d", x->dtype);
+  }
+  return check_launch("cumsum_kernel");
+}
+
+int kk_scatter_nd(const kk_tensor* out, const kk_tensor* updates, const int64_t* offsets,
+                  int64_t nidx, int64_t inner) {
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(out, "out"));
+  KK_TRY(check_tensor(updates, "updates"));
+  if (!is_contiguous(out) || !is_contiguous(updates) || updates->dtype != out->dtype)
+    return set_error(KK_E_ARG, "kk_scatter_nd: contiguous out and updates of one dtype");
+  if (nidx < 0 || inner < 0 || (nidx && !offsets))
+    return set_error(KK_E_ARG, "kk_scatter_nd: bad offsets");
+  if (numel(updates) != nidx * inner) return set_error(KK_E_ARG, "kk_scatter_nd: updates size");
+  const int64_t n = numel(out);
+  for (int64_t i = 0; i < nidx; ++i)
+    if (offsets[i] < 0 || offsets[i] + inner > n)
+      return set_error(KK_E_ARG, "kk_scatter_nd: offset %lld out of range", (long long)offsets[i]);
+  if (!nidx || !inner) return KK_OK;
+  void* dev = nullptr;
+  KK_TRY(kk_alloc(sizeof(int64_t) * nidx, &dev));
+  int rc = kk_upload(dev, offsets, sizeof(int64_t) * nidx);
+  if (rc == KK_OK) {
+    hipLaunchKernelGGL(scatter_kernel, dim3(grid1d(nidx * inner)), dim3(256), 0, ctx().stream,
+                       static_cast<uint8_t*>(out->data), static_cast<const uint8_t*>(updates->data),
+                       static_cast<const int64_t*>(dev), nidx, inner, dtype_size(out->dtype));
+    rc = check_launch("scatter_kernel");
+  }
+  kk_free(dev);
+  return rc;
+}
+
+}  // extern "C"

@@ -141,6 +141,7 @@ int make_dequant(Dequant* d, const kk_tensor* w, const kk_tensor* scale,
 __device__ __forceinline__ float dequant_value(float q, const Dequant& d,
                                                int64_t col) {
   float z = d.zp ? load_as_f32(d.zp, d.zp_dt, col * d.zp_stride) : 0.0f;
+  if (!d.scale) return q - z;  // integer ops: zero-point shift only
   float s = load_as_f32(d.scale, d.scale_dt, col * d.scale_stride);
   return (q - z) * s;
 }

@@ -29,13 +29,16 @@ ONNX_DTYPE = {
     12: np.uint32, 13: np.uint64,
 }
 
-# Ops whose integer/bool host inputs are shape-domain data computed on the
-# host (cpu_ops.gd:66-140 lists the same family).
-_HOST_OPS = {
+# Shape-domain nodes stay on the host when all their inputs are host values
+# (cpu_ops.gd:66-140 lists the same family): pure data movement for any
+# dtype, arithmetic and comparisons only on integer/bool data.
+_HOST_MOVE_OPS = {
     "Shape", "Reshape", "Unsqueeze", "Squeeze", "Concat", "Slice", "Gather",
-    "Cast", "Equal", "Where", "Range", "Greater", "Less", "GreaterOrEqual",
-    "And", "Add", "Sub", "Mul", "Div", "Transpose", "NonZero", "Expand",
-    "ConstantOfShape", "Split", "CumSum",
+    "Cast", "Transpose", "Expand", "Split",
+}
+_HOST_INT_OPS = {
+    "Equal", "Where", "Greater", "Less", "GreaterOrEqual", "And", "Add", "Sub", "Mul",
+    "Div", "CumSum",
 }
 
 
@@ -62,9 +65,10 @@ def _f32(t):
 
 
 def to_host(v):
-    """Host array of a value (a device value is downloaded: a sync point)."""
+    """Host array of a value.  A device value is downloaded (a sync point)
+    unless it is a constant whose host copy was kept at upload."""
     if _is_dev(v):
-        return v.numpy()
+        return v.host if v.host is not None else v.numpy()
     return v
 
 
@@ -97,10 +101,21 @@ def dispatch(op, node_input, node_output, at, env):
     y = inp(1)
 
     # ---------------------------------------------------- host shape domain
-    if op in _HOST_OPS:
-        vals = [inp(i) for i in range(len(node_input))]
-        present = [v for v in vals if v is not None]
-        if present and all(_host_int(v) for v in present) and op != "Shape":
+    if op in ("Range", "NonZero"):
+        # Shape-domain results the host needs (frame counts, alignment
+        # indices): device inputs are downloaded here -- the data-dependent
+        # sync points of the GPU executor (executor.gd:474-491, 543-563).
+        from . import hostops
+        local = {n: to_host(env[n]) for n in node_input if n}
+        hostops.run(op, node_input, node_output, at, local)
+        env[node_output[0]] = local[node_output[0]]
+        return
+    if op in _HOST_MOVE_OPS or op in _HOST_INT_OPS:
+        present = [inp(i) for i in range(len(node_input)) if inp(i) is not None]
+        host = bool(present) and all(not _is_dev(v) for v in present)
+        if host and op in _HOST_INT_OPS:
+            host = all(_host_int(v) for v in present)
+        if host and op != "Shape":
             from . import hostops
             hostops.run(op, node_input, node_output, at, env)
             return
@@ -110,7 +125,7 @@ def dispatch(op, node_input, node_output, at, env):
     if op in ("Add", "Sub", "Mul", "Div", "Pow"):
         out = ops.binary(op, to_device(x), to_device(y))
     elif op in ("Sqrt", "Exp", "Sin", "Cos", "Atan", "Tanh", "Sigmoid", "Floor", "Round", "Erf"):
-        out = ops.unary(op, to_device(x))
+        out = ops.unary(op, _f32(to_device(x)))
     elif op == "LeakyRelu":
         out = ops.unary(op, to_device(x), np.float32(at.get("alpha", 0.01)))
     elif op == "Clip":
@@ -206,8 +221,11 @@ def dispatch(op, node_input, node_output, at, env):
         v = at.get("value", np.array([0], dtype=np.float32))
         v = np.asarray(v)
         dt = np.float32 if v.dtype == np.float16 else v.dtype
-        shape = [int(s) for s in to_host(x)]
-        out = ops.fill(shape, v.reshape(-1)[0], dt)
+        shape = [int(s) for s in np.asarray(to_host(x)).reshape(-1)]
+        if np.dtype(dt).kind == "f":
+            out = ops.fill(shape, v.reshape(-1)[0], dt)
+        else:  # integer fills are shape-domain data: host
+            out = np.full(shape, v.reshape(-1)[0], dtype=dt)
     elif op == "Cast":
         to = ONNX_DTYPE[at["to"]]
         dt = np.float32 if to == np.float16 else to
@@ -263,6 +281,54 @@ def dispatch(op, node_input, node_output, at, env):
                                    at.get("pads", [0, 0]), at.get("strides", [1])[0],
                                    at.get("dilations", [1])[0], at.get("group", 1),
                                    at.get("output_padding", [0])[0])
+
+    elif op == "CumSum":
+        out = ops.cumsum(_f32(to_device(x)), int(np.asarray(to_host(y)).item()))
+    elif op == "Pad":
+        pads = np.asarray(to_host(inp(1))).reshape(-1)
+        value = 0.0 if inp(2) is None else float(np.asarray(to_host(inp(2))).item())
+        out = ops.pad(_f32(to_device(x)), pads, at.get("mode", "constant"), value)
+    elif op == "Resize":
+        scales = inp(2) if inp(2) is not None else inp(3)
+        mode = at.get("mode", "nearest")
+        ctm = at.get("coordinate_transformation_mode", "half_pixel")
+        nearest = at.get("nearest_mode", "round_prefer_floor")
+        if mode == "nearest" and (ctm != "asymmetric" or nearest != "floor"):
+            raise NotImplementedError(f"resize nearest {ctm}/{nearest}")
+        if mode == "linear" and ctm != "half_pixel":
+            raise NotImplementedError(f"resize linear {ctm}")
+        if mode not in ("nearest", "linear"):
+            raise NotImplementedError(f"resize mode {mode}")
+        scale = float(np.asarray(to_host(scales)).reshape(-1)[-1])
+        out = ops.resize(_f32(to_device(x)), scale, mode)
+    elif op == "ScatterND":
+        out = ops.scatter_nd(_f32(to_device(x)), to_host(y), _f32(to_device(inp(2))))
+    elif op == "STFT":
+        out = ops.stft(_f32(to_device(x)), _f32(to_device(inp(2))),
+                       int(np.asarray(to_host(y)).item()),
+                       int(np.asarray(to_host(inp(3))).item()), at.get("onesided", 1))
+    elif op == "DynamicQuantizeLinear":
+        for name, v in zip(node_output, ops.dynamic_quantize_linear(_f32(to_device(x)))):
+            if name:
+                env[name] = v
+        return
+    elif op == "MatMulInteger":
+        out = ops.matmul_integer(to_device(x), to_device(y), to_device(inp(2)),
+                                 to_device(inp(3)))
+    elif op == "ConvInteger":
+        out = ops.conv_integer(to_device(x), to_device(y), to_device(inp(2)), to_device(inp(3)),
+                               at.get("pads", [0, 0]), at.get("strides", [1])[0],
+                               at.get("dilations", [1])[0], at.get("group", 1))
+    elif op == "DynamicQuantizeLSTM":
+        res = ops.lstm(_f32(to_device(x)), to_device(y), to_device(inp(2)),
+                       _f32(to_device(inp(3))), _f32(to_device(inp(5))),
+                       _f32(to_device(inp(6))), _f32(to_device(inp(8))), to_device(inp(9)),
+                       _f32(to_device(inp(10))), to_device(inp(11)), int(at["hidden_size"]),
+                       at.get("direction") == "bidirectional")
+        for name, v in zip(node_output, res):
+            if name:
+                env[name] = v
+        return
 
     # -------------------------------------- fused composites (libkk only)
     elif op == "Snake":

@@ -4,6 +4,8 @@ Each function takes DeviceTensors (or None for optional operands) and
 returns a new DeviceTensor.  Shapes are computed here with numpy's rules;
 the kernels re-validate them before launching.
 """
+import ctypes
+
 import numpy as np
 
 from . import _lib
@@ -12,10 +14,6 @@ from .tensor import DeviceTensor
 
 def _d(t):
     return None if t is None else t.desc()
-
-
-def _float_out(*ts):
-    return np.float32
 
 
 def broadcast_shape(*shapes):
@@ -201,4 +199,123 @@ def conv_transpose1d(x, w, bias=None, pads=(0, 0), stride=1, dilation=1, group=1
     _lib.call("kk_conv_transpose1d", out.desc(), x.desc(), w.contiguous().desc(), _d(w_scale),
               _d(w_zp), _d(bias), int(stride), int(dilation), int(pads[0]), int(pads[1]),
               int(group), int(output_padding))
+    return out
+
+
+# ------------------------------------------------- quantized integer path
+def dynamic_quantize_linear(x):
+    """(y uint8, scale fp32 scalar, zero point uint8 scalar), all on device."""
+    x = x.contiguous()
+    y = DeviceTensor.empty(x.shape, np.uint8)
+    scale = DeviceTensor.empty((), np.float32)
+    zp = DeviceTensor.empty((), np.uint8)
+    _lib.call("kk_dynamic_quantize_linear", y.desc(), scale.desc(), zp.desc(), x.desc())
+    return y, scale, zp
+
+
+def matmul_integer(a, b, a_zp=None, b_zp=None):
+    batch = broadcast_shape(a.shape[:-2], b.shape[:-2])
+    out = DeviceTensor.empty(batch + (a.shape[-2], b.shape[-1]), np.int32)
+    _lib.call("kk_matmul_integer", out.desc(), a.desc(), b.desc(), _d(a_zp), _d(b_zp))
+    return out
+
+
+def conv_integer(x, w, x_zp=None, w_zp=None, pads=(0, 0), stride=1, dilation=1, group=1):
+    x = x.contiguous()
+    w = w.contiguous()
+    n, _, L = x.shape
+    cout, _, k = w.shape
+    lout = (L + pads[0] + pads[1] - dilation * (k - 1) - 1) // stride + 1
+    out = DeviceTensor.empty((n, cout, max(lout, 0)), np.int32)
+    _lib.call("kk_conv_integer", out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
+              int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
+    return out
+
+
+# ------------------------------------------------ recurrent / vocoder
+def lstm(x, w, r, b, init_h, init_c, w_scale, w_zp, r_scale, r_zp, hidden_size, bidirectional):
+    x = x.contiguous()
+    seq, batch, _ = x.shape
+    ndir = 2 if bidirectional else 1
+    ys = DeviceTensor.empty((seq, ndir, batch, hidden_size), np.float32)
+    yh = DeviceTensor.empty((ndir, batch, hidden_size), np.float32)
+    yc = DeviceTensor.empty((ndir, batch, hidden_size), np.float32)
+    c = lambda t: None if t is None else t.contiguous()  # noqa: E731
+    _lib.call("kk_lstm", ys.desc(), yh.desc(), yc.desc(), x.desc(), c(w).desc(), c(r).desc(),
+              _d(c(b)), _d(c(init_h)), _d(c(init_c)), c(w_scale).desc(), _d(c(w_zp)),
+              c(r_scale).desc(), _d(c(r_zp)), int(hidden_size), 1 if bidirectional else 0)
+    return ys, yh, yc
+
+
+def stft(signal, window, frame_step, frame_length, onesided=1):
+    signal = signal.contiguous()
+    batch = signal.shape[0]
+    slen = signal.size // max(batch, 1)
+    n, step = int(frame_length), int(frame_step)
+    nframes = (slen - n) // step + 1 if slen >= n else 0
+    nfreq = n // 2 + 1 if onesided else n
+    out = DeviceTensor.empty((batch, nframes, nfreq, 2), np.float32)
+    _lib.call("kk_stft", out.desc(), signal.desc(), window.contiguous().desc(), step, n,
+              1 if onesided else 0)
+    return out
+
+
+def resize(x, scale, mode):
+    """mode 'nearest' (asymmetric/floor) or 'linear' (half_pixel), last axis."""
+    x = x.contiguous()
+    lout = int(np.floor(x.shape[-1] * scale))
+    out = DeviceTensor.empty(x.shape[:-1] + (lout,), np.float32)
+    _lib.call("kk_resize", out.desc(), x.desc(), 0 if mode == "nearest" else 1, float(scale))
+    return out
+
+
+def pad(x, pads, mode="constant", value=0.0):
+    r = x.ndim
+    pads = np.ascontiguousarray(np.asarray(pads, dtype=np.int64).reshape(-1))
+    shape = [x.shape[i] + int(pads[i]) + int(pads[i + r]) for i in range(r)]
+    out = DeviceTensor.empty(shape, np.float32)
+    m = {"constant": 0, "reflect": 1, "edge": 2}[mode]
+    _lib.call("kk_pad", out.desc(), x.desc(), pads.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)), m, float(value))
+    return out
+
+
+def cumsum(x, axis):
+    x = x.contiguous()
+    out = DeviceTensor.empty(x.shape, x.dtype)
+    _lib.call("kk_cumsum", out.desc(), x.desc(), int(axis))
+    return out
+
+
+def scatter_nd(data, indices, updates):
+    """indices: host int64 [..., k]; later duplicates win (the host keeps the
+    last occurrence of each index, so the device writes never collide)."""
+    out = data.astype(data.dtype)  # a fresh copy, as numpy's data.copy()
+    idx = np.asarray(indices).astype(np.int64)
+    k = idx.shape[-1]
+    flat = idx.reshape(-1, k)
+    inner = int(np.prod(out.shape[k:], dtype=np.int64)) if k < out.ndim else 1
+    for a in range(k):
+        dim = out.shape[a]
+        if flat.size and (flat[:, a].min() < -dim or flat[:, a].max() >= dim):
+            raise IndexError(f"ScatterND index out of bounds for axis {a} with size {dim}")
+    flat = np.where(flat < 0, flat + np.array(out.shape[:k]), flat)
+    strides = np.array([int(np.prod(out.shape[a + 1:], dtype=np.int64)) for a in range(k)],
+                       dtype=np.int64)
+    offsets = flat @ strides if flat.size else np.zeros(0, np.int64)
+    upd = updates.contiguous()
+    if upd.size != len(offsets) * inner:
+        raise ValueError("ScatterND: updates do not match indices")
+    # keep the last occurrence of each offset
+    _, last = np.unique(offsets[::-1], return_index=True)
+    keep = np.sort(len(offsets) - 1 - last)
+    if len(keep) != len(offsets):
+        upd = upd.reshape((len(offsets), inner))
+        sel = DeviceTensor.empty((len(keep), inner), upd.dtype)
+        for j, i in enumerate(keep):
+            copy_into(sel.slice_axis(0, j, j + 1), upd.slice_axis(0, int(i), int(i) + 1))
+        upd, offsets = sel, offsets[keep]
+    offsets = np.ascontiguousarray(offsets, dtype=np.int64)
+    _lib.call("kk_scatter_nd", out.desc(), upd.desc(),
+              offsets.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
+              int(len(offsets)), int(inner))
     return out

@@ -87,7 +87,7 @@ def _contig_strides(shape):
 class DeviceTensor:
     """A strided view of device memory (element strides, numpy semantics)."""
 
-    __slots__ = ("storage", "offset", "shape", "strides", "dtype", "_desc")
+    __slots__ = ("storage", "offset", "shape", "strides", "dtype", "_desc", "host")
 
     def __init__(self, storage, shape, dtype, strides=None, offset=0):
         self.storage = storage
@@ -98,6 +98,7 @@ class DeviceTensor:
         self.strides = tuple(int(s) for s in strides) if strides is not None \
             else _contig_strides(self.shape)
         self.offset = int(offset)
+        self.host = None  # cached host value of a constant uploaded once
         if len(self.shape) > _lib.KK_MAX_RANK:
             raise ValueError(f"rank {len(self.shape)} exceeds {_lib.KK_MAX_RANK}")
         self._desc = None

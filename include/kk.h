@@ -197,6 +197,58 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x,
                         int stride, int dilation, int pad0, int pad1,
                         int group, int output_padding);
 
+/* --------------------------------------------- quantized integer path
+ * DynamicQuantizeLinear (ref_runtime.py:106-116): y = clip(rint(x / scale)
+ * + zp, 0, 255) with the range widened to include 0, scale = range / 255 and
+ * zp = clip(rint(-min / scale)) derived in double; y uint8 like x, scale one
+ * fp32, zp one uint8 (all on the device). */
+int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale,
+                               const kk_tensor* zp, const kk_tensor* x);
+/* MatMulInteger (ref_runtime.py:119-127): int32 (a - a_zp) @ (b - b_zp),
+ * a uint8/int8 [.., M, K], b int8/uint8 [.., K, N], a_zp per tensor, b_zp
+ * per tensor or per column (either may be NULL). */
+int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
+                      const kk_tensor* a_zp, const kk_tensor* b_zp);
+/* ConvInteger (ref_runtime.py:130-134): int32 conv of (x - x_zp) with
+ * (w - w_zp); x uint8 [N, Cin, L], w uint8/int8 [Cout, Cin, K]; padding
+ * reads 0 after the zero-point shift. */
+int kk_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                    const kk_tensor* x_zp, const kk_tensor* w_zp, int stride,
+                    int dilation, int pad0, int pad1, int group);
+
+/* ------------------------------------------------ recurrent / vocoder
+ * DynamicQuantizeLSTM as op_lstm computes it without activation
+ * quantisation (ref_runtime.py:137-210): W int8 [dir, input, 4H] and R int8
+ * [dir, H, 4H] dequantised ((q - zp) * scale, per direction), gate order
+ * i, o, f, c, the reverse direction walking time backwards.  ys [seq, dir,
+ * batch, H]; yh/yc [dir, batch, H] may be NULL; b [dir, 8H], init_h/init_c
+ * [dir, batch, H] and w_zp/r_zp may be NULL.  4H <= 1024. */
+int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc,
+            const kk_tensor* x, const kk_tensor* w, const kk_tensor* r,
+            const kk_tensor* b, const kk_tensor* init_h, const kk_tensor* init_c,
+            const kk_tensor* w_scale, const kk_tensor* w_zp, const kk_tensor* r_scale,
+            const kk_tensor* r_zp, int hidden_size, int bidirectional);
+/* STFT (op_stft, ref_runtime.py:213-233): direct DFT of windowed frames,
+ * out [batch, frames, bins, 2]. */
+int kk_stft(const kk_tensor* out, const kk_tensor* signal, const kk_tensor* window,
+            int64_t frame_step, int64_t frame_length, int onesided);
+/* Resize of the last axis (op_resize, ref_runtime.py:236-256): mode 0
+ * nearest (asymmetric, floor), 1 linear (half_pixel); out length
+ * floor(L * scale). */
+int kk_resize(const kk_tensor* out, const kk_tensor* x, int mode, double scale);
+/* Pad (op_pad, ref_runtime.py:259-266): pads = [begin_0.., end_0..] (host
+ * array of 2*rank), mode 0 constant, 1 reflect, 2 edge. */
+int kk_pad(const kk_tensor* out, const kk_tensor* x, const int64_t* pads, int mode,
+           float value);
+/* CumSum along `axis` (ref_runtime.py:565-567), fp32/int32/int64, summed
+ * sequentially as numpy does. */
+int kk_cumsum(const kk_tensor* out, const kk_tensor* x, int axis);
+/* ScatterND (op_scatternd, ref_runtime.py:296-304) after the copy of data
+ * into out: out[offsets[i] .. + inner] = updates[i]; offsets are host
+ * element offsets, distinct and checked against out. */
+int kk_scatter_nd(const kk_tensor* out, const kk_tensor* updates, const int64_t* offsets,
+                  int64_t nidx, int64_t inner);
+
 /* -------------------------------------------------------------- timing
  * HIP events on the library stream, for measuring kernels where they run.
  * Slots 0..KK_MAX_EVENTS-1.  No counterpart in the reference, which has no

@@ -271,6 +271,163 @@ def conv_transpose1d(x, w, b=None, pads=(0, 0), stride=1, dilation=1, group=1,
     return out
 
 
+# ------------------------------------------------- quantized integer path
+def dynamic_quantize_linear(x):
+    """DynamicQuantizeLinear (ref_runtime.py:106-116): uint8 asymmetric
+    quantisation with the range widened to include 0; scale and zero point
+    in float64, x / scale in float32 (a Python float is a weak scalar), the
+    float64 zero point added after rounding."""
+    x = f32(x).astype(F32)
+    lo = min(0.0, float(x.min())) if x.size else 0.0
+    hi = max(0.0, float(x.max())) if x.size else 0.0
+    scale = (hi - lo) / 255.0
+    if scale == 0:
+        scale = 1.0
+    zp = np.clip(np.rint(0.0 - lo / scale), 0.0, 255.0)
+    y = np.clip(np.rint(x / scale) + zp, 0.0, 255.0).astype(np.uint8)
+    return y, F32(scale), np.uint8(zp)
+
+
+def matmul_integer(a, b, a_zp=None, b_zp=None):
+    """MatMulInteger (ref_runtime.py:119-127): exact int32 (a - a_zp) @ (b - b_zp)
+    with a per-tensor a_zp and a per-tensor or per-column b_zp."""
+    ai = np.asarray(a).astype(np.int64)
+    bi = np.asarray(b).astype(np.int64)
+    if a_zp is not None:
+        ai = ai - np.asarray(a_zp).astype(np.int64)
+    if b_zp is not None:
+        z = np.asarray(b_zp).astype(np.int64)
+        bi = bi - (z if z.ndim == 0 else z.reshape(1, -1))
+    return (ai @ bi).astype(np.int32)
+
+
+def conv_integer(x, w, x_zp=None, w_zp=None, pads=(0, 0), stride=1, dilation=1, group=1):
+    """ConvInteger (ref_runtime.py:130-134): the zero-point-shifted integers
+    convolved in float32 by op_conv1d, then rounded to int32 (exact while
+    partial sums stay below 2**24)."""
+    xi = np.asarray(x).astype(np.int32) - (0 if x_zp is None else np.int32(x_zp))
+    wi = np.asarray(w).astype(np.int32) - (0 if w_zp is None else np.int32(w_zp))
+    out = conv1d(xi.astype(F32), wi.astype(F32), None, pads, stride, dilation, group)
+    return out.round().astype(np.int32)
+
+
+# ------------------------------------------------------------------- LSTM
+def lstm(x, w, r, b, init_h, init_c, w_scale, w_zp, r_scale, r_zp, hidden_size,
+         bidirectional):
+    """DynamicQuantizeLSTM as the shipped runtime computes it (op_lstm with
+    quantize_activations=False, ref_runtime.py:137-210): int8 W [dir, in, 4H]
+    and R [dir, H, 4H] dequantised to fp32, the input projection x @ W for all
+    steps, then per step g = xw[t] + h @ R with ONNX gate order i, o, f, c;
+    the reverse direction walks time backwards."""
+    x = f32(x).astype(F32)
+    seq, batch, _ = x.shape
+    ndir = 2 if bidirectional else 1
+    hs = int(hidden_size)
+
+    def deq(q, scale, zp):
+        q = np.asarray(q).astype(F32)
+        if zp is not None:
+            q = q - np.asarray(zp).astype(F32)
+        return q * np.asarray(scale, dtype=F32)
+
+    ys = np.zeros((seq, ndir, batch, hs), F32)
+    y_h = np.zeros((ndir, batch, hs), F32)
+    y_c = np.zeros((ndir, batch, hs), F32)
+    ws = np.asarray(w_scale).reshape(-1)
+    rs = np.asarray(r_scale).reshape(-1)
+    for d in range(ndir):
+        wz = None if w_zp is None else np.asarray(w_zp).reshape(-1)[d]
+        rz = None if r_zp is None else np.asarray(r_zp).reshape(-1)[d]
+        wd = deq(w[d], ws[d] if ws.size == ndir else ws, wz)
+        rd = deq(r[d], rs[d] if rs.size == ndir else rs, rz)
+        bd = np.zeros(8 * hs, F32) if b is None else f32(b)[d].astype(F32)
+        h = np.zeros((batch, hs), F32) if init_h is None else f32(init_h)[d].astype(F32).copy()
+        c = np.zeros((batch, hs), F32) if init_c is None else f32(init_c)[d].astype(F32).copy()
+        xw = (x.reshape(seq * batch, -1) @ wd).reshape(seq, batch, 4 * hs) + (bd[:4 * hs] + bd[4 * hs:])
+        for t in (range(seq) if d == 0 else range(seq - 1, -1, -1)):
+            g = xw[t] + h @ rd
+            i = 1.0 / (1.0 + np.exp(-g[:, 0:hs]))
+            o = 1.0 / (1.0 + np.exp(-g[:, hs:2 * hs]))
+            fg = 1.0 / (1.0 + np.exp(-g[:, 2 * hs:3 * hs]))
+            cc = np.tanh(g[:, 3 * hs:4 * hs])
+            c = fg * c + i * cc
+            h = o * np.tanh(c)
+            ys[t, d] = h
+        y_h[d], y_c[d] = h, c
+    return ys, y_h, y_c
+
+
+# --------------------------------------------------- vocoder tail / misc
+def stft(signal, frame_step, window, frame_length, onesided=1):
+    """op_stft (ref_runtime.py:213-233): direct DFT of windowed frames with a
+    float64 cos/sin basis; the products are float64 and stored as float32."""
+    sig = f32(signal).astype(F32)
+    if sig.ndim == 3 and sig.shape[-1] == 1:
+        sig = sig[:, :, 0]
+    win = f32(window).astype(F32)
+    n, step = int(frame_length), int(frame_step)
+    batch, slen = sig.shape
+    nframes = (slen - n) // step + 1
+    nfreq = n // 2 + 1 if onesided else n
+    ang = -2.0 * np.pi * np.arange(nfreq)[:, None] * np.arange(n)[None, :] / n
+    cos_b, sin_b = np.cos(ang), np.sin(ang)
+    out = np.empty((batch, nframes, nfreq, 2), F32)
+    idx = np.arange(nframes)[:, None] * step + np.arange(n)[None, :]
+    for bi in range(batch):
+        frames = sig[bi][idx] * win
+        out[bi, :, :, 0] = frames @ cos_b.T
+        out[bi, :, :, 1] = frames @ sin_b.T
+    return out
+
+
+def resize(x, scales, mode, ctm, nearest_mode):
+    """op_resize (ref_runtime.py:236-256): 1-D resize of the last axis,
+    nearest (asymmetric, floor) or linear (half_pixel) with float64 source
+    positions and a float32 blend."""
+    x = f32(x).astype(F32)
+    scale = float(np.asarray(scales).reshape(-1)[-1])
+    lin = x.shape[-1]
+    lout = int(np.floor(lin * scale))
+    if mode == "nearest":
+        if ctm != "asymmetric" or nearest_mode != "floor":
+            raise NotImplementedError(f"resize nearest {ctm}/{nearest_mode}")
+        src = np.floor(np.arange(lout) / scale).astype(np.int64)
+        return x[..., np.clip(src, 0, lin - 1)]
+    if mode == "linear":
+        if ctm != "half_pixel":
+            raise NotImplementedError(f"resize linear {ctm}")
+        pos = np.clip((np.arange(lout) + 0.5) / scale - 0.5, 0, lin - 1)
+        i0 = np.floor(pos).astype(np.int64)
+        i1 = np.clip(i0 + 1, 0, lin - 1)
+        frac = (pos - i0).astype(F32)
+        return x[..., i0] * (1.0 - frac) + x[..., i1] * frac
+    raise NotImplementedError(f"resize mode {mode}")
+
+
+def pad(x, pads, mode="constant", value=0.0):
+    """op_pad (ref_runtime.py:259-266): numpy pad, ONNX pads layout
+    [begin_0 .. begin_r-1, end_0 .. end_r-1]."""
+    r = x.ndim
+    widths = [(int(pads[i]), int(pads[i + r])) for i in range(r)]
+    if mode == "reflect":
+        return np.pad(x, widths, mode="reflect")
+    if mode == "edge":
+        return np.pad(x, widths, mode="edge")
+    return np.pad(x, widths, mode="constant", constant_values=value)
+
+
+def scatter_nd(data, indices, updates):
+    """op_scatternd (ref_runtime.py:296-304): later duplicates win."""
+    out = np.array(data, copy=True)
+    idx = np.asarray(indices).astype(np.int64)
+    k = idx.shape[-1]
+    flat = idx.reshape(-1, k)
+    upd = np.asarray(updates).reshape((flat.shape[0],) + out.shape[k:])
+    for i in range(flat.shape[0]):
+        out[tuple(flat[i])] = upd[i]
+    return out
+
+
 # ------------------------------------------------------------------ pool
 def bucket(nbytes):
     """Pool bucket size: 256-byte floor, four significant bits above 4 KiB
@@ -399,6 +556,49 @@ def dispatch(op, node_input, node_output, at, env):
         out = snake(x, y, inp(2))
     elif op == "AdaIN":
         out = adain(x, y, inp(2), inp(3), at.get("epsilon", 1e-5))
+    # ---- the rest of the graph's branches (ref_runtime.py:446-664)
+    elif op == "Erf":
+        from scipy.special import erf
+        out = erf(f32(x))
+    elif op == "Shape":
+        s = np.array(x.shape, dtype=np.int64)
+        out = s[at.get("start", 0):at.get("end", len(s))]
+    elif op == "Range":
+        out = np.arange(x.item(), y.item(), inp(2).item(), dtype=x.dtype)
+    elif op == "NonZero":
+        out = np.array(np.nonzero(x), dtype=np.int64)
+    elif op == "CumSum":
+        out = np.cumsum(f32(x), axis=int(np.asarray(y).item()))
+    elif op == "Pad":
+        out = pad(f32(x), np.asarray(inp(1)).reshape(-1), at.get("mode", "constant"),
+                  0.0 if inp(2) is None else float(inp(2)))
+    elif op == "ScatterND":
+        out = scatter_nd(f32(x), y, f32(inp(2)))
+    elif op == "Resize":
+        out = resize(x, inp(2) if inp(2) is not None else inp(3), at.get("mode", "nearest"),
+                     at.get("coordinate_transformation_mode", "half_pixel"),
+                     at.get("nearest_mode", "round_prefer_floor"))
+    elif op == "STFT":
+        out = stft(x, np.asarray(y).item(), inp(2), np.asarray(inp(3)).item(),
+                   at.get("onesided", 1))
+    elif op == "DynamicQuantizeLinear":
+        for name, v in zip(node_output, dynamic_quantize_linear(x)):
+            if name:
+                env[name] = v
+        return
+    elif op == "MatMulInteger":
+        out = matmul_integer(x, y, inp(2), inp(3))
+    elif op == "ConvInteger":
+        out = conv_integer(x, y, inp(2), inp(3), at.get("pads", [0, 0]),
+                           at.get("strides", [1])[0], at.get("dilations", [1])[0],
+                           at.get("group", 1))
+    elif op == "DynamicQuantizeLSTM":
+        res = lstm(x, y, inp(2), inp(3), inp(5), inp(6), inp(8), inp(9), inp(10), inp(11),
+                   at["hidden_size"], at.get("direction") == "bidirectional")
+        for name, v in zip(node_output, res):
+            if name:
+                env[name] = v
+        return
     else:
         raise NotImplementedError(op)
     env[node_output[0]] = out

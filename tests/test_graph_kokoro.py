@@ -1,0 +1,148 @@
+"""The full Kokoro-82M-architecture graph (the reference's packed graph
+structure with seeded random learned weights) run node by node through the
+drop-in dispatch on the GPU, against checkpoints the CPU oracle computed for
+the same weights and inputs (tests/golden/graph_golden_t8.npz, written by
+tests/golden/make_graph_golden.py).
+
+Bars: the integer durations bit-exact (they set the output length), the
+pre-round durations and the text LSTM within rel 1e-4; the STFT of the
+harmonic source and the waveform within the reference's own GPU-vs-numpy tap
+gate -- relative RMS 0.05 (tests/test_taps.gd:19-26) -- after ~3900 chained
+fp32 nodes, with non-finite values counted explicitly."""
+import importlib
+import os
+
+import numpy as np
+import pytest
+
+from conftest import assert_close
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def rel_rms(got, want):
+    got = np.asarray(got, np.float64).reshape(-1)
+    want = np.asarray(want, np.float64).reshape(-1)
+    assert got.shape == want.shape
+    assert int((~np.isfinite(got)).sum()) == int((~np.isfinite(want)).sum())
+    return float(np.sqrt(((got - want) ** 2).mean()) / max(np.sqrt((want ** 2).mean()), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def run8(gpu):
+    kkg = importlib.import_module("best-tts-godot_amd.graph")
+    gold = np.load(os.path.join(HERE, "golden", "graph_golden_t8.npz"))
+    g = kkg.load_graph(kkg.default_graph_path())
+    pg = kkg.PackedGraph(g, kkg.synth_weights(g, 0))
+    wav = pg.run(gold["ids"], gold["style"], 1.0, keep=[2430, 2432, 1165, 3037])
+    caps = {k: gpu.to_host(v) for k, v in pg.last_env.items()}
+    return gold, wav, caps, pg
+
+
+def test_durations_exact(run8):
+    gold, wav, caps, _ = run8
+    assert_close(caps["2430"], gold["t2430"], 1e-4, 1e-5, what="pre-round durations")
+    np.testing.assert_array_equal(np.asarray(caps["2432"]), gold["t2432"])
+    assert wav.size == int(gold["wave_len"])
+
+
+def test_text_lstm(run8):
+    gold, _, caps, _ = run8
+    assert_close(caps["1165"], gold["t1165"], 1e-4, floor_rel=1e-5, what="text LSTM")
+
+
+def test_harmonic_stft_and_waveform(run8):
+    """The STFT of the harmonic source within the reference's tap gate; the
+    free-running waveform only for its length, finiteness and level (its
+    samples are compared node by node in the teacher-forced test)."""
+    gold, wav, caps, _ = run8
+    assert rel_rms(caps["3037"], gold["t3037"]) < 0.05
+    wav = wav.reshape(-1).astype(np.float64)
+    assert wav.size == int(gold["wave_len"]) and np.isfinite(wav).all()
+    level = np.sqrt((wav ** 2).mean())
+    want = np.sqrt((gold["wave_block_rms"].astype(np.float64) ** 2).mean())
+    assert 0.25 * want < level < 4.0 * want, (level, want)
+
+
+def _node_close(got, want):
+    """Per-node bar: bit-exact for integer/bool outputs; for float outputs
+    |got - want| <= 1e-4 |want| + 1e-5 max|want| (the contraction/reduction
+    bar, which contains the elementwise one).  Returns None or a message."""
+    got, want = np.asarray(got), np.asarray(want)
+    if got.shape != want.shape:
+        return f"shape {got.shape} != {want.shape}"
+    if want.dtype.kind in "iub":
+        if got.dtype.kind not in "iub" or not np.array_equal(got.astype(np.int64), want.astype(np.int64)):
+            return f"integer/bool output differs ({got.dtype} vs {want.dtype})"
+        return None
+    g, w = got.astype(np.float64), want.astype(np.float64)
+    fin = np.isfinite(w)
+    if not np.array_equal(fin, np.isfinite(g)):
+        return "non-finite pattern differs"
+    if not fin.any():
+        return None
+    err = np.abs(g[fin] - w[fin])
+    lim = 1e-4 * np.abs(w[fin]) + 1e-5 * np.abs(w[fin]).max()
+    if (err > lim).any():
+        k = int(np.argmax(err - lim))
+        return f"{int((err > lim).sum())} elements out of tolerance, worst err {err[k]:.3g} vs {lim[k]:.3g}"
+    return None
+
+
+def test_every_node_teacher_forced(gpu, oracle):
+    """Every one of the graph's nodes run on the GPU with the oracle's exact
+    inputs (placed on host or device as the free-running GPU walk places
+    them) and checked against the oracle's output for that node.
+
+    The free-running waveform is not compared sample by sample: with random
+    learned weights the decoder amplifies fp32 reordering noise (~1e-5)
+    through its 26 int8 re-quantisations (a rounding flip moves a value by a
+    whole quantum) and through sin() of the accumulated F0 phase, so two
+    correct fp32 implementations give uncorrelated waveforms.  This test
+    removes that amplification: every node starts from the same inputs.
+    3 phoneme ids at speed 2.0 keep the CPU oracle near 15 s."""
+    kkg = importlib.import_module("best-tts-godot_amd.graph")
+    kpk_run = importlib.import_module("oracle.kpk_run")
+    g = kkg.load_graph(kkg.default_graph_path())
+    w = kkg.synth_weights(g, 0)
+    pg = kkg.PackedGraph(g, w)
+    ids, style, _ = kkg.synth_inputs(3, 1)
+    oenv = {str(k): v for k, v in w.items()}
+    oenv[pg.inputs["input_ids"]] = np.asarray(ids, np.int64).reshape(1, -1)
+    oenv[pg.inputs["style"]] = np.asarray(style, np.float32).reshape(1, 256)
+    oenv[pg.inputs["speed"]] = np.asarray([2.0], np.float32)
+    on_device = {pg.inputs["input_ids"]: False, pg.inputs["style"]: True, pg.inputs["speed"]: True}
+    failures, counted = [], 0
+    for i, ((op, ins, outs, at), raw) in enumerate(zip(pg.nodes, g["nodes"])):
+        genv = {}
+        for n in ins:
+            if not n or n in genv:
+                continue
+            if n in pg.weights:
+                genv[n] = pg.weights[n]
+            else:
+                genv[n] = gpu.to_device(np.asarray(oenv[n])) if on_device[n] else oenv[n]
+        oracle.dispatch(op, ins, outs, kpk_run.decode_attrs(raw[3]), oenv)
+        gpu.dispatch(op, ins, outs, at, genv)
+        for o in outs:
+            if not o:
+                continue
+            on_device[o] = isinstance(genv[o], gpu.DeviceTensor)
+            msg = _node_close(gpu.to_host(genv[o]), oenv[o])
+            counted += 1
+            if msg:
+                failures.append(f"node {i} {op} -> {o}: {msg}")
+        for n in ins:
+            if n and pg.last_use.get(n) == i:
+                oenv.pop(n, None)
+    assert counted > 3900
+    assert not failures, f"{len(failures)} node outputs differ:\n" + "\n".join(failures[:20])
+
+
+def test_repeat_is_identical(run8):
+    """A second run on the same inputs gives the same bits (the reference
+    gates run-to-run drift at exactly 0, tests/test_repeat.gd:97-112)."""
+    gold, wav, _, pg = run8
+    again = pg.run(gold["ids"], gold["style"], 1.0)
+    np.testing.assert_array_equal(again, wav)

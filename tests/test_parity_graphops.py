@@ -1,0 +1,165 @@
+"""Parity of the rest of the graph's device ops with the oracle:
+DynamicQuantizeLinear, MatMulInteger, ConvInteger, DynamicQuantizeLSTM, STFT,
+Resize, Pad, CumSum, ScatterND, and the host-side Range/NonZero fed from the
+device.
+
+Bars: bit-exact for the integer/quantised outputs, indexing and sequential
+sums; rel 1e-4 (+1e-5*max|ref|) for the LSTM and STFT, whose sums run in a
+different order than numpy's."""
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def node(kk, op, inputs, attrs=None, nout=1):
+    env, names = {}, []
+    for i, v in enumerate(inputs):
+        if v is None:
+            names.append("")
+            continue
+        if isinstance(v, tuple) and v[0] == "host":
+            env[f"i{i}"] = v[1]
+        else:
+            env[f"i{i}"] = kk.to_device(np.asarray(v))
+        names.append(f"i{i}")
+    outs = [f"o{k}" for k in range(nout)]
+    kk.dispatch(op, names, outs, attrs or {}, env)
+    res = [kk.to_host(env[o]) for o in outs]
+    return res[0] if nout == 1 else res
+
+
+def onode(oracle, op, inputs, attrs=None, nout=1):
+    env, names = {}, []
+    for i, v in enumerate(inputs):
+        if v is None:
+            names.append("")
+            continue
+        env[f"i{i}"] = v[1] if isinstance(v, tuple) else np.asarray(v)
+        names.append(f"i{i}")
+    outs = [f"o{k}" for k in range(nout)]
+    oracle.dispatch(op, names, outs, attrs or {}, env)
+    res = [env[o] for o in outs]
+    return res[0] if nout == 1 else res
+
+
+@pytest.mark.parametrize("case", ["normal", "positive", "negative", "zeros", "big"])
+def test_dynamic_quantize_linear(gpu, oracle, case):
+    r = rng(1)
+    x = {"normal": r.normal(0, 1, (1, 130, 768)),
+         "positive": r.uniform(0.5, 3, (4, 1000)),
+         "negative": -r.uniform(0.5, 3, (4, 1000)),
+         "zeros": np.zeros((3, 7)),
+         "big": r.normal(0, 50, (1, 512, 2400))}[case].astype(np.float32)
+    y, s, z = node(gpu, "DynamicQuantizeLinear", [x], nout=3)
+    yo, so, zo = onode(oracle, "DynamicQuantizeLinear", [x], nout=3)
+    assert_bitexact(np.asarray(s, np.float32).reshape(()), np.asarray(so, np.float32), "scale")
+    assert_bitexact(np.asarray(z, np.uint8).reshape(()), np.asarray(zo, np.uint8), "zero point")
+    assert_bitexact(y, yo, f"quantised {case}")
+
+
+def test_matmul_integer(gpu, oracle):
+    r = rng(2)
+    a = r.integers(0, 256, (1, 130, 768)).astype(np.uint8)
+    b = r.integers(-127, 128, (768, 2048)).astype(np.int8)
+    azp = np.uint8(117)
+    bzp = r.integers(-4, 5, 2048).astype(np.int8)
+    got = node(gpu, "MatMulInteger", [a, b, azp, bzp])
+    assert_bitexact(got, onode(oracle, "MatMulInteger", [a, b, azp, bzp]), "MatMulInteger")
+    got = node(gpu, "MatMulInteger", [a[0, :7, :33], b[:33, :50], None, None])
+    assert_bitexact(got, oracle.matmul_integer(a[0, :7, :33], b[:33, :50]), "no zero points")
+    # the duration projection's shape: K a multiple of 4, N = 50 is not
+    ins = [a[:, :10, :512], np.ascontiguousarray(b[:512, :50]), azp, bzp[:50]]
+    assert_bitexact(node(gpu, "MatMulInteger", ins), onode(oracle, "MatMulInteger", ins),
+                    "MatMulInteger N=50")
+
+
+@pytest.mark.parametrize("cin,cout,k,L,pad,dil", [(512, 512, 3, 240, 1, 1), (1090, 1024, 3, 40, 1, 1),
+                                                  (256, 256, 7, 300, 9, 3), (1, 1, 3, 50, 1, 1),
+                                                  (22, 128, 1, 480, 0, 1)])
+def test_conv_integer(gpu, oracle, cin, cout, k, L, pad, dil):
+    r = rng(3)
+    x = r.integers(0, 256, (1, cin, L)).astype(np.uint8)
+    w = r.integers(0, 256, (cout, cin, k)).astype(np.uint8)
+    xzp, wzp = np.uint8(121), np.uint8(128)
+    at = {"pads": [pad, pad], "dilations": [dil], "strides": [1], "group": 1}
+    got = node(gpu, "ConvInteger", [x, w, xzp, wzp], at)
+    assert_bitexact(got, onode(oracle, "ConvInteger", [x, w, xzp, wzp], at),
+                    f"ConvInteger {cin}->{cout} k{k}")
+
+
+@pytest.mark.parametrize("seq,inp", [(40, 640), (7, 512), (1, 64)])
+def test_lstm(gpu, oracle, seq, inp):
+    r = rng(4)
+    H = 256
+    x = r.normal(0, 1, (seq, 1, inp)).astype(np.float32)
+    w = r.integers(-127, 128, (2, inp, 4 * H)).astype(np.int8)
+    rr = r.integers(-127, 128, (2, H, 4 * H)).astype(np.int8)
+    b = r.normal(0, 0.05, (2, 8 * H)).astype(np.float32)
+    h0 = np.zeros((2, 1, H), np.float32)
+    ws = r.uniform(0.002, 0.006, 2).astype(np.float32)
+    rs = r.uniform(0.002, 0.006, 2).astype(np.float32)
+    wz = np.array([0, 1], np.int8)
+    rz = np.array([-1, 0], np.int8)
+    ins = [x, w, rr, b, None, h0, h0, None, ws, wz, rs, rz]
+    at = {"hidden_size": H, "direction": "bidirectional"}
+    got = node(gpu, "DynamicQuantizeLSTM", ins, at, nout=3)
+    want = onode(oracle, "DynamicQuantizeLSTM", ins, at, nout=3)
+    for g, wv, name in zip(got, want, ("Y", "Y_h", "Y_c")):
+        assert_close(g, wv, 1e-4, floor_rel=1e-5, what=f"LSTM {name} seq={seq}")
+
+
+def test_stft(gpu, oracle):
+    r = rng(5)
+    sig = r.normal(0, 1, (1, 3005)).astype(np.float32)
+    win = np.hanning(20).astype(np.float16)
+    ins = [sig, ("host", np.array(5)), win, ("host", np.array(20))]
+    got = node(gpu, "STFT", ins, {"onesided": 1})
+    assert_close(got, onode(oracle, "STFT", ins, {"onesided": 1}), 1e-6, floor_rel=1e-7,
+                 what="STFT")
+
+
+@pytest.mark.parametrize("mode,ctm,nm,scale,L", [("nearest", "asymmetric", "floor", 300.0, 37),
+                                                 ("linear", "half_pixel", "", 2.0, 101),
+                                                 ("nearest", "asymmetric", "floor", 2.0, 64)])
+def test_resize(gpu, oracle, mode, ctm, nm, scale, L):
+    x = rng(6).normal(0, 1, (1, 3, L)).astype(np.float32)
+    scales = np.array([1.0, 1.0, scale], np.float32)
+    at = {"mode": mode, "coordinate_transformation_mode": ctm, "nearest_mode": nm}
+    ins = [x, None, scales]
+    got = node(gpu, "Resize", ins, at)
+    want = onode(oracle, "Resize", ins, at)
+    assert_bitexact(got, want.astype(np.float32), f"Resize {mode} x{scale}")
+
+
+@pytest.mark.parametrize("mode", ["reflect", "edge", "constant"])
+def test_pad(gpu, oracle, mode):
+    x = rng(7).normal(0, 1, (1, 4, 30)).astype(np.float32)
+    pads = np.array([0, 0, 5, 0, 0, 3], np.int64)
+    got = node(gpu, "Pad", [x, ("host", pads)], {"mode": mode})
+    assert_bitexact(got, onode(oracle, "Pad", [x, ("host", pads)], {"mode": mode}), f"Pad {mode}")
+
+
+def test_cumsum_scatter_range_nonzero(gpu, oracle):
+    r = rng(8)
+    x = r.normal(0, 1, (1, 2, 5000)).astype(np.float32)
+    got = node(gpu, "CumSum", [x, ("host", np.array(2, np.int32))])
+    assert_bitexact(got, onode(oracle, "CumSum", [x, ("host", np.array(2, np.int32))]), "CumSum f32")
+    d = r.integers(1, 40, (1, 6)).astype(np.int64)
+    got = node(gpu, "CumSum", [d, ("host", np.array(1, np.int32))])
+    assert_bitexact(got, np.cumsum(d, axis=1), "CumSum int64")
+    data = r.normal(0, 1, (6, 10, 4)).astype(np.float32)
+    idx = np.array([[1], [3], [1], [5]], np.int64)
+    upd = r.normal(0, 1, (4, 10, 4)).astype(np.float32)
+    got = node(gpu, "ScatterND", [data, ("host", idx), upd])
+    assert_bitexact(got, onode(oracle, "ScatterND", [data, ("host", idx), upd]), "ScatterND")
+    # Range / NonZero with device inputs: the host computes them after a download
+    env = {"s": gpu.to_device(np.array(0, np.int64)), "e": gpu.to_device(np.array(11, np.int64)),
+           "d": np.array(3, np.int64)}
+    gpu.dispatch("Range", ["s", "e", "d"], ["o"], {}, env)
+    assert np.array_equal(env["o"], np.arange(0, 11, 3))
+    env["b"] = gpu.to_device(np.array([[True, False, True], [False, False, True]]))
+    gpu.dispatch("NonZero", ["b"], ["nz"], {}, env)
+    assert np.array_equal(env["nz"], np.array(np.nonzero([[1, 0, 1], [0, 0, 1]]), np.int64))
