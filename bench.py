@@ -6,6 +6,10 @@ inputs: AdaIN (InstanceNorm over T, eps 1e-5, with the style Linear
 eps 1e-12) on [1,256,768] and Softmax(last axis) on [1,12,256,256].  `value`
 is the algorithmic HBM bytes of a step divided by its time (GB/s).
 
+The second half of the metric, audio-seconds per wall-second, is the
+`kokoro_graph` object: the whole packed Kokoro graph for 128 phoneme ids,
+timed from host ids to host waveform.
+
 Timing: every step's kernels are recorded once into a HIP graph per input
 set; the timed region replays them with HIP events on libkk's stream.
 Inputs rotate over enough sets (> 512 MB) that the 256 MB Infinity Cache
@@ -13,7 +17,8 @@ cannot serve them.  Per-op lines (elementwise set, reductions, dequant
 GEMM/conv, the decoder upsample stage) are measured the same way, one op
 per graph node.  The CPU baseline runs the numpy oracle on this host.
 
-usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-graph]
+                       [--graph-ids 128] [--graph-reps 5] [--graph-cpu-ids 2]
 """
 import argparse
 import ctypes
@@ -269,6 +274,65 @@ def run_gpu(args):
     return ms_per_step, nsets, ops_out, roofline
 
 
+def run_graph(n_ids, reps):
+    """Config 5: the full Kokoro-architecture graph (packed structure, seeded
+    random learned weights) for `n_ids` phoneme ids.  Wall time runs from host
+    input ids to the host waveform (uploads, the duration readback and the
+    download included); the one-time weight upload is not timed."""
+    kk = importlib.import_module("best-tts-godot_amd")
+    kkg = importlib.import_module("best-tts-godot_amd.graph")
+    g = kkg.load_graph(kkg.default_graph_path())
+    pg = kkg.PackedGraph(g, kkg.synth_weights(g, 0))
+    ids, style, speed = kkg.synth_inputs(n_ids, 0)
+    pg.run(ids, style, speed, keep=[2432])  # warm-up: fills the buffer pool
+    frames = int(np.asarray(kk.to_host(pg.last_env["2432"])).sum())
+    kk.sync()
+    walls = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        wav = pg.run(ids, style, speed)
+        walls.append(time.perf_counter() - t0)
+    wall = float(np.median(walls))
+    audio = wav.size / 24000.0
+    rec = {
+        "audio_sec_per_wall_sec": round(audio / wall, 2),
+        "wall_ms": round(wall * 1e3, 2),
+        "wall_ms_runs": [round(w * 1e3, 2) for w in walls],
+        "tokens_T": int(len(ids)),
+        "frames_F": frames,
+        "samples": int(wav.size),
+        "audio_sec": round(audio, 3),
+        "nodes": len(pg.nodes),
+        "peak_pool_bytes": kk.pool_stats()[2],
+        "workload": (f"full Kokoro-82M-architecture graph ({len(pg.nodes)} nodes, int8 GEMM/conv "
+                     f"+ fp16 weights, seeded random-init), {n_ids} phoneme ids U{{1..177}}, "
+                     "voice-pack row style, speed 1.0"),
+    }
+    log(f"bench: kokoro graph {json.dumps(rec)}")
+    return rec
+
+
+def run_graph_cpu(n_ids):
+    """The oracle's whole-graph walk on a bounded sample (n_ids ids)."""
+    from oracle import kpk_run
+    kkg = importlib.import_module("best-tts-godot_amd.graph")
+    g = kkg.load_graph(kkg.default_graph_path())
+    w = kkg.synth_weights(g, 0)
+    ids, style, speed = kkg.synth_inputs(n_ids, 0)
+    t0 = time.perf_counter()
+    wav = kpk_run.run(g, w, ids, style, speed)
+    wall = time.perf_counter() - t0
+    return {
+        "value": round(wav.size / 24000.0 / wall, 4),
+        "unit": "audio-sec per wall-sec",
+        "cores": len(os.sched_getaffinity(0)),
+        "kind": "port",
+        "sample": (f"numpy oracle whole-graph walk, {n_ids} ids ({len(ids)} tokens), "
+                   f"{wav.size} samples in {wall:.1f} s; numpy ufuncs/einsum on 1 thread, "
+                   f"BLAS matmuls on up to the visible cores"),
+    }
+
+
 def run_cpu(seconds):
     """The numpy oracle on this host, single-threaded, over the same step."""
     from oracle import ref_ops as O
@@ -322,12 +386,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--graph-ids", type=int, default=128)
+    ap.add_argument("--graph-reps", type=int, default=5)
+    ap.add_argument("--graph-cpu-ids", type=int, default=2)
+    ap.add_argument("--no-graph", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the op layer shards by utterance with no collective)", file=sys.stderr)
         return 2
     ms_per_step, nsets, ops_out, roofline = run_gpu(args)
+    graph = None
+    if not args.no_graph:
+        graph = run_graph(args.graph_ids, args.graph_reps)
+        if not args.no_cpu:
+            graph["cpu_baseline"] = run_graph_cpu(args.graph_cpu_ids)
     cpu = None if args.no_cpu else run_cpu(args.cpu_seconds)
     value = STEP_BYTES / (ms_per_step * 1e-3) / 1e9
     line = {
@@ -354,6 +427,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "ops": ops_out,
+        "kokoro_graph": graph,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -419,6 +419,81 @@ __global__ void __launch_bounds__(kRowBlock) reduce_rows_kernel(float* __restric
   if (g == 0) out[row] = v;
 }
 
+// Split-row reduction for long trailing rows (the decoder's InstanceNorm
+// means over T = 10^4..10^6 samples with only 128..512 rows): block
+// (c, row) reduces chunk c of the row into part[row * nchunk + c], then one
+// wave per row folds the partials in chunk order.  Both stages use fixed
+// orders, so the result does not depend on scheduling.
+constexpr int64_t kChunk = 8192;
+
+template <bool VEC>
+__global__ void __launch_bounds__(kRowBlock) reduce_chunks_kernel(float* __restrict__ part,
+                                                                  const float* __restrict__ x,
+                                                                  int64_t cols, int nchunk,
+                                                                  int op) {
+  __shared__ float lds[4];
+  const int64_t row = blockIdx.y;
+  const int c = blockIdx.x;
+  const float* xr = x + row * cols;
+  const int64_t lo = static_cast<int64_t>(c) * kChunk;
+  const int64_t hi = lo + kChunk < cols ? lo + kChunk : cols;
+  const bool is_max = op == KK_REDUCE_MAX;
+  float acc = is_max ? -INFINITY : 0.0f;
+  bool nan = false;
+  if constexpr (VEC) {
+#pragma unroll 4
+    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * kRowBlock) {
+      const float4 v = ld_stream4(xr + i);
+      if (is_max) {
+        nan |= __builtin_isnan(v.x) | __builtin_isnan(v.y) | __builtin_isnan(v.z) |
+               __builtin_isnan(v.w);
+        acc = fmaxf(fmaxf(acc, v.x), fmaxf(v.y, fmaxf(v.z, v.w)));
+      } else {
+        acc += (v.x + v.y) + (v.z + v.w);
+      }
+    }
+  } else {
+#pragma unroll 4
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kRowBlock) {
+      const float v = ld_stream(xr + i);
+      if (is_max) { nan |= __builtin_isnan(v); acc = fmaxf(acc, v); }
+      else acc += v;
+    }
+  }
+  float v;
+  if (is_max) {
+    v = group_max<kRowBlock>(acc, lds);
+    if (group_max<kRowBlock>(nan ? 1.0f : 0.0f, lds) > 0.0f) v = NAN;
+  } else {
+    v = group_sum<kRowBlock>(acc, lds);
+  }
+  if (threadIdx.x == 0) part[row * nchunk + c] = v;
+}
+
+__global__ void __launch_bounds__(kRowBlock) reduce_fold_kernel(float* __restrict__ out,
+                                                                const float* __restrict__ part,
+                                                                int64_t rows, int nchunk,
+                                                                int64_t cols, int op) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kRowBlock / 64) + threadIdx.x / 64;
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const float* p = part + row * nchunk;
+  float v;
+  if (op == KK_REDUCE_MAX) {
+    float m = -INFINITY;
+    bool nan = false;
+    for (int c = lane; c < nchunk; c += 64) { nan |= __builtin_isnan(p[c]); m = fmaxf(m, p[c]); }
+    m = wave_max(m);
+    v = wave_max(nan ? 1.0f : 0.0f) > 0.0f ? NAN : m;
+  } else {
+    float s = 0.0f;
+    for (int c = lane; c < nchunk; c += 64) s += p[c];
+    s = wave_sum(s);
+    v = op == KK_REDUCE_MEAN ? s / static_cast<float>(cols) : s;
+  }
+  if (lane == 0) out[row] = v;
+}
+
 // General reduction: kept axes (kdims/kst) index the output in order,
 // reduced axes (rdims/rst) are walked by each thread; x is strided.
 struct RedArgs {
@@ -734,6 +809,31 @@ int kk_reduce(int op, const kk_tensor* out, const kk_tensor* x, uint32_t axes_ma
   }
   RowShape rs;
   const bool vec_ok = (nred % 4 == 0) && aligned16(x->data);
+  if (trailing && nred > 2 * kChunk) {
+    const int64_t nchunk = ceil_div(nred, kChunk);
+    if (nout > 65535) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)nout);
+    void* part = nullptr;
+    KK_TRY(kk_alloc(sizeof(float) * nout * nchunk, &part));
+    const dim3 grid(static_cast<unsigned>(nchunk), static_cast<unsigned>(nout));
+    if (vec_ok)
+      hipLaunchKernelGGL(reduce_chunks_kernel<true>, grid, dim3(kRowBlock), 0, ctx().stream,
+                         static_cast<float*>(part), static_cast<const float*>(x->data), nred,
+                         static_cast<int>(nchunk), op);
+    else
+      hipLaunchKernelGGL(reduce_chunks_kernel<false>, grid, dim3(kRowBlock), 0, ctx().stream,
+                         static_cast<float*>(part), static_cast<const float*>(x->data), nred,
+                         static_cast<int>(nchunk), op);
+    int rc = check_launch("reduce_chunks_kernel");
+    if (rc == KK_OK) {
+      const unsigned g = static_cast<unsigned>(ceil_div(nout, kRowBlock / 64));
+      hipLaunchKernelGGL(reduce_fold_kernel, dim3(g), dim3(kRowBlock), 0, ctx().stream,
+                         static_cast<float*>(out->data), static_cast<const float*>(part), nout,
+                         static_cast<int>(nchunk), nred, op);
+      rc = check_launch("reduce_fold_kernel");
+    }
+    kk_free(part);  // stream order keeps it alive for the fold
+    return rc;
+  }
   if (trailing && pick_row_shape(nred, vec_ok, &rs)) {
     KK_ROW_DISPATCH(reduce_rows_kernel, rs, nout, static_cast<float*>(out->data),
                     static_cast<const float*>(x->data), nout, nred, op);

@@ -6,9 +6,11 @@ tests/golden/make_graph_golden.py).
 
 Bars: the integer durations bit-exact (they set the output length), the
 pre-round durations and the text LSTM within rel 1e-4; the STFT of the
-harmonic source and the waveform within the reference's own GPU-vs-numpy tap
-gate -- relative RMS 0.05 (tests/test_taps.gd:19-26) -- after ~3900 chained
-fp32 nodes, with non-finite values counted explicitly."""
+harmonic source within the reference's own GPU-vs-numpy tap gate -- relative
+RMS 0.05 (tests/test_taps.gd:19-26) -- with non-finite values counted
+explicitly; every node of the graph, teacher-forced from the oracle's inputs,
+bit-exact for integer outputs and within rel 1e-4 (+1e-5 max) for floats;
+run-to-run identical bits."""
 import importlib
 import os
 
@@ -54,15 +56,14 @@ def test_text_lstm(run8):
 
 def test_harmonic_stft_and_waveform(run8):
     """The STFT of the harmonic source within the reference's tap gate; the
-    free-running waveform only for its length, finiteness and level (its
-    samples are compared node by node in the teacher-forced test)."""
+    free-running waveform only for its length and finiteness.  Its samples
+    (and even its level: the random-weight decoder reaches RMS ~1e15, and a
+    change of summation order in one reduction moves that by several times)
+    are checked node by node in the teacher-forced test instead."""
     gold, wav, caps, _ = run8
     assert rel_rms(caps["3037"], gold["t3037"]) < 0.05
-    wav = wav.reshape(-1).astype(np.float64)
+    wav = wav.reshape(-1)
     assert wav.size == int(gold["wave_len"]) and np.isfinite(wav).all()
-    level = np.sqrt((wav ** 2).mean())
-    want = np.sqrt((gold["wave_block_rms"].astype(np.float64) ** 2).mean())
-    assert 0.25 * want < level < 4.0 * want, (level, want)
 
 
 def _node_close(got, want):

@@ -142,7 +142,8 @@ def test_softmax(gpu, oracle, shape, axis):
 @pytest.mark.parametrize("op", ["ReduceMean", "ReduceSum"])
 @pytest.mark.parametrize("shape,axes,keep", [((1, 512, 2400), [2], 1), ((6, 40), [0], 1),
                                              ((3, 4, 50), [0, 2], 0), ((2, 3, 7), None, 1),
-                                             ((1, 64, 9), [-1], 0)])
+                                             ((1, 64, 9), [-1], 0), ((1, 128, 100000), [2], 1),
+                                             ((1, 3, 40001), [-1], 1)])
 def test_reduce(gpu, oracle, op, shape, axes, keep):
     x = rng(9).normal(0, 1, shape).astype(np.float32)
     env = {"x": gpu.to_device(x)}
