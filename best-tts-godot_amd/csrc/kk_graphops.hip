@@ -85,10 +85,21 @@ __global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x,
 }
 
 // ------------------------------------------------------------------- LSTM
-// One block per (direction, batch row) runs the whole recurrence: thread j
-// owns gate column j of g = (xw[t] + (wb + rb)) + h @ R, with R's column
-// dequantised on the fly ((q - zp) * scale, the value op_lstm.deq builds);
-// h and the gates live in LDS.  Gate order i, o, f, c (ref_runtime.py:194-208).
+// One block of 1024 threads per (direction, batch row) runs the whole
+// recurrence; thread j owns gate column j of
+//   g = (xw[t] + (wb + rb)) + h @ deq(R),  deq(R) = (q - zp) * scale
+// (op_lstm, ref_runtime.py:137-210; gate order i, o, f, c).
+//
+// R's column j stays in registers for all steps: its 256 int8 values,
+// shifted to u = q + 128, packed four to a word (64 VGPRs), so a
+// multiply-accumulate is one byte-to-float conversion and one FMA.  With
+// z = zp + 128 the column sum is
+//   sum_k h_k (q_k - zp) = sum_k h_k u_k - z * sum_k h_k,
+// and the scale multiplies the result once.  h is broadcast from LDS as
+// float4; sum_k h_k is reduced once per step by the threads that update h.
+constexpr int kLstmThreads = 1024;
+constexpr int kLstmMaxH = kLstmThreads / 4;
+
 struct LstmArgs {
   const float* xw;       // [ndir][seq * batch][4H] input projections x @ deq(W)
   const float* bias;     // [ndir][8H] or NULL
@@ -107,57 +118,93 @@ struct LstmArgs {
   int64_t seq, batch, H, ndir;
 };
 
-__global__ void __launch_bounds__(1024) lstm_recurrence(LstmArgs A) {
-  extern __shared__ float lds[];
-  const int64_t H = A.H, G4 = 4 * H;
-  float* hs = lds;        // [H]
-  float* gs = lds + H;    // [4H]
+__global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
+  __shared__ __align__(16) float hs[kLstmMaxH];
+  __shared__ float gs[kLstmThreads];
+  __shared__ float hpart[kLstmMaxH / 64];
+  const int H = static_cast<int>(A.H), G4 = 4 * H;
   const int64_t d = blockIdx.x / A.batch, b = blockIdx.x % A.batch;
+  const int j = threadIdx.x;
+  const int lane = j & 63, wv = j >> 6;
   const float rs = load_as_f32(A.r_scale, A.r_scale_dt, A.r_scale_n > 1 ? d : 0);
-  const float rz = A.r_zp ? load_as_f32(A.r_zp, A.r_zp_dt, A.r_zp_n > 1 ? d : 0) : 0.0f;
-  const int8_t* R = A.r + d * H * G4;
+  const float z = 128.0f + (A.r_zp ? load_as_f32(A.r_zp, A.r_zp_dt, A.r_zp_n > 1 ? d : 0) : 0.0f);
+  const int8_t* R = A.r + d * static_cast<int64_t>(H) * G4;
   const float* xw = A.xw + d * A.seq * A.batch * G4;
-  // c for the units this thread updates (thread u < H)
-  float c = 0.0f;
-  for (int64_t u = threadIdx.x; u < H; u += blockDim.x) {
-    hs[u] = A.init_h ? A.init_h[(d * A.batch + b) * H + u] : 0.0f;
-    if (u == threadIdx.x) c = A.init_c ? A.init_c[(d * A.batch + b) * H + u] : 0.0f;
+  // Column j of R, as u = q + 128 in bytes; rows k >= H hold 0 (and h_k = 0).
+  uint32_t w[kLstmMaxH / 4];
+#pragma unroll
+  for (int m = 0; m < kLstmMaxH / 4; ++m) {
+    uint32_t p = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int k = 4 * m + e;
+      if (j < G4 && k < H)
+        p |= static_cast<uint32_t>(static_cast<uint8_t>(R[static_cast<int64_t>(k) * G4 + j]) ^ 0x80u)
+             << (8 * e);
+    }
+    w[m] = p;
+  }
+  const float bj = (A.bias && j < G4) ? A.bias[d * 2 * G4 + j] + A.bias[d * 2 * G4 + G4 + j] : 0.0f;
+  float c = 0.0f, h0 = 0.0f;
+  if (j < H) {
+    h0 = A.init_h ? A.init_h[(d * A.batch + b) * H + j] : 0.0f;
+    c = A.init_c ? A.init_c[(d * A.batch + b) * H + j] : 0.0f;
+  }
+  if (j < kLstmMaxH) {
+    hs[j] = h0;
+    const float sv = wave_sum(h0);
+    if (lane == 0) hpart[wv] = sv;
   }
   __syncthreads();
+  float hsum = (hpart[0] + hpart[1]) + (hpart[2] + hpart[3]);
+  const float4* hs4 = reinterpret_cast<const float4*>(hs);
   for (int64_t step = 0; step < A.seq; ++step) {
     const int64_t t = d == 0 ? step : A.seq - 1 - step;
-    for (int64_t j = threadIdx.x; j < G4; j += blockDim.x) {
-      float acc = 0.0f;
-      for (int64_t k = 0; k < H; ++k) {
-        const float q = static_cast<float>(R[k * G4 + j]);
-        acc = __builtin_fmaf(hs[k], (q - rz) * rs, acc);
+    // Keep the packed column packed: without this the compiler hoists the
+    // 256 byte-to-float conversions out of the step loop and spills them.
+#pragma unroll
+    for (int m = 0; m < kLstmMaxH / 4; ++m) asm volatile("" : "+v"(w[m]));
+    if (j < G4) {
+      const float xv = xw[(t * A.batch + b) * G4 + j] + bj;
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+#pragma unroll
+      for (int m = 0; m < kLstmMaxH / 4; ++m) {
+        const float4 h4 = hs4[m];
+        const uint32_t p = w[m];
+        a0 = __builtin_fmaf(h4.x, static_cast<float>(p & 0xffu), a0);
+        a1 = __builtin_fmaf(h4.y, static_cast<float>((p >> 8) & 0xffu), a1);
+        a2 = __builtin_fmaf(h4.z, static_cast<float>((p >> 16) & 0xffu), a2);
+        a3 = __builtin_fmaf(h4.w, static_cast<float>(p >> 24), a3);
       }
-      float xv = xw[(t * A.batch + b) * G4 + j];
-      if (A.bias) xv = xv + (A.bias[d * 2 * G4 + j] + A.bias[d * 2 * G4 + G4 + j]);
-      gs[j] = xv + acc;
+      const float acc = ((a0 + a1) + (a2 + a3)) - z * hsum;
+      gs[j] = xv + acc * rs;
     }
     __syncthreads();
-    if (threadIdx.x < H) {
-      const int64_t u = threadIdx.x;
-      const float ig = 1.0f / (1.0f + expf(-gs[u]));
-      const float og = 1.0f / (1.0f + expf(-gs[H + u]));
-      const float fg = 1.0f / (1.0f + expf(-gs[2 * H + u]));
-      const float cc = tanhf(gs[3 * H + u]);
-      c = fg * c + ig * cc;
-      const float h = og * tanhf(c);
-      hs[u] = h;
-      A.ys[((t * A.ndir + d) * A.batch + b) * H + u] = h;
-      if (step == A.seq - 1) {
-        if (A.yh) A.yh[(d * A.batch + b) * H + u] = h;
-        if (A.yc) A.yc[(d * A.batch + b) * H + u] = c;
+    if (j < kLstmMaxH) {
+      float h = 0.0f;
+      if (j < H) {
+        const float ig = 1.0f / (1.0f + expf(-gs[j]));
+        const float og = 1.0f / (1.0f + expf(-gs[H + j]));
+        const float fg = 1.0f / (1.0f + expf(-gs[2 * H + j]));
+        const float cc = tanhf(gs[3 * H + j]);
+        c = fg * c + ig * cc;
+        h = og * tanhf(c);
+        hs[j] = h;
+        A.ys[((t * A.ndir + d) * A.batch + b) * H + j] = h;
+        if (step == A.seq - 1) {
+          if (A.yh) A.yh[(d * A.batch + b) * H + j] = h;
+          if (A.yc) A.yc[(d * A.batch + b) * H + j] = c;
+        }
       }
+      const float sv = wave_sum(h);
+      if (lane == 0) hpart[wv] = sv;
     }
     __syncthreads();
+    hsum = (hpart[0] + hpart[1]) + (hpart[2] + hpart[3]);
   }
-  if (A.seq == 0 && threadIdx.x < H) {
-    const int64_t u = threadIdx.x;
-    if (A.yh) A.yh[(d * A.batch + b) * H + u] = hs[u];
-    if (A.yc) A.yc[(d * A.batch + b) * H + u] = c;
+  if (A.seq == 0 && j < H) {
+    if (A.yh) A.yh[(d * A.batch + b) * H + j] = h0;
+    if (A.yc) A.yc[(d * A.batch + b) * H + j] = c;
   }
 }
 
@@ -360,7 +407,8 @@ int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const
     return set_error(KK_E_ARG, "kk_lstm: W must be [dir, input, 4H]");
   if (r->rank != 3 || r->shape[0] != ndir || r->shape[1] != H || r->shape[2] != 4 * H)
     return set_error(KK_E_ARG, "kk_lstm: R must be [dir, H, 4H]");
-  if (4 * H > 1024) return set_error(KK_E_UNSUPPORTED, "kk_lstm: 4H > 1024");
+  if (H < 1 || H > kLstmMaxH)
+    return set_error(KK_E_UNSUPPORTED, "kk_lstm: hidden size %lld (1..%d)", (long long)H, kLstmMaxH);
   if (numel(ys) != seq * ndir * batch * H) return set_error(KK_E_ARG, "kk_lstm: ys shape");
   const int64_t nws = numel(w_scale), nrs = numel(r_scale);
   if ((nws != 1 && nws != ndir) || (nrs != 1 && nrs != ndir))
@@ -410,9 +458,8 @@ int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const
     A.yh = yh ? static_cast<float*>(yh->data) : nullptr;
     A.yc = yc ? static_cast<float*>(yc->data) : nullptr;
     A.seq = seq; A.batch = batch; A.H = H; A.ndir = ndir;
-    const size_t lds = sizeof(float) * 5 * H;
-    hipLaunchKernelGGL(lstm_recurrence, dim3(static_cast<unsigned>(ndir * batch)), dim3(1024), lds,
-                       ctx().stream, A);
+    hipLaunchKernelGGL(lstm_recurrence, dim3(static_cast<unsigned>(ndir * batch)),
+                       dim3(kLstmThreads), 0, ctx().stream, A);
     rc = check_launch("lstm_recurrence");
   }
   kk_free(xw);
