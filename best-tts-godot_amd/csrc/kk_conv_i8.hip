@@ -1,0 +1,231 @@
+// ConvInteger on the int8 matrix cores (v_mfma_i32_32x32x32_i8), exact in
+// int32 (op_conv_integer, ref_runtime.py:130-134: conv of (x - x_zp) with
+// (w - w_zp), padding contributing 0 after the shift).
+//
+// Both uint8 operands are offset into int8 (u - 128), so a product of
+// shifted values expands as
+//   sum_k (a_k - wz')(b_k - xz') = sum_k a_k b_k - xz' sum_k a_k
+//                                  - wz' sum_k b_k + K wz' xz'
+// with a = w - 128 (uint8 weights; int8 weights are used as they are),
+// b = x - 128, wz' and xz' the zero points offset the same way.  Padded time
+// positions hold b = xz', so they contribute 0 exactly as the reference's
+// zero padding of the shifted input does.
+//
+// Layout: the weights become wT[Cout][Kw][CinP] and the activations
+// xT[N][Lp][CinP] (time-major, channels contiguous, CinP = Cin rounded up
+// to 32 with zero channels), so each MFMA operand fragment -- 16 channels
+// of one tap at one output row or time step -- is one 16-byte load.  The
+// prep kernels also produce sum_k a_k per output channel and
+// sum_ci b[t][ci] per time step for the epilogue.
+#include "kk_internal.h"
+
+namespace kk {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr int kTileM = 128;  // output channels per block (2 waves x 64)
+constexpr int kTileN = 128;  // output time steps per block (2 waves x 64)
+constexpr int kCinAlign = 32;
+
+// wT[co][tap][ci] = offset weight (0 for padding rows/channels);
+// wsum[co] = sum of the offset weights; wzo[co] = offset weight zero point.
+__global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w, int w_dt,
+                                                     const void* __restrict__ wzp, int wzp_dt,
+                                                     int64_t wzp_n, int8_t* __restrict__ wT,
+                                                     int32_t* __restrict__ wsum,
+                                                     int32_t* __restrict__ wzo, int64_t Cout,
+                                                     int64_t Cin, int64_t Kw, int64_t CinP) {
+  __shared__ int part[4];
+  const int64_t co = blockIdx.x;
+  const bool live = co < Cout;
+  const int off = w_dt == KK_U8 ? 128 : 0;
+  int local = 0;
+  for (int64_t idx = threadIdx.x; idx < Kw * CinP; idx += blockDim.x) {
+    const int64_t tap = idx / CinP, ci = idx % CinP;
+    int a = 0;
+    if (live && ci < Cin) {
+      const int64_t src = (co * Cin + ci) * Kw + tap;
+      a = w_dt == KK_U8 ? static_cast<int>(static_cast<const uint8_t*>(w)[src]) - 128
+                        : static_cast<int>(static_cast<const int8_t*>(w)[src]);
+    }
+    wT[(co * Kw + tap) * CinP + ci] = static_cast<int8_t>(a);
+    local += a;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) local += __shfl_xor(local, o, 64);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  if (lane == 0) part[wv] = local;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    wsum[co] = live ? part[0] + part[1] + part[2] + part[3] : 0;
+    int z = 0;  // padding rows: a = 0, so any value works; keep 0
+    if (live) z = (wzp ? static_cast<int>(load_as_i64(wzp, wzp_dt, wzp_n > 1 ? co : 0)) : 0) - off;
+    wzo[co] = z;
+  }
+}
+
+// xT[b][t][ci] = x[b][ci][t - p0] - 128 for t inside the signal, xz - 128 in
+// the padding, 0 in the padding channels; xs[b][t] = sum over real channels.
+__global__ void __launch_bounds__(256) conv_i8_xprep(const uint8_t* __restrict__ x,
+                                                     const uint8_t* __restrict__ xzp,
+                                                     int8_t* __restrict__ xT,
+                                                     int32_t* __restrict__ xs, int64_t Cin,
+                                                     int64_t L, int64_t p0, int64_t Lp,
+                                                     int64_t CinP) {
+  const int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (t >= Lp) return;
+  const int pad = (xzp ? static_cast<int>(xzp[0]) : 0) - 128;
+  const int64_t ts = t - p0;
+  const bool inside = ts >= 0 && ts < L;
+  const uint8_t* xb = x + b * Cin * L;
+  int8_t* dst = xT + (b * Lp + t) * CinP;
+  int sum = 0;
+  for (int64_t c0 = 0; c0 < CinP; c0 += 16) {
+    v4i pack;
+    int8_t* pv = reinterpret_cast<int8_t*>(&pack);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int64_t ci = c0 + e;
+      int v = 0;
+      if (ci < Cin) v = inside ? static_cast<int>(xb[ci * L + ts]) - 128 : pad;
+      pv[e] = static_cast<int8_t>(v);
+      sum += v;
+    }
+    *reinterpret_cast<v4i*>(dst + c0) = pack;
+  }
+  xs[b * Lp + t] = sum;
+}
+
+struct ConvI8Args {
+  const int8_t* wT;     // [CoutP][Kw][CinP]
+  const int32_t* wsum;  // [CoutP]
+  const int32_t* wzo;   // [CoutP]
+  const int8_t* xT;     // [N][Lp][CinP]
+  const int32_t* xs;    // [N][Lp]
+  const uint8_t* xzp;   // one uint8 or NULL
+  int32_t* out;         // [N][Cout][Lout]
+  int64_t Cout, CinP, Kw, s, d, Lp, Lout, Kreal;
+};
+
+// Block: 4 waves as 2 (channels) x 2 (time); wave tile 64 x 64 as 2 x 2
+// MFMA tiles of 32 x 32.  Lane (r, g) = (lane % 32, lane / 32) supplies
+// A[r][16g .. 16g+15] and B[16g .. 16g+15][r] of each 32 x 32 x 32 step;
+// D(i, j) lands in lane j + 32 ((i / 4) % 2), register (i / 8) 4 + i % 4.
+__global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int r = lane & 31, g = lane >> 5;
+  const int64_t co0 = static_cast<int64_t>(blockIdx.y) * kTileM + (wv >> 1) * 64;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTileN + (wv & 1) * 64;
+  const int64_t b = blockIdx.z;
+  const int8_t* xT = A.xT + b * A.Lp * A.CinP;
+  const int8_t* wrow0 = A.wT + (co0 + r) * A.Kw * A.CinP + 16 * g;
+  const int8_t* wrow1 = wrow0 + 32 * A.Kw * A.CinP;
+  const int64_t t0 = (n0 + r) * A.s, t1 = (n0 + 32 + r) * A.s;
+  v16i acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+  for (int64_t tap = 0; tap < A.Kw; ++tap) {
+    // Time rows past the output's end are clamped in bounds; their results
+    // are never stored.
+    int64_t ta = t0 + tap * A.d, tb = t1 + tap * A.d;
+    ta = ta < A.Lp ? ta : A.Lp - 1;
+    tb = tb < A.Lp ? tb : A.Lp - 1;
+    const int8_t* x0 = xT + ta * A.CinP + 16 * g;
+    const int8_t* x1 = xT + tb * A.CinP + 16 * g;
+    const int8_t* w0 = wrow0 + tap * A.CinP;
+    const int8_t* w1 = wrow1 + tap * A.CinP;
+    for (int64_t c0 = 0; c0 < A.CinP; c0 += 32) {
+      const v4i a0 = *reinterpret_cast<const v4i*>(w0 + c0);
+      const v4i a1 = *reinterpret_cast<const v4i*>(w1 + c0);
+      const v4i b0 = *reinterpret_cast<const v4i*>(x0 + c0);
+      const v4i b1 = *reinterpret_cast<const v4i*>(x1 + c0);
+      acc00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc00, 0, 0, 0);
+      acc01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc01, 0, 0, 0);
+      acc10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc10, 0, 0, 0);
+      acc11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc11, 0, 0, 0);
+    }
+  }
+  const int xz = (A.xzp ? static_cast<int>(A.xzp[0]) : 0) - 128;
+  const int32_t* xs = A.xs + b * A.Lp;
+  int32_t* out = A.out + b * A.Cout * A.Lout;
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni) {
+    const int64_t l = n0 + 32 * ni + r;
+    if (l >= A.Lout) continue;
+    int S = 0;  // sum_k b_k of this output column
+    for (int64_t tap = 0; tap < A.Kw; ++tap) S += xs[l * A.s + tap * A.d];
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi) {
+      const v16i& acc = mi == 0 ? (ni == 0 ? acc00 : acc01) : (ni == 0 ? acc10 : acc11);
+#pragma unroll
+      for (int reg = 0; reg < 16; ++reg) {
+        const int64_t co = co0 + 32 * mi + 8 * (reg / 4) + 4 * g + (reg % 4);
+        if (co >= A.Cout) continue;
+        const int wz = A.wzo[co];
+        const int v = acc[reg] - xz * A.wsum[co] - wz * S + static_cast<int>(A.Kreal) * wz * xz;
+        out[co * A.Lout + l] = v;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Called by kk_conv_integer (group 1) after it has validated the operands.
+int conv_integer_i8(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                    const kk_tensor* x_zp, const kk_tensor* w_zp, int stride, int dilation,
+                    int pad0, int pad1) {
+  const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
+  const int64_t Cout = w->shape[0], Kw = w->shape[2];
+  const int64_t Lp = L + pad0 + pad1;
+  const int64_t Lout = out->shape[2];
+  const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
+  const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
+  // |each epilogue term| <= K * 2^14 must stay clear of 2^31.
+  if (Cin * Kw > 32768)
+    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer: Cin*K = %lld exceeds 32768",
+                     (long long)(Cin * Kw));
+  if (N > 65535 || ceil_div(Lout, kTileN) > 0x7fffffff)
+    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer: grid too large");
+  auto up = [](int64_t n) { return ceil_div(n, 256) * 256; };
+  const int64_t o_wT = 0, o_wsum = o_wT + up(CoutP * Kw * CinP);
+  const int64_t o_wzo = o_wsum + up(CoutP * 4), o_xs = o_wzo + up(CoutP * 4);
+  const int64_t o_xT = o_xs + up(N * Lp * 4), total = o_xT + up(N * Lp * CinP);
+  void* ws = nullptr;
+  KK_TRY(kk_alloc(static_cast<size_t>(total), &ws));
+  char* base = static_cast<char*>(ws);
+  int8_t* wT = reinterpret_cast<int8_t*>(base + o_wT);
+  int32_t* wsum = reinterpret_cast<int32_t*>(base + o_wsum);
+  int32_t* wzo = reinterpret_cast<int32_t*>(base + o_wzo);
+  int32_t* xs = reinterpret_cast<int32_t*>(base + o_xs);
+  int8_t* xT = reinterpret_cast<int8_t*>(base + o_xT);
+  hipStream_t st = ctx().stream;
+  hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
+                     w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
+                     w_zp ? numel(w_zp) : 0, wT, wsum, wzo, Cout, Cin, Kw, CinP);
+  int rc = check_launch("conv_i8_wprep");
+  const uint8_t* xzp = x_zp ? static_cast<const uint8_t*>(x_zp->data) : nullptr;
+  if (rc == KK_OK) {
+    hipLaunchKernelGGL(conv_i8_xprep, dim3(static_cast<unsigned>(ceil_div(Lp, 256)),
+                                           static_cast<unsigned>(N)),
+                       dim3(256), 0, st, static_cast<const uint8_t*>(x->data), xzp, xT, xs, Cin,
+                       L, static_cast<int64_t>(pad0), Lp, CinP);
+    rc = check_launch("conv_i8_xprep");
+  }
+  if (rc == KK_OK) {
+    ConvI8Args A{};
+    A.wT = wT; A.wsum = wsum; A.wzo = wzo; A.xT = xT; A.xs = xs; A.xzp = xzp;
+    A.out = static_cast<int32_t*>(out->data);
+    A.Cout = Cout; A.CinP = CinP; A.Kw = Kw; A.s = stride; A.d = dilation; A.Lp = Lp;
+    A.Lout = Lout; A.Kreal = Cin * Kw;
+    const dim3 grid(static_cast<unsigned>(ceil_div(Lout, kTileN)),
+                    static_cast<unsigned>(CoutP / kTileM), static_cast<unsigned>(N));
+    hipLaunchKernelGGL(conv_i8_kernel, grid, dim3(256), 0, st, A);
+    rc = check_launch("conv_i8_kernel");
+  }
+  kk_free(ws);  // stream order keeps the workspace alive for the kernels
+  return rc;
+}
+
+}  // namespace kk

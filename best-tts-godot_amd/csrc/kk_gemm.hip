@@ -268,16 +268,13 @@ struct BScalar {
 };
 
 // Conv1d input as the B operand: B[kk, l] = x[ci, l*s + k*d - p0] with
-// kk = ci*Kw + k; each thread gathers four consecutive l of one kk.  For
-// ConvInteger, x is uint8 and in-range taps read x - x_zp while padding
-// reads 0 (the zero-point shift precedes the padding, ref_runtime.py:131-133).
-template <class C, typename TX = float>
+// kk = ci*Kw + k; each thread gathers four consecutive l of one kk.
+template <class C>
 struct BIm2col {
   static constexpr int QPR = C::BN / 4;
   static constexpr int RPP = kNT / QPR;
   static constexpr int P = kBK / RPP;
-  const TX* x;     // this batch item's [Cin, L]
-  float xzp = 0.0f;
+  const float* x;  // this batch item's [Cin, L]
   int64_t L, Kw, s, d, p0, Kdim, Lout;
   int64_t l0;      // first output position of this thread's quad
   float4 v[P];
@@ -289,15 +286,12 @@ struct BIm2col {
       float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
       if (kk < Kdim) {
         const int64_t ci = kk / Kw, k = kk - ci * Kw;
-        const TX* xr = x + ci * L;
+        const float* xr = x + ci * L;
         const int64_t pos0 = l0 * s + k * d - p0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const int64_t pos = pos0 + c * s;
-          if (l0 + c < Lout && pos >= 0 && pos < L) {
-            if constexpr (std::is_same<TX, float>::value) e[c] = xr[pos];
-            else e[c] = static_cast<float>(xr[pos]) - xzp;
-          }
+          if (l0 + c < Lout && pos >= 0 && pos < L) e[c] = xr[pos];
         }
       }
       v[p] = make_float4(e[0], e[1], e[2], e[3]);
@@ -476,17 +470,15 @@ struct ConvArgs {
   const void* w;       // [Cout, Cin*Kw] (K contiguous)
   int w_dt;
   Dequant dq;          // per output channel (row) or per tensor
-  const void* x;       // [N, Cin, L], fp32 (Conv) or uint8 (ConvInteger)
-  const void* xzp;     // ConvInteger: uint8 zero point of x, or NULL
-  float* out;          // [N, Cout, Lout], fp32 or int32 when out_i32
-  int out_i32;
+  const float* x;      // [N, Cin, L]
+  float* out;          // [N, Cout, Lout]
   const float* bias;   // [Cout] or NULL
   int64_t Cin, L, Kw, s, d, p0, Lout;
   int64_t M, K;        // Cout, Cin*Kw
 };
 
-// AK: 0 = quad loads of TW (K % 4 == 0), 1 = scalar gather.  TX: x's type.
-template <class C, int AK, typename TW, typename TX>
+// AK: 0 = quad loads of TW (K % 4 == 0), 1 = scalar gather.
+template <class C, int AK, typename TW>
 __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
   const int64_t bz = blockIdx.z;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
@@ -494,17 +486,12 @@ __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
   const int64_t M = A.M, N = A.Lout, K = A.K;
   float* out = A.out + bz * M * N;
   const float* bias = A.bias;
-  const bool out_i32 = A.out_i32;
-  auto store = [&](int64_t m, int64_t n, float v) {
-    if (out_i32) reinterpret_cast<int32_t*>(out)[m * N + n] = __float2int_rn(v);
-    else out[m * N + n] = bias ? v + bias[m] : v;
-  };
-  BIm2col<C, TX> lb;
-  lb.x = static_cast<const TX*>(A.x) + bz * A.Cin * A.L;
-  lb.xzp = A.xzp ? static_cast<float>(*static_cast<const uint8_t*>(A.xzp)) : 0.0f;
+  auto store = [&](int64_t m, int64_t n, float v) { out[m * N + n] = bias ? v + bias[m] : v; };
+  BIm2col<C> lb;
+  lb.x = A.x + bz * A.Cin * A.L;
   lb.L = A.L; lb.Kw = A.Kw; lb.s = A.s; lb.d = A.d; lb.p0 = A.p0; lb.Kdim = K; lb.Lout = N;
-  lb.r0 = threadIdx.x / BIm2col<C, TX>::QPR;
-  lb.l0 = n0 + (threadIdx.x % BIm2col<C, TX>::QPR) * 4;
+  lb.r0 = threadIdx.x / BIm2col<C>::QPR;
+  lb.l0 = n0 + (threadIdx.x % BIm2col<C>::QPR) * 4;
   if constexpr (AK == 0) {
     AQuad<C, TW> la;
     la.init(static_cast<const TW*>(A.w), K, M, K, m0, A.dq);
@@ -871,7 +858,7 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
   if (group == 1) {
     ConvArgs args{};
     args.w = w->data; args.w_dt = w->dtype; args.dq = dq;
-    args.x = x->data;
+    args.x = static_cast<const float*>(x->data);
     args.out = static_cast<float*>(out->data);
     args.bias = bp;
     args.Cin = Cin; args.L = L; args.Kw = K; args.s = stride; args.d = dilation; args.p0 = pad0;
@@ -881,13 +868,13 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
     KK_TRY(check_grid(grid, N));
     const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4 * dtype_size(w->dtype));
     if (!quad) {
-      KK_TILED(conv1d_kernel, ts, grid, 1, float, float);
+      KK_TILED(conv1d_kernel, ts, grid, 1, float);
     } else {
       switch (w->dtype) {
-        case KK_F32: KK_TILED(conv1d_kernel, ts, grid, 0, float, float); break;
-        case KK_F16: KK_TILED(conv1d_kernel, ts, grid, 0, __half, float); break;
-        case KK_I8: KK_TILED(conv1d_kernel, ts, grid, 0, int8_t, float); break;
-        default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t, float); break;
+        case KK_F32: KK_TILED(conv1d_kernel, ts, grid, 0, float); break;
+        case KK_F16: KK_TILED(conv1d_kernel, ts, grid, 0, __half); break;
+        case KK_I8: KK_TILED(conv1d_kernel, ts, grid, 0, int8_t); break;
+        default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t); break;
       }
     }
     return check_launch("conv1d_kernel");
@@ -928,33 +915,16 @@ int kk_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w
   if (out->shape[0] != N || out->shape[1] != Cout || out->shape[2] != Lout)
     return set_error(KK_E_ARG, "kk_conv_integer: out must be [%lld, %lld, %lld]", (long long)N,
                      (long long)Cout, (long long)Lout);
-  ConvArgs args{};
-  KK_TRY(zp_shift(&args.dq, w_zp, Cout, "kk_conv_integer"));
+  Dequant zcheck;
+  KK_TRY(zp_shift(&zcheck, w_zp, Cout, "kk_conv_integer"));
   if (x_zp) {
     KK_TRY(check_tensor(x_zp, "x_zp"));
     if (x_zp->dtype != KK_U8 || numel(x_zp) != 1)
       return set_error(KK_E_ARG, "kk_conv_integer: x_zp must be one uint8");
-    args.xzp = x_zp->data;
   }
   if (N * Cout * Lout == 0) return KK_OK;
-  args.w = w->data; args.w_dt = w->dtype;
-  args.x = x->data;
-  args.out = static_cast<float*>(out->data);
-  args.out_i32 = 1;
-  args.Cin = Cin; args.L = L; args.Kw = K; args.s = stride; args.d = dilation; args.p0 = pad0;
-  args.Lout = Lout; args.M = Cout; args.K = Cin * K;
-  const TileSize ts = pick_tile(Cout, Lout, N);
-  const dim3 grid = grid_of(ts, Cout, Lout, N);
-  KK_TRY(check_grid(grid, N));
-  const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4);
-  if (!quad) {
-    KK_TILED(conv1d_kernel, ts, grid, 1, float, uint8_t);
-  } else if (w->dtype == KK_U8) {
-    KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t, uint8_t);
-  } else {
-    KK_TILED(conv1d_kernel, ts, grid, 0, int8_t, uint8_t);
-  }
-  return check_launch("conv1d_kernel");
+  if (Cin * K == 0) return kk_fill(out, 0.0);
+  return conv_integer_i8(out, x, w, x_zp, w_zp, stride, dilation, pad0, pad1);
 }
 
 int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,

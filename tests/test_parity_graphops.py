@@ -83,11 +83,36 @@ def test_conv_integer(gpu, oracle, cin, cout, k, L, pad, dil):
     r = rng(3)
     x = r.integers(0, 256, (1, cin, L)).astype(np.uint8)
     w = r.integers(0, 256, (cout, cin, k)).astype(np.uint8)
-    xzp, wzp = np.uint8(121), np.uint8(128)
+    xzp, wzp = np.uint8(121), np.uint8(63)
     at = {"pads": [pad, pad], "dilations": [dil], "strides": [1], "group": 1}
     got = node(gpu, "ConvInteger", [x, w, xzp, wzp], at)
     assert_bitexact(got, onode(oracle, "ConvInteger", [x, w, xzp, wzp], at),
                     f"ConvInteger {cin}->{cout} k{k}")
+
+
+@pytest.mark.parametrize("case", ["no_zero_points", "int8_weights", "stride2_batch2", "one_output",
+                                  "zp_extremes"])
+def test_conv_integer_variants(gpu, oracle, case):
+    r = rng(13)
+    n, cin, cout, k, L, pad, stride = 1, 96, 40, 5, 333, 2, 1
+    wdt, xzp, wzp = np.uint8, np.uint8(77), np.uint8(140)
+    if case == "no_zero_points":
+        xzp = wzp = None
+    elif case == "int8_weights":
+        wdt, wzp = np.int8, np.int8(-5)
+    elif case == "stride2_batch2":
+        n, stride = 2, 2
+    elif case == "one_output":
+        L, pad = 5, 0
+    elif case == "zp_extremes":
+        xzp, wzp = np.uint8(255), np.uint8(0)
+    x = r.integers(0, 256, (n, cin, L)).astype(np.uint8)
+    lo, hi = (-128, 128) if wdt == np.int8 else (0, 256)
+    w = r.integers(lo, hi, (cout, cin, k)).astype(wdt)
+    at = {"pads": [pad, pad], "dilations": [1], "strides": [stride], "group": 1}
+    ins = [x, w, xzp, wzp]
+    want = onode(oracle, "ConvInteger", ins, at)
+    assert_bitexact(node(gpu, "ConvInteger", ins, at), want, f"ConvInteger {case}")
 
 
 @pytest.mark.parametrize("seq,inp", [(40, 640), (7, 512), (1, 64)])
