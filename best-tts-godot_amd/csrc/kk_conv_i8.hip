@@ -106,7 +106,11 @@ struct ConvI8Args {
   const int8_t* xT;     // [N][Lp][CinP]
   const int32_t* xs;    // [N][Lp]
   const uint8_t* xzp;   // one uint8 or NULL
-  int32_t* out;         // [N][Cout][Lout]
+  int32_t* out;         // [N][Cout][Lout] int32, or NULL when outf is set
+  float* outf;          // [N][Cout][Lout] float(acc + bias[co]) * scale
+  const int32_t* bias;  // [Cout] or NULL
+  const float* scale;   // 1 or Cout values
+  int64_t scale_n;
   int64_t Cout, CinP, Kw, s, d, Lp, Lout, Kreal;
 };
 
@@ -148,7 +152,7 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
   }
   const int xz = (A.xzp ? static_cast<int>(A.xzp[0]) : 0) - 128;
   const int32_t* xs = A.xs + b * A.Lp;
-  int32_t* out = A.out + b * A.Cout * A.Lout;
+  const int64_t obase = b * A.Cout * A.Lout;
 #pragma unroll
   for (int ni = 0; ni < 2; ++ni) {
     const int64_t l = n0 + 32 * ni + r;
@@ -164,7 +168,13 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
         if (co >= A.Cout) continue;
         const int wz = A.wzo[co];
         const int v = acc[reg] - xz * A.wsum[co] - wz * S + static_cast<int>(A.Kreal) * wz * xz;
-        out[co * A.Lout + l] = v;
+        if (A.outf) {
+          const int vb = A.bias ? v + A.bias[co] : v;
+          A.outf[obase + co * A.Lout + l] =
+              static_cast<float>(vb) * A.scale[A.scale_n > 1 ? co : 0];
+        } else {
+          A.out[obase + co * A.Lout + l] = v;
+        }
       }
     }
   }
@@ -172,22 +182,68 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
 
 }  // namespace
 
-// Called by kk_conv_integer (group 1) after it has validated the operands.
-int conv_integer_i8(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
-                    const kk_tensor* x_zp, const kk_tensor* w_zp, int stride, int dilation,
-                    int pad0, int pad1) {
+// Shapes and zero points of ConvInteger (ref_runtime.py:130-134); fills
+// *Lout.  Both zero points must be per tensor, as the reference reads them
+// with np.int32(zp).
+static int check_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                       const kk_tensor* x_zp, const kk_tensor* w_zp, int stride, int dilation,
+                       int pad0, int pad1, int group, int out_dt, const char* who,
+                       int64_t* lout) {
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(out, "out"));
+  KK_TRY(check_tensor(x, "x"));
+  KK_TRY(check_tensor(w, "w"));
+  if (x->rank != 3 || w->rank != 3 || out->rank != 3)
+    return set_error(KK_E_ARG, "%s: x, w and out must be rank 3", who);
+  if (x->dtype != KK_U8 || !(w->dtype == KK_U8 || w->dtype == KK_I8) || out->dtype != out_dt)
+    return set_error(KK_E_ARG, "%s: x uint8, w uint8/int8, out %s", who,
+                     out_dt == KK_I32 ? "int32" : "fp32");
+  if (!is_contiguous(x) || !is_contiguous(out) || !is_contiguous(w))
+    return set_error(KK_E_ARG, "%s: x, w and out must be contiguous", who);
+  if (group != 1) return set_error(KK_E_UNSUPPORTED, "%s: group %d", who, group);
+  const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
+  const int64_t Cout = w->shape[0], K = w->shape[2];
+  if (w->shape[1] != Cin) return set_error(KK_E_ARG, "%s: w must be [Cout, Cin, K]", who);
+  if (stride < 1 || dilation < 1 || pad0 < 0 || pad1 < 0)
+    return set_error(KK_E_ARG, "%s: bad stride/dilation/pads", who);
+  const int64_t span = static_cast<int64_t>(dilation) * (K - 1) + 1;
+  const int64_t Lp = L + pad0 + pad1;
+  const int64_t Lout = Lp >= span ? (Lp - span) / stride + 1 : 0;
+  if (out->shape[0] != N || out->shape[1] != Cout || out->shape[2] != Lout)
+    return set_error(KK_E_ARG, "%s: out must be [%lld, %lld, %lld]", who, (long long)N,
+                     (long long)Cout, (long long)Lout);
+  if (x_zp) {
+    KK_TRY(check_tensor(x_zp, "x_zp"));
+    if (x_zp->dtype != KK_U8 || numel(x_zp) != 1)
+      return set_error(KK_E_ARG, "%s: x_zp must be one uint8", who);
+  }
+  if (w_zp) {
+    KK_TRY(check_tensor(w_zp, "w_zp"));
+    if (!(w_zp->dtype == KK_U8 || w_zp->dtype == KK_I8 || w_zp->dtype == KK_I32) ||
+        numel(w_zp) != 1)
+      return set_error(KK_E_ARG, "%s: w_zp must be one uint8/int8/int32", who);
+  }
+  // |each epilogue term| <= K * 2^14 must stay clear of 2^31.
+  if (Cin * K > 32768)
+    return set_error(KK_E_UNSUPPORTED, "%s: Cin*K = %lld exceeds 32768", who,
+                     (long long)(Cin * K));
+  if (N > 65535 || ceil_div(Lout, kTileN) > 0x7fffffff)
+    return set_error(KK_E_UNSUPPORTED, "%s: grid too large", who);
+  *lout = Lout;
+  return KK_OK;
+}
+
+// Both entry points: `outf` set gives the scaled fp32 form.
+static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                     const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                     const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
+                     bool outf) {
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], Kw = w->shape[2];
   const int64_t Lp = L + pad0 + pad1;
   const int64_t Lout = out->shape[2];
   const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
   const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
-  // |each epilogue term| <= K * 2^14 must stay clear of 2^31.
-  if (Cin * Kw > 32768)
-    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer: Cin*K = %lld exceeds 32768",
-                     (long long)(Cin * Kw));
-  if (N > 65535 || ceil_div(Lout, kTileN) > 0x7fffffff)
-    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer: grid too large");
   auto up = [](int64_t n) { return ceil_div(n, 256) * 256; };
   const int64_t o_wT = 0, o_wsum = o_wT + up(CoutP * Kw * CinP);
   const int64_t o_wzo = o_wsum + up(CoutP * 4), o_xs = o_wzo + up(CoutP * 4);
@@ -216,7 +272,14 @@ int conv_integer_i8(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w
   if (rc == KK_OK) {
     ConvI8Args A{};
     A.wT = wT; A.wsum = wsum; A.wzo = wzo; A.xT = xT; A.xs = xs; A.xzp = xzp;
-    A.out = static_cast<int32_t*>(out->data);
+    if (outf) {
+      A.outf = static_cast<float*>(out->data);
+      A.bias = bias ? static_cast<const int32_t*>(bias->data) : nullptr;
+      A.scale = static_cast<const float*>(scale->data);
+      A.scale_n = numel(scale);
+    } else {
+      A.out = static_cast<int32_t*>(out->data);
+    }
     A.Cout = Cout; A.CinP = CinP; A.Kw = Kw; A.s = stride; A.d = dilation; A.Lp = Lp;
     A.Lout = Lout; A.Kreal = Cin * Kw;
     const dim3 grid(static_cast<unsigned>(ceil_div(Lout, kTileN)),
@@ -229,3 +292,44 @@ int conv_integer_i8(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w
 }
 
 }  // namespace kk
+
+using namespace kk;
+
+extern "C" {
+
+int kk_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                    const kk_tensor* x_zp, const kk_tensor* w_zp, int stride, int dilation,
+                    int pad0, int pad1, int group) {
+  int64_t Lout = 0;
+  KK_TRY(check_conv_integer(out, x, w, x_zp, w_zp, stride, dilation, pad0, pad1, group, KK_I32,
+                            "kk_conv_integer", &Lout));
+  if (numel(out) == 0) return KK_OK;
+  if (x->shape[1] * w->shape[2] == 0) return kk_fill(out, 0.0);
+  return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
+                          false);
+}
+
+int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                           const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                           const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
+                           int group) {
+  int64_t Lout = 0;
+  KK_TRY(check_conv_integer(out, x, w, x_zp, w_zp, stride, dilation, pad0, pad1, group, KK_F32,
+                            "kk_conv_integer_scaled", &Lout));
+  const int64_t Cout = w->shape[0];
+  KK_TRY(check_tensor(scale, "scale"));
+  if (scale->dtype != KK_F32 || !is_contiguous(scale) ||
+      (numel(scale) != 1 && numel(scale) != Cout))
+    return set_error(KK_E_ARG, "kk_conv_integer_scaled: scale must be fp32 with 1 or Cout values");
+  if (bias) {
+    KK_TRY(check_tensor(bias, "bias"));
+    if (bias->dtype != KK_I32 || !is_contiguous(bias) || numel(bias) != Cout)
+      return set_error(KK_E_ARG, "kk_conv_integer_scaled: bias must be int32 with Cout values");
+  }
+  if (numel(out) == 0) return KK_OK;
+  if (x->shape[1] * w->shape[2] == 0)
+    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer_scaled: empty reduction");
+  return conv_integer_run(out, x, w, x_zp, w_zp, bias, scale, stride, dilation, pad0, pad1, true);
+}
+
+}  // extern "C"

@@ -890,42 +890,6 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
   return check_launch("conv1d_direct_kernel");
 }
 
-int kk_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
-                    const kk_tensor* x_zp, const kk_tensor* w_zp, int stride, int dilation,
-                    int pad0, int pad1, int group) {
-  KK_TRY(require_ready());
-  KK_TRY(check_tensor(out, "out"));
-  KK_TRY(check_tensor(x, "x"));
-  KK_TRY(check_tensor(w, "w"));
-  if (x->rank != 3 || w->rank != 3 || out->rank != 3)
-    return set_error(KK_E_ARG, "kk_conv_integer: x, w and out must be rank 3");
-  if (x->dtype != KK_U8 || !(w->dtype == KK_U8 || w->dtype == KK_I8) || out->dtype != KK_I32)
-    return set_error(KK_E_ARG, "kk_conv_integer: x uint8, w uint8/int8, out int32");
-  if (!is_contiguous(x) || !is_contiguous(out) || !is_contiguous(w))
-    return set_error(KK_E_ARG, "kk_conv_integer: x, w and out must be contiguous");
-  if (group != 1) return set_error(KK_E_UNSUPPORTED, "kk_conv_integer: group %d", group);
-  const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
-  const int64_t Cout = w->shape[0], K = w->shape[2];
-  if (w->shape[1] != Cin) return set_error(KK_E_ARG, "kk_conv_integer: w must be [Cout, Cin, K]");
-  if (stride < 1 || dilation < 1 || pad0 < 0 || pad1 < 0)
-    return set_error(KK_E_ARG, "kk_conv_integer: bad stride/dilation/pads");
-  const int64_t span = static_cast<int64_t>(dilation) * (K - 1) + 1;
-  const int64_t Lp = L + pad0 + pad1;
-  const int64_t Lout = Lp >= span ? (Lp - span) / stride + 1 : 0;
-  if (out->shape[0] != N || out->shape[1] != Cout || out->shape[2] != Lout)
-    return set_error(KK_E_ARG, "kk_conv_integer: out must be [%lld, %lld, %lld]", (long long)N,
-                     (long long)Cout, (long long)Lout);
-  Dequant zcheck;
-  KK_TRY(zp_shift(&zcheck, w_zp, Cout, "kk_conv_integer"));
-  if (x_zp) {
-    KK_TRY(check_tensor(x_zp, "x_zp"));
-    if (x_zp->dtype != KK_U8 || numel(x_zp) != 1)
-      return set_error(KK_E_ARG, "kk_conv_integer: x_zp must be one uint8");
-  }
-  if (N * Cout * Lout == 0) return KK_OK;
-  if (Cin * K == 0) return kk_fill(out, 0.0);
-  return conv_integer_i8(out, x, w, x_zp, w_zp, stride, dilation, pad0, pad1);
-}
 
 int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
                         const kk_tensor* w_scale, const kk_tensor* w_zp, const kk_tensor* bias,

@@ -148,10 +148,6 @@ __device__ __forceinline__ float dequant_value(float q, const Dequant& d,
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// ConvInteger (group 1) on the int8 matrix cores; operands validated by the
-// caller, out [N, Cout, Lout] int32 non-empty.
-int conv_integer_i8(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
-                    const kk_tensor* x_zp, const kk_tensor* w_zp, int stride, int dilation,
-                    int pad0, int pad1);
+
 
 }  // namespace kk

@@ -152,13 +152,52 @@ __device__ __forceinline__ void style_affine(const StyleArgs& sa, int64_t C, int
   beta = ab;
 }
 
-// mode 0: no affine; 1: gamma/beta from `gb` ([2C]); 2: from the style Linear.
+// Per-channel affine applied after the normalisation, and an optional
+// LeakyRelu:
+//   mode 0: y = q
+//   mode 1: y = q * (gamma[c] + 1) + beta[c], gb = [gamma | beta] (2C)
+//   mode 2: the same with (gamma, beta) = style . W + b computed in-kernel
+//   mode 3: y = q * scale[c] + shift[c] (either may be NULL: 1 / 0), the
+//           Mul/Add tail of the graph's InstanceNorm chain
+// then, if leaky, y = y < 0 ? y * alpha : y (ref_runtime.py:476-479).
+struct Affine {
+  int mode;
+  const float* gb;
+  const float* scale;
+  const float* shift;
+  int leaky;
+  float alpha;
+};
+
+struct RowAffine {
+  float mul, add;
+  bool has_mul, has_add;
+};
+
+__device__ __forceinline__ RowAffine row_affine(const Affine& af, int64_t C, int64_t c, float gamma,
+                                                float beta) {
+  RowAffine ra{1.0f, 0.0f, false, false};
+  if (af.mode == 1 || af.mode == 2) {
+    ra.mul = gamma + 1.0f; ra.add = beta; ra.has_mul = ra.has_add = true;
+  } else if (af.mode == 3) {
+    if (af.scale) { ra.mul = af.scale[c]; ra.has_mul = true; }
+    if (af.shift) { ra.add = af.shift[c]; ra.has_add = true; }
+  }
+  return ra;
+}
+
+__device__ __forceinline__ float apply_affine(float q, const RowAffine& ra, const Affine& af) {
+  float y = ra.has_mul ? q * ra.mul : q;
+  if (ra.has_add) y = y + ra.add;
+  if (af.leaky) y = y < 0.0f ? y * af.alpha : y;
+  return y;
+}
+
 template <int GROUP, int NV, int VEC>
 __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__ out,
                                                              const float* __restrict__ x,
                                                              int64_t rows, int64_t C, int64_t T,
-                                                             float eps, int mode,
-                                                             const float* __restrict__ gb,
+                                                             float eps, Affine af,
                                                              StyleArgs sa) {
   __shared__ float lds[4];
   constexpr int RPB = kRowBlock / GROUP;
@@ -177,19 +216,16 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
   float r[NV][VEC];
   load_row<GROUP, NV, VEC>(xr, T, g, r);
   float gamma = 0.0f, beta = 0.0f;
-  if (mode == 2) style_affine<GROUP>(sa, C, c, g, lds, gamma, beta);
-  else if (mode == 1) { gamma = gb[c]; beta = gb[C + c]; }
+  if (af.mode == 2) style_affine<GROUP>(sa, C, c, g, lds, gamma, beta);
+  else if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
+  const RowAffine ra = row_affine(af, C, c, gamma, beta);
   float mean, var;
   row_stats<GROUP, NV, VEC>(r, T, g, lds, mean, var);
   const float den = sqrtf(var + eps);
-  const float g1 = gamma + 1.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      const float q = r[j][e] / den;
-      r[j][e] = mode ? (q * g1) + beta : q;
-    }
+    for (int e = 0; e < VEC; ++e) r[j][e] = apply_affine(r[j][e] / den, ra, af);
   store_row<GROUP, NV, VEC>(out + row * T, T, g, r);
 }
 
@@ -197,16 +233,15 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
 __global__ void __launch_bounds__(kRowBlock) instnorm_long_kernel(float* __restrict__ out,
                                                                   const float* __restrict__ x,
                                                                   int64_t C, int64_t T, float eps,
-                                                                  int mode,
-                                                                  const float* __restrict__ gb,
-                                                                  StyleArgs sa) {
+                                                                  Affine af, StyleArgs sa) {
   __shared__ float lds[4];
   const int g = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t c = row % C;
   float gamma = 0.0f, beta = 0.0f;
-  if (mode == 2) style_affine<kRowBlock>(sa, C, c, g, lds, gamma, beta);
-  else if (mode == 1) { gamma = gb[c]; beta = gb[C + c]; }
+  if (af.mode == 2) style_affine<kRowBlock>(sa, C, c, g, lds, gamma, beta);
+  else if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
+  const RowAffine ra = row_affine(af, C, c, gamma, beta);
   const float* xr = x + row * T;
   float s = 0.0f;
   for (int64_t i = g; i < T; i += kRowBlock) s += xr[i];
@@ -218,11 +253,39 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_long_kernel(float* __restr
   }
   const float var = group_sum<kRowBlock>(q, lds) / static_cast<float>(T);
   const float den = sqrtf(var + eps);
-  const float g1 = gamma + 1.0f;
   float* orow = out + row * T;
-  for (int64_t i = g; i < T; i += kRowBlock) {
-    const float v = (xr[i] - mean) / den;
-    orow[i] = mode ? (v * g1) + beta : v;
+  for (int64_t i = g; i < T; i += kRowBlock) orow[i] = apply_affine((xr[i] - mean) / den, ra, af);
+}
+
+// Applies y = affine((x - mean) / den) with per-row (mean, den) from the
+// numpy-order statistics kernels below (long rows).
+__global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ out,
+                                                            const float* __restrict__ x,
+                                                            const float2* __restrict__ stats,
+                                                            int64_t C, int64_t T, Affine af,
+                                                            int vec) {
+  const int64_t row = blockIdx.y;
+  const int64_t c = row % C;
+  float gamma = 0.0f, beta = 0.0f;
+  if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
+  const RowAffine ra = row_affine(af, C, c, gamma, beta);
+  const float2 st = stats[row];
+  const float* xr = x + row * T;
+  float* orow = out + row * T;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  if (vec) {
+    for (int64_t i = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) * 4; i < T;
+         i += stride * 4) {
+      const float4 v = ld_stream4(xr + i);
+      st_stream4(orow + i, make_float4(apply_affine((v.x - st.x) / st.y, ra, af),
+                                       apply_affine((v.y - st.x) / st.y, ra, af),
+                                       apply_affine((v.z - st.x) / st.y, ra, af),
+                                       apply_affine((v.w - st.x) / st.y, ra, af)));
+    }
+  } else {
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < T;
+         i += stride)
+      st_stream(orow + i, apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af));
   }
 }
 
@@ -419,79 +482,260 @@ __global__ void __launch_bounds__(kRowBlock) reduce_rows_kernel(float* __restric
   if (g == 0) out[row] = v;
 }
 
-// Split-row reduction for long trailing rows (the decoder's InstanceNorm
-// means over T = 10^4..10^6 samples with only 128..512 rows): block
-// (c, row) reduces chunk c of the row into part[row * nchunk + c], then one
-// wave per row folds the partials in chunk order.  Both stages use fixed
-// orders, so the result does not depend on scheduling.
-constexpr int64_t kChunk = 8192;
+// ------------------------------------------------- numpy-order summation
+// numpy reduces a float32 row (np.sum / np.mean over a contiguous axis, as
+// every ReduceMean/ReduceSum of the graph and the InstanceNorm statistics
+// do) as
+//   acc = 0; for each 8192-element block of the row, in order: acc += pw(block)
+// where 8192 is the ufunc buffer size and pw is numpy's pairwise_sum
+// (numpy/_core/src/umath/loops_utils.h.src):
+//   n < 8:     sequential from 0
+//   n <= 128:  eight strided accumulators r[j] += a[i + j], combined as
+//              ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)), then the
+//              n % 8 tail added in order
+//   else:      pw(a, n2) + pw(a + n2, n - n2), n2 = n / 2 rounded down to a
+//              multiple of 8.
+// The kernels below evaluate exactly this tree, so their sums and means
+// carry numpy's roundings bit for bit.  A 512-thread block owns one 8192
+// block: eight lanes per leaf (a full block has 64 leaves of 128 in a
+// balanced tree, reduced with shuffles and an 8-entry LDS step); a partial
+// block (a row's tail) enumerates its leaves and evaluates its tree in one
+// thread.  Rows sit in LDS padded by 8 floats per 128, which puts the 64
+// lanes of a leaf step on 64 distinct banks.
+constexpr int kNpBlock = 8192;
+constexpr int kNpLeaf = 128;
+constexpr int kNpThreads = 512;
+constexpr int kNpMaxLeaves = 72;  // at most 65 leaves for n <= 8192
+constexpr int kNpDepth = 8;       // the recursion is at most 7 deep for n <= 8192
 
-template <bool VEC>
-__global__ void __launch_bounds__(kRowBlock) reduce_chunks_kernel(float* __restrict__ part,
-                                                                  const float* __restrict__ x,
-                                                                  int64_t cols, int nchunk,
-                                                                  int op) {
-  __shared__ float lds[4];
-  const int64_t row = blockIdx.y;
-  const int c = blockIdx.x;
-  const float* xr = x + row * cols;
-  const int64_t lo = static_cast<int64_t>(c) * kChunk;
-  const int64_t hi = lo + kChunk < cols ? lo + kChunk : cols;
-  const bool is_max = op == KK_REDUCE_MAX;
-  float acc = is_max ? -INFINITY : 0.0f;
-  bool nan = false;
-  if constexpr (VEC) {
-#pragma unroll 4
-    for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * kRowBlock) {
-      const float4 v = ld_stream4(xr + i);
-      if (is_max) {
-        nan |= __builtin_isnan(v.x) | __builtin_isnan(v.y) | __builtin_isnan(v.z) |
-               __builtin_isnan(v.w);
-        acc = fmaxf(fmaxf(acc, v.x), fmaxf(v.y, fmaxf(v.z, v.w)));
-      } else {
-        acc += (v.x + v.y) + (v.z + v.w);
-      }
-    }
+__device__ __forceinline__ int np_pad(int e) { return e + 8 * (e >> 7); }
+
+struct NpScratch {
+  int lo[kNpMaxLeaves], n[kNpMaxLeaves];
+  float sum[kNpMaxLeaves];
+  float wave[kNpThreads / 64];
+  int count;
+  float total;
+};
+
+template <int D>
+__device__ void np_leaves(int lo, int n, int& k, NpScratch& S) {
+  if constexpr (D == 0) {
+    S.lo[k] = lo; S.n[k] = n; ++k;
   } else {
-#pragma unroll 4
-    for (int64_t i = lo + threadIdx.x; i < hi; i += kRowBlock) {
-      const float v = ld_stream(xr + i);
-      if (is_max) { nan |= __builtin_isnan(v); acc = fmaxf(acc, v); }
-      else acc += v;
-    }
+    if (n <= kNpLeaf) { S.lo[k] = lo; S.n[k] = n; ++k; return; }
+    int n2 = n / 2;
+    n2 -= n2 % 8;
+    np_leaves<D - 1>(lo, n2, k, S);
+    np_leaves<D - 1>(lo + n2, n - n2, k, S);
   }
-  float v;
-  if (is_max) {
-    v = group_max<kRowBlock>(acc, lds);
-    if (group_max<kRowBlock>(nan ? 1.0f : 0.0f, lds) > 0.0f) v = NAN;
-  } else {
-    v = group_sum<kRowBlock>(acc, lds);
-  }
-  if (threadIdx.x == 0) part[row * nchunk + c] = v;
 }
 
-__global__ void __launch_bounds__(kRowBlock) reduce_fold_kernel(float* __restrict__ out,
-                                                                const float* __restrict__ part,
-                                                                int64_t rows, int nchunk,
-                                                                int64_t cols, int op) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kRowBlock / 64) + threadIdx.x / 64;
-  const int lane = threadIdx.x & 63;
-  if (row >= rows) return;
-  const float* p = part + row * nchunk;
-  float v;
-  if (op == KK_REDUCE_MAX) {
-    float m = -INFINITY;
-    bool nan = false;
-    for (int c = lane; c < nchunk; c += 64) { nan |= __builtin_isnan(p[c]); m = fmaxf(m, p[c]); }
-    m = wave_max(m);
-    v = wave_max(nan ? 1.0f : 0.0f) > 0.0f ? NAN : m;
+template <int D>
+__device__ float np_tree(int n, int& k, const NpScratch& S) {
+  if constexpr (D == 0) {
+    return S.sum[k++];
   } else {
-    float s = 0.0f;
-    for (int c = lane; c < nchunk; c += 64) s += p[c];
-    s = wave_sum(s);
-    v = op == KK_REDUCE_MEAN ? s / static_cast<float>(cols) : s;
+    if (n <= kNpLeaf) return S.sum[k++];
+    int n2 = n / 2;
+    n2 -= n2 % 8;
+    const float a = np_tree<D - 1>(n2, k, S);
+    const float b = np_tree<D - 1>(n - n2, k, S);
+    return a + b;
   }
-  if (lane == 0) out[row] = v;
+}
+
+// numpy's pairwise sum of f(i), i in [0, m), 1 <= m <= 8192, by a whole
+// 512-thread block; every thread returns the sum.  f reads LDS or computes.
+template <class F>
+__device__ float np_block_sum(F f, int m, NpScratch& S) {
+  const int q = threadIdx.x >> 3, j = threadIdx.x & 7;
+  if (m == kNpBlock) {
+    float r = f(q * kNpLeaf + j);
+#pragma unroll
+    for (int i = 8; i < kNpLeaf; i += 8) r += f(q * kNpLeaf + i + j);
+    r += __shfl_xor(r, 1, 64);   // leaf q: ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
+    r += __shfl_xor(r, 2, 64);
+    r += __shfl_xor(r, 4, 64);
+    r += __shfl_xor(r, 8, 64);   // leaves 8w .. 8w+7 of wave w, balanced
+    r += __shfl_xor(r, 16, 64);
+    r += __shfl_xor(r, 32, 64);
+    if ((threadIdx.x & 63) == 0) S.wave[threadIdx.x >> 6] = r;
+    __syncthreads();
+    const float s = ((S.wave[0] + S.wave[1]) + (S.wave[2] + S.wave[3])) +
+                    ((S.wave[4] + S.wave[5]) + (S.wave[6] + S.wave[7]));
+    __syncthreads();
+    return s;
+  }
+  if (threadIdx.x == 0) {
+    int k = 0;
+    np_leaves<kNpDepth>(0, m, k, S);
+    S.count = k;
+  }
+  __syncthreads();
+  for (int base = 0; base < S.count; base += kNpThreads / 8) {
+    const int leaf = base + q;
+    if (leaf < S.count) {  // uniform over the leaf's eight lanes
+      const int lo = S.lo[leaf], n = S.n[leaf];
+      float res = 0.0f;
+      if (n < 8) {
+        if (j == 0)
+          for (int i = 0; i < n; ++i) res += f(lo + i);
+      } else {
+        const int body = n - n % 8;
+        float r = f(lo + j);
+        for (int i = 8; i < body; i += 8) r += f(lo + i + j);
+        r += __shfl_xor(r, 1, 64);
+        r += __shfl_xor(r, 2, 64);
+        r += __shfl_xor(r, 4, 64);
+        res = r;
+        if (j == 0)
+          for (int i = body; i < n; ++i) res += f(lo + i);
+      }
+      if (j == 0) S.sum[leaf] = res;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int k = 0;
+    S.total = np_tree<kNpDepth>(m, k, S);
+  }
+  __syncthreads();
+  const float s = S.total;
+  __syncthreads();
+  return s;
+}
+
+// Loads elements [0, n) of `src` into the padded LDS row `dst`.
+__device__ __forceinline__ void np_load_row(float* dst, const float* __restrict__ src, int64_t n,
+                                            bool vec) {
+  if (vec) {
+    for (int64_t e = 4 * threadIdx.x; e < n; e += 4 * kNpThreads) {
+      const float4 v = ld_stream4(src + e);
+      *reinterpret_cast<float4*>(dst + np_pad(static_cast<int>(e))) = v;
+    }
+  } else {
+    for (int64_t e = threadIdx.x; e < n; e += kNpThreads) dst[np_pad(static_cast<int>(e))] = ld_stream(src + e);
+  }
+}
+
+// numpy-order sum of the padded LDS row (n elements) of f(x), acc from 0.
+template <class F>
+__device__ float np_row_sum(const float* row, int n, F f, NpScratch& S) {
+  float acc = 0.0f;
+  for (int b0 = 0; b0 < n; b0 += kNpBlock) {
+    const int m = n - b0 < kNpBlock ? n - b0 : kNpBlock;
+    acc += np_block_sum([&](int i) { return f(row[np_pad(b0 + i)]); }, m, S);
+  }
+  return acc;
+}
+
+// Rows of at most 2 x 8192 elements, one block per row, the row in LDS.
+//   mode 0: out[row] = sum       mode 1: out[row] = sum / n
+//   mode 2: instance norm of the row with the affine `af` into out
+__global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__ out,
+                                                             const float* __restrict__ x,
+                                                             int64_t C, int n, int mode,
+                                                             float eps, Affine af, int vec) {
+  extern __shared__ __align__(16) float np_lds[];
+  __shared__ NpScratch S;
+  const int64_t row = blockIdx.x;
+  const float* xr = x + row * n;
+  np_load_row(np_lds, xr, n, vec);
+  __syncthreads();
+  const float sum = np_row_sum(np_lds, n, [](float v) { return v; }, S);
+  if (mode < 2) {
+    if (threadIdx.x == 0) out[row] = mode == 1 ? sum / static_cast<float>(n) : sum;
+    return;
+  }
+  const float mean = sum / static_cast<float>(n);
+  const float sq = np_row_sum(np_lds, n, [mean](float v) { const float d = v - mean; return d * d; },
+                              S);
+  const float den = sqrtf(sq / static_cast<float>(n) + eps);
+  const int64_t c = row % C;
+  float gamma = 0.0f, beta = 0.0f;
+  if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
+  const RowAffine ra = row_affine(af, C, c, gamma, beta);
+  float* orow = out + row * n;
+  if (vec) {
+    for (int e = 4 * threadIdx.x; e < n; e += 4 * kNpThreads) {
+      const float4 v = *reinterpret_cast<const float4*>(np_lds + np_pad(e));
+      st_stream4(orow + e, make_float4(apply_affine((v.x - mean) / den, ra, af),
+                                       apply_affine((v.y - mean) / den, ra, af),
+                                       apply_affine((v.z - mean) / den, ra, af),
+                                       apply_affine((v.w - mean) / den, ra, af)));
+    }
+  } else {
+    for (int e = threadIdx.x; e < n; e += kNpThreads)
+      st_stream(orow + e, apply_affine((np_lds[np_pad(e)] - mean) / den, ra, af));
+  }
+}
+
+// Long rows: block (b, row) computes pw of 8192-block b of f(x) into
+// part[row][b]; f is x (mode 0) or (x - mean[row])^2 (mode 1, mean from
+// stats[row].x).
+__global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(float* __restrict__ part,
+                                                               const float* __restrict__ x,
+                                                               int64_t T, int nblk, int mode,
+                                                               const float2* __restrict__ stats,
+                                                               int vec) {
+  __shared__ __align__(16) float lds[kNpBlock + kNpBlock / 16];
+  __shared__ NpScratch S;
+  const int64_t row = blockIdx.y;
+  const int b = blockIdx.x;
+  const int64_t lo = static_cast<int64_t>(b) * kNpBlock;
+  const int m = static_cast<int>(T - lo < kNpBlock ? T - lo : kNpBlock);
+  np_load_row(lds, x + row * T + lo, m, vec);
+  __syncthreads();
+  float s;
+  if (mode == 0) {
+    s = np_block_sum([&](int i) { return lds[np_pad(i)]; }, m, S);
+  } else {
+    const float mean = stats[row].x;
+    s = np_block_sum([&](int i) { const float d = lds[np_pad(i)] - mean; return d * d; }, m, S);
+  }
+  if (threadIdx.x == 0) part[row * nblk + b] = s;
+}
+
+// Rows of at most 128 elements (one numpy leaf), one thread per row.
+__global__ void np_leaf_rows_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                    int64_t rows, int n, int mean) {
+  const int64_t row = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (row >= rows) return;
+  const float* a = x + row * n;
+  float res = 0.0f;
+  if (n < 8) {
+    for (int i = 0; i < n; ++i) res += a[i];
+  } else {
+    float r[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = a[j];
+    const int body = n - n % 8;
+    for (int i = 8; i < body; i += 8)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) r[j] += a[i + j];
+    res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    for (int i = body; i < n; ++i) res += a[i];
+  }
+  res = 0.0f + res;  // the reduction's accumulator starts at 0
+  out[row] = mean ? res / static_cast<float>(n) : res;
+}
+
+// acc = 0; acc += part[row][b] in block order; then
+//   mode 0: out[row] = acc          mode 1: out[row] = acc / T
+//   mode 2: stats[row].x = acc / T  mode 3: stats[row].y = sqrt(acc / T + eps)
+__global__ void np_fold_kernel(float* __restrict__ out, float2* __restrict__ stats,
+                               const float* __restrict__ part, int64_t rows, int nblk,
+                               int64_t T, int mode, float eps) {
+  const int64_t row = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (row >= rows) return;
+  float acc = 0.0f;
+  for (int b = 0; b < nblk; ++b) acc += part[row * nblk + b];
+  const float n = static_cast<float>(T);
+  if (mode == 0) out[row] = acc;
+  else if (mode == 1) out[row] = acc / n;
+  else if (mode == 2) stats[row].x = acc / n;
+  else stats[row].y = sqrtf(acc / n + eps);
 }
 
 // General reduction: kept axes (kdims/kst) index the output in order,
@@ -512,7 +756,7 @@ __global__ void reduce_generic_kernel(float* __restrict__ out, const float* __re
       base += (rem % R.kdims[d]) * R.kst[d];
       rem /= R.kdims[d];
     }
-    double s = 0.0;
+    float s = 0.0f;  // numpy sums a non-contiguous axis in order, in fp32
     float m = -INFINITY;
     bool nan = false;
     for (int64_t j = 0; j < R.nred; ++j) {
@@ -528,8 +772,8 @@ __global__ void reduce_generic_kernel(float* __restrict__ out, const float* __re
     }
     float v;
     if (op == KK_REDUCE_MAX) v = nan ? NAN : m;
-    else if (op == KK_REDUCE_MEAN) v = static_cast<float>(s) / static_cast<float>(R.nred);
-    else v = static_cast<float>(s);
+    else if (op == KK_REDUCE_MEAN) v = s / static_cast<float>(R.nred);
+    else v = s;
     out[t] = v;
   }
 }
@@ -611,8 +855,93 @@ static bool same_shape(const kk_tensor* a, const kk_tensor* b) {
   return true;
 }
 
-static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, int mode,
-                           const float* gb, const StyleArgs& sa) {
+constexpr int64_t kNpRowMax = 15000;  // rows held in LDS (<= 64 KB with padding)
+
+static size_t np_row_lds(int64_t n) {
+  return sizeof(float) * static_cast<size_t>(n + 8 * ceil_div(n, kNpLeaf));
+}
+
+// Sum / mean of rows of x (rows x n, contiguous) in numpy's order.
+static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, bool mean,
+                          bool vec) {
+  hipStream_t st = ctx().stream;
+  if (n <= kNpLeaf) {
+    hipLaunchKernelGGL(np_leaf_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 256))),
+                       dim3(256), 0, st, out, x, rows, static_cast<int>(n), mean ? 1 : 0);
+    return check_launch("np_leaf_rows_kernel");
+  }
+  if (n <= kNpRowMax) {
+    Affine af{};
+    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
+                       np_row_lds(n), st, out, x, int64_t{1}, static_cast<int>(n), mean ? 1 : 0,
+                       0.0f, af, vec ? 1 : 0);
+    return check_launch("np_rows_kernel");
+  }
+  if (rows > 65535) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)rows);
+  const int64_t nblk = ceil_div(n, kNpBlock);
+  void* part = nullptr;
+  KK_TRY(kk_alloc(sizeof(float) * rows * nblk, &part));
+  hipLaunchKernelGGL(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
+                     dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
+                     static_cast<int>(nblk), 0, static_cast<const float2*>(nullptr), vec ? 1 : 0);
+  int rc = check_launch("np_blocks_kernel");
+  if (rc == KK_OK) {
+    hipLaunchKernelGGL(np_fold_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 64))), dim3(64), 0,
+                       st, out, static_cast<float2*>(nullptr), static_cast<const float*>(part), rows,
+                       static_cast<int>(nblk), n, mean ? 1 : 0, 0.0f);
+    rc = check_launch("np_fold_kernel");
+  }
+  kk_free(part);  // stream order keeps it alive for the fold
+  return rc;
+}
+
+// Instance norm with the statistics in numpy's order (modes 0, 1, 3).
+static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, int64_t C,
+                       int64_t T, float eps, const Affine& af, bool vec_ok) {
+  hipStream_t st = ctx().stream;
+  const float* xp = static_cast<const float*>(x->data);
+  if (T <= kNpRowMax) {
+    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
+                       np_row_lds(T), st, static_cast<float*>(out->data), xp, C,
+                       static_cast<int>(T), 2, eps, af, vec_ok ? 1 : 0);
+    return check_launch("np_rows_kernel");
+  }
+  if (rows > 65535) return set_error(KK_E_UNSUPPORTED, "instance norm: %lld long rows",
+                                     (long long)rows);
+  const int64_t nblk = ceil_div(T, kNpBlock);
+  const int64_t part_bytes = ceil_div(static_cast<int64_t>(sizeof(float)) * rows * nblk, 256) * 256;
+  void* ws = nullptr;
+  KK_TRY(kk_alloc(static_cast<size_t>(part_bytes + sizeof(float2) * rows), &ws));
+  float* part = static_cast<float*>(ws);
+  float2* stats = reinterpret_cast<float2*>(static_cast<char*>(ws) + part_bytes);
+  const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
+  const dim3 fgrid(static_cast<unsigned>(ceil_div(rows, 64)));
+  int rc = KK_OK;
+  for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
+    hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
+                       static_cast<int>(nblk), pass, static_cast<const float2*>(stats),
+                       vec_ok ? 1 : 0);
+    rc = check_launch("np_blocks_kernel");
+    if (rc != KK_OK) break;
+    hipLaunchKernelGGL(np_fold_kernel, fgrid, dim3(64), 0, st, static_cast<float*>(nullptr), stats,
+                       static_cast<const float*>(part), rows, static_cast<int>(nblk), T, 2 + pass,
+                       eps);
+    rc = check_launch("np_fold_kernel");
+  }
+  if (rc == KK_OK) {
+    const int64_t per_block = kRowBlock * (vec_ok ? 4 : 1) * 8;
+    const unsigned gx = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(
+        ceil_div(T, per_block), 1 << 16)));
+    hipLaunchKernelGGL(instnorm_apply, dim3(gx, static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
+                       st, static_cast<float*>(out->data), xp, stats, C, T, af, vec_ok ? 1 : 0);
+    rc = check_launch("instnorm_apply");
+  }
+  kk_free(ws);  // stream order keeps it alive for the kernels above
+  return rc;
+}
+
+static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, const Affine& af,
+                           const StyleArgs& sa) {
   if (x->rank < 2) return set_error(KK_E_ARG, "instance norm: x must be [N, C, ...T]");
   const int64_t T = x->shape[x->rank - 1];
   const int64_t C = x->shape[x->rank - 2];
@@ -620,13 +949,14 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
   if (numel(x) == 0) return KK_OK;
   RowShape rs;
   const bool vec_ok = (T % 4 == 0) && aligned16(x->data) && aligned16(out->data);
+  if (af.mode != 2) return instnorm_np(out, x, rows, C, T, eps, af, vec_ok);
   if (pick_row_shape(T, vec_ok, &rs)) {
     KK_ROW_DISPATCH(instnorm_kernel, rs, rows, static_cast<float*>(out->data),
-                    static_cast<const float*>(x->data), rows, C, T, eps, mode, gb, sa);
+                    static_cast<const float*>(x->data), rows, C, T, eps, af, sa);
   } else {
     hipLaunchKernelGGL(instnorm_long_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
                        ctx().stream, static_cast<float*>(out->data),
-                       static_cast<const float*>(x->data), C, T, eps, mode, gb, sa);
+                       static_cast<const float*>(x->data), C, T, eps, af, sa);
   }
   return check_launch("instnorm_kernel");
 }
@@ -653,7 +983,35 @@ int kk_instance_norm_affine(const kk_tensor* out, const kk_tensor* x, const kk_t
     gb = static_cast<const float*>(gamma_beta->data);
   }
   StyleArgs sa{};
-  return instnorm_launch(out, x, eps, gb ? 1 : 0, gb, sa);
+  Affine af{};
+  af.mode = gb ? 1 : 0;
+  af.gb = gb;
+  return instnorm_launch(out, x, eps, af, sa);
+}
+
+int kk_instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x, const kk_tensor* scale,
+                                 const kk_tensor* shift, float eps, int leaky, float alpha) {
+  KK_TRY(require_ready());
+  KK_TRY(check_f32_contig(x, "x"));
+  KK_TRY(check_f32_contig(out, "out"));
+  if (!same_shape(out, x)) return set_error(KK_E_ARG, "instance norm: out shape must equal x");
+  if (x->rank < 2) return set_error(KK_E_ARG, "instance norm: x must be [N, C, ...T]");
+  const int64_t C = x->shape[x->rank - 2];
+  Affine af{};
+  af.mode = 3;
+  af.leaky = leaky ? 1 : 0;
+  af.alpha = alpha;
+  for (const kk_tensor* t : {scale, shift}) {
+    if (!t) continue;
+    KK_TRY(check_f32_contig(t, t == scale ? "scale" : "shift"));
+    if (numel(t) != C)
+      return set_error(KK_E_ARG, "instance norm: scale/shift need C = %lld elements",
+                       (long long)C);
+  }
+  af.scale = scale ? static_cast<const float*>(scale->data) : nullptr;
+  af.shift = shift ? static_cast<const float*>(shift->data) : nullptr;
+  StyleArgs sa{};
+  return instnorm_launch(out, x, eps, af, sa);
 }
 
 int kk_adain(const kk_tensor* out, const kk_tensor* x, const kk_tensor* style, const kk_tensor* w,
@@ -685,7 +1043,9 @@ int kk_adain(const kk_tensor* out, const kk_tensor* x, const kk_tensor* style, c
     if (numel(bias) != 2 * C) return set_error(KK_E_ARG, "adain: bias needs 2C elements");
     sa.bias = static_cast<const float*>(bias->data);
   }
-  return instnorm_launch(out, x, eps, 2, nullptr, sa);
+  Affine af{};
+  af.mode = 2;
+  return instnorm_launch(out, x, eps, af, sa);
 }
 
 int kk_layernorm(const kk_tensor* out, const kk_tensor* x, const kk_tensor* skip,
@@ -809,31 +1169,9 @@ int kk_reduce(int op, const kk_tensor* out, const kk_tensor* x, uint32_t axes_ma
   }
   RowShape rs;
   const bool vec_ok = (nred % 4 == 0) && aligned16(x->data);
-  if (trailing && nred > 2 * kChunk) {
-    const int64_t nchunk = ceil_div(nred, kChunk);
-    if (nout > 65535) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)nout);
-    void* part = nullptr;
-    KK_TRY(kk_alloc(sizeof(float) * nout * nchunk, &part));
-    const dim3 grid(static_cast<unsigned>(nchunk), static_cast<unsigned>(nout));
-    if (vec_ok)
-      hipLaunchKernelGGL(reduce_chunks_kernel<true>, grid, dim3(kRowBlock), 0, ctx().stream,
-                         static_cast<float*>(part), static_cast<const float*>(x->data), nred,
-                         static_cast<int>(nchunk), op);
-    else
-      hipLaunchKernelGGL(reduce_chunks_kernel<false>, grid, dim3(kRowBlock), 0, ctx().stream,
-                         static_cast<float*>(part), static_cast<const float*>(x->data), nred,
-                         static_cast<int>(nchunk), op);
-    int rc = check_launch("reduce_chunks_kernel");
-    if (rc == KK_OK) {
-      const unsigned g = static_cast<unsigned>(ceil_div(nout, kRowBlock / 64));
-      hipLaunchKernelGGL(reduce_fold_kernel, dim3(g), dim3(kRowBlock), 0, ctx().stream,
-                         static_cast<float*>(out->data), static_cast<const float*>(part), nout,
-                         static_cast<int>(nchunk), nred, op);
-      rc = check_launch("reduce_fold_kernel");
-    }
-    kk_free(part);  // stream order keeps it alive for the fold
-    return rc;
-  }
+  if (trailing && op != KK_REDUCE_MAX)
+    return np_reduce_rows(static_cast<float*>(out->data), static_cast<const float*>(x->data), nout,
+                          nred, op == KK_REDUCE_MEAN, vec_ok);
   if (trailing && pick_row_shape(nred, vec_ok, &rs)) {
     KK_ROW_DISPATCH(reduce_rows_kernel, rs, nout, static_cast<float*>(out->data),
                     static_cast<const float*>(x->data), nout, nred, op);

@@ -334,6 +334,20 @@ def dispatch(op, node_input, node_output, at, env):
     elif op == "Snake":
         # x + recip * sin(alpha * x)^2: the Mul/Sin/Pow/Mul/Add chain fused.
         out = ops.snake(to_device(x), to_device(y), to_device(inp(2)))
+    elif op == "QConvScaled":
+        # ConvInteger -> Add(int32 bias) -> Cast(float) -> Mul(scale), fused;
+        # inputs x, w, x_zp, w_zp, bias ("" if absent), scale.
+        out = ops.conv_integer_scaled(to_device(x), to_device(y), to_device(inp(2)),
+                                      to_device(inp(3)), to_device(inp(4)),
+                                      _f32(to_device(inp(5))), at.get("pads", [0, 0]),
+                                      at.get("strides", [1])[0], at.get("dilations", [1])[0],
+                                      at.get("group", 1))
+    elif op == "InstanceNormScaleShift":
+        # ReduceMean/Sub/Mul/ReduceMean/Add/Sqrt/Div [-> Mul -> Add -> LeakyRelu], fused;
+        # inputs x, scale ("" if absent), shift ("" if absent).
+        out = ops.instance_norm_scale_shift(_f32(to_device(x)), _f32(to_device(y)),
+                                            _f32(to_device(inp(2))), at["epsilon"],
+                                            at.get("leaky_alpha"))
     elif op == "AdaIN":
         # inputs: x, style, W, bias; attribute epsilon.
         out = ops.adain(to_device(x), to_device(y), to_device(inp(2)),

@@ -1,0 +1,227 @@
+"""Fusion of the packed graph's node chains into single libkk launches.
+
+The packed Kokoro graph spells three hot patterns as chains of small nodes,
+each of which would otherwise read and write a full decoder activation
+(up to [1, 128, 10^6] fp32):
+
+  quantised conv tail   ConvInteger -> Add(int32 bias) -> Cast(float) -> Mul(scale)
+                        (the Add is absent in a few blocks)
+  InstanceNorm          ReduceMean -> Sub -> Mul(d, d) -> ReduceMean -> Add(eps)
+                        -> Sqrt -> Div -> [Mul(scale)] -> [Add(shift)] -> [LeakyRelu]
+  snake                 Mul(alpha, x) -> Sin -> Pow(2) -> Mul(recip) -> Add(x)
+
+`fuse` rewrites each chain whose intermediate tensors have no other reader
+into one pseudo-node that `dispatch` runs as one kernel (the reference's
+executor runs the chains node by node, executor.gd:733-843; the arithmetic
+of every fused form follows the chain's own, see the kernels).  A fused node
+takes the place of the chain's last node, where all of its inputs exist.
+"""
+from collections import defaultdict
+
+import numpy as np
+
+
+def _const(weights, name):
+    """Host value of a constant weight, or None."""
+    v = weights.get(name)
+    if v is None:
+        return None
+    host = getattr(v, "host", v)
+    return None if host is None else np.asarray(host)
+
+
+def fuse(nodes, weights, protect=()):
+    """nodes: [(op, ins, outs, attrs)] with string tensor names; weights:
+    {name: value} (host arrays, or device tensors with a `.host` copy for
+    small constants).  Tensors named in `protect` (the graph output and any
+    tensor a caller wants to read) are never fused away.
+
+    Returns (fused_nodes, groups): groups[k] lists the original node indices
+    that fused node k replaces, in order."""
+    protect = set(protect)
+    readers = defaultdict(list)
+    for i, (_op, ins, _outs, _at) in enumerate(nodes):
+        for n in ins:
+            if n:
+                readers[n].append(i)
+
+    def only_reader(name, want=None):
+        """Index of the single node reading `name` (and, if given, of op
+        `want`), or None."""
+        r = readers.get(name, [])
+        if name in protect or len(set(r)) != 1:
+            return None
+        j = r[0]
+        if want is not None and nodes[j][0] != want:
+            return None
+        return j
+
+    def other(ins, name):
+        a = [n for n in ins if n != name]
+        return a[0] if len(a) == 1 else None
+
+    used = set()
+    replace = {}  # index of the chain's last node -> (fused node, chain indices)
+
+    def claim(chain, fused):
+        if any(i in used for i in chain):
+            return False
+        used.update(chain)
+        replace[chain[-1]] = (fused, chain)
+        return True
+
+    for i, (op, ins, outs, at) in enumerate(nodes):
+        if i in used:
+            continue
+        if op == "ConvInteger" and int(at.get("group", 1)) == 1:
+            _match_qconv(nodes, i, only_reader, other, claim)
+        elif op == "ReduceMean":
+            _match_instnorm(nodes, weights, i, only_reader, readers, protect, other, claim)
+        elif op == "Sin":
+            _match_snake(nodes, weights, i, only_reader, other, claim)
+
+    out, groups = [], []
+    for i, node in enumerate(nodes):
+        if i in replace:
+            fused, chain = replace[i]
+            out.append(fused)
+            groups.append(list(chain))
+        elif i not in used:
+            out.append(node)
+            groups.append([i])
+    return out, groups
+
+
+def _match_qconv(nodes, i, only_reader, other, claim):
+    op, ins, outs, at = nodes[i]
+    acc = outs[0]
+    j = only_reader(acc)
+    if j is None:
+        return
+    chain = [i]
+    bias = ""
+    if nodes[j][0] == "Add":
+        bias = other(nodes[j][1], acc)
+        if bias is None:
+            return
+        chain.append(j)
+        j = only_reader(nodes[j][2][0])
+        if j is None:
+            return
+    if nodes[j][0] != "Cast" or int(nodes[j][3].get("to", 1)) not in (1, 10):
+        return
+    chain.append(j)
+    k = only_reader(nodes[j][2][0], "Mul")
+    if k is None:
+        return
+    scale = other(nodes[k][1], nodes[j][2][0])
+    if scale is None:
+        return
+    chain.append(k)
+    conv_ins = list(ins) + [""] * (4 - len(ins))
+    fused = ("QConvScaled", conv_ins[:4] + [bias, scale], [nodes[k][2][0]], dict(at))
+    claim(chain, fused)
+
+
+def _axes_of(nodes, weights, i):
+    op, ins, outs, at = nodes[i]
+    if len(ins) > 1 and ins[1]:
+        a = _const(weights, ins[1])
+        return None if a is None else [int(v) for v in a.reshape(-1)]
+    a = at.get("axes")
+    return None if a is None else [int(v) for v in np.asarray(a).reshape(-1)]
+
+
+def _match_instnorm(nodes, weights, i, only_reader, readers, protect, other, claim):
+    op, ins, outs, at = nodes[i]
+    axes = _axes_of(nodes, weights, i)
+    if axes not in ([2], [-1]) or not int(at.get("keepdims", 1)):
+        return
+    x, m1 = ins[0], outs[0]
+    a = only_reader(m1, "Sub")
+    if a is None or nodes[a][1] != [x, m1]:
+        return
+    d = nodes[a][2][0]
+    rd = readers.get(d, [])
+    if d in protect or len(rd) != 3:  # Mul reads it twice, Div once
+        return
+    sq_i = [r for r in rd if nodes[r][0] == "Mul" and nodes[r][1] == [d, d]]
+    div_i = [r for r in rd if nodes[r][0] == "Div" and nodes[r][1][0] == d]
+    if len(set(sq_i)) != 1 or len(div_i) != 1:
+        return
+    b, g = sq_i[0], div_i[0]
+    c = only_reader(nodes[b][2][0], "ReduceMean")
+    if c is None or nodes[c][1][0] != nodes[b][2][0] or _axes_of(nodes, weights, c) != axes:
+        return
+    if not int(nodes[c][3].get("keepdims", 1)):
+        return
+    e = only_reader(nodes[c][2][0], "Add")
+    if e is None:
+        return
+    eps_name = other(nodes[e][1], nodes[c][2][0])
+    eps = _const(weights, eps_name) if eps_name else None
+    if eps is None or eps.size != 1:
+        return
+    f = only_reader(nodes[e][2][0], "Sqrt")
+    if f is None or only_reader(nodes[f][2][0]) != g or nodes[g][1] != [d, nodes[f][2][0]]:
+        return
+    chain = [i, a, b, c, e, f, g]
+    y = nodes[g][2][0]
+    scale = shift = ""
+    alpha = None
+    k = only_reader(y, "Mul")
+    if k is not None:
+        s = other(nodes[k][1], y)
+        if s is not None:
+            scale, y = s, nodes[k][2][0]
+            chain.append(k)
+            k = only_reader(y, "Add")
+            if k is not None:
+                s = other(nodes[k][1], y)
+                if s is not None:
+                    shift, y = s, nodes[k][2][0]
+                    chain.append(k)
+                    k = only_reader(y, "LeakyRelu")
+                    if k is not None:
+                        alpha = float(nodes[k][3].get("alpha", 0.01))
+                        y = nodes[k][2][0]
+                        chain.append(k)
+    attrs = {"epsilon": float(np.float32(eps.reshape(-1)[0]))}
+    if alpha is not None:
+        attrs["leaky_alpha"] = alpha
+    claim(chain, ("InstanceNormScaleShift", [x, scale, shift], [y], attrs))
+
+
+def _match_snake(nodes, weights, i, only_reader, other, claim):
+    op, ins, outs, at = nodes[i]
+    # Mul(alpha, x) feeding the Sin
+    prods = [p for p, n in enumerate(nodes) if n[2] and n[2][0] == ins[0]]
+    if len(prods) != 1:
+        return
+    p = prods[0]
+    if nodes[p][0] != "Mul" or only_reader(ins[0]) != i:
+        return
+    m_ins = nodes[p][1]
+    wts = [n for n in m_ins if n in weights]
+    if len(wts) != 1 or len(m_ins) != 2:
+        return
+    alpha = wts[0]
+    x = other(m_ins, alpha)
+    if x is None:
+        return
+    q = only_reader(outs[0], "Pow")
+    if q is None:
+        return
+    two = _const(weights, nodes[q][1][1]) if len(nodes[q][1]) > 1 else None
+    if two is None or two.size != 1 or float(two.reshape(-1)[0]) != 2.0:
+        return
+    r = only_reader(nodes[q][2][0], "Mul")
+    if r is None:
+        return
+    recip = other(nodes[r][1], nodes[q][2][0])
+    if recip is None or recip not in weights:
+        return
+    s = only_reader(nodes[r][2][0], "Add")
+    if s is None or sorted(nodes[s][1]) != sorted([x, nodes[r][2][0]]):
+        return
+    claim([p, i, q, r, s], ("Snake", [x, alpha, recip], [nodes[s][2][0]], {}))

@@ -20,6 +20,7 @@ import os
 import numpy as np
 
 from .dispatch import dispatch, to_device, to_host
+from .fuse import fuse as fuse_chains
 from .tensor import DeviceTensor
 
 CODE_TO_NP = {0: np.float32, 1: np.int8, 2: np.uint8, 3: np.int32, 4: np.int64, 5: np.bool_,
@@ -75,14 +76,19 @@ def _decode_attrs(at):
 
 
 class PackedGraph:
-    """A packed graph with its weights resident on the device."""
+    """A packed graph with its weights resident on the device.
 
-    def __init__(self, graph, weights):
+    With `fuse` (the default) the quantised-conv tails, InstanceNorm chains
+    and snake chains run as single kernels; `groups[k]` lists the original
+    node indices that node k stands for.  Tensors in `protect` stay
+    readable after a run (they are never fused away)."""
+
+    def __init__(self, graph, weights, fuse=True, protect=()):
         self.graph = graph
         self.ops = graph["ops"]
-        self.nodes = [(self.ops[op], ["" if t < 0 else str(t) for t in ins],
-                       ["" if t < 0 else str(t) for t in outs], _decode_attrs(at))
-                      for op, ins, outs, at, _pl in graph["nodes"]]
+        nodes = [(self.ops[op], ["" if t < 0 else str(t) for t in ins],
+                  ["" if t < 0 else str(t) for t in outs], _decode_attrs(at))
+                 for op, ins, outs, at, _pl in graph["nodes"]]
         self.inputs = {k: str(v) for k, v in graph["inputs"].items()}
         self.output = str(graph["output"])
         # Weights: float data on the device once (fp16 widened to fp32 there),
@@ -103,6 +109,11 @@ class PackedGraph:
             if arr.size <= 16:
                 t.host = host  # small constants are also read on the host
             self.weights[str(tid)] = t
+        if fuse:
+            keep = {self.output} | {str(p) for p in protect}
+            self.nodes, self.groups = fuse_chains(nodes, self.weights, keep)
+        else:
+            self.nodes, self.groups = nodes, [[i] for i in range(len(nodes))]
         # Last use of every non-weight tensor (executor.gd:190-195).
         self.last_use = {}
         for i, (_op, ins, _outs, _at) in enumerate(self.nodes):

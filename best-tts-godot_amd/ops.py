@@ -232,6 +232,33 @@ def conv_integer(x, w, x_zp=None, w_zp=None, pads=(0, 0), stride=1, dilation=1, 
     return out
 
 
+def conv_integer_scaled(x, w, x_zp, w_zp, bias, scale, pads=(0, 0), stride=1, dilation=1,
+                        group=1):
+    """float(ConvInteger(x, w) + bias[co]) * scale, fp32 out (bias int32 [Cout] or None)."""
+    x = x.contiguous()
+    w = w.contiguous()
+    n, _, L = x.shape
+    cout, _, k = w.shape
+    lout = (L + pads[0] + pads[1] - dilation * (k - 1) - 1) // stride + 1
+    out = DeviceTensor.empty((n, cout, max(lout, 0)), np.float32)
+    _lib.call("kk_conv_integer_scaled", out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
+              _d(bias.contiguous() if bias is not None else None), scale.contiguous().desc(),
+              int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
+    return out
+
+
+def instance_norm_scale_shift(x, scale=None, shift=None, eps=1e-5, leaky_alpha=None):
+    """(x - mean_T) / sqrt(var_T + eps) * scale[c] + shift[c] over the last
+    axis, then LeakyRelu(leaky_alpha) when given."""
+    x = x.contiguous()
+    out = DeviceTensor.empty(x.shape, np.float32)
+    _lib.call("kk_instance_norm_scale_shift", out.desc(), x.desc(),
+              _d(scale.contiguous() if scale is not None else None),
+              _d(shift.contiguous() if shift is not None else None), float(eps),
+              0 if leaky_alpha is None else 1, 0.0 if leaky_alpha is None else float(leaky_alpha))
+    return out
+
+
 # ------------------------------------------------ recurrent / vocoder
 def lstm(x, w, r, b, init_h, init_c, w_scale, w_zp, r_scale, r_zp, hidden_size, bidirectional):
     x = x.contiguous()

@@ -155,6 +155,16 @@ int kk_reduce(int op, const kk_tensor* out, const kk_tensor* x,
  * (the Split of kpk #80 -> #138); NULL gives gamma = beta = 0. */
 int kk_instance_norm_affine(const kk_tensor* out, const kk_tensor* x,
                             const kk_tensor* gamma_beta, float eps);
+/* The graph's InstanceNorm chain fused: ReduceMean -> Sub -> Mul(d, d) ->
+ * ReduceMean -> Add(eps) -> Sqrt -> Div -> Mul(scale) -> Add(shift), and an
+ * optional LeakyRelu(alpha) after it (ref_runtime.py:589-598 ReduceMean,
+ * :446-455 Sub/Mul/Add/Div, :458-459 Sqrt, :476-479 LeakyRelu):
+ *   y = (x - mean_T) / sqrt(var_T + eps) * scale[c] + shift[c]
+ * over the last axis of x [N, C, T]; scale/shift hold C floats or are NULL
+ * (factor 1 / offset 0).  Rows longer than 16384 are split across blocks. */
+int kk_instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
+                                 const kk_tensor* scale, const kk_tensor* shift, float eps,
+                                 int leaky, float alpha);
 /* AdaIN with the style Linear fused: h = style . W + b with W [S, 2C]
  * (any strides), then kk_instance_norm_affine on x [N,C,T].  bias may be
  * NULL.  W may be f32, f16 or int8/uint8 with w_scale/w_zp (per tensor or
@@ -215,6 +225,16 @@ int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor*
 int kk_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
                     const kk_tensor* x_zp, const kk_tensor* w_zp, int stride,
                     int dilation, int pad0, int pad1, int group);
+/* The graph's quantised-conv tail fused into ConvInteger's epilogue:
+ * ConvInteger -> Add(bias, int32) -> Cast(float) -> Mul(scale)
+ * (ref_runtime.py:130-134, :446-455, :572-578):
+ *   out[n, co, l] = float(conv_int(x, w)[n, co, l] + bias[co]) * scale
+ * with out fp32, bias int32 holding Cout values or NULL, scale fp32 holding
+ * 1 or Cout values.  Same integer arithmetic as kk_conv_integer. */
+int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                           const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                           const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
+                           int group);
 
 /* ------------------------------------------------ recurrent / vocoder
  * DynamicQuantizeLSTM as op_lstm computes it without activation

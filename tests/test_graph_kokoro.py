@@ -92,9 +92,11 @@ def _node_close(got, want):
 
 
 def test_every_node_teacher_forced(gpu, oracle):
-    """Every one of the graph's nodes run on the GPU with the oracle's exact
+    """Every node of the (fused) graph run on the GPU with the oracle's exact
     inputs (placed on host or device as the free-running GPU walk places
-    them) and checked against the oracle's output for that node.
+    them) and checked against the oracle's value of each of its outputs.  A
+    fused node is checked against the output of the original node chain it
+    replaces, which the oracle computes node by node.
 
     The free-running waveform is not compared sample by sample: with random
     learned weights the decoder amplifies fp32 reordering noise (~1e-5)
@@ -108,6 +110,20 @@ def test_every_node_teacher_forced(gpu, oracle):
     g = kkg.load_graph(kkg.default_graph_path())
     w = kkg.synth_weights(g, 0)
     pg = kkg.PackedGraph(g, w)
+    assert len(pg.nodes) < len(g["nodes"])  # the fusion pass ran
+    orig = [(g["ops"][op], ["" if t < 0 else str(t) for t in ins],
+             ["" if t < 0 else str(t) for t in outs], kpk_run.decode_attrs(at))
+            for op, ins, outs, at, _pl in g["nodes"]]
+    ends = {grp[-1]: k for k, grp in enumerate(pg.groups)}
+    # An oracle value is dropped once both its last original reader and its
+    # last (fused) device reader have run.
+    last = {}
+    for i, (_op, ins, _outs, _at) in enumerate(orig):
+        for n in ins:
+            last[n] = max(last.get(n, -1), i)
+    for k, (_op, ins, _outs, _at) in enumerate(pg.nodes):
+        for n in ins:
+            last[n] = max(last.get(n, -1), pg.groups[k][-1])
     ids, style, _ = kkg.synth_inputs(3, 1)
     oenv = {str(k): v for k, v in w.items()}
     oenv[pg.inputs["input_ids"]] = np.asarray(ids, np.int64).reshape(1, -1)
@@ -115,29 +131,32 @@ def test_every_node_teacher_forced(gpu, oracle):
     oenv[pg.inputs["speed"]] = np.asarray([2.0], np.float32)
     on_device = {pg.inputs["input_ids"]: False, pg.inputs["style"]: True, pg.inputs["speed"]: True}
     failures, counted = [], 0
-    for i, ((op, ins, outs, at), raw) in enumerate(zip(pg.nodes, g["nodes"])):
-        genv = {}
+    for i, (op, ins, outs, at) in enumerate(orig):
+        oracle.dispatch(op, ins, outs, at, oenv)
+        if i in ends:
+            k = ends[i]
+            gop, gins, gouts, gat = pg.nodes[k]
+            genv = {}
+            for n in gins:
+                if not n or n in genv:
+                    continue
+                if n in pg.weights:
+                    genv[n] = pg.weights[n]
+                else:
+                    genv[n] = gpu.to_device(np.asarray(oenv[n])) if on_device[n] else oenv[n]
+            gpu.dispatch(gop, gins, gouts, gat, genv)
+            for o in gouts:
+                if not o:
+                    continue
+                on_device[o] = isinstance(genv[o], gpu.DeviceTensor)
+                msg = _node_close(gpu.to_host(genv[o]), oenv[o])
+                counted += 1
+                if msg:
+                    failures.append(f"node {k} {gop} (original {pg.groups[k]}) -> {o}: {msg}")
         for n in ins:
-            if not n or n in genv:
-                continue
-            if n in pg.weights:
-                genv[n] = pg.weights[n]
-            else:
-                genv[n] = gpu.to_device(np.asarray(oenv[n])) if on_device[n] else oenv[n]
-        oracle.dispatch(op, ins, outs, kpk_run.decode_attrs(raw[3]), oenv)
-        gpu.dispatch(op, ins, outs, at, genv)
-        for o in outs:
-            if not o:
-                continue
-            on_device[o] = isinstance(genv[o], gpu.DeviceTensor)
-            msg = _node_close(gpu.to_host(genv[o]), oenv[o])
-            counted += 1
-            if msg:
-                failures.append(f"node {i} {op} -> {o}: {msg}")
-        for n in ins:
-            if n and pg.last_use.get(n) == i:
+            if n and last.get(n) == i and n not in pg.weights:
                 oenv.pop(n, None)
-    assert counted > 3900
+    assert counted == sum(1 for n in pg.nodes for o in n[2] if o)
     assert not failures, f"{len(failures)} node outputs differ:\n" + "\n".join(failures[:20])
 
 

@@ -132,3 +132,69 @@ def test_unknown_op_raises():
     kk = load_pkg()
     with pytest.raises(NotImplementedError):
         kk.dispatch("NoSuchOp", ["a"], ["b"], {}, {"a": np.zeros(1, np.float32)})
+
+
+def _graph_nodes():
+    import importlib
+    kkg = importlib.import_module("best-tts-godot_amd.graph")
+    g = kkg.load_graph(kkg.default_graph_path())
+    nodes = [(g["ops"][op], ["" if t < 0 else str(t) for t in ins],
+              ["" if t < 0 else str(t) for t in outs], kkg._decode_attrs(at))
+             for op, ins, outs, at, _pl in g["nodes"]]
+    return g, nodes, {str(k): v for k, v in kkg.synth_weights(g, 0).items()}
+
+
+def test_fusion_pass_on_the_kokoro_graph():
+    """The fusion pass finds every quantised conv tail (87), InstanceNorm
+    chain (64 of 65: one has a Transpose inside) and snake (48) of the
+    packed graph, keeps a valid topological order, and never drops a tensor
+    that a node outside its group reads."""
+    import importlib
+    from collections import Counter
+    fz = importlib.import_module("best-tts-godot_amd.fuse")
+    g, nodes, weights = _graph_nodes()
+    fused, groups = fz.fuse(nodes, weights, {str(g["output"])})
+    kinds = Counter(n[0] for n in fused)
+    assert (kinds["QConvScaled"], kinds["InstanceNormScaleShift"], kinds["Snake"]) == (87, 64, 48)
+    covered = sorted(i for grp in groups for i in grp)
+    assert covered == list(range(len(nodes)))  # every original node exactly once
+    produced = {}
+    for k, (_op, _ins, outs, _at) in enumerate(fused):
+        for o in outs:
+            if o:
+                produced[o] = k
+    for k, (_op, ins, _outs, _at) in enumerate(fused):
+        for n in ins:
+            if n and n in produced:
+                assert produced[n] < k, (k, n)
+    # tensors produced inside a group and read elsewhere must still be produced
+    inner = {}
+    for k, grp in enumerate(groups):
+        for i in grp:
+            for o in nodes[i][2]:
+                if o:
+                    inner[o] = k
+    for k, (_op, ins, _outs, _at) in enumerate(fused):
+        for n in ins:
+            if n in inner and inner[n] != k:
+                assert n in produced, n
+
+
+def test_fusion_skips_chains_with_outside_readers():
+    import importlib
+    fz = importlib.import_module("best-tts-godot_amd.fuse")
+    nodes = [("ReduceMean", ["x", "ax"], ["m1"], {"keepdims": 1}),
+             ("Sub", ["x", "m1"], ["d"], {}), ("Mul", ["d", "d"], ["sq"], {}),
+             ("ReduceMean", ["sq", "ax"], ["m2"], {"keepdims": 1}),
+             ("Add", ["m2", "eps"], ["ve"], {}), ("Sqrt", ["ve"], ["sd"], {}),
+             ("Div", ["d", "sd"], ["n"], {}), ("Mul", ["g", "n"], ["y"], {})]
+    weights = {"ax": np.array([2], np.int64), "eps": np.array(1e-5, np.float32),
+               "g": np.ones((1, 4, 1), np.float32)}
+    fused, groups = fz.fuse(nodes, weights, {"y"})
+    assert [n[0] for n in fused] == ["InstanceNormScaleShift"] and groups == [list(range(8))]
+    extra = nodes + [("Mul", ["d", "x"], ["z"], {})]  # d gains a reader outside the chain
+    fused, groups = fz.fuse(extra, weights, {"y", "z"})
+    assert [n[0] for n in fused] == [n[0] for n in extra]
+    fused, _ = fz.fuse(nodes, weights, {"y", "n"})  # a protected intermediate
+    assert "InstanceNormScaleShift" in [n[0] for n in fused]
+    assert any(n[2] == ["n"] for n in fused)

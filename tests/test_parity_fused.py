@@ -1,0 +1,116 @@
+"""Parity of the fused graph chains with the node chains they replace, run
+node by node through the oracle, at decoder sizes.
+
+Each case builds the chain as graph nodes, lets the fusion pass rewrite it
+(so the test covers the matcher as well as the kernel) and compares the
+fused launch with the oracle's chain.  Bars: the quantised conv tail
+bit-exact (integer arithmetic, then the chain's own Cast and Mul); the
+InstanceNorm chain bit-exact (its sums follow numpy's summation order, the
+rest are correctly rounded IEEE operations); the snake chain at the
+elementwise bar rel 1e-5 (+1e-6 max|ref|: sin differs by ulps between numpy
+and the device)."""
+import importlib
+
+import numpy as np
+import pytest
+
+from conftest import assert_bitexact, assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def run_chain(gpu, oracle, nodes, inputs, weights, out):
+    """Runs `nodes` (op, ins, outs, attrs) through the fusion pass and the
+    device dispatch, and through the oracle unfused; returns (device result,
+    oracle result, fused node list)."""
+    fz = importlib.import_module("best-tts-godot_amd.fuse")
+    dev_w = {}
+    for k, v in weights.items():  # fp16 widened at upload, as PackedGraph does
+        v = np.asarray(v)
+        v = v.astype(np.float32) if v.dtype == np.float16 else v
+        t = gpu.to_device(v)
+        if v.size <= 16:
+            t.host = v
+        dev_w[k] = t
+    fused, _groups = fz.fuse(nodes, dev_w, {out})
+    env = dict(dev_w)
+    env.update({k: gpu.to_device(np.asarray(v)) for k, v in inputs.items()})
+    for op, ins, outs, at in fused:
+        gpu.dispatch(op, ins, outs, at, env)
+    oenv = {k: np.asarray(v) for k, v in {**weights, **inputs}.items()}
+    for op, ins, outs, at in nodes:
+        oracle.dispatch(op, ins, outs, at, oenv)
+    return gpu.to_host(env[out]), oenv[out], fused
+
+
+@pytest.mark.parametrize("cin,cout,k,L,pad,bias", [(128, 128, 7, 3000, 3, True),
+                                                   (256, 256, 11, 900, 5, True),
+                                                   (96, 40, 3, 257, 1, False)])
+def test_qconv_tail(gpu, oracle, cin, cout, k, L, pad, bias):
+    r = rng(21)
+    x = r.integers(0, 256, (1, cin, L)).astype(np.uint8)
+    w = r.integers(0, 256, (cout, cin, k)).astype(np.uint8)
+    inputs = {"x": x, "xz": np.array(113, np.uint8),
+              "b": r.integers(-3000, 3000, (1, cout, 1)).astype(np.int32),
+              "s": np.array(3.1e-5, np.float32)}
+    weights = {"w": w, "wz": np.array(71, np.uint8)}
+    at = {"pads": [pad, pad], "dilations": [1], "strides": [1], "group": 1, "kernel_shape": [k]}
+    nodes = [("ConvInteger", ["x", "w", "xz", "wz"], ["acc"], at)]
+    last = "acc"
+    if bias:
+        nodes.append(("Add", ["acc", "b"], ["accb"], {}))
+        last = "accb"
+    nodes += [("Cast", [last], ["f"], {"to": 10}), ("Mul", ["f", "s"], ["y"], {})]
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, "y")
+    assert [n[0] for n in fused] == ["QConvScaled"]
+    assert_bitexact(got, want.astype(np.float32), f"QConvScaled {cin}->{cout} k{k}")
+
+
+def norm_chain(affine, leaky):
+    nodes = [("ReduceMean", ["x", "ax"], ["m1"], {"keepdims": 1}),
+             ("Sub", ["x", "m1"], ["d"], {}), ("Mul", ["d", "d"], ["sq"], {}),
+             ("ReduceMean", ["sq", "ax"], ["m2"], {"keepdims": 1}),
+             ("Add", ["m2", "eps"], ["ve"], {}), ("Sqrt", ["ve"], ["sd"], {}),
+             ("Div", ["d", "sd"], ["n"], {})]
+    out = "n"
+    if affine:
+        nodes += [("Mul", ["g", "n"], ["gn"], {}), ("Add", ["gn", "b"], ["y"], {})]
+        out = "y"
+        if leaky:
+            nodes.append(("LeakyRelu", ["y"], ["z"], {"alpha": 0.2}))
+            out = "z"
+    return nodes, out
+
+
+@pytest.mark.parametrize("C,T,affine,leaky", [(128, 40000, True, False), (128, 40001, True, True),
+                                              (256, 700, True, True), (512, 279, False, False),
+                                              (64, 20000, False, False)])
+def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
+    r = rng(22)
+    x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
+    inputs = {"x": x, "g": (1 + 0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32),
+              "b": (0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32)}
+    weights = {"ax": np.array([2], np.int64),
+               "eps": np.array(1e-5, np.float16).astype(np.float32)}
+    nodes, out = norm_chain(affine, leaky)
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, out)
+    assert [n[0] for n in fused] == ["InstanceNormScaleShift"]
+    # statistics in numpy's summation order, then the chain's own IEEE
+    # operations: the same bits
+    assert_bitexact(got, want, f"InstanceNorm chain C={C} T={T}")
+
+
+@pytest.mark.parametrize("C,T", [(128, 30000), (256, 5001)])
+def test_snake_chain(gpu, oracle, C, T):
+    r = rng(23)
+    x = r.normal(0, 1, (1, C, T)).astype(np.float32)
+    alpha = r.uniform(0.5, 2, (1, C, 1)).astype(np.float16)
+    weights = {"a": alpha, "r": (np.float32(1) / alpha.astype(np.float32)).astype(np.float16),
+               "two": np.array(2.0, np.float16)}
+    nodes = [("Mul", ["a", "x"], ["t"], {}), ("Sin", ["t"], ["s"], {}),
+             ("Pow", ["s", "two"], ["p"], {}), ("Mul", ["r", "p"], ["q"], {}),
+             ("Add", ["x", "q"], ["y"], {})]
+    got, want, fused = run_chain(gpu, oracle, nodes, {"x": x}, weights, "y")
+    assert [n[0] for n in fused] == ["Snake"]
+    assert_close(got, want, 1e-5, floor_rel=1e-6, what=f"snake chain C={C} T={T}")
+
