@@ -302,11 +302,13 @@ def run_graph(n_ids, reps):
         "frames_F": frames,
         "samples": int(wav.size),
         "audio_sec": round(audio, 3),
-        "nodes": len(pg.nodes),
+        "nodes": len(g["nodes"]),
+        "launch_nodes": len(pg.nodes),
         "peak_pool_bytes": kk.pool_stats()[2],
-        "workload": (f"full Kokoro-82M-architecture graph ({len(pg.nodes)} nodes, int8 GEMM/conv "
-                     f"+ fp16 weights, seeded random-init), {n_ids} phoneme ids U{{1..177}}, "
-                     "voice-pack row style, speed 1.0"),
+        "workload": (f"full Kokoro-82M-architecture graph ({len(g['nodes'])} nodes, "
+                     f"{len(pg.nodes)} after chain fusion; int8 GEMM/conv + fp16 weights, "
+                     f"seeded random-init), {n_ids} phoneme ids U{{1..177}}, voice-pack row "
+                     "style, speed 1.0"),
     }
     log(f"bench: kokoro graph {json.dumps(rec)}")
     return rec

@@ -29,7 +29,21 @@ see tests/test_oracle.py):
                              <conv(x), y> = <x, convT(y)>, delta kernels.
   fast_gelu               -- float64 closed form.
   bucket                  -- closed-form properties (multiple of 256, at most
-                             4 significant bits, monotone, <= 6.25% slack).
+                             4 significant bits, monotone, <= 12.5% slack).
+  (tests/test_oracle_graphops.py:)
+  dynamic_quantize_linear -- the ONNX specification's example; zero exact,
+                             reconstruction within half a quantum, the
+                             float32 division of x by the double scale.
+  matmul_integer,         -- integer brute force (int64 loops), padding
+  conv_integer               contributing zero after the zero-point shift.
+  lstm                    -- torch.nn.LSTM (float64, bidirectional) on the
+                             dequantised weights, gates reordered.
+  stft                    -- numpy.fft.rfft of the windowed frames (float64).
+  resize                  -- np.repeat (nearest x300), torch interpolate
+                             (linear, half_pixel).
+  pad                     -- torch.nn.functional.pad (reflect/replicate/
+                             constant).
+  scatter_nd, CumSum      -- loops; integer prefix sums in closed form.
 """
 import numpy as np
 
