@@ -68,35 +68,57 @@ __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w,
 
 // xT[b][t][ci] = x[b][ci][t - p0] - 128 for t inside the signal, xz - 128 in
 // the padding, 0 in the padding channels; xs[b][t] = sum over real channels.
+// A block owns 64 time steps and walks the channels in tiles of 64: lane l
+// of wave w loads x[ci][t0 + l] for ci = w, w + 4, ... (64 consecutive bytes
+// per load), the tile is transposed through LDS, and each thread stores 16
+// consecutive channels of one time step as one 16-byte store.
+constexpr int kPrepT = 64;   // time steps per block
+constexpr int kPrepC = 64;   // channels per tile
+
 __global__ void __launch_bounds__(256) conv_i8_xprep(const uint8_t* __restrict__ x,
                                                      const uint8_t* __restrict__ xzp,
                                                      int8_t* __restrict__ xT,
                                                      int32_t* __restrict__ xs, int64_t Cin,
                                                      int64_t L, int64_t p0, int64_t Lp,
                                                      int64_t CinP) {
-  const int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  __shared__ int8_t tile[kPrepC][kPrepT + 4];
+  __shared__ int part[4][kPrepT];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kPrepT;
   const int64_t b = blockIdx.y;
-  if (t >= Lp) return;
   const int pad = (xzp ? static_cast<int>(xzp[0]) : 0) - 128;
-  const int64_t ts = t - p0;
-  const bool inside = ts >= 0 && ts < L;
   const uint8_t* xb = x + b * Cin * L;
-  int8_t* dst = xT + (b * Lp + t) * CinP;
+  // loader: time step t0 + lane
+  const int64_t ts = t0 + lane - p0;
+  const bool inside = ts >= 0 && ts < L;
+  // storer: time step t0 + lane, channels 16 * wv .. 16 * wv + 15 of the tile
+  const int64_t to = t0 + lane;
   int sum = 0;
-  for (int64_t c0 = 0; c0 < CinP; c0 += 16) {
-    v4i pack;
-    int8_t* pv = reinterpret_cast<int8_t*>(&pack);
+  for (int64_t c0 = 0; c0 < CinP; c0 += kPrepC) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int64_t ci = c0 + e;
+    for (int k = 0; k < kPrepC / 4; ++k) {
+      const int r = wv + 4 * k;
+      const int64_t ci = c0 + r;
       int v = 0;
       if (ci < Cin) v = inside ? static_cast<int>(xb[ci * L + ts]) - 128 : pad;
-      pv[e] = static_cast<int8_t>(v);
-      sum += v;
+      tile[r][lane] = static_cast<int8_t>(v);
     }
-    *reinterpret_cast<v4i*>(dst + c0) = pack;
+    __syncthreads();
+    if (to < Lp && c0 + 16 * wv < CinP) {
+      v4i pack;
+      int8_t* pv = reinterpret_cast<int8_t*>(&pack);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        pv[e] = tile[16 * wv + e][lane];
+        sum += pv[e];
+      }
+      *reinterpret_cast<v4i*>(xT + (b * Lp + to) * CinP + c0 + 16 * wv) = pack;
+    }
+    __syncthreads();
   }
-  xs[b * Lp + t] = sum;
+  part[wv][lane] = sum;
+  __syncthreads();
+  if (wv == 0 && to < Lp) xs[b * Lp + to] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
 }
 
 struct ConvI8Args {
@@ -263,7 +285,7 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
   int rc = check_launch("conv_i8_wprep");
   const uint8_t* xzp = x_zp ? static_cast<const uint8_t*>(x_zp->data) : nullptr;
   if (rc == KK_OK) {
-    hipLaunchKernelGGL(conv_i8_xprep, dim3(static_cast<unsigned>(ceil_div(Lp, 256)),
+    hipLaunchKernelGGL(conv_i8_xprep, dim3(static_cast<unsigned>(ceil_div(Lp, kPrepT)),
                                            static_cast<unsigned>(N)),
                        dim3(256), 0, st, static_cast<const uint8_t*>(x->data), xzp, xT, xs, Cin,
                        L, static_cast<int64_t>(pad0), Lp, CinP);

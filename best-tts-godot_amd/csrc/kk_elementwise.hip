@@ -193,6 +193,67 @@ __global__ void __launch_bounds__(256) ew_rows(EwArgs A) {
   }
 }
 
+// Plans of rank <= 2 whose rows are not whole float4s (L % 4 != 0, L >= 4)
+// but whose output is contiguous: the output is walked flat, four elements
+// at a time.  Each input is flat (contiguous like the output: one float4
+// load), per-row (one value per row, the item's row and, where the item
+// runs past the row's end, the next one) or a scalar; `kinds` holds two
+// bits per input (0 flat, 1 per-row).
+template <int OP, int NIN>
+__global__ void __launch_bounds__(256) ew_flat4(EwArgs A, int kinds) {
+  const int64_t L = A.dims[A.rank - 1];
+  const int64_t n = A.n;
+  const double invL = 1.0 / static_cast<double>(L);
+  float* __restrict__ out = static_cast<float*>(A.out);
+  const float* __restrict__ in[3] = {static_cast<const float*>(A.in[0]),
+                                     NIN > 1 ? static_cast<const float*>(A.in[1]) : nullptr,
+                                     NIN > 2 ? static_cast<const float*>(A.in[2]) : nullptr};
+  const int64_t rst[3] = {A.rank == 2 ? A.st[1][0] : 0, A.rank == 2 ? A.st[2][0] : 0,
+                          A.rank == 2 ? A.st[3][0] : 0};
+  auto locate = [&](int64_t i, int64_t& row, int64_t& col) {
+    row = static_cast<int64_t>(static_cast<double>(i) * invL);
+    col = i - row * L;
+    if (col < 0) { --row; col += L; } else if (col >= L) { ++row; col -= L; }
+  };
+  const int64_t items = n / 4;
+  for (int64_t v = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; v < items;
+       v += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = 4 * v;
+    int64_t row, col;
+    locate(i, row, col);
+    float x[3][4];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) {
+      if (((kinds >> (2 * k)) & 3) == 0) {
+        const float4 t = ld_stream4(in[k] + i);
+        x[k][0] = t.x; x[k][1] = t.y; x[k][2] = t.z; x[k][3] = t.w;
+      } else {
+        const float r0 = in[k][row * rst[k]];
+        const float r1 = col + 3 >= L ? in[k][(row + 1) * rst[k]] : r0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[k][e] = col + e < L ? r0 : r1;
+      }
+    }
+    float r[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      r[e] = apply_f32<OP>(x[0][e], NIN > 1 ? x[1][e] : 0.0f, NIN > 2 ? x[2][e] : 0.0f, A.alpha,
+                           A.aux);
+    st_stream4(out + i, make_float4(r[0], r[1], r[2], r[3]));
+  }
+  // the last n % 4 elements
+  if (blockIdx.x == 0 && threadIdx.x < n - 4 * items) {
+    const int64_t i = 4 * items + threadIdx.x;
+    int64_t row, col;
+    locate(i, row, col);
+    float x[3];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k)
+      x[k] = ((kinds >> (2 * k)) & 3) == 0 ? in[k][i] : in[k][row * rst[k]];
+    out[i] = apply_f32<OP>(x[0], NIN > 1 ? x[1] : 0.0f, NIN > 2 ? x[2] : 0.0f, A.alpha, A.aux);
+  }
+}
+
 // Plans of rank > 2: flat index over VEC-wide items; the outer offsets come
 // from a div/mod walk over the outer axes.
 template <int OP, int NIN, int VEC, typename Idx>
@@ -377,9 +438,14 @@ static bool fits_u32(const Plan& p) {
 }
 
 template <int OP, int NIN>
-static int launch_inner_op(const EwArgs& A, int vec, bool u32) {
+static int launch_inner_op(const EwArgs& A, int vec, bool u32, int flat_kinds) {
   const int64_t items = A.n / vec;
   hipStream_t s = ctx().stream;
+  if (flat_kinds >= 0) {
+    hipLaunchKernelGGL((ew_flat4<OP, NIN>), dim3(grid_for(A.n / 4)), dim3(256), 0, s, A,
+                       flat_kinds);
+    return check_launch("ew_flat4");
+  }
   const int64_t per_row = A.dims[A.rank - 1] / vec;
   if (A.rank <= 2 && per_row >= 64) {
     const int64_t rows = A.rank == 2 ? A.dims[0] : 1;
@@ -401,11 +467,11 @@ static int launch_inner_op(const EwArgs& A, int vec, bool u32) {
   return check_launch("ew_inner");
 }
 
-static int launch_inner(const EwArgs& A, int nin, int vec, bool u32) {
+static int launch_inner(const EwArgs& A, int nin, int vec, bool u32, int flat_kinds) {
   switch (A.op) {
-#define KK_U(OPC) case OPC: return launch_inner_op<OPC, 1>(A, vec, u32);
-#define KK_B(OPC) case OPC: return launch_inner_op<OPC, 2>(A, vec, u32);
-#define KK_T(OPC) case OPC: return launch_inner_op<OPC, 3>(A, vec, u32);
+#define KK_U(OPC) case OPC: return launch_inner_op<OPC, 1>(A, vec, u32, flat_kinds);
+#define KK_B(OPC) case OPC: return launch_inner_op<OPC, 2>(A, vec, u32, flat_kinds);
+#define KK_T(OPC) case OPC: return launch_inner_op<OPC, 3>(A, vec, u32, flat_kinds);
     KK_B(KK_OP_ADD) KK_B(KK_OP_SUB) KK_B(KK_OP_MUL) KK_B(KK_OP_DIV) KK_B(KK_OP_POW)
     KK_B(KK_OP_MIN) KK_B(KK_OP_MAX)
     KK_U(KK_OP_SQRT) KK_U(KK_OP_EXP) KK_U(KK_OP_SIN) KK_U(KK_OP_COS) KK_U(KK_OP_ATAN)
@@ -480,7 +546,27 @@ static int run_elementwise(int op, const kk_tensor* out, const kk_tensor* const*
       for (int d = 0; d < p.rank - 1; ++d)
         if (p.st[k][d] % 4) vec4 = false;
     }
-    return launch_inner(A, nin, vec4 ? 4 : 1, fits_u32(p));
+    // Rows that are not whole float4s: the flat float4 walk, when the output
+    // is contiguous and every input is contiguous like it or per-row.
+    int kinds = -1;
+    if (!vec4 && p.rank <= 2 && L >= 4 && L % 4 != 0 && p.n >= 4096 &&
+        reinterpret_cast<uintptr_t>(out->data) % 16 == 0 &&
+        (p.rank == 1 || p.st[0][0] == L)) {
+      kinds = 0;
+      for (int k = 0; k < nin && kinds >= 0; ++k) {
+        const int64_t s1 = p.st[k + 1][p.rank - 1];
+        const int64_t s0 = p.rank == 2 ? p.st[k + 1][0] : 0;
+        if (s1 == 1 && (p.rank == 1 || s0 == L) &&
+            reinterpret_cast<uintptr_t>(ins[k]->data) % 16 == 0) {
+          continue;  // flat
+        } else if (s1 == 0) {
+          kinds |= 1 << (2 * k);  // per-row (or scalar)
+        } else {
+          kinds = -1;
+        }
+      }
+    }
+    return launch_inner(A, nin, vec4 ? 4 : 1, fits_u32(p), kinds);
   }
   hipLaunchKernelGGL(ew_generic, dim3(grid_for(p.n)), dim3(256), 0, ctx().stream, A, nin, mode);
   return check_launch("ew_generic");

@@ -759,7 +759,30 @@ __global__ void reduce_generic_kernel(float* __restrict__ out, const float* __re
     float s = 0.0f;  // numpy sums a non-contiguous axis in order, in fp32
     float m = -INFINITY;
     bool nan = false;
-    for (int64_t j = 0; j < R.nred; ++j) {
+    if (R.rr == 1) {
+      // One reduced axis: sixteen independent loads in flight, then added
+      // (or compared) in order.
+      const int64_t st = R.rst[0];
+      int64_t j = 0;
+      for (; j + 16 <= R.nred; j += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = x[base + (j + u) * st];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          s += v[u];
+          nan |= __builtin_isnan(v[u]);
+          m = fmaxf(m, v[u]);
+        }
+      }
+      for (; j < R.nred; ++j) {
+        const float v = x[base + j * st];
+        s += v;
+        nan |= __builtin_isnan(v);
+        m = fmaxf(m, v);
+      }
+    }
+    for (int64_t j = 0; j < R.nred && R.rr != 1; ++j) {
       int64_t rj = j, off = base;
       for (int d = R.rr - 1; d >= 0; --d) {
         off += (rj % R.rdims[d]) * R.rst[d];

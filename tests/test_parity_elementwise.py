@@ -326,3 +326,32 @@ def test_empty_and_scalar(gpu, oracle):
     assert run_node(gpu, "Add", [e, np.ones(5, np.float32)]).shape == (0, 5)
     s = np.array(3.0, np.float32)
     assert_bitexact(run_node(gpu, "Mul", [s, s]), np.array(9.0, np.float32), "scalar")
+
+
+@pytest.mark.parametrize("case", ["add_per_channel", "mul_full", "snake", "rank1", "sub_scalar"])
+def test_odd_rows_flat_path(gpu, oracle, case):
+    """Rows whose length is not a multiple of 4 (the decoder's odd time axes)
+    go through the flat float4 walk; items straddle row ends."""
+    r = rng(31)
+    if case == "add_per_channel":
+        ins = [r.normal(0, 1, (1, 128, 4097)), r.normal(0, 1, (1, 128, 1))]
+        op = "Add"
+    elif case == "mul_full":
+        ins = [r.normal(0, 1, (1, 3, 100003)), r.normal(0, 1, (1, 3, 100003))]
+        op = "Mul"
+    elif case == "snake":
+        x = r.normal(0, 1, (1, 64, 5001)).astype(np.float32)
+        a = r.uniform(0.5, 2, (1, 64, 1)).astype(np.float32)
+        rec = (np.float32(1) / a).astype(np.float32)
+        got = gpu.ops.snake(gpu.to_device(x), gpu.to_device(a), gpu.to_device(rec)).numpy()
+        assert_close(got, oracle.snake(x, a, rec), 1e-5, floor_rel=1e-6, what="snake odd rows")
+        return
+    elif case == "rank1":
+        ins = [r.normal(0, 1, 10007), r.normal(0, 1, 10007)]
+        op = "Sub"
+    else:
+        ins = [r.normal(0, 1, (2, 9, 999)), np.array(1.5)]
+        op = "Div"
+    ins = [np.asarray(v, np.float32) for v in ins]
+    got = gpu.ops.binary(op, *[gpu.to_device(v) for v in ins]).numpy()
+    assert_bitexact(got, oracle.binary(op, *ins), f"{op} {case}")
