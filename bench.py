@@ -124,6 +124,20 @@ BYTES = {
 STEP_BYTES = sum(BYTES.values())
 
 
+def pmc_traffic(kernel):
+    """HBM bytes per launch of `kernel` measured by the FETCH_SIZE and
+    WRITE_SIZE counter runs summarised in profiles/ (null until measured)."""
+    path = os.path.join(ROOT, "profiles", "instnorm_adain_t9600_hbm_traffic.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        if line.startswith(f"traffic_bytes_per_launch {kernel} = "):
+            return int(line.rsplit("=", 1)[1])
+    return None
+
+
 def run_gpu(args):
     kk = importlib.import_module("best-tts-godot_amd")
     kk.init(0)
@@ -132,7 +146,10 @@ def run_gpu(args):
     host = reduction_inputs()
     nsets = max(2, -(-ROTATE_BYTES // (2 * STEP_BYTES)))  # inputs + outputs per set
     log(f"bench: {nsets} rotating sets x {2 * STEP_BYTES / 1e6:.1f} MB")
-    style, w, b = D(host["style"]), D(host["w"]), D(host["b"])
+    # The style Linear's W [128, 1024] is kept as W^T in memory (a transposed
+    # view): each channel's gamma and beta columns are then contiguous.
+    style, b = D(host["style"]), D(host["b"])
+    w = D(np.ascontiguousarray(host["w"].T)).transpose([1, 0])
     g, beta = D(host["g"]), D(host["beta"])
     xs = {k: B.replicate(D(host[k]), nsets) for k in ("x1200", "x9600", "ln", "sm")}
     outs = {k: [kk.DeviceTensor.empty(v[0].shape) for _ in range(nsets)] for k, v in xs.items()}
@@ -196,6 +213,11 @@ def run_gpu(args):
         log(f"bench: {name:<28} {json.dumps(rec)}")
         return rec
 
+    # A plain fp32 copy of the AdaIN T=9600 input: the achievable bandwidth
+    # at this size, and the calibration kernel for the HBM byte counters.
+    copy_bytes = 2 * 512 * 9600 * 4
+    cp = per_op("copy_512x9600", lambda i: B.call("kk_copy", outs["x9600"][i].desc(),
+                                                  xs["x9600"][i].desc()), copy_bytes)
     per_op("adain_t1200", lambda i: op_adain("x1200", i), BYTES["adain_t1200"])
     dom = per_op("adain_t9600", lambda i: op_adain("x9600", i), BYTES["adain_t9600"])
     per_op("layernorm_768", op_ln, BYTES["layernorm_768"])
@@ -267,9 +289,11 @@ def run_gpu(args):
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(dom["gbps"] / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": pmc_traffic("instnorm_kernel"),
         "algorithmic_bytes_per_launch": BYTES["adain_t9600"],
         "avg_launch_us": dom["us"],
+        "copy_same_size_gbps": cp["gbps"],
+        "frac_of_copy": round(dom["gbps"] / cp["gbps"], 4),
     }
     return ms_per_step, nsets, ops_out, roofline
 
