@@ -235,6 +235,86 @@ static void pool_release_all() {
   p.live_bytes = p.pooled_bytes = 0;
 }
 
+// ---------------------------------------------------------------- uploads
+// kk_upload never waits for the stream.  Up to kUploadArgBytes travel inside
+// the arguments of a one-block copy kernel (kernel arguments are captured at
+// launch); larger uploads are staged in a pinned ring and copied with
+// hipMemcpyAsync, each staged range guarded by an event until its copy has
+// run.  Uploads larger than a quarter of the ring are copied synchronously.
+constexpr size_t kUploadArgBytes = 2048;
+constexpr size_t kStageBytes = size_t(64) << 20;
+
+struct UploadArgs {
+  uint8_t* dst;
+  uint32_t n;
+  uint8_t data[kUploadArgBytes];
+};
+
+__global__ void upload_small_kernel(UploadArgs a) {
+  for (uint32_t i = threadIdx.x; i < a.n; i += blockDim.x) a.dst[i] = a.data[i];
+}
+
+struct Staged {
+  size_t begin, end;
+  hipEvent_t done;
+};
+struct Staging {
+  char* ring = nullptr;
+  size_t head = 0;
+  std::vector<Staged> inflight;
+  std::vector<hipEvent_t> spare;
+};
+static Staging& staging() {
+  static Staging* s = new Staging();  // leaked on purpose: outlives static dtors
+  return *s;
+}
+
+static int stage_upload(void* dst, const void* src, size_t bytes) {
+  Staging& S = staging();
+  if (!S.ring) KK_HIP(hipHostMalloc(reinterpret_cast<void**>(&S.ring), kStageBytes,
+                                    hipHostMallocDefault));
+  const size_t len = (bytes + 255) & ~size_t(255);
+  if (S.head + len > kStageBytes) S.head = 0;
+  const size_t b = S.head, e = b + len;
+  // Wait for (and retire) staged copies that overlap [b, e) or have finished.
+  for (size_t k = 0; k < S.inflight.size();) {
+    Staged& st = S.inflight[k];
+    const bool overlap = st.begin < e && b < st.end;
+    if (overlap) KK_HIP(hipEventSynchronize(st.done));
+    if (overlap || hipEventQuery(st.done) == hipSuccess) {
+      S.spare.push_back(st.done);
+      S.inflight[k] = S.inflight.back();
+      S.inflight.pop_back();
+    } else {
+      ++k;
+    }
+  }
+  std::memcpy(S.ring + b, src, bytes);
+  KK_HIP(hipMemcpyAsync(dst, S.ring + b, bytes, hipMemcpyHostToDevice, ctx().stream));
+  hipEvent_t ev;
+  if (!S.spare.empty()) {
+    ev = S.spare.back();
+    S.spare.pop_back();
+  } else {
+    KK_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  }
+  KK_HIP(hipEventRecord(ev, ctx().stream));
+  S.inflight.push_back(Staged{b, e, ev});
+  S.head = e;
+  return KK_OK;
+}
+
+static void staging_release() {
+  Staging& S = staging();
+  for (auto& st : S.inflight) S.spare.push_back(st.done);
+  S.inflight.clear();
+  for (hipEvent_t ev : S.spare) (void)hipEventDestroy(ev);
+  S.spare.clear();
+  if (S.ring) (void)hipHostFree(S.ring);
+  S.ring = nullptr;
+  S.head = 0;
+}
+
 // ----------------------------------------------------------------- events
 static hipEvent_t g_events[KK_MAX_EVENTS];
 static bool g_event_made[KK_MAX_EVENTS];
@@ -312,6 +392,7 @@ int kk_shutdown(void) {
   (void)hipStreamSynchronize(c.stream);
   destroy_graphs();
   pool_release_all();
+  staging_release();
   for (int i = 0; i < KK_MAX_EVENTS; ++i)
     if (g_event_made[i]) { (void)hipEventDestroy(g_events[i]); g_event_made[i] = false; }
   (void)hipStreamDestroy(c.stream);
@@ -425,8 +506,18 @@ int kk_upload(void* dst, const void* src, size_t bytes) {
   KK_TRY(not_capturing("kk_upload"));
   if (!bytes) return KK_OK;
   if (!dst || !src) return set_error(KK_E_ARG, "kk_upload: NULL pointer");
+  // The host buffer belongs to the caller, who may release it on return: its
+  // bytes are captured (kernel arguments or the staging ring) before that.
+  if (bytes <= kUploadArgBytes) {
+    UploadArgs a;
+    a.dst = static_cast<uint8_t*>(dst);
+    a.n = static_cast<uint32_t>(bytes);
+    std::memcpy(a.data, src, bytes);
+    hipLaunchKernelGGL(upload_small_kernel, dim3(1), dim3(256), 0, ctx().stream, a);
+    return check_launch("upload_small_kernel");
+  }
+  if (bytes <= kStageBytes / 4) return stage_upload(dst, src, bytes);
   KK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx().stream));
-  // The host buffer belongs to the caller, who may release it on return.
   KK_HIP(hipStreamSynchronize(ctx().stream));
   return KK_OK;
 }

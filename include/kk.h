@@ -80,7 +80,11 @@ int kk_pool_stats(size_t* live_bytes, size_t* pooled_bytes,
                   size_t* peak_live_bytes);
 int kk_pool_trim(size_t budget_bytes);
 /* Host <-> device copies (gpu.gd:88-103 create_buffer / read_f32).
- * Both return after the copy has completed. */
+ * kk_upload returns as soon as the source may be reused (its bytes are
+ * captured in kernel arguments or a pinned staging ring) without waiting for
+ * the stream; the device copy runs in stream order before any later op.
+ * Uploads above 16 MB complete before returning.  kk_download returns after
+ * the copy (and all earlier work on the stream) has completed. */
 int kk_upload(void* dst_device, const void* src_host, size_t bytes);
 int kk_download(void* dst_host, const void* src_device, size_t bytes);
 

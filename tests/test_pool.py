@@ -63,3 +63,25 @@ def test_trim(gpu):
     gpu.pool_trim(0)
     live2, pooled2, _ = gpu.pool_stats()
     assert pooled2 == 0 and live2 == live
+
+
+def test_async_uploads_capture_the_host_bytes(gpu):
+    """kk_upload returns without waiting for the stream: the host buffer is
+    overwritten right after each call, through both upload paths (kernel
+    arguments for small uploads, the pinned staging ring for larger ones,
+    enough of them to wrap the ring), and every device copy must still hold
+    the bytes it was given."""
+    import ctypes
+    lib = gpu._lib
+    host = np.zeros(1 << 20, np.float32)  # 4 MB, reused for every upload
+    outs, want = [], []
+    sizes = [1, 7, 512, 600, 3000, 1 << 18, 1 << 20] + [1 << 20] * 20
+    for k, n in enumerate(sizes):
+        host[:n] = np.arange(n, dtype=np.float32) * 0.5 + k
+        t = gpu.DeviceTensor.empty((n,), np.float32)
+        lib.call("kk_upload", ctypes.c_void_p(t.ptr), host.ctypes.data_as(ctypes.c_void_p), n * 4)
+        outs.append(t)
+        want.append(host[:n].copy())
+        host[:n] = -1.0  # overwrite at once
+    for t, w in zip(outs, want):
+        assert np.array_equal(t.numpy(), w)
