@@ -17,7 +17,21 @@ def _d(t):
 
 
 def broadcast_shape(*shapes):
-    return tuple(np.broadcast_shapes(*[tuple(s) for s in shapes]))
+    """numpy's broadcast rule (right-aligned; 1 stretches; else must match)."""
+    if len(shapes) == 2 and tuple(shapes[0]) == tuple(shapes[1]):
+        return tuple(shapes[0])
+    rank = max(len(s) for s in shapes)
+    out = [1] * rank
+    for s in shapes:
+        off = rank - len(s)
+        for i, d in enumerate(s):
+            d = int(d)
+            o = out[off + i]
+            if o == 1:
+                out[off + i] = d
+            elif d != 1 and d != o:
+                raise ValueError(f"shapes {shapes} do not broadcast")
+    return tuple(out)
 
 
 # ------------------------------------------------------------ elementwise

@@ -8,6 +8,7 @@ the reference's Reshape/Transpose/Squeeze/Unsqueeze/Slice/Split branches do
 (kk_alloc/kk_free) and goes back to it when the last view is dropped.
 """
 import ctypes
+import math
 
 import numpy as np
 
@@ -91,11 +92,11 @@ class DeviceTensor:
 
     def __init__(self, storage, shape, dtype, strides=None, offset=0):
         self.storage = storage
-        self.shape = tuple(int(d) for d in shape)
-        self.dtype = np.dtype(dtype)
+        self.shape = tuple(map(int, shape))
+        self.dtype = dtype if isinstance(dtype, np.dtype) else np.dtype(dtype)
         if self.dtype not in NP_TO_CODE:
             raise TypeError(f"unsupported device dtype {self.dtype}")
-        self.strides = tuple(int(s) for s in strides) if strides is not None \
+        self.strides = tuple(map(int, strides)) if strides is not None \
             else _contig_strides(self.shape)
         self.offset = int(offset)
         self.host = None  # cached host value of a constant uploaded once
@@ -107,7 +108,7 @@ class DeviceTensor:
     @classmethod
     def empty(cls, shape, dtype=np.float32):
         shape = tuple(int(d) for d in shape)
-        n = int(np.prod(shape, dtype=np.int64)) if shape else 1
+        n = math.prod(shape)
         return cls(Storage(n * np.dtype(dtype).itemsize), shape, dtype)
 
     @classmethod
@@ -134,7 +135,7 @@ class DeviceTensor:
 
     @property
     def size(self):
-        return int(np.prod(self.shape, dtype=np.int64)) if self.shape else 1
+        return math.prod(self.shape)
 
     @property
     def code(self):
@@ -197,9 +198,9 @@ class DeviceTensor:
     def reshape(self, shape):
         shape = list(int(d) for d in shape)
         if -1 in shape:
-            known = int(np.prod([d for d in shape if d != -1], dtype=np.int64))
+            known = math.prod(d for d in shape if d != -1)
             shape[shape.index(-1)] = self.size // known if known else 0
-        if int(np.prod(shape, dtype=np.int64)) != self.size:
+        if math.prod(shape) != self.size:
             raise ValueError(f"cannot reshape {self.shape} into {tuple(shape)}")
         src = self if self.is_contiguous() else self.contiguous()
         return src._view(shape, _contig_strides(shape))

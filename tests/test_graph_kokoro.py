@@ -166,3 +166,32 @@ def test_repeat_is_identical(run8):
     gold, wav, _, pg = run8
     again = pg.run(gold["ids"], gold["style"], 1.0)
     np.testing.assert_array_equal(again, wav)
+
+
+def test_alternating_runs_repeat_and_pool_plateau(run8, gpu):
+    """Five runs alternating the full input and a short one, as the
+    reference's repeat test does (tests/test_repeat.gd:51-112): identical
+    input gives identical bits (drift exactly 0), no NaN, not silent.  The
+    pool plateaus (tests/test_memory.gd:57-68: regrowth <= 10%): after the
+    first full and short runs, further runs allocate nothing new."""
+    kkg = importlib.import_module("best-tts-godot_amd.graph")
+    gold, wav8, _, pg = run8
+    ids3, style3, _ = kkg.synth_inputs(3, 1)
+    first = {}
+    pooled_after_warm = None
+    for k in range(5):
+        full = k % 2 == 0
+        wav = pg.run(gold["ids"], gold["style"], 1.0) if full else pg.run(ids3, style3, 1.0)
+        w = np.asarray(wav)
+        assert np.isfinite(w).all() and np.abs(w).max() > 0
+        key = "full" if full else "short"
+        if key in first:
+            np.testing.assert_array_equal(w, first[key])
+        else:
+            first[key] = w
+        live, pooled, peak = gpu.pool_stats()
+        if k == 1:
+            pooled_after_warm = live + pooled
+        elif k > 1:
+            assert live + pooled <= 1.10 * pooled_after_warm, (k, live + pooled, pooled_after_warm)
+    np.testing.assert_array_equal(first["full"], wav8)
