@@ -13,7 +13,7 @@
 //
 // Layout: the weights become wT[Cout][Kw][CinP] and the activations
 // xT[N][Lp][CinP] (time-major, channels contiguous, CinP = Cin rounded up
-// to 32 with zero channels), so each MFMA operand fragment -- 16 channels
+// to 64 with zero channels), so each MFMA operand fragment -- 16 channels
 // of one tap at one output row or time step -- is one 16-byte load.  The
 // prep kernels also produce sum_k a_k per output channel and
 // sum_ci b[t][ci] per time step for the epilogue.
@@ -26,8 +26,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kTileM = 128;  // output channels per block (2 waves x 64)
-constexpr int kTileN = 128;  // output time steps per block (2 waves x 64)
-constexpr int kCinAlign = 32;
+constexpr int kCinAlign = 64;   // channels per chunk: two 32-deep MFMA steps
+constexpr int kRowPitch = 80;   // LDS bytes per 64-channel row (16-byte pad: staggered banks)
 
 // wT[co][tap][ci] = offset weight (0 for padding rows/channels);
 // wsum[co] = sum of the offset weights; wzo[co] = offset weight zero point.
@@ -134,62 +134,109 @@ struct ConvI8Args {
   const float* scale;   // 1 or Cout values
   int64_t scale_n;
   int64_t Cout, CinP, Kw, s, d, Lp, Lout, Kreal;
+  int W;                // time rows of a block's input window
 };
 
-// Block: 4 waves as 2 (channels) x 2 (time); wave tile 64 x 64 as 2 x 2
-// MFMA tiles of 32 x 32.  Lane (r, g) = (lane % 32, lane / 32) supplies
-// A[r][16g .. 16g+15] and B[16g .. 16g+15][r] of each 32 x 32 x 32 step;
-// D(i, j) lands in lane j + 32 ((i / 4) % 2), register (i / 8) 4 + i % 4.
+// Block: 128 output channels x TN output steps, 4 waves as 2 (channels) x
+// 2 (time), wave tile 64 x TN/2 as 2 x TN/64 MFMA tiles of 32 x 32.  For each
+// 64-channel chunk the block stages its whole input window -- the
+// ((TN - 1) s + (K - 1) d + 1) time rows every tap reads, each tap shifted by
+// tap * d -- in LDS once, and streams the 128 x 64 weight tile of each tap
+// through a double buffer (the next tap's tile is fetched into registers
+// while this tap's MFMAs run).  Lane (r, g) = (lane % 32, lane / 32) reads
+// A[r][16g .. 16g+15] and B[16g .. 16g+15][r] of each 32 x 32 x 32 step
+// from LDS; D(i, j) lands in lane j + 32 ((i / 4) % 2), register
+// (i / 8) 4 + i % 4.
+// TN (128 or 64) output steps per block; a wave covers TN / 2 of them.
+template <int TN>
 __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  constexpr int NI = TN / 64;  // 32-wide MFMA tiles per wave along time
+  extern __shared__ __align__(16) int8_t conv_lds[];
+  int8_t* Bw = conv_lds;                             // [W][kRowPitch]
+  int8_t* As = conv_lds + A.W * kRowPitch;           // [2][kTileM][kRowPitch]
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r = lane & 31, g = lane >> 5;
-  const int64_t co0 = static_cast<int64_t>(blockIdx.y) * kTileM + (wv >> 1) * 64;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTileN + (wv & 1) * 64;
+  const int wm = wv >> 1, wn = wv & 1;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTileM;
+  const int64_t nb = static_cast<int64_t>(blockIdx.x) * TN;
   const int64_t b = blockIdx.z;
   const int8_t* xT = A.xT + b * A.Lp * A.CinP;
-  const int8_t* wrow0 = A.wT + (co0 + r) * A.Kw * A.CinP + 16 * g;
-  const int8_t* wrow1 = wrow0 + 32 * A.Kw * A.CinP;
-  const int64_t t0 = (n0 + r) * A.s, t1 = (n0 + 32 + r) * A.s;
-  v16i acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
-  for (int64_t tap = 0; tap < A.Kw; ++tap) {
-    // Time rows past the output's end are clamped in bounds; their results
-    // are never stored.
-    int64_t ta = t0 + tap * A.d, tb = t1 + tap * A.d;
-    ta = ta < A.Lp ? ta : A.Lp - 1;
-    tb = tb < A.Lp ? tb : A.Lp - 1;
-    const int8_t* x0 = xT + ta * A.CinP + 16 * g;
-    const int8_t* x1 = xT + tb * A.CinP + 16 * g;
-    const int8_t* w0 = wrow0 + tap * A.CinP;
-    const int8_t* w1 = wrow1 + tap * A.CinP;
-    for (int64_t c0 = 0; c0 < A.CinP; c0 += 32) {
-      const v4i a0 = *reinterpret_cast<const v4i*>(w0 + c0);
-      const v4i a1 = *reinterpret_cast<const v4i*>(w1 + c0);
-      const v4i b0 = *reinterpret_cast<const v4i*>(x0 + c0);
-      const v4i b1 = *reinterpret_cast<const v4i*>(x1 + c0);
-      acc00 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, acc00, 0, 0, 0);
-      acc01 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b1, acc01, 0, 0, 0);
-      acc10 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b0, acc10, 0, 0, 0);
-      acc11 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, acc11, 0, 0, 0);
+  const int64_t tw0 = nb * A.s;
+  // weight-tile loader: 128 rows x four 16-byte pieces, two per thread
+  auto load_a = [&](int64_t tap, int64_t c0, v4i (&reg)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = tid + 256 * j, row = q >> 2, c = q & 3;
+      reg[j] = *reinterpret_cast<const v4i*>(A.wT + ((m0 + row) * A.Kw + tap) * A.CinP + c0 +
+                                              16 * c);
+    }
+  };
+  auto store_a = [&](int buf, const v4i (&reg)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int q = tid + 256 * j, row = q >> 2, c = q & 3;
+      *reinterpret_cast<v4i*>(As + (buf * kTileM + row) * kRowPitch + 16 * c) = reg[j];
+    }
+  };
+  v16i acc[2][NI] = {};
+  for (int64_t c0 = 0; c0 < A.CinP; c0 += kCinAlign) {
+    // The input window; rows past the signal's end are clamped in bounds
+    // (their outputs are never stored).
+    for (int q = tid; q < A.W * 4; q += 256) {
+      const int row = q >> 2, c = q & 3;
+      int64_t t = tw0 + row;
+      t = t < A.Lp ? t : A.Lp - 1;
+      *reinterpret_cast<v4i*>(Bw + row * kRowPitch + 16 * c) =
+          *reinterpret_cast<const v4i*>(xT + t * A.CinP + c0 + 16 * c);
+    }
+    v4i ra[2];
+    load_a(0, c0, ra);
+    store_a(0, ra);
+    __syncthreads();
+    for (int64_t tap = 0; tap < A.Kw; ++tap) {
+      const int buf = static_cast<int>(tap & 1);
+      if (tap + 1 < A.Kw) load_a(tap + 1, c0, ra);
+      const int8_t* Ab = As + buf * kTileM * kRowPitch;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int col = ks * 32 + 16 * g;
+        v4i af[2], bf[NI];
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+          af[mi] = *reinterpret_cast<const v4i*>(Ab + (wm * 64 + mi * 32 + r) * kRowPitch + col);
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const int64_t row = (wn * (TN / 2) + ni * 32 + r) * A.s + tap * A.d;
+          bf[ni] = *reinterpret_cast<const v4i*>(Bw + row * kRowPitch + col);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
+      }
+      if (tap + 1 < A.Kw) store_a(buf ^ 1, ra);
+      __syncthreads();
     }
   }
   const int xz = (A.xzp ? static_cast<int>(A.xzp[0]) : 0) - 128;
   const int32_t* xs = A.xs + b * A.Lp;
   const int64_t obase = b * A.Cout * A.Lout;
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni) {
-    const int64_t l = n0 + 32 * ni + r;
+  for (int ni = 0; ni < NI; ++ni) {
+    const int64_t l = nb + wn * (TN / 2) + 32 * ni + r;
     if (l >= A.Lout) continue;
     int S = 0;  // sum_k b_k of this output column
     for (int64_t tap = 0; tap < A.Kw; ++tap) S += xs[l * A.s + tap * A.d];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
-      const v16i& acc = mi == 0 ? (ni == 0 ? acc00 : acc01) : (ni == 0 ? acc10 : acc11);
 #pragma unroll
       for (int reg = 0; reg < 16; ++reg) {
-        const int64_t co = co0 + 32 * mi + 8 * (reg / 4) + 4 * g + (reg % 4);
+        const int64_t co = m0 + wm * 64 + 32 * mi + 8 * (reg / 4) + 4 * g + (reg % 4);
         if (co >= A.Cout) continue;
         const int wz = A.wzo[co];
-        const int v = acc[reg] - xz * A.wsum[co] - wz * S + static_cast<int>(A.Kreal) * wz * xz;
+        const int v = acc[mi][ni][reg] - xz * A.wsum[co] - wz * S +
+                      static_cast<int>(A.Kreal) * wz * xz;
         if (A.outf) {
           const int vb = A.bias ? v + A.bias[co] : v;
           A.outf[obase + co * A.Lout + l] =
@@ -203,6 +250,19 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
 }
 
 }  // namespace
+
+static int64_t conv_window(int64_t tn, int64_t stride, int64_t dilation, int64_t K) {
+  return (tn - 1) * stride + (K - 1) * dilation + 1;
+}
+
+// The time tile (128, else 64) whose input window fits 64 KB of LDS beside
+// the weight double buffer; 0 if neither does.
+static int conv_tile_n(int64_t stride, int64_t dilation, int64_t K) {
+  for (int tn : {128, 64})
+    if (conv_window(tn, stride, dilation, K) * kRowPitch + 2 * kTileM * kRowPitch <= 65536)
+      return tn;
+  return 0;
+}
 
 // Shapes and zero points of ConvInteger (ref_runtime.py:130-134); fills
 // *Lout.  Both zero points must be per tensor, as the reference reads them
@@ -249,8 +309,13 @@ static int check_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk
   if (Cin * K > 32768)
     return set_error(KK_E_UNSUPPORTED, "%s: Cin*K = %lld exceeds 32768", who,
                      (long long)(Cin * K));
-  if (N > 65535 || ceil_div(Lout, kTileN) > 0x7fffffff)
+  if (N > 65535 || ceil_div(Lout, 64) > 0x7fffffff)
     return set_error(KK_E_UNSUPPORTED, "%s: grid too large", who);
+  // a block's input window must fit LDS beside the weight double buffer
+  if (conv_tile_n(stride, dilation, K) == 0)
+    return set_error(KK_E_UNSUPPORTED, "%s: stride %d / dilation %d / kernel %lld: input window "
+                     "of %lld rows does not fit LDS", who, stride, dilation, (long long)K,
+                     (long long)conv_window(64, stride, dilation, K));
   *lout = Lout;
   return KK_OK;
 }
@@ -304,9 +369,13 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     }
     A.Cout = Cout; A.CinP = CinP; A.Kw = Kw; A.s = stride; A.d = dilation; A.Lp = Lp;
     A.Lout = Lout; A.Kreal = Cin * Kw;
-    const dim3 grid(static_cast<unsigned>(ceil_div(Lout, kTileN)),
+    const int tn = conv_tile_n(stride, dilation, Kw);
+    A.W = static_cast<int>(conv_window(tn, stride, dilation, Kw));
+    const size_t lds = static_cast<size_t>(A.W) * kRowPitch + 2 * kTileM * kRowPitch;
+    const dim3 grid(static_cast<unsigned>(ceil_div(Lout, tn)),
                     static_cast<unsigned>(CoutP / kTileM), static_cast<unsigned>(N));
-    hipLaunchKernelGGL(conv_i8_kernel, grid, dim3(256), 0, st, A);
+    if (tn == 128) hipLaunchKernelGGL(conv_i8_kernel<128>, grid, dim3(256), lds, st, A);
+    else hipLaunchKernelGGL(conv_i8_kernel<64>, grid, dim3(256), lds, st, A);
     rc = check_launch("conv_i8_kernel");
   }
   kk_free(ws);  // stream order keeps the workspace alive for the kernels

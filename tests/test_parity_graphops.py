@@ -91,7 +91,7 @@ def test_conv_integer(gpu, oracle, cin, cout, k, L, pad, dil):
 
 
 @pytest.mark.parametrize("case", ["no_zero_points", "int8_weights", "stride2_batch2", "one_output",
-                                  "zp_extremes"])
+                                  "zp_extremes", "stride6_k12"])
 def test_conv_integer_variants(gpu, oracle, case):
     r = rng(13)
     n, cin, cout, k, L, pad, stride = 1, 96, 40, 5, 333, 2, 1
@@ -106,6 +106,8 @@ def test_conv_integer_variants(gpu, oracle, case):
         L, pad = 5, 0
     elif case == "zp_extremes":
         xzp, wzp = np.uint8(255), np.uint8(0)
+    elif case == "stride6_k12":  # the graph's noise conv: a 64-step time tile
+        cin, cout, k, L, pad, stride = 22, 256, 12, 6000, 3, 6
     x = r.integers(0, 256, (n, cin, L)).astype(np.uint8)
     lo, hi = (-128, 128) if wdt == np.int8 else (0, 256)
     w = r.integers(lo, hi, (cout, cin, k)).astype(wdt)
