@@ -116,23 +116,33 @@ __global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x,
 
 // ------------------------------------------------------------------- LSTM
 // One block of 1024 threads per (direction, batch row) runs the whole
-// recurrence; thread j owns gate column j of
+// recurrence of
 //   g = (xw[t] + (wb + rb)) + h @ deq(R),  deq(R) = (q - zp) * scale
 // (op_lstm, ref_runtime.py:137-210; gate order i, o, f, c).
 //
-// R's column j stays in registers for all steps: its 256 int8 values,
-// shifted to u = q + 128, packed four to a word (64 VGPRs), so a
-// multiply-accumulate is one byte-to-float conversion and one FMA.  With
-// z = zp + 128 the column sum is
-//   sum_k h_k (q_k - zp) = sum_k h_k u_k - z * sum_k h_k,
-// and the scale multiplies the result once.  h is broadcast from LDS as
-// float4; sum_k h_k is reduced once per step by the threads that update h.
+// The per-step product h @ (q - zp) runs on the int8 matrix cores, exactly
+// in integers: h is scaled by a power of two (chosen from max|h0| for the
+// first step, 2^30 after it, since |h| = |o tanh(c)| <= 1 from then on),
+// rounded, and split into four signed base-256 digits,
+// which are four rows of the A operand of v_mfma_i32_16x16x64_i8; R's raw
+// int8 values are the B operand and stay in registers for all steps (each
+// wave owns four 16-column tiles: 64 VGPRs).  The four digit sums of a
+// column recombine exactly in int64 (< 2^45), the zero point comes out
+// through the integer sum of the scaled h, and the result is scaled back in
+// double and rounded once to fp32.  The only approximation is the rounding
+// of h to the 2^-s grid (at most 2^-31 once |h| <= 1), far below the fp32
+// rounding of a 256-term dot product.
 constexpr int kLstmThreads = 1024;
 constexpr int kLstmMaxH = kLstmThreads / 4;
+// Steps per chunk of the input projections: a chunk (4 rows of 4H floats,
+// one float4 per thread) is loaded one whole chunk ahead into a double
+// buffer in LDS, so the load's latency is spread over four steps, and the
+// outputs of a chunk leave in one store per thread.
+constexpr int kLstmChunk = 4;
+typedef int lstm_v4i __attribute__((ext_vector_type(4)));
 
 struct LstmArgs {
-  const float* xw;       // [ndir][seq * batch][4H] input projections x @ deq(W)
-  const float* bias;     // [ndir][8H] or NULL
+  const float* xw;       // [ndir][seq * batch][4H] x @ deq(W) + (wb + rb)
   const int8_t* r;       // [ndir][H][4H]
   const void* r_scale;   // [ndir] (or 1 element)
   int r_scale_dt;
@@ -148,93 +158,201 @@ struct LstmArgs {
   int64_t seq, batch, H, ndir;
 };
 
+// A workgroup barrier that orders LDS only: global loads (the prefetched
+// input projections) and stores (the outputs) stay in flight across it,
+// where __syncthreads would wait for them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
-  __shared__ __align__(16) float hs[kLstmMaxH];
+  // R's staging area at set-up, then the double buffer of input projections
+  // [2][kLstmChunk][4H] floats (both 32 KiB)
+  __shared__ __align__(16) unsigned char big[32 * kLstmThreads];
+  __shared__ __align__(16) int8_t hd[4][kLstmMaxH];  // digits of the scaled h
   __shared__ float gs[kLstmThreads];
-  __shared__ float hpart[kLstmMaxH / 64];
+  __shared__ float hring[kLstmChunk][kLstmMaxH];     // this chunk's h, for ys
+  __shared__ float wmax[kLstmMaxH / 64];
+  __shared__ long long wsum[kLstmMaxH / 64];
+  int8_t (*rbuf)[kLstmThreads] = reinterpret_cast<int8_t (*)[kLstmThreads]>(big);
+  float* xs = reinterpret_cast<float*>(big);
   const int H = static_cast<int>(A.H), G4 = 4 * H;
   const int64_t d = blockIdx.x / A.batch, b = blockIdx.x % A.batch;
-  const int j = threadIdx.x;
-  const int lane = j & 63, wv = j >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar addresses
   const float rs = load_as_f32(A.r_scale, A.r_scale_dt, A.r_scale_n > 1 ? d : 0);
-  const float z = 128.0f + (A.r_zp ? load_as_f32(A.r_zp, A.r_zp_dt, A.r_zp_n > 1 ? d : 0) : 0.0f);
+  const long long rz =
+      A.r_zp ? static_cast<long long>(load_as_i64(A.r_zp, A.r_zp_dt, A.r_zp_n > 1 ? d : 0)) : 0;
   const int8_t* R = A.r + d * static_cast<int64_t>(H) * G4;
   const float* xw = A.xw + d * A.seq * A.batch * G4;
-  // Column j of R, as u = q + 128 in bytes; rows k >= H hold 0 (and h_k = 0).
-  uint32_t w[kLstmMaxH / 4];
+  // B fragments: wave wv owns columns [64 wv, 64 wv + 64), four tiles of
+  // 16; lane (n, g) = (lane % 16, lane / 16) holds R[ks*64 + 16g + e][col].
+  // R arrives through LDS in 32-row chunks (coalesced 4-byte loads).
+  lstm_v4i bf[4][4];
 #pragma unroll
-  for (int m = 0; m < kLstmMaxH / 4; ++m) {
-    uint32_t p = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int k = 4 * m + e;
-      if (j < G4 && k < H)
-        p |= static_cast<uint32_t>(static_cast<uint8_t>(R[static_cast<int64_t>(k) * G4 + j]) ^ 0x80u)
-             << (8 * e);
+  for (int chunk = 0; chunk < kLstmMaxH / 32; ++chunk) {
+    __syncthreads();
+    for (int idx = tid; idx < 32 * kLstmThreads / 4; idx += kLstmThreads) {
+      const int row = idx / (kLstmThreads / 4), col4 = idx % (kLstmThreads / 4);
+      const int k = chunk * 32 + row;
+      int word = 0;
+      if (k < H && 4 * col4 < G4)
+        word = *reinterpret_cast<const int*>(R + static_cast<int64_t>(k) * G4 + 4 * col4);
+      reinterpret_cast<int*>(rbuf[row])[col4] = word;
     }
-    w[m] = p;
+    __syncthreads();
+    const int ks = chunk / 2;                // 64-row MFMA k-step (constant once unrolled)
+    const int g = lane >> 4;                 // this lane's 16 rows: ks*64 + 16g ..
+    if ((g >> 1) == (chunk & 1)) {
+      const int r0 = 16 * (g & 1);           // their offset inside the chunk
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int j = (4 * wv + ct) * 16 + (lane & 15);
+        int w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            word |= static_cast<uint32_t>(static_cast<uint8_t>(rbuf[r0 + 4 * q + e][j])) << (8 * e);
+          w[q] = static_cast<int>(word);
+        }
+        bf[ct][ks] = lstm_v4i{w[0], w[1], w[2], w[3]};
+      }
+    }
   }
-  const float bj = (A.bias && j < G4) ? A.bias[d * 2 * G4 + j] + A.bias[d * 2 * G4 + G4 + j] : 0.0f;
-  float c = 0.0f, h0 = 0.0f;
-  if (j < H) {
-    h0 = A.init_h ? A.init_h[(d * A.batch + b) * H + j] : 0.0f;
-    c = A.init_c ? A.init_c[(d * A.batch + b) * H + j] : 0.0f;
+  float h = 0.0f, c = 0.0f;
+  if (tid < H) {
+    h = A.init_h ? A.init_h[(d * A.batch + b) * H + tid] : 0.0f;
+    c = A.init_c ? A.init_c[(d * A.batch + b) * H + tid] : 0.0f;
   }
-  if (j < kLstmMaxH) {
-    hs[j] = h0;
-    const float sv = wave_sum(h0);
-    if (lane == 0) hpart[wv] = sv;
+  // Chunk k holds the projections of steps 4k .. 4k+3; thread tid < 4H
+  // moves float4 (tid % H) of the row of step 4k + tid / H.  Offsets from
+  // the block's own rows are 32-bit (the host checks the sizes).
+  const int seq = static_cast<int>(A.seq);
+  const int c_t = tid < G4 ? tid : G4 - 1;  // threads past 4H repeat the last float4
+  const int c_sl = c_t / H, c_c4 = c_t % H;
+  // Byte offsets below 2^32 from block-uniform bases: scalar-base
+  // addressing, no 64-bit address registers held across the loop.
+  const char* xw_b = reinterpret_cast<const char*>(xw + b * G4);
+  char* ys_b = reinterpret_cast<char*>(A.ys + (d * A.batch + b) * H);
+  const uint32_t xw_row = static_cast<uint32_t>(A.batch * G4 * sizeof(float));
+  const uint32_t ys_row = static_cast<uint32_t>(A.ndir * A.batch * H * sizeof(float));
+  auto time_of = [&](int step) { return d == 0 ? step : seq - 1 - step; };
+  // Unconditional (rows past the sequence read its last row, never used):
+  // a load under a condition leaves a register copy behind it that waits
+  // for the data at once.
+  auto load_chunk = [&](int k) {
+    int step = k * kLstmChunk + c_sl;
+    step = step < seq ? step : seq - 1;
+    const uint32_t off = static_cast<uint32_t>(time_of(step)) * xw_row + 16u * static_cast<uint32_t>(c_c4);
+    return *reinterpret_cast<const float4*>(xw_b + off);
+  };
+  auto put_chunk = [&](int k, float4 v) {
+    if (tid < G4) reinterpret_cast<float4*>(xs + ((k & 1) * kLstmChunk + c_sl) * G4)[c_c4] = v;
+  };
+  auto flush_chunk = [&](int k) {  // ys rows of chunk k from hring
+    const int step = k * kLstmChunk + c_sl;
+    if (tid < G4 && step < seq) {
+      const uint32_t off = static_cast<uint32_t>(time_of(step)) * ys_row + 4u * static_cast<uint32_t>(c_c4);
+      *reinterpret_cast<float*>(ys_b + off) = hring[c_sl][c_c4];
+    }
+  };
+  // The first step's scale comes from max |h0| (the initial state may be
+  // anything); |h * 2^shift| < 2^30.
+  if (tid < kLstmMaxH) {
+    const float m = wave_max(tid < H ? fabsf(h) : 0.0f);
+    if (lane == 0) wmax[wv] = m;
+  }
+  __syncthreads();  // also ends every read of R's staging area
+  int shift;
+  {
+    int ex = 0;
+    (void)frexpf(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])), &ex);
+    shift = 30 - ex;
+  }
+  float4 pf = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (seq > 0) {
+    put_chunk(0, load_chunk(0));
+    pf = load_chunk(1);  // in flight through chunk 0
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): nothing loaded before the loop stays pending in it
+  for (int step = 0; step < seq; ++step) {
+    const int s = step % kLstmChunk, kc = step / kLstmChunk;
+    // keep the fragments where they are (no rematerialisation across steps)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(bf[ct][ks]));
+    // (b) scale, round and split h into digits (and, with a zero point, the
+    // integer sum of the scaled h).  h * 2^shift is exact in fp32 and below
+    // 2^30 in magnitude, so it rounds to an int exactly.
+    if (tid < kLstmMaxH) {
+      int v = tid < H ? static_cast<int>(rintf(ldexpf(h, shift))) : 0;
+      const int v0 = v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int dg = ((v + 128) & 255) - 128;
+        hd[i][tid] = static_cast<int8_t>(dg);
+        v = (v - dg) >> 8;
+      }
+      if (rz != 0) {
+        long long sum = v0;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (lane == 0) wsum[wv] = sum;
+      }
+    }
+    lds_barrier();
+    if (s == 0 && step > 0) flush_chunk(kc - 1);  // hring is rewritten after the next barrier
+    const long long hsum = rz != 0 ? (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]) : 0;
+    // (c) gates.  A row i carries digit i % 4 (rows 4q .. 4q+3 repeat the
+    // four digits), so tile ct's digit sums for its column n land in every
+    // lane group q: lane n + 16q, registers 0..3.  Lane l takes tile l / 16,
+    // i.e. column 64 wv + l, and applies that gate's activation itself.
+    lstm_v4i acc[4] = {};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const lstm_v4i a = *reinterpret_cast<const lstm_v4i*>(&hd[lane & 3][ks * 64 + 16 * (lane >> 4)]);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        acc[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bf[ct][ks], acc[ct], 0, 0, 0);
+    }
+    {
+      const int q = lane >> 4;
+      const lstm_v4i r = q == 0 ? acc[0] : (q == 1 ? acc[1] : (q == 2 ? acc[2] : acc[3]));
+      const int j = 64 * wv + lane;
+      if (j < G4) {
+        const long long dot = static_cast<long long>(r[0]) + (static_cast<long long>(r[1]) << 8) +
+                              (static_cast<long long>(r[2]) << 16) +
+                              (static_cast<long long>(r[3]) << 24);
+        const float hr = static_cast<float>(ldexp(static_cast<double>(dot - rz * hsum), -shift));
+        const float pre = xs[((kc & 1) * kLstmChunk + s) * G4 + j] + hr * rs;  // (xw + (wb + rb)) + h @ deq(R)
+        gs[j] = j < 3 * H ? 1.0f / (1.0f + expf(-pre)) : tanhf(pre);  // i, o, f: sigmoid; c: tanh
+      }
+    }
+    lds_barrier();
+    // (d) cell update of unit tid
+    if (tid < H) {
+      c = gs[2 * H + tid] * c + gs[tid] * gs[3 * H + tid];
+      h = gs[H + tid] * tanhf(c);
+      hring[s][tid] = h;
+    }
+    // Chunk kc + 1 goes into the buffer chunk kc - 1 used (its last reader
+    // passed this step's barriers); chunk kc + 2 starts loading.
+    if (s == kLstmChunk - 1) {
+      put_chunk(kc + 1, pf);
+      pf = load_chunk(kc + 2);
+    }
+    shift = 30;  // from now on |h| = |o tanh(c)| <= 1
   }
   __syncthreads();
-  float hsum = (hpart[0] + hpart[1]) + (hpart[2] + hpart[3]);
-  const float4* hs4 = reinterpret_cast<const float4*>(hs);
-  for (int64_t step = 0; step < A.seq; ++step) {
-    const int64_t t = d == 0 ? step : A.seq - 1 - step;
-    // Keep the packed column packed: without this the compiler hoists the
-    // 256 byte-to-float conversions out of the step loop and spills them.
-#pragma unroll
-    for (int m = 0; m < kLstmMaxH / 4; ++m) asm volatile("" : "+v"(w[m]));
-    if (j < G4) {
-      const float xv = xw[(t * A.batch + b) * G4 + j] + bj;
-      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-#pragma unroll
-      for (int m = 0; m < kLstmMaxH / 4; ++m) {
-        const float4 h4 = hs4[m];
-        const uint32_t p = w[m];
-        a0 = __builtin_fmaf(h4.x, static_cast<float>(p & 0xffu), a0);
-        a1 = __builtin_fmaf(h4.y, static_cast<float>((p >> 8) & 0xffu), a1);
-        a2 = __builtin_fmaf(h4.z, static_cast<float>((p >> 16) & 0xffu), a2);
-        a3 = __builtin_fmaf(h4.w, static_cast<float>(p >> 24), a3);
-      }
-      const float acc = ((a0 + a1) + (a2 + a3)) - z * hsum;
-      gs[j] = xv + acc * rs;
-    }
-    __syncthreads();
-    if (j < kLstmMaxH) {
-      float h = 0.0f;
-      if (j < H) {
-        const float ig = 1.0f / (1.0f + expf(-gs[j]));
-        const float og = 1.0f / (1.0f + expf(-gs[H + j]));
-        const float fg = 1.0f / (1.0f + expf(-gs[2 * H + j]));
-        const float cc = tanhf(gs[3 * H + j]);
-        c = fg * c + ig * cc;
-        h = og * tanhf(c);
-        hs[j] = h;
-        A.ys[((t * A.ndir + d) * A.batch + b) * H + j] = h;
-        if (step == A.seq - 1) {
-          if (A.yh) A.yh[(d * A.batch + b) * H + j] = h;
-          if (A.yc) A.yc[(d * A.batch + b) * H + j] = c;
-        }
-      }
-      const float sv = wave_sum(h);
-      if (lane == 0) hpart[wv] = sv;
-    }
-    __syncthreads();
-    hsum = (hpart[0] + hpart[1]) + (hpart[2] + hpart[3]);
-  }
-  if (A.seq == 0 && j < H) {
-    if (A.yh) A.yh[(d * A.batch + b) * H + j] = h0;
-    if (A.yc) A.yc[(d * A.batch + b) * H + j] = c;
+  if (seq > 0) flush_chunk((seq - 1) / kLstmChunk);
+  if (tid < H) {
+    if (A.yh) A.yh[(d * A.batch + b) * H + tid] = h;
+    if (A.yc) A.yc[(d * A.batch + b) * H + tid] = c;
   }
 }
 
@@ -447,6 +565,8 @@ int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const
   if (H < 1 || H > kLstmMaxH)
     return set_error(KK_E_UNSUPPORTED, "kk_lstm: hidden size %lld (1..%d)", (long long)H, kLstmMaxH);
   if (numel(ys) != seq * ndir * batch * H) return set_error(KK_E_ARG, "kk_lstm: ys shape");
+  if (seq * ndir * batch * 4 * H >= (int64_t{1} << 30))  // the kernel's 32-bit byte offsets
+    return set_error(KK_E_UNSUPPORTED, "kk_lstm: seq * dir * batch * 4H must stay below 2^30");
   const int64_t nws = numel(w_scale), nrs = numel(r_scale);
   if ((nws != 1 && nws != ndir) || (nrs != 1 && nrs != ndir))
     return set_error(KK_E_ARG, "kk_lstm: scales need 1 or dir elements");
@@ -459,10 +579,13 @@ int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const
       KK_TRY(f32_contig(t, "state"));
       if (numel(t) != ndir * batch * H) return set_error(KK_E_ARG, "kk_lstm: state shape");
     }
-  // Input projections xw[d] = x @ deq(W[d]) on the MFMA GEMM.
+  // Input projections xw[d] = x @ deq(W[d]) + (wb[d] + rb[d]) on the MFMA
+  // GEMM and two elementwise adds (the biases summed first, as op_lstm does).
   void* xw = nullptr;
   const int64_t xw_n = ndir * seq * batch * 4 * H;
-  KK_TRY(kk_alloc(sizeof(float) * std::max<int64_t>(xw_n, 1), &xw));
+  const int64_t xw_bytes = ((sizeof(float) * std::max<int64_t>(xw_n, 1) + 255) / 256) * 256;
+  KK_TRY(kk_alloc(static_cast<size_t>(xw_bytes + sizeof(float) * 4 * H), &xw));
+  float* bsum = reinterpret_cast<float*>(static_cast<char*>(xw) + xw_bytes);
   int rc = KK_OK;
   for (int64_t d = 0; d < ndir && rc == KK_OK && seq * batch > 0; ++d) {
     kk_tensor a{}, wd{}, o{}, sc{}, zpt{};
@@ -481,11 +604,27 @@ int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const
       zptr = &zpt;
     }
     rc = kk_gemm(&o, &a, &wd, &sc, zptr, 1.0f);
+    if (rc == KK_OK && b) {
+      kk_tensor wb{}, rb{}, bs{};
+      for (kk_tensor* t : {&wb, &rb, &bs}) {
+        t->dtype = KK_F32; t->rank = 2; t->shape[0] = 1; t->shape[1] = 4 * H;
+        t->strides[0] = 4 * H; t->strides[1] = 1;
+      }
+      wb.data = static_cast<float*>(b->data) + d * 8 * H;
+      rb.data = static_cast<float*>(b->data) + d * 8 * H + 4 * H;
+      bs.data = bsum;
+      rc = kk_binary(KK_OP_ADD, &bs, &wb, &rb);
+      if (rc == KK_OK) {
+        bs.shape[0] = 1;
+        bs.strides[0] = 0;  // broadcast over the rows of xw[d]
+        bs.shape[0] = seq * batch;
+        rc = kk_binary(KK_OP_ADD, &o, &o, &bs);
+      }
+    }
   }
   if (rc == KK_OK) {
     LstmArgs A{};
     A.xw = static_cast<const float*>(xw);
-    A.bias = b ? static_cast<const float*>(b->data) : nullptr;
     A.r = static_cast<const int8_t*>(r->data);
     A.r_scale = r_scale->data; A.r_scale_dt = r_scale->dtype; A.r_scale_n = nrs;
     if (r_zp) { A.r_zp = r_zp->data; A.r_zp_dt = r_zp->dtype; A.r_zp_n = numel(r_zp); }

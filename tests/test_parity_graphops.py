@@ -117,20 +117,24 @@ def test_conv_integer_variants(gpu, oracle, case):
     assert_bitexact(node(gpu, "ConvInteger", ins, at), want, f"ConvInteger {case}")
 
 
-@pytest.mark.parametrize("seq,inp", [(40, 640), (7, 512), (1, 64)])
-def test_lstm(gpu, oracle, seq, inp):
+@pytest.mark.parametrize("seq,inp,init", [(40, 640, "zero"), (7, 512, "zero"), (1, 64, "zero"),
+                                          (9, 128, "large")])
+def test_lstm(gpu, oracle, seq, inp, init):
+    """Bidirectional int8 LSTM; "large" starts from initial states of
+    |h0| up to ~6 (the first step's scale comes from max|h0|)."""
     r = rng(4)
     H = 256
     x = r.normal(0, 1, (seq, 1, inp)).astype(np.float32)
     w = r.integers(-127, 128, (2, inp, 4 * H)).astype(np.int8)
     rr = r.integers(-127, 128, (2, H, 4 * H)).astype(np.int8)
     b = r.normal(0, 0.05, (2, 8 * H)).astype(np.float32)
-    h0 = np.zeros((2, 1, H), np.float32)
+    h0 = (np.zeros((2, 1, H)) if init == "zero" else r.normal(0, 2, (2, 1, H))).astype(np.float32)
     ws = r.uniform(0.002, 0.006, 2).astype(np.float32)
     rs = r.uniform(0.002, 0.006, 2).astype(np.float32)
     wz = np.array([0, 1], np.int8)
     rz = np.array([-1, 0], np.int8)
-    ins = [x, w, rr, b, None, h0, h0, None, ws, wz, rs, rz]
+    c0 = (np.zeros((2, 1, H)) if init == "zero" else r.normal(0, 1, (2, 1, H))).astype(np.float32)
+    ins = [x, w, rr, b, None, h0, c0, None, ws, wz, rs, rz]
     at = {"hidden_size": H, "direction": "bidirectional"}
     got = node(gpu, "DynamicQuantizeLSTM", ins, at, nout=3)
     want = onode(oracle, "DynamicQuantizeLSTM", ins, at, nout=3)
