@@ -38,6 +38,7 @@ METRIC = ("achieved HBM GB/s (% of peak) per op class; audio-sec per wall-sec on
           "Kokoro graph")
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 (vector and MFMA)
+INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
 ROTATE_BYTES = 640 << 20    # > 2x the 256 MB Infinity Cache
 
 
@@ -80,6 +81,22 @@ class Bench:
         ms = ctypes.c_float()
         self.call("kk_event_elapsed", 0, 1, ctypes.byref(ms))
         return ms.value / (reps * len(gids))
+
+    def time_eager(self, fn, sets, reps):
+        """Average ms per call of fn(i) for i in range(sets), called eagerly
+        (for ops that draw scratch from the pool, which a graph recording
+        does not allow)."""
+        for i in range(sets):  # warm (pool blocks, code objects)
+            fn(i)
+        self.kk.sync()
+        self.call("kk_event_record", 0)
+        for _ in range(reps):
+            for i in range(sets):
+                fn(i)
+        self.call("kk_event_record", 1)
+        ms = ctypes.c_float()
+        self.call("kk_event_elapsed", 0, 1, ctypes.byref(ms))
+        return ms.value / (reps * sets)
 
     def replicate(self, t, n):
         """n device copies of t (device-to-device)."""
@@ -197,11 +214,13 @@ def run_gpu(args):
     # ---- per-op lines: one graph per set, each with a single op node
     ops_out = {}
 
-    def per_op(name, fn, nbytes=None, flops=None, reps=20, sets=nsets):
-        # one graph holding the op once per rotating set
-        gid = B.graph(lambda: [fn(i) for i in range(sets)])
-        t_ms = B.time_graphs([gid], reps) / sets
-        B.call("kk_graph_destroy", gid)
+    def per_op(name, fn, nbytes=None, flops=None, reps=20, sets=nsets, eager=False):
+        if eager:
+            t_ms = B.time_eager(fn, sets, reps)
+        else:  # one graph holding the op once per rotating set
+            gid = B.graph(lambda: [fn(i) for i in range(sets)])
+            t_ms = B.time_graphs([gid], reps) / sets
+            B.call("kk_graph_destroy", gid)
         rec = {"us": round(t_ms * 1e3, 3)}
         if nbytes:
             gbs = nbytes / (t_ms * 1e-3) / 1e9
@@ -274,6 +293,19 @@ def run_gpu(args):
     conv_case("conv_i8_512x512_k3_L2400", 512, 512, 3, 2400, 1, 1)
     conv_case("conv_i8_256x256_k3_d1_L2400", 256, 256, 3, 2400, 1, 1)
     conv_case("conv_i8_256x256_k3_d3_L2400", 256, 256, 3, 2400, 3, 3)
+    # ConvInteger on the int8 matrix cores at the 128-id decoder's largest
+    # shape: uint8 x [1,128,431000], uint8 W [128,128,11], pad 5 (the int8
+    # dense peak is 5.0 POP/s).
+    L8 = 431000
+    xq = B.replicate(D(r.integers(0, 256, (1, 128, L8)).astype(np.uint8)), 3)
+    wq8 = D(r.integers(0, 256, (128, 128, 11)).astype(np.uint8))
+    xz8, wz8 = D(np.array(119, np.uint8)), D(np.array(66, np.uint8))
+    oq = [kk.DeviceTensor.empty((1, 128, L8), np.int32) for _ in range(3)]
+    rec = per_op("conv_int8_128x128_k11_L431000", lambda i: B.call(
+        "kk_conv_integer", oq[i].desc(), xq[i].desc(), wq8.desc(), xz8.desc(), wz8.desc(), 1, 1, 5,
+        5, 1), flops=2 * 128 * 128 * 11 * L8, sets=3, reps=10, eager=True)
+    rec["frac_int8_peak"] = round(rec["tflops"] / INT8_PEAK_TOPS, 4)
+    del xq, oq
     xt = B.replicate(D(r.normal(0, 1, (1, 512, 240)).astype(np.float32)), 4)
     wt = D(r.integers(-127, 128, (512, 256, 20)).astype(np.int8))
     sct = D(np.array(0.005, np.float32))

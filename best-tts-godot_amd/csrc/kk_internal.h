@@ -19,7 +19,11 @@ struct Context {
   hipStream_t stream = nullptr;
   int num_cus = 0;
   bool capturing = false;  // between kk_graph_begin and kk_graph_end
+  // Per-row arrival counters of the multi-block row reductions, zero
+  // between launches (the last block of a row resets its counter).
+  int* row_counters = nullptr;
 };
+constexpr int kRowCounters = 65536;
 Context& ctx();
 
 // Thread-local last error; set_error returns `code` so call sites can

@@ -257,8 +257,26 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_long_kernel(float* __restr
   for (int64_t i = g; i < T; i += kRowBlock) orow[i] = apply_affine((xr[i] - mean) / den, ra, af);
 }
 
-// Applies y = affine((x - mean) / den) with per-row (mean, den) from the
-// numpy-order statistics kernels below (long rows).
+// acc = 0; acc += part[b] for b in order (numpy's outer loop over
+// 8192-blocks), by one whole wave: the lanes load 64 partials at once
+// (device-coherent loads: other blocks wrote them), then the sum walks
+// them in order through readlane.  Every lane returns it.
+__device__ __forceinline__ float np_fold(float* part, int nblk) {
+  const int lane = threadIdx.x & 63;
+  float acc = 0.0f;
+  for (int b0 = 0; b0 < nblk; b0 += 64) {
+    const float v = b0 + lane < nblk ? __hip_atomic_load(part + b0 + lane, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0.0f;
+    const int m = nblk - b0 < 64 ? nblk - b0 : 64;
+    for (int j = 0; j < m; ++j)
+      acc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+  }
+  return acc;
+}
+
+// Applies y = affine((x - mean) / den) with per-row (mean, den) =
+// stats[row] from the numpy-order statistics passes below (long rows).
 __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ out,
                                                             const float* __restrict__ x,
                                                             const float2* __restrict__ stats,
@@ -269,13 +287,13 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
   float gamma = 0.0f, beta = 0.0f;
   if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
   const RowAffine ra = row_affine(af, C, c, gamma, beta);
-  const float2 st = stats[row];
+  const float2 st = stats[row];  // (mean, den)
   const float* xr = x + row * T;
   float* orow = out + row * T;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (vec) {
-    for (int64_t i = (blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x) * 4; i < T;
-         i += stride * 4) {
+    for (int64_t i = 4 * i0; i < T; i += stride * 4) {
       const float4 v = ld_stream4(xr + i);
       st_stream4(orow + i, make_float4(apply_affine((v.x - st.x) / st.y, ra, af),
                                        apply_affine((v.y - st.x) / st.y, ra, af),
@@ -619,6 +637,7 @@ __device__ __forceinline__ void np_load_row(float* dst, const float* __restrict_
   }
 }
 
+
 // numpy-order sum of the padded LDS row (n elements) of f(x), acc from 0.
 template <class F>
 __device__ float np_row_sum(const float* row, int n, F f, NpScratch& S) {
@@ -672,29 +691,77 @@ __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__
 }
 
 // Long rows: block (b, row) computes pw of 8192-block b of f(x) into
-// part[row][b]; f is x (mode 0) or (x - mean[row])^2 (mode 1, mean from
-// stats[row].x).
-__global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(float* __restrict__ part,
-                                                               const float* __restrict__ x,
-                                                               int64_t T, int nblk, int mode,
-                                                               const float2* __restrict__ stats,
-                                                               int vec) {
-  __shared__ __align__(16) float lds[kNpBlock + kNpBlock / 16];
+// part[row][b]; f is x (mode 0) or (x - mean)^2 (mode 1, mean in
+// stats[row].x).  The last block of a row to finish (counted in
+// cnt[row * cstride], which it resets) folds the row's partials in block order, acc = 0;
+// acc += part[b] (numpy's loop over 8192-blocks), and writes
+//   mode 0: red_out[row] = acc (or acc / T when red_mean), or without
+//           red_out stats[row].x = acc / T (ReduceMean's division)
+//   mode 1: stats[row].y = sqrt(acc / T + eps)
+// Once its block sum is formed only wave 0 stays: the other waves leave
+// while it publishes the partial and counts.
+__global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
+    float* __restrict__ part, const float* __restrict__ x, int64_t T, int nblk, int mode,
+    float2* __restrict__ stats, int* __restrict__ cnt, int cstride, float* __restrict__ red_out,
+    int red_mean, float eps) {
   __shared__ NpScratch S;
   const int64_t row = blockIdx.y;
+  cnt += row * cstride;  // counters spaced apart: the rows' atomics do not share a line
   const int b = blockIdx.x;
   const int64_t lo = static_cast<int64_t>(b) * kNpBlock;
   const int m = static_cast<int>(T - lo < kNpBlock ? T - lo : kNpBlock);
-  np_load_row(lds, x + row * T + lo, m, vec);
-  __syncthreads();
+  const float mean = mode == 1 ? stats[row].x : 0.0f;
+  auto f = [&](float e) {
+    if (mode == 0) return e;
+    const float d = e - mean;
+    return d * d;
+  };
+  const float* xb = x + row * T + lo;
   float s;
-  if (mode == 0) {
-    s = np_block_sum([&](int i) { return lds[np_pad(i)]; }, m, S);
-  } else {
-    const float mean = stats[row].x;
-    s = np_block_sum([&](int i) { const float d = lds[np_pad(i)] - mean; return d * d; }, m, S);
+  if (m == kNpBlock) {
+    // A whole block straight from memory into the summation order: lane j
+    // of leaf q (eight lanes per 128-element leaf) holds elements
+    // q*128 + 8k + j, k = 0..15, its accumulator's terms in order.
+    const int q = threadIdx.x >> 3, j = threadIdx.x & 7;
+    float v[kNpLeaf / 8];
+#pragma unroll
+    for (int k = 0; k < kNpLeaf / 8; ++k) v[k] = xb[q * kNpLeaf + 8 * k + j];
+    float r = f(v[0]);
+#pragma unroll
+    for (int k = 1; k < kNpLeaf / 8; ++k) r += f(v[k]);
+    r += __shfl_xor(r, 1, 64);   // leaf q: ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7))
+    r += __shfl_xor(r, 2, 64);
+    r += __shfl_xor(r, 4, 64);
+    r += __shfl_xor(r, 8, 64);   // leaves 8w .. 8w+7 of wave w, balanced
+    r += __shfl_xor(r, 16, 64);
+    r += __shfl_xor(r, 32, 64);
+    if ((threadIdx.x & 63) == 0) S.wave[threadIdx.x >> 6] = r;
+    __syncthreads();
+    if (threadIdx.x >= 64) return;
+    s = ((S.wave[0] + S.wave[1]) + (S.wave[2] + S.wave[3])) +
+        ((S.wave[4] + S.wave[5]) + (S.wave[6] + S.wave[7]));
+  } else {  // the row's last, partial block: the general tree, from memory
+    s = np_block_sum([&](int e) { return f(xb[e]); }, m, S);
+    if (threadIdx.x >= 64) return;
   }
-  if (threadIdx.x == 0) part[row * nblk + b] = s;
+  // wave 0: the partial goes to the device-coherent level (past this XCD's
+  // L2) and has landed before the count moves
+  int last = 0;
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(part + row * nblk + b, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nblk - 1;
+  }
+  if (__shfl(last, 0, 64)) {
+    const float acc = np_fold(part + row * nblk, nblk);
+    if (threadIdx.x == 0) {
+      const float n = static_cast<float>(T);
+      if (mode == 1) stats[row].y = sqrtf(acc / n + eps);
+      else if (red_out) red_out[row] = red_mean ? acc / n : acc;
+      else stats[row].x = acc / n;
+      *cnt = 0;
+    }
+  }
 }
 
 // Rows of at most 128 elements (one numpy leaf), one thread per row.
@@ -719,23 +786,6 @@ __global__ void np_leaf_rows_kernel(float* __restrict__ out, const float* __rest
   }
   res = 0.0f + res;  // the reduction's accumulator starts at 0
   out[row] = mean ? res / static_cast<float>(n) : res;
-}
-
-// acc = 0; acc += part[row][b] in block order; then
-//   mode 0: out[row] = acc          mode 1: out[row] = acc / T
-//   mode 2: stats[row].x = acc / T  mode 3: stats[row].y = sqrt(acc / T + eps)
-__global__ void np_fold_kernel(float* __restrict__ out, float2* __restrict__ stats,
-                               const float* __restrict__ part, int64_t rows, int nblk,
-                               int64_t T, int mode, float eps) {
-  const int64_t row = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  if (row >= rows) return;
-  float acc = 0.0f;
-  for (int b = 0; b < nblk; ++b) acc += part[row * nblk + b];
-  const float n = static_cast<float>(T);
-  if (mode == 0) out[row] = acc;
-  else if (mode == 1) out[row] = acc / n;
-  else if (mode == 2) stats[row].x = acc / n;
-  else stats[row].y = sqrtf(acc / n + eps);
 }
 
 // General reduction: kept axes (kdims/kst) index the output in order,
@@ -880,6 +930,13 @@ static bool same_shape(const kk_tensor* a, const kk_tensor* b) {
 
 constexpr int64_t kNpRowMax = 15000;  // rows held in LDS (<= 64 KB with padding)
 
+// Spacing of the per-row counters: up to 32 ints (128 bytes) apart.
+static int counter_stride(int64_t rows) {
+  int st = 32;
+  while (st > 1 && rows * st > kRowCounters) st >>= 1;
+  return st;
+}
+
 static size_t np_row_lds(int64_t n) {
   return sizeof(float) * static_cast<size_t>(n + 8 * ceil_div(n, kNpLeaf));
 }
@@ -900,21 +957,16 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
                        0.0f, af, vec ? 1 : 0);
     return check_launch("np_rows_kernel");
   }
-  if (rows > 65535) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)rows);
+  if (rows > kRowCounters) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)rows);
   const int64_t nblk = ceil_div(n, kNpBlock);
   void* part = nullptr;
   KK_TRY(kk_alloc(sizeof(float) * rows * nblk, &part));
   hipLaunchKernelGGL(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
                      dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
-                     static_cast<int>(nblk), 0, static_cast<const float2*>(nullptr), vec ? 1 : 0);
-  int rc = check_launch("np_blocks_kernel");
-  if (rc == KK_OK) {
-    hipLaunchKernelGGL(np_fold_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 64))), dim3(64), 0,
-                       st, out, static_cast<float2*>(nullptr), static_cast<const float*>(part), rows,
-                       static_cast<int>(nblk), n, mean ? 1 : 0, 0.0f);
-    rc = check_launch("np_fold_kernel");
-  }
-  kk_free(part);  // stream order keeps it alive for the fold
+                     static_cast<int>(nblk), 0, static_cast<float2*>(nullptr), ctx().row_counters,
+                     counter_stride(rows), out, mean ? 1 : 0, 0.0f);
+  const int rc = check_launch("np_blocks_kernel");
+  kk_free(part);  // stream order keeps it alive for the kernel
   return rc;
 }
 
@@ -929,34 +981,31 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
                        static_cast<int>(T), 2, eps, af, vec_ok ? 1 : 0);
     return check_launch("np_rows_kernel");
   }
-  if (rows > 65535) return set_error(KK_E_UNSUPPORTED, "instance norm: %lld long rows",
-                                     (long long)rows);
+  if (rows > kRowCounters)
+    return set_error(KK_E_UNSUPPORTED, "instance norm: %lld long rows", (long long)rows);
   const int64_t nblk = ceil_div(T, kNpBlock);
   const int64_t part_bytes = ceil_div(static_cast<int64_t>(sizeof(float)) * rows * nblk, 256) * 256;
   void* ws = nullptr;
   KK_TRY(kk_alloc(static_cast<size_t>(part_bytes + sizeof(float2) * rows), &ws));
   float* part = static_cast<float*>(ws);
   float2* stats = reinterpret_cast<float2*>(static_cast<char*>(ws) + part_bytes);
+  // pass 0: the sums, then the mean; pass 1: the squared deviations' sums,
+  // then sqrt(var + eps); then the normalisation
   const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
-  const dim3 fgrid(static_cast<unsigned>(ceil_div(rows, 64)));
   int rc = KK_OK;
   for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
     hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
-                       static_cast<int>(nblk), pass, static_cast<const float2*>(stats),
-                       vec_ok ? 1 : 0);
+                       static_cast<int>(nblk), pass, stats, ctx().row_counters,
+                       counter_stride(rows), static_cast<float*>(nullptr), 0, eps);
     rc = check_launch("np_blocks_kernel");
-    if (rc != KK_OK) break;
-    hipLaunchKernelGGL(np_fold_kernel, fgrid, dim3(64), 0, st, static_cast<float*>(nullptr), stats,
-                       static_cast<const float*>(part), rows, static_cast<int>(nblk), T, 2 + pass,
-                       eps);
-    rc = check_launch("np_fold_kernel");
   }
   if (rc == KK_OK) {
     const int64_t per_block = kRowBlock * (vec_ok ? 4 : 1) * 8;
     const unsigned gx = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(
         ceil_div(T, per_block), 1 << 16)));
     hipLaunchKernelGGL(instnorm_apply, dim3(gx, static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
-                       st, static_cast<float*>(out->data), xp, stats, C, T, af, vec_ok ? 1 : 0);
+                       st, static_cast<float*>(out->data), xp, static_cast<const float2*>(stats), C,
+                       T, af, vec_ok ? 1 : 0);
     rc = check_launch("instnorm_apply");
   }
   kk_free(ws);  // stream order keeps it alive for the kernels above

@@ -375,6 +375,8 @@ int kk_init(int device) {
   hipDeviceProp_t prop;
   KK_HIP(hipGetDeviceProperties(&prop, device));
   c.num_cus = prop.multiProcessorCount;
+  KK_HIP(hipMalloc(reinterpret_cast<void**>(&c.row_counters), sizeof(int) * kRowCounters));
+  KK_HIP(hipMemset(c.row_counters, 0, sizeof(int) * kRowCounters));
   c.device = device;
   c.ready = true;
   return KK_OK;
@@ -393,6 +395,7 @@ int kk_shutdown(void) {
   destroy_graphs();
   pool_release_all();
   staging_release();
+  if (c.row_counters) { (void)hipFree(c.row_counters); c.row_counters = nullptr; }
   for (int i = 0; i < KK_MAX_EVENTS; ++i)
     if (g_event_made[i]) { (void)hipEventDestroy(g_events[i]); g_event_made[i] = false; }
   (void)hipStreamDestroy(c.stream);
