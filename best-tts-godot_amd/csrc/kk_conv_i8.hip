@@ -11,12 +11,16 @@
 // positions hold b = xz', so they contribute 0 exactly as the reference's
 // zero padding of the shifted input does.
 //
-// Layout: the weights become wT[Cout][Kw][CinP] and the activations
-// xT[N][Lp][CinP] (time-major, channels contiguous, CinP = Cin rounded up
-// to 64 with zero channels), so each MFMA operand fragment -- 16 channels
-// of one tap at one output row or time step -- is one 16-byte load.  The
-// prep kernels also produce sum_k a_k per output channel and
-// sum_ci b[t][ci] per time step for the epilogue.
+// Layout: the weights become wT[Cout][Kw][CinP] (CinP = Cin rounded up to
+// 64 with zero channels) with sum_k a_k per output channel, once per call.
+// The activations stay as they are, uint8 [N][Cin][L]: each block stages
+// the time window its outputs read, 64 channels at a time, into LDS
+// time-major (channels contiguous, offset to int8 on the way), so each
+// MFMA operand fragment -- 16 channels of one tap at one output row or time
+// step -- is one 16-byte LDS read; the same staged rows give
+// sum_ci b[t][ci] for the epilogue.
+#include <type_traits>
+
 #include "kk_internal.h"
 
 namespace kk {
@@ -66,149 +70,179 @@ __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w,
   }
 }
 
-// xT[b][t][ci] = x[b][ci][t - p0] - 128 for t inside the signal, xz - 128 in
-// the padding, 0 in the padding channels; xs[b][t] = sum over real channels.
-// A block owns 64 time steps and walks the channels in tiles of 64: lane l
-// of wave w loads x[ci][t0 + l] for ci = w, w + 4, ... (64 consecutive bytes
-// per load), the tile is transposed through LDS, and each thread stores 16
-// consecutive channels of one time step as one 16-byte store.
-constexpr int kPrepT = 64;   // time steps per block
-constexpr int kPrepC = 64;   // channels per tile
-
-__global__ void __launch_bounds__(256) conv_i8_xprep(const uint8_t* __restrict__ x,
-                                                     const uint8_t* __restrict__ xzp,
-                                                     int8_t* __restrict__ xT,
-                                                     int32_t* __restrict__ xs, int64_t Cin,
-                                                     int64_t L, int64_t p0, int64_t Lp,
-                                                     int64_t CinP) {
-  __shared__ int8_t tile[kPrepC][kPrepT + 4];
-  __shared__ int part[4][kPrepT];
-  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kPrepT;
-  const int64_t b = blockIdx.y;
-  const int pad = (xzp ? static_cast<int>(xzp[0]) : 0) - 128;
-  const uint8_t* xb = x + b * Cin * L;
-  // loader: time step t0 + lane
-  const int64_t ts = t0 + lane - p0;
-  const bool inside = ts >= 0 && ts < L;
-  // storer: time step t0 + lane, channels 16 * wv .. 16 * wv + 15 of the tile
-  const int64_t to = t0 + lane;
-  int sum = 0;
-  for (int64_t c0 = 0; c0 < CinP; c0 += kPrepC) {
-#pragma unroll
-    for (int k = 0; k < kPrepC / 4; ++k) {
-      const int r = wv + 4 * k;
-      const int64_t ci = c0 + r;
-      int v = 0;
-      if (ci < Cin) v = inside ? static_cast<int>(xb[ci * L + ts]) - 128 : pad;
-      tile[r][lane] = static_cast<int8_t>(v);
-    }
-    __syncthreads();
-    if (to < Lp && c0 + 16 * wv < CinP) {
-      v4i pack;
-      int8_t* pv = reinterpret_cast<int8_t*>(&pack);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        pv[e] = tile[16 * wv + e][lane];
-        sum += pv[e];
-      }
-      *reinterpret_cast<v4i*>(xT + (b * Lp + to) * CinP + c0 + 16 * wv) = pack;
-    }
-    __syncthreads();
-  }
-  part[wv][lane] = sum;
-  __syncthreads();
-  if (wv == 0 && to < Lp) xs[b * Lp + to] = (part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]);
-}
-
 struct ConvI8Args {
   const int8_t* wT;     // [CoutP][Kw][CinP]
   const int32_t* wsum;  // [CoutP]
-  const int32_t* wzo;   // [CoutP]
-  const int8_t* xT;     // [N][Lp][CinP]
-  const int32_t* xs;    // [N][Lp]
+  const int32_t* wzo;   // [CoutP] (live rows: the tensor's offset zero point)
+  const uint8_t* x;     // [N][Cin][L]
   const uint8_t* xzp;   // one uint8 or NULL
   int32_t* out;         // [N][Cout][Lout] int32, or NULL when outf is set
   float* outf;          // [N][Cout][Lout] float(acc + bias[co]) * scale
   const int32_t* bias;  // [Cout] or NULL
   const float* scale;   // 1 or Cout values
   int64_t scale_n;
-  int64_t Cout, CinP, Kw, s, d, Lp, Lout, Kreal;
-  int W;                // time rows of a block's input window
+  int64_t Cout, Cin, CinP, Kw, s, d, L, p0, Lout, Kreal;
+  int W4;               // time rows staged per block: the window plus alignment slack
+  int aligned;          // rows start 4-byte aligned (L % 4 == 0): dword loads
 };
 
 // Block: 128 output channels x TN output steps, 4 waves as 2 (channels) x
 // 2 (time), wave tile 64 x TN/2 as 2 x TN/64 MFMA tiles of 32 x 32.  For each
 // 64-channel chunk the block stages its whole input window -- the
 // ((TN - 1) s + (K - 1) d + 1) time rows every tap reads, each tap shifted by
-// tap * d -- in LDS once, and streams the 128 x 64 weight tile of each tap
-// through a double buffer (the next tap's tile is fetched into registers
-// while this tap's MFMAs run).  Lane (r, g) = (lane % 32, lane / 32) reads
-// A[r][16g .. 16g+15] and B[16g .. 16g+15][r] of each 32 x 32 x 32 step
-// from LDS; D(i, j) lands in lane j + 32 ((i / 4) % 2), register
-// (i / 8) 4 + i % 4.
+// tap * d -- in LDS once, straight from the uint8 activations: a thread
+// loads four time steps of four channels (one dword per channel), swaps the
+// 4 x 4 bytes into four time rows and flips the top bit (u - 128 = u ^ 0x80);
+// positions in the padding hold xz - 128.  The 128 x 64 weight tile of
+// each tap streams through a double buffer (the next tap's tile is fetched
+// into registers while this tap's MFMAs run).  Lane (r, g) =
+// (lane % 32, lane / 32) reads A[r][16g .. 16g+15] and B[16g .. 16g+15][r]
+// of each 32 x 32 x 32 step from LDS; D(i, j) lands in lane j + 32 ((i / 4)
+// % 2), register (i / 8) 4 + i % 4.  The epilogue's per-channel constants
+// and the staged rows' channel sums sit in LDS.
 // TN (128 or 64) output steps per block; a wave covers TN / 2 of them.
 template <int TN>
 __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
   constexpr int NI = TN / 64;  // 32-wide MFMA tiles per wave along time
   extern __shared__ __align__(16) int8_t conv_lds[];
-  int8_t* Bw = conv_lds;                             // [W][kRowPitch]
-  int8_t* As = conv_lds + A.W * kRowPitch;           // [2][kTileM][kRowPitch]
+  int8_t* Bw = conv_lds;                                          // [W4][kRowPitch]
+  int8_t* As = conv_lds + A.W4 * kRowPitch;                       // [2][kTileM][kRowPitch]
+  int* rs = reinterpret_cast<int*>(As + 2 * kTileM * kRowPitch);  // [W4] channel sums
+  int* cst = rs + A.W4;                                           // [kTileM] constant term
+  float* scl = reinterpret_cast<float*>(cst + kTileM);            // [kTileM] scale
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r = lane & 31, g = lane >> 5;
   const int wm = wv >> 1, wn = wv & 1;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTileM;
   const int64_t nb = static_cast<int64_t>(blockIdx.x) * TN;
   const int64_t b = blockIdx.z;
-  const int8_t* xT = A.xT + b * A.Lp * A.CinP;
-  const int64_t tw0 = nb * A.s;
-  // weight-tile loader: 128 rows x four 16-byte pieces, two per thread
-  auto load_a = [&](int64_t tap, int64_t c0, v4i (&reg)[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int q = tid + 256 * j, row = q >> 2, c = q & 3;
-      reg[j] = *reinterpret_cast<const v4i*>(A.wT + ((m0 + row) * A.Kw + tap) * A.CinP + c0 +
-                                              16 * c);
+  const uint8_t* xb = A.x + b * A.Cin * A.L;
+  const int xz = (A.xzp ? static_cast<int>(A.xzp[0]) : 0) - 128;  // offset x zero point
+  const uint32_t padb = static_cast<uint8_t>(static_cast<int8_t>(xz));
+  const uint32_t padw = padb * 0x01010101u;
+  // staged row 0 is source time a0 (padded time nb*s is source time nb*s - p0);
+  // the window proper starts sh rows in
+  const int64_t a = nb * A.s - A.p0;
+  const int64_t a0 = A.aligned ? (a & ~int64_t{3}) : a;
+  const int sh = static_cast<int>(a - a0);
+  // v = acc + cst[co] - wz * S, with cst = K wz xz - xz sum(a) (+ bias) and
+  // S = sum of b over the receptive field; the weight zero point is one
+  // value for the tensor (every live row of wzo holds it)
+  const int wz = A.wzo[0];
+  if (tid < kTileM) {
+    const int64_t co = m0 + tid;
+    int c = 0;
+    float sc = 0.0f;
+    if (co < A.Cout) {
+      c = static_cast<int>(A.Kreal) * wz * xz - xz * A.wsum[co];
+      if (A.outf) {
+        if (A.bias) c += A.bias[co];
+        sc = A.scale[A.scale_n > 1 ? co : 0];
+      }
     }
+    cst[tid] = c;
+    scl[tid] = sc;
+  }
+  // weight-tile loader: 128 rows x four 16-byte pieces, two per thread
+  // (per-thread bases; a tap or chunk moves them by a uniform offset)
+  const int8_t* wsrc[2];
+  int adst[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int q = tid + 256 * j, row = q >> 2, c = q & 3;
+    wsrc[j] = A.wT + (m0 + row) * A.Kw * A.CinP + 16 * c;
+    adst[j] = row * kRowPitch + 16 * c;
+  }
+  auto load_a = [&](int64_t off, v4i (&reg)[2]) {  // off = tap * CinP + c0
+#pragma unroll
+    for (int j = 0; j < 2; ++j) reg[j] = *reinterpret_cast<const v4i*>(wsrc[j] + off);
   };
   auto store_a = [&](int buf, const v4i (&reg)[2]) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int q = tid + 256 * j, row = q >> 2, c = q & 3;
-      *reinterpret_cast<v4i*>(As + (buf * kTileM + row) * kRowPitch + 16 * c) = reg[j];
-    }
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<v4i*>(As + buf * (kTileM * kRowPitch) + adst[j]) = reg[j];
   };
+  // LDS offsets of this lane's fragments: A rows wm*64 + 32mi + r, B rows
+  // (wn*TN/2 + 32ni + r)*s + tap*d + sh, columns 16g (+32 per k-step)
+  const int a_off = (wm * 64 + r) * kRowPitch + 16 * g;
+  int b_off[NI];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni)
+    b_off[ni] = ((wn * (TN / 2) + ni * 32 + r) * static_cast<int>(A.s) + sh) * kRowPitch + 16 * g;
+  const int tap_step = static_cast<int>(A.d) * kRowPitch;
+  const int ngrp = A.W4 / 4;  // groups of four staged rows
+  // 32-bit staging arithmetic (the host checks Cin * L < 2^31)
+  const int Cin = static_cast<int>(A.Cin), Li = static_cast<int>(A.L);
+  const uint32_t L = static_cast<uint32_t>(A.L);
+  const int a0i = static_cast<int>(a0);
   v16i acc[2][NI] = {};
   for (int64_t c0 = 0; c0 < A.CinP; c0 += kCinAlign) {
-    // The input window; rows past the signal's end are clamped in bounds
-    // (their outputs are never stored).
-    for (int q = tid; q < A.W * 4; q += 256) {
-      const int row = q >> 2, c = q & 3;
-      int64_t t = tw0 + row;
-      t = t < A.Lp ? t : A.Lp - 1;
-      *reinterpret_cast<v4i*>(Bw + row * kRowPitch + 16 * c) =
-          *reinterpret_cast<const v4i*>(xT + t * A.CinP + c0 + 16 * c);
+    // Stage the window: item (tg, cg) = rows 4tg .. 4tg+3 x channels
+    // c0 + 4cg .. 4cg+3.  A wave takes 16 channel groups x 4 consecutive
+    // time groups: its LDS writes of one row offset hit 64 distinct banks,
+    // and each channel row is read 16 contiguous bytes at a time.
+    for (int it = tid; it < ngrp * 16; it += 256) {
+      const int cg = it & 15, tg = it >> 4;
+      const int ts = a0i + 4 * tg;
+      const int ci0 = static_cast<int>(c0) + 4 * cg;
+      uint32_t dw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t v = 0;  // padding channels hold 0
+        if (ci0 + e < Cin) {
+          const uint32_t off = static_cast<uint32_t>(ci0 + e) * L + static_cast<uint32_t>(ts);
+          if (A.aligned) {  // a dword is wholly inside the signal or wholly outside
+            v = (ts >= 0 && ts < Li) ? (*reinterpret_cast<const uint32_t*>(xb + off) ^ 0x80808080u)
+                                     : padw;
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int t = ts + q;
+              const uint32_t by = (t >= 0 && t < Li) ? (static_cast<uint32_t>(xb[off + q]) ^ 0x80u) : padb;
+              v |= by << (8 * q);
+            }
+          }
+        }
+        dw[e] = v;
+      }
+      // 4 x 4 byte transpose (v_perm: bytes 0-3 from the second operand,
+      // 4-7 from the first): word q = the four channels at time 4tg + q
+      const uint32_t t01l = __builtin_amdgcn_perm(dw[1], dw[0], 0x05010400u);
+      const uint32_t t01h = __builtin_amdgcn_perm(dw[1], dw[0], 0x07030602u);
+      const uint32_t t23l = __builtin_amdgcn_perm(dw[3], dw[2], 0x05010400u);
+      const uint32_t t23h = __builtin_amdgcn_perm(dw[3], dw[2], 0x07030602u);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(Bw + 4 * tg * kRowPitch + 4 * cg);
+      dst[0] = __builtin_amdgcn_perm(t23l, t01l, 0x05040100u);
+      dst[kRowPitch / 4] = __builtin_amdgcn_perm(t23l, t01l, 0x07060302u);
+      dst[2 * kRowPitch / 4] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
+      dst[3 * kRowPitch / 4] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
     }
     v4i ra[2];
-    load_a(0, c0, ra);
+    load_a(c0, ra);
     store_a(0, ra);
     __syncthreads();
-    for (int64_t tap = 0; tap < A.Kw; ++tap) {
-      const int buf = static_cast<int>(tap & 1);
-      if (tap + 1 < A.Kw) load_a(tap + 1, c0, ra);
-      const int8_t* Ab = As + buf * kTileM * kRowPitch;
+    // this chunk's share of each staged row's channel sum
+    for (int row = tid; row < A.W4; row += 256) {
+      const int* p = reinterpret_cast<const int*>(Bw + row * kRowPitch);
+      int sum = c0 == 0 ? 0 : rs[row];
+#pragma unroll
+      for (int k = 0; k < kCinAlign / 4; ++k) sum = __builtin_amdgcn_sdot4(p[k], 0x01010101, sum, false);
+      rs[row] = sum;
+    }
+    for (int tap = 0; tap < static_cast<int>(A.Kw); ++tap) {
+      const int buf = tap & 1;
+      if (tap + 1 < A.Kw) load_a((tap + 1) * A.CinP + c0, ra);
+      const int8_t* Ab = As + buf * (kTileM * kRowPitch) + a_off;
+      const int8_t* Bb = Bw + tap * tap_step;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const int col = ks * 32 + 16 * g;
         v4i af[2], bf[NI];
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
-          af[mi] = *reinterpret_cast<const v4i*>(Ab + (wm * 64 + mi * 32 + r) * kRowPitch + col);
+          af[mi] = *reinterpret_cast<const v4i*>(Ab + mi * 32 * kRowPitch + 32 * ks);
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni) {
-          const int64_t row = (wn * (TN / 2) + ni * 32 + r) * A.s + tap * A.d;
-          bf[ni] = *reinterpret_cast<const v4i*>(Bw + row * kRowPitch + col);
-        }
+        for (int ni = 0; ni < NI; ++ni)
+          bf[ni] = *reinterpret_cast<const v4i*>(Bb + b_off[ni] + 32 * ks);
 #pragma unroll
         for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -219,34 +253,50 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
       __syncthreads();
     }
   }
-  const int xz = (A.xzp ? static_cast<int>(A.xzp[0]) : 0) - 128;
-  const int32_t* xs = A.xs + b * A.Lp;
-  const int64_t obase = b * A.Cout * A.Lout;
+  int zS[NI];  // wz * sum_k b_k of each of this lane's output columns
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int64_t l = nb + wn * (TN / 2) + 32 * ni + r;
-    if (l >= A.Lout) continue;
-    int S = 0;  // sum_k b_k of this output column
-    for (int64_t tap = 0; tap < A.Kw; ++tap) S += xs[l * A.s + tap * A.d];
+    const int j = wn * (TN / 2) + 32 * ni + r;
+    int S = 0;
+    for (int tap = 0; tap < static_cast<int>(A.Kw); ++tap)
+      S += rs[sh + j * static_cast<int>(A.s) + tap * static_cast<int>(A.d)];
+    zS[ni] = wz * S;
+  }
+  // outputs from the block's corner, 32-bit byte offsets (the host checks
+  // that a batch's output stays below 2 GiB); a block wholly inside the
+  // output skips the per-element bounds checks
+  char* ob = reinterpret_cast<char*>(A.outf ? static_cast<void*>(A.outf) : static_cast<void*>(A.out)) +
+             4 * ((b * A.Cout + m0) * A.Lout + nb);
+  const uint32_t lout4 = static_cast<uint32_t>(4 * A.Lout);
+  const bool full = m0 + kTileM <= A.Cout && nb + TN <= A.Lout;
+  const int c_rem = static_cast<int>(A.Cout - m0), l_rem = static_cast<int>(A.Lout - nb);
+  const int lane_c = wm * 64 + 4 * g, lane_j = wn * (TN / 2) + r;
+  const uint32_t lane_off = static_cast<uint32_t>(lane_c) * lout4 + 4u * static_cast<uint32_t>(lane_j);
+  auto epilogue = [&](auto full_tile) {
+    constexpr bool kFull = decltype(full_tile)::value;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
       for (int reg = 0; reg < 16; ++reg) {
-        const int64_t co = m0 + wm * 64 + 32 * mi + 8 * (reg / 4) + 4 * g + (reg % 4);
-        if (co >= A.Cout) continue;
-        const int wz = A.wzo[co];
-        const int v = acc[mi][ni][reg] - xz * A.wsum[co] - wz * S +
-                      static_cast<int>(A.Kreal) * wz * xz;
-        if (A.outf) {
-          const int vb = A.bias ? v + A.bias[co] : v;
-          A.outf[obase + co * A.Lout + l] =
-              static_cast<float>(vb) * A.scale[A.scale_n > 1 ? co : 0];
-        } else {
-          A.out[obase + co * A.Lout + l] = v;
+        const int cr = 32 * mi + 8 * (reg / 4) + (reg % 4);  // constant once unrolled
+        const int cl = lane_c + cr;
+        if (!kFull && cl >= c_rem) continue;
+        const int c = cst[cl];
+        const float sc = scl[cl];
+        const uint32_t roff = lane_off + static_cast<uint32_t>(cr) * lout4;
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          if (!kFull && lane_j + 32 * ni >= l_rem) continue;
+          const int v = acc[mi][ni][reg] + c - zS[ni];
+          char* dst = ob + (roff + 128u * ni);
+          if (A.outf) *reinterpret_cast<float*>(dst) = static_cast<float>(v) * sc;
+          else *reinterpret_cast<int*>(dst) = v;
         }
       }
     }
-  }
+  };
+  if (full) epilogue(std::true_type{});
+  else epilogue(std::false_type{});
 }
 
 }  // namespace
@@ -255,12 +305,21 @@ static int64_t conv_window(int64_t tn, int64_t stride, int64_t dilation, int64_t
   return (tn - 1) * stride + (K - 1) * dilation + 1;
 }
 
-// The time tile (128, else 64) whose input window fits 64 KB of LDS beside
-// the weight double buffer; 0 if neither does.
+// Staged rows: the window plus up to 3 rows of alignment slack, in groups of 4.
+static int64_t conv_rows(int64_t tn, int64_t stride, int64_t dilation, int64_t K) {
+  return ceil_div(conv_window(tn, stride, dilation, K) + 3, 4) * 4;
+}
+
+// LDS of a block: the staged rows and their channel sums, the weight double
+// buffer, the per-channel epilogue constants.
+static size_t conv_lds(int64_t rows) {
+  return static_cast<size_t>(rows * (kRowPitch + 4) + 2 * kTileM * kRowPitch + 2 * kTileM * 4);
+}
+
+// The time tile (128, else 64) whose block fits 64 KB of LDS; 0 if neither does.
 static int conv_tile_n(int64_t stride, int64_t dilation, int64_t K) {
   for (int tn : {128, 64})
-    if (conv_window(tn, stride, dilation, K) * kRowPitch + 2 * kTileM * kRowPitch <= 65536)
-      return tn;
+    if (conv_lds(conv_rows(tn, stride, dilation, K)) <= 65536) return tn;
   return 0;
 }
 
@@ -311,6 +370,9 @@ static int check_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk
                      (long long)(Cin * K));
   if (N > 65535 || ceil_div(Lout, 64) > 0x7fffffff)
     return set_error(KK_E_UNSUPPORTED, "%s: grid too large", who);
+  if (ceil_div(Cout, kTileM) * kTileM * Lout * 4 >= (int64_t{1} << 31) ||  // 32-bit offsets
+      (Cin + 64) * (L + 64) >= (int64_t{1} << 31))
+    return set_error(KK_E_UNSUPPORTED, "%s: Cout * Lout or Cin * L too large", who);
   // a block's input window must fit LDS beside the weight double buffer
   if (conv_tile_n(stride, dilation, K) == 0)
     return set_error(KK_E_UNSUPPORTED, "%s: stride %d / dilation %d / kernel %lld: input window "
@@ -327,38 +389,28 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
                      bool outf) {
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], Kw = w->shape[2];
-  const int64_t Lp = L + pad0 + pad1;
   const int64_t Lout = out->shape[2];
   const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
   const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
   auto up = [](int64_t n) { return ceil_div(n, 256) * 256; };
   const int64_t o_wT = 0, o_wsum = o_wT + up(CoutP * Kw * CinP);
-  const int64_t o_wzo = o_wsum + up(CoutP * 4), o_xs = o_wzo + up(CoutP * 4);
-  const int64_t o_xT = o_xs + up(N * Lp * 4), total = o_xT + up(N * Lp * CinP);
+  const int64_t o_wzo = o_wsum + up(CoutP * 4), total = o_wzo + up(CoutP * 4);
   void* ws = nullptr;
   KK_TRY(kk_alloc(static_cast<size_t>(total), &ws));
   char* base = static_cast<char*>(ws);
   int8_t* wT = reinterpret_cast<int8_t*>(base + o_wT);
   int32_t* wsum = reinterpret_cast<int32_t*>(base + o_wsum);
   int32_t* wzo = reinterpret_cast<int32_t*>(base + o_wzo);
-  int32_t* xs = reinterpret_cast<int32_t*>(base + o_xs);
-  int8_t* xT = reinterpret_cast<int8_t*>(base + o_xT);
   hipStream_t st = ctx().stream;
   hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
                      w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
                      w_zp ? numel(w_zp) : 0, wT, wsum, wzo, Cout, Cin, Kw, CinP);
   int rc = check_launch("conv_i8_wprep");
-  const uint8_t* xzp = x_zp ? static_cast<const uint8_t*>(x_zp->data) : nullptr;
-  if (rc == KK_OK) {
-    hipLaunchKernelGGL(conv_i8_xprep, dim3(static_cast<unsigned>(ceil_div(Lp, kPrepT)),
-                                           static_cast<unsigned>(N)),
-                       dim3(256), 0, st, static_cast<const uint8_t*>(x->data), xzp, xT, xs, Cin,
-                       L, static_cast<int64_t>(pad0), Lp, CinP);
-    rc = check_launch("conv_i8_xprep");
-  }
   if (rc == KK_OK) {
     ConvI8Args A{};
-    A.wT = wT; A.wsum = wsum; A.wzo = wzo; A.xT = xT; A.xs = xs; A.xzp = xzp;
+    A.wT = wT; A.wsum = wsum; A.wzo = wzo;
+    A.x = static_cast<const uint8_t*>(x->data);
+    A.xzp = x_zp ? static_cast<const uint8_t*>(x_zp->data) : nullptr;
     if (outf) {
       A.outf = static_cast<float*>(out->data);
       A.bias = bias ? static_cast<const int32_t*>(bias->data) : nullptr;
@@ -367,15 +419,15 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     } else {
       A.out = static_cast<int32_t*>(out->data);
     }
-    A.Cout = Cout; A.CinP = CinP; A.Kw = Kw; A.s = stride; A.d = dilation; A.Lp = Lp;
-    A.Lout = Lout; A.Kreal = Cin * Kw;
+    A.Cout = Cout; A.Cin = Cin; A.CinP = CinP; A.Kw = Kw; A.s = stride; A.d = dilation;
+    A.L = L; A.p0 = pad0; A.Lout = Lout; A.Kreal = Cin * Kw;
+    A.aligned = (L % 4 == 0) && (reinterpret_cast<uintptr_t>(x->data) % 4 == 0);
     const int tn = conv_tile_n(stride, dilation, Kw);
-    A.W = static_cast<int>(conv_window(tn, stride, dilation, Kw));
-    const size_t lds = static_cast<size_t>(A.W) * kRowPitch + 2 * kTileM * kRowPitch;
+    A.W4 = static_cast<int>(conv_rows(tn, stride, dilation, Kw));
     const dim3 grid(static_cast<unsigned>(ceil_div(Lout, tn)),
                     static_cast<unsigned>(CoutP / kTileM), static_cast<unsigned>(N));
-    if (tn == 128) hipLaunchKernelGGL(conv_i8_kernel<128>, grid, dim3(256), lds, st, A);
-    else hipLaunchKernelGGL(conv_i8_kernel<64>, grid, dim3(256), lds, st, A);
+    if (tn == 128) hipLaunchKernelGGL(conv_i8_kernel<128>, grid, dim3(256), conv_lds(A.W4), st, A);
+    else hipLaunchKernelGGL(conv_i8_kernel<64>, grid, dim3(256), conv_lds(A.W4), st, A);
     rc = check_launch("conv_i8_kernel");
   }
   kk_free(ws);  // stream order keeps the workspace alive for the kernels
