@@ -262,6 +262,36 @@ def run_gpu(args):
                                                  None), ebytes, sets=ne)
     del exs, eos
 
+    # The same op classes at the decoder's own activation shapes (the
+    # generator's last two stages for 128 phoneme ids: [1,256,71800] and
+    # [1,128,430800] fp32), where the target of 70% of HBM peak applies.
+    # InstanceNorm+affine is the graph's fused chain (statistics in numpy's
+    # order: three reads and one write of x; its line counts the two
+    # algorithmic passes).
+    for C, T in ((256, 71800), (128, 430800)):
+        nbytes = 4 * C * T
+        nd = max(2, -(-ROTATE_BYTES // (2 * nbytes)))
+        dx = B.replicate(D(r.normal(0, 1, (1, C, T)).astype(np.float32)), nd)
+        do = [kk.DeviceTensor.empty((1, C, T)) for _ in range(nd)]
+        dc = D(r.normal(0, 1, (1, C, 1)).astype(np.float32))
+        da = D(r.uniform(0.5, 2, (1, C, 1)).astype(np.float32))
+        dg = D((1 + 0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32))
+        tag = f"1x{C}x{T}"
+        per_op(f"copy_{tag}", lambda i: B.call("kk_copy", do[i].desc(), dx[i].desc()), 2 * nbytes,
+               sets=nd)
+        per_op(f"add_{tag}", lambda i: B.call("kk_binary", opc["Add"], do[i].desc(), dx[i].desc(),
+                                               dc.desc()), 2 * nbytes + 4 * C, sets=nd)
+        per_op(f"mul_{tag}", lambda i: B.call("kk_binary", opc["Mul"], do[i].desc(), dx[i].desc(),
+                                               dc.desc()), 2 * nbytes + 4 * C, sets=nd)
+        per_op(f"leakyrelu_{tag}", lambda i: B.call("kk_unary", opc["LeakyRelu"], do[i].desc(),
+                                                     dx[i].desc(), 0.2), 2 * nbytes, sets=nd)
+        per_op(f"snake_{tag}", lambda i: B.call("kk_snake", do[i].desc(), dx[i].desc(), da.desc(),
+                                                 None), 2 * nbytes + 4 * C, sets=nd)
+        per_op(f"instnorm_affine_{tag}", lambda i: B.call(
+            "kk_instance_norm_scale_shift", do[i].desc(), dx[i].desc(), dg.desc(), dc.desc(), 1e-5, 0,
+            0.0), 2 * nbytes + 8 * C, sets=nd, reps=10, eager=True)
+        del dx, do
+
     # dequant contractions (fp32 semantics; TFLOP/s against the fp32 peak)
     def gemm_case(name, m, k, n, wdt):
         a = B.replicate(D(r.normal(0, 1, (m, k)).astype(np.float32)), 4)

@@ -24,7 +24,7 @@
 #include "kk_internal.h"
 
 namespace kk {
-namespace {
+namespace i8conv {  // named: the kernels keep readable names in profiles
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -299,7 +299,8 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
   else epilogue(std::false_type{});
 }
 
-}  // namespace
+}  // namespace i8conv
+using namespace i8conv;
 
 static int64_t conv_window(int64_t tn, int64_t stride, int64_t dilation, int64_t K) {
   return (tn - 1) * stride + (K - 1) * dilation + 1;
