@@ -167,22 +167,26 @@ struct Affine {
   const float* shift;
   int leaky;
   float alpha;
+  // optional snake after the affine: y + r * sin(a * y)^2, a and r per channel
+  const float* snake_a;
+  const float* snake_r;
 };
 
 struct RowAffine {
-  float mul, add;
+  float mul, add, sa, sr;
   bool has_mul, has_add;
 };
 
 __device__ __forceinline__ RowAffine row_affine(const Affine& af, int64_t C, int64_t c, float gamma,
                                                 float beta) {
-  RowAffine ra{1.0f, 0.0f, false, false};
+  RowAffine ra{1.0f, 0.0f, 0.0f, 0.0f, false, false};
   if (af.mode == 1 || af.mode == 2) {
     ra.mul = gamma + 1.0f; ra.add = beta; ra.has_mul = ra.has_add = true;
   } else if (af.mode == 3) {
     if (af.scale) { ra.mul = af.scale[c]; ra.has_mul = true; }
     if (af.shift) { ra.add = af.shift[c]; ra.has_add = true; }
   }
+  if (af.snake_a) { ra.sa = af.snake_a[c]; ra.sr = af.snake_r[c]; }
   return ra;
 }
 
@@ -190,6 +194,10 @@ __device__ __forceinline__ float apply_affine(float q, const RowAffine& ra, cons
   float y = ra.has_mul ? q * ra.mul : q;
   if (ra.has_add) y = y + ra.add;
   if (af.leaky) y = y < 0.0f ? y * af.alpha : y;
+  if (af.snake_a) {  // Mul(alpha, y) -> Sin -> Pow(., 2) -> Mul(recip, .) -> Add(y, .)
+    const float sn = sinf(ra.sa * y);
+    y = y + ra.sr * (sn * sn);
+  }
   return y;
 }
 
@@ -1033,6 +1041,43 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
   return check_launch("instnorm_kernel");
 }
 
+static int instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
+                                     const kk_tensor* scale, const kk_tensor* shift,
+                                     const kk_tensor* snake_a, const kk_tensor* snake_r, float eps,
+                                     int leaky, float alpha) {
+  KK_TRY(require_ready());
+  KK_TRY(check_f32_contig(x, "x"));
+  KK_TRY(check_f32_contig(out, "out"));
+  if (!same_shape(out, x)) return set_error(KK_E_ARG, "instance norm: out shape must equal x");
+  if (x->rank < 2) return set_error(KK_E_ARG, "instance norm: x must be [N, C, ...T]");
+  const int64_t C = x->shape[x->rank - 2];
+  Affine af{};
+  af.mode = 3;
+  af.leaky = leaky ? 1 : 0;
+  af.alpha = alpha;
+  for (const kk_tensor* t : {scale, shift}) {
+    if (!t) continue;
+    KK_TRY(check_f32_contig(t, t == scale ? "scale" : "shift"));
+    if (numel(t) != C)
+      return set_error(KK_E_ARG, "instance norm: scale/shift need C = %lld elements",
+                       (long long)C);
+  }
+  af.scale = scale ? static_cast<const float*>(scale->data) : nullptr;
+  af.shift = shift ? static_cast<const float*>(shift->data) : nullptr;
+  if (snake_a) {
+    for (const kk_tensor* t : {snake_a, snake_r}) {
+      KK_TRY(check_f32_contig(t, t == snake_a ? "snake alpha" : "snake recip"));
+      if (numel(t) != C)
+        return set_error(KK_E_ARG, "instance norm: snake alpha/recip need C = %lld elements",
+                         (long long)C);
+    }
+    af.snake_a = static_cast<const float*>(snake_a->data);
+    af.snake_r = static_cast<const float*>(snake_r->data);
+  }
+  StyleArgs sa{};
+  return instnorm_launch(out, x, eps, af, sa);
+}
+
 }  // namespace kk
 
 using namespace kk;
@@ -1063,27 +1108,15 @@ int kk_instance_norm_affine(const kk_tensor* out, const kk_tensor* x, const kk_t
 
 int kk_instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x, const kk_tensor* scale,
                                  const kk_tensor* shift, float eps, int leaky, float alpha) {
-  KK_TRY(require_ready());
-  KK_TRY(check_f32_contig(x, "x"));
-  KK_TRY(check_f32_contig(out, "out"));
-  if (!same_shape(out, x)) return set_error(KK_E_ARG, "instance norm: out shape must equal x");
-  if (x->rank < 2) return set_error(KK_E_ARG, "instance norm: x must be [N, C, ...T]");
-  const int64_t C = x->shape[x->rank - 2];
-  Affine af{};
-  af.mode = 3;
-  af.leaky = leaky ? 1 : 0;
-  af.alpha = alpha;
-  for (const kk_tensor* t : {scale, shift}) {
-    if (!t) continue;
-    KK_TRY(check_f32_contig(t, t == scale ? "scale" : "shift"));
-    if (numel(t) != C)
-      return set_error(KK_E_ARG, "instance norm: scale/shift need C = %lld elements",
-                       (long long)C);
-  }
-  af.scale = scale ? static_cast<const float*>(scale->data) : nullptr;
-  af.shift = shift ? static_cast<const float*>(shift->data) : nullptr;
-  StyleArgs sa{};
-  return instnorm_launch(out, x, eps, af, sa);
+  return instance_norm_scale_shift(out, x, scale, shift, nullptr, nullptr, eps, leaky, alpha);
+}
+
+int kk_instance_norm_scale_shift_snake(const kk_tensor* out, const kk_tensor* x,
+                                       const kk_tensor* scale, const kk_tensor* shift,
+                                       const kk_tensor* alpha, const kk_tensor* recip, float eps) {
+  if (!alpha || !recip)
+    return set_error(KK_E_ARG, "kk_instance_norm_scale_shift_snake: alpha and recip are required");
+  return instance_norm_scale_shift(out, x, scale, shift, alpha, recip, eps, 0, 0.0f);
 }
 
 int kk_adain(const kk_tensor* out, const kk_tensor* x, const kk_tensor* style, const kk_tensor* w,

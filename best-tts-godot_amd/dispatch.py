@@ -348,6 +348,18 @@ def dispatch(op, node_input, node_output, at, env):
         out = ops.instance_norm_scale_shift(_f32(to_device(x)), _f32(to_device(y)),
                                             _f32(to_device(inp(2))), at["epsilon"],
                                             at.get("leaky_alpha"))
+    elif op == "InstanceNormSnake":
+        # the InstanceNorm chain (+ Mul scale, Add shift), then the snake chain on its
+        # output; inputs x, scale, shift ("" if absent), alpha, recip (C values each).
+        xd, a, rc = _f32(to_device(x)), _f32(to_device(inp(3))), _f32(to_device(inp(4)))
+        C = xd.shape[-2] if len(xd.shape) >= 2 else 0
+        if a.size == C and rc.size == C:
+            out = ops.instance_norm_scale_shift_snake(xd, _f32(to_device(y)), _f32(to_device(inp(2))),
+                                                      a, rc, at["epsilon"])
+        else:  # alpha/recip not per channel: the two fused ops one after the other
+            yv = ops.instance_norm_scale_shift(xd, _f32(to_device(y)), _f32(to_device(inp(2))),
+                                               at["epsilon"], None)
+            out = ops.snake(yv, a, rc)
     elif op == "AdaIN":
         # inputs: x, style, W, bias; attribute epsilon.
         out = ops.adain(to_device(x), to_device(y), to_device(inp(2)),

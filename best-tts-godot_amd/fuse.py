@@ -9,6 +9,7 @@ each of which would otherwise read and write a full decoder activation
   InstanceNorm          ReduceMean -> Sub -> Mul(d, d) -> ReduceMean -> Add(eps)
                         -> Sqrt -> Div -> [Mul(scale)] -> [Add(shift)] -> [LeakyRelu]
   snake                 Mul(alpha, x) -> Sin -> Pow(2) -> Mul(recip) -> Add(x)
+  InstanceNorm + snake  the two above back to back (the decoder's residual blocks)
 
 `fuse` rewrites each chain whose intermediate tensors have no other reader
 into one pseudo-node that `dispatch` runs as one kernel (the reference's
@@ -89,7 +90,47 @@ def fuse(nodes, weights, protect=()):
         elif i not in used:
             out.append(node)
             groups.append([i])
-    return out, groups
+    return _merge_norm_snake(out, groups, protect)
+
+
+def _merge_norm_snake(out, groups, protect):
+    """An InstanceNorm chain (without LeakyRelu) whose output only a snake
+    chain reads becomes one InstanceNormSnake node, at the snake's place:
+    inputs x, scale, shift, alpha, recip (the decoder's residual blocks:
+    norm -> snake -> quantised conv)."""
+    readers = defaultdict(list)
+    for k, (_op, ins, _outs, _at) in enumerate(out):
+        for n in ins:
+            if n:
+                readers[n].append(k)
+    merged = {}  # snake index -> norm index
+    for k, (op, ins, outs, at) in enumerate(out):
+        if op != "InstanceNormScaleShift" or "leaky_alpha" in at:
+            continue
+        y = outs[0]
+        r = readers.get(y, [])
+        if y in protect or len(set(r)) != 1:
+            continue
+        j = r[0]
+        s_op, s_ins, _s_outs, _s_at = out[j]
+        if s_op == "Snake" and len(s_ins) == 3 and s_ins[0] == y and y not in s_ins[1:]:
+            merged[j] = k
+    if not merged:
+        return out, groups
+    dropped = set(merged.values())
+    new_out, new_groups = [], []
+    for k, node in enumerate(out):
+        if k in dropped:
+            continue
+        if k in merged:
+            n_op, n_ins, _n_outs, n_at = out[merged[k]]
+            n_ins = list(n_ins) + [""] * (3 - len(n_ins))
+            node = ("InstanceNormSnake", n_ins[:3] + list(node[1][1:3]), [node[2][0]], dict(n_at))
+            new_groups.append(groups[merged[k]] + groups[k])
+        else:
+            new_groups.append(groups[k])
+        new_out.append(node)
+    return new_out, new_groups
 
 
 def _match_qconv(nodes, i, only_reader, other, claim):

@@ -273,6 +273,18 @@ def instance_norm_scale_shift(x, scale=None, shift=None, eps=1e-5, leaky_alpha=N
     return out
 
 
+def instance_norm_scale_shift_snake(x, scale, shift, alpha, recip, eps=1e-5):
+    """instance_norm_scale_shift, then the snake y + recip[c]*sin(alpha[c]*y)^2,
+    in one pass; alpha and recip hold C values."""
+    x = x.contiguous()
+    out = DeviceTensor.empty(x.shape, np.float32)
+    _lib.call("kk_instance_norm_scale_shift_snake", out.desc(), x.desc(),
+              _d(scale.contiguous() if scale is not None else None),
+              _d(shift.contiguous() if shift is not None else None), alpha.contiguous().desc(),
+              recip.contiguous().desc(), float(eps))
+    return out
+
+
 # ------------------------------------------------ recurrent / vocoder
 def lstm(x, w, r, b, init_h, init_c, w_scale, w_zp, r_scale, r_zp, hidden_size, bidirectional):
     x = x.contiguous()

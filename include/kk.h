@@ -169,6 +169,13 @@ int kk_instance_norm_affine(const kk_tensor* out, const kk_tensor* x,
 int kk_instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
                                  const kk_tensor* scale, const kk_tensor* shift, float eps,
                                  int leaky, float alpha);
+/* The same chain followed by the graph's snake chain on its output,
+ * Mul(alpha, y) -> Sin -> Pow(2) -> Mul(recip) -> Add(y) (ref_runtime.py
+ * :446-463; kk_snake): z = y + recip[c] * sin(alpha[c] * y)^2, one pass
+ * instead of two.  alpha and recip hold C floats. */
+int kk_instance_norm_scale_shift_snake(const kk_tensor* out, const kk_tensor* x,
+                                       const kk_tensor* scale, const kk_tensor* shift,
+                                       const kk_tensor* alpha, const kk_tensor* recip, float eps);
 /* AdaIN with the style Linear fused: h = style . W + b with W [S, 2C]
  * (any strides), then kk_instance_norm_affine on x [N,C,T].  bias may be
  * NULL.  W may be f32, f16 or int8/uint8 with w_scale/w_zp (per tensor or

@@ -147,15 +147,17 @@ def _graph_nodes():
 def test_fusion_pass_on_the_kokoro_graph():
     """The fusion pass finds every quantised conv tail (87), InstanceNorm
     chain (64 of 65: one has a Transpose inside) and snake (48) of the
-    packed graph, keeps a valid topological order, and never drops a tensor
-    that a node outside its group reads."""
+    packed graph -- 42 norm chains feed a snake alone and merge with it --
+    keeps a valid topological order, and never drops a tensor that a node
+    outside its group reads."""
     import importlib
     from collections import Counter
     fz = importlib.import_module("best-tts-godot_amd.fuse")
     g, nodes, weights = _graph_nodes()
     fused, groups = fz.fuse(nodes, weights, {str(g["output"])})
     kinds = Counter(n[0] for n in fused)
-    assert (kinds["QConvScaled"], kinds["InstanceNormScaleShift"], kinds["Snake"]) == (87, 64, 48)
+    assert (kinds["QConvScaled"], kinds["InstanceNormScaleShift"], kinds["Snake"],
+            kinds["InstanceNormSnake"]) == (87, 22, 6, 42)
     covered = sorted(i for grp in groups for i in grp)
     assert covered == list(range(len(nodes)))  # every original node exactly once
     produced = {}

@@ -100,6 +100,29 @@ def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
     assert_bitexact(got, want, f"InstanceNorm chain C={C} T={T}")
 
 
+@pytest.mark.parametrize("C,T,affine", [(128, 40000, True), (256, 7180, True), (64, 999, False)])
+def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
+    """The InstanceNorm chain with its output read only by a snake chain:
+    one InstanceNormSnake launch (long rows and rows held in LDS)."""
+    r = rng(24)
+    x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
+    alpha = r.uniform(0.5, 2, (1, C, 1)).astype(np.float16)
+    inputs = {"x": x, "g": (1 + 0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32),
+              "b": (0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32)}
+    weights = {"ax": np.array([2], np.int64),
+               "eps": np.array(1e-5, np.float16).astype(np.float32), "a": alpha,
+               "rc": (np.float32(1) / alpha.astype(np.float32)).astype(np.float16),
+               "two": np.array(2.0, np.float16)}
+    nodes, y = norm_chain(affine, False)
+    nodes += [("Mul", ["a", y], ["t"], {}), ("Sin", ["t"], ["s"], {}),
+              ("Pow", ["s", "two"], ["p"], {}), ("Mul", ["rc", "p"], ["q"], {}),
+              ("Add", [y, "q"], ["z"], {})]
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, "z")
+    assert [n[0] for n in fused] == ["InstanceNormSnake"]
+    # the norm is bit-exact; sin differs from numpy's by ulps (the snake bar)
+    assert_close(got, want, 1e-5, floor_rel=1e-6, what=f"InstanceNorm+snake C={C} T={T}")
+
+
 @pytest.mark.parametrize("C,T", [(128, 30000), (256, 5001)])
 def test_snake_chain(gpu, oracle, C, T):
     r = rng(23)
