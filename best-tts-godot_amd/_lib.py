@@ -123,13 +123,23 @@ def load(path=LIB_PATH):
     return lib
 
 
+_bound = {}  # name -> bound entry point
+
+
+def raise_error(name, rc):
+    """Raise KKError for status `rc` of entry point `name`."""
+    msg = load().kk_last_error().decode(errors="replace")
+    raise KKError(name, rc, msg)
+
+
 def call(name, *args):
     """Call entry point `name`; raise KKError on a non-zero status."""
-    lib = load()
-    rc = getattr(lib, name)(*args)
+    fn = _bound.get(name)
+    if fn is None:
+        fn = _bound[name] = getattr(load(), name)
+    rc = fn(*args)
     if rc != 0:
-        msg = lib.kk_last_error().decode(errors="replace")
-        raise KKError(name, rc, msg)
+        raise_error(name, rc)
     return rc
 
 

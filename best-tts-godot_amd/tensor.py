@@ -56,25 +56,39 @@ def pool_trim(budget_bytes=0):
     _lib.call("kk_pool_trim", int(budget_bytes))
 
 
+_alloc_out = ctypes.c_void_p()  # out-parameter of kk_alloc (the walk is single-threaded)
+_alloc_ref = ctypes.byref(_alloc_out)
+_fast = {}  # bound entry points of the allocation path
+
+
 class Storage:
     """One pooled device buffer."""
 
     __slots__ = ("ptr", "nbytes", "__weakref__")
 
     def __init__(self, nbytes):
-        init()
-        p = ctypes.c_void_p()
-        _lib.call("kk_alloc", max(int(nbytes), 1), ctypes.byref(p))
-        self.ptr = p.value
-        self.nbytes = int(nbytes)
+        if _state["device"] is None:
+            init()
+        alloc = _fast.get("kk_alloc")
+        if alloc is None:
+            alloc = _fast["kk_alloc"] = _lib.load().kk_alloc
+        nbytes = int(nbytes)
+        rc = alloc(nbytes if nbytes > 0 else 1, _alloc_ref)
+        if rc:
+            _lib.raise_error("kk_alloc", rc)
+        self.ptr = _alloc_out.value
+        self.nbytes = nbytes
 
     def __del__(self):
         ptr, self.ptr = getattr(self, "ptr", None), None
         if ptr and _lib._lib is not None:
             try:
-                _lib._lib.kk_free(ctypes.c_void_p(ptr))
+                _lib._lib.kk_free(ptr)
             except Exception:  # interpreter shutdown: the process frees it
                 pass
+
+
+_PROTOS = {}  # (shape, strides, dtype) -> KKTensor with data unset
 
 
 def _contig_strides(shape):
@@ -107,9 +121,21 @@ class DeviceTensor:
     # ----------------------------------------------------------- creation
     @classmethod
     def empty(cls, shape, dtype=np.float32):
-        shape = tuple(int(d) for d in shape)
-        n = math.prod(shape)
-        return cls(Storage(n * np.dtype(dtype).itemsize), shape, dtype)
+        shape = tuple(map(int, shape))
+        dtype = dtype if isinstance(dtype, np.dtype) else np.dtype(dtype)
+        if dtype not in NP_TO_CODE:
+            raise TypeError(f"unsupported device dtype {dtype}")
+        if len(shape) > _lib.KK_MAX_RANK:
+            raise ValueError(f"rank {len(shape)} exceeds {_lib.KK_MAX_RANK}")
+        t = object.__new__(cls)  # a fresh contiguous tensor: no view checks
+        t.storage = Storage(math.prod(shape) * dtype.itemsize)
+        t.shape = shape
+        t.dtype = dtype
+        t.strides = _contig_strides(shape)
+        t.offset = 0
+        t.host = None
+        t._desc = None
+        return t
 
     @classmethod
     def from_numpy(cls, arr):
@@ -152,15 +178,23 @@ class DeviceTensor:
         return True
 
     def desc(self):
-        """The kk_tensor descriptor (cached; views are immutable)."""
+        """The kk_tensor descriptor (cached; views are immutable).  Descriptors
+        of one (shape, strides, dtype) differ only in the data pointer: each
+        is copied from a cached prototype."""
         if self._desc is None:
-            d = _lib.KKTensor()
-            d.data = self.ptr
-            d.dtype = self.code
-            d.rank = len(self.shape)
-            for i, (n, s) in enumerate(zip(self.shape, self.strides)):
-                d.shape[i] = n
-                d.strides[i] = s
+            key = (self.shape, self.strides, self.dtype)
+            proto = _PROTOS.get(key)
+            if proto is None:
+                proto = _lib.KKTensor()
+                proto.dtype = NP_TO_CODE[self.dtype]
+                proto.rank = len(self.shape)
+                for i, (n, s) in enumerate(zip(self.shape, self.strides)):
+                    proto.shape[i] = n
+                    proto.strides[i] = s
+                if len(_PROTOS) < 4096:
+                    _PROTOS[key] = proto
+            d = _lib.KKTensor.from_buffer_copy(proto)
+            d.data = self.storage.ptr + self.offset * self.dtype.itemsize
             self._desc = d
         return ctypes.byref(self._desc)
 
