@@ -171,6 +171,7 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
     b_off[ni] = ((wn * (TN / 2) + ni * 32 + r) * static_cast<int>(A.s) + sh) * kRowPitch + 16 * g;
   const int tap_step = static_cast<int>(A.d) * kRowPitch;
   const int ngrp = A.W4 / 4;  // groups of four staged rows
+  const int nitems = static_cast<int>(ceil_div(ngrp, 16)) * 256;
   // 32-bit staging arithmetic (the host checks Cin * L < 2^31)
   const int Cin = static_cast<int>(A.Cin), Li = static_cast<int>(A.L);
   const uint32_t L = static_cast<uint32_t>(A.L);
@@ -178,11 +179,12 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
   v16i acc[2][NI] = {};
   for (int64_t c0 = 0; c0 < A.CinP; c0 += kCinAlign) {
     // Stage the window: item (tg, cg) = rows 4tg .. 4tg+3 x channels
-    // c0 + 4cg .. 4cg+3.  A wave takes 16 channel groups x 4 consecutive
-    // time groups: its LDS writes of one row offset hit 64 distinct banks,
-    // and each channel row is read 16 contiguous bytes at a time.
-    for (int it = tid; it < ngrp * 16; it += 256) {
-      const int cg = it & 15, tg = it >> 4;
+    // c0 + 4cg .. 4cg+3.  A wave takes 4 channel groups x 16 consecutive
+    // time groups: one channel of its items is 4 rows x 64 contiguous bytes
+    // (its LDS writes meet 4-way bank conflicts, which cost little).
+    for (int it = tid; it < nitems; it += 256) {
+      const int cg = (it >> 4) & 15, tg = (it & 15) + 16 * (it >> 8);
+      if (tg >= ngrp) continue;
       const int ts = a0i + 4 * tg;
       const int ci0 = static_cast<int>(c0) + 4 * cg;
       uint32_t dw[4];
