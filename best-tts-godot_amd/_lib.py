@@ -88,6 +88,7 @@ PROTOTYPES = {
     "kk_conv_integer_scaled": [_T] * 7 + [_i, _i, _i, _i, _i],
     "kk_instance_norm_scale_shift": [_T, _T, _T, _T, _f, _i, _f],
     "kk_instance_norm_scale_shift_snake": [_T, _T, _T, _T, _T, _T, _f],
+    "kk_instance_norm_quant": [_T, _T, _T, _T, _T, _T, _T, _T, _f, _i, _f],
     "kk_lstm": [_T] * 13 + [_i, _i],
     "kk_stft": [_T, _T, _T, ctypes.c_int64, ctypes.c_int64, _i],
     "kk_resize": [_T, _T, _i, _d],

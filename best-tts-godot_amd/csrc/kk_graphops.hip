@@ -87,10 +87,12 @@ __global__ void __launch_bounds__(256) dql_fold(const float2* __restrict__ part,
   }
 }
 
-__device__ __forceinline__ uint32_t dql_byte(float x, float sc, float z) {
-  float v = rintf(x / sc) + z;  // exact integers: the sum is exact in fp32
-  v = v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v);
-  return static_cast<uint32_t>(v);
+
+int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
+                    uint8_t* zp_out) {
+  hipLaunchKernelGGL(dql_fold, dim3(1), dim3(256), 0, ctx().stream, part, npart, params, scale_out,
+                     zp_out);
+  return check_launch("dql_fold");
 }
 
 __global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x, int64_t n,

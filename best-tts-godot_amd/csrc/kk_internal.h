@@ -24,6 +24,20 @@ struct Context {
   int* row_counters = nullptr;
 };
 constexpr int kRowCounters = 65536;
+
+// DynamicQuantizeLinear's byte of x with the scale rounded to fp32 and the
+// zero point as a float: clamp(rint(x / scale) + zp, 0, 255)
+// (ref_runtime.py:106-116; the sum of two integers is exact in fp32).
+__device__ __forceinline__ uint32_t dql_byte(float x, float sc, float z) {
+  float v = rintf(x / sc) + z;
+  v = v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v);
+  return static_cast<uint32_t>(v);
+}
+
+// Folds npart (min, max) partials and derives DynamicQuantizeLinear's scale
+// and zero point: params[0] = (scale, zp) as floats, *scale_out, *zp_out.
+int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
+                    uint8_t* zp_out);
 Context& ctx();
 
 // Thread-local last error; set_error returns `code` so call sites can

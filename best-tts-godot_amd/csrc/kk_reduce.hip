@@ -315,6 +315,74 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
   }
 }
 
+// The normalised results y = affine((x - mean) / den) of long rows, not
+// stored: block (bx, row) writes the (min, max) of its share to
+// mm[row * gridDim.x + bx] (the first half of DynamicQuantizeLinear).
+__global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict__ mm,
+                                                             const float* __restrict__ x,
+                                                             const float2* __restrict__ stats,
+                                                             int64_t C, int64_t T, Affine af) {
+  __shared__ float2 wmm[kRowBlock / 64];
+  const int64_t row = blockIdx.y;
+  const int64_t c = row % C;
+  const RowAffine ra = row_affine(af, C, c, 0.0f, 0.0f);
+  const float2 st = stats[row];
+  const float* xr = x + row * T;
+  float lo = INFINITY, hi = -INFINITY;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < T;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const float y = apply_affine((xr[i] - st.x) / st.y, ra, af);
+    lo = fminf(lo, y);
+    hi = fmaxf(hi, y);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+  }
+  if ((threadIdx.x & 63) == 0) wmm[threadIdx.x >> 6] = make_float2(lo, hi);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < kRowBlock / 64; ++w) {
+      lo = fminf(lo, wmm[w].x);
+      hi = fmaxf(hi, wmm[w].y);
+    }
+    mm[row * gridDim.x + blockIdx.x] = make_float2(lo, hi);
+  }
+}
+
+// y recomputed exactly as above, then DynamicQuantizeLinear's byte with
+// params[0] = (scale, zero point): the float y never reaches memory.
+__global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict__ q,
+                                                            const float* __restrict__ x,
+                                                            const float2* __restrict__ stats,
+                                                            const float2* __restrict__ params,
+                                                            int64_t C, int64_t T, Affine af,
+                                                            int vec) {
+  const int64_t row = blockIdx.y;
+  const int64_t c = row % C;
+  const RowAffine ra = row_affine(af, C, c, 0.0f, 0.0f);
+  const float2 st = stats[row], pz = params[0];
+  const float* xr = x + row * T;
+  uint8_t* qr = q + row * T;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (vec) {
+    for (int64_t i = 4 * i0; i < T; i += stride * 4) {
+      const float4 v = ld_stream4(xr + i);
+      const uint32_t w = dql_byte(apply_affine((v.x - st.x) / st.y, ra, af), pz.x, pz.y) |
+                         (dql_byte(apply_affine((v.y - st.x) / st.y, ra, af), pz.x, pz.y) << 8) |
+                         (dql_byte(apply_affine((v.z - st.x) / st.y, ra, af), pz.x, pz.y) << 16) |
+                         (dql_byte(apply_affine((v.w - st.x) / st.y, ra, af), pz.x, pz.y) << 24);
+      __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(qr + i));
+    }
+  } else {
+    for (int64_t i = i0; i < T; i += stride)
+      qr[i] = static_cast<uint8_t>(dql_byte(apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af),
+                                            pz.x, pz.y));
+  }
+}
+
 // -------------------------------------------------------------- LayerNorm
 struct LnArgs {
   const float* skip;       // [rows, cols] or NULL
@@ -663,7 +731,9 @@ __device__ float np_row_sum(const float* row, int n, F f, NpScratch& S) {
 __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__ out,
                                                              const float* __restrict__ x,
                                                              int64_t C, int n, int mode,
-                                                             float eps, Affine af, int vec) {
+                                                             float eps, Affine af, int vec,
+                                                             float2* __restrict__ stats,
+                                                             float2* __restrict__ mm) {
   extern __shared__ __align__(16) float np_lds[];
   __shared__ NpScratch S;
   const int64_t row = blockIdx.x;
@@ -683,6 +753,31 @@ __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__
   float gamma = 0.0f, beta = 0.0f;
   if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
   const RowAffine ra = row_affine(af, C, c, gamma, beta);
+  if (mode == 3) {  // no output: (mean, den) and the (min, max) of the row's results
+    float lo = INFINITY, hi = -INFINITY;
+    for (int e = threadIdx.x; e < n; e += kNpThreads) {
+      const float y = apply_affine((np_lds[np_pad(e)] - mean) / den, ra, af);
+      lo = fminf(lo, y);
+      hi = fmaxf(hi, y);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lo = fminf(lo, __shfl_xor(lo, off, 64));
+      hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+    }
+    __shared__ float2 wmm[kNpThreads / 64];
+    if ((threadIdx.x & 63) == 0) wmm[threadIdx.x >> 6] = make_float2(lo, hi);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < kNpThreads / 64; ++w) {
+        lo = fminf(lo, wmm[w].x);
+        hi = fmaxf(hi, wmm[w].y);
+      }
+      stats[row] = make_float2(mean, den);
+      mm[row] = make_float2(lo, hi);
+    }
+    return;
+  }
   float* orow = out + row * n;
   if (vec) {
     for (int e = 4 * threadIdx.x; e < n; e += 4 * kNpThreads) {
@@ -962,7 +1057,7 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
     Affine af{};
     hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(n), st, out, x, int64_t{1}, static_cast<int>(n), mean ? 1 : 0,
-                       0.0f, af, vec ? 1 : 0);
+                       0.0f, af, vec ? 1 : 0, static_cast<float2*>(nullptr), static_cast<float2*>(nullptr));
     return check_launch("np_rows_kernel");
   }
   if (rows > kRowCounters) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)rows);
@@ -986,7 +1081,8 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
   if (T <= kNpRowMax) {
     hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(T), st, static_cast<float*>(out->data), xp, C,
-                       static_cast<int>(T), 2, eps, af, vec_ok ? 1 : 0);
+                       static_cast<int>(T), 2, eps, af, vec_ok ? 1 : 0, static_cast<float2*>(nullptr),
+                       static_cast<float2*>(nullptr));
     return check_launch("np_rows_kernel");
   }
   if (rows > kRowCounters)
@@ -1020,6 +1116,72 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
   return rc;
 }
 
+// The instance norm chain (with its affine, LeakyRelu or snake) and the
+// DynamicQuantizeLinear that alone reads its result, without storing the
+// float result: statistics, then one pass for the result's (min, max), the
+// scale and zero point, then one pass that recomputes the result and
+// writes its bytes.
+static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, const kk_tensor* y_zp,
+                              const kk_tensor* x, float eps, const Affine& af) {
+  hipStream_t st = ctx().stream;
+  const int64_t T = x->shape[x->rank - 1];
+  const int64_t C = x->shape[x->rank - 2];
+  const int64_t rows = numel(x) / T;
+  const float* xp = static_cast<const float*>(x->data);
+  const bool vec = (T % 4 == 0) && aligned16(x->data) &&
+                   (reinterpret_cast<uintptr_t>(q->data) % 4 == 0);
+  const int64_t per_block = kRowBlock * (vec ? 4 : 1) * 8;
+  const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(ceil_div(T, per_block), 1 << 16));
+  const bool long_rows = T > kNpRowMax;
+  if (long_rows && rows > kRowCounters)
+    return set_error(KK_E_UNSUPPORTED, "instance norm: %lld long rows", (long long)rows);
+  const int64_t nblk = long_rows ? ceil_div(T, kNpBlock) : 0;
+  const int64_t npart = long_rows ? rows * gx : rows;
+  if (npart > 0x7fffffff) return set_error(KK_E_UNSUPPORTED, "instance norm: too many partials");
+  auto up = [](int64_t b) { return ceil_div(b, 256) * 256; };
+  const int64_t o_stats = 0, o_mm = up(8 * rows), o_par = o_mm + up(8 * npart);
+  const int64_t o_part = o_par + 256, total = o_part + up(4 * rows * nblk + 4);
+  void* ws = nullptr;
+  KK_TRY(kk_alloc(static_cast<size_t>(total), &ws));
+  char* base = static_cast<char*>(ws);
+  float2* stats = reinterpret_cast<float2*>(base + o_stats);
+  float2* mm = reinterpret_cast<float2*>(base + o_mm);
+  float2* params = reinterpret_cast<float2*>(base + o_par);
+  float* part = reinterpret_cast<float*>(base + o_part);
+  int rc = KK_OK;
+  if (!long_rows) {
+    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
+                       np_row_lds(T), st, static_cast<float*>(nullptr), xp, C, static_cast<int>(T), 3,
+                       eps, af, vec ? 1 : 0, stats, mm);
+    rc = check_launch("np_rows_kernel");
+  } else {
+    const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
+    for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
+      hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
+                         static_cast<int>(nblk), pass, stats, ctx().row_counters,
+                         counter_stride(rows), static_cast<float*>(nullptr), 0, eps);
+      rc = check_launch("np_blocks_kernel");
+    }
+    if (rc == KK_OK) {
+      hipLaunchKernelGGL(instnorm_minmax, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(rows)),
+                         dim3(kRowBlock), 0, st, mm, xp, static_cast<const float2*>(stats), C, T, af);
+      rc = check_launch("instnorm_minmax");
+    }
+  }
+  if (rc == KK_OK)
+    rc = launch_dql_fold(mm, static_cast<int>(npart), params, static_cast<float*>(y_scale->data),
+                         static_cast<uint8_t*>(y_zp->data));
+  if (rc == KK_OK) {
+    hipLaunchKernelGGL(instnorm_quant, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(rows)),
+                       dim3(kRowBlock), 0, st, static_cast<uint8_t*>(q->data), xp,
+                       static_cast<const float2*>(stats), static_cast<const float2*>(params), C, T, af,
+                       vec ? 1 : 0);
+    rc = check_launch("instnorm_quant");
+  }
+  kk_free(ws);  // stream order keeps it alive for the kernels above
+  return rc;
+}
+
 static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, const Affine& af,
                            const StyleArgs& sa) {
   if (x->rank < 2) return set_error(KK_E_ARG, "instance norm: x must be [N, C, ...T]");
@@ -1044,11 +1206,25 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
 static int instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
                                      const kk_tensor* scale, const kk_tensor* shift,
                                      const kk_tensor* snake_a, const kk_tensor* snake_r, float eps,
-                                     int leaky, float alpha) {
+                                     int leaky, float alpha, const kk_tensor* y_scale = nullptr,
+                                     const kk_tensor* y_zp = nullptr) {
   KK_TRY(require_ready());
   KK_TRY(check_f32_contig(x, "x"));
-  KK_TRY(check_f32_contig(out, "out"));
-  if (!same_shape(out, x)) return set_error(KK_E_ARG, "instance norm: out shape must equal x");
+  KK_TRY(check_tensor(out, "out"));
+  if (y_scale) {  // out is the quantised result
+    KK_TRY(check_tensor(y_scale, "y_scale"));
+    KK_TRY(check_tensor(y_zp, "y_zero_point"));
+    if (out->dtype != KK_U8 || !is_contiguous(out) || y_scale->dtype != KK_F32 ||
+        numel(y_scale) != 1 || y_zp->dtype != KK_U8 || numel(y_zp) != 1)
+      return set_error(KK_E_ARG, "instance norm quant: y uint8 like x, scale one fp32, zero point "
+                                 "one uint8");
+  } else {
+    KK_TRY(check_f32_contig(out, "out"));
+  }
+  if (out->rank != x->rank || numel(out) != numel(x))
+    return set_error(KK_E_ARG, "instance norm: out shape must equal x");
+  for (int i = 0; i < x->rank; ++i)
+    if (out->shape[i] != x->shape[i]) return set_error(KK_E_ARG, "instance norm: out shape must equal x");
   if (x->rank < 2) return set_error(KK_E_ARG, "instance norm: x must be [N, C, ...T]");
   const int64_t C = x->shape[x->rank - 2];
   Affine af{};
@@ -1073,6 +1249,10 @@ static int instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
     }
     af.snake_a = static_cast<const float*>(snake_a->data);
     af.snake_r = static_cast<const float*>(snake_r->data);
+  }
+  if (y_scale) {
+    if (numel(x) == 0) return set_error(KK_E_ARG, "instance norm quant: empty input");
+    return instnorm_quant_run(out, y_scale, y_zp, x, eps, af);
   }
   StyleArgs sa{};
   return instnorm_launch(out, x, eps, af, sa);
@@ -1109,6 +1289,19 @@ int kk_instance_norm_affine(const kk_tensor* out, const kk_tensor* x, const kk_t
 int kk_instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x, const kk_tensor* scale,
                                  const kk_tensor* shift, float eps, int leaky, float alpha) {
   return instance_norm_scale_shift(out, x, scale, shift, nullptr, nullptr, eps, leaky, alpha);
+}
+
+int kk_instance_norm_quant(const kk_tensor* y, const kk_tensor* y_scale, const kk_tensor* y_zp,
+                           const kk_tensor* x, const kk_tensor* scale, const kk_tensor* shift,
+                           const kk_tensor* alpha, const kk_tensor* recip, float eps, int leaky,
+                           float leaky_alpha) {
+  if ((alpha == nullptr) != (recip == nullptr))
+    return set_error(KK_E_ARG, "kk_instance_norm_quant: snake needs both alpha and recip");
+  if (alpha && leaky)
+    return set_error(KK_E_UNSUPPORTED, "kk_instance_norm_quant: LeakyRelu and snake together");
+  if (!y_scale || !y_zp) return set_error(KK_E_ARG, "kk_instance_norm_quant: scale/zero point outputs");
+  return instance_norm_scale_shift(y, x, scale, shift, alpha, recip, eps, leaky, leaky_alpha,
+                                   y_scale, y_zp);
 }
 
 int kk_instance_norm_scale_shift_snake(const kk_tensor* out, const kk_tensor* x,

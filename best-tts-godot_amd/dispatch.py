@@ -360,6 +360,25 @@ def dispatch(op, node_input, node_output, at, env):
             yv = ops.instance_norm_scale_shift(xd, _f32(to_device(y)), _f32(to_device(inp(2))),
                                                at["epsilon"], None)
             out = ops.snake(yv, a, rc)
+    elif op == "InstanceNormQuant":
+        # the InstanceNorm chain (+ Mul scale, Add shift, then LeakyRelu or the snake
+        # chain) -> Cast(float) -> DynamicQuantizeLinear, fused; inputs x, scale,
+        # shift, alpha, recip ("" if absent); the outputs are the quantiser's.
+        xd = _f32(to_device(x))
+        sc, sh = _f32(to_device(y)), _f32(to_device(inp(2)))
+        a, rc = inp(3), inp(4)
+        a = _f32(to_device(a)) if a is not None else None
+        rc = _f32(to_device(rc)) if rc is not None else None
+        C = xd.shape[-2] if len(xd.shape) >= 2 else 0
+        if a is None or (a.size == C and rc.size == C):
+            res = ops.instance_norm_quant(xd, sc, sh, a, rc, at["epsilon"], at.get("leaky_alpha"))
+        else:  # alpha/recip not per channel: the fused ops one after the other
+            yv = ops.instance_norm_scale_shift(xd, sc, sh, at["epsilon"], None)
+            res = ops.dynamic_quantize_linear(ops.snake(yv, a, rc))
+        for name, v in zip(node_output, res):
+            if name:
+                env[name] = v
+        return
     elif op == "AdaIN":
         # inputs: x, style, W, bias; attribute epsilon.
         out = ops.adain(to_device(x), to_device(y), to_device(inp(2)),

@@ -10,6 +10,7 @@ each of which would otherwise read and write a full decoder activation
                         -> Sqrt -> Div -> [Mul(scale)] -> [Add(shift)] -> [LeakyRelu]
   snake                 Mul(alpha, x) -> Sin -> Pow(2) -> Mul(recip) -> Add(x)
   InstanceNorm + snake  the two above back to back (the decoder's residual blocks)
+  InstanceNorm [+ snake] -> Cast(float) -> DynamicQuantizeLinear   (the float result unstored)
 
 `fuse` rewrites each chain whose intermediate tensors have no other reader
 into one pseudo-node that `dispatch` runs as one kernel (the reference's
@@ -90,7 +91,54 @@ def fuse(nodes, weights, protect=()):
         elif i not in used:
             out.append(node)
             groups.append([i])
-    return _merge_norm_snake(out, groups, protect)
+    out, groups = _merge_norm_snake(out, groups, protect)
+    return _merge_norm_quant(out, groups, protect)
+
+
+def _merge_norm_quant(out, groups, protect):
+    """An InstanceNorm chain (plain, with LeakyRelu or with the snake) whose
+    result only a Cast(float) reads, and that Cast's result only a
+    DynamicQuantizeLinear, becomes one InstanceNormQuant node at the
+    quantiser's place: inputs x, scale, shift, alpha, recip; the quantiser's
+    outputs (the float result is never stored)."""
+    readers = defaultdict(list)
+    for k, (_op, ins, _outs, _at) in enumerate(out):
+        for n in ins:
+            if n:
+                readers[n].append(k)
+
+    def sole(name):
+        r = readers.get(name, [])
+        return r[0] if name not in protect and len(set(r)) == 1 else None
+
+    merged = {}  # quantiser index -> (norm index, cast index)
+    for k, (op, ins, outs, at) in enumerate(out):
+        if op not in ("InstanceNormScaleShift", "InstanceNormSnake"):
+            continue
+        c = sole(outs[0])
+        if c is None or out[c][0] != "Cast" or int(out[c][3].get("to", 0)) != 1:
+            continue
+        q = sole(out[c][2][0])
+        if q is None or out[q][0] != "DynamicQuantizeLinear" or out[q][1][0] != out[c][2][0]:
+            continue
+        merged[q] = (k, c)
+    if not merged:
+        return out, groups
+    dropped = {i for pair in merged.values() for i in pair}
+    new_out, new_groups = [], []
+    for k, node in enumerate(out):
+        if k in dropped:
+            continue
+        if k in merged:
+            n, c = merged[k]
+            n_op, n_ins, _n_outs, n_at = out[n]
+            n_ins = list(n_ins) + [""] * (5 - len(n_ins))
+            node = ("InstanceNormQuant", n_ins[:5], list(node[2]), dict(n_at))
+            new_groups.append(groups[n] + groups[c] + groups[k])
+        else:
+            new_groups.append(groups[k])
+        new_out.append(node)
+    return new_out, new_groups
 
 
 def _merge_norm_snake(out, groups, protect):

@@ -285,6 +285,24 @@ def instance_norm_scale_shift_snake(x, scale, shift, alpha, recip, eps=1e-5):
     return out
 
 
+def instance_norm_quant(x, scale=None, shift=None, alpha=None, recip=None, eps=1e-5,
+                        leaky_alpha=None):
+    """The instance norm chain (affine, then LeakyRelu or snake) and the
+    DynamicQuantizeLinear of its result: (y uint8, scale fp32 [], zero point
+    uint8 []), the float result never stored."""
+    x = x.contiguous()
+    y = DeviceTensor.empty(x.shape, np.uint8)
+    ys = DeviceTensor.empty((), np.float32)
+    yz = DeviceTensor.empty((), np.uint8)
+    _lib.call("kk_instance_norm_quant", y.desc(), ys.desc(), yz.desc(), x.desc(),
+              _d(scale.contiguous() if scale is not None else None),
+              _d(shift.contiguous() if shift is not None else None),
+              _d(alpha.contiguous() if alpha is not None else None),
+              _d(recip.contiguous() if recip is not None else None), float(eps),
+              0 if leaky_alpha is None else 1, 0.0 if leaky_alpha is None else float(leaky_alpha))
+    return y, ys, yz
+
+
 # ------------------------------------------------ recurrent / vocoder
 def lstm(x, w, r, b, init_h, init_c, w_scale, w_zp, r_scale, r_zp, hidden_size, bidirectional):
     x = x.contiguous()

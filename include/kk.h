@@ -176,6 +176,17 @@ int kk_instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
 int kk_instance_norm_scale_shift_snake(const kk_tensor* out, const kk_tensor* x,
                                        const kk_tensor* scale, const kk_tensor* shift,
                                        const kk_tensor* alpha, const kk_tensor* recip, float eps);
+/* kk_instance_norm_scale_shift (or its snake form when alpha and recip are
+ * given) followed by the Cast(float) and DynamicQuantizeLinear that alone
+ * read its result (ref_runtime.py:106-116, :500-508): y (uint8, x's shape),
+ * y_scale (one fp32) and y_zero_point (one uint8) exactly as
+ * kk_dynamic_quantize_linear gives them; the float result is recomputed
+ * instead of stored.  leaky and alpha/recip exclude each other. */
+int kk_instance_norm_quant(const kk_tensor* y, const kk_tensor* y_scale,
+                           const kk_tensor* y_zero_point, const kk_tensor* x,
+                           const kk_tensor* scale, const kk_tensor* shift,
+                           const kk_tensor* alpha, const kk_tensor* recip, float eps,
+                           int leaky, float leaky_alpha);
 /* AdaIN with the style Linear fused: h = style . W + b with W [S, 2C]
  * (any strides), then kk_instance_norm_affine on x [N,C,T].  bias may be
  * NULL.  W may be f32, f16 or int8/uint8 with w_scale/w_zp (per tensor or

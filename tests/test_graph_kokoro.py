@@ -66,16 +66,24 @@ def test_harmonic_stft_and_waveform(run8):
     assert wav.size == int(gold["wave_len"]) and np.isfinite(wav).all()
 
 
-def _node_close(got, want):
+def _node_close(got, want, quant_of_sin=False):
     """Per-node bar: bit-exact for integer/bool outputs; for float outputs
     |got - want| <= 1e-4 |want| + 1e-5 max|want| (the contraction/reduction
-    bar, which contains the elementwise one).  Returns None or a message."""
+    bar, which contains the elementwise one).  `quant_of_sin`: the bytes of
+    a quantiser fused behind a snake, whose sin() differs from numpy's by
+    ulps, so a value on a rounding boundary may land one step away: |diff|
+    <= 1 on at most 0.1% of the elements.  Returns None or a message."""
     got, want = np.asarray(got), np.asarray(want)
     if got.shape != want.shape:
         return f"shape {got.shape} != {want.shape}"
     if want.dtype.kind in "iub":
-        if got.dtype.kind not in "iub" or not np.array_equal(got.astype(np.int64), want.astype(np.int64)):
-            return f"integer/bool output differs ({got.dtype} vs {want.dtype})"
+        if got.dtype.kind not in "iub":
+            return f"integer/bool output has dtype {got.dtype}"
+        d = np.abs(got.astype(np.int64) - want.astype(np.int64))
+        if quant_of_sin and d.size and d.max() <= 1 and (d > 0).mean() <= 1e-3:
+            return None
+        if d.any():
+            return f"integer/bool output differs ({int((d > 0).sum())} of {d.size}, max {d.max()})"
         return None
     g, w = got.astype(np.float64), want.astype(np.float64)
     fin = np.isfinite(w)
@@ -149,7 +157,8 @@ def test_every_node_teacher_forced(gpu, oracle):
                 if not o:
                     continue
                 on_device[o] = isinstance(genv[o], gpu.DeviceTensor)
-                msg = _node_close(gpu.to_host(genv[o]), oenv[o])
+                msg = _node_close(gpu.to_host(genv[o]), oenv[o],
+                                  quant_of_sin=gop == "InstanceNormQuant" and len(gins) > 3 and bool(gins[3]))
                 counted += 1
                 if msg:
                     failures.append(f"node {k} {gop} (original {pg.groups[k]}) -> {o}: {msg}")

@@ -147,9 +147,10 @@ def _graph_nodes():
 def test_fusion_pass_on_the_kokoro_graph():
     """The fusion pass finds every quantised conv tail (87), InstanceNorm
     chain (64 of 65: one has a Transpose inside) and snake (48) of the
-    packed graph -- 42 norm chains feed a snake alone and merge with it --
-    keeps a valid topological order, and never drops a tensor that a node
-    outside its group reads."""
+    packed graph -- 42 norm chains feed a snake alone and merge with it, and
+    59 norm chains (snake or not) feed only a Cast -> DynamicQuantizeLinear
+    and merge with those -- keeps a valid topological order, and never drops
+    a tensor that a node outside its group reads."""
     import importlib
     from collections import Counter
     fz = importlib.import_module("best-tts-godot_amd.fuse")
@@ -157,7 +158,7 @@ def test_fusion_pass_on_the_kokoro_graph():
     fused, groups = fz.fuse(nodes, weights, {str(g["output"])})
     kinds = Counter(n[0] for n in fused)
     assert (kinds["QConvScaled"], kinds["InstanceNormScaleShift"], kinds["Snake"],
-            kinds["InstanceNormSnake"]) == (87, 22, 6, 42)
+            kinds["InstanceNormSnake"], kinds["InstanceNormQuant"]) == (87, 5, 6, 0, 59)
     covered = sorted(i for grp in groups for i in grp)
     assert covered == list(range(len(nodes)))  # every original node exactly once
     produced = {}

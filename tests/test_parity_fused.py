@@ -123,6 +123,64 @@ def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
     assert_close(got, want, 1e-5, floor_rel=1e-6, what=f"InstanceNorm+snake C={C} T={T}")
 
 
+@pytest.mark.parametrize("C,T,kind", [(128, 40000, "affine"), (256, 7180, "leaky"),
+                                      (128, 20000, "snake"), (64, 999, "snake"),
+                                      (96, 2400, "plain")])
+def test_instance_norm_quant_chain(gpu, oracle, C, T, kind):
+    """The InstanceNorm chain (plain, affine, + LeakyRelu, + snake) -> Cast
+    -> DynamicQuantizeLinear: one InstanceNormQuant, its float result never
+    stored.  Without the snake: the same bytes, scale and zero point as the
+    oracle's chain; with it (sin differs from numpy's by ulps) a value on a
+    rounding boundary may land one step away."""
+    r = rng(25)
+    x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
+    alpha = r.uniform(0.5, 2, (1, C, 1)).astype(np.float16)
+    inputs = {"x": x, "g": (1 + 0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32),
+              "b": (0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32)}
+    weights = {"ax": np.array([2], np.int64),
+               "eps": np.array(1e-5, np.float16).astype(np.float32), "a": alpha,
+               "rc": (np.float32(1) / alpha.astype(np.float32)).astype(np.float16),
+               "two": np.array(2.0, np.float16)}
+    nodes, y = norm_chain(kind != "plain", kind == "leaky")
+    if kind == "snake":
+        nodes += [("Mul", ["a", y], ["t"], {}), ("Sin", ["t"], ["s"], {}),
+                  ("Pow", ["s", "two"], ["p"], {}), ("Mul", ["rc", "p"], ["qq"], {}),
+                  ("Add", [y, "qq"], ["z"], {})]
+        y = "z"
+    nodes += [("Cast", [y], ["f"], {"to": 1}),
+              ("DynamicQuantizeLinear", ["f"], ["q", "qs", "qz"], {})]
+    fz = importlib.import_module("best-tts-godot_amd.fuse")
+    dev_w = {}
+    for k, v in weights.items():
+        v = np.asarray(v)
+        v = v.astype(np.float32) if v.dtype == np.float16 else v
+        t = gpu.to_device(v)
+        if v.size <= 16:
+            t.host = v
+        dev_w[k] = t
+    fused, _ = fz.fuse(nodes, dev_w, {"q", "qs", "qz"})
+    assert [n[0] for n in fused] == ["InstanceNormQuant"]
+    env = dict(dev_w)
+    env.update({k: gpu.to_device(np.asarray(v)) for k, v in inputs.items()})
+    for op, ins, outs, at in fused:
+        gpu.dispatch(op, ins, outs, at, env)
+    oenv = {k: np.asarray(v) for k, v in {**weights, **inputs}.items()}
+    for op, ins, outs, at in nodes:
+        oracle.dispatch(op, ins, outs, at, oenv)
+    q, qs, qz = (gpu.to_host(env[n]) for n in ("q", "qs", "qz"))
+    if kind != "snake":
+        assert_bitexact(q, oenv["q"], f"quantised InstanceNorm ({kind})")
+        assert_bitexact(np.asarray(qs, np.float32).reshape(()), np.asarray(oenv["qs"], np.float32),
+                        "scale")
+        assert_bitexact(np.asarray(qz).reshape(()), np.asarray(oenv["qz"]), "zero point")
+    else:
+        assert_close(np.asarray(qs, np.float32).reshape(()), np.asarray(oenv["qs"], np.float32),
+                     1e-6, what="scale")
+        assert abs(int(np.asarray(qz).reshape(())) - int(np.asarray(oenv["qz"]).reshape(()))) <= 1
+        d = np.abs(q.astype(np.int64) - oenv["q"].astype(np.int64))
+        assert d.max() <= 1 and (d > 0).mean() <= 1e-3, (d.max(), (d > 0).mean())
+
+
 @pytest.mark.parametrize("C,T", [(128, 30000), (256, 5001)])
 def test_snake_chain(gpu, oracle, C, T):
     r = rng(23)
