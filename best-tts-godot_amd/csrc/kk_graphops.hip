@@ -53,11 +53,13 @@ __global__ void __launch_bounds__(256) dql_minmax(const float* __restrict__ x, i
 
 // One block folds the partials and derives scale and zero point in double
 // exactly as the reference does; params = (scale, zero point) as floats.
-__global__ void __launch_bounds__(256) dql_fold(const float2* __restrict__ part, int npart,
-                                                float2* __restrict__ params,
-                                                float* __restrict__ scale_out,
-                                                uint8_t* __restrict__ zp_out) {
-  __shared__ float smin[4], smax[4];
+constexpr int kDqlFoldThreads = 1024;
+
+__global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __restrict__ part,
+                                                            int npart, float2* __restrict__ params,
+                                                            float* __restrict__ scale_out,
+                                                            uint8_t* __restrict__ zp_out) {
+  __shared__ float smin[kDqlFoldThreads / 64], smax[kDqlFoldThreads / 64];
   float lo = INFINITY, hi = -INFINITY;
   for (int i = threadIdx.x; i < npart; i += blockDim.x) {
     lo = fminf(lo, part[i].x);
@@ -72,8 +74,13 @@ __global__ void __launch_bounds__(256) dql_fold(const float2* __restrict__ part,
   if (lane == 0) { smin[w] = lo; smax[w] = hi; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    const double mn = fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3]));
-    const double mx = fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3]));
+    float fmn = smin[0], fmx = smax[0];
+    for (int k = 1; k < kDqlFoldThreads / 64; ++k) {
+      fmn = fminf(fmn, smin[k]);
+      fmx = fmaxf(fmx, smax[k]);
+    }
+    const double mn = fmn;
+    const double mx = fmx;
     const double dlo = mn < 0.0 ? mn : 0.0;
     const double dhi = mx > 0.0 ? mx : 0.0;
     double scale = (dhi - dlo) / 255.0;
@@ -90,8 +97,8 @@ __global__ void __launch_bounds__(256) dql_fold(const float2* __restrict__ part,
 
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
                     uint8_t* zp_out) {
-  hipLaunchKernelGGL(dql_fold, dim3(1), dim3(256), 0, ctx().stream, part, npart, params, scale_out,
-                     zp_out);
+  hipLaunchKernelGGL(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
+                     scale_out, zp_out);
   return check_launch("dql_fold");
 }
 
@@ -528,7 +535,7 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
                      static_cast<const float*>(x->data), n, pp, vec);
   int rc = check_launch("dql_minmax");
   if (rc == KK_OK) {
-    hipLaunchKernelGGL(dql_fold, dim3(1), dim3(256), 0, ctx().stream, pp, nblk, pp + nblk,
+    hipLaunchKernelGGL(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, pp, nblk, pp + nblk,
                        static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data));
     rc = check_launch("dql_fold");
   }
