@@ -37,12 +37,21 @@ def _hipcc():
 
 
 def _compile(src):
+    """Compiles one source; returns (object path, [kernels that spill])."""
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [_hipcc(), *HIPFLAGS, "-c", src, "-o", obj]
+    cmd = [_hipcc(), *HIPFLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
-    return obj
+    spills, name = [], None
+    for line in res.stderr.splitlines():
+        if "Function Name:" in line:
+            name = line.split("Function Name:")[1].split("[")[0].strip()
+        elif "ScratchSize [bytes/lane]:" in line:
+            size = int(line.split("ScratchSize [bytes/lane]:")[1].split("[")[0])
+            if size:
+                spills.append(f"{name} ({size} B/lane)")
+    return obj, spills
 
 
 def build(verbose=False):
@@ -51,7 +60,13 @@ def build(verbose=False):
     srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
     workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(_compile, srcs))
+        done = list(ex.map(_compile, srcs))
+    objs = [o for o, _ in done]
+    # A kernel with private (scratch) memory spills registers to memory:
+    # every kernel here is meant to fit, so say which one does not.
+    spills = [k for _, ks in done for k in ks]
+    if spills:
+        print("libkk: kernels using scratch memory: " + ", ".join(spills), file=sys.stderr)
     tmp = LIB + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -190,11 +190,15 @@ __device__ __forceinline__ RowAffine row_affine(const Affine& af, int64_t C, int
   return ra;
 }
 
+// SNAKE false leaves the snake out of the code: kernels that hold whole
+// rows in registers (the style-projected AdaIN) never take it, and sinf's
+// slow path would make them spill.
+template <bool SNAKE = true>
 __device__ __forceinline__ float apply_affine(float q, const RowAffine& ra, const Affine& af) {
   float y = ra.has_mul ? q * ra.mul : q;
   if (ra.has_add) y = y + ra.add;
   if (af.leaky) y = y < 0.0f ? y * af.alpha : y;
-  if (af.snake_a) {  // Mul(alpha, y) -> Sin -> Pow(., 2) -> Mul(recip, .) -> Add(y, .)
+  if (SNAKE && af.snake_a) {  // Mul(alpha, y) -> Sin -> Pow(., 2) -> Mul(recip, .) -> Add(y, .)
     const float sn = sinf(ra.sa * y);
     y = y + ra.sr * (sn * sn);
   }
@@ -233,7 +237,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) r[j][e] = apply_affine(r[j][e] / den, ra, af);
+    for (int e = 0; e < VEC; ++e) r[j][e] = apply_affine<false>(r[j][e] / den, ra, af);
   store_row<GROUP, NV, VEC>(out + row * T, T, g, r);
 }
 
@@ -262,7 +266,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_long_kernel(float* __restr
   const float var = group_sum<kRowBlock>(q, lds) / static_cast<float>(T);
   const float den = sqrtf(var + eps);
   float* orow = out + row * T;
-  for (int64_t i = g; i < T; i += kRowBlock) orow[i] = apply_affine((xr[i] - mean) / den, ra, af);
+  for (int64_t i = g; i < T; i += kRowBlock) orow[i] = apply_affine<false>((xr[i] - mean) / den, ra, af);
 }
 
 // acc = 0; acc += part[b] for b in order (numpy's outer loop over

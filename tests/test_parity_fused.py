@@ -84,7 +84,13 @@ def norm_chain(affine, leaky):
 
 @pytest.mark.parametrize("C,T,affine,leaky", [(128, 40000, True, False), (128, 40001, True, True),
                                               (256, 700, True, True), (512, 279, False, False),
-                                              (64, 20000, False, False)])
+                                              (64, 20000, False, False),
+                                              # long rows in 8192-blocks: two whole blocks;
+                                              # three; three and 100 elements; four and 5;
+                                              # 512 rows of five blocks
+                                              (32, 16384, True, False), (32, 24576, False, False),
+                                              (32, 24676, True, False), (16, 32773, False, True),
+                                              (512, 40000, True, True)])
 def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
     r = rng(22)
     x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
@@ -98,6 +104,26 @@ def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
     # statistics in numpy's summation order, then the chain's own IEEE
     # operations: the same bits
     assert_bitexact(got, want, f"InstanceNorm chain C={C} T={T}")
+
+
+def test_instance_norm_long_rows_repeat(gpu, oracle):
+    """The long-row instance norm leaves its per-row arrival counters at
+    zero: three launches in a row, with one of another shape between each,
+    give the same bits, and those of the oracle's chain."""
+    r = rng(23)
+    x = (r.normal(0, 2, (1, 64, 40000)) + r.normal(0, 3, (1, 64, 1))).astype(np.float32)
+    x2 = r.normal(0, 1, (1, 200, 24676)).astype(np.float32)
+    dx, dx2 = gpu.to_device(x), gpu.to_device(x2)
+    first = gpu.ops.instance_norm(dx, None, 1e-5).numpy()
+    for _ in range(2):
+        gpu.ops.instance_norm(dx2, None, 1e-5)
+        assert_bitexact(gpu.ops.instance_norm(dx, None, 1e-5).numpy(), first, "repeated launch")
+    weights = {"ax": np.array([2], np.int64), "eps": np.array(1e-5, np.float32)}
+    nodes, out = norm_chain(False, False)
+    oenv = {"x": x, **weights}
+    for op, ins, outs, at in nodes:
+        oracle.dispatch(op, ins, outs, at, oenv)
+    assert_bitexact(first, oenv[out], "long rows vs the oracle's chain")
 
 
 @pytest.mark.parametrize("C,T,affine", [(128, 40000, True), (256, 7180, True), (64, 999, False)])
@@ -125,7 +151,8 @@ def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
 
 @pytest.mark.parametrize("C,T,kind", [(128, 40000, "affine"), (256, 7180, "leaky"),
                                       (128, 20000, "snake"), (64, 999, "snake"),
-                                      (96, 2400, "plain")])
+                                      (96, 2400, "plain"), (32, 24676, "leaky"),
+                                      (512, 40000, "affine")])
 def test_instance_norm_quant_chain(gpu, oracle, C, T, kind):
     """The InstanceNorm chain (plain, affine, + LeakyRelu, + snake) -> Cast
     -> DynamicQuantizeLinear: one InstanceNormQuant, its float result never
