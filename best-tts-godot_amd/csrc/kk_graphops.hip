@@ -55,10 +55,16 @@ __global__ void __launch_bounds__(256) dql_minmax(const float* __restrict__ x, i
 // exactly as the reference does; params = (scale, zero point) as floats.
 constexpr int kDqlFoldThreads = 1024;
 
+// only_if: the launch does nothing unless *only_if is set.  clear: also
+// keeps the folded (min, max) in params[1] and zeroes *clear, the flag a
+// later pass sets when one of its values falls outside that range.
 __global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __restrict__ part,
                                                             int npart, float2* __restrict__ params,
                                                             float* __restrict__ scale_out,
-                                                            uint8_t* __restrict__ zp_out) {
+                                                            uint8_t* __restrict__ zp_out,
+                                                            const int* __restrict__ only_if,
+                                                            int* __restrict__ clear) {
+  if (only_if && *only_if == 0) return;
   __shared__ float smin[kDqlFoldThreads / 64], smax[kDqlFoldThreads / 64];
   float lo = INFINITY, hi = -INFINITY;
   for (int i = threadIdx.x; i < npart; i += blockDim.x) {
@@ -91,14 +97,18 @@ __global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __rest
     params[0] = make_float2(static_cast<float>(scale), static_cast<float>(zp));
     *scale_out = static_cast<float>(scale);
     *zp_out = static_cast<uint8_t>(zp);
+    if (clear) {
+      params[1] = make_float2(fmn, fmx);
+      *clear = 0;
+    }
   }
 }
 
 
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
-                    uint8_t* zp_out) {
+                    uint8_t* zp_out, const int* only_if, int* clear) {
   hipLaunchKernelGGL(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
-                     scale_out, zp_out);
+                     scale_out, zp_out, only_if, clear);
   return check_launch("dql_fold");
 }
 
@@ -536,7 +546,8 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
   int rc = check_launch("dql_minmax");
   if (rc == KK_OK) {
     hipLaunchKernelGGL(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, pp, nblk, pp + nblk,
-                       static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data));
+                       static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data),
+                       static_cast<const int*>(nullptr), static_cast<int*>(nullptr));
     rc = check_launch("dql_fold");
   }
   if (rc == KK_OK) {

@@ -36,8 +36,10 @@ __device__ __forceinline__ uint32_t dql_byte(float x, float sc, float z) {
 
 // Folds npart (min, max) partials and derives DynamicQuantizeLinear's scale
 // and zero point: params[0] = (scale, zp) as floats, *scale_out, *zp_out.
+// With only_if, the launch does nothing unless *only_if is set; with clear,
+// params[1] = the folded (min, max) and *clear = 0.
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
-                    uint8_t* zp_out);
+                    uint8_t* zp_out, const int* only_if = nullptr, int* clear = nullptr);
 Context& ctx();
 
 // Thread-local last error; set_error returns `code` so call sites can

@@ -325,7 +325,9 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
 __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict__ mm,
                                                              const float* __restrict__ x,
                                                              const float2* __restrict__ stats,
-                                                             int64_t C, int64_t T, Affine af) {
+                                                             int64_t C, int64_t T, Affine af,
+                                                             const int* __restrict__ only_if) {
+  if (only_if && *only_if == 0) return;
   __shared__ float2 wmm[kRowBlock / 64];
   const int64_t row = blockIdx.y;
   const int64_t c = row % C;
@@ -357,34 +359,46 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict_
 
 // y recomputed exactly as above, then DynamicQuantizeLinear's byte with
 // params[0] = (scale, zero point): the float y never reaches memory.
+// only_if: the launch does nothing unless *only_if is set.  check: any y
+// outside params[1] = (min, max) sets *check.
 __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict__ q,
                                                             const float* __restrict__ x,
                                                             const float2* __restrict__ stats,
                                                             const float2* __restrict__ params,
                                                             int64_t C, int64_t T, Affine af,
-                                                            int vec) {
+                                                            int vec, const int* __restrict__ only_if,
+                                                            int* __restrict__ check) {
+  if (only_if && *only_if == 0) return;
   const int64_t row = blockIdx.y;
   const int64_t c = row % C;
   const RowAffine ra = row_affine(af, C, c, 0.0f, 0.0f);
   const float2 st = stats[row], pz = params[0];
+  const float2 lim = check ? params[1] : make_float2(-INFINITY, INFINITY);
   const float* xr = x + row * T;
   uint8_t* qr = q + row * T;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  bool out = false;
   if (vec) {
     for (int64_t i = 4 * i0; i < T; i += stride * 4) {
       const float4 v = ld_stream4(xr + i);
-      const uint32_t w = dql_byte(apply_affine((v.x - st.x) / st.y, ra, af), pz.x, pz.y) |
-                         (dql_byte(apply_affine((v.y - st.x) / st.y, ra, af), pz.x, pz.y) << 8) |
-                         (dql_byte(apply_affine((v.z - st.x) / st.y, ra, af), pz.x, pz.y) << 16) |
-                         (dql_byte(apply_affine((v.w - st.x) / st.y, ra, af), pz.x, pz.y) << 24);
+      const float y0 = apply_affine((v.x - st.x) / st.y, ra, af);
+      const float y1 = apply_affine((v.y - st.x) / st.y, ra, af);
+      const float y2 = apply_affine((v.z - st.x) / st.y, ra, af);
+      const float y3 = apply_affine((v.w - st.x) / st.y, ra, af);
+      out |= fminf(fminf(y0, y1), fminf(y2, y3)) < lim.x || fmaxf(fmaxf(y0, y1), fmaxf(y2, y3)) > lim.y;
+      const uint32_t w = dql_byte(y0, pz.x, pz.y) | (dql_byte(y1, pz.x, pz.y) << 8) |
+                         (dql_byte(y2, pz.x, pz.y) << 16) | (dql_byte(y3, pz.x, pz.y) << 24);
       __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(qr + i));
     }
   } else {
-    for (int64_t i = i0; i < T; i += stride)
-      qr[i] = static_cast<uint8_t>(dql_byte(apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af),
-                                            pz.x, pz.y));
+    for (int64_t i = i0; i < T; i += stride) {
+      const float y = apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af);
+      out |= y < lim.x || y > lim.y;
+      qr[i] = static_cast<uint8_t>(dql_byte(y, pz.x, pz.y));
+    }
   }
+  if (check && out) *check = 1;  // every writer stores the same 1
 }
 
 // -------------------------------------------------------------- LayerNorm
@@ -612,6 +626,7 @@ struct NpScratch {
   int lo[kNpMaxLeaves], n[kNpMaxLeaves];
   float sum[kNpMaxLeaves];
   float wave[kNpThreads / 64];
+  float wmin[kNpThreads / 64], wmax[kNpThreads / 64];
   int count;
   float total;
 };
@@ -646,7 +661,7 @@ __device__ float np_tree(int n, int& k, const NpScratch& S) {
 // numpy's pairwise sum of f(i), i in [0, m), 1 <= m <= 8192, by a whole
 // 512-thread block; every thread returns the sum.  f reads LDS or computes.
 template <class F>
-__device__ float np_block_sum(F f, int m, NpScratch& S) {
+__device__ __forceinline__ float np_block_sum(F f, int m, NpScratch& S) {
   const int q = threadIdx.x >> 3, j = threadIdx.x & 7;
   if (m == kNpBlock) {
     float r = f(q * kNpLeaf + j);
@@ -797,6 +812,20 @@ __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__
   }
 }
 
+// The (min, max) of wave-spread values lo, hi over the whole block: each
+// wave's lane 0 leaves its pair in S.wmin / S.wmax (read after a barrier).
+__device__ __forceinline__ void np_wave_minmax(float lo, float hi, NpScratch& S) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    S.wmin[threadIdx.x >> 6] = lo;
+    S.wmax[threadIdx.x >> 6] = hi;
+  }
+}
+
 // Long rows: block (b, row) computes pw of 8192-block b of f(x) into
 // part[row][b]; f is x (mode 0) or (x - mean)^2 (mode 1, mean in
 // stats[row].x).  The last block of a row to finish (counted in
@@ -807,10 +836,16 @@ __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__
 //   mode 1: stats[row].y = sqrt(acc / T + eps)
 // Once its block sum is formed only wave 0 stays: the other waves leave
 // while it publishes the partial and counts.
+// With xmm, mode 0 also leaves the block's (min, max) of x in
+// xmm[row * nblk + b]; with mm, mode 1's last block folds the row's xmm
+// into (xmin, xmax) and writes mm[row] = the (min, max) of
+// y = affine((x - mean) / den) at those two points: the row's (min, max)
+// of y whenever y is monotonic in x.
 __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     float* __restrict__ part, const float* __restrict__ x, int64_t T, int nblk, int mode,
     float2* __restrict__ stats, int* __restrict__ cnt, int cstride, float* __restrict__ red_out,
-    int red_mean, float eps) {
+    int red_mean, float eps, float2* __restrict__ xmm, float2* __restrict__ mm, int64_t C,
+    Affine af) {
   __shared__ NpScratch S;
   const int64_t row = blockIdx.y;
   cnt += row * cstride;  // counters spaced apart: the rows' atomics do not share a line
@@ -818,7 +853,7 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
   const int64_t lo = static_cast<int64_t>(b) * kNpBlock;
   const int m = static_cast<int>(T - lo < kNpBlock ? T - lo : kNpBlock);
   const float mean = mode == 1 ? stats[row].x : 0.0f;
-  auto f = [&](float e) {
+  auto f = [mode, mean](float e) {
     if (mode == 0) return e;
     const float d = e - mean;
     return d * d;
@@ -843,13 +878,39 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     r += __shfl_xor(r, 16, 64);
     r += __shfl_xor(r, 32, 64);
     if ((threadIdx.x & 63) == 0) S.wave[threadIdx.x >> 6] = r;
+    if (xmm) {
+      float lo = v[0], hi = v[0];
+#pragma unroll
+      for (int k = 1; k < kNpLeaf / 8; ++k) {
+        lo = fminf(lo, v[k]);
+        hi = fmaxf(hi, v[k]);
+      }
+      np_wave_minmax(lo, hi, S);
+    }
     __syncthreads();
     if (threadIdx.x >= 64) return;
     s = ((S.wave[0] + S.wave[1]) + (S.wave[2] + S.wave[3])) +
         ((S.wave[4] + S.wave[5]) + (S.wave[6] + S.wave[7]));
   } else {  // the row's last, partial block: the general tree, from memory
-    s = np_block_sum([&](int e) { return f(xb[e]); }, m, S);
+    s = np_block_sum([f, xb](int e) { return f(xb[e]); }, m, S);
+    if (xmm) {
+      float lo = INFINITY, hi = -INFINITY;
+      for (int e = threadIdx.x; e < m; e += kNpThreads) {
+        lo = fminf(lo, xb[e]);
+        hi = fmaxf(hi, xb[e]);
+      }
+      np_wave_minmax(lo, hi, S);
+      __syncthreads();
+    }
     if (threadIdx.x >= 64) return;
+  }
+  if (xmm && threadIdx.x == 0) {
+    float lo = S.wmin[0], hi = S.wmax[0];
+    for (int w = 1; w < kNpThreads / 64; ++w) {
+      lo = fminf(lo, S.wmin[w]);
+      hi = fmaxf(hi, S.wmax[w]);
+    }
+    xmm[row * nblk + b] = make_float2(lo, hi);
   }
   // wave 0: the partial goes to the device-coherent level (past this XCD's
   // L2) and has landed before the count moves
@@ -861,8 +922,30 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
   }
   if (__shfl(last, 0, 64)) {
     const float acc = np_fold(part + row * nblk, nblk);
+    const float n = static_cast<float>(T);
+    if (mode == 1 && mm) {  // the row's (xmin, xmax), written by the mode-0 launch
+      float lo = INFINITY, hi = -INFINITY;
+      for (int i = threadIdx.x; i < nblk; i += 64) {
+        const float2 p = xmm[row * nblk + i];
+        lo = fminf(lo, p.x);
+        hi = fmaxf(hi, p.y);
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, off, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+      }
+      // the whole wave evaluates y (even lanes at xmin, odd at xmax)
+      const float den = sqrtf(acc / n + eps);
+      const int64_t c = row % C;
+      float gamma = 0.0f, beta = 0.0f;
+      if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
+      const RowAffine ra = row_affine(af, C, c, gamma, beta);
+      const float y = apply_affine(((threadIdx.x & 1 ? hi : lo) - mean) / den, ra, af);
+      const float y1 = __shfl_xor(y, 1, 64);
+      if (threadIdx.x == 0) mm[row] = make_float2(fminf(y, y1), fmaxf(y, y1));
+    }
     if (threadIdx.x == 0) {
-      const float n = static_cast<float>(T);
       if (mode == 1) stats[row].y = sqrtf(acc / n + eps);
       else if (red_out) red_out[row] = red_mean ? acc / n : acc;
       else stats[row].x = acc / n;
@@ -1071,7 +1154,8 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
   hipLaunchKernelGGL(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
                      dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
                      static_cast<int>(nblk), 0, static_cast<float2*>(nullptr), ctx().row_counters,
-                     counter_stride(rows), out, mean ? 1 : 0, 0.0f);
+                     counter_stride(rows), out, mean ? 1 : 0, 0.0f, static_cast<float2*>(nullptr),
+                     static_cast<float2*>(nullptr), int64_t{0}, Affine{});
   const int rc = check_launch("np_blocks_kernel");
   kk_free(part);  // stream order keeps it alive for the kernel
   return rc;
@@ -1104,7 +1188,9 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
   for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
     hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                        static_cast<int>(nblk), pass, stats, ctx().row_counters,
-                       counter_stride(rows), static_cast<float*>(nullptr), 0, eps);
+                       counter_stride(rows), static_cast<float*>(nullptr), 0, eps,
+                       static_cast<float2*>(nullptr), static_cast<float2*>(nullptr), int64_t{0},
+                       Affine{});
     rc = check_launch("np_blocks_kernel");
   }
   if (rc == KK_OK) {
@@ -1122,9 +1208,17 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
 
 // The instance norm chain (with its affine, LeakyRelu or snake) and the
 // DynamicQuantizeLinear that alone reads its result, without storing the
-// float result: statistics, then one pass for the result's (min, max), the
-// scale and zero point, then one pass that recomputes the result and
-// writes its bytes.
+// float result y.  Rows held in LDS: one pass for the statistics and the
+// rows' (min, max) of y, then one that recomputes y and writes its bytes.
+// Long rows: the two statistics passes, the first also taking each row's
+// (min, max) of x; y is monotonic in x per row (the affine, a LeakyRelu
+// with alpha >= 0, and the snake y + sin^2(a y) / a, whose slope is
+// 1 + sin(2 a y) >= 0), so y at those two points bounds the row and the
+// extremes over all rows give the quantiser's scale and zero point.  Where
+// rounding could break that (the snake: sin's last bit), the quantising pass
+// checks every y against the bounds and, if one falls outside, flags it;
+// three more launches that do nothing unless flagged then take the exact
+// (min, max) of y, the scale and zero point again, and the bytes again.
 static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, const kk_tensor* y_zp,
                               const kk_tensor* x, float eps, const Affine& af) {
   hipStream_t st = ctx().stream;
@@ -1139,12 +1233,15 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   const bool long_rows = T > kNpRowMax;
   if (long_rows && rows > kRowCounters)
     return set_error(KK_E_UNSUPPORTED, "instance norm: %lld long rows", (long long)rows);
+  // y is monotonic in x with exact floats: no snake, and a LeakyRelu slope >= 0
+  const bool exact_bounds = !af.snake_a && (!af.leaky || af.alpha >= 0.0f);
   const int64_t nblk = long_rows ? ceil_div(T, kNpBlock) : 0;
-  const int64_t npart = long_rows ? rows * gx : rows;
-  if (npart > 0x7fffffff) return set_error(KK_E_UNSUPPORTED, "instance norm: too many partials");
+  const int64_t nmm = long_rows && !exact_bounds ? std::max(rows, rows * gx) : rows;
+  if (nmm > 0x7fffffff) return set_error(KK_E_UNSUPPORTED, "instance norm: too many partials");
   auto up = [](int64_t b) { return ceil_div(b, 256) * 256; };
-  const int64_t o_stats = 0, o_mm = up(8 * rows), o_par = o_mm + up(8 * npart);
-  const int64_t o_part = o_par + 256, total = o_part + up(4 * rows * nblk + 4);
+  const int64_t o_stats = 0, o_mm = up(8 * rows), o_par = o_mm + up(8 * nmm);
+  const int64_t o_part = o_par + 256, o_xmm = o_part + up(4 * rows * nblk + 4);
+  const int64_t o_flag = o_xmm + up(8 * rows * nblk + 8), total = o_flag + 256;
   void* ws = nullptr;
   KK_TRY(kk_alloc(static_cast<size_t>(total), &ws));
   char* base = static_cast<char*>(ws);
@@ -1152,6 +1249,17 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   float2* mm = reinterpret_cast<float2*>(base + o_mm);
   float2* params = reinterpret_cast<float2*>(base + o_par);
   float* part = reinterpret_cast<float*>(base + o_part);
+  float2* xmm = reinterpret_cast<float2*>(base + o_xmm);
+  int* flag = long_rows && !exact_bounds ? reinterpret_cast<int*>(base + o_flag) : nullptr;
+  float* ysp = static_cast<float*>(y_scale->data);
+  uint8_t* yzp = static_cast<uint8_t*>(y_zp->data);
+  const dim3 qgrid(static_cast<unsigned>(gx), static_cast<unsigned>(rows));
+  auto quant = [&](const int* only_if, int* check) {
+    hipLaunchKernelGGL(instnorm_quant, qgrid, dim3(kRowBlock), 0, st, static_cast<uint8_t*>(q->data),
+                       xp, static_cast<const float2*>(stats), static_cast<const float2*>(params), C, T,
+                       af, vec ? 1 : 0, only_if, check);
+    return check_launch("instnorm_quant");
+  };
   int rc = KK_OK;
   if (!long_rows) {
     hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
@@ -1163,24 +1271,20 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
     for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
       hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                          static_cast<int>(nblk), pass, stats, ctx().row_counters,
-                         counter_stride(rows), static_cast<float*>(nullptr), 0, eps);
+                         counter_stride(rows), static_cast<float*>(nullptr), 0, eps, xmm,
+                         pass == 1 ? mm : static_cast<float2*>(nullptr), C, af);
       rc = check_launch("np_blocks_kernel");
     }
-    if (rc == KK_OK) {
-      hipLaunchKernelGGL(instnorm_minmax, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(rows)),
-                         dim3(kRowBlock), 0, st, mm, xp, static_cast<const float2*>(stats), C, T, af);
-      rc = check_launch("instnorm_minmax");
-    }
   }
-  if (rc == KK_OK)
-    rc = launch_dql_fold(mm, static_cast<int>(npart), params, static_cast<float*>(y_scale->data),
-                         static_cast<uint8_t*>(y_zp->data));
-  if (rc == KK_OK) {
-    hipLaunchKernelGGL(instnorm_quant, dim3(static_cast<unsigned>(gx), static_cast<unsigned>(rows)),
-                       dim3(kRowBlock), 0, st, static_cast<uint8_t*>(q->data), xp,
-                       static_cast<const float2*>(stats), static_cast<const float2*>(params), C, T, af,
-                       vec ? 1 : 0);
-    rc = check_launch("instnorm_quant");
+  if (rc == KK_OK) rc = launch_dql_fold(mm, static_cast<int>(rows), params, ysp, yzp, nullptr, flag);
+  if (rc == KK_OK) rc = quant(nullptr, flag);
+  if (rc == KK_OK && flag) {  // only if a y fell outside the bounds
+    hipLaunchKernelGGL(instnorm_minmax, qgrid, dim3(kRowBlock), 0, st, mm, xp,
+                       static_cast<const float2*>(stats), C, T, af, static_cast<const int*>(flag));
+    rc = check_launch("instnorm_minmax");
+    if (rc == KK_OK)
+      rc = launch_dql_fold(mm, static_cast<int>(rows * gx), params, ysp, yzp, flag, nullptr);
+    if (rc == KK_OK) rc = quant(flag, nullptr);
   }
   kk_free(ws);  // stream order keeps it alive for the kernels above
   return rc;

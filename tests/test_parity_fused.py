@@ -149,6 +149,36 @@ def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
     assert_close(got, want, 1e-5, floor_rel=1e-6, what=f"InstanceNorm+snake C={C} T={T}")
 
 
+@pytest.mark.parametrize("C,T,rc_mul,leaky", [(64, 20000, 1.0, None), (64, 20000, 5.0, None),
+                                              (32, 24676, None, -0.5), (32, 24676, None, 0.2),
+                                              (48, 3000, 5.0, None)])
+def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leaky):
+    """InstanceNormQuant gives the same bytes, scale and zero point as the
+    device's own unfused chain: the float result stored, then
+    DynamicQuantizeLinear's (min, max) over the stored values.  Long rows
+    take the quantiser's range from each row's result at its x extremes
+    (exact where y is monotonic in x); a snake with recip = 5 / alpha, or a
+    LeakyRelu slope below 0, is not monotonic, so the quantising pass finds
+    values outside that range and the exact fallback passes run.  Rows held
+    in LDS form the exact range in one pass.  Scales of both signs."""
+    r = rng(26)
+    x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
+    g = r.normal(0, 1, (1, C, 1)).astype(np.float32)
+    b = (0.3 * r.normal(0, 1, (1, C, 1))).astype(np.float32)
+    D = gpu.to_device
+    if rc_mul is not None:
+        a = r.uniform(0.5, 2, (1, C, 1)).astype(np.float32)
+        rc = (np.float32(rc_mul) / a).astype(np.float32)
+        y = gpu.ops.instance_norm_scale_shift_snake(D(x), D(g), D(b), D(a), D(rc), 1e-5)
+        fused = gpu.ops.instance_norm_quant(D(x), D(g), D(b), D(a), D(rc), 1e-5)
+    else:
+        y = gpu.ops.instance_norm_scale_shift(D(x), D(g), D(b), 1e-5, leaky)
+        fused = gpu.ops.instance_norm_quant(D(x), D(g), D(b), eps=1e-5, leaky_alpha=leaky)
+    want = gpu.ops.dynamic_quantize_linear(y)
+    for got_t, want_t, what in zip(fused, want, ("bytes", "scale", "zero point")):
+        assert_bitexact(gpu.to_host(got_t), gpu.to_host(want_t), f"{what} C={C} T={T}")
+
+
 @pytest.mark.parametrize("C,T,kind", [(128, 40000, "affine"), (256, 7180, "leaky"),
                                       (128, 20000, "snake"), (64, 999, "snake"),
                                       (96, 2400, "plain"), (32, 24676, "leaky"),
