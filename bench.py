@@ -345,13 +345,13 @@ def run_gpu(args):
         5, 5, 1, 0), flops=2 * 512 * 256 * 2400 * 20 // 10, sets=4)
 
     roofline = {
-        "kernel": "instnorm_kernel (AdaIN T=9600, style Linear fused)",
+        "kernel": "instnorm_wide_kernel (AdaIN T=9600, style Linear fused)",
         "bound": "hbm",
         "achieved": dom["gbps"],
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(dom["gbps"] / HBM_PEAK_GBS, 4),
-        "traffic": pmc_traffic("instnorm_kernel"),
+        "traffic": pmc_traffic("instnorm_wide_kernel"),
         "algorithmic_bytes_per_launch": BYTES["adain_t9600"],
         "avg_launch_us": dom["us"],
         "copy_same_size_gbps": cp["gbps"],

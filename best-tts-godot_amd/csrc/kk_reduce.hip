@@ -126,10 +126,12 @@ struct StyleArgs {
   int64_t S;
 };
 
+// This thread's share (k = g, g + GROUP, ...) of the two dot products.
 template <int GROUP>
-__device__ __forceinline__ void style_affine(const StyleArgs& sa, int64_t C, int64_t c, int g,
-                                             float* lds, float& gamma, float& beta) {
-  float ag = 0.0f, ab = 0.0f;
+__device__ __forceinline__ void style_dots(const StyleArgs& sa, int64_t C, int64_t c, int g,
+                                           float& ag, float& ab) {
+  ag = 0.0f;
+  ab = 0.0f;
   const int64_t jg = c, jb = C + c;
   for (int64_t k = g; k < sa.S; k += GROUP) {
     const float s = sa.style[k];
@@ -142,11 +144,18 @@ __device__ __forceinline__ void style_affine(const StyleArgs& sa, int64_t C, int
     ag = __builtin_fmaf(s, wg, ag);
     ab = __builtin_fmaf(s, wb, ab);
   }
+}
+
+template <int GROUP>
+__device__ __forceinline__ void style_affine(const StyleArgs& sa, int64_t C, int64_t c, int g,
+                                             float* lds, float& gamma, float& beta) {
+  float ag, ab;
+  style_dots<GROUP>(sa, C, c, g, ag, ab);
   ag = group_sum<GROUP>(ag, lds);
   ab = group_sum<GROUP>(ab, lds);
   if (sa.bias) {
-    ag = ag + sa.bias[jg];
-    ab = ab + sa.bias[jb];
+    ag = ag + sa.bias[c];
+    ab = ab + sa.bias[C + c];
   }
   gamma = ag;
   beta = ab;
@@ -239,6 +248,75 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
 #pragma unroll
     for (int e = 0; e < VEC; ++e) r[j][e] = apply_affine<false>(r[j][e] / den, ra, af);
   store_row<GROUP, NV, VEC>(out + row * T, T, g, r);
+}
+
+// AdaIN with NW waves per row (one row per block of 64 * NW threads), for
+// rows long enough that 256 threads would each hold many vectors: more
+// waves in flight per row and fewer registers per thread (at [1,512,9600],
+// 8 waves per row run at 92% of a plain copy's rate against 83% for 4).
+template <int NW>
+__device__ __forceinline__ float wide_sum(float v, float* lds) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) lds[w] = v;
+  __syncthreads();
+  float t[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t[i] = lds[i];
+#pragma unroll
+  for (int h = NW / 2; h > 0; h /= 2)
+#pragma unroll
+    for (int i = 0; i < h; ++i) t[i] = t[i] + t[i + h];
+  return t[0];
+}
+
+template <int NW, int NV>
+__global__ void __launch_bounds__(64 * NW) instnorm_wide_kernel(float* __restrict__ out,
+                                                                const float* __restrict__ x,
+                                                                int64_t C, int64_t T, float eps,
+                                                                StyleArgs sa) {
+  constexpr int G = 64 * NW;
+  __shared__ float lds[NW];
+  const int g = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t c = row % C;
+  float r[NV][4];
+  load_row<G, NV, 4>(x + row * T, T, g, r);
+  float ag, ab;
+  style_dots<G>(sa, C, c, g, ag, ab);
+  ag = wide_sum<NW>(ag, lds);
+  ab = wide_sum<NW>(ab, lds);
+  if (sa.bias) {
+    ag = ag + sa.bias[c];
+    ab = ab + sa.bias[C + c];
+  }
+  Affine af{};
+  af.mode = 2;
+  const RowAffine ra = row_affine(af, C, c, ag, ab);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) s += r[j][e];
+  const float mean = wide_sum<NW>(s, lds) / static_cast<float>(T);
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int64_t base = (static_cast<int64_t>(j) * G + g) * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float d = r[j][e] - mean;
+      r[j][e] = d;
+      if (base + e < T) q += d * d;
+    }
+  }
+  const float den = sqrtf(wide_sum<NW>(q, lds) / static_cast<float>(T) + eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[j][e] = apply_affine<false>(r[j][e] / den, ra, af);
+  store_row<G, NV, 4>(out + row * T, T, g, r);
 }
 
 // Rows too long for registers: three passes over global memory.
@@ -1300,6 +1378,22 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
   RowShape rs;
   const bool vec_ok = (T % 4 == 0) && aligned16(x->data) && aligned16(out->data);
   if (af.mode != 2) return instnorm_np(out, x, rows, C, T, eps, af, vec_ok);
+  const int64_t nvec = T / 4;
+  if (vec_ok && nvec > 4 * kRowBlock && nvec <= 16 * kRowBlock) {
+    const int nv = static_cast<int>(ceil_div(nvec, 512));
+    const dim3 grid(static_cast<unsigned>(rows));
+    float* op = static_cast<float*>(out->data);
+    const float* xp = static_cast<const float*>(x->data);
+    hipStream_t st = ctx().stream;
+    switch (nv) {
+      case 3: hipLaunchKernelGGL((instnorm_wide_kernel<8, 3>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
+      case 4: hipLaunchKernelGGL((instnorm_wide_kernel<8, 4>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
+      case 5: hipLaunchKernelGGL((instnorm_wide_kernel<8, 5>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
+      case 6: hipLaunchKernelGGL((instnorm_wide_kernel<8, 6>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
+      default: hipLaunchKernelGGL((instnorm_wide_kernel<8, 8>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
+    }
+    return check_launch("instnorm_wide_kernel");
+  }
   if (pick_row_shape(T, vec_ok, &rs)) {
     KK_ROW_DISPATCH(instnorm_kernel, rs, rows, static_cast<float*>(out->data),
                     static_cast<const float*>(x->data), rows, C, T, eps, af, sa);

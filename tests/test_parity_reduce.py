@@ -23,7 +23,7 @@ def adain_inputs(c, t, seed=0):
     return x, s, w, b
 
 
-@pytest.mark.parametrize("t", [1200, 9600])
+@pytest.mark.parametrize("t", [1200, 9600, 4100, 6000, 13000, 16384])
 def test_adain_config(gpu, oracle, t):
     x, s, w, b = adain_inputs(512, t)
     got = gpu.ops.adain(gpu.to_device(x), gpu.to_device(s), gpu.to_device(w),
