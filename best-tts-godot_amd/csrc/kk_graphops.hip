@@ -378,28 +378,42 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
 // ------------------------------------------------------------------- STFT
 // out[b, f, k, 0/1] = sum_t (sig[b, f*step + t] * win[t]) * cos/sin(-2 pi k t / n),
 // the product in fp32 and the sum in fp64 (op_stft: float32 frames @ a
-// float64 basis), rounded to fp32.
-__global__ void stft_kernel(float* __restrict__ out, const float* __restrict__ sig,
-                            const void* __restrict__ win, int win_dt, int64_t batch,
-                            int64_t slen, int64_t nframes, int64_t nfreq, int64_t n,
-                            int64_t step) {
-  const int64_t total = batch * nframes * nfreq;
+// float64 basis), rounded to fp32.  Each block first builds the fp64 basis
+// (the same angles, -2.0 * pi * k * t / n) and the window in LDS; a thread
+// then takes one frame and all its frequencies.
+__global__ void __launch_bounds__(256) stft_kernel(float* __restrict__ out,
+                                                   const float* __restrict__ sig,
+                                                   const void* __restrict__ win, int win_dt,
+                                                   int64_t batch, int64_t slen, int64_t nframes,
+                                                   int nfreq, int n, int64_t step) {
+  extern __shared__ __align__(16) double stft_lds[];
+  double2* basis = reinterpret_cast<double2*>(stft_lds);                // [nfreq][n] (cos, sin)
+  float* w = reinterpret_cast<float*>(basis + static_cast<int64_t>(nfreq) * n);  // [n]
+  for (int i = threadIdx.x; i < nfreq * n; i += blockDim.x) {
+    const int k = i / n, t = i % n;
+    const double ang = -2.0 * M_PI * static_cast<double>(k) * static_cast<double>(t) /
+                       static_cast<double>(n);
+    basis[i] = make_double2(cos(ang), sin(ang));
+  }
+  for (int t = threadIdx.x; t < n; t += blockDim.x) w[t] = load_as_f32(win, win_dt, t);
+  __syncthreads();
+  const int64_t total = batch * nframes;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t k = i % nfreq;
-    const int64_t f = (i / nfreq) % nframes;
-    const int64_t bi = i / (nfreq * nframes);
+    const int64_t f = i % nframes, bi = i / nframes;
     const float* s = sig + bi * slen + f * step;
-    double re = 0.0, im = 0.0;
-    for (int64_t t = 0; t < n; ++t) {
-      const float fr = s[t] * load_as_f32(win, win_dt, t);
-      const double ang = -2.0 * M_PI * static_cast<double>(k) * static_cast<double>(t) /
-                         static_cast<double>(n);
-      re += static_cast<double>(fr) * cos(ang);
-      im += static_cast<double>(fr) * sin(ang);
+    float* o = out + i * nfreq * 2;
+    for (int k = 0; k < nfreq; ++k) {
+      const double2* bk = basis + static_cast<int64_t>(k) * n;
+      double re = 0.0, im = 0.0;
+      for (int t = 0; t < n; ++t) {
+        const double fr = static_cast<double>(s[t] * w[t]);
+        re += fr * bk[t].x;
+        im += fr * bk[t].y;
+      }
+      o[2 * k] = static_cast<float>(re);
+      o[2 * k + 1] = static_cast<float>(im);
     }
-    out[i * 2 + 0] = static_cast<float>(re);
-    out[i * 2 + 1] = static_cast<float>(im);
   }
 }
 
@@ -678,12 +692,18 @@ int kk_stft(const kk_tensor* out, const kk_tensor* signal, const kk_tensor* wind
   if (numel(out) != batch * nframes * nfreq * 2)
     return set_error(KK_E_ARG, "kk_stft: out must be [batch, %lld, %lld, 2]", (long long)nframes,
                      (long long)nfreq);
-  const int64_t total = batch * nframes * nfreq;
-  if (!total) return KK_OK;
-  hipLaunchKernelGGL(stft_kernel, dim3(grid1d(total)), dim3(256), 0, ctx().stream,
+  const int64_t total = batch * nframes;
+  if (!total || !nfreq) return KK_OK;
+  const size_t lds = sizeof(double) * 2 * static_cast<size_t>(nfreq * frame_length) +
+                     sizeof(float) * static_cast<size_t>(frame_length);
+  if (lds > 64 * 1024)
+    return set_error(KK_E_UNSUPPORTED, "kk_stft: frame_length %lld too long (basis > 64 KB)",
+                     (long long)frame_length);
+  const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 1024));
+  hipLaunchKernelGGL(stft_kernel, dim3(blocks), dim3(256), lds, ctx().stream,
                      static_cast<float*>(out->data), static_cast<const float*>(signal->data),
-                     window->data, window->dtype, batch, slen, nframes, nfreq, frame_length,
-                     frame_step);
+                     window->data, window->dtype, batch, slen, nframes, static_cast<int>(nfreq),
+                     static_cast<int>(frame_length), frame_step);
   return check_launch("stft_kernel");
 }
 

@@ -221,7 +221,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
                                                              float eps, Affine af,
                                                              StyleArgs sa) {
   __shared__ float lds[4];
-  constexpr int RPB = kRowBlock / GROUP;
+  const int RPB = blockDim.x / GROUP;  // 256 / GROUP, or 1 in 64-thread blocks
   const int g = threadIdx.x % GROUP;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
   // Every thread of the block takes part in the group reductions even when
@@ -493,7 +493,7 @@ __global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict_
                                                               int64_t rows, int64_t cols, float eps,
                                                               LnArgs la) {
   __shared__ float lds[4];
-  constexpr int RPB = kRowBlock / GROUP;
+  const int RPB = blockDim.x / GROUP;  // 256 / GROUP, or 1 in 64-thread blocks
   const int g = threadIdx.x % GROUP;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
   if constexpr (GROUP == 64) {
@@ -577,7 +577,7 @@ __global__ void __launch_bounds__(kRowBlock) softmax_kernel(float* __restrict__ 
                                                             const float* __restrict__ x,
                                                             int64_t rows, int64_t cols) {
   __shared__ float lds[4];
-  constexpr int RPB = kRowBlock / GROUP;
+  const int RPB = blockDim.x / GROUP;  // 256 / GROUP, or 1 in 64-thread blocks
   const int g = threadIdx.x % GROUP;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
   if constexpr (GROUP == 64) {
@@ -638,7 +638,7 @@ __global__ void __launch_bounds__(kRowBlock) reduce_rows_kernel(float* __restric
                                                                 const float* __restrict__ x,
                                                                 int64_t rows, int64_t cols, int op) {
   __shared__ float lds[4];
-  constexpr int RPB = kRowBlock / GROUP;
+  const int RPB = blockDim.x / GROUP;  // 256 / GROUP, or 1 in 64-thread blocks
   const int g = threadIdx.x % GROUP;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
   if constexpr (GROUP == 64) {
@@ -1140,41 +1140,49 @@ static bool pick_row_shape(int64_t n, bool vec_ok, RowShape* rs) {
   return false;
 }
 
+// One-wave rows go four to a 256-thread block, or one to a 64-thread block
+// when four to a block would leave fewer than two blocks per CU.
+static unsigned row_threads(const RowShape& rs, int64_t rows) {
+  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  return rs.group == 64 && ceil_div(rows, kRowBlock / 64) < 2 * cus ? 64u : unsigned(kRowBlock);
+}
+
 #define KK_ROW_DISPATCH(KERNEL, RS, GRID_ROWS, ...)                                          \
   do {                                                                                         \
-    const int _rpb = kRowBlock / (RS).group;                                                   \
+    const unsigned _threads = row_threads((RS), (GRID_ROWS));                                  \
+    const int _rpb = static_cast<int>(_threads) / (RS).group;                                  \
     const dim3 _grid(static_cast<unsigned>(ceil_div((GRID_ROWS), _rpb)));                      \
     hipStream_t _s = ctx().stream;                                                             \
     if ((RS).group == 64) {                                                                    \
       if ((RS).vec == 4) {                                                                     \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<64, 4, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<64, 4, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       } else {                                                                                 \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<64, 4, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<64, 4, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       }                                                                                        \
     } else {                                                                                   \
       if ((RS).vec == 4) {                                                                     \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<256, 16, 4>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<256, 16, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       } else {                                                                                 \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<256, 16, 1>), _grid, dim3(kRowBlock), 0, _s, __VA_ARGS__); break; \
+          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: hipLaunchKernelGGL((KERNEL<256, 16, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       }                                                                                        \
     }                                                                                          \

@@ -142,14 +142,19 @@ def test_lstm(gpu, oracle, seq, inp, init):
         assert_close(g, wv, 1e-4, floor_rel=1e-5, what=f"LSTM {name} seq={seq}")
 
 
-def test_stft(gpu, oracle):
+@pytest.mark.parametrize("batch,slen,n,step,onesided", [(1, 3005, 20, 5, 1), (2, 999, 16, 3, 0),
+                                                         (1, 1400003, 20, 5, 1)])
+def test_stft(gpu, oracle, batch, slen, n, step, onesided):
+    """Frames of n samples every `step` (the graph's n_fft 20, hop 5), the
+    one-sided and full spectra, two signals, and more frames than the grid
+    has threads (1400003 samples: 280,000 frames)."""
     r = rng(5)
-    sig = r.normal(0, 1, (1, 3005)).astype(np.float32)
-    win = np.hanning(20).astype(np.float16)
-    ins = [sig, ("host", np.array(5)), win, ("host", np.array(20))]
-    got = node(gpu, "STFT", ins, {"onesided": 1})
-    assert_close(got, onode(oracle, "STFT", ins, {"onesided": 1}), 1e-6, floor_rel=1e-7,
-                 what="STFT")
+    sig = r.normal(0, 1, (batch, slen)).astype(np.float32)
+    win = np.hanning(n).astype(np.float16)
+    ins = [sig, ("host", np.array(step)), win, ("host", np.array(n))]
+    got = node(gpu, "STFT", ins, {"onesided": onesided})
+    assert_close(got, onode(oracle, "STFT", ins, {"onesided": onesided}), 1e-6, floor_rel=1e-7,
+                 what=f"STFT batch={batch} n={n} step={step}")
 
 
 @pytest.mark.parametrize("mode,ctm,nm,scale,L", [("nearest", "asymmetric", "floor", 300.0, 37),
