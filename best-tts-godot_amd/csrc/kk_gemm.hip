@@ -603,10 +603,20 @@ __global__ void conv_transpose_direct_kernel(DirectArgs D) {
     const int64_t n = t / (D.Lout * D.Cout);
     const int64_t g = co / cout_g, coi = co % cout_g;
     const int64_t j = jo + D.p0;
+    const int64_t q0 = j / D.s, r0 = j - q0 * D.s;
     float acc = 0.0f;
     for (int64_t cl = 0; cl < cin_g; ++cl) {
       const int64_t ci = g * cin_g + cl;
       const float* xr = D.x + (n * D.Cin + ci) * D.L;
+      if (D.d == 1) {  // the taps k = r0, r0 + s, ... (j = q0 s + r0) read x[q0], x[q0 - 1], ...
+        for (int64_t k = r0, l = q0; k < D.K && l >= 0; k += D.s, --l) {
+          if (l >= D.L) continue;
+          float w = load_as_f32(D.w, D.w_dt, (ci * cout_g + coi) * D.K + k);
+          if (D.dq.active) w = dequant_value(w, D.dq, co);
+          acc = __builtin_fmaf(w, xr[l], acc);
+        }
+        continue;
+      }
       for (int64_t k = 0; k < D.K; ++k) {
         const int64_t num = j - k * D.d;
         if (num < 0 || num % D.s) continue;
@@ -618,6 +628,45 @@ __global__ void conv_transpose_direct_kernel(DirectArgs D) {
       }
     }
     D.out[t] = D.bias ? acc + D.bias[co] : acc;
+  }
+}
+
+// Tall, skinny products (N <= 4 columns, K <= 32): a thread per row of A,
+// its K values in registers, B's few values from cache.  The tiled kernel
+// would spend a 32- or 64-wide tile on each column here ([2154000, 9] x
+// [9, 1] in the harmonic source's Linear).
+constexpr int kSkinnyK = 32, kSkinnyN = 4;
+
+__global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs G, int64_t batch) {
+  const int64_t rows = batch * G.M;
+  const int K = static_cast<int>(G.K), N = static_cast<int>(G.N);
+  for (int64_t r = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; r < rows;
+       r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t bz = r / G.M, m = r % G.M;
+    const int64_t oa = batch_offset(G.bm, 0, bz), ob = batch_offset(G.bm, 1, bz),
+                  oo = batch_offset(G.bm, 2, bz);
+    float a[kSkinnyK];
+#pragma unroll
+    for (int k = 0; k < kSkinnyK; ++k) {
+      a[k] = 0.0f;
+      if (k < K) {
+        const float q = load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
+        a[k] = G.adq.active ? dequant_value(q, G.adq, m) : q;
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < kSkinnyN; ++n) {
+      if (n >= N) break;
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < kSkinnyK; ++k) {
+        if (k >= K) break;
+        float b = load_as_f32(G.b, G.b_dt, ob + k * G.b_si + n * G.b_sj);
+        if (G.dq.active) b = dequant_value(b, G.dq, n);
+        acc = __builtin_fmaf(a[k], b, acc);
+      }
+      G.out[oo + m * G.som + n * G.son] = G.alpha == 1.0f ? acc : acc * G.alpha;
+    }
   }
 }
 
@@ -682,6 +731,12 @@ static int conv_common(const kk_tensor* out, const kk_tensor* x, const kk_tensor
 }
 
 static int launch_gemm(const GemmArgs& args, int64_t batch) {
+  if (!args.out_i32 && args.N <= kSkinnyN && args.K <= kSkinnyK && args.M * batch >= 4096) {
+    const int64_t rows = args.M * batch;
+    const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(rows, 256), 1 << 16));
+    hipLaunchKernelGGL(gemm_skinny_kernel, dim3(grid), dim3(256), 0, ctx().stream, args, batch);
+    return check_launch("gemm_skinny_kernel");
+  }
   const TileSize ts = pick_tile(args.M, args.N, batch);
   const dim3 grid = grid_of(ts, args.M, args.N, batch);
   KK_TRY(check_grid(grid, batch));
@@ -915,7 +970,9 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
   KK_TRY(make_dequant(&dq, w, w_scale, w_zp, Cout, "kk_conv_transpose1d"));
   if (N * Cout * Lout == 0) return KK_OK;
   const float* bp = bias ? static_cast<const float*>(bias->data) : nullptr;
-  if (group == 1 && dilation == 1) {
+  // A few output channels: the direct kernel (a thread per output, only the
+  // taps that land on it); the tiles below would be mostly empty rows.
+  if (group == 1 && dilation == 1 && Cout > 4) {
     // Phase decomposition: s sub-GEMMs of MR = ceil(K/s) taps each.  Output
     // position jo maps to j = jo + p0 = q*s + r; every q up to the last
     // needed j is enumerated (x reads are bounds-checked, so the

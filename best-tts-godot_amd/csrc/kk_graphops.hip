@@ -483,9 +483,82 @@ __global__ void pad_kernel(float* __restrict__ out, const float* __restrict__ x,
   }
 }
 
+// Pad with one block row per output row (all axes but the last): the row's
+// source offset is worked out once, the last axis walked contiguously.
+__global__ void pad_rows_kernel(float* __restrict__ out, const float* __restrict__ x, PadArgs P,
+                                int64_t rows) {
+  const int last = P.rank - 1;
+  const int64_t lout = P.out_dims[last], dim = P.in_dims[last], b = P.begin[last];
+  const int64_t st = P.in_st[last];
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    int64_t rem = r, off = 0;
+    bool inside = true;
+    for (int d = last - 1; d >= 0; --d) {
+      const int64_t o = rem % P.out_dims[d];
+      rem /= P.out_dims[d];
+      int64_t s = o - P.begin[d];
+      const int64_t dd = P.in_dims[d];
+      if (s < 0 || s >= dd) {
+        if (P.mode == 0) inside = false;
+        else if (P.mode == 1) s = reflect_index(s, dd);
+        else s = s < 0 ? 0 : dd - 1;
+      }
+      off += s * P.in_st[d];
+    }
+    float* orow = out + r * lout;
+    for (int64_t o = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; o < lout;
+         o += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+      int64_t s = o - b;
+      bool in = inside;
+      if (s < 0 || s >= dim) {
+        if (P.mode == 0) in = false;
+        else if (P.mode == 1) s = reflect_index(s, dim);
+        else s = s < 0 ? 0 : dim - 1;
+      }
+      orow[o] = in ? x[off + s * st] : P.value;
+    }
+  }
+}
+
 // ----------------------------------------------------------------- CumSum
 // One thread per line, a sequential running sum in the input's type (numpy
 // cumsum accumulates in order, so fp32 results match bit for bit).
+// Lines of at most kCumsumLds fp32 values: a block per line stages it in
+// LDS, one thread runs the sum there (its reads do not wait on the chain
+// of additions, as global loads would), the block writes the line back.
+constexpr int kCumsumLds = 16384;
+
+__global__ void __launch_bounds__(256) cumsum_lds_kernel(float* __restrict__ out,
+                                                         const float* __restrict__ x,
+                                                         int64_t dim, int64_t inner) {
+  __shared__ __align__(16) float buf[kCumsumLds];
+  const int64_t line = blockIdx.x;
+  const int64_t o = line / inner, in = line % inner;
+  const float* xs = x + o * dim * inner + in;
+  float* os = out + o * dim * inner + in;
+  const int n = static_cast<int>(dim);
+  for (int d = threadIdx.x; d < n; d += blockDim.x) buf[d] = xs[d * inner];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float acc = 0.0f;
+    int d = 0;
+    for (; d + 4 <= n; d += 4) {
+      float4 v = *reinterpret_cast<const float4*>(buf + d);
+      acc = acc + v.x; v.x = acc;
+      acc = acc + v.y; v.y = acc;
+      acc = acc + v.z; v.z = acc;
+      acc = acc + v.w; v.w = acc;
+      *reinterpret_cast<float4*>(buf + d) = v;
+    }
+    for (; d < n; ++d) {
+      acc = acc + buf[d];
+      buf[d] = acc;
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < n; d += blockDim.x) os[d * inner] = buf[d];
+}
+
 template <typename T>
 __global__ void cumsum_kernel(T* __restrict__ out, const T* __restrict__ x, int64_t outer,
                               int64_t dim, int64_t inner) {
@@ -752,6 +825,15 @@ int kk_pad(const kk_tensor* out, const kk_tensor* x, const int64_t* pads, int mo
   }
   if (out->rank != x->rank) return set_error(KK_E_ARG, "kk_pad: out rank");
   if (!P.n) return KK_OK;
+  const int64_t lout = P.out_dims[P.rank - 1];
+  if (lout >= 1024) {
+    const int64_t rows = P.n / lout;
+    const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(lout, 256 * 4), 1 << 16)),
+                    static_cast<unsigned>(std::min<int64_t>(rows, 65535)));
+    hipLaunchKernelGGL(pad_rows_kernel, grid, dim3(256), 0, ctx().stream,
+                       static_cast<float*>(out->data), static_cast<const float*>(x->data), P, rows);
+    return check_launch("pad_rows_kernel");
+  }
   hipLaunchKernelGGL(pad_kernel, dim3(grid1d(P.n)), dim3(256), 0, ctx().stream,
                      static_cast<float*>(out->data), static_cast<const float*>(x->data), P);
   return check_launch("pad_kernel");
@@ -772,6 +854,12 @@ int kk_cumsum(const kk_tensor* out, const kk_tensor* x, int axis) {
   const int64_t dim = x->shape[axis];
   if (!numel(x)) return KK_OK;
   const dim3 g(grid1d(outer * inner));
+  if (x->dtype == KK_F32 && dim <= kCumsumLds && outer * inner <= 0x7fffffff) {
+    hipLaunchKernelGGL(cumsum_lds_kernel, dim3(static_cast<unsigned>(outer * inner)), dim3(256), 0,
+                       ctx().stream, static_cast<float*>(out->data), static_cast<const float*>(x->data),
+                       dim, inner);
+    return check_launch("cumsum_lds_kernel");
+  }
   switch (x->dtype) {
     case KK_F32:
       hipLaunchKernelGGL(cumsum_kernel<float>, g, dim3(256), 0, ctx().stream,

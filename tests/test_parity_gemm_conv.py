@@ -80,6 +80,18 @@ def test_matmul_odd_shapes(gpu, oracle, m, k, n):
           f"matmul {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("shape_a,shape_w", [((1, 50000, 9), (9, 1)), ((3, 2000, 7), (7, 3)),
+                                             ((4100, 32), (32, 4))])
+def test_matmul_skinny(gpu, oracle, shape_a, shape_w):
+    """Tall, skinny products (N <= 4, K <= 32: a thread per row), as the
+    harmonic source's Linear(9 -> 1) over every sample."""
+    r = rng(4)
+    a = r.normal(0, 1, shape_a).astype(np.float32)
+    w = r.normal(0, 0.3, shape_w).astype(np.float32)
+    check(gpu.ops.matmul(gpu.to_device(a), gpu.to_device(w)).numpy(), oracle.matmul(a, w),
+          f"matmul {shape_a} x {shape_w}")
+
+
 def test_attention_batched_and_fused(gpu, oracle):
     """[1,12,T,64] x [1,12,64,T] with the right operand a transposed view,
     FusedMatMul with transB and alpha, and vector operands."""

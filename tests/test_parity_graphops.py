@@ -171,11 +171,17 @@ def test_resize(gpu, oracle, mode, ctm, nm, scale, L):
 
 
 @pytest.mark.parametrize("mode", ["reflect", "edge", "constant"])
-def test_pad(gpu, oracle, mode):
-    x = rng(7).normal(0, 1, (1, 4, 30)).astype(np.float32)
-    pads = np.array([0, 0, 5, 0, 0, 3], np.int64)
+@pytest.mark.parametrize("shape,pads", [((1, 4, 30), [0, 0, 5, 0, 0, 3]),
+                                        ((1, 5, 2000), [0, 2, 7, 0, 1, 9]),
+                                        ((2, 3, 4097), [0, 0, 0, 0, 0, 1])])
+def test_pad(gpu, oracle, mode, shape, pads):
+    """Short rows (element-wise kernel) and rows of >= 1024 outputs (a block
+    row per output row), padding the middle axis and the last."""
+    x = rng(7).normal(0, 1, shape).astype(np.float32)
+    pads = np.array(pads, np.int64)
     got = node(gpu, "Pad", [x, ("host", pads)], {"mode": mode})
-    assert_bitexact(got, onode(oracle, "Pad", [x, ("host", pads)], {"mode": mode}), f"Pad {mode}")
+    assert_bitexact(got, onode(oracle, "Pad", [x, ("host", pads)], {"mode": mode}),
+                    f"Pad {mode} {shape}")
 
 
 def test_cumsum_scatter_range_nonzero(gpu, oracle):
@@ -183,6 +189,13 @@ def test_cumsum_scatter_range_nonzero(gpu, oracle):
     x = r.normal(0, 1, (1, 2, 5000)).astype(np.float32)
     got = node(gpu, "CumSum", [x, ("host", np.array(2, np.int32))])
     assert_bitexact(got, onode(oracle, "CumSum", [x, ("host", np.array(2, np.int32))]), "CumSum f32")
+    # the harmonic source's phase sum: 9 strided lines of 7180; and a line
+    # longer than the LDS stage (the thread-per-line kernel)
+    for shape, axis in (((1, 7180, 9), 1), ((2, 20000), 1)):
+        x = r.uniform(0, 0.1, shape).astype(np.float32)
+        ax = ("host", np.array(axis, np.int32))
+        assert_bitexact(node(gpu, "CumSum", [x, ax]), onode(oracle, "CumSum", [x, ax]),
+                        f"CumSum f32 {shape}")
     d = r.integers(1, 40, (1, 6)).astype(np.int64)
     got = node(gpu, "CumSum", [d, ("host", np.array(1, np.int32))])
     assert_bitexact(got, np.cumsum(d, axis=1), "CumSum int64")
