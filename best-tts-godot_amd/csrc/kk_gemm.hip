@@ -475,11 +475,13 @@ struct ConvArgs {
   const float* bias;   // [Cout] or NULL
   int64_t Cin, L, Kw, s, d, p0, Lout;
   int64_t M, K;        // Cout, Cin*Kw
+  const int* only_if;  // the launch does nothing unless *only_if is set (NULL: always runs)
 };
 
 // AK: 0 = quad loads of TW (K % 4 == 0), 1 = scalar gather.
 template <class C, int AK, typename TW>
 __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
+  if (A.only_if && *A.only_if == 0) return;
   const int64_t bz = blockIdx.z;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * C::BN;
@@ -519,10 +521,12 @@ struct ConvTArgs {
   float* out;          // [N, Cout, Lout]
   const float* bias;
   int64_t Cin, Cout, L, Kw, s, MR, p0, Lout, nq;
+  const int* only_if;  // the launch does nothing unless *only_if is set (NULL: always runs)
 };
 
 template <class C>
 __global__ void __launch_bounds__(kNT) conv_transpose_kernel(ConvTArgs A) {
+  if (A.only_if && *A.only_if == 0) return;
   const int64_t r = blockIdx.z % A.s;
   const int64_t bz = blockIdx.z / A.s;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
@@ -853,6 +857,12 @@ static int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* 
   return KK_OK;
 }
 
+// fp16-weight convolutions on the fp16 matrix cores (kk_conv_f16.hip):
+// true when launched; *flag is then the condition for the fp32 fallback.
+bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* bias,
+               bool transposed, int64_t stride, int64_t dilation, int64_t pad0, int64_t Nq,
+               void** ws, int** flag, int* rc);
+
 }  // namespace kk
 
 using namespace kk;
@@ -921,6 +931,16 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
     const TileSize ts = pick_tile(Cout, Lout, N);
     const dim3 grid = grid_of(ts, Cout, Lout, N);
     KK_TRY(check_grid(grid, N));
+    // fp16 weights: the fp16 matrix cores, this fp32 kernel only if flagged
+    void* hws = nullptr;
+    int* hflag = nullptr;
+    int rc = KK_OK;
+    if (!dq.active && convh_run(out, x, w, bias, false, stride, dilation, pad0, Lout, &hws, &hflag, &rc))
+      args.only_if = hflag;
+    if (rc != KK_OK) {
+      if (hws) kk_free(hws);
+      return rc;
+    }
     const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4 * dtype_size(w->dtype));
     if (!quad) {
       KK_TILED(conv1d_kernel, ts, grid, 1, float);
@@ -932,7 +952,9 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
         default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t); break;
       }
     }
-    return check_launch("conv1d_kernel");
+    rc = check_launch("conv1d_kernel");
+    if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
+    return rc;
   }
   DirectArgs D{};
   D.x = static_cast<const float*>(x->data); D.w = w->data; D.w_dt = w->dtype; D.dq = dq;
@@ -988,13 +1010,25 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
     const TileSize ts = pick_tile(Cout, args.nq, N * stride);
     const dim3 grid = grid_of(ts, Cout, args.nq, N * stride);
     KK_TRY(check_grid(grid, N * stride));
+    // fp16 weights: the fp16 matrix cores, this fp32 kernel only if flagged
+    void* hws = nullptr;
+    int* hflag = nullptr;
+    int rc = KK_OK;
+    if (!dq.active && convh_run(out, x, w, bias, true, stride, 1, pad0, args.nq, &hws, &hflag, &rc))
+      args.only_if = hflag;
+    if (rc != KK_OK) {
+      if (hws) kk_free(hws);
+      return rc;
+    }
     if (ts == TILE_L)
       hipLaunchKernelGGL(conv_transpose_kernel<CfgL>, grid, dim3(kNT), 0, ctx().stream, args);
     else if (ts == TILE_M)
       hipLaunchKernelGGL(conv_transpose_kernel<CfgM>, grid, dim3(kNT), 0, ctx().stream, args);
     else
       hipLaunchKernelGGL(conv_transpose_kernel<CfgS>, grid, dim3(kNT), 0, ctx().stream, args);
-    return check_launch("conv_transpose_kernel");
+    rc = check_launch("conv_transpose_kernel");
+    if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
+    return rc;
   }
   DirectArgs D{};
   D.x = static_cast<const float*>(x->data); D.w = w->data; D.w_dt = w->dtype; D.dq = dq;

@@ -91,14 +91,24 @@ class PackedGraph:
                  for op, ins, outs, at, _pl in graph["nodes"]]
         self.inputs = {k: str(v) for k, v in graph["inputs"].items()}
         self.output = str(graph["output"])
-        # Weights: float data on the device once (fp16 widened to fp32 there),
-        # integer data as-is; integer constants also stay on the host, where
-        # the shape-domain nodes read them.
+        # Weights: float data on the device once (fp16 widened to fp32 there,
+        # except the fp16 weights that only Conv/ConvTranspose read, which
+        # keep fp16 for the fp16 matrix-core convolutions), integer data
+        # as-is; integer constants also stay on the host, where the
+        # shape-domain nodes read them.
+        conv_w, other = set(), set()
+        for op, ins, _outs, _at in nodes:
+            for k, name in enumerate(ins):
+                (conv_w if op in ("Conv", "ConvTranspose") and k == 1 else other).add(name)
+        conv_w -= other
         self.weights = {}
         for tid, arr in weights.items():
             arr = np.asarray(arr)
             if arr.dtype.kind in "iub" and arr.dtype.itemsize >= 4 or arr.dtype == np.bool_:
                 self.weights[str(tid)] = arr
+                continue
+            if arr.dtype == np.float16 and str(tid) in conv_w:
+                self.weights[str(tid)] = to_device(arr)
                 continue
             if arr.dtype == np.float16:
                 t = to_device(arr).astype(np.float32)

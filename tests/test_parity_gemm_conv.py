@@ -227,6 +227,56 @@ def test_conv_transpose_cases(gpu, oracle, case):
 
 
 # ---------------------------------------------------- decoder stage chain
+# fp16 weights, channels in multiples of 32, enough work: the fp16 matrix
+# cores with each activation split into two fp16 halves (fp32 accuracy)
+F16MC = [  # (kind, n, cin, cout, k, L, p0, p1, s, d, op)
+    ("convT", 1, 256, 128, 12, 2000, 3, 3, 6, 1, 0),     # generator ups.1
+    ("convT", 1, 512, 256, 20, 700, 5, 5, 10, 1, 0),     # generator ups.0
+    ("convT", 2, 256, 64, 7, 1500, 2, 1, 3, 1, 1),       # two items, K not a multiple of s
+    ("conv", 1, 128, 22, 7, 20000, 3, 3, 1, 1, 0),       # conv_post
+    ("conv", 1, 128, 40, 5, 30000, 4, 2, 2, 3, 0),       # stride 2, dilation 3
+    ("conv", 2, 64, 160, 3, 8000, 1, 1, 1, 1, 0),        # two items, 160 channels
+]
+
+
+@pytest.mark.parametrize("case", F16MC)
+def test_fp16_weight_conv_matrix_cores(gpu, oracle, case):
+    kind, n, cin, cout, k, L, p0, p1, s, d, op = case
+    r = rng(9)
+    x = r.normal(0, 1, (n, cin, L)).astype(np.float32)
+    x[0, 0, :50] *= 1e-6  # tiny activations (their low halves are fp16 subnormals)
+    b = r.normal(0, 0.1, cout).astype(np.float32)
+    if kind == "convT":
+        w = r.normal(0, 0.05, (cin, cout, k)).astype(np.float16)
+        got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b),
+                                       (p0, p1), s, d, 1, op).numpy()
+        want = oracle.conv_transpose1d(x, w, b, (p0, p1), s, d, 1, op)
+    else:
+        w = r.normal(0, 0.05, (cout, cin, k)).astype(np.float16)
+        got = gpu.ops.conv1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (p0, p1), s,
+                             d).numpy()
+        want = oracle.conv1d(x, w, b, (p0, p1), s, d)
+    check(got, want, f"fp16-weight {case}")
+
+
+def test_fp16_weight_conv_overflow_falls_back(gpu, oracle):
+    """An activation beyond fp16's range sends the whole convolution to the
+    fp32 kernels (launched after the matrix-core pass, run only if flagged)."""
+    r = rng(10)
+    x = r.normal(0, 1, (1, 256, 2000)).astype(np.float32)
+    x[0, 5, 123] = 1.0e5
+    w = r.normal(0, 0.05, (256, 128, 12)).astype(np.float16)
+    b = r.normal(0, 0.1, 128).astype(np.float32)
+    got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (3, 3),
+                                   6).numpy()
+    check(got, oracle.conv_transpose1d(x, w, b, (3, 3), 6), "convT with a 1e5 activation")
+    x2 = r.normal(0, 1, (1, 128, 20000)).astype(np.float32)
+    x2[0, 100, 7] = -np.float32(4.0e4)
+    w2 = r.normal(0, 0.05, (22, 128, 7)).astype(np.float16)
+    got = gpu.ops.conv1d(gpu.to_device(x2), gpu.to_device(w2), None, (3, 3)).numpy()
+    check(got, oracle.conv1d(x2, w2, None, (3, 3)), "conv with a -4e4 activation")
+
+
 def test_decoder_upsample_stage(gpu, oracle):
     """int8 ConvTranspose1d(512->256, k20, s10, p5) on [1,512,240], snake,
     AdaIN with style [1,128], then two residual blocks
