@@ -1,7 +1,10 @@
-// Conv1d and ConvTranspose1d with fp16 weights on the fp16 matrix cores,
-// fp32 results.
+// Conv1d and ConvTranspose1d with fp16 or 8-bit weights on the fp16 matrix
+// cores, fp32 results.
 //
-// An fp16 weight is exact in fp16.  Each fp32 activation x is split into
+// An fp16 weight is exact in fp16, and so is an 8-bit weight less its zero
+// point (|q - zp| <= 255); the 8-bit weights' scale, per tensor or per
+// output channel, multiplies the fp32 sum (sum (q - zp) s x = s sum (q - zp) x,
+// the same value up to fp32 rounding).  Each fp32 activation x is split into
 // hi = fp16(x) and lo = fp16(x - hi) (x - hi is exact in fp32), so hi + lo
 // equals x to within 2^-22 |x|; every product w*hi and w*lo is exact in
 // fp32 (11 + 11 significant bits), and v_mfma_f32_32x32x16_f16 accumulates
@@ -21,7 +24,12 @@
 //     Wt[co*P + r][m*Cin + ci] = W[ci][co][r + stride*m] (0 past the kernel).
 //     A block's rows hold every phase of its output channels, so its
 //     stores fill whole lines of the interleaved output in its L2.
-// The weights are rearranged into Wt by a small kernel in the same call.
+// A call rearranges W into Wt (fp16, less the zero point) in a pooled
+// workspace first, so each K-step loads its weight rows as 16-byte vectors.
+// While a graph is being recorded nothing may be allocated: the kernel then
+// gathers the same fp16 values from W itself (slower, the same results bit
+// for bit).  The overflow flag is a slot of the library context; a
+// one-thread kernel after the fallback clears it.
 #include <algorithm>
 
 #include "kk_internal.h"
@@ -33,12 +41,19 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 32;        // K-step (halves)
+#ifndef KK_CONVH_BK
+#define KK_CONVH_BK 32
+#endif
+constexpr int kBK = KK_CONVH_BK;  // K-step (halves)
 constexpr int kPitch = kBK + 8;  // LDS row pitch (halves): 80 bytes
 constexpr int kThreads = 256;
 
 struct HArgs {
-  const _Float16* wt;  // [M = Cout*P][Kg]
+  const _Float16* wt;  // [M][Kg] when rearranged, else NULL
+  const void* w;       // conv [Cout][Cin][Kw], transposed [Cin][Cout][Kw]
+  int transposed;
+  int64_t Kw, s;       // kernel taps, stride (the phase count P for transposed)
+  Dequant dq;          // 8-bit weights: zero point subtracted, scale applied to the sums
   const float* x;      // [N, Cin, L]
   float* out;          // [N, Cout, Lout]
   const float* bias;   // [Cout] or NULL
@@ -54,16 +69,17 @@ struct Tile {
   static constexpr int WAVES_M = WAVES_M_, WM_T = WM_T_, WN_T = WN_T_;
   static constexpr int WAVES_N = 4 / WAVES_M;
   static constexpr int BM = WAVES_M * 32 * WM_T, BN = WAVES_N * 32 * WN_T;
-  // A staging: BM rows of 4 chunks of 8 halves
-  static constexpr int A_CHUNKS = BM * 4;
-  static constexpr int A_PER = (A_CHUNKS + kThreads - 1) / kThreads;
+  // A staging: thread -> row t % BM, KPT consecutive k from KPT * (t / BM)
+  static constexpr int KPT = BM * kBK / kThreads;
+  static_assert(kThreads % BM == 0 && KPT % 4 == 0, "A staging shape");
   // B staging: thread -> column n = t % BN, k pairs t / BN + j * (256 / BN)
   static constexpr int KP_STEP = kThreads / BN;
   static constexpr int B_PAIRS = (kBK / 2) / KP_STEP;
   static_assert(kThreads % BN == 0 && (kBK / 2) % KP_STEP == 0, "B staging shape");
 };
 
-template <class T>
+// PRE: the weights come rearranged in A.wt; else gathered from A.w.
+template <class T, typename TW, bool PRE>
 __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
   __shared__ __align__(16) _Float16 As[2][T::BM * kPitch];
   __shared__ __align__(16) _Float16 Bh[2][T::BN * kPitch];
@@ -74,28 +90,50 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T::BN;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * T::BM;
   const int64_t b = blockIdx.z;
-  const _Float16* wt = A.wt;
   const float* xb = A.x + b * A.Cin * A.L;
   const int64_t nk = A.Kg / kBK;
+  const TW* w = static_cast<const TW*>(A.w);
+
+  // this thread's A row: m = co*P + r, and its weights' zero point
+  const int am = tid % T::BM, ak = T::KPT * (tid / T::BM);
+  const int64_t m_row = m0 + am;
+  const int64_t a_co = m_row / A.P, a_r = m_row - a_co * A.P;
+  const bool a_in = m_row < A.M;
+  const float a_zp = A.dq.zp && a_in ? load_as_f32(A.dq.zp, A.dq.zp_dt, a_co * A.dq.zp_stride) : 0.0f;
+  const int64_t cout = A.M / A.P;
+  // step between consecutive ci in W
+  const int64_t w_ci = A.transposed ? cout * A.Kw : A.Kw;
 
   // staging registers
-  uint4 areg[T::A_PER];
+  _Float16 av[T::KPT];
   float bv[T::B_PAIRS][2];
   bool bad = false;
   const int bn = tid % T::BN;
   const int64_t q = n0 + bn;
   auto fetch = [&](int64_t k0) {
+    const int64_t t = k0 / A.Cin, ci0 = k0 - t * A.Cin;
+    if constexpr (PRE) {
+      typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 #pragma unroll
-    for (int p = 0; p < T::A_PER; ++p) {
-      const int c = tid + p * kThreads;
-      areg[p] = make_uint4(0, 0, 0, 0);
-      if (c < T::A_CHUNKS) {
-        const int64_t row = m0 + c / 4;
-        if (row < A.M)
-          areg[p] = *reinterpret_cast<const uint4*>(wt + row * A.Kg + k0 + 8 * (c % 4));
+      for (int e = 0; e < T::KPT; e += 4) {
+        h4v v = {};
+        if (a_in) v = *reinterpret_cast<const h4v*>(A.wt + m_row * A.Kg + k0 + ak + e);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) av[e + u] = v[u];
+      }
+    } else {
+      // W[co][ci][t] (conv) or W[ci][co][r + s*t] (transposed, 0 past the kernel)
+      const int64_t tap = A.transposed ? a_r + A.s * t : t;
+      const bool tap_in = a_in && tap < A.Kw;
+      const int64_t wbase = A.transposed ? ((ci0 + ak) * cout + a_co) * A.Kw + tap
+                                         : (a_co * A.Cin + ci0 + ak) * A.Kw + tap;
+#pragma unroll
+      for (int e = 0; e < T::KPT; ++e) {
+        float v = 0.0f;
+        if (tap_in) v = static_cast<float>(w[wbase + e * w_ci]) - a_zp;
+        av[e] = static_cast<_Float16>(v);
       }
     }
-    const int64_t t = k0 / A.Cin, ci0 = k0 - t * A.Cin;
     const int64_t pos = q * A.qs + t * A.tap_mul + A.tap_add;
     const bool in = q < A.Nq && pos >= 0 && pos < A.L;
 #pragma unroll
@@ -108,10 +146,10 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
   };
   auto stash = [&](int buf) {
 #pragma unroll
-    for (int p = 0; p < T::A_PER; ++p) {
-      const int c = tid + p * kThreads;
-      if (c < T::A_CHUNKS)
-        *reinterpret_cast<uint4*>(&As[buf][(c / 4) * kPitch + 8 * (c % 4)]) = areg[p];
+    for (int e = 0; e < T::KPT; e += 4) {
+      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<h4*>(&As[buf][am * kPitch + ak + e]) =
+          h4{av[e], av[e + 1], av[e + 2], av[e + 3]};
     }
 #pragma unroll
     for (int j = 0; j < T::B_PAIRS; ++j) {
@@ -180,79 +218,89 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
       if (m >= A.M) continue;
       const int64_t co = m / A.P, r = m - co * A.P;
       const float bias = A.bias ? A.bias[co] : 0.0f;
+      const float sc = A.dq.scale ? load_as_f32(A.dq.scale, A.dq.scale_dt, co * A.dq.scale_stride)
+                                  : 1.0f;
 #pragma unroll
       for (int j = 0; j < WN_T; ++j) {
         const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
         const int64_t pos = qq * A.os + r + A.ophase0;
-        if (qq < A.Nq && pos >= 0 && pos < A.Lout)
-          ob[co * A.Lout + pos] = A.bias ? acc[i][j][g] + bias : acc[i][j][g];
+        const float v = A.dq.scale ? acc[i][j][g] * sc : acc[i][j][g];
+        if (qq < A.Nq && pos >= 0 && pos < A.Lout) ob[co * A.Lout + pos] = A.bias ? v + bias : v;
       }
     }
 }
 
-// Wt from W (fp16): conv (transposed = 0) W [Cout][Cin][K] -> Wt[co][k*Cin + ci];
-// transposed W [Cin][Cout][K] -> Wt[co*P + r][m*Cin + ci] = W[ci][co][r + s*m].
-// Also clears the overflow flag.
-__global__ void convh_weights(_Float16* __restrict__ wt, const _Float16* __restrict__ w,
-                              int64_t Cout, int64_t Cin, int64_t Kw, int64_t taps, int64_t P,
-                              int64_t s, int transposed, int* flag) {
-  const int64_t Kg = taps * Cin, total = P * Cout * Kg;
-  if (blockIdx.x == 0 && threadIdx.x == 0) *flag = 0;
+__global__ void convh_flag_clear(int* flag) { *flag = 0; }
+
+// Wt[m][kk] (m = co*P + r, kk = t*Cin + ci): the fp16 value the gathering
+// kernel forms, W less the zero point (0 past the kernel for transposed).
+template <typename TW>
+__global__ void convh_weights(_Float16* __restrict__ wt, HArgs A) {
+  const TW* w = static_cast<const TW*>(A.w);
+  const int64_t total = A.M * A.Kg, cout = A.M / A.P;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t kk = i % Kg, m = i / Kg;
-    const int64_t co = m / P, r = m - co * P;
-    const int64_t t = kk / Cin, ci = kk % Cin;
-    _Float16 v = static_cast<_Float16>(0.0f);
-    if (!transposed) {
-      v = w[(co * Cin + ci) * Kw + t];
-    } else {
-      const int64_t k = r + s * t;
-      if (k < Kw) v = w[(ci * Cout + co) * Kw + k];
+    const int64_t kk = i % A.Kg, m = i / A.Kg;
+    const int64_t co = m / A.P, r = m - co * A.P;
+    const int64_t t = kk / A.Cin, ci = kk - t * A.Cin;
+    const int64_t tap = A.transposed ? r + A.s * t : t;
+    float v = 0.0f;
+    if (tap < A.Kw) {
+      const int64_t idx = A.transposed ? (ci * cout + co) * A.Kw + tap : (co * A.Cin + ci) * A.Kw + tap;
+      const float zp = A.dq.zp ? load_as_f32(A.dq.zp, A.dq.zp_dt, co * A.dq.zp_stride) : 0.0f;
+      v = static_cast<float>(w[idx]) - zp;
     }
-    wt[i] = v;
+    wt[i] = static_cast<_Float16>(v);
   }
 }
 
+template <class T, typename TW>
+static void launch_t(const HArgs& a, const dim3& grid) {
+  if (a.wt)
+    hipLaunchKernelGGL((convh_kernel<T, TW, true>), grid, dim3(kThreads), 0, ctx().stream, a);
+  else
+    hipLaunchKernelGGL((convh_kernel<T, TW, false>), grid, dim3(kThreads), 0, ctx().stream, a);
+}
+
 template <class T>
-static void launch(const HArgs& a, int64_t batch) {
+static void launch(const HArgs& a, int w_dt, int64_t batch) {
   const dim3 grid(static_cast<unsigned>(ceil_div(a.Nq, T::BN)), static_cast<unsigned>(ceil_div(a.M, T::BM)),
                   static_cast<unsigned>(batch));
-  hipLaunchKernelGGL(convh_kernel<T>, grid, dim3(kThreads), 0, ctx().stream, a);
+  if (w_dt == KK_F16) launch_t<T, _Float16>(a, grid);
+  else if (w_dt == KK_I8) launch_t<T, int8_t>(a, grid);
+  else launch_t<T, uint8_t>(a, grid);
 }
 
 }  // namespace convh
 
 using namespace convh;
 
-// Launches the fp16-weight convolution when it applies and returns true;
-// *flag then points at the overflow flag (in *ws, which the caller frees
-// after launching its fp32 fallback with that flag as condition).
-bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* bias,
-               bool transposed, int64_t stride, int64_t dilation, int64_t pad0, int64_t Nq,
-               void** ws, int** flag, int* rc) {
-  *rc = KK_OK;
-  if (w->dtype != KK_F16 || x->dtype != KK_F32) return false;
+// Launches the fp16 matrix-core convolution when it applies and returns
+// true; *flag is then the condition for the caller's fp32 fallback, which
+// the caller launches next and follows with convh_clear(*flag), and *ws the
+// workspace to kk_free after that (NULL while a graph is recorded).
+bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const Dequant& dq,
+               const kk_tensor* bias, bool transposed, int64_t stride, int64_t dilation,
+               int64_t pad0, int64_t Nq, int** flag, void** ws) {
+  *ws = nullptr;
+  // fp16 weights as they are; 8-bit weights less an 8-bit zero point
+  const bool w16 = w->dtype == KK_F16 && !dq.active;
+  const bool w8 = (w->dtype == KK_I8 || w->dtype == KK_U8) &&
+                  (!dq.zp || dq.zp_dt == KK_I8 || dq.zp_dt == KK_U8);
+  if (!(w16 || w8) || x->dtype != KK_F32) return false;
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = out->shape[1], Lout = out->shape[2], Kw = w->shape[2];
-  if (Cin % 32 || (transposed && dilation != 1)) return false;
+  if (Cin % kBK || (transposed && dilation != 1)) return false;
   const int64_t taps = transposed ? ceil_div(Kw, stride) : Kw;
   const int64_t P = transposed ? stride : 1;
   const int64_t Kg = taps * Cin, M = P * Cout;
-  if (M * Nq * Kg < (int64_t{1} << 27) || N > 65535 || ceil_div(M, 32) > 65535 ||
-      ceil_div(Nq, 128) > 0x7fffffff)
+  if (M * Nq * Kg < (int64_t{1} << 26) || N > 65535 || ceil_div(M, 32) > 65535 ||
+      ceil_div(Nq, 32) > 0x7fffffff || numel(w) > 0x7fffffff)
     return false;
-  const int64_t wt_bytes = ceil_div(M * Kg * 2, 256) * 256;
-  *rc = kk_alloc(static_cast<size_t>(wt_bytes + 256), ws);
-  if (*rc != KK_OK) return false;
-  _Float16* wt = static_cast<_Float16*>(*ws);
-  *flag = reinterpret_cast<int*>(static_cast<char*>(*ws) + wt_bytes);
-  const int64_t total = M * Kg;
-  hipLaunchKernelGGL(convh_weights, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 4096))),
-                     dim3(256), 0, ctx().stream, wt, static_cast<const _Float16*>(w->data), Cout, Cin,
-                     Kw, taps, P, stride, transposed ? 1 : 0, *flag);
+  *flag = ctx().row_counters + kRowCounters + kFlagConvh;
   HArgs a{};
-  a.wt = wt; a.x = static_cast<const float*>(x->data); a.out = static_cast<float*>(out->data);
+  a.w = w->data; a.transposed = transposed ? 1 : 0; a.Kw = Kw; a.s = stride; a.dq = dq;
+  a.x = static_cast<const float*>(x->data); a.out = static_cast<float*>(out->data);
   a.bias = bias ? static_cast<const float*>(bias->data) : nullptr; a.flag = *flag;
   a.Cin = Cin; a.L = L; a.M = M; a.Cout = Cout; a.Kg = Kg; a.Nq = Nq; a.Lout = Lout;
   a.P = static_cast<int>(P);
@@ -261,11 +309,28 @@ bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, con
   } else {
     a.qs = stride; a.tap_mul = dilation; a.tap_add = -pad0; a.os = 1; a.ophase0 = 0;
   }
-  if (M <= 32) launch<Tile<1, 1, 1>>(a, N);
-  else if (M <= 64) launch<Tile<2, 1, 2>>(a, N);
-  else launch<Tile<2, 2, 2>>(a, N);
-  *rc = check_launch("convh_kernel");
+  if (!ctx().capturing && kk_alloc(static_cast<size_t>(M * Kg * 2), ws) == KK_OK) {
+    _Float16* wt = static_cast<_Float16*>(*ws);
+    const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(M * Kg, 256), 4096));
+    if (w->dtype == KK_F16)
+      hipLaunchKernelGGL(convh_weights<_Float16>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+    else if (w->dtype == KK_I8)
+      hipLaunchKernelGGL(convh_weights<int8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+    else
+      hipLaunchKernelGGL(convh_weights<uint8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+    a.wt = wt;
+  }
+  // the largest tile that still gives every CU two blocks; 128 x 32 below that
+  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  if (M <= 32) launch<Tile<1, 1, 1>>(a, w->dtype, N);
+  else if (M <= 64) launch<Tile<2, 1, 2>>(a, w->dtype, N);
+  else if (N * ceil_div(M, 128) * ceil_div(Nq, 128) >= 2 * cus) launch<Tile<2, 2, 2>>(a, w->dtype, N);
+  else launch<Tile<4, 1, 1>>(a, w->dtype, N);
   return true;
+}
+
+void convh_clear(int* flag) {
+  hipLaunchKernelGGL(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, flag);
 }
 
 }  // namespace kk

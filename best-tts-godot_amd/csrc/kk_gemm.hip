@@ -859,9 +859,10 @@ static int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* 
 
 // fp16-weight convolutions on the fp16 matrix cores (kk_conv_f16.hip):
 // true when launched; *flag is then the condition for the fp32 fallback.
-bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* bias,
-               bool transposed, int64_t stride, int64_t dilation, int64_t pad0, int64_t Nq,
-               void** ws, int** flag, int* rc);
+bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const Dequant& dq,
+               const kk_tensor* bias, bool transposed, int64_t stride, int64_t dilation,
+               int64_t pad0, int64_t Nq, int** flag, void** ws);
+void convh_clear(int* flag);
 
 }  // namespace kk
 
@@ -931,16 +932,11 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
     const TileSize ts = pick_tile(Cout, Lout, N);
     const dim3 grid = grid_of(ts, Cout, Lout, N);
     KK_TRY(check_grid(grid, N));
-    // fp16 weights: the fp16 matrix cores, this fp32 kernel only if flagged
-    void* hws = nullptr;
+    // fp16 / 8-bit weights: the fp16 matrix cores, this fp32 kernel only if flagged
     int* hflag = nullptr;
-    int rc = KK_OK;
-    if (!dq.active && convh_run(out, x, w, bias, false, stride, dilation, pad0, Lout, &hws, &hflag, &rc))
+    void* hws = nullptr;
+    if (convh_run(out, x, w, dq, bias, false, stride, dilation, pad0, Lout, &hflag, &hws))
       args.only_if = hflag;
-    if (rc != KK_OK) {
-      if (hws) kk_free(hws);
-      return rc;
-    }
     const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4 * dtype_size(w->dtype));
     if (!quad) {
       KK_TILED(conv1d_kernel, ts, grid, 1, float);
@@ -952,9 +948,9 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
         default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t); break;
       }
     }
-    rc = check_launch("conv1d_kernel");
+    if (hflag) convh_clear(hflag);
     if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
-    return rc;
+    return check_launch("conv1d_kernel");
   }
   DirectArgs D{};
   D.x = static_cast<const float*>(x->data); D.w = w->data; D.w_dt = w->dtype; D.dq = dq;
@@ -1010,25 +1006,20 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
     const TileSize ts = pick_tile(Cout, args.nq, N * stride);
     const dim3 grid = grid_of(ts, Cout, args.nq, N * stride);
     KK_TRY(check_grid(grid, N * stride));
-    // fp16 weights: the fp16 matrix cores, this fp32 kernel only if flagged
-    void* hws = nullptr;
+    // fp16 / 8-bit weights: the fp16 matrix cores, this fp32 kernel only if flagged
     int* hflag = nullptr;
-    int rc = KK_OK;
-    if (!dq.active && convh_run(out, x, w, bias, true, stride, 1, pad0, args.nq, &hws, &hflag, &rc))
+    void* hws = nullptr;
+    if (convh_run(out, x, w, dq, bias, true, stride, 1, pad0, args.nq, &hflag, &hws))
       args.only_if = hflag;
-    if (rc != KK_OK) {
-      if (hws) kk_free(hws);
-      return rc;
-    }
     if (ts == TILE_L)
       hipLaunchKernelGGL(conv_transpose_kernel<CfgL>, grid, dim3(kNT), 0, ctx().stream, args);
     else if (ts == TILE_M)
       hipLaunchKernelGGL(conv_transpose_kernel<CfgM>, grid, dim3(kNT), 0, ctx().stream, args);
     else
       hipLaunchKernelGGL(conv_transpose_kernel<CfgS>, grid, dim3(kNT), 0, ctx().stream, args);
-    rc = check_launch("conv_transpose_kernel");
+    if (hflag) convh_clear(hflag);
     if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
-    return rc;
+    return check_launch("conv_transpose_kernel");
   }
   DirectArgs D{};
   D.x = static_cast<const float*>(x->data); D.w = w->data; D.w_dt = w->dtype; D.dq = dq;

@@ -20,10 +20,14 @@ struct Context {
   int num_cus = 0;
   bool capturing = false;  // between kk_graph_begin and kk_graph_end
   // Per-row arrival counters of the multi-block row reductions, zero
-  // between launches (the last block of a row resets its counter).
+  // between launches (the last block of a row resets its counter), then
+  // kFlagSlots flags, also zero between calls (the call that sets one
+  // clears it after reading it).
   int* row_counters = nullptr;
 };
 constexpr int kRowCounters = 65536;
+constexpr int kFlagSlots = 64;
+constexpr int kFlagConvh = 0;  // fp16 matrix-core convolution: an activation out of range
 
 // DynamicQuantizeLinear's byte of x with the scale rounded to fp32 and the
 // zero point as a float: clamp(rint(x / scale) + zp, 0, 255)

@@ -375,8 +375,9 @@ int kk_init(int device) {
   hipDeviceProp_t prop;
   KK_HIP(hipGetDeviceProperties(&prop, device));
   c.num_cus = prop.multiProcessorCount;
-  KK_HIP(hipMalloc(reinterpret_cast<void**>(&c.row_counters), sizeof(int) * kRowCounters));
-  KK_HIP(hipMemset(c.row_counters, 0, sizeof(int) * kRowCounters));
+  KK_HIP(hipMalloc(reinterpret_cast<void**>(&c.row_counters),
+                   sizeof(int) * (kRowCounters + kFlagSlots)));
+  KK_HIP(hipMemset(c.row_counters, 0, sizeof(int) * (kRowCounters + kFlagSlots)));
   c.device = device;
   c.ready = true;
   return KK_OK;

@@ -227,36 +227,54 @@ def test_conv_transpose_cases(gpu, oracle, case):
 
 
 # ---------------------------------------------------- decoder stage chain
-# fp16 weights, channels in multiples of 32, enough work: the fp16 matrix
-# cores with each activation split into two fp16 halves (fp32 accuracy)
-F16MC = [  # (kind, n, cin, cout, k, L, p0, p1, s, d, op)
-    ("convT", 1, 256, 128, 12, 2000, 3, 3, 6, 1, 0),     # generator ups.1
-    ("convT", 1, 512, 256, 20, 700, 5, 5, 10, 1, 0),     # generator ups.0
-    ("convT", 2, 256, 64, 7, 1500, 2, 1, 3, 1, 1),       # two items, K not a multiple of s
-    ("conv", 1, 128, 22, 7, 20000, 3, 3, 1, 1, 0),       # conv_post
-    ("conv", 1, 128, 40, 5, 30000, 4, 2, 2, 3, 0),       # stride 2, dilation 3
-    ("conv", 2, 64, 160, 3, 8000, 1, 1, 1, 1, 0),        # two items, 160 channels
+# fp16 or 8-bit weights, channels in multiples of 32, enough work: the fp16
+# matrix cores with each activation split into two fp16 halves (fp32
+# accuracy); 8-bit weights less their zero point, the scale on the sums
+F16MC = [  # (kind, n, cin, cout, k, L, p0, p1, s, d, op, wdt)
+    ("convT", 1, 256, 128, 12, 2000, 3, 3, 6, 1, 0, "f16"),     # generator ups.1
+    ("convT", 1, 512, 256, 20, 700, 5, 5, 10, 1, 0, "f16"),     # generator ups.0
+    ("convT", 2, 256, 64, 7, 1500, 2, 1, 3, 1, 1, "f16"),       # two items, K not a multiple of s
+    ("conv", 1, 128, 22, 7, 20000, 3, 3, 1, 1, 0, "f16"),       # conv_post
+    ("conv", 1, 128, 40, 5, 30000, 4, 2, 2, 3, 0, "f16"),       # stride 2, dilation 3
+    ("conv", 2, 64, 160, 3, 8000, 1, 1, 1, 1, 0, "f16"),        # two items, 160 channels
+    ("convT", 1, 512, 256, 20, 240, 5, 5, 10, 1, 0, "i8"),      # the upsample config, int8
+    ("convT", 1, 256, 128, 12, 1000, 3, 3, 6, 1, 0, "u8c"),     # uint8, per-channel scale + zp
+    ("conv", 1, 256, 96, 3, 6000, 1, 1, 1, 2, 0, "i8"),         # int8 per tensor, dilation 2
+    ("conv", 1, 128, 64, 5, 8000, 2, 2, 1, 1, 0, "u8c"),        # uint8, per-channel scale + zp
 ]
 
 
 @pytest.mark.parametrize("case", F16MC)
 def test_fp16_weight_conv_matrix_cores(gpu, oracle, case):
-    kind, n, cin, cout, k, L, p0, p1, s, d, op = case
+    kind, n, cin, cout, k, L, p0, p1, s, d, op, wdt = case
     r = rng(9)
     x = r.normal(0, 1, (n, cin, L)).astype(np.float32)
     x[0, 0, :50] *= 1e-6  # tiny activations (their low halves are fp16 subnormals)
     b = r.normal(0, 0.1, cout).astype(np.float32)
-    if kind == "convT":
-        w = r.normal(0, 0.05, (cin, cout, k)).astype(np.float16)
-        got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b),
-                                       (p0, p1), s, d, 1, op).numpy()
-        want = oracle.conv_transpose1d(x, w, b, (p0, p1), s, d, 1, op)
+    shape = (cin, cout, k) if kind == "convT" else (cout, cin, k)
+    bshape = (1, cout, 1) if kind == "convT" else (cout, 1, 1)  # per output channel
+    sc = zp = None
+    if wdt == "f16":
+        w = r.normal(0, 0.05, shape).astype(np.float16)
+        wdeq = w
+    elif wdt == "i8":
+        w, sc = int8_weight(r, shape)
+        wdeq = oracle.dequantize(w, sc)
     else:
-        w = r.normal(0, 0.05, (cout, cin, k)).astype(np.float16)
-        got = gpu.ops.conv1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (p0, p1), s,
-                             d).numpy()
-        want = oracle.conv1d(x, w, b, (p0, p1), s, d)
-    check(got, want, f"fp16-weight {case}")
+        w = r.integers(0, 256, shape).astype(np.uint8)
+        sc = r.uniform(1e-4, 1e-3, cout).astype(np.float32)
+        zp = r.integers(100, 156, cout).astype(np.uint8)
+        wdeq = oracle.dequantize(w, sc.reshape(bshape), zp.reshape(bshape))
+    dv = gpu.to_device
+    kw = dict(w_scale=dv(np.asarray(sc)) if sc is not None else None,
+              w_zp=dv(zp) if zp is not None else None)
+    if kind == "convT":
+        got = gpu.ops.conv_transpose1d(dv(x), dv(w), dv(b), (p0, p1), s, d, 1, op, **kw).numpy()
+        want = oracle.conv_transpose1d(x, wdeq, b, (p0, p1), s, d, 1, op)
+    else:
+        got = gpu.ops.conv1d(dv(x), dv(w), dv(b), (p0, p1), s, d, **kw).numpy()
+        want = oracle.conv1d(x, wdeq, b, (p0, p1), s, d)
+    check(got, want, f"{wdt}-weight {case}")
 
 
 def test_fp16_weight_conv_overflow_falls_back(gpu, oracle):
