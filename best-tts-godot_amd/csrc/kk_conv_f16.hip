@@ -24,12 +24,13 @@
 //     Wt[co*P + r][m*Cin + ci] = W[ci][co][r + stride*m] (0 past the kernel).
 //     A block's rows hold every phase of its output channels, so its
 //     stores fill whole lines of the interleaved output in its L2.
-// A call rearranges W into Wt (fp16, less the zero point) in a pooled
-// workspace first, so each K-step loads its weight rows as 16-byte vectors.
-// While a graph is being recorded nothing may be allocated: the kernel then
-// gathers the same fp16 values from W itself (slower, the same results bit
-// for bit).  The overflow flag is a slot of the library context; a
-// one-thread kernel after the fallback clears it.
+// A call rearranges W into Wt (fp16, less the zero point) first, in the
+// library context's scratch (a pooled workspace when larger), so each K-step
+// loads its weight rows as vectors.  A Wt beyond the scratch while a graph
+// is being recorded (nothing may be allocated then) is not stored: the
+// kernel gathers the same fp16 values from W itself (slower, the same
+// results bit for bit).  The overflow flag is a slot of the library
+// context; a one-thread kernel after the fallback clears it.
 #include <algorithm>
 
 #include "kk_internal.h"
@@ -223,8 +224,8 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
 #pragma unroll
       for (int j = 0; j < WN_T; ++j) {
         const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
-        const int64_t pos = qq * A.os + r + A.ophase0;
         const float v = A.dq.scale ? acc[i][j][g] * sc : acc[i][j][g];
+        const int64_t pos = qq * A.os + r + A.ophase0;
         if (qq < A.Nq && pos >= 0 && pos < A.Lout) ob[co * A.Lout + pos] = A.bias ? v + bias : v;
       }
     }
@@ -271,6 +272,34 @@ static void launch(const HArgs& a, int w_dt, int64_t batch) {
   else launch_t<T, uint8_t>(a, grid);
 }
 
+// Rearranges the weights into the context scratch (or, larger, into a
+// pooled workspace unless a graph is being recorded; else the kernel
+// gathers them); launches the tile that suits M x Nq.
+static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
+  const size_t wt_bytes = static_cast<size_t>(a.M * a.Kg * 2);
+  void* wtp = nullptr;
+  if (wt_bytes <= kScratchBytes) wtp = ctx().scratch;
+  else if (!ctx().capturing && kk_alloc(wt_bytes, ws) == KK_OK) wtp = *ws;
+  if (wtp) {
+    _Float16* wt = static_cast<_Float16*>(wtp);
+    const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(a.M * a.Kg, 256), 4096));
+    if (w->dtype == KK_F16)
+      hipLaunchKernelGGL(convh_weights<_Float16>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+    else if (w->dtype == KK_I8)
+      hipLaunchKernelGGL(convh_weights<int8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+    else
+      hipLaunchKernelGGL(convh_weights<uint8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+    a.wt = wt;
+  }
+  // the largest tile that still gives every CU two blocks; 128 x 32 below that
+  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  if (a.M <= 32) launch<Tile<1, 1, 1>>(a, w->dtype, batch);
+  else if (a.M <= 64) launch<Tile<2, 1, 2>>(a, w->dtype, batch);
+  else if (batch * ceil_div(a.M, 128) * ceil_div(a.Nq, 128) >= 2 * cus)
+    launch<Tile<2, 2, 2>>(a, w->dtype, batch);
+  else launch<Tile<4, 1, 1>>(a, w->dtype, batch);
+}
+
 }  // namespace convh
 
 using namespace convh;
@@ -309,23 +338,7 @@ bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, con
   } else {
     a.qs = stride; a.tap_mul = dilation; a.tap_add = -pad0; a.os = 1; a.ophase0 = 0;
   }
-  if (!ctx().capturing && kk_alloc(static_cast<size_t>(M * Kg * 2), ws) == KK_OK) {
-    _Float16* wt = static_cast<_Float16*>(*ws);
-    const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(M * Kg, 256), 4096));
-    if (w->dtype == KK_F16)
-      hipLaunchKernelGGL(convh_weights<_Float16>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
-    else if (w->dtype == KK_I8)
-      hipLaunchKernelGGL(convh_weights<int8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
-    else
-      hipLaunchKernelGGL(convh_weights<uint8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
-    a.wt = wt;
-  }
-  // the largest tile that still gives every CU two blocks; 128 x 32 below that
-  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
-  if (M <= 32) launch<Tile<1, 1, 1>>(a, w->dtype, N);
-  else if (M <= 64) launch<Tile<2, 1, 2>>(a, w->dtype, N);
-  else if (N * ceil_div(M, 128) * ceil_div(Nq, 128) >= 2 * cus) launch<Tile<2, 2, 2>>(a, w->dtype, N);
-  else launch<Tile<4, 1, 1>>(a, w->dtype, N);
+  run(a, w, N, ws);
   return true;
 }
 

@@ -308,9 +308,11 @@ struct BIm2col {
 // ------------------------------------------------------------- MFMA core
 // Lane layout of v_mfma_f32_16x16x4_f32: lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; D element (i, j) lives in lane j + 16*(i/4), register i%4.
+// K-steps [kt0, kt1) of the product (kt1 < 0: to the end of K).
 template <class C, class LA, class LB, class ST>
 __device__ __forceinline__ void gemm_run(LA& la, LB& lb, const ST& store, int64_t M, int64_t N,
-                                         int64_t K, int64_t m0, int64_t n0) {
+                                         int64_t K, int64_t m0, int64_t n0, int64_t kt0 = 0,
+                                         int64_t kt1 = -1) {
   __shared__ __align__(16) float As[2][kBK * C::PA];
   __shared__ __align__(16) float Bs[2][kBK * C::PB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -321,14 +323,14 @@ __device__ __forceinline__ void gemm_run(LA& la, LB& lb, const ST& store, int64_
 #pragma unroll
     for (int j = 0; j < C::WTN; ++j) acc[i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
-  const int64_t nk = ceil_div(K, kBK);
-  la.fetch(0);
-  lb.fetch(0);
+  const int64_t nk = kt1 < 0 ? ceil_div(K, kBK) : kt1;
+  la.fetch(kt0 * kBK);
+  lb.fetch(kt0 * kBK);
   la.stash(As[0]);
   lb.stash(Bs[0]);
   __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int buf = static_cast<int>(kt & 1);
+  for (int64_t kt = kt0; kt < nk; ++kt) {
+    const int buf = static_cast<int>((kt - kt0) & 1);
     const bool more = kt + 1 < nk;
     if (more) {
       la.fetch((kt + 1) * kBK);
@@ -385,13 +387,22 @@ struct GemmArgs {
   BatchMap bm;
   int64_t M, N, K;
   float alpha;
+  const int* only_if;  // the launch does nothing unless *only_if is set (NULL: always runs)
+  // split-K: blockIdx.z = batch * splits + split; with splits > 1 each
+  // split stores its raw partial tile at part[((b*splits + split)*M + m)*N + n]
+  // and gemm_splitk_reduce forms out
+  int splits;
+  float* part;
 };
 
 // A kinds: 0 = K-contiguous quads of TA, 1 = scalar gather.
 // B kinds: 0 = N-contiguous quads of TB, 1 = scalar gather.
 template <class C, int AK, int BK, typename TA, typename TB>
 __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
-  const int64_t bz = blockIdx.z;
+  if (G.only_if && *G.only_if == 0) return;
+  const int splits = G.splits > 1 ? G.splits : 1;
+  const int64_t bz = blockIdx.z / splits;
+  const int split = static_cast<int>(blockIdx.z % splits);
   const int64_t oa = batch_offset(G.bm, 0, bz), ob = batch_offset(G.bm, 1, bz),
                 oo = batch_offset(G.bm, 2, bz);
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
@@ -400,11 +411,16 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
   const float alpha = G.alpha;
   const int64_t som = G.som, son = G.son;
   const bool out_i32 = G.out_i32;
+  const int64_t M = G.M, N = G.N, K = G.K;
+  float* part = splits > 1 ? G.part + ((bz * splits + split) * M) * N : nullptr;
   auto store = [&](int64_t m, int64_t n, float v) {
-    if (out_i32) reinterpret_cast<int32_t*>(out)[m * som + n * son] = __float2int_rn(v);
+    if (part) part[m * N + n] = v;
+    else if (out_i32) reinterpret_cast<int32_t*>(out)[m * som + n * son] = __float2int_rn(v);
     else out[m * som + n * son] = alpha == 1.0f ? v : v * alpha;
   };
-  const int64_t M = G.M, N = G.N, K = G.K;
+  // this split's K-steps
+  const int64_t nk_all = ceil_div(K, kBK), chunk = ceil_div(nk_all, splits);
+  const int64_t kt0 = split * chunk, kt1 = std::min<int64_t>(nk_all, kt0 + chunk);
   auto getA = [&](int64_t m, int64_t k) -> float {
     if (m >= M || k >= K) return 0.0f;
     const float q = load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
@@ -420,26 +436,26 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
     la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, G.adq);
     BQuad<C, TB> lb;
     lb.init(static_cast<const TB*>(G.b) + ob, G.b_si, N, K, n0, G.dq);
-    gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+    gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
   } else if constexpr (AK == 0) {
     AQuad<C, TA> la;
     la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, G.adq);
     if (G.b_si == 1) {
       BScalar<C, decltype(getB), false> lb{getB, n0};
-      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
     } else {
       BScalar<C, decltype(getB), true> lb{getB, n0};
-      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
     }
   } else if constexpr (BK == 0) {
     BQuad<C, TB> lb;
     lb.init(static_cast<const TB*>(G.b) + ob, G.b_si, N, K, n0, G.dq);
     if (G.a_si == 1) {
       AScalar<C, decltype(getA), false> la{getA, m0};
-      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
     } else {
       AScalar<C, decltype(getA), true> la{getA, m0};
-      gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+      gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
     }
   } else {
     // consecutive threads walk the unit-stride direction of each operand
@@ -447,19 +463,19 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
       AScalar<C, decltype(getA), false> la{getA, m0};
       if (G.b_si == 1) {
         BScalar<C, decltype(getB), false> lb{getB, n0};
-        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
       } else {
         BScalar<C, decltype(getB), true> lb{getB, n0};
-        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
       }
     } else {
       AScalar<C, decltype(getA), true> la{getA, m0};
       if (G.b_si == 1) {
         BScalar<C, decltype(getB), false> lb{getB, n0};
-        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
       } else {
         BScalar<C, decltype(getB), true> lb{getB, n0};
-        gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+        gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
       }
     }
   }
@@ -506,6 +522,24 @@ __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
     };
     AScalar<C, decltype(getA), true> la{getA, m0};
     gemm_run<C>(la, lb, store, M, N, K, m0, n0);
+  }
+}
+
+// out[b][m][n] = the splits' partials summed in split order (then alpha, or
+// MatMulInteger's rounding to int32).
+__global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs G, int64_t batch) {
+  const int64_t MN = G.M * G.N, total = batch * MN;
+  const int S = G.splits;
+  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t bz = i / MN, mn = i - bz * MN;
+    const int64_t m = mn / G.N, n = mn - m * G.N;
+    const float* p = G.part + bz * S * MN + mn;
+    float v = p[0];
+    for (int s = 1; s < S; ++s) v = v + p[s * MN];
+    const int64_t o = batch_offset(G.bm, 2, bz) + m * G.som + n * G.son;
+    if (G.out_i32) reinterpret_cast<int32_t*>(G.out)[o] = __float2int_rn(v);
+    else G.out[o] = G.alpha == 1.0f ? v : v * G.alpha;
   }
 }
 
@@ -642,6 +676,7 @@ __global__ void conv_transpose_direct_kernel(DirectArgs D) {
 constexpr int kSkinnyK = 32, kSkinnyN = 4;
 
 __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs G, int64_t batch) {
+  if (G.only_if && *G.only_if == 0) return;
   const int64_t rows = batch * G.M;
   const int K = static_cast<int>(G.K), N = static_cast<int>(G.N);
   for (int64_t r = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; r < rows;
@@ -671,6 +706,45 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs G, int64_t ba
       }
       G.out[oo + m * G.som + n * G.son] = G.alpha == 1.0f ? acc : acc * G.alpha;
     }
+  }
+}
+
+// ConvTranspose1d with few output channels, group 1, dilation 1 (the
+// iSTFT's 22 -> 1): the dequantised weights in LDS, a thread per output
+// walking only its taps (k = j mod s, + s, ...), the same order of terms as
+// the direct kernel above.
+constexpr int kSmallTW = 4096;  // weights held in LDS
+
+__global__ void __launch_bounds__(256) conv_transpose_small_kernel(DirectArgs D) {
+  __shared__ float ws[kSmallTW];
+  const int nw = static_cast<int>(D.Cin * D.Cout * D.K);
+  for (int i = threadIdx.x; i < nw; i += blockDim.x) {
+    float w = load_as_f32(D.w, D.w_dt, i);
+    if (D.dq.active) w = dequant_value(w, D.dq, (i / static_cast<int>(D.K)) % static_cast<int>(D.Cout));
+    ws[i] = w;
+  }
+  __syncthreads();
+  const int K = static_cast<int>(D.K), s = static_cast<int>(D.s), Cout = static_cast<int>(D.Cout);
+  const int64_t total = D.N * D.Cout * D.Lout;
+  for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+       t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t jo = t % D.Lout;
+    const int64_t nco = t / D.Lout;
+    const int co = static_cast<int>(nco % D.Cout);
+    const int64_t n = nco / D.Cout;
+    const int64_t j = jo + D.p0;
+    const int64_t q0 = j / s;
+    const int r0 = static_cast<int>(j - q0 * s);
+    const float* xn = D.x + n * D.Cin * D.L;
+    float acc = 0.0f;
+    for (int ci = 0; ci < static_cast<int>(D.Cin); ++ci) {
+      const float* xr = xn + ci * D.L;
+      const float* wr = ws + (ci * Cout + co) * K;
+      int64_t l = q0;
+      for (int k = r0; k < K && l >= 0; k += s, --l)
+        if (l < D.L) acc = __builtin_fmaf(wr[k], xr[l], acc);
+    }
+    D.out[t] = D.bias ? acc + D.bias[co] : acc;
   }
 }
 
@@ -742,8 +816,30 @@ static int launch_gemm(const GemmArgs& args, int64_t batch) {
     return check_launch("gemm_skinny_kernel");
   }
   const TileSize ts = pick_tile(args.M, args.N, batch);
-  const dim3 grid = grid_of(ts, args.M, args.N, batch);
+  dim3 grid = grid_of(ts, args.M, args.N, batch);
   KK_TRY(check_grid(grid, batch));
+  // Split K when the tiles leave CUs idle and the K loop is long (each
+  // K-step waits on its loads): partials in the context scratch, summed in
+  // split order by a second kernel.
+  GemmArgs args_s = args;
+  {
+    const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+    const int64_t blocks = static_cast<int64_t>(grid.x) * grid.y * grid.z;
+    const int64_t nk = ceil_div(args.K, kBK);
+    int64_t S = 1;
+    while (S < 8 && blocks * S < 2 * cus && nk / (2 * S) >= 4 &&
+           static_cast<size_t>(batch * 2 * S * args.M * args.N) * 4 <= kScratchBytes &&
+           batch * 2 * S <= 65535)
+      S *= 2;
+    if (S > 1) {
+      args_s.splits = static_cast<int>(S);
+      args_s.part = static_cast<float*>(ctx().scratch);
+      grid.z = static_cast<unsigned>(batch * S);
+    }
+  }
+  const GemmArgs& args0 = args;
+  {
+  const GemmArgs& args = args_s;
   // Vector paths: A fp32 with K contiguous; B with N contiguous; rows (and
   // batch strides) whole 4-element groups, aligned to them.
   const int bsz = dtype_size(args.b_dt);
@@ -780,7 +876,16 @@ static int launch_gemm(const GemmArgs& args, int64_t batch) {
   } else {
     KK_TILED(gemm_kernel, ts, grid, 1, 1, float, float);
   }
-  return check_launch("gemm_kernel");
+  KK_TRY(check_launch("gemm_kernel"));
+  if (args.splits > 1) {
+    const int64_t total = batch * args.M * args.N;
+    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 4096))),
+                       dim3(256), 0, ctx().stream, args, batch);
+    KK_TRY(check_launch("gemm_splitk_reduce"));
+  }
+  }
+  (void)args0;
+  return KK_OK;
 }
 
 
@@ -1027,6 +1132,11 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
   D.N = N; D.Cin = Cin; D.L = L; D.Cout = Cout; D.K = K; D.Lout = Lout;
   D.s = stride; D.d = dilation; D.p0 = pad0; D.group = group;
   const int64_t total = N * Cout * Lout;
+  if (group == 1 && dilation == 1 && Cin * Cout * K <= kSmallTW) {
+    const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 2048));
+    hipLaunchKernelGGL(conv_transpose_small_kernel, dim3(g), dim3(256), 0, ctx().stream, D);
+    return check_launch("conv_transpose_small_kernel");
+  }
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 1 << 20));
   hipLaunchKernelGGL(conv_transpose_direct_kernel, dim3(grid), dim3(256), 0, ctx().stream, D);
   return check_launch("conv_transpose_direct_kernel");

@@ -24,7 +24,14 @@ struct Context {
   // kFlagSlots flags, also zero between calls (the call that sets one
   // clears it after reading it).
   int* row_counters = nullptr;
+  // Device scratch owned by the context from kk_init to kk_shutdown, for
+  // per-call intermediates that must not be allocated (calls recorded into
+  // graphs): every call runs on the one stream, so each use is finished
+  // before the next call's kernels run, and the buffer never moves while a
+  // recorded graph may refer to it.
+  void* scratch = nullptr;
 };
+constexpr size_t kScratchBytes = size_t{16} << 20;
 constexpr int kRowCounters = 65536;
 constexpr int kFlagSlots = 64;
 constexpr int kFlagConvh = 0;  // fp16 matrix-core convolution: an activation out of range

@@ -378,6 +378,7 @@ int kk_init(int device) {
   KK_HIP(hipMalloc(reinterpret_cast<void**>(&c.row_counters),
                    sizeof(int) * (kRowCounters + kFlagSlots)));
   KK_HIP(hipMemset(c.row_counters, 0, sizeof(int) * (kRowCounters + kFlagSlots)));
+  KK_HIP(hipMalloc(&c.scratch, kScratchBytes));
   c.device = device;
   c.ready = true;
   return KK_OK;
@@ -397,6 +398,7 @@ int kk_shutdown(void) {
   pool_release_all();
   staging_release();
   if (c.row_counters) { (void)hipFree(c.row_counters); c.row_counters = nullptr; }
+  if (c.scratch) { (void)hipFree(c.scratch); c.scratch = nullptr; }
   for (int i = 0; i < KK_MAX_EVENTS; ++i)
     if (g_event_made[i]) { (void)hipEventDestroy(g_events[i]); g_event_made[i] = false; }
   (void)hipStreamDestroy(c.stream);

@@ -80,6 +80,40 @@ def test_matmul_odd_shapes(gpu, oracle, m, k, n):
           f"matmul {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("wdt", ["f16", "i8c", "u8c"])
+def test_matmul_weights_batched(gpu, oracle, wdt):
+    """fp16 / 8-bit weights (per-column scale and zero point) shared by a
+    batch of fp32 rows; FusedMatMul's alpha; a large activation.  [2,300,512]
+    x [512,640] leaves CUs idle at one K range per tile, so K is split and
+    the partials summed in split order."""
+    r = rng(11)
+    a = r.normal(0, 1, (2, 300, 512)).astype(np.float32)
+    n = 640
+    if wdt == "f16":
+        w = r.normal(0, 0.05, (512, n)).astype(np.float16)
+        sc = zp = None
+        wdeq = w.astype(np.float32)
+    else:
+        dt = np.int8 if wdt == "i8c" else np.uint8
+        lo, hi = (-127, 128) if wdt == "i8c" else (0, 256)
+        w = r.integers(lo, hi, (512, n)).astype(dt)
+        sc = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+        zp = r.integers(-3, 4, n).astype(dt) if wdt == "i8c" else r.integers(120, 136, n).astype(dt)
+        wdeq = oracle.dequantize(w, sc, zp)
+    dv = gpu.to_device
+    got = gpu.ops.matmul(dv(a), dv(w), dv(sc) if sc is not None else None,
+                         dv(zp) if zp is not None else None).numpy()
+    check(got, oracle.matmul(a, wdeq), f"matmul {wdt} batched")
+    if wdt == "f16":
+        env = {"a": dv(a), "w": dv(w)}
+        gpu.dispatch("FusedMatMul", ["a", "w"], ["y"], {"alpha": 0.125}, env)
+        check(env["y"].numpy(), oracle.fused_matmul(a, wdeq, 0, 0, 0.125), "FusedMatMul alpha")
+        a2 = a.copy()
+        a2[1, 7, 100] = 7.0e4
+        got = gpu.ops.matmul(dv(a2), dv(w)).numpy()
+        check(got, oracle.matmul(a2, wdeq), "matmul with a 7e4 activation")
+
+
 @pytest.mark.parametrize("shape_a,shape_w", [((1, 50000, 9), (9, 1)), ((3, 2000, 7), (7, 3)),
                                              ((4100, 32), (32, 4))])
 def test_matmul_skinny(gpu, oracle, shape_a, shape_w):

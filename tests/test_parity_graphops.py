@@ -74,6 +74,13 @@ def test_matmul_integer(gpu, oracle):
     ins = [a[:, :10, :512], np.ascontiguousarray(b[:512, :50]), azp, bzp[:50]]
     assert_bitexact(node(gpu, "MatMulInteger", ins), onode(oracle, "MatMulInteger", ins),
                     "MatMulInteger N=50")
+    # the FFN's down projection: K = 2048, so K is split four ways and the
+    # integer partials summed (exactly) in split order
+    a2 = r.integers(0, 256, (1, 130, 2048)).astype(np.uint8)
+    b2 = r.integers(-127, 128, (2048, 768)).astype(np.int8)
+    ins = [a2, b2, azp, bzp[:768]]
+    assert_bitexact(node(gpu, "MatMulInteger", ins), onode(oracle, "MatMulInteger", ins),
+                    "MatMulInteger K=2048")
 
 
 @pytest.mark.parametrize("cin,cout,k,L,pad,dil", [(512, 512, 3, 240, 1, 1), (1090, 1024, 3, 40, 1, 1),
