@@ -237,6 +237,7 @@ __global__ void convh_flag_clear(int* flag) { *flag = 0; }
 // kernel forms, W less the zero point (0 past the kernel for transposed).
 template <typename TW>
 __global__ void convh_weights(_Float16* __restrict__ wt, HArgs A) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *A.flag = 0;  // this call's overflow flag starts clear
   const TW* w = static_cast<const TW*>(A.w);
   const int64_t total = A.M * A.Kg, cout = A.M / A.P;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
@@ -290,6 +291,8 @@ static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
     else
       hipLaunchKernelGGL(convh_weights<uint8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
     a.wt = wt;
+  } else {
+    hipLaunchKernelGGL(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, a.flag);
   }
   // the largest tile that still gives every CU two blocks; 128 x 32 below that
   const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
@@ -306,8 +309,9 @@ using namespace convh;
 
 // Launches the fp16 matrix-core convolution when it applies and returns
 // true; *flag is then the condition for the caller's fp32 fallback, which
-// the caller launches next and follows with convh_clear(*flag), and *ws the
-// workspace to kk_free after that (NULL while a graph is recorded).
+// the caller launches next, and *ws a workspace to kk_free after that (or
+// NULL).  The flag is cleared at the start of each call (by the weight
+// rearrangement, or a one-thread kernel when there is none).
 bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const Dequant& dq,
                const kk_tensor* bias, bool transposed, int64_t stride, int64_t dilation,
                int64_t pad0, int64_t Nq, int** flag, void** ws) {
@@ -342,8 +346,5 @@ bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, con
   return true;
 }
 
-void convh_clear(int* flag) {
-  hipLaunchKernelGGL(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, flag);
-}
 
 }  // namespace kk

@@ -967,7 +967,6 @@ static int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* 
 bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const Dequant& dq,
                const kk_tensor* bias, bool transposed, int64_t stride, int64_t dilation,
                int64_t pad0, int64_t Nq, int** flag, void** ws);
-void convh_clear(int* flag);
 
 }  // namespace kk
 
@@ -1053,7 +1052,6 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
         default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t); break;
       }
     }
-    if (hflag) convh_clear(hflag);
     if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
     return check_launch("conv1d_kernel");
   }
@@ -1122,7 +1120,6 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
       hipLaunchKernelGGL(conv_transpose_kernel<CfgM>, grid, dim3(kNT), 0, ctx().stream, args);
     else
       hipLaunchKernelGGL(conv_transpose_kernel<CfgS>, grid, dim3(kNT), 0, ctx().stream, args);
-    if (hflag) convh_clear(hflag);
     if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
     return check_launch("conv_transpose_kernel");
   }
