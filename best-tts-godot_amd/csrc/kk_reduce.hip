@@ -45,6 +45,25 @@ __device__ __forceinline__ float group_max(float v, float* lds) {
   }
 }
 
+// Two independent group sums in one LDS round (each sum in group_sum's
+// order, so the results are the same bits); lds holds 8 floats.
+template <int GROUP>
+__device__ __forceinline__ void group_sum_pair(float& a, float& b, float* lds) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  if constexpr (GROUP != 64) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) {
+      lds[w] = a;
+      lds[4 + w] = b;
+    }
+    __syncthreads();
+    a = (lds[0] + lds[1]) + (lds[2] + lds[3]);
+    b = (lds[4] + lds[5]) + (lds[6] + lds[7]);
+  }
+}
+
 // Loads this thread's share of a row of `n` floats into r[NV][VEC].
 // Element index of (j, e) is (j * GROUP + g) * VEC + e; missing ones are 0.
 // STREAM rows are read once (non-temporal); parameter vectors shared by
@@ -149,13 +168,19 @@ __device__ __forceinline__ void style_dots(const StyleArgs& sa, int64_t C, int64
 template <int GROUP>
 __device__ __forceinline__ void style_affine(const StyleArgs& sa, int64_t C, int64_t c, int g,
                                              float* lds, float& gamma, float& beta) {
+  // the bias loads go out with the dot products' loads, not after the
+  // block-wide sums (whose barriers keep the compiler from moving them up)
+  float bg = 0.0f, bb = 0.0f;
+  if (sa.bias) {
+    bg = sa.bias[c];
+    bb = sa.bias[C + c];
+  }
   float ag, ab;
   style_dots<GROUP>(sa, C, c, g, ag, ab);
-  ag = group_sum<GROUP>(ag, lds);
-  ab = group_sum<GROUP>(ab, lds);
+  group_sum_pair<GROUP>(ag, ab, lds);
   if (sa.bias) {
-    ag = ag + sa.bias[c];
-    ab = ab + sa.bias[C + c];
+    ag = ag + bg;
+    ab = ab + bb;
   }
   gamma = ag;
   beta = ab;
@@ -220,7 +245,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
                                                              int64_t rows, int64_t C, int64_t T,
                                                              float eps, Affine af,
                                                              StyleArgs sa) {
-  __shared__ float lds[4];
+  __shared__ float lds[8];
   const int RPB = blockDim.x / GROUP;  // 256 / GROUP, or 1 in 64-thread blocks
   const int g = threadIdx.x % GROUP;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / GROUP;
@@ -271,25 +296,57 @@ __device__ __forceinline__ float wide_sum(float v, float* lds) {
   return t[0];
 }
 
+template <int NW>
+__device__ __forceinline__ void wide_sum_pair(float& a, float& b, float* lds) {
+  a = wave_sum(a);
+  b = wave_sum(b);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) {
+    lds[w] = a;
+    lds[NW + w] = b;
+  }
+  __syncthreads();
+  float t[NW], u[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    t[i] = lds[i];
+    u[i] = lds[NW + i];
+  }
+#pragma unroll
+  for (int h = NW / 2; h > 0; h /= 2)
+#pragma unroll
+    for (int i = 0; i < h; ++i) {
+      t[i] = t[i] + t[i + h];
+      u[i] = u[i] + u[i + h];
+    }
+  a = t[0];
+  b = u[0];
+}
+
 template <int NW, int NV>
 __global__ void __launch_bounds__(64 * NW) instnorm_wide_kernel(float* __restrict__ out,
                                                                 const float* __restrict__ x,
                                                                 int64_t C, int64_t T, float eps,
                                                                 StyleArgs sa) {
   constexpr int G = 64 * NW;
-  __shared__ float lds[NW];
+  __shared__ float lds[2 * NW];
   const int g = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t c = row % C;
   float r[NV][4];
   load_row<G, NV, 4>(x + row * T, T, g, r);
+  float bg = 0.0f, bb = 0.0f;  // issued before the barriers of the sums
+  if (sa.bias) {
+    bg = sa.bias[c];
+    bb = sa.bias[C + c];
+  }
   float ag, ab;
   style_dots<G>(sa, C, c, g, ag, ab);
-  ag = wide_sum<NW>(ag, lds);
-  ab = wide_sum<NW>(ab, lds);
+  wide_sum_pair<NW>(ag, ab, lds);
   if (sa.bias) {
-    ag = ag + sa.bias[c];
-    ab = ab + sa.bias[C + c];
+    ag = ag + bg;
+    ab = ab + bb;
   }
   Affine af{};
   af.mode = 2;
@@ -324,7 +381,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_long_kernel(float* __restr
                                                                   const float* __restrict__ x,
                                                                   int64_t C, int64_t T, float eps,
                                                                   Affine af, StyleArgs sa) {
-  __shared__ float lds[4];
+  __shared__ float lds[8];
   const int g = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int64_t c = row % C;
@@ -517,21 +574,23 @@ __global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict_
         for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] + k[j][e];
     }
   }
+  // scale and bias are loaded before the statistics, so their latency
+  // overlaps the row's instead of following the reductions
+  float sc[NV][VEC], bi[NV][VEC];
+  load_row<GROUP, NV, VEC, false>(la.scale, cols, g, sc);
+  if (la.bias) load_row<GROUP, NV, VEC, false>(la.bias, cols, g, bi);
   float mean, var;
   row_stats<GROUP, NV, VEC>(r, cols, g, lds, mean, var);
   const float den = sqrtf(var + eps);
-  float sc[NV][VEC];
-  load_row<GROUP, NV, VEC, false>(la.scale, cols, g, sc);
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) r[j][e] = (r[j][e] / den) * sc[j][e];
   if (la.bias) {
-    load_row<GROUP, NV, VEC, false>(la.bias, cols, g, sc);
 #pragma unroll
     for (int j = 0; j < NV; ++j)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] + sc[j][e];
+      for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] + bi[j][e];
   }
   store_row<GROUP, NV, VEC>(out + row * cols, cols, g, r);
 }
