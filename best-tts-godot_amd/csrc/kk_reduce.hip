@@ -422,6 +422,26 @@ __device__ __forceinline__ float np_fold(float* part, int nblk) {
   return acc;
 }
 
+// A row of T elements of a flat [rows, T] tensor, cut where the flat index
+// row * T + i is a multiple of 4: hh head elements, nv groups of four from
+// i = hh (there a float row takes 16-byte and a byte row 4-byte accesses,
+// given bases so aligned), and the tail from hh + 4 nv.  edge() gives the
+// head and tail elements, at most three each, to threads 0-7 of the row's
+// first block.
+struct RowSplit {
+  int64_t hh, nv, T;
+  __device__ __forceinline__ bool edge(int64_t& i) const {
+    if (blockIdx.x != 0 || threadIdx.x >= 8) return false;
+    const int t = static_cast<int>(threadIdx.x);
+    i = t < 4 ? t : hh + 4 * nv + (t - 4);
+    return t < 4 ? i < hh : i < T;
+  }
+};
+__device__ __forceinline__ RowSplit row_split(int64_t row, int64_t T) {
+  const int64_t hh = std::min<int64_t>(T, (4 - (row * T) % 4) % 4);
+  return RowSplit{hh, (T - hh) / 4, T};
+}
+
 // Applies y = affine((x - mean) / den) with per-row (mean, den) =
 // stats[row] from the numpy-order statistics passes below (long rows).
 __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ out,
@@ -440,16 +460,20 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (vec) {
-    for (int64_t i = 4 * i0; i < T; i += stride * 4) {
+    const RowSplit rsp = row_split(row, T);
+    for (int64_t k = i0; k < rsp.nv; k += stride) {
+      const int64_t i = rsp.hh + 4 * k;
       const float4 v = ld_stream4(xr + i);
       st_stream4(orow + i, make_float4(apply_affine((v.x - st.x) / st.y, ra, af),
                                        apply_affine((v.y - st.x) / st.y, ra, af),
                                        apply_affine((v.z - st.x) / st.y, ra, af),
                                        apply_affine((v.w - st.x) / st.y, ra, af)));
     }
+    int64_t i;
+    if (rsp.edge(i))
+      st_stream(orow + i, apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af));
   } else {
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < T;
-         i += stride)
+    for (int64_t i = i0; i < T; i += stride)
       st_stream(orow + i, apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af));
   }
 }
@@ -461,6 +485,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict_
                                                              const float* __restrict__ x,
                                                              const float2* __restrict__ stats,
                                                              int64_t C, int64_t T, Affine af,
+                                                             int vec,
                                                              const int* __restrict__ only_if) {
   if (only_if && *only_if == 0) return;
   __shared__ float2 wmm[kRowBlock / 64];
@@ -470,11 +495,26 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict_
   const float2 st = stats[row];
   const float* xr = x + row * T;
   float lo = INFINITY, hi = -INFINITY;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < T;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const float y = apply_affine((xr[i] - st.x) / st.y, ra, af);
+  auto take = [&](float v) {
+    const float y = apply_affine((v - st.x) / st.y, ra, af);
     lo = fminf(lo, y);
     hi = fmaxf(hi, y);
+  };
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (vec) {
+    const RowSplit rsp = row_split(row, T);
+    for (int64_t k = i0; k < rsp.nv; k += stride) {
+      const float4 v = *reinterpret_cast<const float4*>(xr + rsp.hh + 4 * k);  // read again next
+      take(v.x);
+      take(v.y);
+      take(v.z);
+      take(v.w);
+    }
+    int64_t i;
+    if (rsp.edge(i)) take(xr[i]);
+  } else {
+    for (int64_t i = i0; i < T; i += stride) take(xr[i]);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
@@ -515,7 +555,9 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
   const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   bool out = false;
   if (vec) {
-    for (int64_t i = 4 * i0; i < T; i += stride * 4) {
+    const RowSplit rsp = row_split(row, T);
+    for (int64_t k = i0; k < rsp.nv; k += stride) {
+      const int64_t i = rsp.hh + 4 * k;
       const float4 v = ld_stream4(xr + i);
       const float y0 = apply_affine((v.x - st.x) / st.y, ra, af);
       const float y1 = apply_affine((v.y - st.x) / st.y, ra, af);
@@ -524,7 +566,15 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
       out |= fminf(fminf(y0, y1), fminf(y2, y3)) < lim.x || fmaxf(fmaxf(y0, y1), fmaxf(y2, y3)) > lim.y;
       const uint32_t w = dql_byte(y0, pz.x, pz.y) | (dql_byte(y1, pz.x, pz.y) << 8) |
                          (dql_byte(y2, pz.x, pz.y) << 16) | (dql_byte(y3, pz.x, pz.y) << 24);
-      __builtin_nontemporal_store(w, reinterpret_cast<uint32_t*>(qr + i));
+      // an ordinary store: the convolution that reads the bytes next finds
+      // them in the last-level cache
+      *reinterpret_cast<uint32_t*>(qr + i) = w;
+    }
+    int64_t i;
+    if (rsp.edge(i)) {
+      const float y = apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af);
+      out |= y < lim.x || y > lim.y;
+      qr[i] = static_cast<uint8_t>(dql_byte(y, pz.x, pz.y));
     }
   } else {
     for (int64_t i = i0; i < T; i += stride) {
@@ -1000,7 +1050,8 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
   if (m == kNpBlock) {
     // A whole block straight from memory into the summation order: lane j
     // of leaf q (eight lanes per 128-element leaf) holds elements
-    // q*128 + 8k + j, k = 0..15, its accumulator's terms in order.
+    // q*128 + 8k + j, k = 0..15, its accumulator's terms in order.  (Staging
+    // the block through LDS with 16-byte loads measured slower.)
     const int q = threadIdx.x >> 3, j = threadIdx.x & 7;
     float v[kNpLeaf / 8];
 #pragma unroll
@@ -1339,12 +1390,14 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
     rc = check_launch("np_blocks_kernel");
   }
   if (rc == KK_OK) {
-    const int64_t per_block = kRowBlock * (vec_ok ? 4 : 1) * 8;
+    // any row length vectorises once both bases are 16-byte aligned
+    const bool avec = aligned16(x->data) && aligned16(out->data);
+    const int64_t per_block = kRowBlock * (avec ? 4 : 1) * 8;
     const unsigned gx = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(
         ceil_div(T, per_block), 1 << 16)));
     hipLaunchKernelGGL(instnorm_apply, dim3(gx, static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
                        st, static_cast<float*>(out->data), xp, static_cast<const float2*>(stats), C,
-                       T, af, vec_ok ? 1 : 0);
+                       T, af, avec ? 1 : 0);
     rc = check_launch("instnorm_apply");
   }
   kk_free(ws);  // stream order keeps it alive for the kernels above
@@ -1371,8 +1424,10 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   const int64_t C = x->shape[x->rank - 2];
   const int64_t rows = numel(x) / T;
   const float* xp = static_cast<const float*>(x->data);
-  const bool vec = (T % 4 == 0) && aligned16(x->data) &&
-                   (reinterpret_cast<uintptr_t>(q->data) % 4 == 0);
+  // the quantising pass vectorises any row length once the bases are
+  // aligned; the rows held in LDS take 16-byte loads only when T % 4 == 0
+  const bool vec = aligned16(x->data) && (reinterpret_cast<uintptr_t>(q->data) % 4 == 0);
+  const bool rows_vec = vec && T % 4 == 0;
   const int64_t per_block = kRowBlock * (vec ? 4 : 1) * 8;
   const int64_t gx = std::max<int64_t>(1, std::min<int64_t>(ceil_div(T, per_block), 1 << 16));
   const bool long_rows = T > kNpRowMax;
@@ -1399,8 +1454,13 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   float* ysp = static_cast<float*>(y_scale->data);
   uint8_t* yzp = static_cast<uint8_t*>(y_zp->data);
   const dim3 qgrid(static_cast<unsigned>(gx), static_cast<unsigned>(rows));
+  // the fallback launches (rarely flagged) take about 2048 blocks, so that
+  // an unflagged one ends at once; their loops stride over the rows
+  const int64_t fgx = std::min<int64_t>(gx, std::max<int64_t>(1, ceil_div(2048, rows)));
+  const dim3 fgrid(static_cast<unsigned>(fgx), static_cast<unsigned>(rows));
   auto quant = [&](const int* only_if, int* check) {
-    hipLaunchKernelGGL(instnorm_quant, qgrid, dim3(kRowBlock), 0, st, static_cast<uint8_t*>(q->data),
+    hipLaunchKernelGGL(instnorm_quant, only_if ? fgrid : qgrid, dim3(kRowBlock), 0, st,
+                       static_cast<uint8_t*>(q->data),
                        xp, static_cast<const float2*>(stats), static_cast<const float2*>(params), C, T,
                        af, vec ? 1 : 0, only_if, check);
     return check_launch("instnorm_quant");
@@ -1409,7 +1469,7 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   if (!long_rows) {
     hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(T), st, static_cast<float*>(nullptr), xp, C, static_cast<int>(T), 3,
-                       eps, af, vec ? 1 : 0, stats, mm);
+                       eps, af, rows_vec ? 1 : 0, stats, mm);
     rc = check_launch("np_rows_kernel");
   } else {
     const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
@@ -1424,11 +1484,12 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   if (rc == KK_OK) rc = launch_dql_fold(mm, static_cast<int>(rows), params, ysp, yzp, nullptr, flag);
   if (rc == KK_OK) rc = quant(nullptr, flag);
   if (rc == KK_OK && flag) {  // only if a y fell outside the bounds
-    hipLaunchKernelGGL(instnorm_minmax, qgrid, dim3(kRowBlock), 0, st, mm, xp,
-                       static_cast<const float2*>(stats), C, T, af, static_cast<const int*>(flag));
+    hipLaunchKernelGGL(instnorm_minmax, fgrid, dim3(kRowBlock), 0, st, mm, xp,
+                       static_cast<const float2*>(stats), C, T, af, vec ? 1 : 0,
+                       static_cast<const int*>(flag));
     rc = check_launch("instnorm_minmax");
     if (rc == KK_OK)
-      rc = launch_dql_fold(mm, static_cast<int>(rows * gx), params, ysp, yzp, flag, nullptr);
+      rc = launch_dql_fold(mm, static_cast<int>(rows * fgx), params, ysp, yzp, flag, nullptr);
     if (rc == KK_OK) rc = quant(flag, nullptr);
   }
   kk_free(ws);  // stream order keeps it alive for the kernels above

@@ -151,7 +151,11 @@ def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
 
 @pytest.mark.parametrize("C,T,rc_mul,leaky", [(64, 20000, 1.0, None), (64, 20000, 5.0, None),
                                               (32, 24676, None, -0.5), (32, 24676, None, 0.2),
-                                              (48, 3000, 5.0, None)])
+                                              (48, 3000, 5.0, None),
+                                              # odd long rows: rows start at every
+                                              # offset mod 4 (scalar head and tail)
+                                              (24, 20001, 1.0, None), (16, 16386, None, 0.2),
+                                              (24, 20003, 5.0, None)])
 def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leaky):
     """InstanceNormQuant gives the same bytes, scale and zero point as the
     device's own unfused chain: the float result stored, then
@@ -182,7 +186,10 @@ def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leak
 @pytest.mark.parametrize("C,T,kind", [(128, 40000, "affine"), (256, 7180, "leaky"),
                                       (128, 20000, "snake"), (64, 999, "snake"),
                                       (96, 2400, "plain"), (32, 24676, "leaky"),
-                                      (512, 40000, "affine")])
+                                      (512, 40000, "affine"),
+                                      # long rows with T % 4 = 1, 2, 3
+                                      (32, 24677, "snake"), (16, 16386, "affine"),
+                                      (24, 20003, "leaky")])
 def test_instance_norm_quant_chain(gpu, oracle, C, T, kind):
     """The InstanceNorm chain (plain, affine, + LeakyRelu, + snake) -> Cast
     -> DynamicQuantizeLinear: one InstanceNormQuant, its float result never
