@@ -110,7 +110,7 @@ def dispatch(op, node_input, node_output, at, env):
         hostops.run(op, node_input, node_output, at, local)
         env[node_output[0]] = local[node_output[0]]
         return
-    if op in _HOST_MOVE_OPS or op in _HOST_INT_OPS:
+    if (op in _HOST_MOVE_OPS or op in _HOST_INT_OPS) and not (_is_dev(x) or _is_dev(y)):
         present = [inp(i) for i in range(len(node_input)) if inp(i) is not None]
         host = bool(present) and all(not _is_dev(v) for v in present)
         if host and op in _HOST_INT_OPS:

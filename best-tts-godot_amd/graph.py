@@ -131,6 +131,9 @@ class PackedGraph:
                 if name and name not in self.weights:
                     self.last_use[name] = i
         self.last_use.pop(self.output, None)
+        self.frees = [[] for _ in self.nodes]  # names whose last use is node i
+        for name, i in self.last_use.items():
+            self.frees[i].append(name)
 
     def run(self, input_ids, style, speed=1.0, keep=()):
         """Returns the waveform on the host (a numpy array)."""
@@ -139,13 +142,14 @@ class PackedGraph:
         env[self.inputs["style"]] = to_device(np.asarray(style, np.float32).reshape(1, 256))
         env[self.inputs["speed"]] = to_device(np.asarray([speed], np.float32))
         keep = {str(k) for k in keep}
+        frees = self.frees
         for i, (op, ins, outs, at) in enumerate(self.nodes):
             try:
                 dispatch(op, ins, outs, at, env)
             except Exception as exc:
                 raise RuntimeError(f"node {i} {op}: {exc}") from exc
-            for name in ins:
-                if name and self.last_use.get(name) == i and name not in keep:
+            for name in frees[i]:
+                if name not in keep:
                     env.pop(name, None)
         out = env[self.output]
         self.last_env = {k: env[k] for k in keep if k in env}

@@ -8,6 +8,7 @@ the reference's Reshape/Transpose/Squeeze/Unsqueeze/Slice/Split branches do
 (kk_alloc/kk_free) and goes back to it when the last view is dropped.
 """
 import ctypes
+import functools
 import math
 
 import numpy as np
@@ -91,6 +92,7 @@ class Storage:
 _PROTOS = {}  # (shape, strides, dtype) -> KKTensor with data unset
 
 
+@functools.lru_cache(maxsize=4096)
 def _contig_strides(shape):
     st, acc = [], 1
     for d in reversed(shape):
@@ -237,7 +239,7 @@ class DeviceTensor:
         if math.prod(shape) != self.size:
             raise ValueError(f"cannot reshape {self.shape} into {tuple(shape)}")
         src = self if self.is_contiguous() else self.contiguous()
-        return src._view(shape, _contig_strides(shape))
+        return src._view(shape, _contig_strides(tuple(shape)))
 
     def transpose(self, perm=None):
         if perm is None:
