@@ -51,6 +51,23 @@ __global__ void __launch_bounds__(256) dql_minmax(const float* __restrict__ x, i
   }
 }
 
+// Scale and zero point from the (min, max) of x, in double exactly as the
+// reference does; returns (scale, zero point) as floats (x / scale runs in
+// float32 against the scale rounded to float32) and stores the outputs.
+__device__ float2 dql_params(float fmn, float fmx, float* scale_out, uint8_t* zp_out) {
+  const double mn = fmn;
+  const double mx = fmx;
+  const double dlo = mn < 0.0 ? mn : 0.0;
+  const double dhi = mx > 0.0 ? mx : 0.0;
+  double scale = (dhi - dlo) / 255.0;
+  if (scale == 0.0) scale = 1.0;
+  double zp = rint(0.0 - dlo / scale);
+  zp = zp < 0.0 ? 0.0 : (zp > 255.0 ? 255.0 : zp);
+  *scale_out = static_cast<float>(scale);
+  *zp_out = static_cast<uint8_t>(zp);
+  return make_float2(static_cast<float>(scale), static_cast<float>(zp));
+}
+
 // One block folds the partials and derives scale and zero point in double
 // exactly as the reference does; params = (scale, zero point) as floats.
 constexpr int kDqlFoldThreads = 1024;
@@ -85,18 +102,7 @@ __global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __rest
       fmn = fminf(fmn, smin[k]);
       fmx = fmaxf(fmx, smax[k]);
     }
-    const double mn = fmn;
-    const double mx = fmx;
-    const double dlo = mn < 0.0 ? mn : 0.0;
-    const double dhi = mx > 0.0 ? mx : 0.0;
-    double scale = (dhi - dlo) / 255.0;
-    if (scale == 0.0) scale = 1.0;
-    double zp = rint(0.0 - dlo / scale);
-    zp = zp < 0.0 ? 0.0 : (zp > 255.0 ? 255.0 : zp);
-    // x / scale runs in float32 against the scale rounded to float32
-    params[0] = make_float2(static_cast<float>(scale), static_cast<float>(zp));
-    *scale_out = static_cast<float>(scale);
-    *zp_out = static_cast<uint8_t>(zp);
+    params[0] = dql_params(fmn, fmx, scale_out, zp_out);
     if (clear) {
       params[1] = make_float2(fmn, fmx);
       *clear = 0;
@@ -131,6 +137,60 @@ __global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x,
     head = 4 * n4;
   }
   for (int64_t i = head + tid; i < n; i += nthreads) y[i] = static_cast<uint8_t>(dql_byte(x[i], sc, z));
+}
+
+// Inputs up to kDqlSmall elements: one block of 1024 threads takes the
+// (min, max), the scale and zero point and the bytes in one launch (the
+// same values as the three-kernel path: min and max do not depend on the
+// order, and the parameters come from dql_params).  Saves two launches and
+// the partials' allocation for the many small activations of the text
+// encoder and the predictors.
+constexpr int64_t kDqlSmall = 131072;
+constexpr int kDqlSmallThreads = 1024;
+
+__global__ void __launch_bounds__(kDqlSmallThreads) dql_small(const float* __restrict__ x, int64_t n,
+                                                              float* __restrict__ scale_out,
+                                                              uint8_t* __restrict__ zp_out,
+                                                              uint8_t* __restrict__ y, int vec) {
+  __shared__ float smin[kDqlSmallThreads / 64], smax[kDqlSmallThreads / 64];
+  __shared__ float2 pz;
+  const int tid = threadIdx.x;
+  const int64_t n4 = vec ? n / 4 : 0;
+  float lo = INFINITY, hi = -INFINITY;
+  for (int64_t i = tid; i < n4; i += kDqlSmallThreads) {
+    const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);  // read again below
+    lo = fminf(lo, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
+    hi = fmaxf(hi, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+  }
+  for (int64_t i = 4 * n4 + tid; i < n; i += kDqlSmallThreads) {
+    lo = fminf(lo, x[i]);
+    hi = fmaxf(hi, x[i]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+  }
+  const int lane = tid & 63, w = tid >> 6;
+  if (lane == 0) { smin[w] = lo; smax[w] = hi; }
+  __syncthreads();
+  if (tid == 0) {
+    float fmn = smin[0], fmx = smax[0];
+    for (int k = 1; k < kDqlSmallThreads / 64; ++k) {
+      fmn = fminf(fmn, smin[k]);
+      fmx = fmaxf(fmx, smax[k]);
+    }
+    pz = dql_params(fmn, fmx, scale_out, zp_out);
+  }
+  __syncthreads();
+  const float sc = pz.x, z = pz.y;
+  for (int64_t i = tid; i < n4; i += kDqlSmallThreads) {
+    const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);
+    reinterpret_cast<uint32_t*>(y)[i] = dql_byte(v.x, sc, z) | (dql_byte(v.y, sc, z) << 8) |
+                                        (dql_byte(v.z, sc, z) << 16) | (dql_byte(v.w, sc, z) << 24);
+  }
+  for (int64_t i = 4 * n4 + tid; i < n; i += kDqlSmallThreads)
+    y[i] = static_cast<uint8_t>(dql_byte(x[i], sc, z));
 }
 
 // ------------------------------------------------------------------- LSTM
@@ -625,6 +685,12 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
   const int nblk = static_cast<int>(std::min<int64_t>(kDqlBlocks, ceil_div(n, 1024)));
   const int vec = (reinterpret_cast<uintptr_t>(x->data) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(y->data) % 4 == 0) ? 1 : 0;
+  if (n <= kDqlSmall) {
+    hipLaunchKernelGGL(dql_small, dim3(1), dim3(kDqlSmallThreads), 0, ctx().stream,
+                       static_cast<const float*>(x->data), n, static_cast<float*>(scale->data),
+                       static_cast<uint8_t*>(zp->data), static_cast<uint8_t*>(y->data), vec);
+    return check_launch("dql_small");
+  }
   void* part = nullptr;
   KK_TRY(kk_alloc(sizeof(float2) * (nblk + 1), &part));
   float2* pp = static_cast<float2*>(part);

@@ -45,14 +45,19 @@ def onode(oracle, op, inputs, attrs=None, nout=1):
     return res[0] if nout == 1 else res
 
 
-@pytest.mark.parametrize("case", ["normal", "positive", "negative", "zeros", "big"])
+@pytest.mark.parametrize("case", ["normal", "positive", "negative", "zeros", "big", "odd_small",
+                                  "just_over"])
 def test_dynamic_quantize_linear(gpu, oracle, case):
+    """Inputs up to 131072 elements take the one-block kernel, larger ones
+    the three-kernel path; both against the oracle, bit for bit."""
     r = rng(1)
     x = {"normal": r.normal(0, 1, (1, 130, 768)),
          "positive": r.uniform(0.5, 3, (4, 1000)),
          "negative": -r.uniform(0.5, 3, (4, 1000)),
          "zeros": np.zeros((3, 7)),
-         "big": r.normal(0, 50, (1, 512, 2400))}[case].astype(np.float32)
+         "big": r.normal(0, 50, (1, 512, 2400)),
+         "odd_small": r.normal(0.3, 2, (1, 3, 43689)),
+         "just_over": r.normal(-0.2, 1, (2, 65537))}[case].astype(np.float32)
     y, s, z = node(gpu, "DynamicQuantizeLinear", [x], nout=3)
     yo, so, zo = onode(oracle, "DynamicQuantizeLinear", [x], nout=3)
     assert_bitexact(np.asarray(s, np.float32).reshape(()), np.asarray(so, np.float32), "scale")
