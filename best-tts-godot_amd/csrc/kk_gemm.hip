@@ -393,7 +393,27 @@ struct GemmArgs {
   // and gemm_splitk_reduce forms out
   int splits;
   float* part;
+  // MatMulInteger's Cast -> Mul(scale) (-> Add(bias)) tail, fused: with cs
+  // set, out is fp32 = float(int32 result) * cs[n] (+ cb[n]), two roundings
+  // as the chain computes them; cs_n / cb_n are 1 (one value) or N
+  const float* cs;
+  int64_t cs_n;
+  const float* cb;
+  int64_t cb_n;
 };
+
+// The int32 result of MatMulInteger, or with the fused tail its scaled fp32.
+__device__ __forceinline__ void store_int_result(const GemmArgs& G, float* out, int64_t o, int64_t n,
+                                                 float v) {
+  const int32_t iv = __float2int_rn(v);
+  if (G.cs) {
+    float y = static_cast<float>(iv) * G.cs[G.cs_n > 1 ? n : 0];
+    if (G.cb) y = y + G.cb[G.cb_n > 1 ? n : 0];
+    out[o] = y;
+  } else {
+    reinterpret_cast<int32_t*>(out)[o] = iv;
+  }
+}
 
 // A kinds: 0 = K-contiguous quads of TA, 1 = scalar gather.
 // B kinds: 0 = N-contiguous quads of TB, 1 = scalar gather.
@@ -415,7 +435,7 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
   float* part = splits > 1 ? G.part + ((bz * splits + split) * M) * N : nullptr;
   auto store = [&](int64_t m, int64_t n, float v) {
     if (part) part[m * N + n] = v;
-    else if (out_i32) reinterpret_cast<int32_t*>(out)[m * som + n * son] = __float2int_rn(v);
+    else if (out_i32) store_int_result(G, out, m * som + n * son, n, v);
     else out[m * som + n * son] = alpha == 1.0f ? v : v * alpha;
   };
   // this split's K-steps
@@ -538,7 +558,7 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs G, int64_t ba
     float v = p[0];
     for (int s = 1; s < S; ++s) v = v + p[s * MN];
     const int64_t o = batch_offset(G.bm, 2, bz) + m * G.som + n * G.son;
-    if (G.out_i32) reinterpret_cast<int32_t*>(G.out)[o] = __float2int_rn(v);
+    if (G.out_i32) store_int_result(G, G.out, o, n, v);
     else G.out[o] = G.alpha == 1.0f ? v : v * G.alpha;
   }
 }
@@ -1001,6 +1021,39 @@ int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor*
   G.out_i32 = 1;
   if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
   if (G.K == 0) return kk_fill(out, 0.0);
+  return launch_gemm(G, batch);
+}
+
+int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
+                             const kk_tensor* a_zp, const kk_tensor* b_zp, const kk_tensor* scale,
+                             const kk_tensor* bias) {
+  GemmArgs G{};
+  int64_t batch = 0;
+  KK_TRY(setup_gemm(&G, out, a, b, &batch, "kk_matmul_integer_scaled"));
+  if (!(a->dtype == KK_U8 || a->dtype == KK_I8) || !(b->dtype == KK_U8 || b->dtype == KK_I8))
+    return set_error(KK_E_ARG, "kk_matmul_integer_scaled: a and b must be uint8/int8");
+  if (out->dtype != KK_F32) return set_error(KK_E_ARG, "kk_matmul_integer_scaled: out must be fp32");
+  KK_TRY(zp_shift(&G.adq, a_zp, 1, "kk_matmul_integer_scaled"));
+  KK_TRY(zp_shift(&G.dq, b_zp, G.N, "kk_matmul_integer_scaled"));
+  // scale and bias: one value or one per output column, contiguous fp32
+  auto per_col = [&](const kk_tensor* t, const char* what, const float** p, int64_t* n) -> int {
+    KK_TRY(check_tensor(t, what));
+    if (t->dtype != KK_F32 || !is_contiguous(t))
+      return set_error(KK_E_ARG, "kk_matmul_integer_scaled: %s must be contiguous fp32", what);
+    const int64_t c = numel(t);
+    if (c != 1 && !(c == G.N && t->rank >= 1 && t->shape[t->rank - 1] == G.N))
+      return set_error(KK_E_ARG, "kk_matmul_integer_scaled: %s must hold 1 or N = %lld values", what,
+                       (long long)G.N);
+    *p = static_cast<const float*>(t->data);
+    *n = c;
+    return KK_OK;
+  };
+  if (!scale) return set_error(KK_E_ARG, "kk_matmul_integer_scaled: scale is required");
+  KK_TRY(per_col(scale, "scale", &G.cs, &G.cs_n));
+  if (bias) KK_TRY(per_col(bias, "bias", &G.cb, &G.cb_n));
+  G.out_i32 = 1;
+  if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
+  if (G.K == 0) return set_error(KK_E_UNSUPPORTED, "kk_matmul_integer_scaled: K = 0");
   return launch_gemm(G, batch);
 }
 

@@ -342,6 +342,26 @@ def dispatch(op, node_input, node_output, at, env):
                                       _f32(to_device(inp(5))), at.get("pads", [0, 0]),
                                       at.get("strides", [1])[0], at.get("dilations", [1])[0],
                                       at.get("group", 1))
+    elif op == "QMatMulScaled":
+        # MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)), fused;
+        # inputs a, b, a_zp, b_zp, scale, bias ("" if absent).  A scale or
+        # bias that is not one value or one per output column (it would
+        # broadcast the product to another shape) runs the chain node by node.
+        a, b = to_device(x), to_device(y)
+        a_zp, b_zp = to_device(inp(2)), to_device(inp(3))
+        scale, bias = _f32(to_device(inp(4))), _f32(to_device(inp(5)))
+        n, rank = b.shape[-1], max(a.ndim, b.ndim)
+
+        def per_col(t):
+            return t is None or (t.ndim <= rank and t.size in (1, n) and
+                                 (t.size == 1 or t.shape[-1] == n))
+        if a.shape[-1] and per_col(scale) and per_col(bias):
+            out = ops.matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias)
+        else:
+            out = ops.binary("Mul", ops.matmul_integer(a, b, a_zp, b_zp).astype(np.float32),
+                             scale)
+            if bias is not None:
+                out = ops.binary("Add", out, bias)
     elif op == "InstanceNormScaleShift":
         # ReduceMean/Sub/Mul/ReduceMean/Add/Sqrt/Div [-> Mul -> Add -> LeakyRelu], fused;
         # inputs x, scale ("" if absent), shift ("" if absent).

@@ -77,6 +77,8 @@ def fuse(nodes, weights, protect=()):
             continue
         if op == "ConvInteger" and int(at.get("group", 1)) == 1:
             _match_qconv(nodes, i, only_reader, other, claim)
+        elif op == "MatMulInteger":
+            _match_qmatmul(nodes, weights, i, only_reader, other, claim)
         elif op == "ReduceMean":
             _match_instnorm(nodes, weights, i, only_reader, readers, protect, other, claim)
         elif op == "Sin":
@@ -210,6 +212,31 @@ def _match_qconv(nodes, i, only_reader, other, claim):
     conv_ins = list(ins) + [""] * (4 - len(ins))
     fused = ("QConvScaled", conv_ins[:4] + [bias, scale], [nodes[k][2][0]], dict(at))
     claim(chain, fused)
+
+
+def _match_qmatmul(nodes, weights, i, only_reader, other, claim):
+    """MatMulInteger -> Cast(float) -> Mul(scale) -> Add(bias), the Add only
+    when its other operand is a float constant (the Linear's bias)."""
+    op, ins, outs, at = nodes[i]
+    j = only_reader(outs[0], "Cast")
+    if j is None or int(nodes[j][3].get("to", 1)) not in (1, 10):
+        return
+    k = only_reader(nodes[j][2][0], "Mul")
+    if k is None:
+        return
+    scale = other(nodes[k][1], nodes[j][2][0])
+    if scale is None:
+        return
+    chain, bias, out = [i, j, k], "", nodes[k][2][0]
+    a = only_reader(out, "Add")
+    if a is not None:
+        b = other(nodes[a][1], out)
+        w = weights.get(b) if b is not None else None
+        if w is not None and np.dtype(getattr(w, "dtype", np.float64)).kind == "f":
+            chain.append(a)
+            bias, out = b, nodes[a][2][0]
+    mm_ins = list(ins) + [""] * (4 - len(ins))
+    claim(chain, ("QMatMulScaled", mm_ins[:4] + [scale, bias], [out], {}))
 
 
 def _axes_of(nodes, weights, i):

@@ -234,6 +234,16 @@ def matmul_integer(a, b, a_zp=None, b_zp=None):
     return out
 
 
+def matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias=None):
+    """MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)) in one
+    launch; scale and bias hold 1 or N (the output's columns) values."""
+    batch = broadcast_shape(a.shape[:-2], b.shape[:-2])
+    out = DeviceTensor.empty(batch + (a.shape[-2], b.shape[-1]), np.float32)
+    _lib.call("kk_matmul_integer_scaled", out.desc(), a.desc(), b.desc(), _d(a_zp), _d(b_zp),
+              scale.contiguous().desc(), _d(None if bias is None else bias.contiguous()))
+    return out
+
+
 def conv_integer(x, w, x_zp=None, w_zp=None, pads=(0, 0), stride=1, dilation=1, group=1):
     x = x.contiguous()
     w = w.contiguous()

@@ -145,7 +145,8 @@ def _graph_nodes():
 
 
 def test_fusion_pass_on_the_kokoro_graph():
-    """The fusion pass finds every quantised conv tail (87), InstanceNorm
+    """The fusion pass finds every quantised conv tail (87) and quantised
+    Linear tail (148, 136 with their bias), InstanceNorm
     chain (64 of 65: one has a Transpose inside) and snake (48) of the
     packed graph -- 42 norm chains feed a snake alone and merge with it, and
     59 norm chains (snake or not) feed only a Cast -> DynamicQuantizeLinear
@@ -159,6 +160,9 @@ def test_fusion_pass_on_the_kokoro_graph():
     kinds = Counter(n[0] for n in fused)
     assert (kinds["QConvScaled"], kinds["InstanceNormScaleShift"], kinds["Snake"],
             kinds["InstanceNormSnake"], kinds["InstanceNormQuant"]) == (87, 5, 6, 0, 59)
+    assert kinds["QMatMulScaled"] == 148 and kinds["MatMulInteger"] == 0
+    assert sum(1 for n in fused if n[0] == "QMatMulScaled" and n[1][5]) == 136
+    assert len(fused) == 2379
     covered = sorted(i for grp in groups for i in grp)
     assert covered == list(range(len(nodes)))  # every original node exactly once
     produced = {}

@@ -3,8 +3,9 @@ node by node through the oracle, at decoder sizes.
 
 Each case builds the chain as graph nodes, lets the fusion pass rewrite it
 (so the test covers the matcher as well as the kernel) and compares the
-fused launch with the oracle's chain.  Bars: the quantised conv tail
-bit-exact (integer arithmetic, then the chain's own Cast and Mul); the
+fused launch with the oracle's chain.  Bars: the quantised conv and
+Linear tails bit-exact (integer arithmetic, then the chain's own Cast, Mul
+and Add); the
 InstanceNorm chain bit-exact (its sums follow numpy's summation order, the
 rest are correctly rounded IEEE operations); the snake chain at the
 elementwise bar rel 1e-5 (+1e-6 max|ref|: sin differs by ulps between numpy
@@ -64,6 +65,51 @@ def test_qconv_tail(gpu, oracle, cin, cout, k, L, pad, bias):
     got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, "y")
     assert [n[0] for n in fused] == ["QConvScaled"]
     assert_bitexact(got, want.astype(np.float32), f"QConvScaled {cin}->{cout} k{k}")
+
+
+@pytest.mark.parametrize("M,K,N,wdt,per_col,bias", [(130, 768, 768, np.int8, True, True),
+                                                    (130, 2048, 768, np.uint8, False, True),
+                                                    (37, 100, 9, np.int8, True, False),
+                                                    (256, 768, 2048, np.uint8, True, True)])
+def test_qmatmul_tail(gpu, oracle, M, K, N, wdt, per_col, bias):
+    """MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)), the
+    quantised Linear of the text encoder and predictors, as one launch: the
+    same bits as the chain (exact integer sums, then the chain's Mul and
+    Add, each rounded once)."""
+    r = rng(27)
+    a = r.integers(0, 256, (1, M, K)).astype(np.uint8)
+    w = (r.integers(-128, 128, (K, N)) if wdt == np.int8 else r.integers(0, 256, (K, N))).astype(wdt)
+    s = (r.uniform(1e-4, 1e-3, (N,)) if per_col else np.array(3.7e-4)).astype(np.float32)
+    inputs = {"a": a, "az": np.array(121, np.uint8), "s": s}
+    weights = {"w": w, "wz": np.array(0 if wdt == np.int8 else 131, wdt),
+               "b": r.normal(0, 1, (N,)).astype(np.float32)}
+    nodes = [("MatMulInteger", ["a", "w", "az", "wz"], ["acc"], {}),
+             ("Cast", ["acc"], ["f"], {"to": 1}), ("Mul", ["f", "s"], ["y"], {})]
+    last = "y"
+    if bias:
+        nodes.append(("Add", ["y", "b"], ["z"], {}))
+        last = "z"
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, last)
+    assert [n[0] for n in fused] == ["QMatMulScaled"]
+    assert_bitexact(got, want.astype(np.float32), f"QMatMulScaled {M}x{K}x{N}")
+
+
+def test_qmatmul_tail_row_scale_runs_the_chain(gpu, oracle):
+    """A scale that is not one value or one per column (here one per row)
+    would change the product's shape handling: the fused node then runs the
+    chain node by node, with the same result as the oracle."""
+    r = rng(28)
+    a = r.integers(0, 256, (1, 40, 64)).astype(np.uint8)
+    inputs = {"a": a, "az": np.array(100, np.uint8),
+              "s": r.uniform(1e-4, 1e-3, (40, 1)).astype(np.float32)}
+    weights = {"w": r.integers(-128, 128, (64, 24)).astype(np.int8), "wz": np.array(0, np.int8),
+               "b": r.normal(0, 1, (24,)).astype(np.float32)}
+    nodes = [("MatMulInteger", ["a", "w", "az", "wz"], ["acc"], {}),
+             ("Cast", ["acc"], ["f"], {"to": 1}), ("Mul", ["f", "s"], ["y"], {}),
+             ("Add", ["y", "b"], ["z"], {})]
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, "z")
+    assert [n[0] for n in fused] == ["QMatMulScaled"]
+    assert_bitexact(got, want.astype(np.float32), "QMatMulScaled, per-row scale")
 
 
 def norm_chain(affine, leaky):
