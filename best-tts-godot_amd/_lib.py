@@ -84,7 +84,7 @@ PROTOTYPES = {
     "kk_event_elapsed": [_i, _i, ctypes.POINTER(_f)],
     "kk_dynamic_quantize_linear": [_T, _T, _T, _T],
     "kk_matmul_integer": [_T, _T, _T, _T, _T],
-    "kk_matmul_integer_scaled": [_T, _T, _T, _T, _T, _T, _T],
+    "kk_matmul_integer_scaled": [_T, _T, _T, _T, _T, _T, _T, _T],
     "kk_conv_integer": [_T, _T, _T, _T, _T, _i, _i, _i, _i, _i],
     "kk_conv_integer_scaled": [_T] * 7 + [_i, _i, _i, _i, _i],
     "kk_instance_norm_scale_shift": [_T, _T, _T, _T, _f, _i, _f],

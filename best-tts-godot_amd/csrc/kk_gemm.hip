@@ -398,6 +398,8 @@ struct GemmArgs {
   // as the chain computes them; cs_n / cb_n are 1 (one value) or N
   const float* cs;
   int64_t cs_n;
+  const float* cs2;  // optional second factor: the scale is cs[n] * cs2[n], rounded once
+  int64_t cs2_n;
   const float* cb;
   int64_t cb_n;
 };
@@ -407,7 +409,9 @@ __device__ __forceinline__ void store_int_result(const GemmArgs& G, float* out, 
                                                  float v) {
   const int32_t iv = __float2int_rn(v);
   if (G.cs) {
-    float y = static_cast<float>(iv) * G.cs[G.cs_n > 1 ? n : 0];
+    float sc = G.cs[G.cs_n > 1 ? n : 0];
+    if (G.cs2) sc = sc * G.cs2[G.cs2_n > 1 ? n : 0];
+    float y = static_cast<float>(iv) * sc;
     if (G.cb) y = y + G.cb[G.cb_n > 1 ? n : 0];
     out[o] = y;
   } else {
@@ -1026,7 +1030,7 @@ int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor*
 
 int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
                              const kk_tensor* a_zp, const kk_tensor* b_zp, const kk_tensor* scale,
-                             const kk_tensor* bias) {
+                             const kk_tensor* scale2, const kk_tensor* bias) {
   GemmArgs G{};
   int64_t batch = 0;
   KK_TRY(setup_gemm(&G, out, a, b, &batch, "kk_matmul_integer_scaled"));
@@ -1050,6 +1054,7 @@ int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_
   };
   if (!scale) return set_error(KK_E_ARG, "kk_matmul_integer_scaled: scale is required");
   KK_TRY(per_col(scale, "scale", &G.cs, &G.cs_n));
+  if (scale2) KK_TRY(per_col(scale2, "scale2", &G.cs2, &G.cs2_n));
   if (bias) KK_TRY(per_col(bias, "bias", &G.cb, &G.cb_n));
   G.out_i32 = 1;
   if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;

@@ -344,20 +344,31 @@ def dispatch(op, node_input, node_output, at, env):
                                       at.get("group", 1))
     elif op == "QMatMulScaled":
         # MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)), fused;
-        # inputs a, b, a_zp, b_zp, scale, bias ("" if absent).  A scale or
-        # bias that is not one value or one per output column (it would
-        # broadcast the product to another shape) runs the chain node by node.
+        # inputs a, b, a_zp, b_zp, scale, bias ("" if absent), and with
+        # scale_product the scale's two factors (the Mul that formed it) as
+        # inputs 6 and 7.  A scale or bias that is not one value or one per
+        # output column (it would broadcast the product to another shape)
+        # runs the chain node by node.
         a, b = to_device(x), to_device(y)
         a_zp, b_zp = to_device(inp(2)), to_device(inp(3))
-        scale, bias = _f32(to_device(inp(4))), _f32(to_device(inp(5)))
+        bias = _f32(to_device(inp(5)))
         n, rank = b.shape[-1], max(a.ndim, b.ndim)
 
         def per_col(t):
             return t is None or (t.ndim <= rank and t.size in (1, n) and
                                  (t.size == 1 or t.shape[-1] == n))
-        if a.shape[-1] and per_col(scale) and per_col(bias):
-            out = ops.matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias)
+        scale2 = None
+        if at.get("scale_product"):
+            scale, scale2 = _f32(to_device(inp(6))), _f32(to_device(inp(7)))
+            if not (per_col(scale) and per_col(scale2)):
+                scale, scale2 = ops.binary("Mul", scale, scale2), None
         else:
+            scale = _f32(to_device(inp(4)))
+        if a.shape[-1] and per_col(scale) and per_col(bias):
+            out = ops.matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias, scale2)
+        else:
+            if scale2 is not None:
+                scale = ops.binary("Mul", scale, scale2)
             out = ops.binary("Mul", ops.matmul_integer(a, b, a_zp, b_zp).astype(np.float32),
                              scale)
             if bias is not None:

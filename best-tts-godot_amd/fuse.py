@@ -62,6 +62,7 @@ def fuse(nodes, weights, protect=()):
         a = [n for n in ins if n != name]
         return a[0] if len(a) == 1 else None
 
+    producer = {o: i for i, (_op, _ins, outs, _at) in enumerate(nodes) for o in outs if o}
     used = set()
     replace = {}  # index of the chain's last node -> (fused node, chain indices)
 
@@ -78,7 +79,7 @@ def fuse(nodes, weights, protect=()):
         if op == "ConvInteger" and int(at.get("group", 1)) == 1:
             _match_qconv(nodes, i, only_reader, other, claim)
         elif op == "MatMulInteger":
-            _match_qmatmul(nodes, weights, i, only_reader, other, claim)
+            _match_qmatmul(nodes, weights, producer, i, only_reader, other, claim)
         elif op == "ReduceMean":
             _match_instnorm(nodes, weights, i, only_reader, readers, protect, other, claim)
         elif op == "Sin":
@@ -214,7 +215,7 @@ def _match_qconv(nodes, i, only_reader, other, claim):
     claim(chain, fused)
 
 
-def _match_qmatmul(nodes, weights, i, only_reader, other, claim):
+def _match_qmatmul(nodes, weights, producer, i, only_reader, other, claim):
     """MatMulInteger -> Cast(float) -> Mul(scale) -> Add(bias), the Add only
     when its other operand is a float constant (the Linear's bias)."""
     op, ins, outs, at = nodes[i]
@@ -236,7 +237,16 @@ def _match_qmatmul(nodes, weights, i, only_reader, other, claim):
             chain.append(a)
             bias, out = b, nodes[a][2][0]
     mm_ins = list(ins) + [""] * (4 - len(ins))
-    claim(chain, ("QMatMulScaled", mm_ins[:4] + [scale, bias], [out], {}))
+    fused_ins, attrs = mm_ins[:4] + [scale, bias], {}
+    # the scale formed by a Mul that only this chain reads: its two factors
+    # go in instead (the epilogue forms the product, rounded once)
+    m = producer.get(scale)
+    if m is not None and nodes[m][0] == "Mul" and only_reader(scale) == k and \
+            all(f for f in nodes[m][1]) and len(nodes[m][1]) == 2:
+        chain.append(m)
+        fused_ins = mm_ins[:4] + ["", bias] + list(nodes[m][1])
+        attrs = {"scale_product": 1}
+    claim(sorted(chain), ("QMatMulScaled", fused_ins, [out], attrs))
 
 
 def _axes_of(nodes, weights, i):

@@ -234,13 +234,16 @@ def matmul_integer(a, b, a_zp=None, b_zp=None):
     return out
 
 
-def matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias=None):
+def matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias=None, scale2=None):
     """MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)) in one
-    launch; scale and bias hold 1 or N (the output's columns) values."""
+    launch, the scale optionally the product scale * scale2 (rounded once,
+    as a Mul node forms it); each holds 1 or N (the output's columns)
+    values."""
     batch = broadcast_shape(a.shape[:-2], b.shape[:-2])
     out = DeviceTensor.empty(batch + (a.shape[-2], b.shape[-1]), np.float32)
     _lib.call("kk_matmul_integer_scaled", out.desc(), a.desc(), b.desc(), _d(a_zp), _d(b_zp),
-              scale.contiguous().desc(), _d(None if bias is None else bias.contiguous()))
+              scale.contiguous().desc(), _d(None if scale2 is None else scale2.contiguous()),
+              _d(None if bias is None else bias.contiguous()))
     return out
 
 

@@ -242,14 +242,17 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale,
 int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
                       const kk_tensor* a_zp, const kk_tensor* b_zp);
 /* The graph's quantised-linear tail fused into MatMulInteger's epilogue:
- * MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias))
+ * MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)), the scale
+ * itself the Mul of the activation's and the weights' scales
  * (ref_runtime.py:119-127, 572-578, 446-451): out fp32 [.., M, N] =
- * float(int32 result) * scale[n] (+ bias[n]), the Mul and Add rounded
- * separately as the chain does; scale and bias contiguous fp32 holding 1 or
- * N values (bias may be NULL); K >= 1. */
+ * float(int32 result) * (scale[n] * scale2[n]) (+ bias[n]), each Mul and
+ * the Add rounded separately as the chain does; scale, scale2 and bias
+ * contiguous fp32 holding 1 or N values (scale2 and bias may be NULL);
+ * K >= 1. */
 int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
                              const kk_tensor* a_zp, const kk_tensor* b_zp,
-                             const kk_tensor* scale, const kk_tensor* bias);
+                             const kk_tensor* scale, const kk_tensor* scale2,
+                             const kk_tensor* bias);
 /* ConvInteger (ref_runtime.py:130-134): int32 conv of (x - x_zp) with
  * (w - w_zp); x uint8 [N, Cin, L], w uint8/int8 [Cout, Cin, K]; padding
  * reads 0 after the zero-point shift. */

@@ -146,7 +146,8 @@ def _graph_nodes():
 
 def test_fusion_pass_on_the_kokoro_graph():
     """The fusion pass finds every quantised conv tail (87) and quantised
-    Linear tail (148, 136 with their bias), InstanceNorm
+    Linear tail (148, 136 with their bias, each with its scale product),
+    InstanceNorm
     chain (64 of 65: one has a Transpose inside) and snake (48) of the
     packed graph -- 42 norm chains feed a snake alone and merge with it, and
     59 norm chains (snake or not) feed only a Cast -> DynamicQuantizeLinear
@@ -162,7 +163,10 @@ def test_fusion_pass_on_the_kokoro_graph():
             kinds["InstanceNormSnake"], kinds["InstanceNormQuant"]) == (87, 5, 6, 0, 59)
     assert kinds["QMatMulScaled"] == 148 and kinds["MatMulInteger"] == 0
     assert sum(1 for n in fused if n[0] == "QMatMulScaled" and n[1][5]) == 136
-    assert len(fused) == 2379
+    # each Linear's scale is the Mul of the activation's and the weights'
+    # scales, read by the chain alone: folded in as well
+    assert sum(1 for n in fused if n[0] == "QMatMulScaled" and n[3].get("scale_product")) == 148
+    assert len(fused) == 2231
     covered = sorted(i for grp in groups for i in grp)
     assert covered == list(range(len(nodes)))  # every original node exactly once
     produced = {}

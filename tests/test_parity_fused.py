@@ -94,6 +94,27 @@ def test_qmatmul_tail(gpu, oracle, M, K, N, wdt, per_col, bias):
     assert_bitexact(got, want.astype(np.float32), f"QMatMulScaled {M}x{K}x{N}")
 
 
+@pytest.mark.parametrize("per_col", [True, False])
+def test_qmatmul_tail_scale_product(gpu, oracle, per_col):
+    """The graph's form: the Linear's scale is Mul(activation scale, weight
+    scale), read by the chain alone, and folds in with it; the epilogue forms
+    the product (rounded once) before scaling, the same bits as the chain."""
+    r = rng(29)
+    M, K, N = 130, 512, 640
+    a = r.integers(0, 256, (1, M, K)).astype(np.uint8)
+    inputs = {"a": a, "az": np.array(117, np.uint8), "sa": np.array(0.0213, np.float32)}
+    sw = r.uniform(1e-3, 1e-2, (N,) if per_col else ()).astype(np.float16)
+    weights = {"w": r.integers(-128, 128, (K, N)).astype(np.int8), "wz": np.array(0, np.int8),
+               "sw": sw, "b": r.normal(0, 1, (N,)).astype(np.float16)}
+    nodes = [("Mul", ["sa", "sw"], ["s"], {}),
+             ("MatMulInteger", ["a", "w", "az", "wz"], ["acc"], {}),
+             ("Cast", ["acc"], ["f"], {"to": 1}), ("Mul", ["f", "s"], ["y"], {}),
+             ("Add", ["y", "b"], ["z"], {})]
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, "z")
+    assert [n[0] for n in fused] == ["QMatMulScaled"] and fused[0][3].get("scale_product")
+    assert_bitexact(got, want.astype(np.float32), "QMatMulScaled with the scale product")
+
+
 def test_qmatmul_tail_row_scale_runs_the_chain(gpu, oracle):
     """A scale that is not one value or one per column (here one per row)
     would change the product's shape handling: the fused node then runs the
