@@ -33,14 +33,27 @@ constexpr int kTileM = 128;  // output channels per block (2 waves x 64)
 constexpr int kCinAlign = 64;   // channels per chunk: two 32-deep MFMA steps
 constexpr int kRowPitch = 80;   // LDS bytes per 64-channel row (16-byte pad: staggered banks)
 
+// The graph's per-call bias quantisation ahead of a quantised conv:
+// scale = Mul(sa, sw), bias_int32 = Cast(Floor(Div(bias, scale))); sa and sw
+// one value each, bias Cout values.  qb.scale / qb.bias receive them.
+struct QBias {
+  const float* sa;
+  const float* sw;
+  const float* bias;
+  float* scale;
+  int32_t* ibias;
+};
+
 // wT[co][tap][ci] = offset weight (0 for padding rows/channels);
-// wsum[co] = sum of the offset weights; wzo[co] = offset weight zero point.
+// wsum[co] = sum of the offset weights; wzo[co] = offset weight zero point;
+// with qb.scale set also channel co's quantised bias and scale.
 __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w, int w_dt,
                                                      const void* __restrict__ wzp, int wzp_dt,
                                                      int64_t wzp_n, int8_t* __restrict__ wT,
                                                      int32_t* __restrict__ wsum,
                                                      int32_t* __restrict__ wzo, int64_t Cout,
-                                                     int64_t Cin, int64_t Kw, int64_t CinP) {
+                                                     int64_t Cin, int64_t Kw, int64_t CinP,
+                                                     QBias qb) {
   __shared__ int part[4];
   const int64_t co = blockIdx.x;
   const bool live = co < Cout;
@@ -67,6 +80,17 @@ __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w,
     int z = 0;  // padding rows: a = 0, so any value works; keep 0
     if (live) z = (wzp ? static_cast<int>(load_as_i64(wzp, wzp_dt, wzp_n > 1 ? co : 0)) : 0) - off;
     wzo[co] = z;
+    if (qb.scale && live) {
+      // the chain's operations, each rounded as its node rounds it; the
+      // float -> int32 Cast as the device's Cast node does it (truncation,
+      // INT64_MIN outside the int64 range, then the low 32 bits)
+      const float sc = qb.sa[0] * qb.sw[0];
+      const float t = truncf(floorf(qb.bias[co] / sc));
+      const int64_t v = (t >= -9.223372036854775808e18f && t < 9.223372036854775808e18f)
+                            ? static_cast<int64_t>(t) : INT64_MIN;
+      qb.scale[co] = sc;
+      qb.ibias[co] = static_cast<int32_t>(v);
+    }
   }
 }
 
@@ -389,7 +413,8 @@ static int check_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk
 static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
                      const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
                      const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
-                     bool outf) {
+                     bool outf, const kk_tensor* qb_sa = nullptr, const kk_tensor* qb_sw = nullptr,
+                     const kk_tensor* qb_bias = nullptr) {
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], Kw = w->shape[2];
   const int64_t Lout = out->shape[2];
@@ -397,24 +422,38 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
   const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
   auto up = [](int64_t n) { return ceil_div(n, 256) * 256; };
   const int64_t o_wT = 0, o_wsum = o_wT + up(CoutP * Kw * CinP);
-  const int64_t o_wzo = o_wsum + up(CoutP * 4), total = o_wzo + up(CoutP * 4);
+  const int64_t o_wzo = o_wsum + up(CoutP * 4), o_qs = o_wzo + up(CoutP * 4);
+  const int64_t o_qb = o_qs + up(CoutP * 4), total = o_qb + up(CoutP * 4);
   void* ws = nullptr;
   KK_TRY(kk_alloc(static_cast<size_t>(total), &ws));
   char* base = static_cast<char*>(ws);
   int8_t* wT = reinterpret_cast<int8_t*>(base + o_wT);
   int32_t* wsum = reinterpret_cast<int32_t*>(base + o_wsum);
   int32_t* wzo = reinterpret_cast<int32_t*>(base + o_wzo);
+  QBias qb{};
+  if (qb_sa) {
+    qb.sa = static_cast<const float*>(qb_sa->data);
+    qb.sw = static_cast<const float*>(qb_sw->data);
+    qb.bias = static_cast<const float*>(qb_bias->data);
+    qb.scale = reinterpret_cast<float*>(base + o_qs);
+    qb.ibias = reinterpret_cast<int32_t*>(base + o_qb);
+  }
   hipStream_t st = ctx().stream;
   hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
                      w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
-                     w_zp ? numel(w_zp) : 0, wT, wsum, wzo, Cout, Cin, Kw, CinP);
+                     w_zp ? numel(w_zp) : 0, wT, wsum, wzo, Cout, Cin, Kw, CinP, qb);
   int rc = check_launch("conv_i8_wprep");
   if (rc == KK_OK) {
     ConvI8Args A{};
     A.wT = wT; A.wsum = wsum; A.wzo = wzo;
     A.x = static_cast<const uint8_t*>(x->data);
     A.xzp = x_zp ? static_cast<const uint8_t*>(x_zp->data) : nullptr;
-    if (outf) {
+    if (outf && qb.scale) {
+      A.outf = static_cast<float*>(out->data);
+      A.bias = qb.ibias;
+      A.scale = qb.scale;
+      A.scale_n = Cout;
+    } else if (outf) {
       A.outf = static_cast<float*>(out->data);
       A.bias = bias ? static_cast<const int32_t*>(bias->data) : nullptr;
       A.scale = static_cast<const float*>(scale->data);
@@ -476,6 +515,31 @@ int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_te
   if (x->shape[1] * w->shape[2] == 0)
     return set_error(KK_E_UNSUPPORTED, "kk_conv_integer_scaled: empty reduction");
   return conv_integer_run(out, x, w, x_zp, w_zp, bias, scale, stride, dilation, pad0, pad1, true);
+}
+
+int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                                 const kk_tensor* x_zp, const kk_tensor* w_zp,
+                                 const kk_tensor* bias, const kk_tensor* scale_a,
+                                 const kk_tensor* scale_w, int stride, int dilation, int pad0,
+                                 int pad1, int group) {
+  int64_t Lout = 0;
+  KK_TRY(check_conv_integer(out, x, w, x_zp, w_zp, stride, dilation, pad0, pad1, group, KK_F32,
+                            "kk_conv_integer_scaled_qbias", &Lout));
+  const int64_t Cout = w->shape[0];
+  const kk_tensor* one[2] = {scale_a, scale_w};
+  for (const kk_tensor* t : one) {
+    KK_TRY(check_tensor(t, "scale"));
+    if (t->dtype != KK_F32 || numel(t) != 1)
+      return set_error(KK_E_ARG, "kk_conv_integer_scaled_qbias: scale_a and scale_w are one fp32 each");
+  }
+  KK_TRY(check_tensor(bias, "bias"));
+  if (bias->dtype != KK_F32 || !is_contiguous(bias) || numel(bias) != Cout)
+    return set_error(KK_E_ARG, "kk_conv_integer_scaled_qbias: bias must be fp32 with Cout values");
+  if (numel(out) == 0) return KK_OK;
+  if (x->shape[1] * w->shape[2] == 0)
+    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer_scaled_qbias: empty reduction");
+  return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
+                          true, scale_a, scale_w, bias);
 }
 
 }  // extern "C"

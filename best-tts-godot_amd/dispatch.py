@@ -334,6 +334,18 @@ def dispatch(op, node_input, node_output, at, env):
     elif op == "Snake":
         # x + recip * sin(alpha * x)^2: the Mul/Sin/Pow/Mul/Add chain fused.
         out = ops.snake(to_device(x), to_device(y), to_device(inp(2)))
+    elif op == "QConvScaled" and at.get("bias_quant"):
+        # the same with the bias quantisation ahead of it folded in: inputs
+        # x, w, x_zp, w_zp, "", "", scale_a, scale_w, bias (fp32); scale =
+        # scale_a * scale_w, int32 bias = Cast(Floor(Div(bias, scale))).
+        conv_at = {k: v for k, v in at.items() if k != "bias_quant"}
+        out = ops.conv_integer_scaled_qbias(to_device(x), to_device(y), to_device(inp(2)),
+                                            to_device(inp(3)), _f32(to_device(inp(8))),
+                                            _f32(to_device(inp(6))), _f32(to_device(inp(7))),
+                                            conv_at.get("pads", [0, 0]),
+                                            conv_at.get("strides", [1])[0],
+                                            conv_at.get("dilations", [1])[0],
+                                            conv_at.get("group", 1))
     elif op == "QConvScaled":
         # ConvInteger -> Add(int32 bias) -> Cast(float) -> Mul(scale), fused;
         # inputs x, w, x_zp, w_zp, bias ("" if absent), scale.

@@ -95,7 +95,95 @@ def fuse(nodes, weights, protect=()):
             out.append(node)
             groups.append([i])
     out, groups = _merge_norm_snake(out, groups, protect)
-    return _merge_norm_quant(out, groups, protect)
+    out, groups = _merge_norm_quant(out, groups, protect)
+    return _merge_qconv_bias(out, groups, weights, protect)
+
+
+def _merge_qconv_bias(out, groups, weights, protect):
+    """A quantised conv whose int32 bias the graph forms per call --
+    scale = Mul(sa, sw); bias = Reshape(Cast(int32, Floor(Div(b, scale)))),
+    every link read by the next alone and the scale by the Div and the conv
+    alone -- takes those five nodes in: QConvScaled with bias_quant, inputs
+    x, w, x_zp, w_zp, "", "", sa, sw, b.  Only where sa and sw are single
+    values and b, a constant, has one value per output channel (the chain
+    then broadcasts exactly per channel)."""
+    readers = defaultdict(list)
+    producer = {}
+    for k, (_op, ins, outs, _at) in enumerate(out):
+        for n in ins:
+            if n:
+                readers[n].append(k)
+        for o in outs:
+            if o:
+                producer[o] = k
+
+    def sole(name, k):
+        return name not in protect and readers.get(name) == [k]
+
+    def size(name):
+        v = weights.get(name)
+        return None if v is None else int(np.prod(getattr(v, "shape", ())))
+
+    def single(name, depth=0):
+        """One value: a one-element constant, or the scale output of a
+        quantiser (DynamicQuantizeLinear, InstanceNormQuant), through Casts."""
+        if size(name) is not None:
+            return size(name) == 1
+        p = producer.get(name)
+        if p is None or depth > 4:
+            return False
+        p_op, p_ins, p_outs = out[p][0], out[p][1], out[p][2]
+        if p_op == "Cast":
+            return single(p_ins[0], depth + 1)
+        return p_op in ("DynamicQuantizeLinear", "InstanceNormQuant") and \
+            len(p_outs) > 1 and p_outs[1] == name
+
+    takes = {}  # conv index -> indices of the five nodes it absorbs
+    for k, (op, ins, outs, at) in enumerate(out):
+        if op != "QConvScaled" or at.get("bias_quant") or len(ins) < 6 or not ins[4]:
+            continue
+        bias_i, scale = ins[4], ins[5]
+        r = producer.get(bias_i)
+        if r is None or out[r][0] != "Reshape" or not sole(bias_i, k):
+            continue
+        c = producer.get(out[r][1][0])
+        if c is None or out[c][0] != "Cast" or int(out[c][3].get("to", 0)) != 6 or \
+                not sole(out[r][1][0], r):
+            continue
+        f = producer.get(out[c][1][0])
+        if f is None or out[f][0] != "Floor" or not sole(out[c][1][0], c):
+            continue
+        d = producer.get(out[f][1][0])
+        if d is None or out[d][0] != "Div" or not sole(out[f][1][0], f) or \
+                len(out[d][1]) != 2 or out[d][1][1] != scale:
+            continue
+        m = producer.get(scale)
+        b = out[d][1][0]
+        if m is None or out[m][0] != "Mul" or len(out[m][1]) != 2 or scale in protect or \
+                sorted(readers.get(scale, [])) != sorted([d, k]):
+            continue
+        sa, sw = out[m][1]
+        cout = getattr(weights.get(ins[1]), "shape", (None,))[0]
+        if not (single(sa) and single(sw) and cout is not None and size(b) == cout):
+            continue
+        takes[k] = [m, d, f, c, r]
+    if not takes:
+        return out, groups
+    dropped = {i for v in takes.values() for i in v}
+    new_out, new_groups = [], []
+    for k, node in enumerate(out):
+        if k in dropped:
+            continue
+        if k in takes:
+            m, d = takes[k][0], takes[k][1]
+            op, ins, outs, at = node
+            ins = list(ins[:4]) + ["", ""] + list(out[m][1]) + [out[d][1][0]]
+            node = (op, ins, outs, dict(at, bias_quant=1))
+            new_groups.append(sorted(sum((groups[i] for i in takes[k]), []) + groups[k]))
+        else:
+            new_groups.append(groups[k])
+        new_out.append(node)
+    return new_out, new_groups
 
 
 def _merge_norm_quant(out, groups, protect):

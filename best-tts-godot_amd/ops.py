@@ -274,6 +274,23 @@ def conv_integer_scaled(x, w, x_zp, w_zp, bias, scale, pads=(0, 0), stride=1, di
     return out
 
 
+def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0, 0), stride=1,
+                              dilation=1, group=1):
+    """conv_integer_scaled with its int32 bias and scale formed in the same
+    launch sequence: scale = scale_a * scale_w, bias_int32 =
+    int32(floor(bias / scale)) (bias fp32 [Cout], the scales one value each)."""
+    x = x.contiguous()
+    w = w.contiguous()
+    n, _, L = x.shape
+    cout, _, k = w.shape
+    lout = (L + pads[0] + pads[1] - dilation * (k - 1) - 1) // stride + 1
+    out = DeviceTensor.empty((n, cout, max(lout, 0)), np.float32)
+    _lib.call("kk_conv_integer_scaled_qbias", out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
+              bias.contiguous().desc(), scale_a.contiguous().desc(), scale_w.contiguous().desc(),
+              int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
+    return out
+
+
 def instance_norm_scale_shift(x, scale=None, shift=None, eps=1e-5, leaky_alpha=None):
     """(x - mean_T) / sqrt(var_T + eps) * scale[c] + shift[c] over the last
     axis, then LeakyRelu(leaky_alpha) when given."""

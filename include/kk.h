@@ -269,6 +269,16 @@ int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_te
                            const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
                            const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
                            int group);
+/* The same with the graph's per-call bias quantisation ahead of it folded in
+ * (ref_runtime.py:446-455, 462-467 Floor, 572-578): scale = Mul(scale_a,
+ * scale_w) and bias_int32 = Cast(Floor(Div(bias, scale))), each rounded as
+ * its node rounds it, then the conv tail as above with that bias and scale;
+ * scale_a and scale_w one fp32 each, bias fp32 with Cout values. */
+int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                                 const kk_tensor* x_zp, const kk_tensor* w_zp,
+                                 const kk_tensor* bias, const kk_tensor* scale_a,
+                                 const kk_tensor* scale_w, int stride, int dilation, int pad0,
+                                 int pad1, int group);
 
 /* ------------------------------------------------ recurrent / vocoder
  * DynamicQuantizeLSTM as op_lstm computes it without activation

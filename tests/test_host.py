@@ -166,7 +166,10 @@ def test_fusion_pass_on_the_kokoro_graph():
     # each Linear's scale is the Mul of the activation's and the weights'
     # scales, read by the chain alone: folded in as well
     assert sum(1 for n in fused if n[0] == "QMatMulScaled" and n[3].get("scale_product")) == 148
-    assert len(fused) == 2231
+    # and each quantised conv whose int32 bias the graph forms per call
+    # (Mul -> Div -> Floor -> Cast -> Reshape) takes those nodes in
+    assert sum(1 for n in fused if n[0] == "QConvScaled" and n[3].get("bias_quant")) == 80
+    assert len(fused) == 1831
     covered = sorted(i for grp in groups for i in grp)
     assert covered == list(range(len(nodes)))  # every original node exactly once
     produced = {}

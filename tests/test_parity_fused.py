@@ -133,6 +133,34 @@ def test_qmatmul_tail_row_scale_runs_the_chain(gpu, oracle):
     assert_bitexact(got, want.astype(np.float32), "QMatMulScaled, per-row scale")
 
 
+@pytest.mark.parametrize("cin,cout,k,L", [(128, 128, 5, 2000), (256, 96, 3, 777)])
+def test_qconv_tail_with_bias_quantisation(gpu, oracle, cin, cout, k, L):
+    """The graph's whole quantised-conv sequence: the activation's scale
+    times the weight scale, the float bias divided by that, floored, cast
+    to int32 and reshaped, then ConvInteger + bias -> Cast -> Mul(scale).
+    The bias quantisation folds into the conv (one launch after the
+    quantiser); the result is the chain's, bit for bit."""
+    r = rng(30)
+    xf = (r.normal(0.2, 1.5, (1, cin, L))).astype(np.float32)
+    weights = {"w": r.integers(0, 256, (cout, cin, k)).astype(np.uint8),
+               "wz": np.array(129, np.uint8), "sw": np.array(0.00371, np.float16),
+               "b": r.normal(0, 0.5, (cout,)).astype(np.float16),
+               "shp": np.array([1, cout, 1], np.int64)}
+    at = {"pads": [k // 2, k // 2], "dilations": [1], "strides": [1], "group": 1,
+          "kernel_shape": [k]}
+    nodes = [("DynamicQuantizeLinear", ["xf"], ["q", "sa", "za"], {}),
+             ("Cast", ["sa"], ["saf"], {"to": 10}), ("Mul", ["saf", "sw"], ["s"], {}),
+             ("Div", ["b", "s"], ["bd"], {}), ("Floor", ["bd"], ["bf"], {}),
+             ("Cast", ["bf"], ["bi"], {"to": 6}), ("Reshape", ["bi", "shp"], ["br"], {}),
+             ("ConvInteger", ["q", "w", "za", "wz"], ["acc"], at),
+             ("Add", ["acc", "br"], ["accb"], {}), ("Cast", ["accb"], ["f"], {"to": 10}),
+             ("Mul", ["f", "s"], ["y"], {})]
+    got, want, fused = run_chain(gpu, oracle, nodes, {"xf": xf}, weights, "y")
+    assert [n[0] for n in fused] == ["DynamicQuantizeLinear", "Cast", "QConvScaled"]
+    assert fused[-1][3].get("bias_quant")
+    assert_bitexact(got, want.astype(np.float32), f"QConvScaled + bias quantisation {cin}->{cout}")
+
+
 def norm_chain(affine, leaky):
     nodes = [("ReduceMean", ["x", "ax"], ["m1"], {"keepdims": 1}),
              ("Sub", ["x", "m1"], ["d"], {}), ("Mul", ["d", "d"], ["sq"], {}),
