@@ -157,10 +157,24 @@ __global__ void __launch_bounds__(kDqlSmallThreads) dql_small(const float* __res
   const int tid = threadIdx.x;
   const int64_t n4 = vec ? n / 4 : 0;
   float lo = INFINITY, hi = -INFINITY;
-  for (int64_t i = tid; i < n4; i += kDqlSmallThreads) {
-    const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);  // read again below
-    lo = fminf(lo, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
-    hi = fmaxf(hi, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+  // eight independent 16-byte loads in flight per thread (one block has to
+  // cover the whole tensor: a load at a time would wait out each round trip)
+  // (past the end a slot holds x[0] again, which moves neither extreme)
+  constexpr int kU = 8;
+  const float x0 = x[0];
+  for (int64_t i0 = tid; i0 < n4; i0 += kDqlSmallThreads * kU) {
+    float4 v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t i = i0 + static_cast<int64_t>(u) * kDqlSmallThreads;
+      v[u] = i < n4 ? *reinterpret_cast<const float4*>(x + 4 * i)  // read again below
+                    : make_float4(x0, x0, x0, x0);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      lo = fminf(lo, fminf(fminf(v[u].x, v[u].y), fminf(v[u].z, v[u].w)));
+      hi = fmaxf(hi, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
+    }
   }
   for (int64_t i = 4 * n4 + tid; i < n; i += kDqlSmallThreads) {
     lo = fminf(lo, x[i]);
@@ -184,10 +198,21 @@ __global__ void __launch_bounds__(kDqlSmallThreads) dql_small(const float* __res
   }
   __syncthreads();
   const float sc = pz.x, z = pz.y;
-  for (int64_t i = tid; i < n4; i += kDqlSmallThreads) {
-    const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);
-    reinterpret_cast<uint32_t*>(y)[i] = dql_byte(v.x, sc, z) | (dql_byte(v.y, sc, z) << 8) |
-                                        (dql_byte(v.z, sc, z) << 16) | (dql_byte(v.w, sc, z) << 24);
+  for (int64_t i0 = tid; i0 < n4; i0 += kDqlSmallThreads * kU) {
+    float4 v[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t i = i0 + static_cast<int64_t>(u) * kDqlSmallThreads;
+      if (i < n4) v[u] = *reinterpret_cast<const float4*>(x + 4 * i);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t i = i0 + static_cast<int64_t>(u) * kDqlSmallThreads;
+      if (i < n4)
+        reinterpret_cast<uint32_t*>(y)[i] = dql_byte(v[u].x, sc, z) | (dql_byte(v[u].y, sc, z) << 8) |
+                                            (dql_byte(v[u].z, sc, z) << 16) |
+                                            (dql_byte(v[u].w, sc, z) << 24);
+    }
   }
   for (int64_t i = 4 * n4 + tid; i < n; i += kDqlSmallThreads)
     y[i] = static_cast<uint8_t>(dql_byte(x[i], sc, z));
