@@ -270,7 +270,7 @@ int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_te
                            const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
                            int group);
 /* The same with the graph's per-call bias quantisation ahead of it folded in
- * (ref_runtime.py:446-455, 462-467 Floor, 572-578): scale = Mul(scale_a,
+ * (ref_runtime.py:450-455 Mul/Div, 472-473 Floor, 572-578 Cast): scale = Mul(scale_a,
  * scale_w) and bias_int32 = Cast(Floor(Div(bias, scale))), each rounded as
  * its node rounds it, then the conv tail as above with that bias and scale;
  * scale_a and scale_w one fp32 each, bias fp32 with Cout values. */
