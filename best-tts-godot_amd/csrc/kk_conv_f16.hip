@@ -4,14 +4,19 @@
 // An fp16 weight is exact in fp16, and so is an 8-bit weight less its zero
 // point (|q - zp| <= 255); the 8-bit weights' scale, per tensor or per
 // output channel, multiplies the fp32 sum (sum (q - zp) s x = s sum (q - zp) x,
-// the same value up to fp32 rounding).  Each fp32 activation x is split into
-// hi = fp16(x) and lo = fp16(x - hi) (x - hi is exact in fp32), so hi + lo
-// equals x to within 2^-22 |x|; every product w*hi and w*lo is exact in
-// fp32 (11 + 11 significant bits), and v_mfma_f32_32x32x16_f16 accumulates
-// them in fp32: the accuracy of fp32 products accumulated in fp32, at the
-// fp16 matrix rate.  An activation of magnitude >= 2^15 (fp16 ends at
-// 65504) or infinite sets a flag instead; the fp32 kernels, launched after
-// this one with that flag as their condition, then redo the convolution.
+// the same value up to fp32 rounding).  A first pass forms m = max |x| over
+// the input; every activation is then scaled by 2^k, the power of two that
+// puts m in [2^14, 2^15) (exact in fp32), and the scaled y = x 2^k is split
+// into hi = fp16(y) and lo = fp16(y - hi) (y - hi is exact in fp32).  For
+// |y| >= 2^-3 lo is a normal fp16 number and hi + lo equals y to within
+// 2^-22 |y|; below that (|x| < m 2^-17) the error is at most 2^-25 in
+// scaled units, m 2^-39 or less.  Every product w*hi and w*lo is exact in
+// fp32 (11 + 11 significant bits), v_mfma_f32_32x32x16_f16 accumulates them
+// in fp32, and the sum is scaled back by 2^-k (exact): the accuracy of fp32
+// products accumulated in fp32, at the fp16 matrix rate, whatever the
+// activations' magnitude.  A non-finite activation (m inf or NaN) sets a
+// flag instead; the fp32 kernels, launched after this one with that flag as
+// their condition, then compute the convolution.
 //
 // Both operations are one implicit GEMM with rows m = co*P + r (output
 // channel co, phase r < P):
@@ -29,8 +34,8 @@
 // loads its weight rows as vectors.  A Wt beyond the scratch while a graph
 // is being recorded (nothing may be allocated then) is not stored: the
 // kernel gathers the same fp16 values from W itself (slower, the same
-// results bit for bit).  The overflow flag is a slot of the library
-// context; a one-thread kernel after the fallback clears it.
+// results bit for bit).  The non-finite flag and m are slots of the library
+// context, cleared at the start of each call.
 #include <algorithm>
 
 #include "kk_internal.h"
@@ -58,7 +63,8 @@ struct HArgs {
   const float* x;      // [N, Cin, L]
   float* out;          // [N, Cout, Lout]
   const float* bias;   // [Cout] or NULL
-  int* flag;
+  int* flag;           // set: an activation is not finite
+  unsigned* xmax;      // bits of max |x| (a non-negative float, so ordered as unsigned)
   int64_t Cin, L, M, Cout, Kg, Nq, Lout;
   int64_t qs, tap_mul, tap_add, os, ophase0;
   int P;
@@ -79,6 +85,14 @@ struct Tile {
   static_assert(kThreads % BN == 0 && (kBK / 2) % KP_STEP == 0, "B staging shape");
 };
 
+// The power of two k with m 2^k in [2^14, 2^15) for m = max |x| > 0 (0 for
+// m = 0), kept within [-120, 120] so that 2^k and 2^-k are normal floats.
+__device__ __forceinline__ int convh_scale_exp(unsigned mbits) {
+  if (mbits == 0) return 0;
+  const int e = static_cast<int>(mbits >> 23) - 127;  // floor(log2 m); -127 for subnormal m
+  return min(120, 14 - e);
+}
+
 // PRE: the weights come rearranged in A.wt; else gathered from A.w.
 template <class T, typename TW, bool PRE>
 __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
@@ -86,6 +100,13 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
   __shared__ __align__(16) _Float16 Bh[2][T::BN * kPitch];
   __shared__ __align__(16) _Float16 Bl[2][T::BN * kPitch];
   constexpr int WM_T = T::WM_T, WN_T = T::WN_T;
+  const unsigned mbits = *A.xmax;
+  if (mbits >= 0x7f800000u) {  // an infinite or NaN activation: the fp32 kernels compute it
+    if (threadIdx.x == 0) *A.flag = 1;  // every writer stores the same 1
+    return;
+  }
+  const int kexp = convh_scale_exp(mbits);
+  const float xscale = ldexpf(1.0f, kexp), unscale = ldexpf(1.0f, -kexp);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m_w = (wave / T::WAVES_N) * 32 * WM_T, n_w = (wave % T::WAVES_N) * 32 * WN_T;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T::BN;
@@ -108,7 +129,6 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
   // staging registers
   _Float16 av[T::KPT];
   float bv[T::B_PAIRS][2];
-  bool bad = false;
   const int bn = tid % T::BN;
   const int64_t q = n0 + bn;
   auto fetch = [&](int64_t k0) {
@@ -158,8 +178,7 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
       h2 hi, lo;
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        const float v = bv[j][e];
-        bad |= !(fabsf(v) < 32768.0f) && !(v != v);  // too large, or infinite (NaN passes)
+        const float v = bv[j][e] * xscale;  // |v| < 2^15: exact
         const _Float16 h = static_cast<_Float16>(v);
         hi[e] = h;
         lo[e] = static_cast<_Float16>(v - static_cast<float>(h));
@@ -207,8 +226,6 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
     if (more) stash(buf ^ 1);
     __syncthreads();
   }
-  if (bad) *A.flag = 1;  // every writer stores the same 1
-
   // D(i, j) of a 32x32 tile: lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
   float* ob = A.out + b * A.Cout * A.Lout;
 #pragma unroll
@@ -224,20 +241,55 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
 #pragma unroll
       for (int j = 0; j < WN_T; ++j) {
         const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
-        const float v = A.dq.scale ? acc[i][j][g] * sc : acc[i][j][g];
+        const float u = acc[i][j][g] * unscale;  // exact: a power of two
+        const float v = A.dq.scale ? u * sc : u;
         const int64_t pos = qq * A.os + r + A.ophase0;
         if (qq < A.Nq && pos >= 0 && pos < A.Lout) ob[co * A.Lout + pos] = A.bias ? v + bias : v;
       }
     }
 }
 
-__global__ void convh_flag_clear(int* flag) { *flag = 0; }
+__global__ void convh_flag_clear(int* flag, unsigned* xmax) {
+  *flag = 0;
+  *xmax = 0u;
+}
+
+// *xmax = max(*xmax, bits of max |x|) over n floats: |x| is a non-negative
+// float (NaN above infinity), so its bits order as unsigned integers.
+// vec: x is 16-byte aligned.
+__global__ void __launch_bounds__(256) convh_absmax(const float* __restrict__ x, int64_t n, int vec,
+                                                    unsigned* xmax) {
+  __shared__ unsigned part[4];
+  unsigned m = 0;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t t0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  int64_t done = 0;
+  if (vec) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const int64_t n4 = n / 4;
+    for (int64_t i = t0; i < n4; i += stride) {
+      const float4 v = x4[i];
+      m = max(m, max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
+                     max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w)))));
+    }
+    done = 4 * n4;
+  }
+  for (int64_t i = done + t0; i < n; i += stride) m = max(m, __float_as_uint(fabsf(x[i])));
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = max(m, static_cast<unsigned>(__shfl_xor(static_cast<int>(m), off, 64)));
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) atomicMax(xmax, max(max(part[0], part[1]), max(part[2], part[3])));
+}
 
 // Wt[m][kk] (m = co*P + r, kk = t*Cin + ci): the fp16 value the gathering
 // kernel forms, W less the zero point (0 past the kernel for transposed).
 template <typename TW>
 __global__ void convh_weights(_Float16* __restrict__ wt, HArgs A) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) *A.flag = 0;  // this call's overflow flag starts clear
+  if (blockIdx.x == 0 && threadIdx.x == 0) {  // this call's flag and max start clear
+    *A.flag = 0;
+    *A.xmax = 0u;
+  }
   const TW* w = static_cast<const TW*>(A.w);
   const int64_t total = A.M * A.Kg, cout = A.M / A.P;
   for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
@@ -292,7 +344,13 @@ static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
       hipLaunchKernelGGL(convh_weights<uint8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
     a.wt = wt;
   } else {
-    hipLaunchKernelGGL(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, a.flag);
+    hipLaunchKernelGGL(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, a.flag, a.xmax);
+  }
+  {
+    const int64_t n = a.Cin * a.L * batch;
+    const unsigned g = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256 * 16), 1024)));
+    const int vec = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 ? 1 : 0;
+    hipLaunchKernelGGL(convh_absmax, dim3(g), dim3(256), 0, ctx().stream, a.x, n, vec, a.xmax);
   }
   // the largest tile that still gives every CU two blocks; 128 x 32 below that
   const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
@@ -335,6 +393,7 @@ bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, con
   a.w = w->data; a.transposed = transposed ? 1 : 0; a.Kw = Kw; a.s = stride; a.dq = dq;
   a.x = static_cast<const float*>(x->data); a.out = static_cast<float*>(out->data);
   a.bias = bias ? static_cast<const float*>(bias->data) : nullptr; a.flag = *flag;
+  a.xmax = reinterpret_cast<unsigned*>(ctx().row_counters + kRowCounters + kFlagConvhMax);
   a.Cin = Cin; a.L = L; a.M = M; a.Cout = Cout; a.Kg = Kg; a.Nq = Nq; a.Lout = Lout;
   a.P = static_cast<int>(P);
   if (transposed) {

@@ -36,22 +36,6 @@ using CfgL = Cfg<64, 64, 2, 2>;  // 32x32 per wave
 using CfgM = Cfg<64, 32, 1, 2>;  // 16x32 per wave
 using CfgS = Cfg<32, 32, 1, 1>;  // 16x16 per wave
 
-// Batch offsets: up to 6 batch axes with per-operand strides (0 = broadcast).
-struct BatchMap {
-  int nb = 0;
-  int64_t dims[6];
-  int64_t st[3][6];  // 0 = a, 1 = b, 2 = out
-};
-
-__device__ __forceinline__ int64_t batch_offset(const BatchMap& bm, int which, int64_t b) {
-  int64_t off = 0;
-  for (int d = bm.nb - 1; d >= 0; --d) {
-    off += (b % bm.dims[d]) * bm.st[which][d];
-    b /= bm.dims[d];
-  }
-  return off;
-}
-
 // Scale and zero point of one weight row/column, read once per block.
 // A NULL scale means 1 (the integer ops shift by their zero point only).
 __device__ __forceinline__ void dq_params(const Dequant& dq, int64_t idx, float& s, float& z) {
@@ -376,13 +360,11 @@ struct GemmArgs {
   const void* a;
   int a_dt;
   int64_t a_si, a_sj;  // element strides of A [M, K]
-  Dequant adq;         // A's zero-point shift (MatMulInteger), per tensor
   const void* b;
   int b_dt;
   int64_t b_si, b_sj;  // element strides of B [K, N]
   Dequant dq;          // B's dequantisation (per column or per tensor)
-  float* out;          // fp32, or int32 when out_i32
-  int out_i32;         // store round-half-even(acc) as int32 (MatMulInteger)
+  float* out;
   int64_t som, son;
   BatchMap bm;
   int64_t M, N, K;
@@ -393,31 +375,7 @@ struct GemmArgs {
   // and gemm_splitk_reduce forms out
   int splits;
   float* part;
-  // MatMulInteger's Cast -> Mul(scale) (-> Add(bias)) tail, fused: with cs
-  // set, out is fp32 = float(int32 result) * cs[n] (+ cb[n]), two roundings
-  // as the chain computes them; cs_n / cb_n are 1 (one value) or N
-  const float* cs;
-  int64_t cs_n;
-  const float* cs2;  // optional second factor: the scale is cs[n] * cs2[n], rounded once
-  int64_t cs2_n;
-  const float* cb;
-  int64_t cb_n;
 };
-
-// The int32 result of MatMulInteger, or with the fused tail its scaled fp32.
-__device__ __forceinline__ void store_int_result(const GemmArgs& G, float* out, int64_t o, int64_t n,
-                                                 float v) {
-  const int32_t iv = __float2int_rn(v);
-  if (G.cs) {
-    float sc = G.cs[G.cs_n > 1 ? n : 0];
-    if (G.cs2) sc = sc * G.cs2[G.cs2_n > 1 ? n : 0];
-    float y = static_cast<float>(iv) * sc;
-    if (G.cb) y = y + G.cb[G.cb_n > 1 ? n : 0];
-    out[o] = y;
-  } else {
-    reinterpret_cast<int32_t*>(out)[o] = iv;
-  }
-}
 
 // A kinds: 0 = K-contiguous quads of TA, 1 = scalar gather.
 // B kinds: 0 = N-contiguous quads of TB, 1 = scalar gather.
@@ -434,21 +392,19 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
   float* out = G.out + oo;
   const float alpha = G.alpha;
   const int64_t som = G.som, son = G.son;
-  const bool out_i32 = G.out_i32;
   const int64_t M = G.M, N = G.N, K = G.K;
   float* part = splits > 1 ? G.part + ((bz * splits + split) * M) * N : nullptr;
   auto store = [&](int64_t m, int64_t n, float v) {
     if (part) part[m * N + n] = v;
-    else if (out_i32) store_int_result(G, out, m * som + n * son, n, v);
     else out[m * som + n * son] = alpha == 1.0f ? v : v * alpha;
   };
+  const Dequant none{};  // fp32 activations: no per-row dequantisation
   // this split's K-steps
   const int64_t nk_all = ceil_div(K, kBK), chunk = ceil_div(nk_all, splits);
   const int64_t kt0 = split * chunk, kt1 = std::min<int64_t>(nk_all, kt0 + chunk);
   auto getA = [&](int64_t m, int64_t k) -> float {
     if (m >= M || k >= K) return 0.0f;
-    const float q = load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
-    return G.adq.active ? dequant_value(q, G.adq, m) : q;
+    return load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
   };
   auto getB = [&](int64_t k, int64_t n) -> float {
     if (k >= K || n >= N) return 0.0f;
@@ -457,13 +413,13 @@ __global__ void __launch_bounds__(kNT) gemm_kernel(GemmArgs G) {
   };
   if constexpr (AK == 0 && BK == 0) {
     AQuad<C, TA> la;
-    la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, G.adq);
+    la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, none);
     BQuad<C, TB> lb;
     lb.init(static_cast<const TB*>(G.b) + ob, G.b_si, N, K, n0, G.dq);
     gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
   } else if constexpr (AK == 0) {
     AQuad<C, TA> la;
-    la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, G.adq);
+    la.init(static_cast<const TA*>(G.a) + oa, G.a_si, M, K, m0, none);
     if (G.b_si == 1) {
       BScalar<C, decltype(getB), false> lb{getB, n0};
       gemm_run<C>(la, lb, store, M, N, K, m0, n0, kt0, kt1);
@@ -549,8 +505,7 @@ __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
   }
 }
 
-// out[b][m][n] = the splits' partials summed in split order (then alpha, or
-// MatMulInteger's rounding to int32).
+// out[b][m][n] = the splits' partials summed in split order, then alpha.
 __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs G, int64_t batch) {
   const int64_t MN = G.M * G.N, total = batch * MN;
   const int S = G.splits;
@@ -562,8 +517,7 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(GemmArgs G, int64_t ba
     float v = p[0];
     for (int s = 1; s < S; ++s) v = v + p[s * MN];
     const int64_t o = batch_offset(G.bm, 2, bz) + m * G.som + n * G.son;
-    if (G.out_i32) store_int_result(G, G.out, o, n, v);
-    else G.out[o] = G.alpha == 1.0f ? v : v * G.alpha;
+    G.out[o] = G.alpha == 1.0f ? v : v * G.alpha;
   }
 }
 
@@ -713,8 +667,7 @@ __global__ void __launch_bounds__(256) gemm_skinny_kernel(GemmArgs G, int64_t ba
     for (int k = 0; k < kSkinnyK; ++k) {
       a[k] = 0.0f;
       if (k < K) {
-        const float q = load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
-        a[k] = G.adq.active ? dequant_value(q, G.adq, m) : q;
+        a[k] = load_as_f32(G.a, G.a_dt, oa + m * G.a_si + k * G.a_sj);
       }
     }
 #pragma unroll
@@ -833,7 +786,7 @@ static int conv_common(const kk_tensor* out, const kk_tensor* x, const kk_tensor
 }
 
 static int launch_gemm(const GemmArgs& args, int64_t batch) {
-  if (!args.out_i32 && args.N <= kSkinnyN && args.K <= kSkinnyK && args.M * batch >= 4096) {
+  if (args.N <= kSkinnyN && args.K <= kSkinnyK && args.M * batch >= 4096) {
     const int64_t rows = args.M * batch;
     const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(rows, 256), 1 << 16));
     hipLaunchKernelGGL(gemm_skinny_kernel, dim3(grid), dim3(256), 0, ctx().stream, args, batch);
@@ -867,28 +820,21 @@ static int launch_gemm(const GemmArgs& args, int64_t batch) {
   // Vector paths: A fp32 with K contiguous; B with N contiguous; rows (and
   // batch strides) whole 4-element groups, aligned to them.
   const int bsz = dtype_size(args.b_dt);
-  // (uint8 A -- MatMulInteger -- is vectorised only together with int8 B.)
-  const int asz = dtype_size(args.a_dt);
-  bool a_quad = (args.a_dt == KK_F32 || (args.a_dt == KK_U8 && args.b_dt == KK_I8)) &&
-                args.a_sj == 1 && args.K % 4 == 0 && args.a_si % 4 == 0 &&
-                aligned(args.a, 4 * asz);
+  bool a_quad = args.a_dt == KK_F32 && args.a_sj == 1 && args.K % 4 == 0 &&
+                args.a_si % 4 == 0 && aligned(args.a, 16);
   bool b_quad = args.b_sj == 1 && args.N % 4 == 0 && args.b_si % 4 == 0 && aligned(args.b, 4 * bsz);
   for (int d = 0; d < args.bm.nb; ++d) {
     if (args.bm.st[0][d] % 4) a_quad = false;
     if (args.bm.st[1][d] % 4) b_quad = false;
   }
   if (a_quad && b_quad) {
-    if (args.a_dt == KK_U8) {  // MatMulInteger: uint8 activations, int8 weights
-      KK_TILED(gemm_kernel, ts, grid, 0, 0, uint8_t, int8_t);
-    } else {
-      switch (args.b_dt) {
-        case KK_F32: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, float); break;
-        case KK_F16: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, __half); break;
-        case KK_I8: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, int8_t); break;
-        default: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, uint8_t); break;
-      }
+    switch (args.b_dt) {
+      case KK_F32: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, float); break;
+      case KK_F16: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, __half); break;
+      case KK_I8: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, int8_t); break;
+      default: KK_TILED(gemm_kernel, ts, grid, 0, 0, float, uint8_t); break;
     }
-  } else if (a_quad && args.a_dt == KK_F32) {
+  } else if (a_quad) {
     KK_TILED(gemm_kernel, ts, grid, 0, 1, float, float);
   } else if (b_quad) {
     switch (args.b_dt) {
@@ -913,10 +859,8 @@ static int launch_gemm(const GemmArgs& args, int64_t batch) {
 }
 
 
-// Shapes, batch broadcasting and strides of out = a @ w (numpy matmul rules
-// for rank >= 2 operands).  Leaves the dequantisation to the caller.
-static int setup_gemm(GemmArgs* G, const kk_tensor* out, const kk_tensor* a, const kk_tensor* w,
-                      int64_t* batch_out, const char* who) {
+int matmul_shape(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, BatchMap* bm,
+                 int64_t* M_, int64_t* N_, int64_t* K_, int64_t* batch_out, const char* who) {
   KK_TRY(require_ready());
   KK_TRY(check_tensor(out, "out"));
   KK_TRY(check_tensor(a, "a"));
@@ -936,22 +880,32 @@ static int setup_gemm(GemmArgs* G, const kk_tensor* out, const kk_tensor* a, con
   if (a->rank - 2 > nb || w->rank - 2 > nb)
     return set_error(KK_E_ARG, "%s: operand has more batch axes than out", who);
   int64_t batch = 1;
-  G->bm.nb = nb;
+  bm->nb = nb;
   for (int i = 0; i < nb; ++i) {
     const int64_t od = out->shape[i];
-    G->bm.dims[i] = od;
-    G->bm.st[2][i] = out->strides[i];
+    bm->dims[i] = od;
+    bm->st[2][i] = out->strides[i];
     batch *= od;
     const kk_tensor* ops[2] = {a, w};
     for (int k = 0; k < 2; ++k) {
       const int pad = nb - (ops[k]->rank - 2);
-      if (i < pad) { G->bm.st[k][i] = 0; continue; }
+      if (i < pad) { bm->st[k][i] = 0; continue; }
       const int64_t d = ops[k]->shape[i - pad];
-      if (d == od) G->bm.st[k][i] = ops[k]->strides[i - pad];
-      else if (d == 1) G->bm.st[k][i] = 0;
+      if (d == od) bm->st[k][i] = ops[k]->strides[i - pad];
+      else if (d == 1) bm->st[k][i] = 0;
       else return set_error(KK_E_ARG, "%s: batch axis %d does not broadcast", who, i);
     }
   }
+  *M_ = M; *N_ = N; *K_ = K;
+  *batch_out = batch;
+  return KK_OK;
+}
+
+// Shapes, batch broadcasting and strides of out = a @ w (numpy matmul rules
+// for rank >= 2 operands).  Leaves the dequantisation to the caller.
+static int setup_gemm(GemmArgs* G, const kk_tensor* out, const kk_tensor* a, const kk_tensor* w,
+                      int64_t* batch_out, const char* who) {
+  KK_TRY(matmul_shape(out, a, w, &G->bm, &G->M, &G->N, &G->K, batch_out, who));
   G->a = a->data; G->a_dt = a->dtype;
   G->a_si = a->strides[a->rank - 2]; G->a_sj = a->strides[a->rank - 1];
   G->b = w->data; G->b_dt = w->dtype;
@@ -959,15 +913,11 @@ static int setup_gemm(GemmArgs* G, const kk_tensor* out, const kk_tensor* a, con
   G->out = static_cast<float*>(out->data);
   G->som = out->strides[out->rank - 2];
   G->son = out->strides[out->rank - 1];
-  G->M = M; G->N = N; G->K = K;
   G->alpha = 1.0f;
-  *batch_out = batch;
   return KK_OK;
 }
 
-// A zero-point-only shift (scale 1) for the integer ops: per tensor, or per
-// element of `count` when the zero point has that many elements.
-static int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* who) {
+int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* who) {
   *d = Dequant();
   if (!zp) return KK_OK;
   KK_TRY(check_tensor(zp, "zero point"));
@@ -1009,56 +959,6 @@ int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const 
   G.alpha = alpha;
   if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
   if (G.K == 0) return kk_fill(out, 0.0);
-  return launch_gemm(G, batch);
-}
-
-int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
-                      const kk_tensor* a_zp, const kk_tensor* b_zp) {
-  GemmArgs G{};
-  int64_t batch = 0;
-  KK_TRY(setup_gemm(&G, out, a, b, &batch, "kk_matmul_integer"));
-  if (!(a->dtype == KK_U8 || a->dtype == KK_I8) || !(b->dtype == KK_U8 || b->dtype == KK_I8))
-    return set_error(KK_E_ARG, "kk_matmul_integer: a and b must be uint8/int8");
-  if (out->dtype != KK_I32) return set_error(KK_E_ARG, "kk_matmul_integer: out must be int32");
-  KK_TRY(zp_shift(&G.adq, a_zp, 1, "kk_matmul_integer"));
-  KK_TRY(zp_shift(&G.dq, b_zp, G.N, "kk_matmul_integer"));
-  G.out_i32 = 1;
-  if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
-  if (G.K == 0) return kk_fill(out, 0.0);
-  return launch_gemm(G, batch);
-}
-
-int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
-                             const kk_tensor* a_zp, const kk_tensor* b_zp, const kk_tensor* scale,
-                             const kk_tensor* scale2, const kk_tensor* bias) {
-  GemmArgs G{};
-  int64_t batch = 0;
-  KK_TRY(setup_gemm(&G, out, a, b, &batch, "kk_matmul_integer_scaled"));
-  if (!(a->dtype == KK_U8 || a->dtype == KK_I8) || !(b->dtype == KK_U8 || b->dtype == KK_I8))
-    return set_error(KK_E_ARG, "kk_matmul_integer_scaled: a and b must be uint8/int8");
-  if (out->dtype != KK_F32) return set_error(KK_E_ARG, "kk_matmul_integer_scaled: out must be fp32");
-  KK_TRY(zp_shift(&G.adq, a_zp, 1, "kk_matmul_integer_scaled"));
-  KK_TRY(zp_shift(&G.dq, b_zp, G.N, "kk_matmul_integer_scaled"));
-  // scale and bias: one value or one per output column, contiguous fp32
-  auto per_col = [&](const kk_tensor* t, const char* what, const float** p, int64_t* n) -> int {
-    KK_TRY(check_tensor(t, what));
-    if (t->dtype != KK_F32 || !is_contiguous(t))
-      return set_error(KK_E_ARG, "kk_matmul_integer_scaled: %s must be contiguous fp32", what);
-    const int64_t c = numel(t);
-    if (c != 1 && !(c == G.N && t->rank >= 1 && t->shape[t->rank - 1] == G.N))
-      return set_error(KK_E_ARG, "kk_matmul_integer_scaled: %s must hold 1 or N = %lld values", what,
-                       (long long)G.N);
-    *p = static_cast<const float*>(t->data);
-    *n = c;
-    return KK_OK;
-  };
-  if (!scale) return set_error(KK_E_ARG, "kk_matmul_integer_scaled: scale is required");
-  KK_TRY(per_col(scale, "scale", &G.cs, &G.cs_n));
-  if (scale2) KK_TRY(per_col(scale2, "scale2", &G.cs2, &G.cs2_n));
-  if (bias) KK_TRY(per_col(bias, "bias", &G.cb, &G.cb_n));
-  G.out_i32 = 1;
-  if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
-  if (G.K == 0) return set_error(KK_E_UNSUPPORTED, "kk_matmul_integer_scaled: K = 0");
   return launch_gemm(G, batch);
 }
 

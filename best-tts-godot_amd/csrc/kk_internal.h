@@ -21,8 +21,8 @@ struct Context {
   bool capturing = false;  // between kk_graph_begin and kk_graph_end
   // Per-row arrival counters of the multi-block row reductions, zero
   // between launches (the last block of a row resets its counter), then
-  // kFlagSlots flags, also zero between calls (the call that sets one
-  // clears it after reading it).
+  // kFlagSlots per-call slots, each cleared by the call that uses it before
+  // it is set.
   int* row_counters = nullptr;
   // Device scratch owned by the context from kk_init to kk_shutdown, for
   // per-call intermediates that must not be allocated (calls recorded into
@@ -34,7 +34,8 @@ struct Context {
 constexpr size_t kScratchBytes = size_t{16} << 20;
 constexpr int kRowCounters = 65536;
 constexpr int kFlagSlots = 64;
-constexpr int kFlagConvh = 0;  // fp16 matrix-core convolution: an activation out of range
+constexpr int kFlagConvh = 0;     // fp16 matrix-core convolution: a non-finite activation
+constexpr int kFlagConvhMax = 1;  // fp16 matrix-core convolution: max |x| (float bits)
 
 // DynamicQuantizeLinear's byte of x with the scale rounded to fp32 and the
 // zero point as a float: clamp(rint(x / scale) + zp, 0, 255)
@@ -178,6 +179,31 @@ __device__ __forceinline__ float dequant_value(float q, const Dequant& d,
 }
 
 __host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Batch offsets of a batched matmul: up to 6 batch axes with per-operand
+// strides (0 = broadcast).
+struct BatchMap {
+  int nb = 0;
+  int64_t dims[6];
+  int64_t st[3][6];  // 0 = a, 1 = b, 2 = out
+};
+
+__device__ __forceinline__ int64_t batch_offset(const BatchMap& bm, int which, int64_t b) {
+  int64_t off = 0;
+  for (int d = bm.nb - 1; d >= 0; --d) {
+    off += (b % bm.dims[d]) * bm.st[which][d];
+    b /= bm.dims[d];
+  }
+  return off;
+}
+
+// Shapes of out = a @ w under numpy's matmul rules (rank >= 2 operands,
+// batch axes broadcast): fills *bm and M, N, K and the batch count.
+int matmul_shape(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, BatchMap* bm,
+                 int64_t* M, int64_t* N, int64_t* K, int64_t* batch, const char* who);
+// A zero-point-only shift (scale 1) for the integer ops: per tensor, or per
+// element of `count` when the zero point has that many elements.
+int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* who);
 
 
 

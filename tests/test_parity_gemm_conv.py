@@ -311,9 +311,9 @@ def test_fp16_weight_conv_matrix_cores(gpu, oracle, case):
     check(got, want, f"{wdt}-weight {case}")
 
 
-def test_fp16_weight_conv_overflow_falls_back(gpu, oracle):
-    """An activation beyond fp16's range sends the whole convolution to the
-    fp32 kernels (launched after the matrix-core pass, run only if flagged)."""
+def test_fp16_weight_conv_large_activations(gpu, oracle):
+    """Activations far beyond fp16's range: the input is scaled by a power of
+    two before the split, so the matrix-core pass stays exact in range."""
     r = rng(10)
     x = r.normal(0, 1, (1, 256, 2000)).astype(np.float32)
     x[0, 5, 123] = 1.0e5
@@ -322,11 +322,65 @@ def test_fp16_weight_conv_overflow_falls_back(gpu, oracle):
     got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (3, 3),
                                    6).numpy()
     check(got, oracle.conv_transpose1d(x, w, b, (3, 3), 6), "convT with a 1e5 activation")
-    x2 = r.normal(0, 1, (1, 128, 20000)).astype(np.float32)
-    x2[0, 100, 7] = -np.float32(4.0e4)
+    x2 = r.normal(0, 3e8, (1, 128, 20000)).astype(np.float32)
+    x2[0, 100, 7] = -np.float32(4.0e12)
     w2 = r.normal(0, 0.05, (22, 128, 7)).astype(np.float16)
     got = gpu.ops.conv1d(gpu.to_device(x2), gpu.to_device(w2), None, (3, 3)).numpy()
-    check(got, oracle.conv1d(x2, w2, None, (3, 3)), "conv with a -4e4 activation")
+    check(got, oracle.conv1d(x2, w2, None, (3, 3)), "conv with activations ~3e8 and -4e12")
+
+
+@pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
+def test_fp16_weight_conv_nonfinite_falls_back(gpu, oracle, bad):
+    """A non-finite activation sends the whole convolution to the fp32
+    kernels (launched after the matrix-core pass, run only if flagged), which
+    propagate it as numpy does; the next call runs on the matrix cores again."""
+    r = rng(11)
+    x = r.normal(0, 1, (1, 256, 2000)).astype(np.float32)
+    x[0, 5, 123] = bad
+    w = r.normal(0, 0.05, (256, 128, 12)).astype(np.float16)
+    b = r.normal(0, 0.1, 128).astype(np.float32)
+    got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (3, 3),
+                                   6).numpy()
+    with np.errstate(invalid="ignore"):
+        want = oracle.conv_transpose1d(x, w, b, (3, 3), 6)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+    fin = np.isfinite(want)
+    check(np.where(fin, got, 0), np.where(fin, want, 0), f"convT with a {bad} activation")
+    x[0, 5, 123] = 0.5
+    got = gpu.ops.conv_transpose1d(gpu.to_device(x), gpu.to_device(w), gpu.to_device(b), (3, 3),
+                                   6).numpy()
+    check(got, oracle.conv_transpose1d(x, w, b, (3, 3), 6), "convT after the fallback")
+
+
+@pytest.mark.parametrize("sigma", [1e-4, 1e-5, 1e-7])
+@pytest.mark.parametrize("kind", ["conv_i8", "convT_i8", "conv_f16", "convT_f16"])
+def test_fp16_weight_conv_small_activations(gpu, oracle, sigma, kind):
+    """Whole inputs of magnitude 1e-4 .. 1e-7 (a quiet stretch of the vocoder),
+    where an unscaled split's low halves would be fp16 subnormals: held to the
+    same bar as unit-scale inputs.  K = 1536 reductions, as in the 512-channel
+    convolutions."""
+    r = rng(12)
+    if kind.startswith("conv_"):
+        x = r.normal(0, sigma, (1, 512, 600)).astype(np.float32)
+        shape = (256, 512, 3)
+    else:
+        x = r.normal(0, sigma, (1, 512, 120)).astype(np.float32)
+        shape = (512, 256, 20)
+    if kind.endswith("i8"):
+        w, sc = int8_weight(r, shape)
+        wdeq, kw = oracle.dequantize(w, sc), dict(w_scale=gpu.to_device(np.array(sc)))
+    else:
+        w = r.normal(0, 0.05, shape).astype(np.float16)
+        wdeq, kw = w, {}
+    dv = gpu.to_device
+    if kind.startswith("conv_"):
+        got = gpu.ops.conv1d(dv(x), dv(w), None, (1, 1), **kw).numpy()
+        want = oracle.conv1d(x, wdeq, None, (1, 1))
+    else:
+        got = gpu.ops.conv_transpose1d(dv(x), dv(w), None, (5, 5), 10, **kw).numpy()
+        want = oracle.conv_transpose1d(x, wdeq, None, (5, 5), 10)
+    check(got, want, f"{kind} sigma {sigma}")
 
 
 def test_decoder_upsample_stage(gpu, oracle):

@@ -79,13 +79,95 @@ def test_matmul_integer(gpu, oracle):
     ins = [a[:, :10, :512], np.ascontiguousarray(b[:512, :50]), azp, bzp[:50]]
     assert_bitexact(node(gpu, "MatMulInteger", ins), onode(oracle, "MatMulInteger", ins),
                     "MatMulInteger N=50")
-    # the FFN's down projection: K = 2048, so K is split four ways and the
-    # integer partials summed (exactly) in split order
+    # the FFN's down projection: K = 2048
     a2 = r.integers(0, 256, (1, 130, 2048)).astype(np.uint8)
     b2 = r.integers(-127, 128, (2048, 768)).astype(np.int8)
     ins = [a2, b2, azp, bzp[:768]]
     assert_bitexact(node(gpu, "MatMulInteger", ins), onode(oracle, "MatMulInteger", ins),
                     "MatMulInteger K=2048")
+
+
+def brute_matmul_integer(a, b, azp, bzp):
+    """int64 sums, one output at a time, wrapped to int32 as numpy's int32
+    matmul wraps (ref_runtime.py:119-127)."""
+    a = np.asarray(a, np.int64) - (0 if azp is None else int(azp))
+    b = np.asarray(b, np.int64) - (0 if bzp is None else np.asarray(bzp, np.int64).reshape(1, -1))
+    out = np.einsum("mk,kn->mn", a, b)
+    return ((out + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int32)
+
+
+def test_matmul_integer_sums_beyond_fp32(gpu, oracle):
+    """Partial sums far above 2^24, where fp32 accumulation would round: K =
+    2048, all-255 activations (zero point 0), weights +-127 against the
+    opposite extreme of an int8 per-column zero point, so every product is
+    255 * 255 (|sum| = 1.33e8).  Bit-exact against int64 brute force and the
+    oracle."""
+    K, M, N = 2048, 70, 192
+    a = np.full((1, M, K), 255, np.uint8)
+    r = rng(21)
+    sign = r.choice([-1, 1], N)
+    b = np.tile((127 * sign).astype(np.int8), (K, 1))
+    bzp = np.where(sign > 0, -128, 127).astype(np.int8)
+    bzp[:8] = r.integers(-128, 128, 8)  # a few ordinary columns
+    want = brute_matmul_integer(a[0], b, 0, bzp)[None]
+    assert int(np.abs(want.astype(np.int64)).max()) > 2 ** 26
+    assert_bitexact(want, onode(oracle, "MatMulInteger", [a, b, np.uint8(0), bzp]), "oracle")
+    got = node(gpu, "MatMulInteger", [a, b, np.uint8(0), bzp])
+    assert_bitexact(got, want, "MatMulInteger |sum| 1.3e8")
+    # and a random case at the same size, with an extreme activation zero point
+    a = r.integers(0, 256, (1, M, K)).astype(np.uint8)
+    b = r.integers(-128, 128, (K, N)).astype(np.int8)
+    for azp in (np.uint8(0), np.uint8(255)):
+        want = brute_matmul_integer(a[0], b, azp, bzp)[None]
+        assert_bitexact(node(gpu, "MatMulInteger", [a, b, azp, bzp]), want, f"random, a_zp {azp}")
+
+
+@pytest.mark.parametrize("case", ["u8_u8", "i8_i8", "batch_broadcast", "gather_paths", "strided",
+                                  "wraps_mod_2_32"])
+def test_matmul_integer_variants(gpu, oracle, case):
+    """Both byte types on both sides, numpy batch broadcasting, the byte-gather
+    loaders (K not a multiple of 16, N not of 4, strided views) and results
+    beyond int32, which wrap modulo 2^32 as numpy's int32 matmul does."""
+    r = rng(22)
+    if case == "u8_u8":
+        a = r.integers(0, 256, (1, 77, 300)).astype(np.uint8)
+        b = r.integers(0, 256, (300, 130)).astype(np.uint8)
+        azp, bzp = np.uint8(200), np.uint8(3)
+    elif case == "i8_i8":
+        a = r.integers(-128, 128, (65, 512)).astype(np.int8)
+        b = r.integers(-128, 128, (512, 68)).astype(np.int8)
+        azp, bzp = np.int8(-100), r.integers(-128, 128, 68).astype(np.int8)
+    elif case == "batch_broadcast":
+        a = r.integers(0, 256, (2, 3, 40, 96)).astype(np.uint8)
+        b = r.integers(-128, 128, (2, 1, 96, 72)).astype(np.int8)
+        azp, bzp = np.uint8(9), r.integers(-5, 6, 72).astype(np.int8)
+    elif case == "gather_paths":
+        a = r.integers(0, 256, (1, 33, 37)).astype(np.uint8)
+        b = r.integers(-128, 128, (37, 50)).astype(np.int8)
+        azp, bzp = np.uint8(128), r.integers(-128, 128, 50).astype(np.int8)
+    elif case == "strided":
+        # device views: every other column of A (a_sj = 2), and B the
+        # transpose of an [N, K] buffer (b_si = 1, b_sj = K)
+        a_full = r.integers(0, 256, (64, 200)).astype(np.uint8)
+        bt = r.integers(-128, 128, (96, 100)).astype(np.int8)
+        a, b, azp = a_full[:, ::2], bt.T, np.uint8(1)
+        want = brute_matmul_integer(a, b, azp, None)
+        assert_bitexact(onode(oracle, "MatMulInteger", [a, b, azp, None]), want, "oracle")
+        da = gpu.to_device(a_full).slice_axis(1, 0, 200, 2)
+        db = gpu.to_device(bt).transpose((1, 0))
+        got = gpu.to_host(gpu.ops.matmul_integer(da, db, gpu.to_device(np.asarray(azp)), None))
+        assert_bitexact(got, want, "MatMulInteger on strided views")
+        return
+    else:
+        a = np.full((1, 4, 40000), 255, np.uint8)
+        b = np.full((40000, 8), 127, np.int8)
+        azp, bzp = np.uint8(0), np.full(8, -128, np.int8)
+    ins = [a, b, azp, bzp]
+    want = onode(oracle, "MatMulInteger", ins)
+    if a.ndim == 2 and b.ndim == 2:
+        assert_bitexact(want, brute_matmul_integer(a, b, azp, bzp), "oracle vs brute force")
+    got = node(gpu, "MatMulInteger", ins)
+    assert_bitexact(got, want, f"MatMulInteger {case}")
 
 
 @pytest.mark.parametrize("cin,cout,k,L,pad,dil", [(512, 512, 3, 240, 1, 1), (1090, 1024, 3, 40, 1, 1),
@@ -100,6 +182,43 @@ def test_conv_integer(gpu, oracle, cin, cout, k, L, pad, dil):
     got = node(gpu, "ConvInteger", [x, w, xzp, wzp], at)
     assert_bitexact(got, onode(oracle, "ConvInteger", [x, w, xzp, wzp], at),
                     f"ConvInteger {cin}->{cout} k{k}")
+
+
+def brute_conv_integer(x, w, xzp, wzp, pad, dil):
+    """int64 ConvInteger, group 1, stride 1: sum over (ci, k) of
+    (x - xzp)[ci, l + k*dil - pad] * (w - wzp)[co, ci, k], padding 0 after
+    the shift."""
+    xi = np.asarray(x, np.int64)[0] - int(xzp)
+    wi = np.asarray(w, np.int64) - int(wzp)
+    cout, cin, k = wi.shape
+    L = xi.shape[1]
+    xp = np.zeros((cin, L + 2 * pad), np.int64)
+    xp[:, pad:pad + L] = xi
+    lout = L + 2 * pad - dil * (k - 1)
+    out = np.zeros((cout, lout), np.int64)
+    for t in range(k):
+        out += wi[:, :, t] @ xp[:, t * dil:t * dil + lout]
+    return out[None]
+
+
+def test_conv_integer_exact_beyond_2_24(gpu, oracle):
+    """Sums above 2^24: the device is exact int32 (int8 matrix cores), while
+    the reference convolves the shifted integers in float32 and rounds
+    (ref_runtime.py:130-134), which can miss by a few units there.  The
+    device matches int64 brute force bit for bit; the oracle, which restates
+    the reference, stays within float32 rounding of it."""
+    r = rng(23)
+    x = np.full((1, 512, 64), 255, np.uint8)
+    x[0, :, ::7] = r.integers(0, 256, (512, 10))
+    w = r.integers(0, 256, (96, 512, 3)).astype(np.uint8)
+    xzp, wzp = np.uint8(0), np.uint8(255)
+    at = {"pads": [1, 1], "dilations": [1], "strides": [1], "group": 1}
+    exact = brute_conv_integer(x, w, xzp, wzp, 1, 1)
+    assert np.abs(exact).max() > 2 ** 25
+    got = node(gpu, "ConvInteger", [x, w, xzp, wzp], at)
+    assert_bitexact(got, exact.astype(np.int32), "ConvInteger |sum| > 2^25")
+    ref = onode(oracle, "ConvInteger", [x, w, xzp, wzp], at).astype(np.int64)
+    assert np.abs(ref - exact).max() <= 2.0 ** -23 * 1536 * np.abs(exact).max()
 
 
 @pytest.mark.parametrize("case", ["no_zero_points", "int8_weights", "stride2_batch2", "one_output",
