@@ -369,7 +369,7 @@ def run_graph(n_ids, reps):
     download included); the one-time weight upload is not timed."""
     kk = importlib.import_module("best-tts-godot_amd")
     kkg = importlib.import_module("best-tts-godot_amd.graph")
-    g = kkg.load_graph(kkg.default_graph_path())
+    g = kkg.load_graph()
     pg = kkg.PackedGraph(g, kkg.synth_weights(g, 0))
     ids, style, speed = kkg.synth_inputs(n_ids, 0)
     pg.run(ids, style, speed, keep=[2432])  # warm-up: fills the buffer pool
@@ -406,7 +406,7 @@ def run_graph_cpu(n_ids):
     """The oracle's whole-graph walk on a bounded sample (n_ids ids)."""
     from oracle import kpk_run
     kkg = importlib.import_module("best-tts-godot_amd.graph")
-    g = kkg.load_graph(kkg.default_graph_path())
+    g = kkg.load_graph()
     w = kkg.synth_weights(g, 0)
     ids, style, speed = kkg.synth_inputs(n_ids, 0)
     t0 = time.perf_counter()

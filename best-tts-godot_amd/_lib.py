@@ -97,6 +97,9 @@ PROTOTYPES = {
     "kk_pad": [_T, _T, ctypes.POINTER(ctypes.c_int64), _i, _f],
     "kk_cumsum": [_T, _T, _i],
     "kk_scatter_nd": [_T, _T, ctypes.POINTER(ctypes.c_int64), ctypes.c_int64, ctypes.c_int64],
+    "kk_fir": [_T, _T, _T, _i],
+    "kk_pcm16": [_T, _T, _f],
+    "kk_fir_pcm16": [_T, _T, _T, _i, _f],
     "kk_graph_begin": [],
     "kk_graph_end": [ctypes.POINTER(_i)],
     "kk_graph_launch": [_i],

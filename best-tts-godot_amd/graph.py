@@ -6,12 +6,15 @@ executor's memory discipline (executor.gd:190-195, 270-280): every
 intermediate tensor is dropped from `env` after its last use, which returns
 its buffer to libkk's pool.
 
-`load_graph` reads the structure fixture extracted from the reference's
-model.kpk (nodes, ops, shapes, structural constants, per-tensor statistics of
-the learned weights); `synth_weights` draws seeded random learned weights of
-the same dtype, shape and scale, which together give the full
+A model comes from a KPK1 file (`PackedGraph.from_kpk`, the format the
+reference ships its model in, tools/pack_model.py:11-19) or from a graph
+description and its weights.  The package carries the structure of the
+Kokoro-82M graph (`data/kokoro_graph.json.gz`: nodes, ops, shapes, structural
+constants and per-tensor statistics of the learned weights, extracted from
+the reference's model.kpk); `synth_weights` draws seeded random learned
+weights of the same dtype, shape and scale, which together give the full
 Kokoro-82M-architecture graph with random-init weights (int8/uint8 for the
-quantized contractions, fp16 elsewhere).
+quantized contractions, fp16 elsewhere); `synth_model` packs the two.
 """
 import gzip
 import json
@@ -19,31 +22,87 @@ import os
 
 import numpy as np
 
+from . import audio
 from .dispatch import dispatch, to_device, to_host
 from .fuse import fuse as fuse_chains
+from .kpk import CODE_TO_NP, read_kpk
 from .tensor import DeviceTensor
 
-CODE_TO_NP = {0: np.float32, 1: np.int8, 2: np.uint8, 3: np.int32, 4: np.int64, 5: np.bool_,
-              6: np.float16}
+DATA = os.path.join(os.path.dirname(os.path.abspath(__file__)), "data")
 
 
-def load_graph(path):
-    with gzip.open(path, "rt") as f:
+def structure_path():
+    """The packaged structure of the Kokoro-82M graph."""
+    return os.path.join(DATA, "kokoro_graph.json.gz")
+
+
+def load_graph(path=None):
+    """The graph description at `path` (default: the packaged structure)."""
+    with gzip.open(path or structure_path(), "rt") as f:
         return json.load(f)
+
+
+# Three learned tensors of the synthetic model are not drawn at the trained
+# tensors' statistics, so that it produces voiced excitation and an
+# audio-range waveform:
+#  * the pitch head (F0_proj) is a monotone 150 Hz voice: its quantised
+#    weights all equal their zero point (so the conv's sum is exactly 0)
+#    and its bias is 150 Hz.  Drawn at their statistics the weights lack
+#    the trained head's structure and give |F0| < 2 Hz, below the sine
+#    source's voiced threshold: the harmonic source is then a constant whose
+#    STFT frames are all alike, and the generator's instance norms divide a
+#    zero-padding step at the two ends by a near-zero spread -- a 10x edge
+#    transient that sets every quantiser's range behind it.  A random head
+#    at a voiced level does not do either, but its F0 carries the
+#    predictor's quantisation noise (~1e-4 relative between two fp32
+#    implementations), which the sine source integrates over 10^5 samples
+#    and 9 harmonics into phase differences of radians; a constant head
+#    leaves F0 equal to within one quantum of the bias (~2e-5 Hz);
+#  * the generator's output projection (conv_post, whose first 11 channels
+#    are log-magnitudes fed to Exp) is drawn at 1/20 of the trained std:
+#    with random weights the activations reaching it are ~20x the trained
+#    model's (|x| ~ 100 against ~5), which would put the log-magnitudes at
+#    +-50 (exp ~ 1e21); scaled, they stay within +-2.5 and the waveform has
+#    an RMS of ~0.25.
+PITCH_WEIGHT = "encoder.predictor.F0_proj.weight_quantized"
+PITCH_BIAS = ("encoder.predictor.F0_proj.bias", 150.0)
+OUTPUT_HEAD = ("/decoder/decoder/generator/Mul_2_output_0", 1.0 / 20.0)
+
+
+def _zero_point_of(graph, tid):
+    """The constant weight zero point of the ConvInteger / MatMulInteger that
+    reads weight tensor `tid` (input 3), or 0."""
+    for op, ins, _outs, _at, _pl in graph["nodes"]:
+        if graph["ops"][op] in ("ConvInteger", "MatMulInteger") and len(ins) > 1 and ins[1] == tid:
+            if len(ins) > 3 and ins[3] >= 0 and "v" in graph["weights"].get(str(ins[3]), {}):
+                return graph["weights"][str(ins[3])]["v"][0]
+            return 0
+    return 0
 
 
 def synth_weights(graph, seed=0):
     """{tensor id: ndarray}: structural constants exact, learned tensors drawn
     from N(mean, std) of the original tensor, clipped to its [min, max] (and
-    rounded for the integer types), one RNG stream per tensor id."""
+    rounded for the integer types), one RNG stream per tensor id; the pitch
+    head and the output head as stated above."""
     out = {}
+    names = graph.get("tensors", [])
     for tid, w in graph["weights"].items():
         dt = CODE_TO_NP[w["d"]]
         shape = tuple(w["s"])
+        name = names[int(tid)] if int(tid) < len(names) else ""
+        if name == PITCH_BIAS[0]:
+            out[int(tid)] = np.full(shape, PITCH_BIAS[1], dtype=dt)
+            continue
+        if name == PITCH_WEIGHT:
+            out[int(tid)] = np.full(shape, _zero_point_of(graph, int(tid)), dtype=dt)
+            continue
         if "v" in w:
             out[int(tid)] = np.array(w["v"], dtype=dt).reshape(shape)
             continue
         mean, std, lo, hi = w["stat"]
+        if name == OUTPUT_HEAD[0]:
+            mean, std, lo, hi = (v * OUTPUT_HEAD[1] for v in (mean, std, lo, hi))
         r = np.random.default_rng([int(seed), int(tid)])
         v = r.normal(mean, std, shape)
         if np.dtype(dt).kind in "iu":
@@ -83,8 +142,15 @@ class PackedGraph:
     node indices that node k stands for.  Tensors in `protect` stay
     readable after a run (they are never fused away)."""
 
+    @classmethod
+    def from_kpk(cls, path, fuse=True, protect=()):
+        """The model in the KPK1 file at `path` (tools/kpk_runtime.py:27-50)."""
+        desc, weights = read_kpk(path)
+        return cls(desc, weights, fuse=fuse, protect=protect)
+
     def __init__(self, graph, weights, fuse=True, protect=()):
         self.graph = graph
+        self._notch = None  # the notch filter's taps on the device, made on first use
         self.ops = graph["ops"]
         nodes = [(self.ops[op], ["" if t < 0 else str(t) for t in ins],
                   ["" if t < 0 else str(t) for t in outs], _decode_attrs(at))
@@ -135,8 +201,11 @@ class PackedGraph:
         for name, i in self.last_use.items():
             self.frees[i].append(name)
 
-    def run(self, input_ids, style, speed=1.0, keep=()):
-        """Returns the waveform on the host (a numpy array)."""
+    def run(self, input_ids, style, speed=1.0, keep=(), pcm16=False, notch=True, gain=1.0):
+        """Returns the waveform on the host: float32 samples, or with
+        `pcm16` the 16-bit PCM samples (int16) the reference's output stage
+        makes of them on the device (audio.gd:59-106), through the notch
+        filter first unless `notch` is false."""
         env = dict(self.weights)
         env[self.inputs["input_ids"]] = np.asarray(input_ids, np.int64).reshape(1, -1)
         env[self.inputs["style"]] = to_device(np.asarray(style, np.float32).reshape(1, 256))
@@ -153,13 +222,23 @@ class PackedGraph:
                     env.pop(name, None)
         out = env[self.output]
         self.last_env = {k: env[k] for k in keep if k in env}
+        if pcm16:
+            taps = None
+            if notch:
+                if self._notch is None:
+                    self._notch = to_device(audio.notch_taps())
+                taps = self._notch
+            return to_host(audio.to_pcm16(out, taps, gain)).view("<i2")
         return to_host(out)
 
 
-def default_graph_path():
-    here = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    return os.path.join(here, "tests", "golden", "kokoro_graph.json.gz")
+def synth_model(graph=None, seed=0):
+    """(description, {tensor id: ndarray}) of the Kokoro-82M-architecture
+    graph with seeded random learned weights, ready for `kpk.write_kpk`."""
+    graph = graph if graph is not None else load_graph()
+    desc = {k: v for k, v in graph.items() if k not in ("source", "weights")}
+    return desc, synth_weights(graph, seed)
 
 
-__all__ = ["load_graph", "synth_weights", "synth_inputs", "PackedGraph", "DeviceTensor",
-           "default_graph_path"]
+__all__ = ["load_graph", "structure_path", "synth_weights", "synth_model", "synth_inputs",
+           "PackedGraph", "DeviceTensor"]

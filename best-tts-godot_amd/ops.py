@@ -420,3 +420,31 @@ def scatter_nd(data, indices, updates):
               offsets.ctypes.data_as(ctypes.POINTER(ctypes.c_int64)),
               int(len(offsets)), int(inner))
     return out
+
+
+# ------------------------------------------------------ audio output stage
+def fir(x, taps, center=-1):
+    """The notch FIR over the flattened waveform (kernels/fir.glsl:35-47);
+    center < 0: (len(taps) - 1) / 2."""
+    x = x.contiguous()
+    out = DeviceTensor.empty(x.shape, np.float32)
+    _lib.call("kk_fir", out.desc(), x.desc(), taps.contiguous().desc(), int(center))
+    return out
+
+
+def pcm16(x, gain=1.0):
+    """16-bit PCM bytes of the waveform (kernels/pcm16.glsl:28-46): uint8
+    [2 * numel], the little-endian int16 stream."""
+    x = x.contiguous()
+    out = DeviceTensor.empty((2 * x.size,), np.uint8)
+    _lib.call("kk_pcm16", out.desc(), x.desc(), float(gain))
+    return out
+
+
+def fir_pcm16(x, taps, center=-1, gain=1.0):
+    """fir then pcm16 in one pass."""
+    x = x.contiguous()
+    out = DeviceTensor.empty((2 * x.size,), np.uint8)
+    _lib.call("kk_fir_pcm16", out.desc(), x.desc(), taps.contiguous().desc(), int(center),
+              float(gain))
+    return out

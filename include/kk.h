@@ -238,7 +238,8 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale,
                                const kk_tensor* zp, const kk_tensor* x);
 /* MatMulInteger (ref_runtime.py:119-127): int32 (a - a_zp) @ (b - b_zp),
  * a uint8/int8 [.., M, K], b int8/uint8 [.., K, N], a_zp per tensor, b_zp
- * per tensor or per column (either may be NULL). */
+ * per tensor or per column (either may be NULL).  Exact integer
+ * arithmetic modulo 2^32, as numpy's int32 matmul. */
 int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
                       const kk_tensor* a_zp, const kk_tensor* b_zp);
 /* The graph's quantised-linear tail fused into MatMulInteger's epilogue:
@@ -312,6 +313,25 @@ int kk_cumsum(const kk_tensor* out, const kk_tensor* x, int axis);
  * element offsets, distinct and checked against out. */
 int kk_scatter_nd(const kk_tensor* out, const kk_tensor* updates, const int64_t* offsets,
                   int64_t nidx, int64_t inner);
+
+/* -------------------------------------------------- audio output stage
+ * The product's output stage, KokoroAudio.stream_from_gpu
+ * (addons/best-tts/runtime/audio.gd:59-106).
+ * Notch FIR (kernels/fir.glsl:35-47): out[i] = sum_k taps[k] *
+ * x[clamp(i - center + k, 0, n - 1)] over the flattened waveform, each
+ * output's taps accumulated in order in fp32; center < 0 selects
+ * (taps - 1) / 2, as audio.gd passes it.  x and out contiguous fp32 of equal
+ * size, 16-byte aligned; 1 <= taps <= 4096. */
+int kk_fir(const kk_tensor* out, const kk_tensor* x, const kk_tensor* taps, int center);
+/* 16-bit PCM (kernels/pcm16.glsl:28-46): sample i becomes
+ * round(clamp(x[i] * gain, -1, 1) * 32767) as int16 (a .5 tie rounds away
+ * from zero), stored as the little-endian byte stream the reference reads
+ * back: out_bytes uint8 with 2 * numel(x) elements, 16-byte aligned. */
+int kk_pcm16(const kk_tensor* out_bytes, const kk_tensor* x, float gain);
+/* kk_fir followed by kk_pcm16 in one pass (the FIR's fp32 result never
+ * reaches memory), as audio.gd:76-99 applies them in turn. */
+int kk_fir_pcm16(const kk_tensor* out_bytes, const kk_tensor* x, const kk_tensor* taps,
+                 int center, float gain);
 
 /* -------------------------------------------------------------- timing
  * HIP events on the library stream, for measuring kernels where they run.

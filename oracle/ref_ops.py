@@ -44,6 +44,19 @@ see tests/test_oracle.py):
   pad                     -- torch.nn.functional.pad (reflect/replicate/
                              constant).
   scatter_nd, CumSum      -- loops; integer prefix sums in closed form.
+  (tests/test_oracle_audio.py:)
+  notch_taps              -- scipy.signal.firwin's Blackman band-pass designs
+                             (an impulse minus one per tone), symmetry, the
+                             frequency response (>= 40 dB nulls at 4800 and
+                             9600 Hz, < 0.1 dB elsewhere); planted mistakes
+                             (Hamming window, a missing tone, half the
+                             bandwidth) fail the comparison.
+  fir                     -- np.correlate of the edge-clamped signal, brute
+                             force on tiny inputs, impulse response = taps,
+                             DC gain = sum of the taps.
+  pcm16                   -- known answers (clamp, rounding, byte order);
+                             .5 ties round away from zero, which GLSL leaves
+                             open: ties are parity unpinned.
 """
 import numpy as np
 
@@ -440,6 +453,64 @@ def scatter_nd(data, indices, updates):
     for i in range(flat.shape[0]):
         out[tuple(flat[i])] = upd[i]
     return out
+
+
+# ------------------------------------------------- audio output stage
+def notch_taps(sample_rate=24000, tones=(4800.0, 9600.0), bw=80.0, n=1023):
+    """KokoroAudio.notch_taps (runtime/audio.gd:30-45): an impulse at the
+    centre tap c = (n - 1) // 2 minus one Blackman-windowed sinc band-pass
+    [f0 - bw, f0 + bw] per tone.  GDScript computes in double and stores in a
+    PackedFloat32Array, so each tone's subtraction is rounded to float32."""
+    k = np.arange(n, dtype=np.float64)
+    c = (n - 1) // 2
+    m = k - c
+    taps = np.zeros(n, F32)
+    taps[c] = 1.0
+    two_pi = 2.0 * np.pi
+
+    def sinc(x):
+        out = np.ones_like(x)
+        big = np.abs(x) >= 1e-9
+        out[big] = np.sin(np.pi * x[big]) / (np.pi * x[big])
+        return out
+
+    w = 0.42 - 0.5 * np.cos(two_pi * k / (n - 1)) + 0.08 * np.cos(2.0 * two_pi * k / (n - 1))
+    for f0 in tones:
+        f1 = (f0 - bw) / sample_rate
+        f2 = (f0 + bw) / sample_rate
+        band = (2.0 * f2 * sinc(2.0 * f2 * m) - 2.0 * f1 * sinc(2.0 * f1 * m)) * w
+        taps = (taps.astype(np.float64) - band).astype(F32)
+    return taps
+
+
+def fir(x, h, center=None):
+    """The notch FIR of kernels/fir.glsl:35-47 over one waveform:
+    y[i] = sum_k h[k] * x[clamp(i - center + k, 0, n - 1)], the taps summed
+    in order in float32 (edges clamp to the first and last sample; center
+    defaults to (taps - 1) / 2, as audio.gd:72-76 passes it)."""
+    x = np.asarray(x, F32).reshape(-1)
+    h = np.asarray(h, F32).reshape(-1)
+    n, t = x.size, h.size
+    c = (t - 1) // 2 if center is None else int(center)
+    if n == 0:
+        return x.copy()
+    xp = x[np.clip(np.arange(-c, n - c + t - 1), 0, n - 1)]
+    acc = np.zeros(n, F32)
+    for k in range(t):
+        acc = acc + h[k] * xp[k:k + n]
+    return acc
+
+
+def pcm16(x, gain=1.0):
+    """16-bit PCM of a waveform (kernels/pcm16.glsl:28-46 as audio.gd:59-106
+    drives it): round(clamp(x * gain, -1, 1) * 32767) as int16, the
+    little-endian pairs of the GLSL being the int16 stream itself.  GLSL's
+    round() leaves the direction of a .5 tie to the implementation; here a
+    tie rounds away from zero (so ties are parity unpinned)."""
+    v = np.asarray(x, F32) * F32(gain)
+    c = np.minimum(np.maximum(v, F32(-1.0)), F32(1.0))
+    s = (c * F32(32767.0)).astype(np.float64)
+    return (np.sign(s) * np.floor(np.abs(s) + 0.5)).astype(np.int16)
 
 
 # ------------------------------------------------------------------ pool

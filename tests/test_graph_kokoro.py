@@ -1,16 +1,30 @@
-"""The full Kokoro-82M-architecture graph (the reference's packed graph
-structure with seeded random learned weights) run node by node through the
-drop-in dispatch on the GPU, against checkpoints the CPU oracle computed for
-the same weights and inputs (tests/golden/graph_golden_t8.npz, written by
+"""The full Kokoro-82M-architecture graph (the packaged graph structure with
+seeded random learned weights, loaded from a KPK1 file written by the
+product's packer) run node by node through the drop-in dispatch on the GPU,
+against checkpoints the CPU oracle computed for the same weights and inputs
+(tests/golden/graph_golden_t8.npz, written by
 tests/golden/make_graph_golden.py).
 
-Bars: the integer durations bit-exact (they set the output length), the
-pre-round durations and the text LSTM within rel 1e-4; the STFT of the
-harmonic source within the reference's own GPU-vs-numpy tap gate -- relative
-RMS 0.05 (tests/test_taps.gd:19-26) -- with non-finite values counted
-explicitly; every node of the graph, teacher-forced from the oracle's inputs,
-bit-exact for integer outputs and within rel 1e-4 (+1e-5 max) for floats;
-run-to-run identical bits."""
+Bars:
+  * the integer durations bit-exact (they set the output length), the
+    pre-round durations and the text LSTM within rel 1e-4;
+  * every stored checkpoint of the free-running run within the reference's
+    own GPU-vs-numpy tap gate (tests/test_taps.gd:19-26, 118-140): peak-
+    relative error <= 0.2 and relative RMS <= 0.05, non-finite values
+    counted explicitly;
+  * the free-running waveform within the reference's own waveform gate
+    (tests/test_executor.gd:79-100): SNR >= 10 dB and RMSE <= 0.02;
+  * every node of the graph, teacher-forced from the oracle's inputs,
+    bit-exact for integer outputs and within rel 1e-4 (+1e-5 max) for
+    floats, at 3 and at 8 phoneme ids;
+  * run-to-run identical bits (tests/test_repeat.gd:97-112).
+Free-running, the two sides differ by fp32 summation order only, which the
+graph's 26 dynamic int8 re-quantisations amplify (a value on a rounding
+boundary moves by a whole quantum): measured at 8 ids, relative RMS 1.3e-5
+after the shared LSTM, 3e-3 at the decoder's input, 1.6e-2 after decode.0,
+4.6e-2 after decode.3, 7.8e-2 after ups.0; the harmonic source's excitation
+then dominates and conv_post is at 9e-4, the waveform at 1.7e-3 (SNR 55 dB,
+RMSE 4e-4)."""
 import importlib
 import os
 
@@ -21,6 +35,7 @@ from conftest import assert_close
 
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
+CHECKPOINTS = [2430, 2432, 1165, 2892, 3037, 3304, 5038]
 
 
 def rel_rms(got, want):
@@ -31,13 +46,29 @@ def rel_rms(got, want):
     return float(np.sqrt(((got - want) ** 2).mean()) / max(np.sqrt((want ** 2).mean()), 1e-30))
 
 
+def tap_gate(got, want, what):
+    """tests/test_taps.gd:118-140: no non-finite values, max|err| <= 0.2
+    max|ref|, relative RMS <= 0.05."""
+    got = np.asarray(got, np.float64).reshape(-1)
+    want = np.asarray(want, np.float64).reshape(-1)
+    assert got.shape == want.shape, f"{what}: size {got.shape} != {want.shape}"
+    assert np.isfinite(got).all(), f"{what}: {int((~np.isfinite(got)).sum())} non-finite values"
+    worst = float(np.abs(got - want).max())
+    scale = max(1e-9, float(np.abs(want).max()))
+    rr = float(np.sqrt(((got - want) ** 2).sum() / max(1e-30, (want ** 2).sum())))
+    assert worst / scale <= 0.2 and rr <= 0.05, f"{what}: max|err|/scale {worst / scale:.3g}, relRMS {rr:.3g}"
+    return rr
+
+
 @pytest.fixture(scope="module")
-def run8(gpu):
+def run8(gpu, tmp_path_factory):
     kkg = importlib.import_module("best-tts-godot_amd.graph")
+    kpk = importlib.import_module("best-tts-godot_amd.kpk")
     gold = np.load(os.path.join(HERE, "golden", "graph_golden_t8.npz"))
-    g = kkg.load_graph(kkg.default_graph_path())
-    pg = kkg.PackedGraph(g, kkg.synth_weights(g, 0))
-    wav = pg.run(gold["ids"], gold["style"], 1.0, keep=[2430, 2432, 1165, 3037])
+    path = str(tmp_path_factory.mktemp("kpk") / "synthetic.kpk")
+    kpk.write_kpk(path, *kkg.synth_model(seed=0))
+    pg = kkg.PackedGraph.from_kpk(path, protect=CHECKPOINTS)
+    wav = pg.run(gold["ids"], gold["style"], 1.0, keep=CHECKPOINTS)
     caps = {k: gpu.to_host(v) for k, v in pg.last_env.items()}
     return gold, wav, caps, pg
 
@@ -54,16 +85,46 @@ def test_text_lstm(run8):
     assert_close(caps["1165"], gold["t1165"], 1e-4, floor_rel=1e-5, what="text LSTM")
 
 
-def test_harmonic_stft_and_waveform(run8):
-    """The STFT of the harmonic source within the reference's tap gate; the
-    free-running waveform only for its length and finiteness.  Its samples
-    (and even its level: the random-weight decoder reaches RMS ~1e15, and a
-    change of summation order in one reduction moves that by several times)
-    are checked node by node in the teacher-forced test instead."""
-    gold, wav, caps, _ = run8
-    assert rel_rms(caps["3037"], gold["t3037"]) < 0.05
-    wav = wav.reshape(-1)
-    assert wav.size == int(gold["wave_len"]) and np.isfinite(wav).all()
+def test_free_running_checkpoints(run8):
+    """The reference's tap gate on every stored checkpoint: the F0 curve, the
+    harmonic source's STFT, decoder block decode.0 and conv_post (stored as
+    their leading frames)."""
+    gold, _, caps, _ = run8
+    for k in (2892, 3037, 3304, 5038):
+        want = gold[f"t{k}"]
+        got = np.asarray(caps[str(k)])
+        axis = {3037: 1}.get(k, got.ndim - 1)
+        got = np.take(got, np.arange(want.shape[axis]), axis=axis)
+        tap_gate(got, want, f"checkpoint {k}")
+
+
+def test_free_running_waveform(run8):
+    """The reference's waveform gate (tests/test_executor.gd:79-100): SNR >=
+    10 dB and RMSE <= 0.02 against the oracle's waveform for the same
+    weights and inputs."""
+    gold, wav, _, _ = run8
+    want = gold["wave_f16"].astype(np.float64)
+    got = np.asarray(wav, np.float64).reshape(-1)
+    assert got.size == want.size and np.isfinite(got).all()
+    rmse = float(np.sqrt(((got - want) ** 2).mean()))
+    snr = 20.0 * np.log10(np.sqrt((want ** 2).mean()) / max(rmse, 1e-20))
+    assert snr >= 10.0 and rmse <= 0.02, f"SNR {snr:.1f} dB, RMSE {rmse:.3g}"
+    assert np.sqrt((want ** 2).mean()) > 0.05  # an audio-range signal, not silence
+
+
+def test_pcm16_output(run8, gpu, oracle):
+    """The output stage on the device (notch FIR + PCM16, audio.gd:59-106)
+    against the oracle's FIR and PCM16 of the same waveform: samples equal,
+    or one step apart where the FIR's fp32 sums (fused multiply-adds on the
+    device, separate roundings in the oracle) straddle a rounding boundary."""
+    gold, wav, _, pg = run8
+    pcm = pg.run(gold["ids"], gold["style"], 1.0, pcm16=True)
+    assert pcm.dtype == np.int16 and pcm.size == wav.size
+    want = oracle.pcm16(oracle.fir(wav, oracle.notch_taps()))
+    d = np.abs(pcm.astype(np.int64) - want.astype(np.int64))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3, (int(d.max()), float((d > 0).mean()))
+    raw = pg.run(gold["ids"], gold["style"], 1.0, pcm16=True, notch=False, gain=0.5)
+    np.testing.assert_array_equal(raw, oracle.pcm16(wav, 0.5).reshape(-1))
 
 
 def _node_close(got, want, quant_of_sin=False):
@@ -99,7 +160,8 @@ def _node_close(got, want, quant_of_sin=False):
     return None
 
 
-def test_every_node_teacher_forced(gpu, oracle):
+@pytest.mark.parametrize("n_ids,speed", [(3, 2.0), (8, 1.0)])
+def test_every_node_teacher_forced(gpu, oracle, n_ids, speed):
     """Every node of the (fused) graph run on the GPU with the oracle's exact
     inputs (placed on host or device as the free-running GPU walk places
     them) and checked against the oracle's value of each of its outputs.  A
@@ -112,10 +174,13 @@ def test_every_node_teacher_forced(gpu, oracle):
     whole quantum) and through sin() of the accumulated F0 phase, so two
     correct fp32 implementations give uncorrelated waveforms.  This test
     removes that amplification: every node starts from the same inputs.
-    3 phoneme ids at speed 2.0 keep the CPU oracle near 15 s."""
+    3 ids at speed 2.0 keep the CPU oracle near 15 s; 8 ids at speed 1.0
+    give the generator rows of 120 F > 16384 samples, so the long-row
+    kernels (multi-block numpy-order statistics, InstanceNormQuant's
+    long-row passes) run inside the graph too."""
     kkg = importlib.import_module("best-tts-godot_amd.graph")
     kpk_run = importlib.import_module("oracle.kpk_run")
-    g = kkg.load_graph(kkg.default_graph_path())
+    g = kkg.load_graph()
     w = kkg.synth_weights(g, 0)
     pg = kkg.PackedGraph(g, w)
     assert len(pg.nodes) < len(g["nodes"])  # the fusion pass ran
@@ -132,18 +197,20 @@ def test_every_node_teacher_forced(gpu, oracle):
     for k, (_op, ins, _outs, _at) in enumerate(pg.nodes):
         for n in ins:
             last[n] = max(last.get(n, -1), pg.groups[k][-1])
-    ids, style, _ = kkg.synth_inputs(3, 1)
+    ids, style, _ = kkg.synth_inputs(n_ids, 1)
     oenv = {str(k): v for k, v in w.items()}
     oenv[pg.inputs["input_ids"]] = np.asarray(ids, np.int64).reshape(1, -1)
     oenv[pg.inputs["style"]] = np.asarray(style, np.float32).reshape(1, 256)
-    oenv[pg.inputs["speed"]] = np.asarray([2.0], np.float32)
+    oenv[pg.inputs["speed"]] = np.asarray([speed], np.float32)
     on_device = {pg.inputs["input_ids"]: False, pg.inputs["style"]: True, pg.inputs["speed"]: True}
-    failures, counted = [], 0
+    failures, counted, longest = [], 0, 0
     for i, (op, ins, outs, at) in enumerate(orig):
         oracle.dispatch(op, ins, outs, at, oenv)
         if i in ends:
             k = ends[i]
             gop, gins, gouts, gat = pg.nodes[k]
+            if gop.startswith("InstanceNorm"):
+                longest = max(longest, int(np.asarray(oenv[gins[0]]).shape[-1]))
             genv = {}
             for n in gins:
                 if not n or n in genv:
@@ -166,6 +233,8 @@ def test_every_node_teacher_forced(gpu, oracle):
             if n and last.get(n) == i and n not in pg.weights:
                 oenv.pop(n, None)
     assert counted == sum(1 for n in pg.nodes for o in n[2] if o)
+    if n_ids == 8:
+        assert longest > 16384, longest  # the long-row paths ran
     assert not failures, f"{len(failures)} node outputs differ:\n" + "\n".join(failures[:20])
 
 

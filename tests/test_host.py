@@ -137,7 +137,7 @@ def test_unknown_op_raises():
 def _graph_nodes():
     import importlib
     kkg = importlib.import_module("best-tts-godot_amd.graph")
-    g = kkg.load_graph(kkg.default_graph_path())
+    g = kkg.load_graph()
     nodes = [(g["ops"][op], ["" if t < 0 else str(t) for t in ins],
               ["" if t < 0 else str(t) for t in outs], kkg._decode_attrs(at))
              for op, ins, outs, at, _pl in g["nodes"]]

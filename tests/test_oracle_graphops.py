@@ -15,7 +15,7 @@ import torch.nn.functional as F
 
 from conftest import ROOT
 
-GRAPH = os.path.join(ROOT, "tests", "golden", "kokoro_graph.json.gz")
+GRAPH = os.path.join(ROOT, "best-tts-godot_amd", "data", "kokoro_graph.json.gz")
 
 
 # ------------------------------------------------ DynamicQuantizeLinear
