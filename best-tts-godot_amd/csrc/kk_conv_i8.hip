@@ -350,6 +350,50 @@ static int conv_tile_n(int64_t stride, int64_t dilation, int64_t K) {
   return 0;
 }
 
+// The allocation-free entry point's workspace: a file-scope device array of
+// a fixed size (2.4x the largest the Kokoro graph's convolutions need,
+// 3.4 MiB), which each device holds from the library's first use of it until
+// the process ends.  Its host-side name is only a stand-in for the symbol:
+// the device address comes from hipGetSymbolAddress, taken once per device
+// by conv_i8_scratch_setup (called from kk_init with the device current) and
+// kept in g_scratch; kernels and copies only ever see that address.
+constexpr size_t kNoAllocBytes = size_t{8} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+constexpr int kMaxDevices = 64;
+static void* g_scratch[kMaxDevices];
+
+int conv_i8_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(KK_E_UNSUPPORTED, "device %d beyond the %d the library tracks", device,
+                     kMaxDevices);
+  if (g_scratch[device]) return KK_OK;
+  void* p = nullptr;
+  KK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+  if (!p) return set_error(KK_E_HIP, "hipGetSymbolAddress gave no address for the conv scratch");
+  g_scratch[device] = p;
+  return KK_OK;
+}
+
+// Byte offsets of a call's workspace: the re-laid weights wT, then four
+// per-channel int32/fp32 arrays (weight sums, offset zero points, scale,
+// quantised bias), each 256-byte aligned.
+struct ConvWs {
+  int64_t wT, wsum, wzo, qs, qb, total;
+};
+static ConvWs conv_ws_layout(int64_t Cout, int64_t Cin, int64_t Kw) {
+  const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
+  const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
+  auto up = [](int64_t n) { return ceil_div(n, 256) * 256; };
+  ConvWs L{};
+  L.wT = 0;
+  L.wsum = L.wT + up(CoutP * Kw * CinP);
+  L.wzo = L.wsum + up(CoutP * 4);
+  L.qs = L.wzo + up(CoutP * 4);
+  L.qb = L.qs + up(CoutP * 4);
+  L.total = L.qb + up(CoutP * 4);
+  return L;
+}
+
 // Shapes and zero points of ConvInteger (ref_runtime.py:130-134); fills
 // *Lout.  Both zero points must be per tensor, as the reference reads them
 // with np.int32(zp).
@@ -409,34 +453,33 @@ static int check_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk
   return KK_OK;
 }
 
-// Both entry points: `outf` set gives the scaled fp32 form.
+// Every entry point: `outf` set gives the scaled fp32 form; `fixed_ws`, when
+// given, is the workspace (conv_ws_layout(...).total bytes, checked by the
+// caller) instead of one from the pool.
 static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
                      const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
                      const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
                      bool outf, const kk_tensor* qb_sa = nullptr, const kk_tensor* qb_sw = nullptr,
-                     const kk_tensor* qb_bias = nullptr) {
+                     const kk_tensor* qb_bias = nullptr, void* fixed_ws = nullptr) {
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], Kw = w->shape[2];
   const int64_t Lout = out->shape[2];
   const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
   const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
-  auto up = [](int64_t n) { return ceil_div(n, 256) * 256; };
-  const int64_t o_wT = 0, o_wsum = o_wT + up(CoutP * Kw * CinP);
-  const int64_t o_wzo = o_wsum + up(CoutP * 4), o_qs = o_wzo + up(CoutP * 4);
-  const int64_t o_qb = o_qs + up(CoutP * 4), total = o_qb + up(CoutP * 4);
-  void* ws = nullptr;
-  KK_TRY(kk_alloc(static_cast<size_t>(total), &ws));
+  const ConvWs lay = conv_ws_layout(Cout, Cin, Kw);
+  void* ws = fixed_ws;
+  if (!ws) KK_TRY(kk_alloc(static_cast<size_t>(lay.total), &ws));
   char* base = static_cast<char*>(ws);
-  int8_t* wT = reinterpret_cast<int8_t*>(base + o_wT);
-  int32_t* wsum = reinterpret_cast<int32_t*>(base + o_wsum);
-  int32_t* wzo = reinterpret_cast<int32_t*>(base + o_wzo);
+  int8_t* wT = reinterpret_cast<int8_t*>(base + lay.wT);
+  int32_t* wsum = reinterpret_cast<int32_t*>(base + lay.wsum);
+  int32_t* wzo = reinterpret_cast<int32_t*>(base + lay.wzo);
   QBias qb{};
   if (qb_sa) {
     qb.sa = static_cast<const float*>(qb_sa->data);
     qb.sw = static_cast<const float*>(qb_sw->data);
     qb.bias = static_cast<const float*>(qb_bias->data);
-    qb.scale = reinterpret_cast<float*>(base + o_qs);
-    qb.ibias = reinterpret_cast<int32_t*>(base + o_qb);
+    qb.scale = reinterpret_cast<float*>(base + lay.qs);
+    qb.ibias = reinterpret_cast<int32_t*>(base + lay.qb);
   }
   hipStream_t st = ctx().stream;
   hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
@@ -472,7 +515,7 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     else hipLaunchKernelGGL(conv_i8_kernel<64>, grid, dim3(256), conv_lds(A.W4), st, A);
     rc = check_launch("conv_i8_kernel");
   }
-  kk_free(ws);  // stream order keeps the workspace alive for the kernels
+  if (!fixed_ws) kk_free(ws);  // stream order keeps the workspace alive for the kernels
   return rc;
 }
 
@@ -517,29 +560,70 @@ int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_te
   return conv_integer_run(out, x, w, x_zp, w_zp, bias, scale, stride, dilation, pad0, pad1, true);
 }
 
-int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
-                                 const kk_tensor* x_zp, const kk_tensor* w_zp,
-                                 const kk_tensor* bias, const kk_tensor* scale_a,
-                                 const kk_tensor* scale_w, int stride, int dilation, int pad0,
-                                 int pad1, int group) {
+}  // extern "C"
+
+// The checks of kk_conv_integer_scaled_qbias (and its allocation-free form):
+// KK_OK to run, or an error; *empty when there is nothing to compute.
+static int check_qbias(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                       const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                       const kk_tensor* scale_a, const kk_tensor* scale_w, int stride, int dilation,
+                       int pad0, int pad1, int group, const char* who, bool* empty) {
   int64_t Lout = 0;
   KK_TRY(check_conv_integer(out, x, w, x_zp, w_zp, stride, dilation, pad0, pad1, group, KK_F32,
-                            "kk_conv_integer_scaled_qbias", &Lout));
+                            who, &Lout));
   const int64_t Cout = w->shape[0];
   const kk_tensor* one[2] = {scale_a, scale_w};
   for (const kk_tensor* t : one) {
     KK_TRY(check_tensor(t, "scale"));
     if (t->dtype != KK_F32 || numel(t) != 1)
-      return set_error(KK_E_ARG, "kk_conv_integer_scaled_qbias: scale_a and scale_w are one fp32 each");
+      return set_error(KK_E_ARG, "%s: scale_a and scale_w are one fp32 each", who);
   }
   KK_TRY(check_tensor(bias, "bias"));
   if (bias->dtype != KK_F32 || !is_contiguous(bias) || numel(bias) != Cout)
-    return set_error(KK_E_ARG, "kk_conv_integer_scaled_qbias: bias must be fp32 with Cout values");
-  if (numel(out) == 0) return KK_OK;
-  if (x->shape[1] * w->shape[2] == 0)
-    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer_scaled_qbias: empty reduction");
+    return set_error(KK_E_ARG, "%s: bias must be fp32 with Cout values", who);
+  *empty = numel(out) == 0;
+  if (!*empty && x->shape[1] * w->shape[2] == 0)
+    return set_error(KK_E_UNSUPPORTED, "%s: empty reduction", who);
+  return KK_OK;
+}
+
+extern "C" {
+
+int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                                 const kk_tensor* x_zp, const kk_tensor* w_zp,
+                                 const kk_tensor* bias, const kk_tensor* scale_a,
+                                 const kk_tensor* scale_w, int stride, int dilation, int pad0,
+                                 int pad1, int group) {
+  bool empty = false;
+  KK_TRY(check_qbias(out, x, w, x_zp, w_zp, bias, scale_a, scale_w, stride, dilation, pad0, pad1,
+                     group, "kk_conv_integer_scaled_qbias", &empty));
+  if (empty) return KK_OK;
   return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
                           true, scale_a, scale_w, bias);
+}
+
+int kk_conv_integer_scaled_qbias_noalloc(const kk_tensor* out, const kk_tensor* x,
+                                         const kk_tensor* w, const kk_tensor* x_zp,
+                                         const kk_tensor* w_zp, const kk_tensor* bias,
+                                         const kk_tensor* scale_a, const kk_tensor* scale_w,
+                                         int stride, int dilation, int pad0, int pad1, int group) {
+  const char* who = "kk_conv_integer_scaled_qbias_noalloc";
+  bool empty = false;
+  KK_TRY(check_qbias(out, x, w, x_zp, w_zp, bias, scale_a, scale_w, stride, dilation, pad0, pad1,
+                     group, who, &empty));
+  const ConvWs lay = conv_ws_layout(w->shape[0], w->shape[1], w->shape[2]);
+  if (lay.total > static_cast<int64_t>(kNoAllocBytes))
+    return set_error(KK_E_UNSUPPORTED,
+                     "%s: Cout %lld x Cin %lld x K %lld needs a %lld-byte workspace, beyond the "
+                     "%zu bytes of the allocation-free scratch", who, (long long)w->shape[0],
+                     (long long)w->shape[1], (long long)w->shape[2], (long long)lay.total,
+                     kNoAllocBytes);
+  const int dev = ctx().device;
+  if (dev < 0 || dev >= kMaxDevices || !g_scratch[dev])
+    return set_error(KK_E_STATE, "%s: the scratch of device %d is not set up", who, dev);
+  if (empty) return KK_OK;
+  return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
+                          true, scale_a, scale_w, bias, g_scratch[dev]);
 }
 
 }  // extern "C"

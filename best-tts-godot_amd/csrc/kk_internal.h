@@ -53,6 +53,9 @@ __device__ __forceinline__ uint32_t dql_byte(float x, float sc, float z) {
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
                     uint8_t* zp_out, const int* only_if = nullptr, int* clear = nullptr);
 Context& ctx();
+// Takes the device address of the allocation-free convolution's file-scope
+// scratch for `device` (current), once per device (kk_conv_i8.hip).
+int conv_i8_scratch_setup(int device);
 
 // Thread-local last error; set_error returns `code` so call sites can
 // `return set_error(KK_E_ARG, "...")`.

@@ -379,6 +379,7 @@ int kk_init(int device) {
                    sizeof(int) * (kRowCounters + kFlagSlots)));
   KK_HIP(hipMemset(c.row_counters, 0, sizeof(int) * (kRowCounters + kFlagSlots)));
   KK_HIP(hipMalloc(&c.scratch, kScratchBytes));
+  KK_TRY(conv_i8_scratch_setup(device));
   c.device = device;
   c.ready = true;
   return KK_OK;

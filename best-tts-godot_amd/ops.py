@@ -275,17 +275,20 @@ def conv_integer_scaled(x, w, x_zp, w_zp, bias, scale, pads=(0, 0), stride=1, di
 
 
 def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0, 0), stride=1,
-                              dilation=1, group=1):
+                              dilation=1, group=1, noalloc=False):
     """conv_integer_scaled with its int32 bias and scale formed in the same
     launch sequence: scale = scale_a * scale_w, bias_int32 =
-    int32(floor(bias / scale)) (bias fp32 [Cout], the scales one value each)."""
+    int32(floor(bias / scale)) (bias fp32 [Cout], the scales one value each).
+    With `noalloc` the library allocates nothing for the call (its workspace
+    is a fixed device array); the output is still allocated here."""
     x = x.contiguous()
     w = w.contiguous()
     n, _, L = x.shape
     cout, _, k = w.shape
     lout = (L + pads[0] + pads[1] - dilation * (k - 1) - 1) // stride + 1
     out = DeviceTensor.empty((n, cout, max(lout, 0)), np.float32)
-    _lib.call("kk_conv_integer_scaled_qbias", out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
+    entry = "kk_conv_integer_scaled_qbias_noalloc" if noalloc else "kk_conv_integer_scaled_qbias"
+    _lib.call(entry, out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
               bias.contiguous().desc(), scale_a.contiguous().desc(), scale_w.contiguous().desc(),
               int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
     return out

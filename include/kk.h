@@ -281,6 +281,23 @@ int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const
                                  const kk_tensor* scale_w, int stride, int dilation, int pad0,
                                  int pad1, int group);
 
+/* kk_conv_integer_scaled_qbias without any allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The same checks, kernels and results; the per-call workspace
+ * (the re-laid weights and per-channel constants, normally from the pool)
+ * lives in a fixed 8 MiB device array that each GPU holds from kk_init to the
+ * end of the process.  A convolution whose workspace exceeds it
+ * (CoutP * K * CinP + 4 * CoutP * 4 bytes, CoutP = Cout rounded up to 128,
+ * CinP = Cin rounded up to 64; the Kokoro graph's largest is 3.4 MiB) is
+ * rejected with KK_E_UNSUPPORTED.  Every call on a GPU shares that array:
+ * calls that overlap on one GPU (e.g. from other streams or threads) race. */
+int kk_conv_integer_scaled_qbias_noalloc(const kk_tensor* out, const kk_tensor* x,
+                                         const kk_tensor* w, const kk_tensor* x_zp,
+                                         const kk_tensor* w_zp, const kk_tensor* bias,
+                                         const kk_tensor* scale_a, const kk_tensor* scale_w,
+                                         int stride, int dilation, int pad0, int pad1, int group);
+
 /* ------------------------------------------------ recurrent / vocoder
  * DynamicQuantizeLSTM as op_lstm computes it without activation
  * quantisation (ref_runtime.py:137-210): W int8 [dir, input, 4H] and R int8
