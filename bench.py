@@ -232,15 +232,25 @@ def run_gpu(args):
         log(f"bench: {name:<28} {json.dumps(rec)}")
         return rec
 
-    # A plain fp32 copy of the AdaIN T=9600 input: the achievable bandwidth
-    # at this size, and the calibration kernel for the HBM byte counters.
-    copy_bytes = 2 * 512 * 9600 * 4
-    cp = per_op("copy_512x9600", lambda i: B.call("kk_copy", outs["x9600"][i].desc(),
-                                                  xs["x9600"][i].desc()), copy_bytes)
-    per_op("adain_t1200", lambda i: op_adain("x1200", i), BYTES["adain_t1200"])
-    dom = per_op("adain_t9600", lambda i: op_adain("x9600", i), BYTES["adain_t9600"])
-    per_op("layernorm_768", op_ln, BYTES["layernorm_768"])
-    per_op("softmax_12x256x256", op_sm, BYTES["softmax_12x256x256"])
+    # A plain fp32 copy of each reduction's input (read + write of the same
+    # bytes): the bandwidth a kernel of that size can reach at all (launch
+    # and ramp dominate at a few MB), each op's frac_of_copy against it; the
+    # T=9600 copy is also the calibration kernel for the HBM byte counters.
+    copies = {}
+    for key, tag in (("x1200", "512x1200"), ("x9600", "512x9600"), ("ln", "256x768"),
+                     ("sm", "12x256x256")):
+        copies[key] = per_op(f"copy_{tag}", lambda i, k=key: B.call(
+            "kk_copy", outs[k][i].desc(), xs[k][i].desc()), 2 * 4 * xs[key][0].size)
+    cp = copies["x9600"]
+
+    def vs_copy(rec, key):
+        rec["frac_of_copy"] = round(rec["gbps"] / copies[key]["gbps"], 4)
+        return rec
+
+    vs_copy(per_op("adain_t1200", lambda i: op_adain("x1200", i), BYTES["adain_t1200"]), "x1200")
+    dom = vs_copy(per_op("adain_t9600", lambda i: op_adain("x9600", i), BYTES["adain_t9600"]), "x9600")
+    vs_copy(per_op("layernorm_768", op_ln, BYTES["layernorm_768"]), "ln")
+    vs_copy(per_op("softmax_12x256x256", op_sm, BYTES["softmax_12x256x256"]), "sm")
 
     # elementwise set: x [1,512,2400], per-channel c, alpha
     r = np.random.default_rng(0)
@@ -252,14 +262,16 @@ def run_gpu(args):
     eos = [kk.DeviceTensor.empty(ex.shape) for _ in range(ne)]
     ebytes = 2 * 4915200 + 2048
     opc = kk._lib.OP
-    per_op("add_1x512x2400", lambda i: B.call("kk_binary", opc["Add"], eos[i].desc(), exs[i].desc(),
-                                               ec.desc()), ebytes, sets=ne)
-    per_op("mul_1x512x2400", lambda i: B.call("kk_binary", opc["Mul"], eos[i].desc(), exs[i].desc(),
-                                               ec.desc()), ebytes, sets=ne)
-    per_op("leakyrelu_1x512x2400", lambda i: B.call("kk_unary", opc["LeakyRelu"], eos[i].desc(),
-                                                     exs[i].desc(), 0.2), 2 * 4915200, sets=ne)
-    per_op("snake_1x512x2400", lambda i: B.call("kk_snake", eos[i].desc(), exs[i].desc(), ea.desc(),
-                                                 None), ebytes, sets=ne)
+    copies["e"] = per_op("copy_1x512x2400", lambda i: B.call("kk_copy", eos[i].desc(), exs[i].desc()),
+                         2 * 4915200, sets=ne)
+    vs_copy(per_op("add_1x512x2400", lambda i: B.call("kk_binary", opc["Add"], eos[i].desc(),
+                                                       exs[i].desc(), ec.desc()), ebytes, sets=ne), "e")
+    vs_copy(per_op("mul_1x512x2400", lambda i: B.call("kk_binary", opc["Mul"], eos[i].desc(),
+                                                       exs[i].desc(), ec.desc()), ebytes, sets=ne), "e")
+    vs_copy(per_op("leakyrelu_1x512x2400", lambda i: B.call("kk_unary", opc["LeakyRelu"], eos[i].desc(),
+                                                             exs[i].desc(), 0.2), 2 * 4915200, sets=ne), "e")
+    vs_copy(per_op("snake_1x512x2400", lambda i: B.call("kk_snake", eos[i].desc(), exs[i].desc(),
+                                                         ea.desc(), None), ebytes, sets=ne), "e")
     del exs, eos
 
     # The same op classes at the decoder's own activation shapes (the
@@ -277,19 +289,22 @@ def run_gpu(args):
         da = D(r.uniform(0.5, 2, (1, C, 1)).astype(np.float32))
         dg = D((1 + 0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32))
         tag = f"1x{C}x{T}"
-        per_op(f"copy_{tag}", lambda i: B.call("kk_copy", do[i].desc(), dx[i].desc()), 2 * nbytes,
-               sets=nd)
-        per_op(f"add_{tag}", lambda i: B.call("kk_binary", opc["Add"], do[i].desc(), dx[i].desc(),
-                                               dc.desc()), 2 * nbytes + 4 * C, sets=nd)
-        per_op(f"mul_{tag}", lambda i: B.call("kk_binary", opc["Mul"], do[i].desc(), dx[i].desc(),
-                                               dc.desc()), 2 * nbytes + 4 * C, sets=nd)
-        per_op(f"leakyrelu_{tag}", lambda i: B.call("kk_unary", opc["LeakyRelu"], do[i].desc(),
-                                                     dx[i].desc(), 0.2), 2 * nbytes, sets=nd)
-        per_op(f"snake_{tag}", lambda i: B.call("kk_snake", do[i].desc(), dx[i].desc(), da.desc(),
-                                                 None), 2 * nbytes + 4 * C, sets=nd)
-        per_op(f"instnorm_affine_{tag}", lambda i: B.call(
+        copies[tag] = per_op(f"copy_{tag}", lambda i: B.call("kk_copy", do[i].desc(), dx[i].desc()),
+                             2 * nbytes, sets=nd)
+        vs_copy(per_op(f"add_{tag}", lambda i: B.call("kk_binary", opc["Add"], do[i].desc(),
+                                                       dx[i].desc(), dc.desc()), 2 * nbytes + 4 * C,
+                       sets=nd), tag)
+        vs_copy(per_op(f"mul_{tag}", lambda i: B.call("kk_binary", opc["Mul"], do[i].desc(),
+                                                       dx[i].desc(), dc.desc()), 2 * nbytes + 4 * C,
+                       sets=nd), tag)
+        vs_copy(per_op(f"leakyrelu_{tag}", lambda i: B.call("kk_unary", opc["LeakyRelu"], do[i].desc(),
+                                                             dx[i].desc(), 0.2), 2 * nbytes, sets=nd), tag)
+        vs_copy(per_op(f"snake_{tag}", lambda i: B.call("kk_snake", do[i].desc(), dx[i].desc(),
+                                                         da.desc(), None), 2 * nbytes + 4 * C,
+                       sets=nd), tag)
+        vs_copy(per_op(f"instnorm_affine_{tag}", lambda i: B.call(
             "kk_instance_norm_scale_shift", do[i].desc(), dx[i].desc(), dg.desc(), dc.desc(), 1e-5, 0,
-            0.0), 2 * nbytes + 8 * C, sets=nd, reps=10, eager=True)
+            0.0), 2 * nbytes + 8 * C, sets=nd, reps=10, eager=True), tag)
         del dx, do
 
     # dequant contractions (fp32 semantics; TFLOP/s against the fp32 peak)

@@ -546,10 +546,16 @@ static int run_elementwise(int op, const kk_tensor* out, const kk_tensor* const*
       for (int d = 0; d < p.rank - 1; ++d)
         if (p.st[k][d] % 4) vec4 = false;
     }
-    // Rows that are not whole float4s: the flat float4 walk, when the output
-    // is contiguous and every input is contiguous like it or per-row.
+    // The flat float4 walk, when the output is contiguous and every input
+    // is contiguous like it or per-row: for rows that are not whole float4s,
+    // and for rows whose float4s leave ew_rows' 256-wide column blocks more
+    // than 5% idle ([1,512,2400]: 600 float4s a row, three blocks of which
+    // the last has 88 of 256 lanes busy) -- the flat walk packs every lane.
+    const int64_t per_row4 = L / 4;
+    const bool rows_idle = vec4 && p.rank == 2 &&
+                           (ceil_div(per_row4, 256) * 256 - per_row4) * 20 > per_row4;
     int kinds = -1;
-    if (!vec4 && p.rank <= 2 && L >= 4 && L % 4 != 0 && p.n >= 4096 &&
+    if ((!vec4 || rows_idle) && p.rank <= 2 && L >= 4 && p.n >= 4096 &&
         reinterpret_cast<uintptr_t>(out->data) % 16 == 0 &&
         (p.rank == 1 || p.st[0][0] == L)) {
       kinds = 0;

@@ -112,6 +112,37 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// Wave-wide sum / max through DPP lane moves instead of the butterfly's six
+// ds_bpermute round trips through LDS: pairs (quad_perm 1,0,3,2), quads
+// (quad_perm 2,3,0,1), half rows (row_half_mirror), rows of 16
+// (row_mirror), then rows 0+1 and 2+3 (row_bcast15 into rows 1 and 3) and
+// all four (row_bcast31 into rows 2 and 3); lane 63 ends with the total,
+// which readlane makes wave-uniform.  A different (fixed) order of additions
+// than wave_sum: for kernels held to a tolerance, not to numpy's bits.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_move(float v, float fill) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), CTRL,
+                                                    ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = v + dpp_move<0xB1, 0xF>(v, 0.0f);
+  v = v + dpp_move<0x4E, 0xF>(v, 0.0f);
+  v = v + dpp_move<0x141, 0xF>(v, 0.0f);
+  v = v + dpp_move<0x140, 0xF>(v, 0.0f);
+  v = v + dpp_move<0x142, 0xA>(v, 0.0f);
+  v = v + dpp_move<0x143, 0xC>(v, 0.0f);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_move<0xB1, 0xF>(v, -INFINITY));
+  v = fmaxf(v, dpp_move<0x4E, 0xF>(v, -INFINITY));
+  v = fmaxf(v, dpp_move<0x141, 0xF>(v, -INFINITY));
+  v = fmaxf(v, dpp_move<0x140, 0xF>(v, -INFINITY));
+  v = fmaxf(v, dpp_move<0x142, 0xA>(v, -INFINITY));
+  v = fmaxf(v, dpp_move<0x143, 0xC>(v, -INFINITY));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 // Streaming (non-temporal) 128-bit and 32-bit accesses for data that is
 // read or written once per kernel.  Several 16-byte stores per thread with
 // ordinary write-back stores measured 3-5x slower on MI355X than the same

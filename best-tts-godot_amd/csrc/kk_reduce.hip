@@ -17,9 +17,11 @@ namespace kk {
 
 constexpr int kRowBlock = 256;
 
-template <int GROUP>
+// DPP: wave sums through DPP lane moves (kernels held to a tolerance); else
+// the butterfly, whose order the numpy-order kernels rely on.
+template <int GROUP, bool DPP = false>
 __device__ __forceinline__ float group_sum(float v, float* lds) {
-  v = wave_sum(v);
+  v = DPP ? wave_sum_dpp(v) : wave_sum(v);
   if constexpr (GROUP == 64) {
     return v;
   } else {
@@ -31,9 +33,9 @@ __device__ __forceinline__ float group_sum(float v, float* lds) {
   }
 }
 
-template <int GROUP>
+template <int GROUP, bool DPP = false>
 __device__ __forceinline__ float group_max(float v, float* lds) {
-  v = wave_max(v);
+  v = DPP ? wave_max_dpp(v) : wave_max(v);
   if constexpr (GROUP == 64) {
     return v;
   } else {
@@ -47,10 +49,10 @@ __device__ __forceinline__ float group_max(float v, float* lds) {
 
 // Two independent group sums in one LDS round (each sum in group_sum's
 // order, so the results are the same bits); lds holds 8 floats.
-template <int GROUP>
+template <int GROUP, bool DPP = false>
 __device__ __forceinline__ void group_sum_pair(float& a, float& b, float* lds) {
-  a = wave_sum(a);
-  b = wave_sum(b);
+  a = DPP ? wave_sum_dpp(a) : wave_sum(a);
+  b = DPP ? wave_sum_dpp(b) : wave_sum(b);
   if constexpr (GROUP != 64) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     __syncthreads();
@@ -106,7 +108,7 @@ __device__ __forceinline__ void store_row(float* __restrict__ row, int64_t n, in
 
 // Two-pass mean and variance of the row held in r (n valid elements; the
 // padding lanes hold 0 and are masked out of the second pass).
-template <int GROUP, int NV, int VEC>
+template <int GROUP, int NV, int VEC, bool DPP = false>
 __device__ __forceinline__ void row_stats(float (&r)[NV][VEC], int64_t n, int g, float* lds,
                                           float& mean, float& var) {
   float s = 0.0f;
@@ -114,7 +116,7 @@ __device__ __forceinline__ void row_stats(float (&r)[NV][VEC], int64_t n, int g,
   for (int j = 0; j < NV; ++j)
 #pragma unroll
     for (int e = 0; e < VEC; ++e) s += r[j][e];
-  s = group_sum<GROUP>(s, lds);
+  s = group_sum<GROUP, DPP>(s, lds);
   mean = s / static_cast<float>(n);
   float q = 0.0f;
 #pragma unroll
@@ -127,7 +129,7 @@ __device__ __forceinline__ void row_stats(float (&r)[NV][VEC], int64_t n, int g,
       if (base + e < n) q += d * d;
     }
   }
-  q = group_sum<GROUP>(q, lds);
+  q = group_sum<GROUP, DPP>(q, lds);
   var = q / static_cast<float>(n);
 }
 
@@ -177,7 +179,7 @@ __device__ __forceinline__ void style_affine(const StyleArgs& sa, int64_t C, int
   }
   float ag, ab;
   style_dots<GROUP>(sa, C, c, g, ag, ab);
-  group_sum_pair<GROUP>(ag, ab, lds);
+  group_sum_pair<GROUP, true>(ag, ab, lds);
   if (sa.bias) {
     ag = ag + bg;
     ab = ab + bb;
@@ -266,7 +268,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
   else if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
   const RowAffine ra = row_affine(af, C, c, gamma, beta);
   float mean, var;
-  row_stats<GROUP, NV, VEC>(r, T, g, lds, mean, var);
+  row_stats<GROUP, NV, VEC, true>(r, T, g, lds, mean, var);
   const float den = sqrtf(var + eps);
 #pragma unroll
   for (int j = 0; j < NV; ++j)
@@ -281,7 +283,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
 // 8 waves per row run at 92% of a plain copy's rate against 83% for 4).
 template <int NW>
 __device__ __forceinline__ float wide_sum(float v, float* lds) {
-  v = wave_sum(v);
+  v = wave_sum_dpp(v);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) lds[w] = v;
@@ -298,8 +300,8 @@ __device__ __forceinline__ float wide_sum(float v, float* lds) {
 
 template <int NW>
 __device__ __forceinline__ void wide_sum_pair(float& a, float& b, float* lds) {
-  a = wave_sum(a);
-  b = wave_sum(b);
+  a = wave_sum_dpp(a);
+  b = wave_sum_dpp(b);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   __syncthreads();
   if (lane == 0) {
@@ -630,7 +632,7 @@ __global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict_
   load_row<GROUP, NV, VEC, false>(la.scale, cols, g, sc);
   if (la.bias) load_row<GROUP, NV, VEC, false>(la.bias, cols, g, bi);
   float mean, var;
-  row_stats<GROUP, NV, VEC>(r, cols, g, lds, mean, var);
+  row_stats<GROUP, NV, VEC, true>(r, cols, g, lds, mean, var);
   const float den = sqrtf(var + eps);
 #pragma unroll
   for (int j = 0; j < NV; ++j)
@@ -702,7 +704,7 @@ __global__ void __launch_bounds__(kRowBlock) softmax_kernel(float* __restrict__ 
     for (int e = 0; e < VEC; ++e)
       if (base + e < cols) m = fmaxf(m, r[j][e]);
   }
-  m = group_max<GROUP>(m, lds);
+  m = group_max<GROUP, true>(m, lds);
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -714,7 +716,7 @@ __global__ void __launch_bounds__(kRowBlock) softmax_kernel(float* __restrict__ 
       if (base + e < cols) s += v;
     }
   }
-  s = group_sum<GROUP>(s, lds);
+  s = group_sum<GROUP, true>(s, lds);
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
@@ -1521,6 +1523,23 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
       default: hipLaunchKernelGGL((instnorm_wide_kernel<8, 8>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
     }
     return check_launch("instnorm_wide_kernel");
+  }
+  if (vec_ok && nvec > 4 * 64 && nvec <= 8 * 64) {
+    // One wave per row (T up to 2048, the decoder's [1,512,1200]): its sums
+    // are DPP moves within the wave, with no LDS round or barrier, and each
+    // lane keeps its 5-8 vectors' loads in flight together.
+    const int nv = static_cast<int>(ceil_div(nvec, 64));
+    const dim3 grid(static_cast<unsigned>(rows));
+    float* op = static_cast<float*>(out->data);
+    const float* xp = static_cast<const float*>(x->data);
+    hipStream_t st = ctx().stream;
+    if (nv == 5)
+      hipLaunchKernelGGL((instnorm_kernel<64, 5, 4>), grid, dim3(64), 0, st, op, xp, rows, C, T, eps, af, sa);
+    else if (nv == 6)
+      hipLaunchKernelGGL((instnorm_kernel<64, 6, 4>), grid, dim3(64), 0, st, op, xp, rows, C, T, eps, af, sa);
+    else
+      hipLaunchKernelGGL((instnorm_kernel<64, 8, 4>), grid, dim3(64), 0, st, op, xp, rows, C, T, eps, af, sa);
+    return check_launch("instnorm_kernel");
   }
   if (pick_row_shape(T, vec_ok, &rs)) {
     KK_ROW_DISPATCH(instnorm_kernel, rs, rows, static_cast<float*>(out->data),
