@@ -785,12 +785,24 @@ static int conv_common(const kk_tensor* out, const kk_tensor* x, const kk_tensor
   return KK_OK;
 }
 
-static int launch_gemm(const GemmArgs& args, int64_t batch) {
+// weights_rounded: keep numpy's per-weight rounding of (q - zp) * scale
+// (the fp32 matrix cores); else 8-bit and fp16 weights may take the bf16
+// matrix cores, which scale the exact sum instead.
+static int launch_gemm(const GemmArgs& args, int64_t batch, bool weights_rounded = false) {
   if (args.N <= kSkinnyN && args.K <= kSkinnyK && args.M * batch >= 4096) {
     const int64_t rows = args.M * batch;
     const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(rows, 256), 1 << 16));
     hipLaunchKernelGGL(gemm_skinny_kernel, dim3(grid), dim3(256), 0, ctx().stream, args, batch);
     return check_launch("gemm_skinny_kernel");
+  }
+  // 8-bit and fp16 weights with fp32 activations: the bf16 matrix cores
+  // with split activations (fp32 accuracy)
+  if (!weights_rounded && args.a_dt == KK_F32 && args.a_sj == 1 && args.b_sj == 1) {
+    int st = KK_OK;
+    if (gemm_dq_try(static_cast<const float*>(args.a), args.a_si, args.b, args.b_dt, args.b_si,
+                    args.dq, args.out, args.som, args.son, args.bm, args.M, args.N, args.K, batch,
+                    args.alpha, args.only_if, &st))
+      return st;
   }
   const TileSize ts = pick_tile(args.M, args.N, batch);
   dim3 grid = grid_of(ts, args.M, args.N, batch);
@@ -942,14 +954,8 @@ bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, con
                const kk_tensor* bias, bool transposed, int64_t stride, int64_t dilation,
                int64_t pad0, int64_t Nq, int** flag, void** ws);
 
-}  // namespace kk
-
-using namespace kk;
-
-extern "C" {
-
-int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
-            const kk_tensor* w_zp, float alpha) {
+int gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
+         const kk_tensor* w_zp, float alpha, bool weights_rounded) {
   GemmArgs G{};
   int64_t batch = 0;
   KK_TRY(setup_gemm(&G, out, a, w, &batch, "kk_gemm"));
@@ -959,7 +965,18 @@ int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const 
   G.alpha = alpha;
   if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
   if (G.K == 0) return kk_fill(out, 0.0);
-  return launch_gemm(G, batch);
+  return launch_gemm(G, batch, weights_rounded);
+}
+
+}  // namespace kk
+
+using namespace kk;
+
+extern "C" {
+
+int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
+            const kk_tensor* w_zp, float alpha) {
+  return gemm(out, a, w, w_scale, w_zp, alpha, false);
 }
 
 int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* w_scale,

@@ -801,7 +801,9 @@ int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const
       zpt.dtype = w_zp->dtype; zpt.rank = 0;
       zptr = &zpt;
     }
-    rc = kk_gemm(&o, &a, &wd, &sc, zptr, 1.0f);
+    // the recurrence amplifies the projection's rounding: keep numpy's
+    // (each dequantised weight rounded to fp32, exact fp32 products)
+    rc = gemm(&o, &a, &wd, &sc, zptr, 1.0f, true);
     if (rc == KK_OK && b) {
       kk_tensor wb{}, rb{}, bs{};
       for (kk_tensor* t : {&wb, &rb, &bs}) {

@@ -235,6 +235,18 @@ __device__ __forceinline__ int64_t batch_offset(const BatchMap& bm, int which, i
 // batch axes broadcast): fills *bm and M, N, K and the batch count.
 int matmul_shape(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, BatchMap* bm,
                  int64_t* M, int64_t* N, int64_t* K, int64_t* batch, const char* who);
+// kk_gemm; weights_rounded keeps numpy's rounding of each dequantised weight
+// (the fp32 matrix cores) where a caller's result feeds a recurrence.
+int gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
+         const kk_tensor* w_zp, float alpha, bool weights_rounded);
+// out = A @ dequant(B) on the bf16 matrix cores (kk_gemm_dq.hip) when the
+// operands fit: fp32 A with K contiguous, int8/uint8 B (zero point of the
+// same type) or fp16 B with N contiguous.  Returns false, launching nothing,
+// when they do not; *status is the launch's status otherwise.
+bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t b_si,
+                 const Dequant& dq, float* out, int64_t som, int64_t son, const BatchMap& bm,
+                 int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, const int* only_if,
+                 int* status);
 // A zero-point-only shift (scale 1) for the integer ops: per tensor, or per
 // element of `count` when the zero point has that many elements.
 int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* who);

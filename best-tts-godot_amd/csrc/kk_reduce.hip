@@ -1102,15 +1102,23 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     }
     xmm[row * nblk + b] = make_float2(lo, hi);
   }
-  // wave 0: the partial goes to the device-coherent level (past this XCD's
-  // L2) and has landed before the count moves
+  // wave 0: the partial goes to the device-coherent level (an agent-scope
+  // store writes through this XCD's L2) and has landed before the count
+  // moves: vmcnt(0) waits for the store's acknowledgement, and the compiler
+  // fence keeps the compiler from moving either access across the other.  A
+  // release fence would order the same two accesses by writing back this
+  // XCD's whole L2 from every block (7x slower).
   int last = 0;
   if (threadIdx.x == 0) {
     __hip_atomic_store(part + row * nblk + b, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
     last = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nblk - 1;
   }
   if (__shfl(last, 0, 64)) {
+    // the row's last block: an agent-scope acquire orders its reads of the
+    // other blocks' partials after the count it saw (once per row)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float acc = np_fold(part + row * nblk, nblk);
     const float n = static_cast<float>(T);
     if (mode == 1 && mm) {  // the row's (xmin, xmax), written by the mode-0 launch
@@ -1552,6 +1560,15 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
   return check_launch("instnorm_kernel");
 }
 
+// A per-channel operand of x [N, C, T]: C values that broadcast along T, i.e.
+// shaped [..., C, 1] (or any shape of one value when C is 1).  A [C] operand
+// would broadcast along T instead, so it is not one.
+static bool per_channel(const kk_tensor* t, const kk_tensor* x, int64_t C) {
+  if (numel(t) != C || t->rank > x->rank) return false;
+  if (C == 1) return true;
+  return t->rank >= 2 && t->shape[t->rank - 1] == 1 && t->shape[t->rank - 2] == C;
+}
+
 static int instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
                                      const kk_tensor* scale, const kk_tensor* shift,
                                      const kk_tensor* snake_a, const kk_tensor* snake_r, float eps,
@@ -1583,17 +1600,18 @@ static int instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
   for (const kk_tensor* t : {scale, shift}) {
     if (!t) continue;
     KK_TRY(check_f32_contig(t, t == scale ? "scale" : "shift"));
-    if (numel(t) != C)
-      return set_error(KK_E_ARG, "instance norm: scale/shift need C = %lld elements",
-                       (long long)C);
+    if (!per_channel(t, x, C))
+      return set_error(KK_E_ARG, "instance norm: scale/shift need C = %lld values shaped "
+                       "[..., C, 1]", (long long)C);
   }
   af.scale = scale ? static_cast<const float*>(scale->data) : nullptr;
   af.shift = shift ? static_cast<const float*>(shift->data) : nullptr;
   if (snake_a) {
     for (const kk_tensor* t : {snake_a, snake_r}) {
       KK_TRY(check_f32_contig(t, t == snake_a ? "snake alpha" : "snake recip"));
-      if (numel(t) != C)
-        return set_error(KK_E_ARG, "instance norm: snake alpha/recip need C = %lld elements",
+      if (!per_channel(t, x, C))
+        return set_error(KK_E_ARG, "instance norm: snake alpha/recip need C = %lld values shaped "
+                         "[..., C, 1]",
                          (long long)C);
     }
     af.snake_a = static_cast<const float*>(snake_a->data);

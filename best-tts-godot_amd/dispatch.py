@@ -20,6 +20,7 @@ Cast(to=float16) yields fp32.
 import numpy as np
 
 from . import ops
+from .hostops import slice_clamp
 from .tensor import DeviceTensor
 
 # ONNX TensorProto element types -> numpy (ref_runtime.py:24-28)
@@ -79,14 +80,38 @@ def _host_int(v):
 def _slice_params(dim, s, e, st):
     """Clamp like op_slice (ref_runtime.py:307-325) and resolve the python
     slice to (start, stop, step) of the selected range."""
-    if st > 0:
-        s = min(max(s if s >= 0 else s + dim, 0), dim)
-        e = min(max(e if e >= 0 else e + dim, 0), dim)
-    else:
-        s = min(max(s if s >= 0 else s + dim, -1), dim - 1)
-        e = min(max(e if e >= 0 else e + dim, -1), dim - 1)
+    s, e = slice_clamp(dim, s, e, st)
     r = range(dim)[slice(s, e, st)]
     return r.start, r.stop, r.step, len(r)
+
+
+def _per_channel(t, x):
+    """True when t is absent or holds x's C values broadcasting along T
+    (shape [..., C, 1]; any shape of one value when C is 1), the operand form
+    the fused instance-norm kernels apply per channel."""
+    if t is None:
+        return True
+    C = x.shape[-2] if len(x.shape) >= 2 else 0
+    sh = tuple(t.shape)
+    if int(np.prod(sh, dtype=np.int64)) != C or len(sh) > len(x.shape):
+        return False
+    return C == 1 or (len(sh) >= 2 and sh[-1] == 1 and sh[-2] == C)
+
+
+def _norm_chain(xd, sc, sh, eps, leaky_alpha):
+    """The fused InstanceNorm chain's float result: one launch when scale and
+    shift are per channel, else the statistics' launch and then the chain's
+    Mul, Add and LeakyRelu nodes, broadcasting as numpy does."""
+    if _per_channel(sc, xd) and _per_channel(sh, xd):
+        return ops.instance_norm_scale_shift(xd, sc, sh, eps, leaky_alpha)
+    y = ops.instance_norm_scale_shift(xd, None, None, eps, None)
+    if sc is not None:
+        y = ops.binary("Mul", y, sc)
+    if sh is not None:
+        y = ops.binary("Add", y, sh)
+    if leaky_alpha is not None:
+        y = ops.unary("LeakyRelu", y, np.float32(leaky_alpha))
+    return y
 
 
 def dispatch(op, node_input, node_output, at, env):
@@ -388,21 +413,18 @@ def dispatch(op, node_input, node_output, at, env):
     elif op == "InstanceNormScaleShift":
         # ReduceMean/Sub/Mul/ReduceMean/Add/Sqrt/Div [-> Mul -> Add -> LeakyRelu], fused;
         # inputs x, scale ("" if absent), shift ("" if absent).
-        out = ops.instance_norm_scale_shift(_f32(to_device(x)), _f32(to_device(y)),
-                                            _f32(to_device(inp(2))), at["epsilon"],
-                                            at.get("leaky_alpha"))
+        # Operands that are not per channel run past the statistics node by node.
+        out = _norm_chain(_f32(to_device(x)), _f32(to_device(y)), _f32(to_device(inp(2))),
+                          at["epsilon"], at.get("leaky_alpha"))
     elif op == "InstanceNormSnake":
         # the InstanceNorm chain (+ Mul scale, Add shift), then the snake chain on its
         # output; inputs x, scale, shift ("" if absent), alpha, recip (C values each).
         xd, a, rc = _f32(to_device(x)), _f32(to_device(inp(3))), _f32(to_device(inp(4)))
-        C = xd.shape[-2] if len(xd.shape) >= 2 else 0
-        if a.size == C and rc.size == C:
-            out = ops.instance_norm_scale_shift_snake(xd, _f32(to_device(y)), _f32(to_device(inp(2))),
-                                                      a, rc, at["epsilon"])
-        else:  # alpha/recip not per channel: the two fused ops one after the other
-            yv = ops.instance_norm_scale_shift(xd, _f32(to_device(y)), _f32(to_device(inp(2))),
-                                               at["epsilon"], None)
-            out = ops.snake(yv, a, rc)
+        sc, sh = _f32(to_device(y)), _f32(to_device(inp(2)))
+        if all(_per_channel(t, xd) for t in (sc, sh, a, rc)):
+            out = ops.instance_norm_scale_shift_snake(xd, sc, sh, a, rc, at["epsilon"])
+        else:  # an operand not per channel: the two chains one after the other
+            out = ops.snake(_norm_chain(xd, sc, sh, at["epsilon"], None), a, rc)
     elif op == "InstanceNormQuant":
         # the InstanceNorm chain (+ Mul scale, Add shift, then LeakyRelu or the snake
         # chain) -> Cast(float) -> DynamicQuantizeLinear, fused; inputs x, scale,
@@ -412,12 +434,12 @@ def dispatch(op, node_input, node_output, at, env):
         a, rc = inp(3), inp(4)
         a = _f32(to_device(a)) if a is not None else None
         rc = _f32(to_device(rc)) if rc is not None else None
-        C = xd.shape[-2] if len(xd.shape) >= 2 else 0
-        if a is None or (a.size == C and rc.size == C):
+        if all(_per_channel(t, xd) for t in (sc, sh, a, rc)):
             res = ops.instance_norm_quant(xd, sc, sh, a, rc, at["epsilon"], at.get("leaky_alpha"))
-        else:  # alpha/recip not per channel: the fused ops one after the other
-            yv = ops.instance_norm_scale_shift(xd, sc, sh, at["epsilon"], None)
-            res = ops.dynamic_quantize_linear(ops.snake(yv, a, rc))
+        else:  # an operand not per channel: the chains one after the other
+            yv = _norm_chain(xd, sc, sh, at["epsilon"], None if a is not None else
+                             at.get("leaky_alpha"))
+            res = ops.dynamic_quantize_linear(ops.snake(yv, a, rc) if a is not None else yv)
         for name, v in zip(node_output, res):
             if name:
                 env[name] = v

@@ -15,6 +15,19 @@ ONNX_DTYPE = {
 }
 
 
+def slice_clamp(dim, s, e, st):
+    """Clamp one axis's start/end like op_slice (ref_runtime.py:307-325):
+    into [0, dim] for a positive step, into [-1, dim - 1] for a negative one,
+    where a python slice then reads -1 as the last element."""
+    if st > 0:
+        s = min(max(s if s >= 0 else s + dim, 0), dim)
+        e = min(max(e if e >= 0 else e + dim, 0), dim)
+    else:
+        s = min(max(s if s >= 0 else s + dim, -1), dim - 1)
+        e = min(max(e if e >= 0 else e + dim, -1), dim - 1)
+    return s, e
+
+
 def _slice(data, starts, ends, axes, steps):
     r = data.ndim
     axes = list(range(len(starts))) if axes is None else axes
@@ -22,14 +35,8 @@ def _slice(data, starts, ends, axes, steps):
     sl = [slice(None)] * r
     for s, e, a, st in zip(starts, ends, axes, steps):
         a = int(a) % r
-        s, e, st = int(s), int(e), int(st)
-        dim = data.shape[a]
-        if st > 0:
-            s = min(max(s if s >= 0 else s + dim, 0), dim)
-            e = min(max(e if e >= 0 else e + dim, 0), dim)
-        else:
-            s = min(max(s if s >= 0 else s + dim, -1), dim - 1)
-            e = min(max(e if e >= 0 else e + dim, -1), dim - 1)
+        st = int(st)
+        s, e = slice_clamp(data.shape[a], int(s), int(e), st)
         sl[a] = slice(s, e, st)
     return data[tuple(sl)]
 

@@ -201,6 +201,41 @@ def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
     assert_bitexact(got, want, f"InstanceNorm chain C={C} T={T}")
 
 
+@pytest.mark.parametrize("gshape,bshape,leaky,snake", [((64,), (1, 64, 1), False, False),
+                                                      ((1, 64, 1), (64,), True, False),
+                                                      ((), (1, 64, 1), False, False),
+                                                      ((1, 64, 1), (1, 64, 1), False, True),
+                                                      ((64,), (64,), False, True)])
+def test_instance_norm_chain_operands_not_per_channel(gpu, oracle, gshape, bshape, leaky, snake):
+    """A scale or shift of C values shaped [C] broadcasts along T, not along
+    the channels; with T == C the graph is valid and the fused per-channel
+    kernel would give a different result.  Such chains (and one-value
+    scales) run past the statistics node by node and match the oracle's
+    chain bit for bit; the snake's operands stay per channel."""
+    C = T = 64
+    r = rng(27)
+    x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
+    inputs = {"x": x, "g": (1 + 0.1 * r.normal(0, 1, gshape)).astype(np.float32),
+              "b": (0.1 * r.normal(0, 1, bshape)).astype(np.float32)}
+    weights = {"ax": np.array([2], np.int64),
+               "eps": np.array(1e-5, np.float16).astype(np.float32)}
+    nodes, y = norm_chain(True, leaky)
+    if snake:
+        alpha = r.uniform(0.5, 2, (1, C, 1)).astype(np.float16)
+        weights.update({"a": alpha, "two": np.array(2.0, np.float16),
+                        "rc": (np.float32(1) / alpha.astype(np.float32)).astype(np.float16)})
+        nodes += [("Mul", ["a", y], ["t"], {}), ("Sin", ["t"], ["s"], {}),
+                  ("Pow", ["s", "two"], ["p"], {}), ("Mul", ["rc", "p"], ["q"], {}),
+                  ("Add", [y, "q"], ["z"], {})]
+        y = "z"
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, y)
+    assert fused[0][0] in ("InstanceNormScaleShift", "InstanceNormSnake")
+    if snake:
+        assert_close(got, want, 1e-5, floor_rel=1e-6, what=f"{gshape} {bshape} + snake")
+    else:
+        assert_bitexact(got, want, f"InstanceNorm chain scale {gshape} shift {bshape}")
+
+
 def test_instance_norm_long_rows_repeat(gpu, oracle):
     """The long-row instance norm leaves its per-row arrival counters at
     zero: three launches in a row, with one of another shape between each,

@@ -70,6 +70,77 @@ def test_per_column_dequant_u8_and_i8(gpu, oracle):
     check(got, oracle.matmul(a, oracle.dequantize(u, np.float32(0.01), np.uint8(128))), "uint8")
 
 
+@pytest.mark.parametrize("m,k,n,wdt", [(1024, 256, 1024, "i8"),   # 64x64 tiles
+                                       (256, 768, 2048, "i8"),    # 32x64, K over two waves
+                                       (256, 768, 768, "u8"),     # 32x32, K over four waves
+                                       (1, 100, 36, "i8"), (33, 36, 100, "f16"),
+                                       (70, 4, 8, "u8"), (300, 2052, 68, "i8")])
+def test_dequant_matmul_bf16_split_accuracy(gpu, oracle, m, k, n, wdt):
+    """The 8-bit-weight MatMul on the bf16 matrix cores (activations split
+    into three bf16 parts, every product exact; fp16 weights take the fp32
+    matrix cores): the oracle's bar, and no less accurate than numpy's own
+    fp32 result against a float64 product (K and N off the tile sizes,
+    M = 1, per-column and per-tensor zero points of both byte types)."""
+    r = rng(12)
+    a = r.normal(0, 1, (m, k)).astype(np.float32)
+    if wdt == "f16":
+        w = r.normal(0, 0.05, (k, n)).astype(np.float16)
+        sc = zp = None
+        wdeq = w.astype(np.float32)
+    elif wdt == "i8":
+        w = r.integers(-128, 128, (k, n)).astype(np.int8)
+        sc = r.uniform(1e-3, 1e-2, n).astype(np.float32)
+        zp = r.integers(-127, 128, n).astype(np.int8)  # |q - zp| up to 255
+        wdeq = oracle.dequantize(w, sc, zp)
+    else:
+        w = r.integers(0, 256, (k, n)).astype(np.uint8)
+        sc = np.float32(0.004)
+        zp = np.uint8(255)
+        wdeq = oracle.dequantize(w, sc, zp)
+    dv = gpu.to_device
+    got = gpu.ops.matmul(dv(a), dv(w), dv(np.asarray(sc)) if sc is not None else None,
+                         dv(np.asarray(zp)) if zp is not None else None).numpy()
+    want = oracle.matmul(a, wdeq)
+    check(got, want, f"{wdt} {m}x{k}x{n}")
+    exact = a.astype(np.float64) @ wdeq.astype(np.float64)
+    terms = np.abs(a.astype(np.float64)) @ np.abs(wdeq.astype(np.float64))
+    e_dev = (np.abs(got - exact) / np.maximum(terms, 1e-300)).max()
+    e_np = (np.abs(want - exact) / np.maximum(terms, 1e-300)).max()
+    assert e_dev <= 4 * e_np + 2 ** -22, (e_dev, e_np)
+
+
+@pytest.mark.parametrize("mag", [1e-30, 1e-7, 1e20])
+def test_dequant_matmul_activation_range(gpu, oracle, mag):
+    """Activations of any magnitude keep fp32 accuracy (on the bf16 matrix
+    cores the split needs no scaling); inf and NaN activations reach the
+    same outputs as numpy's."""
+    r = rng(13)
+    a = (r.normal(0, 1, (40, 256)) * mag).astype(np.float32)
+    for wdt in ("i8", "f16"):
+        if wdt == "i8":
+            w = r.integers(-127, 128, (256, 96)).astype(np.int8)
+            sc, wdeq = np.float32(0.01), None
+            wdeq = oracle.dequantize(w, sc, np.int8(0))
+        else:
+            w = r.normal(0, 0.05, (256, 96)).astype(np.float16)
+            sc, wdeq = None, w.astype(np.float32)
+        dv = gpu.to_device
+        got = gpu.ops.matmul(dv(a), dv(w), dv(np.asarray(sc)) if sc is not None else None).numpy()
+        check(got, oracle.matmul(a, wdeq), f"{wdt} activations ~{mag:g}")
+    a2 = r.normal(0, 1, (40, 256)).astype(np.float32)
+    a2[3, 17], a2[9, 200] = np.inf, np.nan
+    w = r.integers(-127, 128, (256, 96)).astype(np.int8)
+    w[17, :] = np.where(w[17, :] == 0, 1, w[17, :])  # inf meets no zero weight
+    got = gpu.ops.matmul(gpu.to_device(a2), gpu.to_device(w),
+                         gpu.to_device(np.float32(0.01))).numpy()
+    want = oracle.matmul(a2, oracle.dequantize(w, np.float32(0.01), np.int8(0)))
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_array_equal(np.isinf(got), np.isinf(want))
+    fin = np.isfinite(want)
+    assert np.array_equal(np.sign(got[np.isinf(want)]), np.sign(want[np.isinf(want)]))
+    check(np.where(fin, got, 0), np.where(fin, want, 0), "finite rows beside inf/NaN")
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 13, 5), (33, 65, 97), (130, 512, 50),
                                    (64, 64, 64)])
 def test_matmul_odd_shapes(gpu, oracle, m, k, n):
