@@ -40,6 +40,15 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 (vector and MFMA)
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
 ROTATE_BYTES = 640 << 20    # > 2x the 256 MB Infinity Cache
+# Matrix-core paths of the contraction lines: (description, effective peak
+# in TFLOP/s of fp32-accurate work) from MI355X's dense peaks (bf16/fp16
+# 2.5 PFLOP/s, int8 5.0 POPS, fp32 157.3 TFLOP/s) and the MFMAs per product.
+MFMA_PEAKS = {
+    "fp32": ("fp32 MFMA (v_mfma_f32_16x16x4_f32)", 157.3),
+    "bf16x3": ("bf16 MFMA, activations in 3 bf16 parts (v_mfma_f32_32x32x16_bf16 x3)", 2500.0 / 3),
+    "f16x2": ("fp16 MFMA, activations in 2 fp16 parts (v_mfma_f32_32x32x16_f16 x2)", 1250.0),
+    "i8": ("int8 MFMA (v_mfma_i32_32x32x32_i8)", INT8_PEAK_TOPS),
+}
 
 
 def log(msg):
@@ -214,7 +223,7 @@ def run_gpu(args):
     # ---- per-op lines: one graph per set, each with a single op node
     ops_out = {}
 
-    def per_op(name, fn, nbytes=None, flops=None, reps=20, sets=nsets, eager=False):
+    def per_op(name, fn, nbytes=None, flops=None, reps=20, sets=nsets, eager=False, mfma=None):
         if eager:
             t_ms = B.time_eager(fn, sets, reps)
         else:  # one graph holding the op once per rotating set
@@ -228,6 +237,9 @@ def run_gpu(args):
         if flops:
             tf = flops / (t_ms * 1e-3) / 1e12
             rec.update(flops=flops, tflops=round(tf, 2), frac_fp32=round(tf / FP32_PEAK_TFLOPS, 4))
+            if mfma:  # the matrix-core type the kernel runs on, at its effective peak
+                kind, peak = MFMA_PEAKS[mfma]
+                rec.update(mfma=kind, mfma_peak_tflops=peak, frac_mfma=round(tf / peak, 4))
         ops_out[name] = rec
         log(f"bench: {name:<28} {json.dumps(rec)}")
         return rec
@@ -319,7 +331,7 @@ def run_gpu(args):
         o = [kk.DeviceTensor.empty((m, n)) for _ in range(4)]
         per_op(name, lambda i: B.call("kk_gemm", o[i].desc(), a[i].desc(), wq.desc(),
                                       sc.desc() if sc else None, None, 1.0),
-               flops=2 * m * n * k, sets=4)
+               flops=2 * m * n * k, sets=4, mfma="bf16x3" if wdt == "i8" else "fp32")
 
     gemm_case("gemm_i8_256x768x2048", 256, 768, 2048, "i8")
     gemm_case("gemm_i8_256x2048x768", 256, 2048, 768, "i8")
@@ -335,7 +347,7 @@ def run_gpu(args):
         # workspace, which graph capture does not allow
         per_op(name, lambda i: B.call("kk_conv1d", o[i].desc(), x[i].desc(), wq.desc(), sc.desc(),
                                       None, None, 1, dil, pad, pad, 1),
-               flops=2 * cout * cin * k * lout, sets=4, eager=True)
+               flops=2 * cout * cin * k * lout, sets=4, eager=True, mfma="f16x2")
 
     conv_case("conv_i8_512x512_k3_L2400", 512, 512, 3, 2400, 1, 1)
     conv_case("conv_i8_256x256_k3_d1_L2400", 256, 256, 3, 2400, 1, 1)
@@ -350,8 +362,7 @@ def run_gpu(args):
     oq = [kk.DeviceTensor.empty((1, 128, L8), np.int32) for _ in range(3)]
     rec = per_op("conv_int8_128x128_k11_L431000", lambda i: B.call(
         "kk_conv_integer", oq[i].desc(), xq[i].desc(), wq8.desc(), xz8.desc(), wz8.desc(), 1, 1, 5,
-        5, 1), flops=2 * 128 * 128 * 11 * L8, sets=3, reps=10, eager=True)
-    rec["frac_int8_peak"] = round(rec["tflops"] / INT8_PEAK_TOPS, 4)
+        5, 1), flops=2 * 128 * 128 * 11 * L8, sets=3, reps=10, eager=True, mfma="i8")
     del xq, oq
     xt = B.replicate(D(r.normal(0, 1, (1, 512, 240)).astype(np.float32)), 4)
     wt = D(r.integers(-127, 128, (512, 256, 20)).astype(np.int8))
@@ -359,7 +370,63 @@ def run_gpu(args):
     ot = [kk.DeviceTensor.empty((1, 256, 2400)) for _ in range(4)]
     per_op("convT_i8_512x256_k20_s10", lambda i: B.call(
         "kk_conv_transpose1d", ot[i].desc(), xt[i].desc(), wt.desc(), sct.desc(), None, None, 10, 1,
-        5, 5, 1, 0), flops=2 * 512 * 256 * 2400 * 20 // 10, sets=4, eager=True)
+        5, 5, 1, 0), flops=2 * 512 * 256 * 2400 * 20 // 10, sets=4, eager=True, mfma="f16x2")
+
+    # The decoder upsample stage as one chain (13 launches): int8
+    # ConvTranspose1d 512->256 (k20, s10, p5) on [1,512,240], snake, AdaIN
+    # (style [1,128], Linear 128->512), then two residual blocks AdaIN ->
+    # snake -> int8 Conv1d 256->256 k3 (dilation 1, then 3) -> AdaIN -> snake
+    # -> int8 Conv1d k3 -> + input; per-tensor int8 scales.  Eager: the
+    # convolutions draw workspace from the pool.
+    qt4 = D(r.integers(-127, 128, (512, 256, 20)).astype(np.int8))
+    st4 = D(np.array(r.uniform(1e-3, 1e-2), np.float32))
+    sty4 = D(r.normal(0, 0.1, (1, 128)).astype(np.float32))
+    al4 = [D(r.uniform(0.5, 2, (1, 256, 1)).astype(np.float32)) for _ in range(5)]
+    fc4 = [D(r.normal(0, 0.05, (128, 512)).astype(np.float32)) for _ in range(5)]
+    cv4 = [(D(r.integers(-127, 128, (256, 256, 3)).astype(np.int8)),
+            D(np.array(r.uniform(1e-3, 1e-2), np.float32))) for _ in range(4)]
+    ops_ = kk.ops
+
+    def stage4(i):
+        h = ops_.conv_transpose1d(xt[i], qt4, None, (5, 5), 10, w_scale=st4)
+        h = ops_.adain(ops_.snake(h, al4[0]), sty4, fc4[0], None, 1e-5)
+        for blk, dil in enumerate((1, 3)):
+            y = ops_.snake(ops_.adain(h, sty4, fc4[1 + 2 * blk], None, 1e-5), al4[1 + 2 * blk])
+            q, s = cv4[2 * blk]
+            y = ops_.conv1d(y, q, None, (dil, dil), 1, dil, w_scale=s)
+            y = ops_.snake(ops_.adain(y, sty4, fc4[2 + 2 * blk], None, 1e-5), al4[2 + 2 * blk])
+            q, s = cv4[2 * blk + 1]
+            y = ops_.conv1d(y, q, None, (1, 1), w_scale=s)
+            h = ops_.binary("Add", h, y)
+        return h
+
+    flops4 = 2 * 512 * 256 * 2400 * 20 // 10 + 4 * 2 * 256 * 256 * 3 * 2400
+    rec = per_op("decoder_upsample_stage_1x512x240", stage4, flops=flops4, sets=4, reps=10,
+                 eager=True)
+    rec["launches"] = 13
+    rec["workload"] = ("int8 ConvT 512->256 k20 s10 + snake + AdaIN, then 2 residual blocks "
+                       "(AdaIN, snake, int8 Conv1d 256 k3 d1/d3, AdaIN, snake, Conv1d k3, Add)")
+
+    # The output stage at the 128-id waveform's length (~2.15M samples): the
+    # 1023-tap notch FIR (fp32 FMAs: 2 * 1023 flops per sample), the PCM16
+    # conversion (4 B read, 2 B written per sample) and both in one pass.
+    aud = importlib.import_module("best-tts-godot_amd.audio")
+    ns = 2154000
+    na = max(2, -(-ROTATE_BYTES // (6 * ns)))
+    wav = B.replicate(D((0.25 * r.normal(0, 1, ns)).astype(np.float32)), na)
+    taps = D(aud.notch_taps())
+    ntap = int(taps.shape[0])
+    wout = [kk.DeviceTensor.empty((ns,)) for _ in range(na)]
+    pout = [kk.DeviceTensor.empty((2 * ns,), np.uint8) for _ in range(na)]
+    per_op("fir_notch_1023_x2154000", lambda i: B.call(
+        "kk_fir", wout[i].desc(), wav[i].desc(), taps.desc(), -1), flops=2 * ntap * ns, sets=na,
+        reps=5)
+    rec = per_op("pcm16_x2154000", lambda i: B.call("kk_pcm16", pout[i].desc(), wav[i].desc(), 1.0),
+                 6 * ns, sets=na)
+    rec = per_op("fir_pcm16_x2154000", lambda i: B.call(
+        "kk_fir_pcm16", pout[i].desc(), wav[i].desc(), taps.desc(), -1, 1.0), 6 * ns,
+        flops=2 * ntap * ns, sets=na, reps=5)
+    del wav, wout, pout
 
     roofline = {
         "kernel": "instnorm_wide_kernel (AdaIN T=9600, style Linear fused)",

@@ -454,53 +454,112 @@ def test_fp16_weight_conv_small_activations(gpu, oracle, sigma, kind):
     check(got, want, f"{kind} sigma {sigma}")
 
 
-def test_decoder_upsample_stage(gpu, oracle):
-    """int8 ConvTranspose1d(512->256, k20, s10, p5) on [1,512,240], snake,
-    AdaIN with style [1,128], then two residual blocks
+def decoder_stage(r):
+    """The decoder upsample stage's operands (the fixed draws of the stage
+    tests and of the bench): int8 ConvTranspose1d(512->256, k20, s10, p5)
+    on [1,512,240], snake, AdaIN with style [1,128], then two residual blocks
     AdaIN -> snake -> conv(d) -> AdaIN -> snake -> conv(d1) -> + x with
     dilations 1 and 3 (int8 weights, per-tensor scales)."""
-    r = rng(0)
-    x = r.normal(0, 1, (1, 512, 240)).astype(np.float32)
-    style = r.normal(0, 0.1, (1, 128)).astype(np.float32)
-    qt, st = int8_weight(r, (512, 256, 20))
-    alphas = [r.uniform(0.5, 2, (1, 256, 1)).astype(np.float32) for _ in range(5)]
-    fcs = [r.normal(0, 0.05, (128, 512)).astype(np.float32) for _ in range(5)]
-    convs = [int8_weight(r, (256, 256, 3)) for _ in range(4)]
+    return dict(
+        x=r.normal(0, 1, (1, 512, 240)).astype(np.float32),
+        style=r.normal(0, 0.1, (1, 128)).astype(np.float32),
+        convt=int8_weight(r, (512, 256, 20)),
+        alphas=[r.uniform(0.5, 2, (1, 256, 1)).astype(np.float32) for _ in range(5)],
+        fcs=[r.normal(0, 0.05, (128, 512)).astype(np.float32) for _ in range(5)],
+        convs=[int8_weight(r, (256, 256, 3)) for _ in range(4)])
 
-    def run(lib):
-        if lib is None:
-            h = oracle.conv_transpose1d(x, oracle.dequantize(qt, st), None, (5, 5), 10)
-            h = oracle.snake(h, alphas[0])
-            h = oracle.adain(h, style, fcs[0], None, 1e-5)
-            for blk, dil in enumerate((1, 3)):
-                y = oracle.adain(h, style, fcs[1 + 2 * blk], None, 1e-5)
-                y = oracle.snake(y, alphas[1 + 2 * blk])
-                q, s = convs[2 * blk]
-                y = oracle.conv1d(y, oracle.dequantize(q, s), None, (dil, dil), 1, dil)
-                y = oracle.adain(y, style, fcs[2 + 2 * blk], None, 1e-5)
-                y = oracle.snake(y, alphas[2 + 2 * blk])
-                q, s = convs[2 * blk + 1]
-                y = oracle.conv1d(y, oracle.dequantize(q, s), None, (1, 1))
-                h = oracle.binary("Add", h, y)
-            return h
-        D = lib.to_device
-        sty = D(style)
-        h = lib.ops.conv_transpose1d(D(x), D(qt), None, (5, 5), 10, w_scale=D(np.array(st)))
-        h = lib.ops.snake(h, D(alphas[0]))
-        h = lib.ops.adain(h, sty, D(fcs[0]), None, 1e-5)
-        for blk, dil in enumerate((1, 3)):
-            y = lib.ops.adain(h, sty, D(fcs[1 + 2 * blk]), None, 1e-5)
-            y = lib.ops.snake(y, D(alphas[1 + 2 * blk]))
-            q, s = convs[2 * blk]
-            y = lib.ops.conv1d(y, D(q), None, (dil, dil), 1, dil, w_scale=D(np.array(s)))
-            y = lib.ops.adain(y, sty, D(fcs[2 + 2 * blk]), None, 1e-5)
-            y = lib.ops.snake(y, D(alphas[2 + 2 * blk]))
-            q, s = convs[2 * blk + 1]
-            y = lib.ops.conv1d(y, D(q), None, (1, 1), w_scale=D(np.array(s)))
-            h = lib.ops.binary("Add", h, y)
-        return h.numpy()
 
-    got, want = run(gpu), run(None)
-    # Five normalisations in series amplify per-op rounding; the chain is
-    # held to 10x the single-op bar.
-    assert_close(got, want, 1e-3, floor_rel=1e-4, what="decoder stage")
+def decoder_stage_ops(P):
+    """The stage as a list of (name, bar, run(lib_or_None, inputs...)) steps,
+    each taking the previous step's output (and, for the residual Add, the
+    stage input of its block); lib None runs the oracle."""
+    qt, st = P["convt"]
+
+    def convt(L, O, h):
+        if L is None:
+            return O.conv_transpose1d(h, O.dequantize(qt, st), None, (5, 5), 10)
+        return L.ops.conv_transpose1d(L.to_device(h), L.to_device(qt), None, (5, 5), 10,
+                                      w_scale=L.to_device(np.array(st))).numpy()
+
+    def snake(i):
+        def f(L, O, h):
+            a = P["alphas"][i]
+            return O.snake(h, a) if L is None else \
+                L.ops.snake(L.to_device(h), L.to_device(a)).numpy()
+        return f
+
+    def adain(i):
+        def f(L, O, h):
+            if L is None:
+                return O.adain(h, P["style"], P["fcs"][i], None, 1e-5)
+            return L.ops.adain(L.to_device(h), L.to_device(P["style"]), L.to_device(P["fcs"][i]),
+                               None, 1e-5).numpy()
+        return f
+
+    def conv(i, dil):
+        def f(L, O, h):
+            q, s = P["convs"][i]
+            if L is None:
+                return O.conv1d(h, O.dequantize(q, s), None, (dil, dil), 1, dil)
+            return L.ops.conv1d(L.to_device(h), L.to_device(q), None, (dil, dil), 1, dil,
+                                w_scale=L.to_device(np.array(s))).numpy()
+        return f
+
+    ew, red, mm = (1e-5, 1e-6), (1e-4, 1e-5), (1e-4, 1e-5)
+    steps = [("convT", mm, convt), ("snake0", ew, snake(0)), ("adain0", red, adain(0))]
+    for blk, dil in enumerate((1, 3)):
+        steps += [(f"res{blk}.adain1", red, adain(1 + 2 * blk)),
+                  (f"res{blk}.snake1", ew, snake(1 + 2 * blk)),
+                  (f"res{blk}.conv_d{dil}", mm, conv(2 * blk, dil)),
+                  (f"res{blk}.adain2", red, adain(2 + 2 * blk)),
+                  (f"res{blk}.snake2", ew, snake(2 + 2 * blk)),
+                  (f"res{blk}.conv1", mm, conv(2 * blk + 1, 1)),
+                  (f"res{blk}.add", (0.0, 0.0), "add")]
+    return steps
+
+
+def test_decoder_upsample_stage_teacher_forced(gpu, oracle):
+    """Every step of the decoder upsample stage against the oracle, each fed
+    the oracle's output of the step before: contractions and the AdaINs at
+    rel 1e-4 + 1e-5 max, the snakes at rel 1e-5 + 1e-6 max, the residual Add
+    bit for bit."""
+    P = decoder_stage(rng(0))
+    h = P["x"]
+    block_in = None
+    for name, (rtol, floor), fn in decoder_stage_ops(P):
+        if name.endswith("adain1"):
+            block_in = h
+        if fn == "add":
+            want = oracle.binary("Add", block_in, h)
+            got = gpu.ops.binary("Add", gpu.to_device(block_in), gpu.to_device(h)).numpy()
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=name)
+        else:
+            want = fn(None, oracle, h)
+            got = fn(gpu, oracle, h)
+            if rtol == RTOL:
+                check(got, want, f"decoder stage {name}")
+            else:
+                assert_close(got, want, rtol, floor_rel=floor, what=f"decoder stage {name}")
+        h = want
+
+
+def test_decoder_upsample_stage_free_running(gpu, oracle):
+    """The whole stage run through on each side: five normalisations in
+    series amplify the per-step rounding, so the end result is held to 10x
+    the single-step bar (each step is held to its own bar above)."""
+    P = decoder_stage(rng(0))
+
+    def run(L):
+        h = P["x"]
+        block_in = None
+        for name, _bar, fn in decoder_stage_ops(P):
+            if name.endswith("adain1"):
+                block_in = h
+            if fn == "add":
+                h = oracle.binary("Add", block_in, h) if L is None else \
+                    L.ops.binary("Add", L.to_device(block_in), L.to_device(h)).numpy()
+            else:
+                h = fn(L, oracle, h)
+        return h
+
+    assert_close(run(gpu), run(None), 1e-3, floor_rel=1e-4, what="decoder stage")
