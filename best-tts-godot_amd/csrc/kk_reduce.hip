@@ -270,10 +270,18 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
   float mean, var;
   row_stats<GROUP, NV, VEC, true>(r, T, g, lds, mean, var);
   const float den = sqrtf(var + eps);
+  if (af.mode == 2) {  // AdaIN (held to rel 1e-4): one division per row
+    const float inv = 1.0f / den;
 #pragma unroll
-  for (int j = 0; j < NV; ++j)
+    for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) r[j][e] = apply_affine<false>(r[j][e] / den, ra, af);
+      for (int e = 0; e < VEC; ++e) r[j][e] = apply_affine<false>(r[j][e] * inv, ra, af);
+  } else {  // the InstanceNorm chain's own Div, per element
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) r[j][e] = apply_affine<false>(r[j][e] / den, ra, af);
+  }
   store_row<GROUP, NV, VEC>(out + row * T, T, g, r);
 }
 
@@ -370,11 +378,12 @@ __global__ void __launch_bounds__(64 * NW) instnorm_wide_kernel(float* __restric
       if (base + e < T) q += d * d;
     }
   }
-  const float den = sqrtf(wide_sum<NW>(q, lds) / static_cast<float>(T) + eps);
+  // one division per row (AdaIN is held to rel 1e-4)
+  const float inv = 1.0f / sqrtf(wide_sum<NW>(q, lds) / static_cast<float>(T) + eps);
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[j][e] = apply_affine<false>(r[j][e] / den, ra, af);
+    for (int e = 0; e < 4; ++e) r[j][e] = apply_affine<false>(r[j][e] * inv, ra, af);
   store_row<G, NV, 4>(out + row * T, T, g, r);
 }
 
@@ -633,11 +642,11 @@ __global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict_
   if (la.bias) load_row<GROUP, NV, VEC, false>(la.bias, cols, g, bi);
   float mean, var;
   row_stats<GROUP, NV, VEC, true>(r, cols, g, lds, mean, var);
-  const float den = sqrtf(var + eps);
+  const float inv = 1.0f / sqrtf(var + eps);  // one division per row (rel 1e-4 bar)
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) r[j][e] = (r[j][e] / den) * sc[j][e];
+    for (int e = 0; e < VEC; ++e) r[j][e] = (r[j][e] * inv) * sc[j][e];
   if (la.bias) {
 #pragma unroll
     for (int j = 0; j < NV; ++j)
@@ -716,11 +725,11 @@ __global__ void __launch_bounds__(kRowBlock) softmax_kernel(float* __restrict__ 
       if (base + e < cols) s += v;
     }
   }
-  s = group_sum<GROUP, true>(s, lds);
+  const float inv = 1.0f / group_sum<GROUP, true>(s, lds);  // one division per row (rel 1e-4)
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] / s;
+    for (int e = 0; e < VEC; ++e) r[j][e] = r[j][e] * inv;
   store_row<GROUP, NV, VEC>(out + row * cols, cols, g, r);
 }
 
