@@ -71,7 +71,7 @@ __device__ __forceinline__ float apply_f32(float a, float b, float c, float alph
   else if constexpr (OP == KK_OP_POW) return b == 2.0f ? a * a : powf(a, b);
   else if constexpr (OP == KK_OP_SQRT) return sqrtf(a);
   else if constexpr (OP == KK_OP_EXP) return expf(a);
-  else if constexpr (OP == KK_OP_SIN) return sinf(a);
+  else if constexpr (OP == KK_OP_SIN) return kk_sin(a);
   else if constexpr (OP == KK_OP_COS) return cosf(a);
   else if constexpr (OP == KK_OP_ATAN) return atanf(a);
   else if constexpr (OP == KK_OP_TANH) return tanhf(a);
@@ -89,7 +89,7 @@ __device__ __forceinline__ float apply_f32(float a, float b, float c, float alph
   else if constexpr (OP == OPX_SNAKE || OP == OPX_SNAKE_ALPHA) {
     // Mul(alpha, x) -> Sin -> Pow(., 2) -> Mul(recip, .) -> Add(x, .)
     const float r = (OP == OPX_SNAKE) ? c : 1.0f / b;
-    const float s = sinf(b * a);
+    const float s = kk_sin(b * a);
     const float p = s * s;
     const float q = r * p;
     return a + q;
