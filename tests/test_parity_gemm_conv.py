@@ -346,6 +346,9 @@ F16MC = [  # (kind, n, cin, cout, k, L, p0, p1, s, d, op, wdt)
     ("convT", 1, 256, 128, 12, 1000, 3, 3, 6, 1, 0, "u8c"),     # uint8, per-channel scale + zp
     ("conv", 1, 256, 96, 3, 6000, 1, 1, 1, 2, 0, "i8"),         # int8 per tensor, dilation 2
     ("conv", 1, 128, 64, 5, 8000, 2, 2, 1, 1, 0, "u8c"),        # uint8, per-channel scale + zp
+    # input channels a multiple of the 32-wide K step but not of 64
+    ("conv", 1, 96, 64, 3, 12000, 1, 1, 1, 1, 0, "i8"),
+    ("convT", 1, 160, 64, 12, 1200, 3, 3, 6, 1, 0, "f16"),
 ]
 
 
