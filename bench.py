@@ -47,6 +47,8 @@ ROTATE_BYTES = 640 << 20    # > 2x the 256 MB Infinity Cache
 MFMA_PEAKS = {
     "fp32": ("fp32 MFMA (v_mfma_f32_16x16x4_f32)", 157.3),
     "bf16x3": ("bf16 MFMA, activations in 3 bf16 parts (v_mfma_f32_32x32x16_bf16 x3)", 2500.0 / 3),
+    "bf16x6": ("bf16 MFMA, activations in 3 bf16 parts, fp16 weights in 2 "
+               "(v_mfma_f32_32x32x16_bf16 x6)", 2500.0 / 6),
     "f16x2": ("fp16 MFMA, activations in 2 fp16 parts (v_mfma_f32_32x32x16_f16 x2)", 1250.0),
     "i8": ("int8 MFMA (v_mfma_i32_32x32x32_i8)", INT8_PEAK_TOPS),
 }
@@ -354,7 +356,7 @@ def run_gpu(args):
         o = [kk.DeviceTensor.empty((m, n)) for _ in range(4)]
         per_op(name, lambda i: B.call("kk_gemm", o[i].desc(), a[i].desc(), wq.desc(),
                                       sc.desc() if sc else None, None, 1.0),
-               flops=2 * m * n * k, sets=4, mfma="bf16x3" if wdt == "i8" else "fp32")
+               flops=2 * m * n * k, sets=4, mfma="bf16x3" if wdt == "i8" else "bf16x6")
 
     gemm_case("gemm_i8_256x768x2048", 256, 768, 2048, "i8")
     gemm_case("gemm_i8_256x2048x768", 256, 2048, 768, "i8")

@@ -70,15 +70,21 @@ def test_per_column_dequant_u8_and_i8(gpu, oracle):
     check(got, oracle.matmul(a, oracle.dequantize(u, np.float32(0.01), np.uint8(128))), "uint8")
 
 
-@pytest.mark.parametrize("m,k,n,wdt", [(1024, 256, 1024, "i8"),   # 64x64 tiles
-                                       (256, 768, 2048, "i8"),    # 32x64, K over two waves
-                                       (256, 768, 768, "u8"),     # 32x32, K over four waves
-                                       (1, 100, 36, "i8"), (33, 36, 100, "f16"),
-                                       (70, 4, 8, "u8"), (300, 2052, 68, "i8")])
+@pytest.mark.parametrize("m,k,n,wdt", [(1024, 256, 1024, "i8"),   # 32x64 tiles, eight waves
+                                       (256, 768, 2048, "i8"),    # 32x64, eight waves
+                                       (256, 512, 1024, "u8"),    # 32x32, four waves
+                                       (256, 768, 768, "u8"),     # 32x32, eight waves
+                                       (256, 768, 768, "f16"),    # the same, two weight planes
+                                       (1024, 256, 1024, "f16"),  # 32x64, four waves, two planes
+                                       (1, 100, 36, "i8"),        # waves with no K-steps
+                                       (33, 36, 100, "f16"),
+                                       (70, 4, 8, "u8"),
+                                       (300, 2052, 68, "i8"),     # runs of 8 and 9 K-steps
+                                       (300, 2052, 68, "f16")])
 def test_dequant_matmul_bf16_split_accuracy(gpu, oracle, m, k, n, wdt):
-    """The 8-bit-weight MatMul on the bf16 matrix cores (activations split
-    into three bf16 parts, every product exact; fp16 weights take the fp32
-    matrix cores): the oracle's bar, and no less accurate than numpy's own
+    """The 8-bit- and fp16-weight MatMul on the bf16 matrix cores
+    (activations split into three bf16 parts, fp16 weights into two, every
+    product exact): the oracle's bar, and no less accurate than numpy's own
     fp32 result against a float64 product (K and N off the tile sizes,
     M = 1, per-column and per-tensor zero points of both byte types)."""
     r = rng(12)
@@ -139,6 +145,49 @@ def test_dequant_matmul_activation_range(gpu, oracle, mag):
     fin = np.isfinite(want)
     assert np.array_equal(np.sign(got[np.isinf(want)]), np.sign(want[np.isinf(want)]))
     check(np.where(fin, got, 0), np.where(fin, want, 0), "finite rows beside inf/NaN")
+
+
+def test_fp16_matmul_nonfinite_and_extreme_weights(gpu, oracle):
+    """fp16 weights on the bf16 matrix cores: subnormal, largest and
+    zero weights at fp32 accuracy; an infinite or NaN weight or activation
+    gives numpy's inf / NaN pattern (those calls take the exact scalar
+    tiles), and the next finite call is back on the matrix cores."""
+    r = rng(14)
+    m, k, n = 64, 320, 96
+    a = r.normal(0, 1, (m, k)).astype(np.float32)
+    w = r.normal(0, 0.05, (k, n)).astype(np.float16)
+    w[:40, 3] = np.float16(6.0e-8)      # fp16 subnormals (2^-24 steps)
+    w[40:80, 3] = np.float16(3.0e-6)
+    w[5, 7] = np.float16(65504.0)       # the largest fp16
+    w[:, 9] = 0
+    w[::7, 11] = np.float16(1.0)        # 8 significant bits or fewer: second plane 0
+    dv = gpu.to_device
+
+    def run(a_, w_):
+        return gpu.ops.matmul(dv(a_), dv(w_)).numpy()
+
+    def same_nonfinite(got, want, what):
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(want), err_msg=what)
+        np.testing.assert_array_equal(np.isinf(got), np.isinf(want), err_msg=what)
+        inf = np.isinf(want)
+        assert np.array_equal(np.sign(got[inf]), np.sign(want[inf])), what
+        fin = np.isfinite(want)
+        check(np.where(fin, got, 0), np.where(fin, want, 0), what)
+
+    check(run(a, w), oracle.matmul(a, w.astype(np.float32)), "fp16 extremes")
+    w2 = w.copy()
+    w2[17, 20], w2[30, 21], w2[31, 21] = np.inf, -np.inf, np.inf   # column 21: inf - inf
+    w2[50, 22] = np.nan
+    a2 = a.copy()
+    a2[4, 17] = 0.0                     # 0 * inf in row 4, column 20
+    with np.errstate(invalid="ignore", over="ignore"):
+        same_nonfinite(run(a2, w2), oracle.matmul(a2, w2.astype(np.float32)), "inf/NaN weights")
+    w[100, 30] = np.float16(0.5)        # second plane 0: inf * (b0 + 0) must stay inf
+    a3 = a.copy()
+    a3[6, 100], a3[8, 5] = np.inf, np.nan
+    with np.errstate(invalid="ignore", over="ignore"):
+        same_nonfinite(run(a3, w), oracle.matmul(a3, w.astype(np.float32)), "inf/NaN activations")
+    check(run(a, w), oracle.matmul(a, w.astype(np.float32)), "finite call after a stamped one")
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 13, 5), (33, 65, 97), (130, 512, 50),
