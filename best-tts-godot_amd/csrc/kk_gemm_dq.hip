@@ -21,318 +21,51 @@
 // v_mfma_f32_32x32x16_bf16 per pair of parts (three for 8-bit weights, six
 // for fp16) accumulates them in fp32.  The scale (per tensor or per column)
 // multiplies the fp32 sum, where the numpy reference scales each weight
-// first: the same value up to fp32 rounding.  For a = +-inf, a0 = a and
-// a1 = a2 = 0 (likewise for b); a NaN gives NaN parts.  With 8-bit weights
-// that reproduces numpy's inf and NaN outputs (inf * (q - z) is inf, or NaN
-// at q = z, as in numpy); with fp16 weights a part of 0 meets an infinite
-// one (a0 * b1 with b1 = 0), which gives NaN where numpy has +-inf.  So the
-// fp16 prep stamps a flag with the call's number when any operand is not
-// finite, and a block that finds its call's stamp computes its tile with
-// scalar fp32 products of the reassembled operands (a0 + a1 + a2 and
-// b0 + b1 are a and b exactly, infinities and NaN included) instead.  A
-// stale stamp (a recorded graph replays its calls' numbers) only costs that
-// slower path.
+// first: the same value up to fp32 rounding.
 //
-// Two launches.  gemm_dq_prep writes the operands once, into the library
-// scratch: A as three bf16 planes and B as one or two, each of Mp x Kp
-// (Np x Kp) values (M, N, K rounded up to the padding below, zero-filled;
-// 8-bit B is filled with its zero point past K), in fragment order: the
-// values of rows 32 t .. 32 t + 31 and K-step s (k = 32 s .. 32 s + 31) are
-// two fragments of 64 lanes x 8 bf16 (half h), lane l holding row
-// 32 t + l % 32 at k = 32 s + 16 (l / 32) + 8 h + 0..7, so that one
-// 16-byte load per lane is its share of a matrix-core operand (row =
-// lane % 32, 8 consecutive k) and a wave's load is 1 KB of consecutive
-// bytes.  Splitting inside the GEMM instead repeated the split for every
-// block column (and B's conversion for every block row) and left the
-// kernel VALU-bound at 4-5x its matrix-core time.
+// One launch.  A block owns a 32 x (32 NT) output tile; each of its KS
+// waves takes a run of 32-wide K-steps and, per step, loads the raw
+// operands with coalesced 16-byte buffer loads (A: 32 rows x 128 bytes of
+// fp32; B: 32 k rows of 32 NT weights) into a register ring that keeps the
+// next steps in flight, stages them in its own LDS region (no block
+// barrier in the K loop), reads them back as matrix-core operands -- A rows
+// with 16-byte reads, B columns with the transposing reads
+// ds_read_b64_tr_b8 (8-bit: each lane gets 8 consecutive k of its column)
+// or ds_read_b64_tr_b16 (fp16: 4 consecutive k per read) -- splits and
+// converts them in registers and accumulates into 2 NT independent 32x32
+// tiles (one per half of each K-step).  The waves' partial tiles are summed
+// through LDS in wave order.  Buffer loads past an operand's last byte
+// return zeros, so rows past M, weight rows past K and the ragged edges
+// need no per-lane branches; activation columns past K (the next row's
+// values when K is not a multiple of 32) are cleared in the last K-step.
+// Non-finite operands need no check per value: split without a guard, an
+// infinite activation gives a1 = inf - inf = NaN (likewise b1 for an
+// infinite fp16 weight, and a NaN gives NaN parts), and a NaN part makes
+// every output it meets NaN on the matrix cores (NaN * 0 is NaN), so a
+// block whose accumulators hold a NaN computes its tile with scalar fp32
+// products instead (numpy's inf / NaN pattern).  Any other NaN there
+// (overflowing sums) takes that path too, which is exact as well.
 //
-// gemm_bf16_kernel: every wave loads its fragments straight into
-// registers, with no LDS staging and no barrier in the K loop (with the
-// operands row-major instead, each load touched 32 rows and the kernel was
-// slower than the staged one).  A block of KS waves owns a 32 x (32 NT) output tile; wave w takes
-// the w-th of KS consecutive runs of 32-wide K-steps, keeps the loads of its
-// next RING steps in flight in a register ring and accumulates into 2 NT
-// independent 32x32 tiles (one per half of each K-step, so consecutive
-// matrix-core operations do not wait on one another).  At the end the
-// waves hand their partial tiles through LDS and each sums a share of the
-// tile in wave order and writes it.  An earlier form staged both operands
-// through LDS with a barrier per K-step and one accumulator per wave: at
-// 256 x 768 x 2048 its waves spent half their time waiting (10.0 us).
-// Splitting K over blocks as well (the last block of a tile to arrive
-// summing the partial tiles) measured slower: at M = 256 the partials'
-// round trip through the device-coherent level costs more than the added
-// blocks gain.
+// What was measured on the way (per call at 256 x 768 x 2048 int8 / fp16
+// 256 x 768 x 768): operands prepared by a first launch (A as three bf16
+// planes, B converted and transposed, in the matrix-core fragment order)
+// and a GEMM loading them straight into registers, 12.3 / 11.7 us -- two
+// dependent launches, each waiting on a full memory round trip, and 6
+// bytes of activation planes per value through L2; this one launch,
+// 8.7 / 6.9 us.  A check per value for non-finite operands compiled to
+// about 3.5 VALU instructions a value (the loop is VALU-bound) and gave way
+// to the accumulator test.
 #include <algorithm>
 #include <type_traits>
 
 #include "kk_internal.h"
 
 namespace kk {
-namespace gdq {
-
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef float f16v __attribute__((ext_vector_type(16)));
-typedef unsigned u4 __attribute__((ext_vector_type(4)));
-
-constexpr int kPadM = 64, kPadN = 64, kPadK = 128;  // prepared operand padding
-
-// ------------------------------------------------------------- operand prep
-// a = a0 + a1 + a2 (see the top of the file): each part's bf16 bits are the
-// upper half of the returned word (the lower half is not used).
-__device__ __forceinline__ void split3(float a, unsigned& h0, unsigned& h1, unsigned& h2) {
-  const unsigned u = __float_as_uint(a);
-  const float a0 = __uint_as_float(u & 0xffff0000u);
-  const float r = a0 == a ? 0.0f : a - a0;
-  const unsigned ur = __float_as_uint(r);
-  h0 = u;
-  h1 = ur;
-  h2 = __float_as_uint(r - __uint_as_float(ur & 0xffff0000u));
-}
+namespace gfu {
 
 // The upper halves of lo and hi as two packed bf16 (lo first).
 __device__ __forceinline__ unsigned pack_hi(unsigned lo, unsigned hi) {
   return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
-}
-
-// Offset (in bf16) of the 8-value lane chunk of fragment (row tile t,
-// K-step s, half h), lane l, within a plane of nk K-steps.
-__device__ __forceinline__ int64_t frag_chunk(int64_t t, int64_t s, int h, int l, int64_t nk) {
-  return ((t * nk + s) * 2 + h) * 512 + l * 8;
-}
-
-// Offset of value (row, k) within a plane of nk K-steps.
-__device__ __forceinline__ int64_t frag_index(int64_t row, int64_t k, int64_t nk) {
-  const int kk = static_cast<int>(k & 31);
-  return frag_chunk(row >> 5, k >> 5, (kk >> 3) & 1, static_cast<int>(row & 31) + 32 * (kk >> 4),
-                    nk) +
-         (kk & 7);
-}
-
-struct PrepArgs {
-  const float* a;  // A [M, K] rows a_si apart, K contiguous (K % 4 == 0, 16-byte aligned rows)
-  int64_t a_si;
-  const void* b;   // B [K, N] rows b_si apart, N contiguous (N % 4 == 0)
-  int64_t b_si;
-  int b_dt;        // KK_I8, KK_U8 or KK_F16
-  const void* zp;  // zero point (same type as 8-bit B) or NULL
-  int64_t zp_stride;
-  __bf16* ap;      // 3 planes of Mp x Kp, fragment order
-  __bf16* bp;      // BP planes of Np x Kp, fragment order (BP = 2 for fp16 B, else 1)
-  int64_t M, N, K, Mp, Np, Kp;
-  int a_blocks;    // blocks [0, a_blocks) split A (a lane chunk per thread); the rest
-                   // convert B tiles of 64 k x 64 n
-  int* flag;       // fp16 B: set to seq when an operand is not finite; else NULL
-  int seq;
-};
-
-__device__ __forceinline__ bool f32_nonfinite(float x) {
-  return (__float_as_uint(x) & 0x7f800000u) == 0x7f800000u;
-}
-
-constexpr int kTileRow = 64 * 2 + 16;  // LDS bytes per n row of a B tile: 64 k of 2 bytes, padded
-
-__global__ void __launch_bounds__(256) gemm_dq_prep(PrepArgs P) {
-  __shared__ __align__(16) unsigned char tile[64 * kTileRow];  // [n][k], 2 bytes per k
-  const int tid = threadIdx.x;
-  if (static_cast<int>(blockIdx.x) < P.a_blocks) {
-    // thread -> lane chunk q: lane q % 64, half (q / 64) % 2, K-step
-    // (q / 128) % nk, row tile q / (128 nk); each plane's chunk is written
-    // whole, so a wave writes 1 KB of consecutive bytes per plane
-    const int64_t nk = P.Kp / 32;
-    const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + tid;
-    if (q >= P.Mp * P.Kp / 8) return;
-    const int l = static_cast<int>(q & 63), h = static_cast<int>((q >> 6) & 1);
-    const int64_t st = q >> 7, s = st % nk, t = st / nk;
-    const int64_t m = 32 * t + (l & 31), k = 32 * s + 16 * (l >> 5) + 8 * h;
-    float v[8];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {  // K % 4 == 0: four values or none
-      float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      if (m < P.M && k + 4 * e < P.K)
-        x = *reinterpret_cast<const float4*>(P.a + m * P.a_si + k + 4 * e);
-      v[4 * e] = x.x;
-      v[4 * e + 1] = x.y;
-      v[4 * e + 2] = x.z;
-      v[4 * e + 3] = x.w;
-    }
-    unsigned hp[3][8];
-    bool bad = false;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      bad |= f32_nonfinite(v[e]);
-      split3(v[e], hp[0][e], hp[1][e], hp[2][e]);
-    }
-    if (P.flag && bad) *P.flag = P.seq;  // every writer stores the same value
-    const int64_t off = frag_chunk(t, s, h, l, nk);
-#pragma unroll
-    for (int pl = 0; pl < 3; ++pl)
-      *reinterpret_cast<uint4*>(P.ap + pl * P.Mp * P.Kp + off) =
-          make_uint4(pack_hi(hp[pl][0], hp[pl][1]), pack_hi(hp[pl][2], hp[pl][3]),
-                     pack_hi(hp[pl][4], hp[pl][5]), pack_hi(hp[pl][6], hp[pl][7]));
-    return;
-  }
-  // a B tile: k0..k0+63 x n0..n0+63, read n-contiguous, written k-contiguous
-  const int64_t bt = blockIdx.x - P.a_blocks, ntn = P.Np / 64;
-  const int64_t k0 = (bt / ntn) * 64, n0 = (bt % ntn) * 64;
-  const bool f16 = P.b_dt == KK_F16;
-  // stage: thread -> k rows tid / 16 + 16 j, n quad tid % 16; each weight's
-  // raw bits (a byte zero-extended, or the fp16 encoding) go to its [n][k]
-  // slot
-  {
-    const int nq = tid % 16;
-    const int64_t n = n0 + 4 * nq;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kr = tid / 16 + 16 * j;
-      const int64_t k = k0 + kr;
-      const bool in = k < P.K && n < P.N;  // N % 4 == 0: four columns or none
-      unsigned short e[4] = {0, 0, 0, 0};
-      if (f16) {
-        if (in) {
-          const uint2 u =
-              *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(P.b) + k * P.b_si + n);
-          e[0] = static_cast<unsigned short>(u.x & 0xffffu);
-          e[1] = static_cast<unsigned short>(u.x >> 16);
-          e[2] = static_cast<unsigned short>(u.y & 0xffffu);
-          e[3] = static_cast<unsigned short>(u.y >> 16);
-          if ((e[0] & 0x7c00u) == 0x7c00u || (e[1] & 0x7c00u) == 0x7c00u ||
-              (e[2] & 0x7c00u) == 0x7c00u || (e[3] & 0x7c00u) == 0x7c00u)
-            *P.flag = P.seq;  // an fp16 inf or NaN (every writer stores the same value)
-        }
-      } else {
-        // outside K: the zero point itself, so that q - zp = 0 there
-        unsigned u = 0u;
-        if (in) {
-          u = *reinterpret_cast<const unsigned*>(static_cast<const uint8_t*>(P.b) + k * P.b_si + n);
-        } else if (P.zp && n < P.N) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            u |= static_cast<unsigned>(static_cast<const uint8_t*>(P.zp)[(n + c) * P.zp_stride])
-                 << (8 * c);
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c) e[c] = static_cast<unsigned short>((u >> (8 * c)) & 0xffu);
-      }
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        *reinterpret_cast<unsigned short*>(&tile[(4 * nq + c) * kTileRow + 2 * kr]) = e[c];
-    }
-  }
-  __syncthreads();
-  // write: thread -> n row tid / 4, k values 16 (tid % 4) .. + 15: the
-  // chunks of halves 0 and 1 of lane n % 32 + 32 (tid % 2) in K-step
-  // (k0 + 16 (tid % 4)) / 32
-  const int nr = tid / 4, c = tid % 4, kc = 16 * c;
-  const int64_t n = n0 + nr;
-  const uint4* src = reinterpret_cast<const uint4*>(&tile[nr * kTileRow + 2 * kc]);
-  const uint4 s0 = src[0], s1 = src[1];
-  const unsigned w[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-  const int64_t nkb = P.Kp / 32;
-  __bf16* out0 = P.bp + frag_chunk(n >> 5, (k0 + kc) >> 5, 0, static_cast<int>(n & 31) + 32 * (c & 1),
-                                   nkb);
-  __bf16* out0h = out0 + 512;  // half 1 of the same lane
-  unsigned p[8], p1[8];
-  if (f16) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      unsigned h0[2], h1[2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const unsigned short bits = static_cast<unsigned short>((w[i] >> (16 * e)) & 0xffffu);
-        const float b = static_cast<float>(__builtin_bit_cast(_Float16, bits));  // exact
-        const float b0 = __uint_as_float(__float_as_uint(b) & 0xffff0000u);
-        h0[e] = __float_as_uint(b);
-        h1[e] = __float_as_uint(b0 == b ? 0.0f : b - b0);  // <= 3 significant bits: exact
-      }
-      p[i] = pack_hi(h0[0], h0[1]);
-      p1[i] = pack_hi(h1[0], h1[1]);
-    }
-  } else {
-    const bool i8 = P.b_dt == KK_I8;
-    float z = 0.0f;
-    if (P.zp && n < P.N) {
-      const uint8_t zb = static_cast<const uint8_t*>(P.zp)[n * P.zp_stride];
-      z = i8 ? static_cast<float>(static_cast<int8_t>(zb)) : static_cast<float>(zb);
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      unsigned h[2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const unsigned byte = (w[i] >> (16 * e)) & 0xffu;
-        const float q =
-            i8 ? static_cast<float>(static_cast<int8_t>(byte)) : static_cast<float>(byte);
-        h[e] = __float_as_uint(q - z);  // an integer of magnitude <= 255: exact in bf16
-      }
-      p[i] = n < P.N ? pack_hi(h[0], h[1]) : 0u;  // padding columns: zeros
-      p1[i] = 0u;
-    }
-  }
-  *reinterpret_cast<uint4*>(out0) = make_uint4(p[0], p[1], p[2], p[3]);
-  *reinterpret_cast<uint4*>(out0h) = make_uint4(p[4], p[5], p[6], p[7]);
-  if (f16) {
-    const int64_t pl = P.Np * P.Kp;
-    *reinterpret_cast<uint4*>(out0 + pl) = make_uint4(p1[0], p1[1], p1[2], p1[3]);
-    *reinterpret_cast<uint4*>(out0h + pl) = make_uint4(p1[4], p1[5], p1[6], p1[7]);
-  }
-}
-
-// ------------------------------------------------------------------- GEMM
-// NT 32-wide column tiles per block, KS waves splitting K, BP planes of B.
-template <int NT_, int KS_, int BP_>
-struct Shape {
-  static constexpr int NT = NT_, KS = KS_, BP = BP_;
-  static constexpr int BN = 32 * NT, THREADS = 64 * KS;
-  // 16-byte loads per lane per 32-wide K-step: two halves of 3 A planes and
-  // of BP B planes per column tile
-  static constexpr int LOADS = 2 * (3 + BP * NT);
-  static constexpr int RING = LOADS * 4 <= 40 ? 4 : 3;  // K-steps in flight (<= 42 loads)
-  static constexpr int SHARE = NT * 16 / KS;             // output registers each wave sums
-  static_assert(kPadN % BN == 0 && kPadK % 32 == 0, "the padding covers the tiles");
-  static_assert(SHARE * KS == NT * 16, "the tile's registers divide over the waves");
-};
-
-struct Args {
-  const __bf16* ap;   // 3 planes of Mp x Kp, fragment order
-  const __bf16* bp;   // BP planes of Np x Kp, fragment order
-  const void* scale;  // per tensor or per column, or NULL (1)
-  int scale_dt;
-  int64_t scale_stride;
-  float* out;
-  int64_t som, son;
-  int64_t M, N, Mp, Np, Kp;
-  float alpha;
-  const int* flag;  // fp16 B: equal to seq when an operand of this call is not finite
-  int seq;
-};
-
-// The tile of block (blockIdx.x, blockIdx.y) with scalar fp32 products of
-// the reassembled operands (a = a0 + a1 + a2 and b = b0 + b1 exactly),
-// summed in k order: numpy's results for infinite and NaN operands.
-template <class S>
-__device__ void exact_tile(const Args& G) {
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 32;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * S::BN;
-  const int64_t a_pl = G.Mp * G.Kp, b_pl = G.Np * G.Kp;
-  for (int e = threadIdx.x; e < 32 * S::BN; e += S::THREADS) {
-    const int64_t m = m0 + e / S::BN, n = n0 + e % S::BN;
-    if (m >= G.M || n >= G.N) continue;
-    const int64_t nk = G.Kp / 32;
-    float acc = 0.0f;
-    for (int64_t k = 0; k < G.Kp; ++k) {
-      const __bf16* ar = G.ap + frag_index(m, k, nk);
-      const __bf16* br = G.bp + frag_index(n, k, nk);
-      const float a = (static_cast<float>(ar[0]) + static_cast<float>(ar[a_pl])) +
-                      static_cast<float>(ar[2 * a_pl]);
-      float b = static_cast<float>(br[0]);
-      if (S::BP == 2) b += static_cast<float>(br[b_pl]);
-      acc += a * b;
-    }
-    const float sc = G.scale ? load_as_f32(G.scale, G.scale_dt, n * G.scale_stride) : 1.0f;
-    float v = acc * sc;
-    if (G.alpha != 1.0f) v *= G.alpha;
-    G.out[m * G.som + n * G.son] = v;
-  }
 }
 
 // Runs f(integral_constant<U>, t + U) for U = 0 .. R - 1 while t + U < end.
@@ -351,51 +84,154 @@ struct Unroll<R, R> {
   __device__ __forceinline__ static void run(F&, int, int) {}
 };
 
-template <class S>
-__global__ void __launch_bounds__(S::THREADS) gemm_bf16_kernel(Args G) {
-  constexpr int NT = S::NT, KS = S::KS, BP = S::BP, L = S::LOADS, R = S::RING;
-  __shared__ float red[KS][NT][16][64];  // partial tiles, [wave][tile][register][lane]
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef unsigned u4 __attribute__((ext_vector_type(4)));
+typedef int i2v __attribute__((ext_vector_type(2)));
+typedef short s4v __attribute__((ext_vector_type(4)));
+#define KK_LDS __attribute__((address_space(3)))
 
-  // the wave index as a uniform value, so that the K loop's bounds and
-  // branches are scalar
+// NT 32-wide column tiles, KS waves splitting K, BT bytes per weight (1:
+// 8-bit, 2: fp16).  Staging pitches keep the LDS reads free of bank
+// conflicts: A rows of 144 bytes (16 rows of a 16-byte read land on
+// distinct banks), B rows of 32 / 96 bytes (8-bit, two 16-lane groups of
+// transposing reads over 8 rows cover the 64 banks once) or 64 bytes (fp16,
+// 4 rows).
+template <int NT_, int KS_, int BT_>
+struct Shape {
+  static constexpr int NT = NT_, KS = KS_, BT = BT_;
+  static constexpr int BN = 32 * NT, THREADS = 64 * KS;
+  static constexpr int A_PITCH = 144;
+  static constexpr int B_ROW = BN * BT;  // bytes of one k row of the B tile
+  static constexpr int B_PITCH = BT == 1 ? (NT == 2 ? 96 : 32) : 64;
+  static constexpr int B_CH = B_ROW / 16;          // 16-byte chunks per B row
+  static constexpr int B_LOADS = 32 * B_CH / 64;   // 16-byte B loads per lane per K-step
+  static constexpr int LOADS = 4 + B_LOADS;
+  static constexpr int STAGE = 32 * A_PITCH + 32 * B_PITCH;  // one wave's staging bytes
+  static constexpr int RED = KS * NT * 16 * 64 * 4;          // the partial tiles
+  static constexpr int LDS = KS * STAGE > RED ? KS * STAGE : RED;
+  static constexpr int RING = KS == 8 ? 2 : 3;  // (two waves per SIMD share the registers)
+  static constexpr int SHARE = NT * 16 / KS;
+  static constexpr int B_ROWS_PER_LOAD = 64 / B_CH;  // B rows one 16-byte load per lane covers
+  static_assert(BT == 1 || NT == 1, "fp16 weights: 32-wide column tiles");
+  static_assert(B_LOADS * 64 == 32 * B_CH && SHARE * KS == NT * 16, "staging shape");
+};
+
+struct Args {
+  const float* a;     // [Mt, K], rows a_si apart
+  const void* b;      // [K, N], rows b_si apart (elements)
+  uint32_t a_bytes, b_bytes;  // extents from each base (past them loads return zeros)
+  int64_t a_si, b_si;
+  int b_dt;
+  const void* zp;     // 8-bit zero point or NULL
+  int64_t zp_stride;
+  const void* scale;  // per tensor or per column, or NULL (1)
+  int scale_dt;
+  int64_t scale_stride;
+  float* out;
+  int64_t som, son;
+  int64_t M, N, K;
+  float alpha;
+};
+
+__device__ __forceinline__ float zero_point(const Args& G, int64_t n) {
+  if (!G.zp || n >= G.N) return 0.0f;
+  const uint8_t zb = static_cast<const uint8_t*>(G.zp)[n * G.zp_stride];
+  return G.b_dt == KK_I8 ? static_cast<float>(static_cast<int8_t>(zb)) : static_cast<float>(zb);
+}
+
+// The tile with scalar fp32 products of the raw operands, summed in k order.
+template <class S>
+__device__ void exact_tile(const Args& G, int64_t m0, int64_t n0) {
+  for (int e = threadIdx.x; e < 32 * S::BN; e += S::THREADS) {
+    const int64_t m = m0 + e / S::BN, n = n0 + e % S::BN;
+    if (m >= G.M || n >= G.N) continue;
+    const float* ar = G.a + m * G.a_si;
+    float acc = 0.0f;
+    if (S::BT == 2) {
+      const _Float16* bc = static_cast<const _Float16*>(G.b) + n;
+      for (int64_t k = 0; k < G.K; ++k) acc += ar[k] * static_cast<float>(bc[k * G.b_si]);
+    } else {
+      const float z = zero_point(G, n);
+      const bool i8 = G.b_dt == KK_I8;
+      const uint8_t* bc = static_cast<const uint8_t*>(G.b) + n;
+      for (int64_t k = 0; k < G.K; ++k) {
+        const uint8_t q = bc[k * G.b_si];
+        const float qf = i8 ? static_cast<float>(static_cast<int8_t>(q)) : static_cast<float>(q);
+        acc += ar[k] * (qf - z);
+      }
+    }
+    const float sc = G.scale ? load_as_f32(G.scale, G.scale_dt, n * G.scale_stride) : 1.0f;
+    float v = acc * sc;
+    if (G.alpha != 1.0f) v *= G.alpha;
+    G.out[m * G.som + n * G.son] = v;
+  }
+}
+
+template <class S>
+__global__ void __launch_bounds__(S::THREADS) gemm_fused_kernel(Args G) {
+  constexpr int NT = S::NT, KS = S::KS, BT = S::BT, L = S::LOADS, R = S::RING;
+  __shared__ __align__(16) unsigned char lds[S::LDS];
+  __shared__ int bad_w[KS];
+
   const int lane = threadIdx.x & 63,
             wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 32;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * S::BN;
-  const int64_t Kp = G.Kp;
-  const int nk = static_cast<int>(Kp / 32);
+  const int nk = static_cast<int>((G.K + 31) / 32);
   const int s0 = wave * nk / KS, s1 = (wave + 1) * nk / KS;  // this wave's K-steps
-  if constexpr (BP == 2) {
-    if (*G.flag == G.seq) {  // a non-finite operand in this call
-      exact_tile<S>(G);
-      return;
-    }
-  }
 
-  // this lane's chunk of K-step 0, half 0 of the block's row tile of A and
-  // first column tile of B; K-step s, half h is 1024 s + 512 h further, the
-  // next column tile 1024 nk further
-  const __bf16* a_fr = G.ap + frag_chunk(m0 >> 5, 0, 0, lane, nk);
-  const __bf16* b_fr = G.bp + frag_chunk(n0 >> 5, 0, 0, lane, nk);
-  const int64_t a_pl = G.Mp * Kp, b_pl = G.Np * Kp, b_t = 1024 * static_cast<int64_t>(nk);
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(G.a), 0, static_cast<int>(G.a_bytes), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(G.b), 0, static_cast<int>(G.b_bytes), 0x00020000);
+  // this lane's loads: A row lane / 8 + 8 i, 16 bytes at 16 (lane % 8) of
+  // the K-step's 128; B row lane / B_CH + B_ROWS_PER_LOAD i, chunk
+  // lane % B_CH.  The whole offset goes in the per-lane register (the
+  // range check that returns zeros past the extent covers that offset), the
+  // row group's and K-step's parts formed as scalars.
+  const int a_off = static_cast<int>((m0 + (lane >> 3)) * G.a_si * 4 + 16 * (lane & 7));
+  const int a_st = (lane >> 3) * S::A_PITCH + 16 * (lane & 7);
+  const int b_off = static_cast<int>((lane / S::B_CH) * G.b_si * BT + n0 * BT + 16 * (lane % S::B_CH));
+  const int b_st = 32 * S::A_PITCH + (lane / S::B_CH) * S::B_PITCH + 16 * (lane % S::B_CH);
+  const int a_grp = static_cast<int>(8 * G.a_si * 4), a_step = 128;
+  const int b_grp = static_cast<int>(S::B_ROWS_PER_LOAD * G.b_si * BT),
+            b_step = static_cast<int>(32 * G.b_si * BT);
 
-  u4 ring[R][L];  // [slot][A plane x half, then B (tile, plane) x half]
+  unsigned char* st = lds + wave * S::STAGE;
+  u4 ring[R][L];
   auto fetch = [&](int sl, int s) {
-    const int64_t k0 = static_cast<int64_t>(s) * 1024;
 #pragma unroll
-    for (int p = 0; p < 3; ++p)
+    for (int i = 0; i < 4; ++i)
+      ring[sl][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off + (s * a_step + i * a_grp), 0, 0);
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-        ring[sl][2 * p + h] = *reinterpret_cast<const u4*>(a_fr + p * a_pl + k0 + 512 * h);
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-      for (int p = 0; p < BP; ++p)
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-          ring[sl][6 + 2 * (t * BP + p) + h] =
-              *reinterpret_cast<const u4*>(b_fr + t * b_t + p * b_pl + k0 + 512 * h);
+    for (int i = 0; i < S::B_LOADS; ++i)
+      ring[sl][4 + i] =
+          __builtin_amdgcn_raw_buffer_load_b128(rb, b_off + (s * b_step + i * b_grp), 0, 0);
   };
+
+  // per-lane constants of the operand reads and conversions
+  const int g = lane >> 5, r16 = lane & 15, grp = (lane >> 4) & 1;
+  const int a_rd = (lane & 31) * S::A_PITCH + 64 * g;  // + 32 h: 8 fp32 of row lane % 32
+  int b_rd[NT][2][2];  // [tile][half][read]: transposing-read addresses within the B region
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        if (BT == 1)  // 8 rows x 16 bytes per group: lane r gives row r / 2, bytes 8 (r % 2)
+          b_rd[t][h][e] = (16 * g + 8 * h + (r16 >> 1)) * S::B_PITCH + 32 * t + 16 * grp +
+                          8 * (r16 & 1);
+        else  // 4 rows x 16 halves per group and read: lane r gives row r / 4, halves 4 (r % 4)
+          b_rd[t][h][e] = (16 * g + 8 * h + 4 * e + (r16 >> 2)) * S::B_PITCH + 32 * grp +
+                          8 * (r16 & 3);
+      }
+  const unsigned xmask = G.b_dt == KK_I8 ? 0x80808080u : 0u;  // int8 bytes as uint8 + 128
+  float zoff[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    zoff[t] = zero_point(G, n0 + 32 * t + (lane & 31)) + (G.b_dt == KK_I8 ? 128.0f : 0.0f);
 
   f16v acc[NT][2];
 #pragma unroll
@@ -403,62 +239,183 @@ __global__ void __launch_bounds__(S::THREADS) gemm_bf16_kernel(Args G) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int g = 0; g < 16; ++g) acc[t][h][g] = 0.0f;
-
-  auto multiply = [&](auto uc) {
+      for (int q = 0; q < 16; ++q) acc[t][h][q] = 0.0f;
+  auto multiply = [&](auto uc, int s) {
     constexpr int u = decltype(uc)::value;
+    // stage this step's raw operands in the wave's region
 #pragma unroll
-    for (int pa = 0; pa < 3; ++pa)
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u4*>(st + a_st + 8 * S::A_PITCH * i) = ring[u][i];
 #pragma unroll
-      for (int pb = 0; pb < BP; ++pb)
+    for (int i = 0; i < S::B_LOADS; ++i)
+      *reinterpret_cast<u4*>(st + b_st + S::B_ROWS_PER_LOAD * S::B_PITCH * i) = ring[u][4 + i];
+    // read them back as operands
+    float av[2][8];
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < 2; ++h) {
+      const float4 x0 = *reinterpret_cast<const float4*>(st + a_rd + 32 * h);
+      const float4 x1 = *reinterpret_cast<const float4*>(st + a_rd + 32 * h + 16);
+      av[h][0] = x0.x; av[h][1] = x0.y; av[h][2] = x0.z; av[h][3] = x0.w;
+      av[h][4] = x1.x; av[h][5] = x1.y; av[h][6] = x1.z; av[h][7] = x1.w;
+    }
+    unsigned bw[NT][2][4];  // raw weights: 8 bytes (8-bit) or 8 halves (fp16) per tile and half
+    KK_LDS unsigned char* sb = (KK_LDS unsigned char*)(st) + 32 * S::A_PITCH;
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const bf8 a = __builtin_bit_cast(bf8, ring[u][2 * pa + h]);
-            const bf8 b = __builtin_bit_cast(bf8, ring[u][6 + 2 * (t * BP + pb) + h]);
-            acc[t][h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[t][h], 0, 0, 0);
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (BT == 1) {
+          const i2v w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              reinterpret_cast<KK_LDS i2v*>(sb + b_rd[t][h][0]));
+          bw[t][h][0] = w[0];
+          bw[t][h][1] = w[1];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const s4v w = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                reinterpret_cast<KK_LDS s4v*>(sb + b_rd[t][h][e]));
+            bw[t][h][2 * e] = static_cast<unsigned short>(w[0]) |
+                              (static_cast<unsigned>(static_cast<unsigned short>(w[1])) << 16);
+            bw[t][h][2 * e + 1] = static_cast<unsigned short>(w[2]) |
+                                  (static_cast<unsigned>(static_cast<unsigned short>(w[3])) << 16);
           }
+        }
+      }
+    // activation columns past K hold the next row's values: clear them
+    if (s == nk - 1 && (G.K & 31)) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (32 * s + 16 * g + 8 * h + j >= G.K) av[h][j] = 0.0f;
+    }
+    // A: three bf16 parts per half
+    bf8 ap[3][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      unsigned p0[4], p1[4], p2[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        unsigned q0[2], q1[2], q2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float x = av[h][j + e];
+                    const unsigned ux = __float_as_uint(x);
+          const float r = x - __uint_as_float(ux & 0xffff0000u);
+          const unsigned ur = __float_as_uint(r);
+          q0[e] = ux;
+          q1[e] = ur;
+          q2[e] = __float_as_uint(r - __uint_as_float(ur & 0xffff0000u));
+        }
+        p0[j / 2] = pack_hi(q0[0], q0[1]);
+        p1[j / 2] = pack_hi(q1[0], q1[1]);
+        p2[j / 2] = pack_hi(q2[0], q2[1]);
+      }
+      ap[0][h] = __builtin_bit_cast(bf8, u4{p0[0], p0[1], p0[2], p0[3]});
+      ap[1][h] = __builtin_bit_cast(bf8, u4{p1[0], p1[1], p1[2], p1[3]});
+      ap[2][h] = __builtin_bit_cast(bf8, u4{p2[0], p2[1], p2[2], p2[3]});
+    }
+    // B: bf16 operands (8-bit: q - z exact; fp16: two exact parts)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (BT == 1) {
+          unsigned pb[4];
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            const unsigned w = bw[t][h][d] ^ xmask;
+            float f[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) f[c] = static_cast<float>((w >> (8 * c)) & 0xffu) - zoff[t];
+            pb[2 * d] = pack_hi(__float_as_uint(f[0]), __float_as_uint(f[1]));
+            pb[2 * d + 1] = pack_hi(__float_as_uint(f[2]), __float_as_uint(f[3]));
+          }
+          const bf8 b = __builtin_bit_cast(bf8, u4{pb[0], pb[1], pb[2], pb[3]});
+#pragma unroll
+          for (int pa = 0; pa < 3; ++pa)
+            acc[t][h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[pa][h], b, acc[t][h], 0, 0, 0);
+        } else {
+          unsigned pb0[4], pb1[4];
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            unsigned q0[2], q1[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+              const float x = static_cast<float>(__builtin_bit_cast(
+                  _Float16, static_cast<unsigned short>((bw[t][h][d] >> (16 * e)) & 0xffffu)));
+                            const unsigned ux = __float_as_uint(x);
+              q0[e] = ux;
+              q1[e] = __float_as_uint(x - __uint_as_float(ux & 0xffff0000u));
+            }
+            pb0[d] = pack_hi(q0[0], q0[1]);
+            pb1[d] = pack_hi(q1[0], q1[1]);
+          }
+          const bf8 b0 = __builtin_bit_cast(bf8, u4{pb0[0], pb0[1], pb0[2], pb0[3]});
+          const bf8 b1 = __builtin_bit_cast(bf8, u4{pb1[0], pb1[1], pb1[2], pb1[3]});
+#pragma unroll
+          for (int pa = 0; pa < 3; ++pa) {
+            acc[t][h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[pa][h], b0, acc[t][h], 0, 0, 0);
+            acc[t][h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[pa][h], b1, acc[t][h], 0, 0, 0);
+          }
+        }
+      }
   };
-  // step s multiplies ring slot (s - s0) % R and refills it with step s + R:
-  // always (step), while there is one (step_tail), or not at all (step_last).
-  // The barrier keeps each refill in its step: scheduled later it would
-  // leave the next round's first step waiting on a fresh burst of loads.
+  // step s: stage and multiply ring slot (s - s0) % R, then refill it with
+  // step s + R -- always (step), while there is one (step_tail), or not at
+  // all (step_last).  The barrier keeps each refill in its step: scheduled
+  // later, it left the next round's first step waiting on a fresh burst of
+  // loads.
   auto step = [&](auto uc, int s) {
-    multiply(uc);
+    multiply(uc, s);
     fetch(decltype(uc)::value, s + R);
     __builtin_amdgcn_sched_barrier(0);
   };
   auto step_tail = [&](auto uc, int s) {
-    multiply(uc);
-    if (s + R < s1) fetch(decltype(uc)::value, s + R);  // (s and s1 are uniform)
+    multiply(uc, s);
+    if (s + R < s1) fetch(decltype(uc)::value, s + R);
     __builtin_amdgcn_sched_barrier(0);
   };
-  auto step_last = [&](auto uc, int) { multiply(uc); };
+  auto step_last = [&](auto uc, int s) { multiply(uc, s); };
   if (s1 - s0 >= R) {
 #pragma unroll
     for (int u = 0; u < R; ++u) fetch(u, s0 + u);
+    int t = s0;
     // whole rounds of R steps whose refills all exist (straight-line bodies,
     // so the loads in flight are the same at every round's start and each
     // step waits only for its own slot); then the round that refills what
     // is left (fewer than 2R steps remain), then the rest
-    int t = s0;
     for (; t + 2 * R <= s1; t += R) Unroll<0, R>::run(step, t, t + R);
     Unroll<0, R>::run(step_tail, t, t + R);
     Unroll<0, R>::run(step_last, t + R, s1);
-  } else if (s0 < s1) {  // fewer steps than ring slots
+  } else if (s0 < s1) {
 #pragma unroll
     for (int u = 0; u < R; ++u)
       if (s0 + u < s1) fetch(u, s0 + u);
     Unroll<0, R>::run(step_last, s0, s1);
   }
 
-  // every wave's partial tile to LDS; wave w then sums registers
-  // w * SHARE .. + SHARE - 1 (over the tiles) in wave order
+  bool bad = false;  // a NaN in this lane's accumulators (see the top of the section)
 #pragma unroll
   for (int t = 0; t < NT; ++t)
 #pragma unroll
-    for (int g = 0; g < 16; ++g) red[wave][t][g][lane] = acc[t][0][g] + acc[t][1][g];
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) bad |= __builtin_isnan(acc[t][h][q]);
+  const int wave_bad = __any(bad);  // (all lanes active: the vote covers the whole wave)
+  if (lane == 0) bad_w[wave] = wave_bad;
+  __syncthreads();  // every wave is done with its staging (the partial tiles reuse it)
+  bool any_bad = false;
+#pragma unroll
+  for (int w = 0; w < KS; ++w) any_bad |= bad_w[w] != 0;
+  if (any_bad) {
+    exact_tile<S>(G, m0, n0);
+    return;
+  }
+  float* red = reinterpret_cast<float*>(lds);  // [wave][tile][register][lane]
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) red[((wave * NT + t) * 16 + q) * 64 + lane] = acc[t][0][q] + acc[t][1][q];
   __syncthreads();
 
   float sc[NT];
@@ -467,49 +424,91 @@ __global__ void __launch_bounds__(S::THREADS) gemm_bf16_kernel(Args G) {
     const int64_t n = n0 + 32 * t + (lane & 31);
     sc[t] = G.scale && n < G.N ? load_as_f32(G.scale, G.scale_dt, n * G.scale_stride) : 1.0f;
   }
-  const float alpha = G.alpha;
   // D(i, j) of a 32x32 tile: lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
 #pragma unroll
   for (int i = 0; i < S::SHARE; ++i) {
-    const int e = wave * S::SHARE + i, t = e / 16, g = e % 16;
-    float v = red[0][t][g][lane];
+    const int e = wave * S::SHARE + i, t = e / 16, q = e % 16;
+    float v = red[(t * 16 + q) * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < KS; ++w) v += red[w][t][g][lane];
+    for (int w = 1; w < KS; ++w) v += red[((w * NT + t) * 16 + q) * 64 + lane];
     const int64_t n = n0 + 32 * t + (lane & 31);
-    const int64_t m = m0 + 8 * (g / 4) + 4 * (lane >> 5) + (g % 4);
+    const int64_t m = m0 + 8 * (q / 4) + 4 * (lane >> 5) + (q % 4);
     if (m >= G.M || n >= G.N) continue;
     v *= sc[t];
-    if (alpha != 1.0f) v *= alpha;
+    if (G.alpha != 1.0f) v *= G.alpha;
     G.out[m * G.som + n * G.son] = v;
   }
 }
 
-}  // namespace gdq
+}  // namespace gfu
+
+// Launches the kernel when B's rows are 16-byte aligned and every offset a
+// load forms is below 2^31; false, launching nothing, otherwise.
+static bool gemm_fused_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t b_si,
+                           const Dequant& dq, float* out, int64_t som, int64_t son, int64_t Mt,
+                           int64_t N, int64_t K, float alpha, int* status) {
+  using namespace gfu;
+  const int bt = b_dt == KK_F16 ? 2 : 1;
+  if ((reinterpret_cast<uintptr_t>(b) & 15) || (b_si * bt) % 16) return false;
+  const int64_t a_bytes = ((Mt - 1) * a_si + K) * 4, b_bytes = ((K - 1) * b_si + N) * bt;
+  // the largest offset a load forms: a whole 32-row, 32-wide K-step past the extents
+  const int64_t a_reach = (ceil_div(Mt, 32) * 32 * a_si + ceil_div(K, 32) * 32) * 4;
+  const int64_t b_reach = (ceil_div(K, 32) * 32 * b_si + ceil_div(N, 64) * 64) * bt;
+  if (a_reach >= (int64_t{1} << 31) || b_reach >= (int64_t{1} << 31)) return false;
+  const Args g{a, b, static_cast<uint32_t>(a_bytes), static_cast<uint32_t>(b_bytes), a_si, b_si,
+               b_dt, bt == 1 ? dq.zp : nullptr, dq.zp_stride, bt == 1 ? dq.scale : nullptr,
+               dq.scale_dt, dq.scale_stride, out, som, son, Mt, N, K, alpha};
+  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  const int64_t mt = ceil_div(Mt, 32);
+#ifdef KK_GFU_SHAPE
+  const int shape = KK_GFU_SHAPE;  // a fixed tile shape (for measuring them one by one)
+#else
+  const int shape = bt == 1 && mt * ceil_div(N, 64) >= cus ? 0 : 1;
+#endif
+#define KK_GFU_LAUNCH(SH)                                                                       \
+  hipLaunchKernelGGL((gemm_fused_kernel<SH>),                                                   \
+                     dim3(static_cast<unsigned>(ceil_div(N, SH::BN)), static_cast<unsigned>(mt)), \
+                     dim3(SH::THREADS), 0, ctx().stream, g)
+  using H4 = Shape<1, 4, 2>;
+  using H8 = Shape<1, 8, 2>;
+  using Q64x8 = Shape<2, 8, 1>;
+  using Q32x8 = Shape<1, 8, 1>;
+  using Q32x4 = Shape<1, 4, 1>;
+  using Q64x4 = Shape<2, 4, 1>;
+  if (bt == 2) {
+    if (shape == 2) KK_GFU_LAUNCH(H4);
+    else KK_GFU_LAUNCH(H8);
+  } else {
+    if (shape == 0) KK_GFU_LAUNCH(Q64x8);
+    else if (shape == 2) KK_GFU_LAUNCH(Q32x4);
+    else if (shape == 3) KK_GFU_LAUNCH(Q64x4);
+    else KK_GFU_LAUNCH(Q32x8);
+  }
+#undef KK_GFU_LAUNCH
+  *status = check_launch("gemm_fused_kernel");
+  return true;
+}
+
 
 // Runs out = A @ dequant(B) on the bf16 matrix cores when the operands fit
 // (see the top of the file); returns false, launching nothing, otherwise:
 // A fp32 with K contiguous (K % 4 == 0, 16-byte aligned rows), B int8/uint8
 // (scale, zero point of the same type or none) or fp16 (no dequantisation)
-// with N contiguous and N % 4 == 0; batch axes only where B is shared and A
-// and out are whole [batch * M] row ranges; the prepared operands within
-// the scratch.
+// with N contiguous and 16-byte aligned rows; batch axes only where B is
+// shared and A and out are whole [batch * M] row ranges.
 bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t b_si,
                  const Dequant& dq, float* out, int64_t som, int64_t son, const BatchMap& bm,
                  int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, const int* only_if,
                  int* status) {
-  using namespace gdq;
   *status = KK_OK;
   if (only_if) return false;
-  const bool f16 = b_dt == KK_F16;
-  if (f16) {
-    if (dq.active || (reinterpret_cast<uintptr_t>(b) & 7)) return false;
+  if (b_dt == KK_F16) {
+    if (dq.active) return false;
   } else {
     if (!(b_dt == KK_I8 || b_dt == KK_U8)) return false;
     if (!dq.active || !dq.scale || (dq.zp && dq.zp_dt != b_dt)) return false;
-    if (reinterpret_cast<uintptr_t>(b) & 3) return false;
   }
   if (K % 4 || a_si % 4 || (reinterpret_cast<uintptr_t>(a) & 15)) return false;
-  if (N % 4 || b_si % 4) return false;
   // batch axes: B shared; A and out rows of consecutive batches follow on
   int64_t ea = M * a_si, eo = M * som;
   for (int d = bm.nb - 1; d >= 0; --d) {
@@ -518,70 +517,9 @@ bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t 
     ea *= bm.dims[d];
     eo *= bm.dims[d];
   }
-  const int bplanes = f16 ? 2 : 1;
   const int64_t Mt = M * batch;  // A and out as [batch * M] rows
-  const int64_t Mp = ceil_div(Mt, kPadM) * kPadM, Np = ceil_div(N, kPadN) * kPadN,
-                Kp = ceil_div(K, kPadK) * kPadK;
-  const size_t a_bytes = static_cast<size_t>(3 * Mp * Kp) * 2;
-  const size_t b_bytes = static_cast<size_t>(bplanes * Np * Kp) * 2;
-  if (a_bytes + b_bytes > kScratchBytes || ceil_div(Mt, 32) > 65535 ||
-      ceil_div(N, 32) > (int64_t{1} << 30))
-    return false;
-
-  char* scratch = static_cast<char*>(ctx().scratch);
-  PrepArgs pa{a, a_si, b, b_si, b_dt, f16 ? nullptr : dq.zp, dq.zp_stride,
-              reinterpret_cast<__bf16*>(scratch), reinterpret_cast<__bf16*>(scratch + a_bytes),
-              Mt, N, K, Mp, Np, Kp, 0, nullptr, 0};
-  int* flag = ctx().row_counters + kRowCounters + kFlagGemmBf16;
-  int seq = 0;
-  if (f16) {
-    seq = ctx().gemm_seq = ctx().gemm_seq == 0x7fffffff ? 1 : ctx().gemm_seq + 1;
-    pa.flag = flag;
-    pa.seq = seq;
-  }
-  pa.a_blocks = static_cast<int>(ceil_div(Mp * Kp / 8, 256));
-  const int64_t b_blocks = (Kp / 64) * (Np / 64);
-  hipLaunchKernelGGL(gemm_dq_prep, dim3(static_cast<unsigned>(pa.a_blocks + b_blocks)), dim3(256), 0,
-                     ctx().stream, pa);
-  *status = check_launch("gemm_dq_prep");
-  if (*status != KK_OK) return true;
-
-  const Args g{pa.ap, pa.bp, f16 ? nullptr : dq.scale, dq.scale_dt, dq.scale_stride, out, som,
-               son, Mt, N, Mp, Np, Kp, alpha, flag, seq};
-  // 32 x 64 tiles when they cover every CU (eight waves for 8-bit weights,
-  // four for fp16, whose ring of fourteen loads a step leaves no registers
-  // for a second wave per SIMD), else 32 x 32 tiles of four waves, else
-  // 32 x 32 tiles of eight (more loads in flight per CU when the tiles are
-  // few).  Measured at 256 x 768 x 2048: 7.2 us (eight waves) vs 7.6 (four).
-  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
-  const int64_t mt = ceil_div(Mt, 32);
-#ifdef KK_GDQ_SHAPE
-  const int shape = KK_GDQ_SHAPE;  // a fixed tile shape (for measuring them one by one)
-#else
-  const int shape = mt * ceil_div(N, 64) >= cus ? 0 : mt * ceil_div(N, 32) >= cus ? 1 : 2;
-#endif
-#define KK_DQ_LAUNCH(SH)                                                                        \
-  hipLaunchKernelGGL((gemm_bf16_kernel<SH>),                                                    \
-                     dim3(static_cast<unsigned>(ceil_div(N, SH::BN)), static_cast<unsigned>(mt)), \
-                     dim3(SH::THREADS), 0, ctx().stream, g)
-#define KK_DQ_SHAPES(BPL)                \
-  do {                                   \
-    using SA = Shape<2, 4, BPL>;         \
-    using SB = Shape<1, 4, BPL>;         \
-    using SC = Shape<1, 8, BPL>;         \
-    using SD = Shape<2, 8, BPL>;         \
-    if (shape == 0 && BPL == 1) KK_DQ_LAUNCH(SD); \
-    else if (shape == 0) KK_DQ_LAUNCH(SA); \
-    else if (shape == 1) KK_DQ_LAUNCH(SB); \
-    else if (shape == 2) KK_DQ_LAUNCH(SC); \
-    else KK_DQ_LAUNCH(SD);               \
-  } while (0)
-  if (f16) KK_DQ_SHAPES(2);
-  else KK_DQ_SHAPES(1);
-#undef KK_DQ_SHAPES
-#undef KK_DQ_LAUNCH
-  *status = check_launch("gemm_bf16_kernel");
-  return true;
+  if (ceil_div(Mt, 32) > 65535 || ceil_div(N, 32) > (int64_t{1} << 30)) return false;
+  return gemm_fused_try(a, a_si, b, b_dt, b_si, dq, out, som, son, Mt, N, K, alpha, status);
 }
 
 }  // namespace kk

@@ -22,9 +22,8 @@ struct Context {
   // Per-row arrival counters of the multi-block row reductions, zero
   // between launches (the last block of a row resets its counter), then
   // kFlagSlots per-call slots, each cleared by the call that uses it before
-  // it is set (or, for a stamp slot, compared with the call's own number).
+  // it is set.
   int* row_counters = nullptr;
-  int gemm_seq = 0;  // number of the last bf16 matrix-core MatMul call (never 0)
   // Device scratch owned by the context from kk_init to kk_shutdown, for
   // per-call intermediates that must not be allocated (calls recorded into
   // graphs): every call runs on the one stream, so each use is finished
@@ -37,8 +36,6 @@ constexpr int kRowCounters = 65536;
 constexpr int kFlagSlots = 64;
 constexpr int kFlagConvh = 0;     // fp16 matrix-core convolution: a non-finite activation
 constexpr int kFlagConvhMax = 1;  // fp16 matrix-core convolution: max |x| (float bits)
-constexpr int kFlagGemmBf16 = 2;  // stamp: the last bf16 MatMul call with fp16 weights that
-                                  // met a non-finite operand
 
 // DynamicQuantizeLinear's byte of x with the scale rounded to fp32 and the
 // zero point as a float: clamp(rint(x / scale) + zp, 0, 255)

@@ -76,17 +76,22 @@ def test_per_column_dequant_u8_and_i8(gpu, oracle):
                                        (256, 768, 768, "u8"),     # 32x32, eight waves
                                        (256, 768, 768, "f16"),    # the same, two weight planes
                                        (1024, 256, 1024, "f16"),  # 32x64, four waves, two planes
-                                       (1, 100, 36, "i8"),        # waves with no K-steps
-                                       (33, 36, 100, "f16"),
-                                       (70, 4, 8, "u8"),
-                                       (300, 2052, 68, "i8"),     # runs of 8 and 9 K-steps
-                                       (300, 2052, 68, "f16")])
+                                       (45, 200, 80, "i8"),       # ragged M, K (a partial
+                                       (45, 200, 88, "f16"),      #   K-step) and N
+                                       (5, 12, 16, "u8"),         # K under one K-step
+                                       (1, 36, 48, "f16"),        # waves with no K-steps
+                                       (300, 2052, 64, "i8"),     # runs of 8 and 9 K-steps
+                                       (300, 2052, 64, "f16"),
+                                       # weight rows not 16-byte aligned: fp32 matrix cores
+                                       (1, 100, 36, "i8"), (33, 36, 100, "f16"),
+                                       (70, 4, 8, "u8"), (300, 2052, 68, "i8")])
 def test_dequant_matmul_bf16_split_accuracy(gpu, oracle, m, k, n, wdt):
     """The 8-bit- and fp16-weight MatMul on the bf16 matrix cores
     (activations split into three bf16 parts, fp16 weights into two, every
     product exact): the oracle's bar, and no less accurate than numpy's own
-    fp32 result against a float64 product (K and N off the tile sizes,
-    M = 1, per-column and per-tensor zero points of both byte types)."""
+    fp32 result against a float64 product (M, K and N off the tile sizes,
+    M = 1, per-column and per-tensor zero points of both byte types; weights
+    whose rows are not 16-byte aligned take the fp32 matrix cores)."""
     r = rng(12)
     a = r.normal(0, 1, (m, k)).astype(np.float32)
     if wdt == "f16":
