@@ -54,6 +54,9 @@ MFMA_PEAKS = {
 }
 
 
+GRAPH_REPEAT = 4  # calls of an op per rotating input set in a per-op timing graph
+
+
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
@@ -251,9 +254,11 @@ def run_gpu(args):
     def per_op(name, fn, nbytes=None, flops=None, reps=20, sets=nsets, eager=False, mfma=None):
         if eager:
             t_ms = B.time_eager(fn, sets, reps)
-        else:  # one graph holding the op once per rotating set
-            gid = B.graph(lambda: [fn(i) for i in range(sets)])
-            t_ms = B.time_graphs([gid], reps) / sets
+        else:  # one graph holding the op GRAPH_REPEAT times per rotating set
+            # (each replay's own launch cost spread over as many calls as a
+            # graph of a few ops would; the model graph holds thousands)
+            gid = B.graph(lambda: [fn(i) for _ in range(GRAPH_REPEAT) for i in range(sets)])
+            t_ms = B.time_graphs([gid], reps) / (sets * GRAPH_REPEAT)
             B.call("kk_graph_destroy", gid)
         rec = {"us": round(t_ms * 1e3, 3)}
         if nbytes:
