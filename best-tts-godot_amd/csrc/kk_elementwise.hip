@@ -89,8 +89,7 @@ __device__ __forceinline__ float apply_f32(float a, float b, float c, float alph
   else if constexpr (OP == OPX_SNAKE || OP == OPX_SNAKE_ALPHA) {
     // Mul(alpha, x) -> Sin -> Pow(., 2) -> Mul(recip, .) -> Add(x, .)
     const float r = (OP == OPX_SNAKE) ? c : 1.0f / b;
-    const float s = kk_sin(b * a);
-    const float p = s * s;
+    const float p = kk_sin_sq(b * a);
     const float q = r * p;
     return a + q;
   } else if constexpr (OP == OPX_FASTGELU || OP == OPX_FASTGELU_NB) {

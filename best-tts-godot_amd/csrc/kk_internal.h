@@ -240,6 +240,30 @@ __device__ __forceinline__ float kk_sin(float t) {
   return t == 0.0f ? t : v;
 }
 
+// kk_sin(t) * kk_sin(t), bit for bit, for the snake: squaring drops the sign,
+// so the odd-k negation, the signed-zero return and k's -0 -> +0 are not
+// needed (they only change the sign of the sine: +-s and +-0 square to the
+// same bits).
+__device__ __forceinline__ float kk_sin_sq(float t) {
+  if (!(fabsf(t) <= 1.0e5f)) {
+    const float s = sinf(t);
+    return s * s;
+  }
+  const float k = rintf(t * 0x1.45f306p-2f);
+  float r = __builtin_fmaf(-k, 0x1.921fb6p+1f, t);
+  r = __builtin_fmaf(-k, -0x1.777a5cp-24f, r);
+  r = __builtin_fmaf(-k, -0x1.ee58p-49f, r);
+  const float r2 = r * r;
+  float p = 0x1.612462p-33f;
+  p = __builtin_fmaf(p, r2, -0x1.ae6456p-26f);
+  p = __builtin_fmaf(p, r2, 0x1.71de3ap-19f);
+  p = __builtin_fmaf(p, r2, -0x1.a01a02p-13f);
+  p = __builtin_fmaf(p, r2, 0x1.111112p-7f);
+  p = __builtin_fmaf(p, r2, -0x1.555556p-3f);
+  const float s = __builtin_fmaf(r2 * r, p, r);
+  return s * s;
+}
+
 // Batch offsets of a batched matmul: up to 6 batch axes with per-operand
 // strides (0 = broadcast).
 struct BatchMap {

@@ -235,8 +235,7 @@ __device__ __forceinline__ float apply_affine(float q, const RowAffine& ra, cons
   if (ra.has_add) y = y + ra.add;
   if (af.leaky) y = y < 0.0f ? y * af.alpha : y;
   if (SNAKE && af.snake_a) {  // Mul(alpha, y) -> Sin -> Pow(., 2) -> Mul(recip, .) -> Add(y, .)
-    const float sn = kk_sin(ra.sa * y);
-    y = y + ra.sr * (sn * sn);
+    y = y + ra.sr * kk_sin_sq(ra.sa * y);
   }
   return y;
 }

@@ -103,6 +103,26 @@ def test_set1_snake_is_the_node_chain(gpu, oracle, set1):
     assert_bitexact(fused, chain, "fused snake vs node chain")
 
 
+def test_snake_chain_edge_arguments(gpu):
+    """Bit-exact against the node chain where the fused kernel's squared
+    sine skips the sine's sign handling: signed zeros, tiny values, both
+    parities of the multiple of pi taken off, and arguments past the
+    reduction's range (the library sinf there)."""
+    vals = np.array([0.0, -0.0, 1e-30, -1e-30, 1.5707964, -3.1415927, 4.712389, -7.8539815,
+                     1e4, -1e4, 99999.0, -99999.0, 3e5, -3e5, 1e30, -1e30], np.float32)
+    x = np.tile(vals, (4, 1))[None].astype(np.float32)          # [1, 4, 16]
+    al = np.array([1.0, 0.5, 2.0, 1.3], np.float32).reshape(1, 4, 1)
+    rec = (np.float32(1) / al).astype(np.float32)
+    env = {"x": gpu.to_device(x), "a": gpu.to_device(al), "r": gpu.to_device(rec),
+           "two": gpu.to_device(np.array(2.0, np.float32))}
+    for op, ins, out in [("Mul", ["a", "x"], "t"), ("Sin", ["t"], "s"),
+                         ("Pow", ["s", "two"], "p"), ("Mul", ["r", "p"], "q"),
+                         ("Add", ["x", "q"], "y")]:
+        gpu.dispatch(op, ins, [out], {}, env)
+    fused = gpu.ops.snake(env["x"], env["a"], env["r"]).numpy()
+    assert_bitexact(fused, env["y"].numpy(), "fused snake vs node chain, edge arguments")
+
+
 # ------------------------------------------------------- reference KATs
 @pytest.mark.parametrize("case", KATS["binary_shape_cases"], ids=lambda c: c[0])
 def test_kat_binary_shapes(gpu, oracle, case):
