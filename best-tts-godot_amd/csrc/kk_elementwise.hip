@@ -604,6 +604,71 @@ __global__ void __launch_bounds__(256) gather_kernel(T* __restrict__ out, const 
 
 using namespace kk;
 
+// Snake over rows: x and out [rows, L] (fp32, L % 4 == 0, rows xs / os
+// floats apart, 16-byte aligned), alpha and recip (or 1 / alpha) one value
+// per row (fp32 or fp16).  A block of up to 256 threads spans one float4 a
+// thread of one row, its row's parameters loaded once (scalar loads), with
+// none of the generic kernels' per-lane broadcast loads and index walk.
+// Two or four float4 a thread (fewer, longer waves) measured slower at
+// every decoder shape: the matching copy's speed needs the many short waves
+// whose sines overlap the later waves' loads.  The same operations as
+// apply_f32<OPX_SNAKE(_ALPHA)>, so the same bits.
+struct SnakeRowArgs {
+  float* out;
+  const float* x;
+  const void* alpha;
+  const void* recip;
+  int a_dt, r_dt;
+  int64_t a_st, r_st, xs, os;
+  int per_row4;
+};
+
+template <bool RECIP>
+__global__ void __launch_bounds__(256) snake_rows(SnakeRowArgs S) {
+  const int64_t row = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= S.per_row4) return;
+  const float al = load_as_f32(S.alpha, S.a_dt, row * S.a_st);
+  const float rc = RECIP ? load_as_f32(S.recip, S.r_dt, row * S.r_st) : 1.0f / al;
+  const float4 v = ld_stream4(S.x + row * S.xs + 4 * static_cast<int64_t>(i));
+  const float a[4] = {v.x, v.y, v.z, v.w};
+  float r[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = a[e] + rc * kk_sin_sq(al * a[e]);
+  st_stream4(S.out + row * S.os + 4 * static_cast<int64_t>(i), make_float4(r[0], r[1], r[2], r[3]));
+}
+
+// The row kernel when the operands have its layout; false, launching
+// nothing, otherwise.
+static bool snake_rows_try(const kk_tensor* out, const kk_tensor* x, const kk_tensor* alpha,
+                           const kk_tensor* recip, int* status) {
+  if (x->dtype != KK_F32 || out->dtype != KK_F32) return false;
+  if (!(alpha->dtype == KK_F32 || alpha->dtype == KK_F16)) return false;
+  if (recip && !(recip->dtype == KK_F32 || recip->dtype == KK_F16)) return false;
+  const kk_tensor* ins[3] = {x, alpha, recip};
+  Plan p;
+  if (make_plan(&p, out, ins, recip ? 3 : 2) != KK_OK || p.n == 0 || p.rank > 2) return false;
+  const int last = p.rank - 1;
+  const int64_t L = p.dims[last], rows = p.rank == 2 ? p.dims[0] : 1;
+  if (L % 4 || L / 4 >= (int64_t{1} << 30) || rows > 65535) return false;
+  if (p.st[0][last] != 1 || p.st[1][last] != 1 || p.st[2][last] != 0) return false;
+  if (recip && p.st[3][last] != 0) return false;
+  const int64_t os = p.rank == 2 ? p.st[0][0] : 0, xs = p.rank == 2 ? p.st[1][0] : 0;
+  if (os % 4 || xs % 4 || (reinterpret_cast<uintptr_t>(out->data) & 15) ||
+      (reinterpret_cast<uintptr_t>(x->data) & 15))
+    return false;
+  SnakeRowArgs S{static_cast<float*>(out->data), static_cast<const float*>(x->data), alpha->data,
+                 recip ? recip->data : nullptr, alpha->dtype, recip ? recip->dtype : KK_F32,
+                 p.rank == 2 ? p.st[2][0] : 0, recip && p.rank == 2 ? p.st[3][0] : 0, xs, os,
+                 static_cast<int>(L / 4)};
+  const int width = static_cast<int>(std::min<int64_t>(256, ceil_div(L / 4, 64) * 64));
+  const dim3 grid(static_cast<unsigned>(ceil_div(L / 4, int64_t{width})), static_cast<unsigned>(rows));
+  if (recip) hipLaunchKernelGGL((snake_rows<true>), grid, dim3(width), 0, ctx().stream, S);
+  else hipLaunchKernelGGL((snake_rows<false>), grid, dim3(width), 0, ctx().stream, S);
+  *status = check_launch("snake_rows");
+  return true;
+}
+
 extern "C" {
 
 int kk_binary(int op, const kk_tensor* out, const kk_tensor* a, const kk_tensor* b) {
@@ -687,8 +752,12 @@ int kk_snake(const kk_tensor* out, const kk_tensor* x, const kk_tensor* alpha,
   KK_TRY(check_tensor(alpha, "alpha"));
   if (!is_float(x->dtype) || !is_float(alpha->dtype) || out->dtype != KK_F32)
     return set_error(KK_E_ARG, "kk_snake: float tensors only, fp32 output");
+  if (recip) KK_TRY(check_tensor(recip, "recip"));
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(out, "out"));
+  int st = KK_OK;
+  if (snake_rows_try(out, x, alpha, recip, &st)) return st;
   if (recip) {
-    KK_TRY(check_tensor(recip, "recip"));
     const kk_tensor* ins[3] = {x, alpha, recip};
     return run_elementwise(OPX_SNAKE, out, ins, 3, 0.0f, 0, MODE_FLOAT);
   }
