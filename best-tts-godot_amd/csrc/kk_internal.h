@@ -264,6 +264,17 @@ __device__ __forceinline__ float kk_sin_sq(float t) {
   return s * s;
 }
 
+// exp(x) for x <= 0 (softmax's x - max): 2^(x log2 e) on the hardware
+// exp2, with the rounding error of the product x * log2(e) recovered by an
+// FMA (and log2(e)'s own low part) and applied as 2^e ~ 1 + e ln 2.  Within
+// a few ulp of the correctly rounded exp over [-87, 0] (results below 2^-126
+// flush to 0); exp(0) = 1 exactly.
+__device__ __forceinline__ float kk_exp_neg(float x) {
+  const float t = x * 0x1.715476p+0f;                   // log2(e), rounded
+  const float e = __builtin_fmaf(x, 0x1.715476p+0f, -t) + x * 0x1.4ae0bep-26f;
+  return __builtin_amdgcn_exp2f(t) * __builtin_fmaf(e, 0x1.62e430p-1f, 1.0f);  // ln 2
+}
+
 // Batch offsets of a batched matmul: up to 6 batch axes with per-operand
 // strides (0 = broadcast).
 struct BatchMap {

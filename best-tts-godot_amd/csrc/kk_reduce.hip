@@ -284,6 +284,65 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_kernel(float* __restrict__
   store_row<GROUP, NV, VEC>(out + row * T, T, g, r);
 }
 
+// AdaIN over one row per wave, for rows of 64 (NV - 1) < T / 4 <= 64 NV
+// float4s (the decoder's [1,512,1200]): the row in registers, vectors
+// 0 .. NV-2 whole for every lane (only the last one guarded), the three sums
+// (style projection, mean, variance) DPP moves within the wave, the
+// statistics scaled by 1 / T and normalised with the hardware reciprocal
+// square root (within 1 ulp: AdaIN is held to rel 1e-4), and the output
+// y = d * (inv * (gamma + 1)) + beta one FMA per element.  The
+// generic row kernel's affine modes, LeakyRelu and per-element division
+// cost it 841 VALU instructions a wave against ~160 here; with one wave on
+// half the SIMDs, none of that overlapped anything.
+template <int NV>
+__global__ void __launch_bounds__(64) adain_row_kernel(float* __restrict__ out,
+                                                      const float* __restrict__ x, int64_t C,
+                                                      int T, float inv_t, float eps,
+                                                      StyleArgs sa) {
+  const int g = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int64_t c = row % C;
+  const float* __restrict__ xr = x + row * T;
+  const bool tail = (NV - 1) * 64 + g < (T >> 2);  // this lane's last vector in the row
+  float4 v[NV];
+#pragma unroll
+  for (int j = 0; j < NV - 1; ++j) v[j] = ld_stream4(xr + 4 * (j * 64 + g));
+  v[NV - 1] = tail ? ld_stream4(xr + 4 * ((NV - 1) * 64 + g)) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float bg = 0.0f, bb = 0.0f;
+  if (sa.bias) {
+    bg = sa.bias[c];
+    bb = sa.bias[C + c];
+  }
+  float ag, ab;
+  style_dots<64>(sa, C, c, g, ag, ab);
+  const float mul = (wave_sum_dpp(ag) + bg) + 1.0f, add = wave_sum_dpp(ab) + bb;
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  const float mean = wave_sum_dpp(s) * inv_t;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    v[j].x -= mean;
+    v[j].y -= mean;
+    v[j].z -= mean;
+    v[j].w -= mean;
+    float t = __builtin_fmaf(v[j].x, v[j].x, v[j].y * v[j].y);
+    t = __builtin_fmaf(v[j].z, v[j].z, t);
+    t = __builtin_fmaf(v[j].w, v[j].w, t);
+    if (j < NV - 1 || tail) q += t;
+  }
+  const float inv = __builtin_amdgcn_rsqf(__builtin_fmaf(wave_sum_dpp(q), inv_t, eps));
+  const float sc = inv * mul;
+  float* __restrict__ orow = out + row * T;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const float4 y = make_float4(__builtin_fmaf(v[j].x, sc, add), __builtin_fmaf(v[j].y, sc, add),
+                                 __builtin_fmaf(v[j].z, sc, add), __builtin_fmaf(v[j].w, sc, add));
+    if (j < NV - 1 || tail) st_stream4(orow + 4 * (j * 64 + g), y);
+  }
+}
+
 // AdaIN with NW waves per row (one row per block of 64 * NW threads), for
 // rows long enough that 256 threads would each hold many vectors: more
 // waves in flight per row and fewer registers per thread (at [1,512,9600],
@@ -336,8 +395,8 @@ __device__ __forceinline__ void wide_sum_pair(float& a, float& b, float* lds) {
 template <int NW, int NV>
 __global__ void __launch_bounds__(64 * NW) instnorm_wide_kernel(float* __restrict__ out,
                                                                 const float* __restrict__ x,
-                                                                int64_t C, int64_t T, float eps,
-                                                                StyleArgs sa) {
+                                                                int64_t C, int64_t T, float inv_t,
+                                                                float eps, StyleArgs sa) {
   constexpr int G = 64 * NW;
   __shared__ float lds[2 * NW];
   const int g = threadIdx.x;
@@ -365,7 +424,7 @@ __global__ void __launch_bounds__(64 * NW) instnorm_wide_kernel(float* __restric
   for (int j = 0; j < NV; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) s += r[j][e];
-  const float mean = wide_sum<NW>(s, lds) / static_cast<float>(T);
+  const float mean = wide_sum<NW>(s, lds) * inv_t;
   float q = 0.0f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
@@ -377,8 +436,9 @@ __global__ void __launch_bounds__(64 * NW) instnorm_wide_kernel(float* __restric
       if (base + e < T) q += d * d;
     }
   }
-  // one division per row (AdaIN is held to rel 1e-4)
-  const float inv = 1.0f / sqrtf(wide_sum<NW>(q, lds) / static_cast<float>(T) + eps);
+  // the statistics scaled by 1 / T and the hardware reciprocal square root
+  // (within 1 ulp: AdaIN is held to rel 1e-4)
+  const float inv = __builtin_amdgcn_rsqf(__builtin_fmaf(wide_sum<NW>(q, lds), inv_t, eps));
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
@@ -655,6 +715,61 @@ __global__ void __launch_bounds__(kRowBlock) layernorm_kernel(float* __restrict_
   store_row<GROUP, NV, VEC>(out + row * cols, cols, g, r);
 }
 
+// LayerNorm (no skip input) over one row per wave, for rows of
+// 64 (NV - 1) < cols / 4 <= 64 NV float4s ([256, 768]: three each): the
+// row, scale and bias in registers, vectors 0 .. NV-2 whole for every lane
+// (only the last one guarded), the two sums DPP moves within the wave, the
+// statistics scaled by 1 / cols and normalised with the hardware reciprocal
+// square root (within 1 ulp; LayerNorm is held to rel 1e-4), the output
+// (d * inv) * scale + bias one multiply and one FMA per element.
+template <int NV, bool BIAS>
+__global__ void __launch_bounds__(64) layernorm_row_kernel(float* __restrict__ out,
+                                                          const float* __restrict__ x, int cols,
+                                                          float inv_c, float eps,
+                                                          const float* __restrict__ scale,
+                                                          const float* __restrict__ bias) {
+  const int g = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const float* __restrict__ xr = x + row * cols;
+  const bool tail = (NV - 1) * 64 + g < (cols >> 2);
+  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  float4 v[NV], sc[NV], bi[NV];
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int i = 4 * (j * 64 + g);
+    const bool in = j < NV - 1 || tail;
+    v[j] = in ? ld_stream4(xr + i) : z;
+    sc[j] = in ? *reinterpret_cast<const float4*>(scale + i) : z;
+    bi[j] = BIAS && in ? *reinterpret_cast<const float4*>(bias + i) : z;
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) s += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  const float mean = wave_sum_dpp(s) * inv_c;
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    v[j].x -= mean;
+    v[j].y -= mean;
+    v[j].z -= mean;
+    v[j].w -= mean;
+    float t = __builtin_fmaf(v[j].x, v[j].x, v[j].y * v[j].y);
+    t = __builtin_fmaf(v[j].z, v[j].z, t);
+    t = __builtin_fmaf(v[j].w, v[j].w, t);
+    if (j < NV - 1 || tail) q += t;
+  }
+  const float inv = __builtin_amdgcn_rsqf(__builtin_fmaf(wave_sum_dpp(q), inv_c, eps));
+  float* __restrict__ orow = out + row * cols;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const float4 y = make_float4(__builtin_fmaf(v[j].x * inv, sc[j].x, bi[j].x),
+                                 __builtin_fmaf(v[j].y * inv, sc[j].y, bi[j].y),
+                                 __builtin_fmaf(v[j].z * inv, sc[j].z, bi[j].z),
+                                 __builtin_fmaf(v[j].w * inv, sc[j].w, bi[j].w));
+    if (j < NV - 1 || tail) st_stream4(orow + 4 * (j * 64 + g), y);
+  }
+}
+
 __global__ void __launch_bounds__(kRowBlock) layernorm_long_kernel(float* __restrict__ out,
                                                                    const float* __restrict__ x,
                                                                    int64_t cols, float eps,
@@ -719,12 +834,13 @@ __global__ void __launch_bounds__(kRowBlock) softmax_kernel(float* __restrict__ 
     const int64_t base = (static_cast<int64_t>(j) * GROUP + g) * VEC;
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-      const float v = expf(r[j][e] - m);
+      const float v = kk_exp_neg(r[j][e] - m);  // (x - max <= 0; held to rel 1e-4)
       r[j][e] = v;
       if (base + e < cols) s += v;
     }
   }
-  const float inv = 1.0f / group_sum<GROUP, true>(s, lds);  // one division per row (rel 1e-4)
+  // the hardware reciprocal, once per row (within 1 ulp; rel 1e-4 bar)
+  const float inv = __builtin_amdgcn_rcpf(group_sum<GROUP, true>(s, lds));
 #pragma unroll
   for (int j = 0; j < NV; ++j)
 #pragma unroll
@@ -1528,15 +1644,16 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
   if (vec_ok && nvec > 4 * kRowBlock && nvec <= 16 * kRowBlock) {
     const int nv = static_cast<int>(ceil_div(nvec, 512));
     const dim3 grid(static_cast<unsigned>(rows));
+    const float it = 1.0f / static_cast<float>(T);
     float* op = static_cast<float*>(out->data);
     const float* xp = static_cast<const float*>(x->data);
     hipStream_t st = ctx().stream;
     switch (nv) {
-      case 3: hipLaunchKernelGGL((instnorm_wide_kernel<8, 3>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
-      case 4: hipLaunchKernelGGL((instnorm_wide_kernel<8, 4>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
-      case 5: hipLaunchKernelGGL((instnorm_wide_kernel<8, 5>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
-      case 6: hipLaunchKernelGGL((instnorm_wide_kernel<8, 6>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
-      default: hipLaunchKernelGGL((instnorm_wide_kernel<8, 8>), grid, dim3(512), 0, st, op, xp, C, T, eps, sa); break;
+      case 3: hipLaunchKernelGGL((instnorm_wide_kernel<8, 3>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      case 4: hipLaunchKernelGGL((instnorm_wide_kernel<8, 4>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      case 5: hipLaunchKernelGGL((instnorm_wide_kernel<8, 5>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      case 6: hipLaunchKernelGGL((instnorm_wide_kernel<8, 6>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      default: hipLaunchKernelGGL((instnorm_wide_kernel<8, 8>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
     }
     return check_launch("instnorm_wide_kernel");
   }
@@ -1549,13 +1666,15 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
     float* op = static_cast<float*>(out->data);
     const float* xp = static_cast<const float*>(x->data);
     hipStream_t st = ctx().stream;
-    if (nv == 5)
-      hipLaunchKernelGGL((instnorm_kernel<64, 5, 4>), grid, dim3(64), 0, st, op, xp, rows, C, T, eps, af, sa);
-    else if (nv == 6)
-      hipLaunchKernelGGL((instnorm_kernel<64, 6, 4>), grid, dim3(64), 0, st, op, xp, rows, C, T, eps, af, sa);
-    else
-      hipLaunchKernelGGL((instnorm_kernel<64, 8, 4>), grid, dim3(64), 0, st, op, xp, rows, C, T, eps, af, sa);
-    return check_launch("instnorm_kernel");
+    const int Ti = static_cast<int>(T);  // (T <= 2048 here)
+    const float it = 1.0f / static_cast<float>(T);
+    switch (nv) {
+      case 5: hipLaunchKernelGGL((adain_row_kernel<5>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+      case 6: hipLaunchKernelGGL((adain_row_kernel<6>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+      case 7: hipLaunchKernelGGL((adain_row_kernel<7>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+      default: hipLaunchKernelGGL((adain_row_kernel<8>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+    }
+    return check_launch("adain_row_kernel");
   }
   if (pick_row_shape(T, vec_ok, &rs)) {
     KK_ROW_DISPATCH(instnorm_kernel, rs, rows, static_cast<float*>(out->data),
@@ -1759,6 +1878,34 @@ int kk_layernorm(const kk_tensor* out, const kk_tensor* x, const kk_tensor* skip
   bool vec_ok = (cols % 4 == 0) && aligned16(x->data) && aligned16(out->data) &&
                 aligned16(la.scale) && (!la.bias || aligned16(la.bias)) &&
                 (!la.skip || aligned16(la.skip)) && (!la.skip_bias || aligned16(la.skip_bias));
+  const int64_t nvec = cols / 4;
+  if (vec_ok && !la.skip && nvec > 64 && nvec <= 8 * 64) {
+    const int nv = static_cast<int>(ceil_div(nvec, 64));
+    const dim3 grid(static_cast<unsigned>(rows));
+    float* op = static_cast<float*>(out->data);
+    const float* xp = static_cast<const float*>(x->data);
+    const int ci = static_cast<int>(cols);
+    const float ic = 1.0f / static_cast<float>(cols);
+    hipStream_t st = ctx().stream;
+#define KK_LN_ROW(NVV)                                                                        \
+  if (la.bias)                                                                                \
+    hipLaunchKernelGGL((layernorm_row_kernel<NVV, true>), grid, dim3(64), 0, st, op, xp, ci,  \
+                       ic, eps, la.scale, la.bias);                                           \
+  else                                                                                        \
+    hipLaunchKernelGGL((layernorm_row_kernel<NVV, false>), grid, dim3(64), 0, st, op, xp, ci, \
+                       ic, eps, la.scale, la.bias);
+    switch (nv) {
+      case 2: KK_LN_ROW(2) break;
+      case 3: KK_LN_ROW(3) break;
+      case 4: KK_LN_ROW(4) break;
+      case 5: KK_LN_ROW(5) break;
+      case 6: KK_LN_ROW(6) break;
+      case 7: KK_LN_ROW(7) break;
+      default: KK_LN_ROW(8) break;
+    }
+#undef KK_LN_ROW
+    return check_launch("layernorm_row_kernel");
+  }
   RowShape rs;
   if (pick_row_shape(cols, vec_ok, &rs)) {
     KK_ROW_DISPATCH(layernorm_kernel, rs, rows, static_cast<float*>(out->data),

@@ -31,6 +31,29 @@ def test_adain_config(gpu, oracle, t):
     assert_close(got, oracle.adain(x, s, w, b, 1e-5), RTOL, ATOL, what=f"AdaIN T={t}")
 
 
+@pytest.mark.parametrize("t,w8", [(1028, False), (1360, True), (1700, False), (2048, True)])
+def test_adain_one_wave_rows(gpu, oracle, t, w8):
+    """Rows of 257 .. 512 float4s (one wave a row; a last vector only some
+    lanes hold), offset from zero, fp32 and int8 style weights."""
+    r = rng(9)
+    c = 96
+    x = (3.0 + 2.0 * r.normal(0, 1, (1, c, t))).astype(np.float32)
+    s = r.normal(0, 0.1, (1, 128)).astype(np.float32)
+    b = r.normal(0, 0.05, 2 * c).astype(np.float32)
+    if w8:
+        q = r.integers(-127, 128, (128, 2 * c)).astype(np.int8)
+        sc = r.uniform(1e-3, 1e-2, 2 * c).astype(np.float32)
+        got = gpu.ops.adain(gpu.to_device(x), gpu.to_device(s), gpu.to_device(q),
+                            gpu.to_device(b), 1e-5, w_scale=gpu.to_device(sc)).numpy()
+        want = oracle.adain(x, s, oracle.dequantize(q, sc), b, 1e-5)
+    else:
+        w = r.normal(0, 0.05, (128, 2 * c)).astype(np.float32)
+        got = gpu.ops.adain(gpu.to_device(x), gpu.to_device(s), gpu.to_device(w),
+                            gpu.to_device(b), 1e-5).numpy()
+        want = oracle.adain(x, s, w, b, 1e-5)
+    assert_close(got, want, RTOL, ATOL, what=f"AdaIN T={t} int8 fc {w8}")
+
+
 def test_adain_transposed_weight_and_dispatch(gpu, oracle):
     x, s, w, b = adain_inputs(256, 2400, seed=1)
     b = rng(2).normal(0, 0.05, 512).astype(np.float32)
@@ -115,6 +138,25 @@ def test_layernorm_config(gpu, oracle):
                      what=f"LayerNorm eps {eps}")
 
 
+@pytest.mark.parametrize("rows,cols,with_bias", [(5, 260, False), (4, 512, True), (3, 1000, True),
+                                                  (2, 2048, False), (7, 1996, True)])
+def test_layernorm_row_lengths(gpu, oracle, rows, cols, with_bias):
+    """Rows of 65 .. 512 float4s (one wave a row; a last vector only some
+    lanes hold), with and without the bias, mean offset from zero."""
+    r = rng(8)
+    x = (3.0 + r.normal(0, 2, (rows, cols))).astype(np.float32)
+    g = (1 + 0.1 * r.normal(0, 1, cols)).astype(np.float32)
+    b = (0.1 * r.normal(0, 1, cols)).astype(np.float32) if with_bias else None
+    env = {"x": gpu.to_device(x), "g": gpu.to_device(g)}
+    ins = ["x", "g"]
+    if with_bias:
+        env["b"] = gpu.to_device(b)
+        ins.append("b")
+    gpu.dispatch("LayerNormalization", ins, ["y"], {"epsilon": 1e-5}, env)
+    assert_close(env["y"].numpy(), oracle.layernorm(x, g, b, -1, 1e-5), RTOL, ATOL,
+                 what=f"LayerNorm [{rows}, {cols}] bias {with_bias}")
+
+
 def test_skip_layernorm(gpu, oracle):
     r = rng(7)
     x, skip = (r.normal(0, 1, (1, 130, 768)).astype(np.float32) for _ in range(2))
@@ -137,6 +179,26 @@ def test_softmax(gpu, oracle, shape, axis):
     y = env["y"].numpy()
     assert_close(y, oracle.softmax(x, axis), RTOL, ATOL, what=f"softmax {shape} ax {axis}")
     assert np.allclose(y.astype(np.float64).sum(axis), 1.0, atol=1e-5)
+
+
+def test_softmax_exp_range(gpu):
+    """Rows spanning the whole range of exp below the row maximum (x - max
+    from 0 to -87): every probability within rel 1e-5 of the float64 value,
+    the smallest ones included."""
+    r = rng(10)
+    base = -np.linspace(0, 87, 256)
+    x = np.stack([base + r.uniform(-5, 5) for _ in range(12)]).astype(np.float32)
+    for row in x:
+        r.shuffle(row)
+    env = {"x": gpu.to_device(x)}
+    gpu.dispatch("Softmax", ["x"], ["y"], {"axis": -1}, env)
+    y = env["y"].numpy().astype(np.float64)
+    xd = x.astype(np.float64)
+    want = np.exp(xd - xd.max(-1, keepdims=True))
+    want /= want.sum(-1, keepdims=True)
+    keep = want > 2.0 ** -120  # (exp results below 2^-126 may flush to 0)
+    rel = np.abs(y - want)[keep] / want[keep]
+    assert rel.max() < 1e-5, rel.max()
 
 
 @pytest.mark.parametrize("op", ["ReduceMean", "ReduceSum"])
