@@ -54,7 +54,7 @@ MFMA_PEAKS = {
 }
 
 
-GRAPH_REPEAT = 4  # calls of an op per rotating input set in a per-op timing graph
+GRAPH_REPEAT = 4  # calls of an op per rotating input set in a per-op timing graph (--graph-repeat)
 
 
 def log(msg):
@@ -579,7 +579,11 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-output-stage", action="store_true",
                     help="skip the FIR/PCM16 lines (rocprofv3's kernel trace crashes on them)")
+    ap.add_argument("--graph-repeat", type=int, default=GRAPH_REPEAT,
+                    help="calls of an op per rotating set in its timing graph (rocprofv3's "
+                         "kernel trace crashes on graphs of 4)")
     args = ap.parse_args()
+    globals()["GRAPH_REPEAT"] = max(1, args.graph_repeat)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the op layer shards by utterance with no collective)", file=sys.stderr)
