@@ -350,6 +350,21 @@ static int conv_tile_n(int64_t stride, int64_t dilation, int64_t K) {
   return 0;
 }
 
+// The launch's time tile: 128 when its blocks still give every CU two (the
+// kernel is latency-bound and three blocks share a CU), else 64 for twice
+// the blocks.  Measured on the 128-id graph (whose convolutions run at
+// 240 .. 431,000 steps): 128 everywhere 39.6 ms, 64 everywhere 38.4 ms, and
+// 64 everywhere 7% slower on [1,128,431000] alone.
+static int conv_launch_tile(int64_t stride, int64_t dilation, int64_t K, int64_t N,
+                            int64_t CoutP, int64_t Lout) {
+  const int tn = conv_tile_n(stride, dilation, K);
+  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  if (tn == 128 && N * (CoutP / kTileM) * ceil_div(Lout, 128) < 2 * cus &&
+      conv_lds(conv_rows(64, stride, dilation, K)) <= 65536)
+    return 64;
+  return tn;
+}
+
 // The allocation-free entry point's workspace: a file-scope device array of
 // a fixed size (2.4x the largest the Kokoro graph's convolutions need,
 // 3.4 MiB), which each device holds from the library's first use of it until
@@ -507,7 +522,7 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     A.Cout = Cout; A.Cin = Cin; A.CinP = CinP; A.Kw = Kw; A.s = stride; A.d = dilation;
     A.L = L; A.p0 = pad0; A.Lout = Lout; A.Kreal = Cin * Kw;
     A.aligned = (L % 4 == 0) && (reinterpret_cast<uintptr_t>(x->data) % 4 == 0);
-    const int tn = conv_tile_n(stride, dilation, Kw);
+    const int tn = conv_launch_tile(stride, dilation, Kw, N, CoutP, Lout);
     A.W4 = static_cast<int>(conv_rows(tn, stride, dilation, Kw));
     const dim3 grid(static_cast<unsigned>(ceil_div(Lout, tn)),
                     static_cast<unsigned>(CoutP / kTileM), static_cast<unsigned>(N));

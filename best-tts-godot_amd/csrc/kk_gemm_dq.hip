@@ -68,21 +68,6 @@ __device__ __forceinline__ unsigned pack_hi(unsigned lo, unsigned hi) {
   return __builtin_amdgcn_perm(hi, lo, 0x07060302u);
 }
 
-// Runs f(integral_constant<U>, t + U) for U = 0 .. R - 1 while t + U < end.
-template <int U, int R>
-struct Unroll {
-  template <class F>
-  __device__ __forceinline__ static void run(F& f, int t, int end) {
-    if (t + U >= end) return;
-    f(std::integral_constant<int, U>{}, t + U);
-    Unroll<U + 1, R>::run(f, t, end);
-  }
-};
-template <int R>
-struct Unroll<R, R> {
-  template <class F>
-  __device__ __forceinline__ static void run(F&, int, int) {}
-};
 
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <hip/hip_fp16.h>
 
 #include <cstdint>
@@ -274,6 +275,24 @@ __device__ __forceinline__ float kk_exp_neg(float x) {
   const float e = __builtin_fmaf(x, 0x1.715476p+0f, -t) + x * 0x1.4ae0bep-26f;
   return __builtin_amdgcn_exp2f(t) * __builtin_fmaf(e, 0x1.62e430p-1f, 1.0f);  // ln 2
 }
+
+// Runs f(integral_constant<U>, t + U) for U = 0 .. R - 1 while t + U < end:
+// a loop body written out R times, so that a register ring indexed by U
+// keeps constant indices (a runtime index would put the ring in scratch).
+template <int U, int R>
+struct Unroll {
+  template <class F>
+  __device__ __forceinline__ static void run(F& f, int t, int end) {
+    if (t + U >= end) return;
+    f(std::integral_constant<int, U>{}, t + U);
+    Unroll<U + 1, R>::run(f, t, end);
+  }
+};
+template <int R>
+struct Unroll<R, R> {
+  template <class F>
+  __device__ __forceinline__ static void run(F&, int, int) {}
+};
 
 // Batch offsets of a batched matmul: up to 6 batch axes with per-operand
 // strides (0 = broadcast).
