@@ -276,6 +276,45 @@ __device__ __forceinline__ float kk_exp_neg(float x) {
   return __builtin_amdgcn_exp2f(t) * __builtin_fmaf(e, 0x1.62e430p-1f, 1.0f);  // ln 2
 }
 
+// a / b for many a over one divisor b, bit-identical to the division: with
+// rb = 1 / b correctly rounded, q0 = a * rb, the exact remainder
+// r = fma(-q0, b, a) and q = fma(r, rb, q0) is a / b correctly rounded
+// (Markstein's theorem: P. Markstein, IBM J. Res. Dev. 34(1), 1990) when no
+// step underflows or overflows, which 2^-60 <= b <= 2^60 and
+// 2^-60 < |a| < 2^60 guarantee.  Three instructions and two compares against
+// the division's ten; other divisors (rb = 0) and dividends (zeros, tiny or
+// huge values, inf, NaN) take the division itself.
+struct KkDivisor {
+  float b, rb;
+};
+__device__ __forceinline__ KkDivisor kk_divisor(float b) {
+  return KkDivisor{b, (b >= 0x1p-60f && b <= 0x1p60f) ? 1.0f / b : 0.0f};
+}
+__device__ __forceinline__ float kk_div_fast(float a, const KkDivisor& d) {
+  const float q0 = a * d.rb;
+  return __builtin_fmaf(__builtin_fmaf(-q0, d.b, a), d.rb, q0);
+}
+// (the tests are combined with & rather than &&: short-circuit evaluation
+// compiles to a branch per test)
+__device__ __forceinline__ int kk_div_in_range(float a) {
+  const float m = __builtin_fabsf(a);
+  return static_cast<int>(m > 0x1p-60f) & static_cast<int>(m < 0x1p60f);
+}
+__device__ __forceinline__ float kk_div(float a, const KkDivisor& d) {
+  float q = kk_div_fast(a, d);
+  if (!(static_cast<int>(d.rb != 0.0f) & kk_div_in_range(a))) q = a / d.b;
+  return q;
+}
+// Four quotients; the divisions run only where one of the four is out of range.
+__device__ __forceinline__ float4 kk_div4(float4 a, const KkDivisor& d) {
+  float4 q = make_float4(kk_div_fast(a.x, d), kk_div_fast(a.y, d), kk_div_fast(a.z, d),
+                         kk_div_fast(a.w, d));
+  const int ok = static_cast<int>(d.rb != 0.0f) & kk_div_in_range(a.x) & kk_div_in_range(a.y) &
+                 kk_div_in_range(a.z) & kk_div_in_range(a.w);
+  if (!ok) q = make_float4(a.x / d.b, a.y / d.b, a.z / d.b, a.w / d.b);
+  return q;
+}
+
 // Runs f(integral_constant<U>, t + U) for U = 0 .. R - 1 while t + U < end:
 // a loop body written out R times, so that a register ring indexed by U
 // keeps constant indices (a runtime index would put the ring in scratch).

@@ -10,6 +10,9 @@
 // Statistics follow numpy: mean = sum / n in fp32, variance two-pass
 // mean((x - mean)^2), normalisation a true division by sqrt(var + eps).
 #include <algorithm>
+#include <numeric>
+#include <utility>
+#include <vector>
 
 #include "kk_internal.h"
 
@@ -1276,6 +1279,318 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
   }
 }
 
+// ------------------------------------- instance norm, row in registers
+// numpy's pairwise tree over a row's last, partial 8192-block of m
+// elements (0 < m < 8192; nleaf = 0 when the row has none): its leaves
+// (lo, n) in order, then its internal nodes level by level, node k =
+// v[ca[k]] + v[cb[k]] over ids 0 .. nleaf-1 (the leaves) and nleaf + k (the
+// nodes), each node's children in earlier levels; level l's nodes end at
+// lev_end[l].  Built on the host: every row of a launch shares m.
+constexpr int kTailMax = 72;
+struct NpTail {
+  int m, nleaf, nnode, nlev;
+  uint16_t lo[kTailMax];
+  uint8_t n[kTailMax];
+  uint8_t ca[kTailMax], cb[kTailMax];
+  uint8_t lev_end[kNpDepth];
+};
+
+struct ResArgs {
+  float* out;     // MODE 0: y = affine((x - mean) / den), no snake
+  const float* x;
+  float2* stats;  // MODE 2: (mean, den) per row
+  float2* mm;     // MODE 2: (min, max) of y at the row's x extremes
+  int64_t C, T;
+  float eps;
+  int stage_off;  // floats from the LDS base to the waves' stages
+  Affine af;
+  NpTail tail;
+};
+
+// Instance norm over rows of NB whole 8192-blocks and a partial one
+// (15000 < T < 9 * 8192, T % 4 == 0; the decoder's [1,256,71800]), one
+// workgroup of 128 NB threads per row, x read once.  Wave w holds the 4096
+// floats (32 numpy leaves of 128) from 8192 (w / 2) + 4096 (w % 2) as
+// sixteen float4s a lane in load order, k = 0..15 at 256 k + 4 lane: each
+// load and each store of the wave is one contiguous 1 KB (holding each
+// leaf's eight accumulators in a lane pair instead, 32-byte pieces, halved
+// the read rate).  For a statistic the wave passes its leaves through its
+// own LDS stage eight at a time (leaf pitch 136 floats: the 64 lanes'
+// reads fall on distinct banks), where lane 8 q + j sums accumulator j of
+// leaf q over its sixteen terms in order; three shuffles make the leaf
+// ((r0 + r1) + (r2 + r3)) + ((r4 + r5) + (r6 + r7)), three more the
+// balanced tree of the eight leaves, and ((c0 + c1) + (c2 + c3)) the
+// wave's 32.  The block's two halves meet in LDS.  The partial block waits
+// in LDS (padded as in np_rows_kernel) for eight lanes a leaf and wave 0's
+// walk of its tree.  Both statistics are taken from registers, then
+//   MODE 0: y is written from registers (no snake: sinf's slow path would
+//           spill the held row);
+//   MODE 2: nothing is written but stats[row] and mm[row] = the (min, max)
+//           of y at the row's x extremes (for DynamicQuantizeLinear; x is
+//           read with cached loads, for the quantising pass after it).
+// The division by den is kk_div4's, bit-identical to the division.
+template <int NB, int MODE>
+__global__ void __launch_bounds__(128 * NB) np_resident_kernel(ResArgs A) {
+  constexpr int NT = 128 * NB;
+  constexpr int TPT = (kNpBlock / 4 + NT - 1) / NT;  // partial-block float4s a thread
+  constexpr int kPitch = kNpLeaf + 8;
+  extern __shared__ __align__(16) float res_lds[];  // the partial block, padded; the waves' stages
+  __shared__ float ws[NT / 64];
+  __shared__ float tv[2 * kTailMax];
+  __shared__ float2 wmm[NT / 64];
+  __shared__ float bc[4];
+  __shared__ uint16_t p_lo[kTailMax];
+  __shared__ uint8_t p_n[kTailMax], p_ca[kTailMax], p_cb[kTailMax];
+  float* const res_tail = res_lds;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int64_t row = blockIdx.x;
+  const float* xr = A.x + row * A.T;
+  const int m = A.tail.m, nleaf = A.tail.nleaf;
+  // the partial block (buffer loads: past m they return zeros), the tree
+  // plan, then the sixteen whole-block vectors
+  const float* xt = xr + NB * kNpBlock;
+  const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(xt), 0, 4 * m, 0x00020000);
+  float4 u[TPT];
+#pragma unroll
+  for (int i = 0; i < TPT; ++i) {
+    const kk_f4v r = __builtin_bit_cast(
+        kk_f4v, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * (t + i * NT), 0, 0));
+    u[i] = make_float4(r.x, r.y, r.z, r.w);
+  }
+  if (w == NT / 64 - 1) {
+    // the tree plan into LDS (its lane-indexed reads would otherwise be
+    // memory loads each time), by one wave before its row loads: a wait
+    // for the plan after them would wait for them all
+    for (int i = lane; i < kTailMax; i += 64) {
+      p_lo[i] = A.tail.lo[i];
+      p_n[i] = A.tail.n[i];
+      p_ca[i] = A.tail.ca[i];
+      p_cb[i] = A.tail.cb[i];
+    }
+  }
+  // (the partial block's loads stay ahead of the row's, so that waiting for
+  // them leaves those in flight)
+  __builtin_amdgcn_sched_barrier(0);
+  const int wbase = (w >> 1) * kNpBlock + (w & 1) * (kNpBlock / 2) + 4 * lane;
+  float v[64];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float4 e = MODE == 2 ? *reinterpret_cast<const float4*>(xr + wbase + 256 * k)
+                               : ld_stream4(xr + wbase + 256 * k);
+    v[4 * k] = e.x;
+    v[4 * k + 1] = e.y;
+    v[4 * k + 2] = e.z;
+    v[4 * k + 3] = e.w;
+  }
+#pragma unroll
+  for (int i = 0; i < TPT; ++i) {
+    const int e = 4 * (t + i * NT);
+    if (e < m) *reinterpret_cast<float4*>(res_tail + np_pad(e)) = u[i];
+  }
+  __syncthreads();
+
+  // numpy's sums of f over the partial block's leaves, eight lanes a leaf,
+  // into tv (LDS only)
+  auto tail_leaves = [&](auto f) {
+    const int j = t & 7;
+    for (int leaf = t >> 3; leaf < nleaf; leaf += NT / 8) {  // uniform over the leaf's lanes
+      const int lo = p_lo[leaf], n = p_n[leaf];
+      float res = 0.0f;
+      if (n < 8) {
+        if (j == 0)
+          for (int i = 0; i < n; ++i) res += f(res_tail[np_pad(lo + i)]);
+      } else {
+        // the accumulator's terms (at most sixteen) read together, indexes
+        // held inside the partial block, the ones past the body left out
+        const int body = n - n % 8;
+        float term[kNpLeaf / 8];
+#pragma unroll
+        for (int k = 0; k < kNpLeaf / 8; ++k)
+          term[k] = f(res_tail[np_pad(min(lo + 8 * k + j, m - 1))]);
+        float q = term[0];
+#pragma unroll
+        for (int k = 1; k < kNpLeaf / 8; ++k)
+          if (8 * k < body) q += term[k];
+        q += dpp_move<0xB1, 0xF>(q, 0.0f);   // lane pairs (xor 1)
+        q += dpp_move<0x4E, 0xF>(q, 0.0f);   // quads (xor 2)
+        q += dpp_move<0x141, 0xF>(q, 0.0f);  // eights (row half mirror: xor 4 once quads agree)
+        res = q;
+        if (j == 0)
+          for (int i = body; i < n; ++i) res += f(res_tail[np_pad(lo + i)]);
+      }
+      if (j == 0) tv[leaf] = res;
+    }
+  };
+  // wave 0, after tail_leaves and a barrier: the partial block's tree, a
+  // level at a time (LDS accesses of one wave take effect in order); its root
+  auto tail_tree = [&]() -> float {
+    if (!nleaf) return 0.0f;
+    for (int l = 0; l < A.tail.nlev; ++l) {
+      const int k = (l ? A.tail.lev_end[l - 1] : 0) + lane;
+      if (k < A.tail.lev_end[l]) tv[nleaf + k] = tv[p_ca[k]] + tv[p_cb[k]];
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+    return tv[A.tail.nnode ? nleaf + A.tail.nnode - 1 : 0];
+  };
+  float* const stg = res_lds + A.stage_off + w * 8 * kPitch;
+  // Chunk Q (leaves 8Q .. 8Q+7 of the wave, v[16Q .. 16Q+15] in load
+  // order) turned in place, through the wave's stage, into numpy's order:
+  // lane 8 q + j then holds the sixteen terms of accumulator j of leaf q.
+  auto to_leaf_order = [&](auto Qc) {
+    constexpr int Q = decltype(Qc)::value;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int pos = 256 * r + 4 * lane;
+      *reinterpret_cast<float4*>(stg + (pos >> 7) * kPitch + (pos & 127)) =
+          make_float4(v[16 * Q + 4 * r], v[16 * Q + 4 * r + 1], v[16 * Q + 4 * r + 2],
+                      v[16 * Q + 4 * r + 3]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    const float* src = stg + (lane >> 3) * kPitch + (lane & 7);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[16 * Q + k] = src[8 * k];
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  };
+  // the wave's 32 leaves of f, from registers; lane 0 leaves their balanced
+  // sum in ws[w]
+  auto wave_leaves = [&](auto f) {
+    float part[4];
+#pragma unroll
+    for (int Q = 0; Q < 4; ++Q) {
+      float a = f(v[16 * Q]);
+#pragma unroll
+      for (int k = 1; k < 16; ++k) a += f(v[16 * Q + k]);
+      // lane pairs, quads, eights (the leaf's eight accumulators), then
+      // leaf pairs, fours and eights: each DPP stage adds the same two
+      // partial sums as an xor butterfly over 1, 2, 4, 8, 16, 32, so the
+      // total (lane 63's) carries the balanced tree's roundings
+      part[Q] = wave_sum_dpp(a);
+    }
+    if (lane == 0) ws[w] = (part[0] + part[1]) + (part[2] + part[3]);  // the wave's 32 leaves
+  };
+  // wave 0, after a barrier: numpy's loop over the 8192-blocks, acc = 0,
+  // acc += each whole block, then the partial block's sum
+  auto block_loop = [&](float tail_sum) -> float {
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc += ws[2 * b] + ws[2 * b + 1];
+    if (nleaf) acc += tail_sum;
+    return acc;
+  };
+
+  // the sum of x: the partial block's leaves and tree first, while the row's
+  // loads are still arriving
+  auto ident = [](float e) { return e; };
+  tail_leaves(ident);
+  __syncthreads();
+  const float ts1 = w == 0 ? tail_tree() : 0.0f;
+  to_leaf_order(std::integral_constant<int, 0>{});
+  to_leaf_order(std::integral_constant<int, 1>{});
+  to_leaf_order(std::integral_constant<int, 2>{});
+  to_leaf_order(std::integral_constant<int, 3>{});
+  wave_leaves(ident);
+  __syncthreads();
+  if (w == 0 && lane == 0) bc[0] = block_loop(ts1);
+  __syncthreads();
+  const float n = static_cast<float>(A.T);
+  const float mean = bc[0] / n;
+  // the sum of (x - mean)^2 (tv and ws free again: wave 0 read them before
+  // the last barrier)
+  auto sqdev = [mean](float e) {
+    const float d = e - mean;
+    return d * d;
+  };
+  wave_leaves(sqdev);
+  tail_leaves(sqdev);
+  __syncthreads();
+  if (w == 0) {
+    const float ts2 = tail_tree();
+    if (lane == 0) bc[1] = block_loop(ts2);
+  }
+  __syncthreads();
+  const float den = sqrtf(bc[1] / n + A.eps);
+  const int64_t c = row % A.C;
+  float gamma = 0.0f, beta = 0.0f;
+  if (A.af.mode == 1) { gamma = A.af.gb[c]; beta = A.af.gb[A.C + c]; }
+  const RowAffine ra = row_affine(A.af, A.C, c, gamma, beta);
+  const KkDivisor dv = kk_divisor(den);
+  if constexpr (MODE == 0) {
+    float* orow = A.out + row * A.T;
+    auto y4 = [&](float4 e) {
+      const float4 q = kk_div4(make_float4(e.x - mean, e.y - mean, e.z - mean, e.w - mean), dv);
+      return make_float4(apply_affine<false>(q.x, ra, A.af), apply_affine<false>(q.y, ra, A.af),
+                         apply_affine<false>(q.z, ra, A.af), apply_affine<false>(q.w, ra, A.af));
+    };
+    // y in leaf order, then back to load order through the stage, chunk by
+    // chunk, for 1 KB stores
+#pragma unroll
+    for (int Q = 0; Q < 4; ++Q) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 y = y4(make_float4(v[16 * Q + 4 * g], v[16 * Q + 4 * g + 1],
+                                        v[16 * Q + 4 * g + 2], v[16 * Q + 4 * g + 3]));
+        float* dst = stg + (lane >> 3) * kPitch + (lane & 7) + 32 * g;
+        dst[0] = y.x;
+        dst[8] = y.y;
+        dst[16] = y.z;
+        dst[24] = y.w;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int pos = 256 * r + 4 * lane;
+        st_stream4(orow + wbase + 256 * (4 * Q + r),
+                   *reinterpret_cast<const float4*>(stg + (pos >> 7) * kPitch + (pos & 127)));
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+    float* ot = orow + NB * kNpBlock;
+    for (int e = 4 * t; e < m; e += 4 * NT)
+      st_stream4(ot + e, y4(*reinterpret_cast<const float4*>(res_tail + np_pad(e))));
+  } else {
+    // the row's x extremes; y is monotonic in x up to rounding (the caller
+    // checks every y against the bounds where it may not be)
+    float lo = v[0], hi = v[0];
+#pragma unroll
+    for (int k = 1; k < 64; ++k) {
+      lo = fminf(lo, v[k]);
+      hi = fmaxf(hi, v[k]);
+    }
+    for (int e = 4 * t; e < m; e += 4 * NT) {
+      const float4 x4 = *reinterpret_cast<const float4*>(res_tail + np_pad(e));
+      lo = fminf(fminf(lo, x4.x), fminf(fminf(x4.y, x4.z), x4.w));
+      hi = fmaxf(fmaxf(hi, x4.x), fmaxf(fmaxf(x4.y, x4.z), x4.w));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lo = fminf(lo, __shfl_xor(lo, off, 64));
+      hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+    }
+    if (lane == 0) wmm[w] = make_float2(lo, hi);
+    __syncthreads();
+    if (w == 0) {
+      lo = wmm[0].x;
+      hi = wmm[0].y;
+      for (int i = 1; i < NT / 64; ++i) {
+        lo = fminf(lo, wmm[i].x);
+        hi = fmaxf(hi, wmm[i].y);
+      }
+      // even lanes at xmin, odd at xmax
+      const float y = apply_affine(kk_div(((lane & 1) ? hi : lo) - mean, dv), ra, A.af);
+      const float y1 = __shfl_xor(y, 1, 64);
+      if (lane == 0) {
+        A.stats[row] = make_float2(mean, den);
+        A.mm[row] = make_float2(fminf(y, y1), fmaxf(y, y1));
+      }
+    }
+  }
+}
+
 // Rows of at most 128 elements (one numpy leaf), one thread per row.
 __global__ void np_leaf_rows_kernel(float* __restrict__ out, const float* __restrict__ x,
                                     int64_t rows, int n, int mean) {
@@ -1491,6 +1806,94 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
   return rc;
 }
 
+// numpy's pairwise tree over the m elements of a row's partial last block
+// (0 <= m < 8192) as an NpTail: the leaves as np_leaves lists them, the
+// internal nodes ordered by height.
+static void np_tail_plan(int m, NpTail* P) {
+  *P = NpTail{};
+  P->m = m;
+  if (m <= 0) return;
+  struct Node {
+    int a, b, h;  // children: id >= 0 a leaf, else internal node -1 - id
+  };
+  std::vector<Node> nodes;
+  auto rec = [&](auto&& self, int lo, int n) -> std::pair<int, int> {  // (id, height)
+    if (n <= kNpLeaf) {
+      P->lo[P->nleaf] = static_cast<uint16_t>(lo);
+      P->n[P->nleaf] = static_cast<uint8_t>(n);
+      return {P->nleaf++, 0};
+    }
+    int n2 = n / 2;
+    n2 -= n2 % 8;
+    const auto l = self(self, lo, n2);
+    const auto r = self(self, lo + n2, n - n2);
+    nodes.push_back({l.first, r.first, 1 + std::max(l.second, r.second)});
+    return {-static_cast<int>(nodes.size()), nodes.back().h};
+  };
+  rec(rec, 0, m);
+  std::vector<int> order(nodes.size()), pos(nodes.size());
+  std::iota(order.begin(), order.end(), 0);
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int a, int b) { return nodes[a].h < nodes[b].h; });
+  for (size_t i = 0; i < order.size(); ++i) pos[order[i]] = static_cast<int>(i);
+  auto id = [&](int c) { return static_cast<uint8_t>(c >= 0 ? c : P->nleaf + pos[-1 - c]); };
+  P->nnode = static_cast<int>(nodes.size());
+  for (size_t i = 0; i < order.size(); ++i) {
+    const Node& nd = nodes[order[i]];
+    P->ca[i] = id(nd.a);
+    P->cb[i] = id(nd.b);
+    P->nlev = std::max(P->nlev, nd.h);
+    P->lev_end[nd.h - 1] = static_cast<uint8_t>(i + 1);
+  }
+}
+
+// Rows np_resident_kernel takes: 15000 < T < 9 * 8192 (one to eight whole
+// 8192-blocks and a partial one), T % 4 == 0, x 16-byte aligned.
+static bool np_resident_ok(int64_t T, const void* x) {
+  return T > kNpRowMax && T < 9 * kNpBlock && T % 4 == 0 && aligned16(x);
+}
+
+// out set: writes y (MODE 0; no snake); else stats and mm (MODE 2).
+static int np_resident_launch(float* out, const float* x, int64_t rows, int64_t C, int64_t T,
+                              float eps, const Affine& af, float2* stats, float2* mm) {
+  ResArgs A{};
+  A.out = out;
+  A.x = x;
+  A.stats = stats;
+  A.mm = mm;
+  A.C = C;
+  A.T = T;
+  A.eps = eps;
+  A.af = af;
+  const int nb = static_cast<int>(T / kNpBlock);
+  np_tail_plan(static_cast<int>(T - nb * kNpBlock), &A.tail);
+  // the partial block, then 8 leaves of 136 floats a wave
+  A.stage_off = static_cast<int>(ceil_div(static_cast<int64_t>(np_row_lds(A.tail.m)), 16) * 4);
+  const size_t lds = 4 * static_cast<size_t>(A.stage_off) +
+                     sizeof(float) * (2 * nb) * 8 * (kNpLeaf + 8);
+  const dim3 grid(static_cast<unsigned>(rows));
+  hipStream_t st = ctx().stream;
+#define KK_RES_CASE(NBV)                                                                          \
+  case NBV:                                                                                       \
+    if (out) hipLaunchKernelGGL((np_resident_kernel<NBV, 0>), grid, dim3(128 * NBV), lds, st, A); \
+    else hipLaunchKernelGGL((np_resident_kernel<NBV, 2>), grid, dim3(128 * NBV), lds, st, A);  \
+    break;
+  switch (nb) {
+    KK_RES_CASE(1)
+    KK_RES_CASE(2)
+    KK_RES_CASE(3)
+    KK_RES_CASE(4)
+    KK_RES_CASE(5)
+    KK_RES_CASE(6)
+    KK_RES_CASE(7)
+    KK_RES_CASE(8)
+    default:
+      return set_error(KK_E_UNSUPPORTED, "instance norm: no resident kernel for T = %lld", (long long)T);
+  }
+#undef KK_RES_CASE
+  return check_launch("np_resident_kernel");
+}
+
 // Instance norm with the statistics in numpy's order (modes 0, 1, 3).
 static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, int64_t C,
                        int64_t T, float eps, const Affine& af, bool vec_ok) {
@@ -1503,6 +1906,9 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
                        static_cast<float2*>(nullptr));
     return check_launch("np_rows_kernel");
   }
+  if (np_resident_ok(T, x->data) && aligned16(out->data) && !af.snake_a)
+    return np_resident_launch(static_cast<float*>(out->data), xp, rows, C, T, eps, af, nullptr,
+                              nullptr);
   if (rows > kRowCounters)
     return set_error(KK_E_UNSUPPORTED, "instance norm: %lld long rows", (long long)rows);
   const int64_t nblk = ceil_div(T, kNpBlock);
@@ -1605,6 +2011,8 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
                        np_row_lds(T), st, static_cast<float*>(nullptr), xp, C, static_cast<int>(T), 3,
                        eps, af, rows_vec ? 1 : 0, stats, mm);
     rc = check_launch("np_rows_kernel");
+  } else if (np_resident_ok(T, x->data)) {
+    rc = np_resident_launch(nullptr, xp, rows, C, T, eps, af, stats, mm);
   } else {
     const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
     for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {

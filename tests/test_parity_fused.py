@@ -185,7 +185,14 @@ def norm_chain(affine, leaky):
                                               # 512 rows of five blocks
                                               (32, 16384, True, False), (32, 24576, False, False),
                                               (32, 24676, True, False), (16, 32773, False, True),
-                                              (512, 40000, True, True)])
+                                              (512, 40000, True, True),
+                                              # rows held in registers: the decoder's
+                                              # [1,256,71800]; eight blocks and 8188;
+                                              # whole blocks only; a 4-element last
+                                              # block (a leaf under eight); one block
+                                              (256, 71800, True, True), (8, 73724, True, False),
+                                              (16, 65536, False, False), (16, 65540, True, False),
+                                              (40, 15004, False, True)])
 def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
     r = rng(22)
     x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
@@ -234,6 +241,32 @@ def test_instance_norm_chain_operands_not_per_channel(gpu, oracle, gshape, bshap
         assert_close(got, want, 1e-5, floor_rel=1e-6, what=f"{gshape} {bshape} + snake")
     else:
         assert_bitexact(got, want, f"InstanceNorm chain scale {gshape} shift {bshape}")
+
+
+def test_instance_norm_resident_edge_values(gpu, oracle):
+    """Rows held in registers divide by den with one reciprocal and two FMAs,
+    exact only away from underflow and overflow; the values outside that
+    range take the division itself.  Rows whose x - mean is exactly 0, tiny
+    (1e-19), or whose variance overflows (den = inf), beside ordinary rows:
+    the same bits as the oracle's chain."""
+    r = rng(28)
+    C, T = 6, 20000
+    x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
+    x[0, 0] = 3.0                                                       # constant row
+    x[0, 1] = (r.normal(0, 1, T) * 1e-19).astype(np.float32)            # tiny deviations
+    x[0, 2] = (r.normal(0, 1, T) * 2e18).astype(np.float32)             # variance overflows
+    x[0, 3, ::7] = np.float32(0.0)                                      # zeros among values
+    x[0, 4, :T // 2] = np.float32(1.5)                                  # half the row constant
+    inputs = {"x": x, "g": (1 + 0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32),
+              "b": (0.1 * r.normal(0, 1, (1, C, 1))).astype(np.float32)}
+    weights = {"ax": np.array([2], np.int64),
+               "eps": np.array(1e-5, np.float16).astype(np.float32)}
+    for affine in (False, True):
+        nodes, out = norm_chain(affine, False)
+        with np.errstate(over="ignore", invalid="ignore"):
+            got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, out)
+        assert [n[0] for n in fused] == ["InstanceNormScaleShift"]
+        assert_bitexact(got, want, f"edge rows affine={affine}")
 
 
 def test_instance_norm_long_rows_repeat(gpu, oracle):
@@ -285,7 +318,11 @@ def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
                                               # odd long rows: rows start at every
                                               # offset mod 4 (scalar head and tail)
                                               (24, 20001, 1.0, None), (16, 16386, None, 0.2),
-                                              (24, 20003, 5.0, None)])
+                                              (24, 20003, 5.0, None),
+                                              # rows held in registers (the decoder's
+                                              # [1,256,71800]; a 4-element last block)
+                                              (256, 71800, 1.0, None), (256, 71800, None, 0.2),
+                                              (16, 65540, 5.0, None)])
 def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leaky):
     """InstanceNormQuant gives the same bytes, scale and zero point as the
     device's own unfused chain: the float result stored, then
@@ -319,7 +356,10 @@ def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leak
                                       (512, 40000, "affine"),
                                       # long rows with T % 4 = 1, 2, 3
                                       (32, 24677, "snake"), (16, 16386, "affine"),
-                                      (24, 20003, "leaky")])
+                                      (24, 20003, "leaky"),
+                                      # rows held in registers
+                                      (256, 71800, "snake"), (8, 73724, "affine"),
+                                      (16, 15004, "leaky")])
 def test_instance_norm_quant_chain(gpu, oracle, C, T, kind):
     """The InstanceNorm chain (plain, affine, + LeakyRelu, + snake) -> Cast
     -> DynamicQuantizeLinear: one InstanceNormQuant, its float result never
