@@ -123,15 +123,14 @@ __global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x,
                                                      uint8_t* __restrict__ y, int vec) {
   const float2 pz = params[0];
   const float sc = pz.x, z = pz.y;
+  const KkDivisor dsc = kk_divisor(sc);
   const int64_t tid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   const int64_t nthreads = static_cast<int64_t>(gridDim.x) * blockDim.x;
   int64_t head = 0;
   if (vec) {
     const int64_t n4 = n / 4;
     for (int64_t i = tid; i < n4; i += nthreads) {
-      const float4 v = ld_stream4(x + 4 * i);
-      const uint32_t q = dql_byte(v.x, sc, z) | (dql_byte(v.y, sc, z) << 8) |
-                         (dql_byte(v.z, sc, z) << 16) | (dql_byte(v.w, sc, z) << 24);
+      const uint32_t q = dql_bytes4(ld_stream4(x + 4 * i), dsc, z);
       __builtin_nontemporal_store(q, reinterpret_cast<uint32_t*>(y) + i);
     }
     head = 4 * n4;
@@ -198,6 +197,7 @@ __global__ void __launch_bounds__(kDqlSmallThreads) dql_small(const float* __res
   }
   __syncthreads();
   const float sc = pz.x, z = pz.y;
+  const KkDivisor dsc = kk_divisor(sc);
   for (int64_t i0 = tid; i0 < n4; i0 += kDqlSmallThreads * kU) {
     float4 v[kU];
 #pragma unroll
@@ -209,9 +209,7 @@ __global__ void __launch_bounds__(kDqlSmallThreads) dql_small(const float* __res
     for (int u = 0; u < kU; ++u) {
       const int64_t i = i0 + static_cast<int64_t>(u) * kDqlSmallThreads;
       if (i < n4)
-        reinterpret_cast<uint32_t*>(y)[i] = dql_byte(v[u].x, sc, z) | (dql_byte(v[u].y, sc, z) << 8) |
-                                            (dql_byte(v[u].z, sc, z) << 16) |
-                                            (dql_byte(v[u].w, sc, z) << 24);
+        reinterpret_cast<uint32_t*>(y)[i] = dql_bytes4(v[u], dsc, z);
     }
   }
   for (int64_t i = 4 * n4 + tid; i < n; i += kDqlSmallThreads)

@@ -315,6 +315,20 @@ __device__ __forceinline__ float4 kk_div4(float4 a, const KkDivisor& d) {
   return q;
 }
 
+// DynamicQuantizeLinear's bytes of four values, dql_byte's rounding with
+// the quotients x / scale formed by kk_div4 (the same bits), packed
+// little-endian.
+__device__ __forceinline__ uint32_t dql_byte_of_quotient(float q, float z) {
+  float v = rintf(q) + z;
+  v = v < 0.0f ? 0.0f : (v > 255.0f ? 255.0f : v);
+  return static_cast<uint32_t>(v);
+}
+__device__ __forceinline__ uint32_t dql_bytes4(float4 x, const KkDivisor& sc, float z) {
+  const float4 q = kk_div4(x, sc);
+  return dql_byte_of_quotient(q.x, z) | (dql_byte_of_quotient(q.y, z) << 8) |
+         (dql_byte_of_quotient(q.z, z) << 16) | (dql_byte_of_quotient(q.w, z) << 24);
+}
+
 // Runs f(integral_constant<U>, t + U) for U = 0 .. R - 1 while t + U < end:
 // a loop body written out R times, so that a register ring indexed by U
 // keeps constant indices (a runtime index would put the ring in scratch).

@@ -528,6 +528,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
   if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
   const RowAffine ra = row_affine(af, C, c, gamma, beta);
   const float2 st = stats[row];  // (mean, den)
+  const KkDivisor dden = kk_divisor(st.y);
   const float* xr = x + row * T;
   float* orow = out + row * T;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -537,10 +538,9 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
     for (int64_t k = i0; k < rsp.nv; k += stride) {
       const int64_t i = rsp.hh + 4 * k;
       const float4 v = ld_stream4(xr + i);
-      st_stream4(orow + i, make_float4(apply_affine((v.x - st.x) / st.y, ra, af),
-                                       apply_affine((v.y - st.x) / st.y, ra, af),
-                                       apply_affine((v.z - st.x) / st.y, ra, af),
-                                       apply_affine((v.w - st.x) / st.y, ra, af)));
+      const float4 q = kk_div4(make_float4(v.x - st.x, v.y - st.x, v.z - st.x, v.w - st.x), dden);
+      st_stream4(orow + i, make_float4(apply_affine(q.x, ra, af), apply_affine(q.y, ra, af),
+                                       apply_affine(q.z, ra, af), apply_affine(q.w, ra, af)));
     }
     int64_t i;
     if (rsp.edge(i))
@@ -566,23 +566,25 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict_
   const int64_t c = row % C;
   const RowAffine ra = row_affine(af, C, c, 0.0f, 0.0f);
   const float2 st = stats[row];
+  const KkDivisor dden = kk_divisor(st.y);
   const float* xr = x + row * T;
   float lo = INFINITY, hi = -INFINITY;
-  auto take = [&](float v) {
-    const float y = apply_affine((v - st.x) / st.y, ra, af);
+  auto take_y = [&](float y) {
     lo = fminf(lo, y);
     hi = fmaxf(hi, y);
   };
+  auto take = [&](float v) { take_y(apply_affine(kk_div(v - st.x, dden), ra, af)); };
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (vec) {
     const RowSplit rsp = row_split(row, T);
     for (int64_t k = i0; k < rsp.nv; k += stride) {
       const float4 v = *reinterpret_cast<const float4*>(xr + rsp.hh + 4 * k);  // read again next
-      take(v.x);
-      take(v.y);
-      take(v.z);
-      take(v.w);
+      const float4 q = kk_div4(make_float4(v.x - st.x, v.y - st.x, v.z - st.x, v.w - st.x), dden);
+      take_y(apply_affine(q.x, ra, af));
+      take_y(apply_affine(q.y, ra, af));
+      take_y(apply_affine(q.z, ra, af));
+      take_y(apply_affine(q.w, ra, af));
     }
     int64_t i;
     if (rsp.edge(i)) take(xr[i]);
@@ -621,6 +623,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
   const int64_t c = row % C;
   const RowAffine ra = row_affine(af, C, c, 0.0f, 0.0f);
   const float2 st = stats[row], pz = params[0];
+  const KkDivisor dden = kk_divisor(st.y), dsc = kk_divisor(pz.x);
   const float2 lim = check ? params[1] : make_float2(-INFINITY, INFINITY);
   const float* xr = x + row * T;
   uint8_t* qr = q + row * T;
@@ -632,13 +635,13 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
     for (int64_t k = i0; k < rsp.nv; k += stride) {
       const int64_t i = rsp.hh + 4 * k;
       const float4 v = ld_stream4(xr + i);
-      const float y0 = apply_affine((v.x - st.x) / st.y, ra, af);
-      const float y1 = apply_affine((v.y - st.x) / st.y, ra, af);
-      const float y2 = apply_affine((v.z - st.x) / st.y, ra, af);
-      const float y3 = apply_affine((v.w - st.x) / st.y, ra, af);
+      const float4 q = kk_div4(make_float4(v.x - st.x, v.y - st.x, v.z - st.x, v.w - st.x), dden);
+      const float y0 = apply_affine(q.x, ra, af);
+      const float y1 = apply_affine(q.y, ra, af);
+      const float y2 = apply_affine(q.z, ra, af);
+      const float y3 = apply_affine(q.w, ra, af);
       out |= fminf(fminf(y0, y1), fminf(y2, y3)) < lim.x || fmaxf(fmaxf(y0, y1), fmaxf(y2, y3)) > lim.y;
-      const uint32_t w = dql_byte(y0, pz.x, pz.y) | (dql_byte(y1, pz.x, pz.y) << 8) |
-                         (dql_byte(y2, pz.x, pz.y) << 16) | (dql_byte(y3, pz.x, pz.y) << 24);
+      const uint32_t w = dql_bytes4(make_float4(y0, y1, y2, y3), dsc, pz.y);
       // an ordinary store: the convolution that reads the bytes next finds
       // them in the last-level cache
       *reinterpret_cast<uint32_t*>(qr + i) = w;
@@ -1088,10 +1091,11 @@ __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__
   float gamma = 0.0f, beta = 0.0f;
   if (af.mode == 1) { gamma = af.gb[c]; beta = af.gb[C + c]; }
   const RowAffine ra = row_affine(af, C, c, gamma, beta);
+  const KkDivisor dden = kk_divisor(den);
   if (mode == 3) {  // no output: (mean, den) and the (min, max) of the row's results
     float lo = INFINITY, hi = -INFINITY;
     for (int e = threadIdx.x; e < n; e += kNpThreads) {
-      const float y = apply_affine((np_lds[np_pad(e)] - mean) / den, ra, af);
+      const float y = apply_affine(kk_div(np_lds[np_pad(e)] - mean, dden), ra, af);
       lo = fminf(lo, y);
       hi = fmaxf(hi, y);
     }
@@ -1117,10 +1121,9 @@ __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__
   if (vec) {
     for (int e = 4 * threadIdx.x; e < n; e += 4 * kNpThreads) {
       const float4 v = *reinterpret_cast<const float4*>(np_lds + np_pad(e));
-      st_stream4(orow + e, make_float4(apply_affine((v.x - mean) / den, ra, af),
-                                       apply_affine((v.y - mean) / den, ra, af),
-                                       apply_affine((v.z - mean) / den, ra, af),
-                                       apply_affine((v.w - mean) / den, ra, af)));
+      const float4 q = kk_div4(make_float4(v.x - mean, v.y - mean, v.z - mean, v.w - mean), dden);
+      st_stream4(orow + e, make_float4(apply_affine(q.x, ra, af), apply_affine(q.y, ra, af),
+                                       apply_affine(q.z, ra, af), apply_affine(q.w, ra, af)));
     }
   } else {
     for (int e = threadIdx.x; e < n; e += kNpThreads)
