@@ -1145,6 +1145,21 @@ __device__ __forceinline__ void np_wave_minmax(float lo, float hi, NpScratch& S)
   }
 }
 
+// numpy's pairwise tree over a row's last, partial 8192-block of m
+// elements (0 < m < 8192; nleaf = 0 when the row has none): its leaves
+// (lo, n) in order, then its internal nodes level by level, node k =
+// v[ca[k]] + v[cb[k]] over ids 0 .. nleaf-1 (the leaves) and nleaf + k (the
+// nodes), each node's children in earlier levels; level l's nodes end at
+// lev_end[l].  Built on the host: every row of a launch shares m.
+constexpr int kTailMax = 72;
+struct NpTail {
+  int m, nleaf, nnode, nlev;
+  uint16_t lo[kTailMax];
+  uint8_t n[kTailMax];
+  uint8_t ca[kTailMax], cb[kTailMax];
+  uint8_t lev_end[kNpDepth];
+};
+
 // Long rows: block (b, row) computes pw of 8192-block b of f(x) into
 // part[row][b]; f is x (mode 0) or (x - mean)^2 (mode 1, mean in
 // stats[row].x).  The last block of a row to finish (counted in
@@ -1164,7 +1179,7 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     float* __restrict__ part, const float* __restrict__ x, int64_t T, int nblk, int mode,
     float2* __restrict__ stats, int* __restrict__ cnt, int cstride, float* __restrict__ red_out,
     int red_mean, float eps, float2* __restrict__ xmm, float2* __restrict__ mm, int64_t C,
-    Affine af) {
+    Affine af, NpTail tail) {
   __shared__ NpScratch S;
   const int64_t row = blockIdx.y;
   cnt += row * cstride;  // counters spaced apart: the rows' atomics do not share a line
@@ -1211,18 +1226,70 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     if (threadIdx.x >= 64) return;
     s = ((S.wave[0] + S.wave[1]) + (S.wave[2] + S.wave[3])) +
         ((S.wave[4] + S.wave[5]) + (S.wave[6] + S.wave[7]));
-  } else {  // the row's last, partial block: the general tree, from memory
-    s = np_block_sum([f, xb](int e) { return f(xb[e]); }, m, S);
-    if (xmm) {
-      float lo = INFINITY, hi = -INFINITY;
-      for (int e = threadIdx.x; e < m; e += kNpThreads) {
-        lo = fminf(lo, xb[e]);
-        hi = fmaxf(hi, xb[e]);
-      }
-      np_wave_minmax(lo, hi, S);
-      __syncthreads();
+  } else {
+    // the row's last, partial block: its leaves and tree from the
+    // host-built plan (every row of the launch shares m), eight lanes a
+    // leaf with all sixteen terms of an accumulator loaded at once (a loop
+    // of dependent loads, one memory round trip a term, cost ~10 us a
+    // launch at [1,128,430800]), then wave 0's walk of the tree
+    __shared__ uint16_t p_lo[kTailMax];
+    __shared__ uint8_t p_n[kTailMax], p_ca[kTailMax], p_cb[kTailMax];
+    __shared__ float tv[2 * kTailMax];
+    if (threadIdx.x < kTailMax) {
+      p_lo[threadIdx.x] = tail.lo[threadIdx.x];
+      p_n[threadIdx.x] = tail.n[threadIdx.x];
+      p_ca[threadIdx.x] = tail.ca[threadIdx.x];
+      p_cb[threadIdx.x] = tail.cb[threadIdx.x];
     }
+    __syncthreads();
+    const int j = threadIdx.x & 7;
+    float lo_x = INFINITY, hi_x = -INFINITY;
+    for (int leaf = threadIdx.x >> 3; leaf < tail.nleaf; leaf += kNpThreads / 8) {
+      const int lo = p_lo[leaf], n = p_n[leaf];  // uniform over the leaf's lanes
+      const int body = n - n % 8;
+      float xv[kNpLeaf / 8], xt[7];
+#pragma unroll
+      for (int k = 0; k < kNpLeaf / 8; ++k) xv[k] = xb[min(lo + 8 * k + j, m - 1)];
+#pragma unroll
+      for (int i = 0; i < 7; ++i) xt[i] = xb[min(lo + body + i, m - 1)];
+      float res = 0.0f;
+      if (body) {
+        float q = f(xv[0]);
+#pragma unroll
+        for (int k = 1; k < kNpLeaf / 8; ++k)
+          if (8 * k < body) q += f(xv[k]);
+        q += dpp_move<0xB1, 0xF>(q, 0.0f);   // lane pairs (xor 1)
+        q += dpp_move<0x4E, 0xF>(q, 0.0f);   // quads (xor 2)
+        q += dpp_move<0x141, 0xF>(q, 0.0f);  // eights (row half mirror: xor 4 once quads agree)
+        res = q;
+#pragma unroll
+        for (int k = 0; k < kNpLeaf / 8; ++k)
+          if (8 * k < body) {
+            lo_x = fminf(lo_x, xv[k]);
+            hi_x = fmaxf(hi_x, xv[k]);
+          }
+      }
+      if (j == 0) {  // the leaf's n % 8 last terms (all of it when n < 8), in order
+#pragma unroll
+        for (int i = 0; i < 7; ++i)
+          if (body + i < n) {
+            res += f(xt[i]);
+            lo_x = fminf(lo_x, xt[i]);
+            hi_x = fmaxf(hi_x, xt[i]);
+          }
+        tv[leaf] = res;
+      }
+    }
+    if (xmm) np_wave_minmax(lo_x, hi_x, S);
+    __syncthreads();
     if (threadIdx.x >= 64) return;
+    for (int l = 0; l < tail.nlev; ++l) {  // wave 0: the tree, a level at a time
+      const int k = (l ? tail.lev_end[l - 1] : 0) + static_cast<int>(threadIdx.x);
+      if (k < tail.lev_end[l]) tv[tail.nleaf + k] = tv[p_ca[k]] + tv[p_cb[k]];
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+    s = tv[tail.nnode ? tail.nleaf + tail.nnode - 1 : 0];
   }
   if (xmm && threadIdx.x == 0) {
     float lo = S.wmin[0], hi = S.wmax[0];
@@ -1283,21 +1350,6 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
 }
 
 // ------------------------------------- instance norm, row in registers
-// numpy's pairwise tree over a row's last, partial 8192-block of m
-// elements (0 < m < 8192; nleaf = 0 when the row has none): its leaves
-// (lo, n) in order, then its internal nodes level by level, node k =
-// v[ca[k]] + v[cb[k]] over ids 0 .. nleaf-1 (the leaves) and nleaf + k (the
-// nodes), each node's children in earlier levels; level l's nodes end at
-// lev_end[l].  Built on the host: every row of a launch shares m.
-constexpr int kTailMax = 72;
-struct NpTail {
-  int m, nleaf, nnode, nlev;
-  uint16_t lo[kTailMax];
-  uint8_t n[kTailMax];
-  uint8_t ca[kTailMax], cb[kTailMax];
-  uint8_t lev_end[kNpDepth];
-};
-
 struct ResArgs {
   float* out;     // MODE 0: y = affine((x - mean) / den), no snake
   const float* x;
@@ -1779,36 +1831,6 @@ static size_t np_row_lds(int64_t n) {
   return sizeof(float) * static_cast<size_t>(n + 8 * ceil_div(n, kNpLeaf));
 }
 
-// Sum / mean of rows of x (rows x n, contiguous) in numpy's order.
-static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, bool mean,
-                          bool vec) {
-  hipStream_t st = ctx().stream;
-  if (n <= kNpLeaf) {
-    hipLaunchKernelGGL(np_leaf_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 256))),
-                       dim3(256), 0, st, out, x, rows, static_cast<int>(n), mean ? 1 : 0);
-    return check_launch("np_leaf_rows_kernel");
-  }
-  if (n <= kNpRowMax) {
-    Affine af{};
-    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
-                       np_row_lds(n), st, out, x, int64_t{1}, static_cast<int>(n), mean ? 1 : 0,
-                       0.0f, af, vec ? 1 : 0, static_cast<float2*>(nullptr), static_cast<float2*>(nullptr));
-    return check_launch("np_rows_kernel");
-  }
-  if (rows > kRowCounters) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)rows);
-  const int64_t nblk = ceil_div(n, kNpBlock);
-  void* part = nullptr;
-  KK_TRY(kk_alloc(sizeof(float) * rows * nblk, &part));
-  hipLaunchKernelGGL(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
-                     dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
-                     static_cast<int>(nblk), 0, static_cast<float2*>(nullptr), ctx().row_counters,
-                     counter_stride(rows), out, mean ? 1 : 0, 0.0f, static_cast<float2*>(nullptr),
-                     static_cast<float2*>(nullptr), int64_t{0}, Affine{});
-  const int rc = check_launch("np_blocks_kernel");
-  kk_free(part);  // stream order keeps it alive for the kernel
-  return rc;
-}
-
 // numpy's pairwise tree over the m elements of a row's partial last block
 // (0 <= m < 8192) as an NpTail: the leaves as np_leaves lists them, the
 // internal nodes ordered by height.
@@ -1848,6 +1870,38 @@ static void np_tail_plan(int m, NpTail* P) {
     P->nlev = std::max(P->nlev, nd.h);
     P->lev_end[nd.h - 1] = static_cast<uint8_t>(i + 1);
   }
+}
+
+// Sum / mean of rows of x (rows x n, contiguous) in numpy's order.
+static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, bool mean,
+                          bool vec) {
+  hipStream_t st = ctx().stream;
+  if (n <= kNpLeaf) {
+    hipLaunchKernelGGL(np_leaf_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 256))),
+                       dim3(256), 0, st, out, x, rows, static_cast<int>(n), mean ? 1 : 0);
+    return check_launch("np_leaf_rows_kernel");
+  }
+  if (n <= kNpRowMax) {
+    Affine af{};
+    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
+                       np_row_lds(n), st, out, x, int64_t{1}, static_cast<int>(n), mean ? 1 : 0,
+                       0.0f, af, vec ? 1 : 0, static_cast<float2*>(nullptr), static_cast<float2*>(nullptr));
+    return check_launch("np_rows_kernel");
+  }
+  if (rows > kRowCounters) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)rows);
+  const int64_t nblk = ceil_div(n, kNpBlock);
+  void* part = nullptr;
+  KK_TRY(kk_alloc(sizeof(float) * rows * nblk, &part));
+  NpTail tail;
+  np_tail_plan(static_cast<int>(n % kNpBlock), &tail);
+  hipLaunchKernelGGL(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
+                     dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
+                     static_cast<int>(nblk), 0, static_cast<float2*>(nullptr), ctx().row_counters,
+                     counter_stride(rows), out, mean ? 1 : 0, 0.0f, static_cast<float2*>(nullptr),
+                     static_cast<float2*>(nullptr), int64_t{0}, Affine{}, tail);
+  const int rc = check_launch("np_blocks_kernel");
+  kk_free(part);  // stream order keeps it alive for the kernel
+  return rc;
 }
 
 // Rows np_resident_kernel takes: 15000 < T < 9 * 8192 (one to eight whole
@@ -1923,13 +1977,15 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
   // pass 0: the sums, then the mean; pass 1: the squared deviations' sums,
   // then sqrt(var + eps); then the normalisation
   const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
+  NpTail tail;
+  np_tail_plan(static_cast<int>(T % kNpBlock), &tail);
   int rc = KK_OK;
   for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
     hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                        static_cast<int>(nblk), pass, stats, ctx().row_counters,
                        counter_stride(rows), static_cast<float*>(nullptr), 0, eps,
                        static_cast<float2*>(nullptr), static_cast<float2*>(nullptr), int64_t{0},
-                       Affine{});
+                       Affine{}, tail);
     rc = check_launch("np_blocks_kernel");
   }
   if (rc == KK_OK) {
@@ -2018,11 +2074,13 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
     rc = np_resident_launch(nullptr, xp, rows, C, T, eps, af, stats, mm);
   } else {
     const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
+    NpTail tail;
+    np_tail_plan(static_cast<int>(T % kNpBlock), &tail);
     for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
       hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                          static_cast<int>(nblk), pass, stats, ctx().row_counters,
                          counter_stride(rows), static_cast<float*>(nullptr), 0, eps, xmm,
-                         pass == 1 ? mm : static_cast<float2*>(nullptr), C, af);
+                         pass == 1 ? mm : static_cast<float2*>(nullptr), C, af, tail);
       rc = check_launch("np_blocks_kernel");
     }
   }

@@ -192,7 +192,12 @@ def norm_chain(affine, leaky):
                                               # block (a leaf under eight); one block
                                               (256, 71800, True, True), (8, 73724, True, False),
                                               (16, 65536, False, False), (16, 65540, True, False),
-                                              (40, 15004, False, True)])
+                                              (40, 15004, False, True),
+                                              # longer rows (statistics passes): a
+                                              # partial last block of 1696, the
+                                              # decoder's 430800, a 6-element one
+                                              (4, 100000, True, False), (2, 430800, True, True),
+                                              (3, 81926, False, False)])
 def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
     r = rng(22)
     x = (r.normal(0, 2, (1, C, T)) + r.normal(0, 3, (1, C, 1))).astype(np.float32)
@@ -359,7 +364,10 @@ def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leak
                                       (24, 20003, "leaky"),
                                       # rows held in registers
                                       (256, 71800, "snake"), (8, 73724, "affine"),
-                                      (16, 15004, "leaky")])
+                                      (16, 15004, "leaky"),
+                                      # longer rows (statistics passes)
+                                      (4, 100000, "snake"), (2, 430800, "leaky"),
+                                      (3, 81926, "affine")])
 def test_instance_norm_quant_chain(gpu, oracle, C, T, kind):
     """The InstanceNorm chain (plain, affine, + LeakyRelu, + snake) -> Cast
     -> DynamicQuantizeLinear: one InstanceNormQuant, its float result never

@@ -208,7 +208,7 @@ def test_softmax_exp_range(gpu):
                                              ((1, 3, 40001), [-1], 1), ((3590, 1, 512), [0], 1),
                                              ((2, 14999), [1], 1), ((2, 15001), [1], 1),
                                              ((4, 8192), [1], 1), ((1, 7), [1], 1),
-                                             ((5, 129), [1], 0)])
+                                             ((5, 129), [1], 0), ((2, 16390), [1], 1)])
 def test_reduce(gpu, oracle, op, shape, axes, keep):
     x = rng(9).normal(0, 1, shape).astype(np.float32)
     env = {"x": gpu.to_device(x)}
