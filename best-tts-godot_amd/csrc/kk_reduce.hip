@@ -1052,13 +1052,97 @@ __device__ __forceinline__ void np_load_row(float* dst, const float* __restrict_
 }
 
 
-// numpy-order sum of the padded LDS row (n elements) of f(x), acc from 0.
+// numpy's pairwise tree over a row's last, partial 8192-block of m
+// elements (0 < m < 8192; nleaf = 0 when the row has none): its leaves
+// (lo, n) in order, then its internal nodes level by level, node k =
+// v[ca[k]] + v[cb[k]] over ids 0 .. nleaf-1 (the leaves) and nleaf + k (the
+// nodes), each node's children in earlier levels; level l's nodes end at
+// lev_end[l].  Built on the host: every row of a launch shares m.
+constexpr int kTailMax = 72;
+struct NpTail {
+  int m, nleaf, nnode, nlev;
+  uint16_t lo[kTailMax];
+  uint8_t n[kTailMax];
+  uint8_t ca[kTailMax], cb[kTailMax];
+  uint8_t lev_end[kNpDepth];
+};
+
+// The plan in LDS (its lane-indexed reads would otherwise be memory loads)
+// and the partial block's node values.
+struct NpPlanLds {
+  uint16_t lo[kTailMax];
+  uint8_t n[kTailMax], ca[kTailMax], cb[kTailMax];
+  float tv[2 * kTailMax];
+};
+__device__ __forceinline__ void np_plan_to_lds(const NpTail& tail, NpPlanLds& P) {
+  if (threadIdx.x < kTailMax) {
+    P.lo[threadIdx.x] = tail.lo[threadIdx.x];
+    P.n[threadIdx.x] = tail.n[threadIdx.x];
+    P.ca[threadIdx.x] = tail.ca[threadIdx.x];
+    P.cb[threadIdx.x] = tail.cb[threadIdx.x];
+  }
+}
+
+// numpy's pairwise sum of f(i), i in [0, tail.m), over the plan: eight lanes
+// a leaf with all sixteen terms of an accumulator read at once, then wave 0
+// walks the tree a level at a time (LDS accesses of one wave take effect in
+// order).  By the whole block (plan in P, after a barrier); every thread
+// returns the sum.
 template <class F>
-__device__ float np_row_sum(const float* row, int n, F f, NpScratch& S) {
+__device__ float np_tail_sum(F f, const NpTail& tail, NpPlanLds& P, NpScratch& S) {
+  const int j = threadIdx.x & 7, m = tail.m;
+  for (int leaf = threadIdx.x >> 3; leaf < tail.nleaf; leaf += blockDim.x / 8) {
+    const int lo = P.lo[leaf], n = P.n[leaf];  // uniform over the leaf's lanes
+    const int body = n - n % 8;
+    float res = 0.0f;
+    if (body) {
+      float term[kNpLeaf / 8];
+#pragma unroll
+      for (int k = 0; k < kNpLeaf / 8; ++k) term[k] = f(min(lo + 8 * k + j, m - 1));
+      float q = term[0];
+#pragma unroll
+      for (int k = 1; k < kNpLeaf / 8; ++k)
+        if (8 * k < body) q += term[k];
+      q += dpp_move<0xB1, 0xF>(q, 0.0f);   // lane pairs (xor 1)
+      q += dpp_move<0x4E, 0xF>(q, 0.0f);   // quads (xor 2)
+      q += dpp_move<0x141, 0xF>(q, 0.0f);  // eights (row half mirror: xor 4 once quads agree)
+      res = q;
+    }
+    if (j == 0) {  // the n % 8 last terms (all of them when n < 8), in order
+      float xt[7];
+#pragma unroll
+      for (int i = 0; i < 7; ++i) xt[i] = f(min(lo + body + i, m - 1));
+#pragma unroll
+      for (int i = 0; i < 7; ++i)
+        if (body + i < n) res += xt[i];
+      P.tv[leaf] = res;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    for (int l = 0; l < tail.nlev; ++l) {
+      const int k = (l ? tail.lev_end[l - 1] : 0) + static_cast<int>(threadIdx.x);
+      if (k < tail.lev_end[l]) P.tv[tail.nleaf + k] = P.tv[P.ca[k]] + P.tv[P.cb[k]];
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (threadIdx.x == 0) S.total = P.tv[tail.nnode ? tail.nleaf + tail.nnode - 1 : 0];
+  }
+  __syncthreads();
+  const float s = S.total;
+  __syncthreads();
+  return s;
+}
+
+// numpy-order sum of the padded LDS row (n elements) of f(x), acc from 0.
+// The partial block (if any) over the plan, whose m is n % 8192.
+template <class F>
+__device__ float np_row_sum(const float* row, int n, F f, NpScratch& S, const NpTail& tail,
+                            NpPlanLds& P) {
   float acc = 0.0f;
   for (int b0 = 0; b0 < n; b0 += kNpBlock) {
-    const int m = n - b0 < kNpBlock ? n - b0 : kNpBlock;
-    acc += np_block_sum([&](int i) { return f(row[np_pad(b0 + i)]); }, m, S);
+    const auto g = [&](int i) { return f(row[np_pad(b0 + i)]); };
+    acc += n - b0 < kNpBlock ? np_tail_sum(g, tail, P, S) : np_block_sum(g, kNpBlock, S);
   }
   return acc;
 }
@@ -1071,21 +1155,24 @@ __global__ void __launch_bounds__(kNpThreads) np_rows_kernel(float* __restrict__
                                                              int64_t C, int n, int mode,
                                                              float eps, Affine af, int vec,
                                                              float2* __restrict__ stats,
-                                                             float2* __restrict__ mm) {
+                                                             float2* __restrict__ mm,
+                                                             NpTail tail) {
   extern __shared__ __align__(16) float np_lds[];
   __shared__ NpScratch S;
+  __shared__ NpPlanLds P;
   const int64_t row = blockIdx.x;
   const float* xr = x + row * n;
+  np_plan_to_lds(tail, P);
   np_load_row(np_lds, xr, n, vec);
   __syncthreads();
-  const float sum = np_row_sum(np_lds, n, [](float v) { return v; }, S);
+  const float sum = np_row_sum(np_lds, n, [](float v) { return v; }, S, tail, P);
   if (mode < 2) {
     if (threadIdx.x == 0) out[row] = mode == 1 ? sum / static_cast<float>(n) : sum;
     return;
   }
   const float mean = sum / static_cast<float>(n);
   const float sq = np_row_sum(np_lds, n, [mean](float v) { const float d = v - mean; return d * d; },
-                              S);
+                              S, tail, P);
   const float den = sqrtf(sq / static_cast<float>(n) + eps);
   const int64_t c = row % C;
   float gamma = 0.0f, beta = 0.0f;
@@ -1144,21 +1231,6 @@ __device__ __forceinline__ void np_wave_minmax(float lo, float hi, NpScratch& S)
     S.wmax[threadIdx.x >> 6] = hi;
   }
 }
-
-// numpy's pairwise tree over a row's last, partial 8192-block of m
-// elements (0 < m < 8192; nleaf = 0 when the row has none): its leaves
-// (lo, n) in order, then its internal nodes level by level, node k =
-// v[ca[k]] + v[cb[k]] over ids 0 .. nleaf-1 (the leaves) and nleaf + k (the
-// nodes), each node's children in earlier levels; level l's nodes end at
-// lev_end[l].  Built on the host: every row of a launch shares m.
-constexpr int kTailMax = 72;
-struct NpTail {
-  int m, nleaf, nnode, nlev;
-  uint16_t lo[kTailMax];
-  uint8_t n[kTailMax];
-  uint8_t ca[kTailMax], cb[kTailMax];
-  uint8_t lev_end[kNpDepth];
-};
 
 // Long rows: block (b, row) computes pw of 8192-block b of f(x) into
 // part[row][b]; f is x (mode 0) or (x - mean)^2 (mode 1, mean in
@@ -1876,6 +1948,8 @@ static void np_tail_plan(int m, NpTail* P) {
 static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, bool mean,
                           bool vec) {
   hipStream_t st = ctx().stream;
+  NpTail tail;  // the rows' partial 8192-block, if any
+  np_tail_plan(static_cast<int>(n % kNpBlock), &tail);
   if (n <= kNpLeaf) {
     hipLaunchKernelGGL(np_leaf_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 256))),
                        dim3(256), 0, st, out, x, rows, static_cast<int>(n), mean ? 1 : 0);
@@ -1885,15 +1959,14 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
     Affine af{};
     hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(n), st, out, x, int64_t{1}, static_cast<int>(n), mean ? 1 : 0,
-                       0.0f, af, vec ? 1 : 0, static_cast<float2*>(nullptr), static_cast<float2*>(nullptr));
+                       0.0f, af, vec ? 1 : 0, static_cast<float2*>(nullptr), static_cast<float2*>(nullptr),
+                       tail);
     return check_launch("np_rows_kernel");
   }
   if (rows > kRowCounters) return set_error(KK_E_UNSUPPORTED, "reduce: %lld long rows", (long long)rows);
   const int64_t nblk = ceil_div(n, kNpBlock);
   void* part = nullptr;
   KK_TRY(kk_alloc(sizeof(float) * rows * nblk, &part));
-  NpTail tail;
-  np_tail_plan(static_cast<int>(n % kNpBlock), &tail);
   hipLaunchKernelGGL(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
                      dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
                      static_cast<int>(nblk), 0, static_cast<float2*>(nullptr), ctx().row_counters,
@@ -1955,12 +2028,14 @@ static int np_resident_launch(float* out, const float* x, int64_t rows, int64_t 
 static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, int64_t C,
                        int64_t T, float eps, const Affine& af, bool vec_ok) {
   hipStream_t st = ctx().stream;
+  NpTail tail;  // the rows' partial 8192-block, if any
+  np_tail_plan(static_cast<int>(T % kNpBlock), &tail);
   const float* xp = static_cast<const float*>(x->data);
   if (T <= kNpRowMax) {
     hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(T), st, static_cast<float*>(out->data), xp, C,
                        static_cast<int>(T), 2, eps, af, vec_ok ? 1 : 0, static_cast<float2*>(nullptr),
-                       static_cast<float2*>(nullptr));
+                       static_cast<float2*>(nullptr), tail);
     return check_launch("np_rows_kernel");
   }
   if (np_resident_ok(T, x->data) && aligned16(out->data) && !af.snake_a)
@@ -1977,8 +2052,6 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
   // pass 0: the sums, then the mean; pass 1: the squared deviations' sums,
   // then sqrt(var + eps); then the normalisation
   const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
-  NpTail tail;
-  np_tail_plan(static_cast<int>(T % kNpBlock), &tail);
   int rc = KK_OK;
   for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
     hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
@@ -2022,6 +2095,8 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   const int64_t T = x->shape[x->rank - 1];
   const int64_t C = x->shape[x->rank - 2];
   const int64_t rows = numel(x) / T;
+  NpTail tail;  // the rows' partial 8192-block, if any
+  np_tail_plan(static_cast<int>(T % kNpBlock), &tail);
   const float* xp = static_cast<const float*>(x->data);
   // the quantising pass vectorises any row length once the bases are
   // aligned; the rows held in LDS take 16-byte loads only when T % 4 == 0
@@ -2068,14 +2143,12 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   if (!long_rows) {
     hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(T), st, static_cast<float*>(nullptr), xp, C, static_cast<int>(T), 3,
-                       eps, af, rows_vec ? 1 : 0, stats, mm);
+                       eps, af, rows_vec ? 1 : 0, stats, mm, tail);
     rc = check_launch("np_rows_kernel");
   } else if (np_resident_ok(T, x->data)) {
     rc = np_resident_launch(nullptr, xp, rows, C, T, eps, af, stats, mm);
   } else {
     const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
-    NpTail tail;
-    np_tail_plan(static_cast<int>(T % kNpBlock), &tail);
     for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
       hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                          static_cast<int>(nblk), pass, stats, ctx().row_counters,
