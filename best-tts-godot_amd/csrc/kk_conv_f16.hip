@@ -68,6 +68,11 @@ struct HArgs {
   int64_t Cin, L, M, Cout, Kg, Nq, Lout;
   int64_t qs, tap_mul, tap_add, os, ophase0;
   int P;
+  // split-K (ring kernel): blockIdx.z = batch * ksplit + split; each split
+  // sums its share of the K-steps into part[(b * ksplit + split) * M + m][q]
+  // (raw, in the activations' scaled units), NULL for the direct epilogue
+  int ksplit;
+  float* part;
 };
 
 // WAVES_M x (4 / WAVES_M) wavefronts, each owning WM_T x WN_T tiles of 32x32.
@@ -249,6 +254,238 @@ __global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
     }
 }
 
+// The same GEMM over rearranged weights with three K-steps of loads in
+// flight: step kt issues the loads of step kt + 3 into the register slot
+// that step kt's data has just left, computes step kt from LDS, then moves
+// step kt + 1's registers into the other LDS buffer.  With one step of
+// prefetch each of the 48 K-steps of Conv1d 512->512 k3 waited a whole
+// memory round trip (about one wave per SIMD to cover it).  Buffer loads
+// return zeros past the weight rows and, with the offset pushed out of
+// range, at padding and past the output positions, so every step issues
+// the same loads and the wait counts are exact; the last steps re-load
+// the final K-step (unused).  Needs M Kg 2 and Cin L 4 below 2^31.
+template <class T>
+__global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
+  __shared__ __align__(16) _Float16 As[2][T::BM * kPitch];
+  __shared__ __align__(16) _Float16 Bh[2][T::BN * kPitch];
+  __shared__ __align__(16) _Float16 Bl[2][T::BN * kPitch];
+  constexpr int WM_T = T::WM_T, WN_T = T::WN_T, KPT = T::KPT, BP = T::B_PAIRS;
+  constexpr int AW = KPT / 2;  // dwords of A a thread stages per step
+  static_assert(KPT == 4 || KPT % 8 == 0, "A staging width");
+  const unsigned mbits = *A.xmax;
+  if (mbits >= 0x7f800000u) {  // an infinite or NaN activation: the fp32 kernels compute it
+    if (threadIdx.x == 0) *A.flag = 1;  // every writer stores the same 1
+    return;
+  }
+  const int kexp = convh_scale_exp(mbits);
+  const float xscale = ldexpf(1.0f, kexp), unscale = ldexpf(1.0f, -kexp);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m_w = (wave / T::WAVES_N) * 32 * WM_T, n_w = (wave % T::WAVES_N) * 32 * WN_T;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T::BN;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * T::BM;
+  const int64_t b = blockIdx.z / A.ksplit;
+  const int split = static_cast<int>(blockIdx.z - b * A.ksplit);
+  const int nk_all = static_cast<int>(A.Kg / kBK);
+  const int kt0 = static_cast<int>(static_cast<int64_t>(nk_all) * split / A.ksplit);
+  const int nk = static_cast<int>(static_cast<int64_t>(nk_all) * (split + 1) / A.ksplit) - kt0;
+  const int am = tid % T::BM, ak = KPT * (tid / T::BM);
+  const int Kg = static_cast<int>(A.Kg), Cin = static_cast<int>(A.Cin), L = static_cast<int>(A.L);
+  const auto wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A.wt), 0,
+                                                     static_cast<int>(A.M * A.Kg * 2), 0x00020000);
+  const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A.x + b * A.Cin * A.L), 0,
+                                                     static_cast<int>(A.Cin * A.L * 4), 0x00020000);
+  // rows past M read past the buffer's end: zeros
+  const uint32_t a_base = static_cast<uint32_t>((m0 + am) * A.Kg + ak) * 2u;
+  const int bn = tid % T::BN;
+  const int64_t q = n0 + bn;
+  const int q_pos = static_cast<int>(q * A.qs + A.tap_add);
+  const bool q_in = q < A.Nq;
+  struct Slot {
+    uint32_t a[AW];
+    float b[BP][2];
+  };
+  Slot ring[3];
+  // the next K-step to fetch (k0, its tap t and first channel ci0), moved
+  // on after each fetch and held at the split's last step (the final
+  // fetches repeat it): no division per step
+  int f_k0 = kt0 * kBK, f_t = f_k0 / Cin, f_ci0 = f_k0 - f_t * Cin;
+  const int k_last = (kt0 + nk - 1) * kBK;
+  auto fetch = [&](Slot& sl) {
+    const int k0 = f_k0, t = f_t, ci0 = f_ci0;
+    if (f_k0 < k_last) {
+      f_k0 += kBK;
+      f_ci0 += kBK;
+      if (f_ci0 >= Cin) {
+        f_ci0 -= Cin;
+        ++f_t;
+      }
+    }
+    const uint32_t ao = a_base + static_cast<uint32_t>(k0) * 2u;
+    if constexpr (KPT == 4) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(wrs, ao, 0, 0);
+      sl.a[0] = v[0];
+      sl.a[1] = v[1];
+    } else {
+#pragma unroll
+      for (int e = 0; e < AW; e += 4) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, ao + 4u * e, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sl.a[e + u] = v[u];
+      }
+    }
+    const int pos = q_pos + t * static_cast<int>(A.tap_mul);
+    const bool in = q_in && pos >= 0 && pos < L;
+#pragma unroll
+    for (int j = 0; j < BP; ++j) {
+      const int kp = tid / T::BN + j * T::KP_STEP;
+      uint32_t off = in ? static_cast<uint32_t>((ci0 + 2 * kp) * L + pos) * 4u : 0x80000000u;
+      // the offset held in a register: without it the compiler turned the
+      // select into a branch around each load, and the waits then covered
+      // every load in flight
+      asm volatile("" : "+v"(off));
+      sl.b[j][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, off, 0, 0));
+      // (past the buffer stays past it: its size is below 2^31)
+      sl.b[j][1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, off + 4u * L, 0, 0));
+    }
+  };
+  auto stash = [&](const Slot& sl, int buf) {
+#pragma unroll
+    for (int e = 0; e < AW; e += 2)
+      *reinterpret_cast<uint2*>(&As[buf][am * kPitch + ak + 2 * e]) = make_uint2(sl.a[e], sl.a[e + 1]);
+#pragma unroll
+    for (int j = 0; j < BP; ++j) {
+      const int kp = tid / T::BN + j * T::KP_STEP;
+      h2 hi, lo;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float v = sl.b[j][e] * xscale;  // |v| < 2^15: exact
+        const _Float16 h = static_cast<_Float16>(v);
+        hi[e] = h;
+        lo[e] = static_cast<_Float16>(v - static_cast<float>(h));
+      }
+      *reinterpret_cast<h2*>(&Bh[buf][bn * kPitch + 2 * kp]) = hi;
+      *reinterpret_cast<h2*>(&Bl[buf][bn * kPitch + 2 * kp]) = lo;
+    }
+  };
+
+  f16v acc[WM_T][WN_T];
+#pragma unroll
+  for (int i = 0; i < WM_T; ++i)
+#pragma unroll
+    for (int j = 0; j < WN_T; ++j)
+#pragma unroll
+      for (int g = 0; g < 16; ++g) acc[i][j][g] = 0.0f;
+
+  fetch(ring[0]);
+  fetch(ring[1]);
+  fetch(ring[2]);
+  stash(ring[0], 0);
+  __syncthreads();
+  auto step = [&](auto sc, int kt) {
+    constexpr int S = decltype(sc)::value;  // kt % 3
+    fetch(ring[S]);  // step min(kt + 3, nk - 1)
+    const int buf = kt & 1;
+#pragma unroll
+    for (int ks = 0; ks < kBK; ks += 16) {
+      const int kofs = ks + 8 * (lane >> 5);
+      h8 a[WM_T], bh[WN_T], bl[WN_T];
+#pragma unroll
+      for (int i = 0; i < WM_T; ++i)
+        a[i] = *reinterpret_cast<const h8*>(&As[buf][(m_w + 32 * i + (lane & 31)) * kPitch + kofs]);
+#pragma unroll
+      for (int j = 0; j < WN_T; ++j) {
+        bh[j] = *reinterpret_cast<const h8*>(&Bh[buf][(n_w + 32 * j + (lane & 31)) * kPitch + kofs]);
+        bl[j] = *reinterpret_cast<const h8*>(&Bl[buf][(n_w + 32 * j + (lane & 31)) * kPitch + kofs]);
+      }
+#pragma unroll
+      for (int i = 0; i < WM_T; ++i)
+#pragma unroll
+        for (int j = 0; j < WN_T; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], acc[i][j], 0, 0, 0);
+        }
+    }
+    if (kt + 1 < nk) stash(ring[(S + 1) % 3], buf ^ 1);
+    __syncthreads();
+  };
+  // whole rounds of three steps, then the rest: an early exit between the
+  // steps of a round put a wait for every load at the loop's head
+  const int nr = nk / 3;
+  for (int r = 0; r < nr; ++r) {
+    step(std::integral_constant<int, 0>{}, 3 * r);
+    step(std::integral_constant<int, 1>{}, 3 * r + 1);
+    step(std::integral_constant<int, 2>{}, 3 * r + 2);
+  }
+  if (3 * nr < nk) step(std::integral_constant<int, 0>{}, 3 * nr);
+  if (3 * nr + 1 < nk) step(std::integral_constant<int, 1>{}, 3 * nr + 1);
+
+  // D(i, j) of a 32x32 tile: lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
+  if (A.part) {  // this split's raw sums
+    float* pb = A.part + (b * A.ksplit + split) * A.M * A.Nq;
+#pragma unroll
+    for (int i = 0; i < WM_T; ++i)
+#pragma unroll
+      for (int g = 0; g < 16; ++g) {
+        const int64_t m = m0 + m_w + 32 * i + 8 * (g / 4) + 4 * (lane >> 5) + (g % 4);
+        if (m >= A.M) continue;
+#pragma unroll
+        for (int j = 0; j < WN_T; ++j) {
+          const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
+          if (qq < A.Nq) pb[m * A.Nq + qq] = acc[i][j][g];
+        }
+      }
+    return;
+  }
+  float* ob = A.out + b * A.Cout * A.Lout;
+#pragma unroll
+  for (int i = 0; i < WM_T; ++i)
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const int64_t m = m0 + m_w + 32 * i + 8 * (g / 4) + 4 * (lane >> 5) + (g % 4);
+      if (m >= A.M) continue;
+      const int64_t co = m / A.P, r = m - co * A.P;
+      const float bias = A.bias ? A.bias[co] : 0.0f;
+      const float sc = A.dq.scale ? load_as_f32(A.dq.scale, A.dq.scale_dt, co * A.dq.scale_stride)
+                                  : 1.0f;
+#pragma unroll
+      for (int j = 0; j < WN_T; ++j) {
+        const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
+        const float u = acc[i][j][g] * unscale;  // exact: a power of two
+        const float v = A.dq.scale ? u * sc : u;
+        const int64_t pos = qq * A.os + r + A.ophase0;
+        if (qq < A.Nq && pos >= 0 && pos < A.Lout) ob[co * A.Lout + pos] = A.bias ? v + bias : v;
+      }
+    }
+}
+
+// Split-K's finish: out at (m, q) = the splits' sums added in split order,
+// then the epilogue above.  Row m on the grid's y axis (and batch on z), q
+// along x.  Nothing to do after a non-finite activation (the fp32 kernels
+// compute the convolution).
+__global__ void __launch_bounds__(256) convh_splitk_finish(HArgs A) {
+  const unsigned mbits = *A.xmax;
+  if (mbits >= 0x7f800000u) return;
+  const float unscale = ldexpf(1.0f, -convh_scale_exp(mbits));
+  const int64_t b = blockIdx.z;
+  for (int64_t m = blockIdx.y; m < A.M; m += gridDim.y) {
+    const int64_t co = m / A.P, r = m - co * A.P;
+    const float bias = A.bias ? A.bias[co] : 0.0f;
+    const float sc = A.dq.scale ? load_as_f32(A.dq.scale, A.dq.scale_dt, co * A.dq.scale_stride)
+                                : 1.0f;
+    const float* p0 = A.part + (b * A.ksplit * A.M + m) * A.Nq;
+    float* orow = A.out + (b * A.Cout + co) * A.Lout;
+    for (int64_t qq = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; qq < A.Nq;
+         qq += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+      float acc = p0[qq];
+      for (int s = 1; s < A.ksplit; ++s) acc += p0[s * A.M * A.Nq + qq];
+      const float u = acc * unscale;  // exact: a power of two
+      const float v = A.dq.scale ? u * sc : u;
+      const int64_t pos = qq * A.os + r + A.ophase0;
+      if (pos >= 0 && pos < A.Lout) orow[pos] = A.bias ? v + bias : v;
+    }
+  }
+}
+
 __global__ void convh_flag_clear(int* flag, unsigned* xmax) {
   *flag = 0;
   *xmax = 0u;
@@ -284,45 +521,87 @@ __global__ void __launch_bounds__(256) convh_absmax(const float* __restrict__ x,
 
 // Wt[m][kk] (m = co*P + r, kk = t*Cin + ci): the fp16 value the gathering
 // kernel forms, W less the zero point (0 past the kernel for transposed).
+// Rows m on the grid's y axis, kk along x, 32-bit index arithmetic (the
+// host checks the weight count and M * Kg against 2^31): a flat 64-bit walk
+// with a division chain per element took 16.8 us for ConvTranspose1d
+// 512->256 k20's 2.6M values, this 14 us -- bound by the transposed
+// weights' reads, one cache line per element (a block per output channel
+// staging its weights through LDS measured slower, 23 us).
 template <typename TW>
-__global__ void convh_weights(_Float16* __restrict__ wt, HArgs A) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) {  // this call's flag and max start clear
+__global__ void __launch_bounds__(256) convh_weights(_Float16* __restrict__ wt, HArgs A) {
+  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
     *A.flag = 0;
     *A.xmax = 0u;
   }
   const TW* w = static_cast<const TW*>(A.w);
-  const int64_t total = A.M * A.Kg, cout = A.M / A.P;
-  for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t kk = i % A.Kg, m = i / A.Kg;
-    const int64_t co = m / A.P, r = m - co * A.P;
-    const int64_t t = kk / A.Cin, ci = kk - t * A.Cin;
-    const int64_t tap = A.transposed ? r + A.s * t : t;
-    float v = 0.0f;
-    if (tap < A.Kw) {
-      const int64_t idx = A.transposed ? (ci * cout + co) * A.Kw + tap : (co * A.Cin + ci) * A.Kw + tap;
-      const float zp = A.dq.zp ? load_as_f32(A.dq.zp, A.dq.zp_dt, co * A.dq.zp_stride) : 0.0f;
-      v = static_cast<float>(w[idx]) - zp;
+  const int P = A.P, Kg = static_cast<int>(A.Kg), Cin = static_cast<int>(A.Cin);
+  const int Kw = static_cast<int>(A.Kw), s = static_cast<int>(A.s);
+  const int M = static_cast<int>(A.M), cout = M / P;
+  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+    const int co = m / P, r = m - co * P;
+    const float zp = A.dq.zp ? load_as_f32(A.dq.zp, A.dq.zp_dt, co * A.dq.zp_stride) : 0.0f;
+    _Float16* row = wt + static_cast<int64_t>(m) * Kg;
+    for (int kk = blockIdx.x * blockDim.x + threadIdx.x; kk < Kg; kk += gridDim.x * blockDim.x) {
+      const int t = kk / Cin, ci = kk - t * Cin;
+      const int tap = A.transposed ? r + s * t : t;
+      float v = 0.0f;
+      if (tap < Kw) {
+        const int idx = A.transposed ? (ci * cout + co) * Kw + tap : (co * Cin + ci) * Kw + tap;
+        v = static_cast<float>(w[idx]) - zp;
+      }
+      row[kk] = static_cast<_Float16>(v);
     }
-    wt[i] = static_cast<_Float16>(v);
   }
+}
+
+// The ring kernel needs the rearranged weights and 32-bit buffer offsets.
+static bool ring_ok(const HArgs& a) {
+  return a.wt && a.M * a.Kg * 2 < (int64_t{1} << 31) && a.Cin * a.L * 4 < (int64_t{1} << 31);
 }
 
 template <class T, typename TW>
 static void launch_t(const HArgs& a, const dim3& grid) {
-  if (a.wt)
+  if (ring_ok(a))
+    hipLaunchKernelGGL((convh_ring_kernel<T>), grid, dim3(kThreads), 0, ctx().stream, a);
+  else if (a.wt)
     hipLaunchKernelGGL((convh_kernel<T, TW, true>), grid, dim3(kThreads), 0, ctx().stream, a);
   else
     hipLaunchKernelGGL((convh_kernel<T, TW, false>), grid, dim3(kThreads), 0, ctx().stream, a);
 }
 
+// Split-K count for the ring kernel: enough splits that every CU gets two
+// blocks, at most 4, at least 8 K-steps a split, and the partial sums
+// within `part_bytes` (the context scratch left beside the rearranged
+// weights); 1 when no CU is short.  The choice depends on sizes alone, so a
+// call recorded into a graph sums in the same order as the same call made
+// eagerly.
 template <class T>
-static void launch(const HArgs& a, int w_dt, int64_t batch) {
+static int ksplit_for(const HArgs& a, int64_t batch, size_t part_bytes) {
+  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  const int64_t blocks = batch * ceil_div(a.Nq, T::BN) * ceil_div(a.M, T::BM);
+  if (!ring_ok(a) || blocks >= 2 * cus) return 1;
+  const int64_t nk = a.Kg / kBK;
+  const int64_t room = static_cast<int64_t>(part_bytes) / (4 * batch * a.M * a.Nq);
+  const int64_t s = std::min<int64_t>({4, ceil_div(2 * cus, blocks), nk / 8, room});
+  return static_cast<int>(std::max<int64_t>(1, s));
+}
+
+template <class T>
+static void launch(HArgs& a, int w_dt, int64_t batch, float* part, size_t part_bytes) {
+  a.ksplit = ksplit_for<T>(a, batch, part_bytes);
+  a.part = a.ksplit > 1 ? part : nullptr;
   const dim3 grid(static_cast<unsigned>(ceil_div(a.Nq, T::BN)), static_cast<unsigned>(ceil_div(a.M, T::BM)),
-                  static_cast<unsigned>(batch));
+                  static_cast<unsigned>(batch * a.ksplit));
   if (w_dt == KK_F16) launch_t<T, _Float16>(a, grid);
   else if (w_dt == KK_I8) launch_t<T, int8_t>(a, grid);
   else launch_t<T, uint8_t>(a, grid);
+  if (a.part) {
+    const dim3 fg(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Nq, 256), 64)),
+                  static_cast<unsigned>(std::min<int64_t>(a.M, 65535)), static_cast<unsigned>(batch));
+    hipLaunchKernelGGL(convh_splitk_finish, fg, dim3(256), 0, ctx().stream, a);
+    a.part = nullptr;
+    a.ksplit = 1;
+  }
 }
 
 // Rearranges the weights into the context scratch (or, larger, into a
@@ -335,13 +614,14 @@ static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
   else if (!ctx().capturing && kk_alloc(wt_bytes, ws) == KK_OK) wtp = *ws;
   if (wtp) {
     _Float16* wt = static_cast<_Float16*>(wtp);
-    const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(a.M * a.Kg, 256), 4096));
+    const dim3 g(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Kg, 256), 64)),
+                 static_cast<unsigned>(std::min<int64_t>(a.M, 65535)));
     if (w->dtype == KK_F16)
-      hipLaunchKernelGGL(convh_weights<_Float16>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+      hipLaunchKernelGGL(convh_weights<_Float16>, g, dim3(256), 0, ctx().stream, wt, a);
     else if (w->dtype == KK_I8)
-      hipLaunchKernelGGL(convh_weights<int8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+      hipLaunchKernelGGL(convh_weights<int8_t>, g, dim3(256), 0, ctx().stream, wt, a);
     else
-      hipLaunchKernelGGL(convh_weights<uint8_t>, dim3(g), dim3(256), 0, ctx().stream, wt, a);
+      hipLaunchKernelGGL(convh_weights<uint8_t>, g, dim3(256), 0, ctx().stream, wt, a);
     a.wt = wt;
   } else {
     hipLaunchKernelGGL(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, a.flag, a.xmax);
@@ -352,13 +632,23 @@ static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
     const int vec = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 ? 1 : 0;
     hipLaunchKernelGGL(convh_absmax, dim3(g), dim3(256), 0, ctx().stream, a.x, n, vec, a.xmax);
   }
+  // split-K partial sums: the context scratch beside weights rearranged there
+  float* part = nullptr;
+  size_t part_bytes = 0;
+  if (wtp == ctx().scratch) {
+    const size_t off = (wt_bytes + 255) & ~size_t{255};
+    if (off < kScratchBytes) {
+      part = reinterpret_cast<float*>(static_cast<char*>(ctx().scratch) + off);
+      part_bytes = kScratchBytes - off;
+    }
+  }
   // the largest tile that still gives every CU two blocks; 128 x 32 below that
   const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
-  if (a.M <= 32) launch<Tile<1, 1, 1>>(a, w->dtype, batch);
-  else if (a.M <= 64) launch<Tile<2, 1, 2>>(a, w->dtype, batch);
+  if (a.M <= 32) launch<Tile<1, 1, 1>>(a, w->dtype, batch, part, part_bytes);
+  else if (a.M <= 64) launch<Tile<2, 1, 2>>(a, w->dtype, batch, part, part_bytes);
   else if (batch * ceil_div(a.M, 128) * ceil_div(a.Nq, 128) >= 2 * cus)
-    launch<Tile<2, 2, 2>>(a, w->dtype, batch);
-  else launch<Tile<4, 1, 1>>(a, w->dtype, batch);
+    launch<Tile<2, 2, 2>>(a, w->dtype, batch, part, part_bytes);
+  else launch<Tile<4, 1, 1>>(a, w->dtype, batch, part, part_bytes);
 }
 
 }  // namespace convh
@@ -396,6 +686,7 @@ bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, con
   a.xmax = reinterpret_cast<unsigned*>(ctx().row_counters + kRowCounters + kFlagConvhMax);
   a.Cin = Cin; a.L = L; a.M = M; a.Cout = Cout; a.Kg = Kg; a.Nq = Nq; a.Lout = Lout;
   a.P = static_cast<int>(P);
+  a.ksplit = 1;
   if (transposed) {
     a.qs = 1; a.tap_mul = -1; a.tap_add = 0; a.os = stride; a.ophase0 = -pad0;
   } else {
