@@ -73,6 +73,7 @@ struct HArgs {
   // (raw, in the activations' scaled units), NULL for the direct epilogue
   int ksplit;
   float* part;
+  int64_t Mp;  // rows of the rearranged weights: M rounded up to 128 (zeros past M)
 };
 
 // WAVES_M x (4 / WAVES_M) wavefronts, each owning WM_T x WN_T tiles of 32x32.
@@ -269,9 +270,10 @@ __global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
   __shared__ __align__(16) _Float16 As[2][T::BM * kPitch];
   __shared__ __align__(16) _Float16 Bh[2][T::BN * kPitch];
   __shared__ __align__(16) _Float16 Bl[2][T::BN * kPitch];
-  constexpr int WM_T = T::WM_T, WN_T = T::WN_T, KPT = T::KPT, BP = T::B_PAIRS;
-  constexpr int AW = KPT / 2;  // dwords of A a thread stages per step
-  static_assert(KPT == 4 || KPT % 8 == 0, "A staging width");
+  constexpr int WM_T = T::WM_T, WN_T = T::WN_T, BP = T::B_PAIRS;
+  // A: a step's BM x 32 weight tile is BM * 4 16-byte pieces in a row;
+  // thread t takes pieces t and t + 256 (as many as there are)
+  constexpr int NPC = T::BM * 4, APT = (NPC + kThreads - 1) / kThreads;
   const unsigned mbits = *A.xmax;
   if (mbits >= 0x7f800000u) {  // an infinite or NaN activation: the fp32 kernels compute it
     if (threadIdx.x == 0) *A.flag = 1;  // every writer stores the same 1
@@ -288,20 +290,17 @@ __global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
   const int nk_all = static_cast<int>(A.Kg / kBK);
   const int kt0 = static_cast<int>(static_cast<int64_t>(nk_all) * split / A.ksplit);
   const int nk = static_cast<int>(static_cast<int64_t>(nk_all) * (split + 1) / A.ksplit) - kt0;
-  const int am = tid % T::BM, ak = KPT * (tid / T::BM);
-  const int Kg = static_cast<int>(A.Kg), Cin = static_cast<int>(A.Cin), L = static_cast<int>(A.L);
+  const int Cin = static_cast<int>(A.Cin), L = static_cast<int>(A.L);
   const auto wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A.wt), 0,
-                                                     static_cast<int>(A.M * A.Kg * 2), 0x00020000);
+                                                     static_cast<int>(A.Kg * A.Mp * 2), 0x00020000);
   const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A.x + b * A.Cin * A.L), 0,
                                                      static_cast<int>(A.Cin * A.L * 4), 0x00020000);
-  // rows past M read past the buffer's end: zeros
-  const uint32_t a_base = static_cast<uint32_t>((m0 + am) * A.Kg + ak) * 2u;
   const int bn = tid % T::BN;
   const int64_t q = n0 + bn;
   const int q_pos = static_cast<int>(q * A.qs + A.tap_add);
   const bool q_in = q < A.Nq;
   struct Slot {
-    uint32_t a[AW];
+    uint4 a[APT];
     float b[BP][2];
   };
   Slot ring[3];
@@ -320,18 +319,17 @@ __global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
         ++f_t;
       }
     }
-    const uint32_t ao = a_base + static_cast<uint32_t>(k0) * 2u;
-    if constexpr (KPT == 4) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(wrs, ao, 0, 0);
-      sl.a[0] = v[0];
-      sl.a[1] = v[1];
-    } else {
+    // the step's weight tile: Wt rows m0 .. m0+BM-1 of step k0 / 32, one
+    // contiguous stretch (the old row-major Wt gave every lane of a load its
+    // own cache line)
+    const uint32_t ao = static_cast<uint32_t>(((k0 / kBK) * A.Mp + m0) * 64);
 #pragma unroll
-      for (int e = 0; e < AW; e += 4) {
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, ao + 4u * e, 0, 0);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) sl.a[e + u] = v[u];
-      }
+    for (int e = 0; e < APT; ++e) {
+      const int pc = tid + kThreads * e;
+      uint32_t off = pc < NPC ? ao + 16u * pc : 0x80000000u;
+      asm volatile("" : "+v"(off));
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+      sl.a[e] = make_uint4(v[0], v[1], v[2], v[3]);
     }
     const int pos = q_pos + t * static_cast<int>(A.tap_mul);
     const bool in = q_in && pos >= 0 && pos < L;
@@ -350,8 +348,10 @@ __global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
   };
   auto stash = [&](const Slot& sl, int buf) {
 #pragma unroll
-    for (int e = 0; e < AW; e += 2)
-      *reinterpret_cast<uint2*>(&As[buf][am * kPitch + ak + 2 * e]) = make_uint2(sl.a[e], sl.a[e + 1]);
+    for (int e = 0; e < APT; ++e) {
+      const int pc = tid + kThreads * e;  // row pc / 4, halves 8 (pc % 4)
+      if (pc < NPC) *reinterpret_cast<uint4*>(&As[buf][(pc >> 2) * kPitch + 8 * (pc & 3)]) = sl.a[e];
+    }
 #pragma unroll
     for (int j = 0; j < BP; ++j) {
       const int kp = tid / T::BN + j * T::KP_STEP;
@@ -519,8 +519,10 @@ __global__ void __launch_bounds__(256) convh_absmax(const float* __restrict__ x,
   if (threadIdx.x == 0) atomicMax(xmax, max(max(part[0], part[1]), max(part[2], part[3])));
 }
 
-// Wt[m][kk] (m = co*P + r, kk = t*Cin + ci): the fp16 value the gathering
-// kernel forms, W less the zero point (0 past the kernel for transposed).
+// Wt[kk / 32][m][kk % 32] (m = co*P + r, kk = t*Cin + ci; Mp rows a step,
+// zeros past M): the fp16 value the gathering kernel forms, W less the zero
+// point (0 past the kernel for transposed), stored step by step so that a
+// step's weight tile is one stretch.
 // Rows m on the grid's y axis, kk along x, 32-bit index arithmetic (the
 // host checks the weight count and M * Kg against 2^31): a flat 64-bit walk
 // with a division chain per element took 16.8 us for ConvTranspose1d
@@ -536,35 +538,35 @@ __global__ void __launch_bounds__(256) convh_weights(_Float16* __restrict__ wt, 
   const TW* w = static_cast<const TW*>(A.w);
   const int P = A.P, Kg = static_cast<int>(A.Kg), Cin = static_cast<int>(A.Cin);
   const int Kw = static_cast<int>(A.Kw), s = static_cast<int>(A.s);
-  const int M = static_cast<int>(A.M), cout = M / P;
-  for (int m = blockIdx.y; m < M; m += gridDim.y) {
+  const int M = static_cast<int>(A.M), Mp = static_cast<int>(A.Mp), cout = M / P;
+  for (int m = blockIdx.y; m < Mp; m += gridDim.y) {
     const int co = m / P, r = m - co * P;
-    const float zp = A.dq.zp ? load_as_f32(A.dq.zp, A.dq.zp_dt, co * A.dq.zp_stride) : 0.0f;
-    _Float16* row = wt + static_cast<int64_t>(m) * Kg;
+    const float zp = A.dq.zp && m < M ? load_as_f32(A.dq.zp, A.dq.zp_dt, co * A.dq.zp_stride) : 0.0f;
     for (int kk = blockIdx.x * blockDim.x + threadIdx.x; kk < Kg; kk += gridDim.x * blockDim.x) {
       const int t = kk / Cin, ci = kk - t * Cin;
       const int tap = A.transposed ? r + s * t : t;
       float v = 0.0f;
-      if (tap < Kw) {
+      if (m < M && tap < Kw) {
         const int idx = A.transposed ? (ci * cout + co) * Kw + tap : (co * Cin + ci) * Kw + tap;
         v = static_cast<float>(w[idx]) - zp;
       }
-      row[kk] = static_cast<_Float16>(v);
+      wt[(static_cast<int64_t>(kk / kBK) * Mp + m) * kBK + (kk % kBK)] = static_cast<_Float16>(v);
     }
   }
 }
 
-// The ring kernel needs the rearranged weights and 32-bit buffer offsets.
+// The ring kernel's 32-bit buffer offsets: weights (step-major) and one
+// batch of activations below 2^31 bytes; else the gathering kernel runs.
 static bool ring_ok(const HArgs& a) {
-  return a.wt && a.M * a.Kg * 2 < (int64_t{1} << 31) && a.Cin * a.L * 4 < (int64_t{1} << 31);
+  return a.Kg * a.Mp * 2 < (int64_t{1} << 31) && a.Cin * a.L * 4 < (int64_t{1} << 31);
 }
 
+// Rearranged weights (a.wt) go to the ring kernel, else the kernel gathers
+// them from W.
 template <class T, typename TW>
 static void launch_t(const HArgs& a, const dim3& grid) {
-  if (ring_ok(a))
+  if (a.wt)
     hipLaunchKernelGGL((convh_ring_kernel<T>), grid, dim3(kThreads), 0, ctx().stream, a);
-  else if (a.wt)
-    hipLaunchKernelGGL((convh_kernel<T, TW, true>), grid, dim3(kThreads), 0, ctx().stream, a);
   else
     hipLaunchKernelGGL((convh_kernel<T, TW, false>), grid, dim3(kThreads), 0, ctx().stream, a);
 }
@@ -579,7 +581,7 @@ template <class T>
 static int ksplit_for(const HArgs& a, int64_t batch, size_t part_bytes) {
   const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
   const int64_t blocks = batch * ceil_div(a.Nq, T::BN) * ceil_div(a.M, T::BM);
-  if (!ring_ok(a) || blocks >= 2 * cus) return 1;
+  if (!a.wt || blocks >= 2 * cus) return 1;
   const int64_t nk = a.Kg / kBK;
   const int64_t room = static_cast<int64_t>(part_bytes) / (4 * batch * a.M * a.Nq);
   const int64_t s = std::min<int64_t>({4, ceil_div(2 * cus, blocks), nk / 8, room});
@@ -608,14 +610,16 @@ static void launch(HArgs& a, int w_dt, int64_t batch, float* part, size_t part_b
 // pooled workspace unless a graph is being recorded; else the kernel
 // gathers them); launches the tile that suits M x Nq.
 static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
-  const size_t wt_bytes = static_cast<size_t>(a.M * a.Kg * 2);
+  a.Mp = ceil_div(a.M, 128) * 128;
+  const size_t wt_bytes = static_cast<size_t>(a.Kg * a.Mp * 2);
   void* wtp = nullptr;
-  if (wt_bytes <= kScratchBytes) wtp = ctx().scratch;
+  if (!ring_ok(a)) wtp = nullptr;
+  else if (wt_bytes <= kScratchBytes) wtp = ctx().scratch;
   else if (!ctx().capturing && kk_alloc(wt_bytes, ws) == KK_OK) wtp = *ws;
   if (wtp) {
     _Float16* wt = static_cast<_Float16*>(wtp);
     const dim3 g(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Kg, 256), 64)),
-                 static_cast<unsigned>(std::min<int64_t>(a.M, 65535)));
+                 static_cast<unsigned>(std::min<int64_t>(a.Mp, 65535)));
     if (w->dtype == KK_F16)
       hipLaunchKernelGGL(convh_weights<_Float16>, g, dim3(256), 0, ctx().stream, wt, a);
     else if (w->dtype == KK_I8)
