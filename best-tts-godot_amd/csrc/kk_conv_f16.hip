@@ -458,30 +458,37 @@ __global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
     }
 }
 
-// Split-K's finish: out at (m, q) = the splits' sums added in split order,
-// then the epilogue above.  Row m on the grid's y axis (and batch on z), q
-// along x.  Nothing to do after a non-finite activation (the fp32 kernels
-// compute the convolution).
+// Split-K's finish: out[b, co, pos] = the splits' sums at (m, q) added in
+// split order, then the epilogue above, where pos - ophase0 = q P + r and
+// m = co P + r (P = os: one phase per output position).  A thread per
+// output position (blocks along the row on x, channels on y, batch on z),
+// so the stores run along each output row; 32-bit indexes (the host keeps
+// M Nq and Cout Lout below 2^31).  Nothing to do after a non-finite
+// activation (the fp32 kernels compute the convolution).
 __global__ void __launch_bounds__(256) convh_splitk_finish(HArgs A) {
   const unsigned mbits = *A.xmax;
   if (mbits >= 0x7f800000u) return;
   const float unscale = ldexpf(1.0f, -convh_scale_exp(mbits));
-  const int64_t b = blockIdx.z;
-  for (int64_t m = blockIdx.y; m < A.M; m += gridDim.y) {
-    const int64_t co = m / A.P, r = m - co * A.P;
+  const int P = A.P, Nq = static_cast<int>(A.Nq), Lout = static_cast<int>(A.Lout);
+  const int MN = static_cast<int>(A.M * A.Nq), ks = A.ksplit, ph0 = static_cast<int>(A.ophase0);
+  const int b = blockIdx.z;
+  for (int co = blockIdx.y; co < static_cast<int>(A.Cout); co += gridDim.y) {
     const float bias = A.bias ? A.bias[co] : 0.0f;
     const float sc = A.dq.scale ? load_as_f32(A.dq.scale, A.dq.scale_dt, co * A.dq.scale_stride)
                                 : 1.0f;
-    const float* p0 = A.part + (b * A.ksplit * A.M + m) * A.Nq;
-    float* orow = A.out + (b * A.Cout + co) * A.Lout;
-    for (int64_t qq = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; qq < A.Nq;
-         qq += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-      float acc = p0[qq];
-      for (int s = 1; s < A.ksplit; ++s) acc += p0[s * A.M * A.Nq + qq];
-      const float u = acc * unscale;  // exact: a power of two
-      const float v = A.dq.scale ? u * sc : u;
-      const int64_t pos = qq * A.os + r + A.ophase0;
-      if (pos >= 0 && pos < A.Lout) orow[pos] = A.bias ? v + bias : v;
+    const float* pb = A.part + static_cast<int64_t>(b) * ks * MN;
+    float* orow = A.out + (static_cast<int64_t>(b) * A.Cout + co) * Lout;
+    for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < Lout; pos += gridDim.x * blockDim.x) {
+      const int u = pos - ph0;
+      if (u < 0) continue;
+      const int q = u / P, r = u - q * P;
+      if (q >= Nq) continue;
+      const int i = (co * P + r) * Nq + q;
+      float acc = pb[i];
+      for (int sp = 1; sp < ks; ++sp) acc += pb[sp * MN + i];
+      const float v0 = acc * unscale;  // exact: a power of two
+      const float v = A.dq.scale ? v0 * sc : v0;
+      orow[pos] = A.bias ? v + bias : v;
     }
   }
 }
@@ -581,7 +588,9 @@ template <class T>
 static int ksplit_for(const HArgs& a, int64_t batch, size_t part_bytes) {
   const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
   const int64_t blocks = batch * ceil_div(a.Nq, T::BN) * ceil_div(a.M, T::BM);
-  if (!a.wt || blocks >= 2 * cus) return 1;
+  if (!a.wt || blocks >= 2 * cus || a.M * a.Nq >= (int64_t{1} << 31) / 4 ||
+      a.Cout * a.Lout >= (int64_t{1} << 31))
+    return 1;
   const int64_t nk = a.Kg / kBK;
   const int64_t room = static_cast<int64_t>(part_bytes) / (4 * batch * a.M * a.Nq);
   const int64_t s = std::min<int64_t>({4, ceil_div(2 * cus, blocks), nk / 8, room});
@@ -598,8 +607,8 @@ static void launch(HArgs& a, int w_dt, int64_t batch, float* part, size_t part_b
   else if (w_dt == KK_I8) launch_t<T, int8_t>(a, grid);
   else launch_t<T, uint8_t>(a, grid);
   if (a.part) {
-    const dim3 fg(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Nq, 256), 64)),
-                  static_cast<unsigned>(std::min<int64_t>(a.M, 65535)), static_cast<unsigned>(batch));
+    const dim3 fg(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Lout, 256), 64)),
+                  static_cast<unsigned>(std::min<int64_t>(a.Cout, 65535)), static_cast<unsigned>(batch));
     hipLaunchKernelGGL(convh_splitk_finish, fg, dim3(256), 0, ctx().stream, a);
     a.part = nullptr;
     a.ksplit = 1;
