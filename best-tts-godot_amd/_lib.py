@@ -88,6 +88,8 @@ PROTOTYPES = {
     "kk_conv_integer": [_T, _T, _T, _T, _T, _i, _i, _i, _i, _i],
     "kk_conv_integer_scaled": [_T] * 7 + [_i, _i, _i, _i, _i],
     "kk_conv_integer_scaled_qbias": [_T] * 8 + [_i, _i, _i, _i, _i],
+    "kk_conv_integer_scaled_add": [_T] * 8 + [_i, _i, _i, _i, _i],
+    "kk_conv_integer_scaled_qbias_add": [_T] * 9 + [_i, _i, _i, _i, _i],
     "kk_conv_integer_scaled_qbias_noalloc": [_T] * 8 + [_i, _i, _i, _i, _i],
     "kk_instance_norm_scale_shift": [_T, _T, _T, _T, _f, _i, _f],
     "kk_instance_norm_scale_shift_snake": [_T, _T, _T, _T, _T, _T, _f],

@@ -104,6 +104,7 @@ struct ConvI8Args {
   float* outf;          // [N][Cout][Lout] float(acc + bias[co]) * scale
   const int32_t* bias;  // [Cout] or NULL
   const float* scale;   // 1 or Cout values
+  const float* resid;   // with outf: [N][Cout][Lout] added after the scale (the Add), or NULL
   int64_t scale_n;
   int64_t Cout, Cin, CinP, Kw, s, d, L, p0, Lout, Kreal;
   int W4;               // time rows staged per block: the window plus alignment slack
@@ -125,8 +126,10 @@ struct ConvI8Args {
 // % 2), register (i / 8) 4 + i % 4.  The epilogue's per-channel constants
 // and the staged rows' channel sums sit in LDS.
 // TN (128 or 64) output steps per block; a wave covers TN / 2 of them.
-template <int TN>
-__global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
+// RES: the scaled fp32 output plus A.resid (its own instantiation: the
+// residual's registers would lower the plain kernel's occupancy).
+template <int TN, bool RES>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) conv_i8_kernel(ConvI8Args A) {
   constexpr int NI = TN / 64;  // 32-wide MFMA tiles per wave along time
   extern __shared__ __align__(16) int8_t conv_lds[];
   int8_t* Bw = conv_lds;                                          // [W4][kRowPitch]
@@ -291,17 +294,40 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
   // outputs from the block's corner, 32-bit byte offsets (the host checks
   // that a batch's output stays below 2 GiB); a block wholly inside the
   // output skips the per-element bounds checks
+  const int64_t o_elem = (b * A.Cout + m0) * A.Lout + nb;
   char* ob = reinterpret_cast<char*>(A.outf ? static_cast<void*>(A.outf) : static_cast<void*>(A.out)) +
-             4 * ((b * A.Cout + m0) * A.Lout + nb);
+             4 * o_elem;
   const uint32_t lout4 = static_cast<uint32_t>(4 * A.Lout);
   const bool full = m0 + kTileM <= A.Cout && nb + TN <= A.Lout;
   const int c_rem = static_cast<int>(A.Cout - m0), l_rem = static_cast<int>(A.Lout - nb);
   const int lane_c = wm * 64 + 4 * g, lane_j = wn * (TN / 2) + r;
   const uint32_t lane_off = static_cast<uint32_t>(lane_c) * lout4 + 4u * static_cast<uint32_t>(lane_j);
+  // the residual at the output's element offsets, through a buffer resource
+  // over this batch's [Cout][Lout] (a read past it returns 0: rows past Cout
+  // and columns past Lout of edge blocks are read but never stored)
+  const auto rrs = __builtin_amdgcn_make_buffer_rsrc(
+      RES ? const_cast<float*>(A.resid) + b * A.Cout * A.Lout : nullptr, 0,
+      RES ? static_cast<int>(A.Cout * A.Lout * 4) : 0, 0x00020000);
+  const uint32_t r_off = static_cast<uint32_t>(4 * (m0 * A.Lout + nb)) + lane_off;
   auto epilogue = [&](auto full_tile) {
     constexpr bool kFull = decltype(full_tile)::value;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
+      // the residual of this half of the lane's outputs, all loads issued
+      // before the first store (a load after a store to a possibly aliasing
+      // address would wait for it: one memory round trip per element)
+      float rv[16][NI];
+      if constexpr (RES) {
+#pragma unroll
+        for (int reg = 0; reg < 16; ++reg) {
+          const int cr = 32 * mi + 8 * (reg / 4) + (reg % 4);
+          const uint32_t roff = r_off + static_cast<uint32_t>(cr) * lout4;
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni)
+            rv[reg][ni] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(rrs, roff + 128u * ni, 0, 0));
+        }
+      }
 #pragma unroll
       for (int reg = 0; reg < 16; ++reg) {
         const int cr = 32 * mi + 8 * (reg / 4) + (reg % 4);  // constant once unrolled
@@ -315,8 +341,13 @@ __global__ void __launch_bounds__(256) conv_i8_kernel(ConvI8Args A) {
           if (!kFull && lane_j + 32 * ni >= l_rem) continue;
           const int v = acc[mi][ni][reg] + c - zS[ni];
           char* dst = ob + (roff + 128u * ni);
-          if (A.outf) *reinterpret_cast<float*>(dst) = static_cast<float>(v) * sc;
-          else *reinterpret_cast<int*>(dst) = v;
+          if constexpr (RES) {
+            *reinterpret_cast<float*>(dst) = static_cast<float>(v) * sc + rv[reg][ni];
+          } else if (A.outf) {
+            *reinterpret_cast<float*>(dst) = static_cast<float>(v) * sc;
+          } else {
+            *reinterpret_cast<int*>(dst) = v;
+          }
         }
       }
     }
@@ -475,7 +506,8 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
                      const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
                      const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
                      bool outf, const kk_tensor* qb_sa = nullptr, const kk_tensor* qb_sw = nullptr,
-                     const kk_tensor* qb_bias = nullptr, void* fixed_ws = nullptr) {
+                     const kk_tensor* qb_bias = nullptr, void* fixed_ws = nullptr,
+                     const kk_tensor* resid = nullptr) {
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], Kw = w->shape[2];
   const int64_t Lout = out->shape[2];
@@ -521,13 +553,19 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     }
     A.Cout = Cout; A.Cin = Cin; A.CinP = CinP; A.Kw = Kw; A.s = stride; A.d = dilation;
     A.L = L; A.p0 = pad0; A.Lout = Lout; A.Kreal = Cin * Kw;
+    A.resid = resid ? static_cast<const float*>(resid->data) : nullptr;
     A.aligned = (L % 4 == 0) && (reinterpret_cast<uintptr_t>(x->data) % 4 == 0);
     const int tn = conv_launch_tile(stride, dilation, Kw, N, CoutP, Lout);
     A.W4 = static_cast<int>(conv_rows(tn, stride, dilation, Kw));
     const dim3 grid(static_cast<unsigned>(ceil_div(Lout, tn)),
                     static_cast<unsigned>(CoutP / kTileM), static_cast<unsigned>(N));
-    if (tn == 128) hipLaunchKernelGGL(conv_i8_kernel<128>, grid, dim3(256), conv_lds(A.W4), st, A);
-    else hipLaunchKernelGGL(conv_i8_kernel<64>, grid, dim3(256), conv_lds(A.W4), st, A);
+    if (A.resid) {
+      if (tn == 128) hipLaunchKernelGGL((conv_i8_kernel<128, true>), grid, dim3(256), conv_lds(A.W4), st, A);
+      else hipLaunchKernelGGL((conv_i8_kernel<64, true>), grid, dim3(256), conv_lds(A.W4), st, A);
+    } else {
+      if (tn == 128) hipLaunchKernelGGL((conv_i8_kernel<128, false>), grid, dim3(256), conv_lds(A.W4), st, A);
+      else hipLaunchKernelGGL((conv_i8_kernel<64, false>), grid, dim3(256), conv_lds(A.W4), st, A);
+    }
     rc = check_launch("conv_i8_kernel");
   }
   if (!fixed_ws) kk_free(ws);  // stream order keeps the workspace alive for the kernels
@@ -552,27 +590,60 @@ int kk_conv_integer(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w
                           false);
 }
 
-int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
-                           const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
-                           const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
-                           int group) {
+}  // extern "C"
+
+// The residual of the _add entry points: fp32, contiguous, shaped like out.
+static int check_resid(const kk_tensor* out, const kk_tensor* resid, const char* who) {
+  KK_TRY(check_tensor(resid, "resid"));
+  bool same = resid->rank == out->rank;
+  for (int i = 0; same && i < out->rank; ++i) same = resid->shape[i] == out->shape[i];
+  if (resid->dtype != KK_F32 || !is_contiguous(resid) || !same)
+    return set_error(KK_E_ARG, "%s: resid must be fp32, contiguous and shaped like out", who);
+  return KK_OK;
+}
+
+static int scaled_entry(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                        const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                        const kk_tensor* scale, const kk_tensor* resid, int stride, int dilation,
+                        int pad0, int pad1, int group, const char* who) {
   int64_t Lout = 0;
   KK_TRY(check_conv_integer(out, x, w, x_zp, w_zp, stride, dilation, pad0, pad1, group, KK_F32,
-                            "kk_conv_integer_scaled", &Lout));
+                            who, &Lout));
+  if (resid) KK_TRY(check_resid(out, resid, who));
   const int64_t Cout = w->shape[0];
   KK_TRY(check_tensor(scale, "scale"));
   if (scale->dtype != KK_F32 || !is_contiguous(scale) ||
       (numel(scale) != 1 && numel(scale) != Cout))
-    return set_error(KK_E_ARG, "kk_conv_integer_scaled: scale must be fp32 with 1 or Cout values");
+    return set_error(KK_E_ARG, "%s: scale must be fp32 with 1 or Cout values", who);
   if (bias) {
     KK_TRY(check_tensor(bias, "bias"));
     if (bias->dtype != KK_I32 || !is_contiguous(bias) || numel(bias) != Cout)
-      return set_error(KK_E_ARG, "kk_conv_integer_scaled: bias must be int32 with Cout values");
+      return set_error(KK_E_ARG, "%s: bias must be int32 with Cout values", who);
   }
   if (numel(out) == 0) return KK_OK;
   if (x->shape[1] * w->shape[2] == 0)
-    return set_error(KK_E_UNSUPPORTED, "kk_conv_integer_scaled: empty reduction");
-  return conv_integer_run(out, x, w, x_zp, w_zp, bias, scale, stride, dilation, pad0, pad1, true);
+    return set_error(KK_E_UNSUPPORTED, "%s: empty reduction", who);
+  return conv_integer_run(out, x, w, x_zp, w_zp, bias, scale, stride, dilation, pad0, pad1, true,
+                          nullptr, nullptr, nullptr, nullptr, resid);
+}
+
+extern "C" {
+
+int kk_conv_integer_scaled(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                           const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                           const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
+                           int group) {
+  return scaled_entry(out, x, w, x_zp, w_zp, bias, scale, nullptr, stride, dilation, pad0, pad1,
+                      group, "kk_conv_integer_scaled");
+}
+
+int kk_conv_integer_scaled_add(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                               const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                               const kk_tensor* scale, const kk_tensor* resid, int stride,
+                               int dilation, int pad0, int pad1, int group) {
+  if (!resid) return set_error(KK_E_ARG, "kk_conv_integer_scaled_add: resid is required");
+  return scaled_entry(out, x, w, x_zp, w_zp, bias, scale, resid, stride, dilation, pad0, pad1,
+                      group, "kk_conv_integer_scaled_add");
 }
 
 }  // extern "C"
@@ -615,6 +686,22 @@ int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const
   if (empty) return KK_OK;
   return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
                           true, scale_a, scale_w, bias);
+}
+
+int kk_conv_integer_scaled_qbias_add(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                                     const kk_tensor* x_zp, const kk_tensor* w_zp,
+                                     const kk_tensor* bias, const kk_tensor* scale_a,
+                                     const kk_tensor* scale_w, const kk_tensor* resid, int stride,
+                                     int dilation, int pad0, int pad1, int group) {
+  const char* who = "kk_conv_integer_scaled_qbias_add";
+  bool empty = false;
+  KK_TRY(check_qbias(out, x, w, x_zp, w_zp, bias, scale_a, scale_w, stride, dilation, pad0, pad1,
+                     group, who, &empty));
+  if (!resid) return set_error(KK_E_ARG, "%s: resid is required", who);
+  KK_TRY(check_resid(out, resid, who));
+  if (empty) return KK_OK;
+  return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
+                          true, scale_a, scale_w, bias, nullptr, resid);
 }
 
 int kk_conv_integer_scaled_qbias_noalloc(const kk_tensor* out, const kk_tensor* x,

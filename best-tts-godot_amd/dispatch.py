@@ -114,6 +114,26 @@ def _norm_chain(xd, sc, sh, eps, leaky_alpha):
     return y
 
 
+def _qconv_resid(at, inp, x, w):
+    """A quantised conv that took in the residual Add after it (attribute
+    "resid", the residual's input index): the residual when the epilogue can
+    add it -- an fp32 device tensor of the conv output's shape (the Add's
+    x + y in fp32, ref_runtime.py:446-447, commutes) -- else None (and the
+    Add runs after the conv, with its broadcasting)."""
+    k = at.get("resid")
+    if k is None:
+        return None
+    r = inp(k)
+    pads = at.get("pads", [0, 0])
+    s, d = at.get("strides", [1])[0], at.get("dilations", [1])[0]
+    n, _, L = x.shape
+    cout, _, kw = w.shape
+    lout = (L + pads[0] + pads[1] - d * (kw - 1) - 1) // s + 1
+    if isinstance(r, DeviceTensor) and r.dtype == np.float32 and tuple(r.shape) == (n, cout, lout):
+        return r
+    return None
+
+
 def dispatch(op, node_input, node_output, at, env):
     """Execute one node.  Mirrors tools/ref_runtime.py:428-668."""
 
@@ -363,22 +383,29 @@ def dispatch(op, node_input, node_output, at, env):
         # the same with the bias quantisation ahead of it folded in: inputs
         # x, w, x_zp, w_zp, "", "", scale_a, scale_w, bias (fp32); scale =
         # scale_a * scale_w, int32 bias = Cast(Floor(Div(bias, scale))).
-        conv_at = {k: v for k, v in at.items() if k != "bias_quant"}
-        out = ops.conv_integer_scaled_qbias(to_device(x), to_device(y), to_device(inp(2)),
+        x, y = to_device(x), to_device(y)
+        resid = _qconv_resid(at, inp, x, y)
+        out = ops.conv_integer_scaled_qbias(x, y, to_device(inp(2)),
                                             to_device(inp(3)), _f32(to_device(inp(8))),
                                             _f32(to_device(inp(6))), _f32(to_device(inp(7))),
-                                            conv_at.get("pads", [0, 0]),
-                                            conv_at.get("strides", [1])[0],
-                                            conv_at.get("dilations", [1])[0],
-                                            conv_at.get("group", 1))
+                                            at.get("pads", [0, 0]),
+                                            at.get("strides", [1])[0],
+                                            at.get("dilations", [1])[0],
+                                            at.get("group", 1), resid=resid)
+        if "resid" in at and resid is None:  # the Add it took in, after it
+            out = ops.binary("Add", out, to_device(inp(at["resid"])))
     elif op == "QConvScaled":
         # ConvInteger -> Add(int32 bias) -> Cast(float) -> Mul(scale), fused;
         # inputs x, w, x_zp, w_zp, bias ("" if absent), scale.
-        out = ops.conv_integer_scaled(to_device(x), to_device(y), to_device(inp(2)),
+        x, y = to_device(x), to_device(y)
+        resid = _qconv_resid(at, inp, x, y)
+        out = ops.conv_integer_scaled(x, y, to_device(inp(2)),
                                       to_device(inp(3)), to_device(inp(4)),
                                       _f32(to_device(inp(5))), at.get("pads", [0, 0]),
                                       at.get("strides", [1])[0], at.get("dilations", [1])[0],
-                                      at.get("group", 1))
+                                      at.get("group", 1), resid=resid)
+        if "resid" in at and resid is None:
+            out = ops.binary("Add", out, to_device(inp(at["resid"])))
     elif op == "QMatMulScaled":
         # MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)), fused;
         # inputs a, b, a_zp, b_zp, scale, bias ("" if absent), and with

@@ -96,7 +96,59 @@ def fuse(nodes, weights, protect=()):
             groups.append([i])
     out, groups = _merge_norm_snake(out, groups, protect)
     out, groups = _merge_norm_quant(out, groups, protect)
-    return _merge_qconv_bias(out, groups, weights, protect)
+    out, groups = _merge_qconv_bias(out, groups, weights, protect)
+    return _merge_qconv_add(out, groups, protect)
+
+
+def _merge_qconv_add(out, groups, protect):
+    """An Add one of whose inputs is a quantised conv's output read by the
+    Add alone (and not kept) takes the conv in (the decoder's residual sums):
+    the conv's node, producing the Add's output, with the Add's other input
+    appended (attribute "resid": its input index), placed where the Add was,
+    so the residual already exists when it runs.  Whether the residual has the
+    conv output's shape is known only when the node runs; dispatch adds it in
+    the conv's epilogue then, else runs the Add after the conv."""
+    readers = defaultdict(list)
+    producer = {}
+    for k, (_op, ins, outs, _at) in enumerate(out):
+        for n in ins:
+            if n:
+                readers[n].append(k)
+        for o in outs:
+            if o:
+                producer[o] = k
+    takes = {}  # Add index -> (conv index, residual name)
+    convs = set()
+    for k, (op, ins, outs, _at) in enumerate(out):
+        if op != "Add" or len(ins) != 2 or not ins[0] or not ins[1]:
+            continue
+        for side in (0, 1):
+            name = ins[side]
+            p = producer.get(name)
+            if p is None or p in convs or out[p][0] != "QConvScaled" or "resid" in out[p][3]:
+                continue
+            if name in protect or readers.get(name) != [k] or len(out[p][2]) != 1:
+                continue
+            takes[k] = (p, ins[1 - side])
+            convs.add(p)
+            break
+    if not takes:
+        return out, groups
+    new_out, new_groups = [], []
+    for k, node in enumerate(out):
+        if k in convs:
+            continue
+        if k in takes:
+            p, resid = takes[k]
+            c_op, c_ins, _c_outs, c_at = out[p]
+            at = dict(c_at)
+            at["resid"] = len(c_ins)
+            new_out.append((c_op, list(c_ins) + [resid], list(node[2]), at))
+            new_groups.append(list(groups[p]) + list(groups[k]))
+        else:
+            new_out.append(node)
+            new_groups.append(groups[k])
+    return new_out, new_groups
 
 
 def _merge_qconv_bias(out, groups, weights, protect):

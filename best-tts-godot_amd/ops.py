@@ -260,37 +260,51 @@ def conv_integer(x, w, x_zp=None, w_zp=None, pads=(0, 0), stride=1, dilation=1, 
 
 
 def conv_integer_scaled(x, w, x_zp, w_zp, bias, scale, pads=(0, 0), stride=1, dilation=1,
-                        group=1):
-    """float(ConvInteger(x, w) + bias[co]) * scale, fp32 out (bias int32 [Cout] or None)."""
+                        group=1, resid=None):
+    """float(ConvInteger(x, w) + bias[co]) * scale, fp32 out (bias int32 [Cout] or None);
+    with `resid` (fp32, the output's shape) that added too: the residual Add fused."""
     x = x.contiguous()
     w = w.contiguous()
     n, _, L = x.shape
     cout, _, k = w.shape
     lout = (L + pads[0] + pads[1] - dilation * (k - 1) - 1) // stride + 1
     out = DeviceTensor.empty((n, cout, max(lout, 0)), np.float32)
-    _lib.call("kk_conv_integer_scaled", out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
-              _d(bias.contiguous() if bias is not None else None), scale.contiguous().desc(),
-              int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
+    b = _d(bias.contiguous() if bias is not None else None)
+    tail = (int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
+    if resid is None:
+        _lib.call("kk_conv_integer_scaled", out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
+                  b, scale.contiguous().desc(), *tail)
+    else:
+        _lib.call("kk_conv_integer_scaled_add", out.desc(), x.desc(), w.desc(), _d(x_zp),
+                  _d(w_zp), b, scale.contiguous().desc(), resid.contiguous().desc(), *tail)
     return out
 
 
 def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0, 0), stride=1,
-                              dilation=1, group=1, noalloc=False):
+                              dilation=1, group=1, noalloc=False, resid=None):
     """conv_integer_scaled with its int32 bias and scale formed in the same
     launch sequence: scale = scale_a * scale_w, bias_int32 =
     int32(floor(bias / scale)) (bias fp32 [Cout], the scales one value each).
     With `noalloc` the library allocates nothing for the call (its workspace
-    is a fixed device array); the output is still allocated here."""
+    is a fixed device array); the output is still allocated here.  With
+    `resid` (fp32, the output's shape) that is added too: the residual Add
+    fused (not with `noalloc`)."""
     x = x.contiguous()
     w = w.contiguous()
     n, _, L = x.shape
     cout, _, k = w.shape
     lout = (L + pads[0] + pads[1] - dilation * (k - 1) - 1) // stride + 1
     out = DeviceTensor.empty((n, cout, max(lout, 0)), np.float32)
-    entry = "kk_conv_integer_scaled_qbias_noalloc" if noalloc else "kk_conv_integer_scaled_qbias"
-    _lib.call(entry, out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp),
-              bias.contiguous().desc(), scale_a.contiguous().desc(), scale_w.contiguous().desc(),
-              int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
+    args = [out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp), bias.contiguous().desc(),
+            scale_a.contiguous().desc(), scale_w.contiguous().desc()]
+    tail = (int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
+    if resid is not None:
+        if noalloc:
+            raise ValueError("conv_integer_scaled_qbias: resid with noalloc is not supported")
+        _lib.call("kk_conv_integer_scaled_qbias_add", *args, resid.contiguous().desc(), *tail)
+    else:
+        entry = "kk_conv_integer_scaled_qbias_noalloc" if noalloc else "kk_conv_integer_scaled_qbias"
+        _lib.call(entry, *args, *tail)
     return out
 
 

@@ -281,6 +281,23 @@ int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const
                                  const kk_tensor* scale_w, int stride, int dilation, int pad0,
                                  int pad1, int group);
 
+/* The quantised conv's output read only by an Add whose other operand has
+ * the output's shape (the decoder's residual sums), the Add fused into the
+ * epilogue (ref_runtime.py:446-447: Add, out = x + y in fp32):
+ *   out = float(conv_int + bias) * scale + resid
+ * the conv tail's value rounded as before, then the Add's one rounding;
+ * resid fp32, contiguous, shaped like out (it may be out itself). */
+int kk_conv_integer_scaled_add(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                               const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias,
+                               const kk_tensor* scale, const kk_tensor* resid, int stride,
+                               int dilation, int pad0, int pad1, int group);
+/* kk_conv_integer_scaled_qbias with the same residual Add fused in. */
+int kk_conv_integer_scaled_qbias_add(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                                     const kk_tensor* x_zp, const kk_tensor* w_zp,
+                                     const kk_tensor* bias, const kk_tensor* scale_a,
+                                     const kk_tensor* scale_w, const kk_tensor* resid, int stride,
+                                     int dilation, int pad0, int pad1, int group);
+
 /* kk_conv_integer_scaled_qbias without any allocation.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -169,7 +169,11 @@ def test_fusion_pass_on_the_kokoro_graph():
     # and each quantised conv whose int32 bias the graph forms per call
     # (Mul -> Div -> Floor -> Cast -> Reshape) takes those nodes in
     assert sum(1 for n in fused if n[0] == "QConvScaled" and n[3].get("bias_quant")) == 80
-    assert len(fused) == 1831
+    # 35 of those feed a residual Add alone, which they take in (the sum in
+    # the conv's epilogue); the residual is the merged node's last input
+    res = [n for n in fused if n[0] == "QConvScaled" and "resid" in n[3]]
+    assert len(res) == 35 and all(n[3]["resid"] == len(n[1]) - 1 for n in res)
+    assert len(fused) == 1796
     covered = sorted(i for grp in groups for i in grp)
     assert covered == list(range(len(nodes)))  # every original node exactly once
     produced = {}

@@ -161,6 +161,65 @@ def test_qconv_tail_with_bias_quantisation(gpu, oracle, cin, cout, k, L):
     assert_bitexact(got, want.astype(np.float32), f"QConvScaled + bias quantisation {cin}->{cout}")
 
 
+@pytest.mark.parametrize("cin,cout,k,L,side,rshape", [
+    (128, 128, 5, 2000, 0, "full"), (256, 96, 3, 777, 1, "full"),
+    # a residual the epilogue cannot take (broadcast over time, or over
+    # channels): the Add runs after the conv, with its broadcasting
+    (128, 64, 3, 500, 1, "channel"), (64, 64, 7, 300, 0, "time")])
+def test_qconv_bias_quantisation_residual_add(gpu, oracle, cin, cout, k, L, side, rshape):
+    """The decoder's residual sums: a quantised conv's output read only by
+    an Add.  The Add folds into the conv (the residual added to the scaled
+    result in the epilogue, fp32 x + y, which commutes), with the residual on
+    either side of the Add; bit-exact to the chain."""
+    r = rng(31)
+    xf = (r.normal(0.1, 1.2, (1, cin, L))).astype(np.float32)
+    shp = {"full": (1, cout, L), "channel": (1, cout, 1), "time": (1, 1, L)}[rshape]
+    weights = {"w": r.integers(0, 256, (cout, cin, k)).astype(np.uint8),
+               "wz": np.array(127, np.uint8), "sw": np.array(0.0029, np.float16),
+               "b": r.normal(0, 0.5, (cout,)).astype(np.float16),
+               "shp": np.array([1, cout, 1], np.int64)}
+    at = {"pads": [k // 2, k // 2], "dilations": [1], "strides": [1], "group": 1,
+          "kernel_shape": [k]}
+    nodes = [("DynamicQuantizeLinear", ["xf"], ["q", "sa", "za"], {}),
+             ("Cast", ["sa"], ["saf"], {"to": 10}), ("Mul", ["saf", "sw"], ["s"], {}),
+             ("Div", ["b", "s"], ["bd"], {}), ("Floor", ["bd"], ["bf"], {}),
+             ("Cast", ["bf"], ["bi"], {"to": 6}), ("Reshape", ["bi", "shp"], ["br"], {}),
+             ("ConvInteger", ["q", "w", "za", "wz"], ["acc"], at),
+             ("Add", ["acc", "br"], ["accb"], {}), ("Cast", ["accb"], ["f"], {"to": 10}),
+             ("Mul", ["f", "s"], ["y"], {}),
+             ("Add", ["y", "res"] if side == 0 else ["res", "y"], ["z"], {})]
+    inputs = {"xf": xf, "res": r.normal(0, 2.0, shp).astype(np.float32)}
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, "z")
+    assert [n[0] for n in fused] == ["DynamicQuantizeLinear", "Cast", "QConvScaled"]
+    assert fused[-1][3].get("bias_quant") and fused[-1][1][fused[-1][3]["resid"]] == "res"
+    assert got.shape == want.shape
+    assert_bitexact(got, want.astype(np.float32), f"QConvScaled + residual ({rshape}, side {side})")
+
+
+@pytest.mark.parametrize("stride,dil,pad", [(1, 1, 2), (2, 1, 1), (1, 3, 6)])
+def test_qconv_tail_residual_add(gpu, oracle, stride, dil, pad):
+    """The plain quantised-conv tail (int32 bias given) followed by a residual
+    Add, with strided and dilated convs (the residual sized to the output)."""
+    r = rng(32)
+    cin, cout, k, L = 96, 80, 5, 1501
+    lout = (L + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    x = r.integers(0, 256, (1, cin, L)).astype(np.uint8)
+    inputs = {"x": x, "xz": np.array(90, np.uint8),
+              "b": r.integers(-3000, 3000, (1, cout, 1)).astype(np.int32),
+              "s": np.array(2.7e-5, np.float32),
+              "res": r.normal(0, 1.0, (1, cout, lout)).astype(np.float32)}
+    weights = {"w": r.integers(0, 256, (cout, cin, k)).astype(np.uint8),
+               "wz": np.array(140, np.uint8)}
+    at = {"pads": [pad, pad], "dilations": [dil], "strides": [stride], "group": 1,
+          "kernel_shape": [k]}
+    nodes = [("ConvInteger", ["x", "w", "xz", "wz"], ["acc"], at),
+             ("Add", ["acc", "b"], ["accb"], {}), ("Cast", ["accb"], ["f"], {"to": 1}),
+             ("Mul", ["f", "s"], ["y"], {}), ("Add", ["res", "y"], ["z"], {})]
+    got, want, fused = run_chain(gpu, oracle, nodes, inputs, weights, "z")
+    assert [n[0] for n in fused] == ["QConvScaled"] and "resid" in fused[0][3]
+    assert_bitexact(got, want.astype(np.float32), f"QConvScaled + residual s{stride} d{dil}")
+
+
 def norm_chain(affine, leaky):
     nodes = [("ReduceMean", ["x", "ax"], ["m1"], {"keepdims": 1}),
              ("Sub", ["x", "m1"], ["d"], {}), ("Mul", ["d", "d"], ["sq"], {}),
