@@ -11,8 +11,9 @@
 // positions hold b = xz', so they contribute 0 exactly as the reference's
 // zero padding of the shifted input does.
 //
-// Layout: the weights become wT[Cout][Kw][CinP] (CinP = Cin rounded up to
-// 64 with zero channels) with sum_k a_k per output channel, once per call.
+// Layout: the weights become CoutP x Kw x CinP bytes in MFMA fragment order
+// (CinP = Cin rounded up to 64 with zero channels) with sum_k a_k per output
+// channel, once per call.
 // The activations stay as they are, uint8 [N][Cin][L]: each block stages
 // the time window its outputs read, 64 channels at a time, into LDS
 // time-major (channels contiguous, offset to int8 on the way), so each
@@ -44,7 +45,11 @@ struct QBias {
   int32_t* ibias;
 };
 
-// wT[co][tap][ci] = offset weight (0 for padding rows/channels);
+// The offset weights (0 for padding rows/channels) in MFMA fragment order:
+// for row block mb = co / 128, step st = (ci / 64) Kw + tap, wave row wm =
+// (co % 128) / 64, fragment q = 2 ((ci % 64) / 32) + (co % 64) / 32 and lane
+// l = co % 32 + 32 ((ci % 32) / 16), the 16 bytes ci % 16 = 0..15 sit at
+// ((mb S + st) 2 + wm) 4096 + 1024 q + 16 l (S = Kw CinP / 64 steps);
 // wsum[co] = sum of the offset weights; wzo[co] = offset weight zero point;
 // with qb.scale set also channel co's quantised bias and scale.
 __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w, int w_dt,
@@ -58,17 +63,34 @@ __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w,
   const int64_t co = blockIdx.x;
   const bool live = co < Cout;
   const int off = w_dt == KK_U8 ? 128 : 0;
+  const int64_t S = Kw * (CinP / kCinAlign);
+  const int rr = static_cast<int>(co % kTileM);
+  const int64_t row_base = ((co / kTileM) * S * 2 + rr / 64) * 4096 + 1024 * ((rr / 32) % 2) +
+                           16 * (rr % 32);
   int local = 0;
-  for (int64_t idx = threadIdx.x; idx < Kw * CinP; idx += blockDim.x) {
-    const int64_t tap = idx / CinP, ci = idx % CinP;
-    int a = 0;
-    if (live && ci < Cin) {
-      const int64_t src = (co * Cin + ci) * Kw + tap;
-      a = w_dt == KK_U8 ? static_cast<int>(static_cast<const uint8_t*>(w)[src]) - 128
-                        : static_cast<int>(static_cast<const int8_t*>(w)[src]);
+  for (int64_t idx = threadIdx.x; idx < Kw * (CinP / 16); idx += blockDim.x) {
+    const int64_t tap = idx / (CinP / 16), ci0 = 16 * (idx % (CinP / 16));
+    uint32_t wd[4];
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t ci = ci0 + 4 * e4 + e;
+        int a = 0;
+        if (live && ci < Cin) {
+          const int64_t src = (co * Cin + ci) * Kw + tap;
+          a = w_dt == KK_U8 ? static_cast<int>(static_cast<const uint8_t*>(w)[src]) - 128
+                            : static_cast<int>(static_cast<const int8_t*>(w)[src]);
+        }
+        local += a;
+        v |= (static_cast<uint32_t>(a) & 0xffu) << (8 * e);
+      }
+      wd[e4] = v;
     }
-    wT[(co * Kw + tap) * CinP + ci] = static_cast<int8_t>(a);
-    local += a;
+    const int64_t st = (ci0 / kCinAlign) * Kw + tap, kk = ci0 % kCinAlign;
+    const int64_t dst = row_base + st * 8192 + 2048 * (kk / 32) + 512 * ((kk / 16) % 2);
+    *reinterpret_cast<uint4*>(wT + dst) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) local += __shfl_xor(local, o, 64);
@@ -95,7 +117,7 @@ __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w,
 }
 
 struct ConvI8Args {
-  const int8_t* wT;     // [CoutP][Kw][CinP]
+  const int8_t* wT;     // fragment order (conv_i8_wprep), CoutP Kw CinP bytes
   const int32_t* wsum;  // [CoutP]
   const int32_t* wzo;   // [CoutP] (live rows: the tensor's offset zero point)
   const uint8_t* x;     // [N][Cin][L]
@@ -118,13 +140,14 @@ struct ConvI8Args {
 // tap * d -- in LDS once, straight from the uint8 activations: a thread
 // loads four time steps of four channels (one dword per channel), swaps the
 // 4 x 4 bytes into four time rows and flips the top bit (u - 128 = u ^ 0x80);
-// positions in the padding hold xz - 128.  The 128 x 64 weight tile of
-// each tap streams through a double buffer (the next tap's tile is fetched
-// into registers while this tap's MFMAs run).  Lane (r, g) =
-// (lane % 32, lane / 32) reads A[r][16g .. 16g+15] and B[16g .. 16g+15][r]
-// of each 32 x 32 x 32 step from LDS; D(i, j) lands in lane j + 32 ((i / 4)
-// % 2), register (i / 8) 4 + i % 4.  The epilogue's per-channel constants
-// and the staged rows' channel sums sit in LDS.
+// positions in the padding hold xz - 128.  The weights' MFMA fragments come
+// from global memory in the order the waves read them (each wave's 4
+// fragments of a (chunk, tap) step are 4 KB contiguous, loaded three steps
+// ahead), so the taps run without LDS weight tiles or barriers.  Lane (r, g)
+// = (lane % 32, lane / 32) holds A[r][16g .. 16g+15] and reads
+// B[16g .. 16g+15][r] of each 32 x 32 x 32 step from LDS; D(i, j) lands in
+// lane j + 32 ((i / 4) % 2), register (i / 8) 4 + i % 4.  The epilogue's
+// per-channel constants and the staged rows' channel sums sit in LDS.
 // TN (128 or 64) output steps per block; a wave covers TN / 2 of them.
 // RES: the scaled fp32 output plus A.resid (its own instantiation: the
 // residual's registers would lower the plain kernel's occupancy).
@@ -133,8 +156,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
   constexpr int NI = TN / 64;  // 32-wide MFMA tiles per wave along time
   extern __shared__ __align__(16) int8_t conv_lds[];
   int8_t* Bw = conv_lds;                                          // [W4][kRowPitch]
-  int8_t* As = conv_lds + A.W4 * kRowPitch;                       // [2][kTileM][kRowPitch]
-  int* rs = reinterpret_cast<int*>(As + 2 * kTileM * kRowPitch);  // [W4] channel sums
+  int* rs = reinterpret_cast<int*>(conv_lds + A.W4 * kRowPitch);  // [W4] channel sums
   int* cst = rs + A.W4;                                           // [kTileM] constant term
   float* scl = reinterpret_cast<float*>(cst + kTileM);            // [kTileM] scale
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -170,28 +192,26 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
     cst[tid] = c;
     scl[tid] = sc;
   }
-  // weight-tile loader: 128 rows x four 16-byte pieces, two per thread
-  // (per-thread bases; a tap or chunk moves them by a uniform offset)
-  const int8_t* wsrc[2];
-  int adst[2];
+  // A fragments straight from the fragment-ordered weights (no LDS): step
+  // st = chunk * Kw + tap of row block m0 / 128 is 8 KB, wave row wm's four
+  // fragments (ks, mi) 4 KB of it, lane l's 16 bytes of fragment q at
+  // q * 1024 + 16 l.  A ring of three steps' fragments runs three steps
+  // ahead; a load past the block's last step reads 0 (the buffer's range
+  // check) and is never used.
+  const int nch = static_cast<int>(A.CinP / kCinAlign), Kw = static_cast<int>(A.Kw);
+  const int S = nch * Kw;
+  const auto wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(A.wT) + (m0 / kTileM) * static_cast<int64_t>(S) * 8192, 0, S * 8192,
+      0x00020000);
+  const uint32_t w_lane = static_cast<uint32_t>(wm * 4096 + lane * 16);
+  auto lda = [&](int st, v4i (&f)[4]) {
+    const uint32_t off = static_cast<uint32_t>(st) * 8192u + w_lane;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int q = tid + 256 * j, row = q >> 2, c = q & 3;
-    wsrc[j] = A.wT + (m0 + row) * A.Kw * A.CinP + 16 * c;
-    adst[j] = row * kRowPitch + 16 * c;
-  }
-  auto load_a = [&](int64_t off, v4i (&reg)[2]) {  // off = tap * CinP + c0
-#pragma unroll
-    for (int j = 0; j < 2; ++j) reg[j] = *reinterpret_cast<const v4i*>(wsrc[j] + off);
+    for (int q = 0; q < 4; ++q)
+      f[q] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + 1024u * q, 0, 0));
   };
-  auto store_a = [&](int buf, const v4i (&reg)[2]) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-      *reinterpret_cast<v4i*>(As + buf * (kTileM * kRowPitch) + adst[j]) = reg[j];
-  };
-  // LDS offsets of this lane's fragments: A rows wm*64 + 32mi + r, B rows
-  // (wn*TN/2 + 32ni + r)*s + tap*d + sh, columns 16g (+32 per k-step)
-  const int a_off = (wm * 64 + r) * kRowPitch + 16 * g;
+  // LDS offsets of this lane's B fragments: rows (wn*TN/2 + 32ni + r)*s +
+  // tap*d + sh, columns 16g (+32 per k-step)
   int b_off[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni)
@@ -203,37 +223,48 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
   const int Cin = static_cast<int>(A.Cin), Li = static_cast<int>(A.L);
   const uint32_t L = static_cast<uint32_t>(A.L);
   const int a0i = static_cast<int>(a0);
-  v16i acc[2][NI] = {};
-  for (int64_t c0 = 0; c0 < A.CinP; c0 += kCinAlign) {
-    // Stage the window: item (tg, cg) = rows 4tg .. 4tg+3 x channels
-    // c0 + 4cg .. 4cg+3.  A wave takes 4 channel groups x 16 consecutive
-    // time groups: one channel of its items is 4 rows x 64 contiguous bytes
-    // (its LDS writes meet 4-way bank conflicts, which cost little).
+  // A chunk's window: item (tg, cg) = rows 4tg .. 4tg+3 x channels c0 +
+  // 4cg .. 4cg+3.  A wave takes 4 channel groups x 16 consecutive time
+  // groups: one channel of its items is 4 rows x 64 contiguous bytes (its
+  // LDS writes meet 4-way bank conflicts, which cost little).  Then each
+  // staged row's channel sum gains this chunk's share.
+  // The window's loads are buffer loads, issued whatever the position (a
+  // read outside x returns 0), with padding and missing channels chosen by
+  // selects: no branch around a load, which keeps the compiler's wait counts
+  // for the weight ring exact.
+  const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(xb), 0, Cin * Li,
+                                                     0x00020000);
+  auto stage = [&](int c0) {
     for (int it = tid; it < nitems; it += 256) {
       const int cg = (it >> 4) & 15, tg = (it & 15) + 16 * (it >> 8);
-      if (tg >= ngrp) continue;
       const int ts = a0i + 4 * tg;
-      const int ci0 = static_cast<int>(c0) + 4 * cg;
+      const int ci0 = c0 + 4 * cg;
       uint32_t dw[4];
+      if (A.aligned) {  // a dword is wholly inside the signal or wholly outside
+        const bool in = ts >= 0 && ts < Li;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        uint32_t v = 0;  // padding channels hold 0
-        if (ci0 + e < Cin) {
-          const uint32_t off = static_cast<uint32_t>(ci0 + e) * L + static_cast<uint32_t>(ts);
-          if (A.aligned) {  // a dword is wholly inside the signal or wholly outside
-            v = (ts >= 0 && ts < Li) ? (*reinterpret_cast<const uint32_t*>(xb + off) ^ 0x80808080u)
-                                     : padw;
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int t = ts + q;
-              const uint32_t by = (t >= 0 && t < Li) ? (static_cast<uint32_t>(xb[off + q]) ^ 0x80u) : padb;
-              v |= by << (8 * q);
-            }
-          }
+        for (int e = 0; e < 4; ++e) {
+          uint32_t off = static_cast<uint32_t>(ci0 + e) * L + static_cast<uint32_t>(ts);
+          asm volatile("" : "+v"(off));  // keeps the load unconditional
+          const uint32_t ld = __builtin_amdgcn_raw_buffer_load_b32(xrs, off, 0, 0);
+          dw[e] = ci0 + e < Cin ? (in ? (ld ^ 0x80808080u) : padw) : 0u;  // padding channels hold 0
         }
-        dw[e] = v;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          uint32_t off = static_cast<uint32_t>(ci0 + e) * L + static_cast<uint32_t>(ts);
+          asm volatile("" : "+v"(off));
+          uint32_t v = 0;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int t = ts + q;
+            const uint32_t ld = __builtin_amdgcn_raw_buffer_load_b8(xrs, off + q, 0, 0);
+            v |= ((t >= 0 && t < Li) ? (ld ^ 0x80u) : padb) << (8 * q);
+          }
+          dw[e] = ci0 + e < Cin ? v : 0u;
+        }
       }
+      if (tg >= ngrp) continue;
       // 4 x 4 byte transpose (v_perm: bytes 0-3 from the second operand,
       // 4-7 from the first): word q = the four channels at time 4tg + q
       const uint32_t t01l = __builtin_amdgcn_perm(dw[1], dw[0], 0x05010400u);
@@ -246,11 +277,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
       dst[2 * kRowPitch / 4] = __builtin_amdgcn_perm(t23h, t01h, 0x05040100u);
       dst[3 * kRowPitch / 4] = __builtin_amdgcn_perm(t23h, t01h, 0x07060302u);
     }
-    v4i ra[2];
-    load_a(c0, ra);
-    store_a(0, ra);
     __syncthreads();
-    // this chunk's share of each staged row's channel sum
     for (int row = tid; row < A.W4; row += 256) {
       const int* p = reinterpret_cast<const int*>(Bw + row * kRowPitch);
       int sum = c0 == 0 ? 0 : rs[row];
@@ -258,30 +285,54 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
       for (int k = 0; k < kCinAlign / 4; ++k) sum = __builtin_amdgcn_sdot4(p[k], 0x01010101, sum, false);
       rs[row] = sum;
     }
-    for (int tap = 0; tap < static_cast<int>(A.Kw); ++tap) {
-      const int buf = tap & 1;
-      if (tap + 1 < A.Kw) load_a((tap + 1) * A.CinP + c0, ra);
-      const int8_t* Ab = As + buf * (kTileM * kRowPitch) + a_off;
-      const int8_t* Bb = Bw + tap * tap_step;
+  };
+  v16i acc[2][NI] = {};
+  // one step's MFMAs: B fragments of the tap from the staged window
+  auto mma = [&](int tap, const v4i (&f)[4]) {
+    const int8_t* Bb = Bw + tap * tap_step;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        v4i af[2], bf[NI];
+    for (int ks = 0; ks < 2; ++ks) {
+      v4i bf[NI];
 #pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-          af[mi] = *reinterpret_cast<const v4i*>(Ab + mi * 32 * kRowPitch + 32 * ks);
+      for (int ni = 0; ni < NI; ++ni)
+        bf[ni] = *reinterpret_cast<const v4i*>(Bb + b_off[ni] + 32 * ks);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni)
-          bf[ni] = *reinterpret_cast<const v4i*>(Bb + b_off[ni] + 32 * ks);
-#pragma unroll
-        for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-          for (int ni = 0; ni < NI; ++ni)
-            acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
-      }
-      if (tap + 1 < A.Kw) store_a(buf ^ 1, ra);
-      __syncthreads();
+          acc[mi][ni] = __builtin_amdgcn_mfma_i32_32x32x32_i8(f[2 * ks + mi], bf[ni], acc[mi][ni], 0, 0, 0);
     }
+  };
+  v4i f0[4], f1[4], f2[4];
+  lda(0, f0);
+  lda(1, f1);
+  lda(2, f2);
+  int tap = 0, c0 = 0;
+  // a chunk's first step stages its window (after every wave is done with
+  // the previous one); the ring slot of step st is st % 3.  Every slot's
+  // refill is issued whether or not its step exists (past the last step it
+  // reads 0): a refill skipped on some path leaves the compiler's wait
+  // counts for the other slots at "all loads", which drains the ring.
+  auto run = [&](int st, v4i (&f)[4]) {
+    if (st < S) {
+      if (tap == 0) {
+        if (st > 0) __syncthreads();
+        stage(c0);
+      }
+      mma(tap, f);
+      if (++tap == Kw) {
+        tap = 0;
+        c0 += kCinAlign;
+      }
+    }
+    lda(st + 3, f);
+  };
+  for (int st = 0; st < S; st += 3) {
+    run(st, f0);
+    run(st + 1, f1);
+    run(st + 2, f2);
   }
+  __syncthreads();  // the last chunk's row sums, for the epilogue
   int zS[NI];  // wz * sum_k b_k of each of this lane's output columns
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
@@ -368,10 +419,10 @@ static int64_t conv_rows(int64_t tn, int64_t stride, int64_t dilation, int64_t K
   return ceil_div(conv_window(tn, stride, dilation, K) + 3, 4) * 4;
 }
 
-// LDS of a block: the staged rows and their channel sums, the weight double
-// buffer, the per-channel epilogue constants.
+// LDS of a block: the staged rows and their channel sums, the per-channel
+// epilogue constants.
 static size_t conv_lds(int64_t rows) {
-  return static_cast<size_t>(rows * (kRowPitch + 4) + 2 * kTileM * kRowPitch + 2 * kTileM * 4);
+  return static_cast<size_t>(rows * (kRowPitch + 4) + 2 * kTileM * 4);
 }
 
 // The time tile (128, else 64) whose block fits 64 KB of LDS; 0 if neither does.
