@@ -283,10 +283,11 @@ __global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
   const float xscale = ldexpf(1.0f, kexp), unscale = ldexpf(1.0f, -kexp);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m_w = (wave / T::WAVES_N) * 32 * WM_T, n_w = (wave % T::WAVES_N) * 32 * WN_T;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T::BN;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * T::BM;
-  const int64_t b = blockIdx.z / A.ksplit;
-  const int split = static_cast<int>(blockIdx.z - b * A.ksplit);
+  const uint3 tile = xcd_tile();  // neighbouring time tiles on one XCD
+  const int64_t n0 = static_cast<int64_t>(tile.x) * T::BN;
+  const int64_t m0 = static_cast<int64_t>(tile.y) * T::BM;
+  const int64_t b = tile.z / A.ksplit;
+  const int split = static_cast<int>(tile.z - b * A.ksplit);
   const int nk_all = static_cast<int>(A.Kg / kBK);
   const int kt0 = static_cast<int>(static_cast<int64_t>(nk_all) * split / A.ksplit);
   const int nk = static_cast<int>(static_cast<int64_t>(nk_all) * (split + 1) / A.ksplit) - kt0;

@@ -162,18 +162,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r = lane & 31, g = lane >> 5;
   const int wm = wv >> 1, wn = wv & 1;
-  // XCD-aware tile order: workgroup w goes to XCD w % 8, so XCD x is given
-  // the contiguous run of tiles x q + min(x, r) .. (T = 8 q + r tiles, the
-  // first r XCDs one more): neighbouring time tiles, whose windows overlap,
-  // share an L2.  A bijection on [0, T).
-  const uint32_t gx = gridDim.x, gy = gridDim.y;
-  const uint32_t tiles = gx * gy * gridDim.z;
-  const uint32_t wid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-  const uint32_t xcd = wid % 8u, q8 = tiles / 8u, r8 = tiles % 8u;
-  const uint32_t tile = xcd * q8 + (xcd < r8 ? xcd : r8) + wid / 8u;
-  const int64_t m0 = static_cast<int64_t>((tile / gx) % gy) * kTileM;
-  const int64_t nb = static_cast<int64_t>(tile % gx) * TN;
-  const int64_t b = tile / (gx * gy);
+  const uint3 tile = xcd_tile();  // neighbouring time tiles on one XCD
+  const int64_t m0 = static_cast<int64_t>(tile.y) * kTileM;
+  const int64_t nb = static_cast<int64_t>(tile.x) * TN;
+  const int64_t b = tile.z;
   const uint8_t* xb = A.x + b * A.Cin * A.L;
   const int xz = (A.xzp ? static_cast<int>(A.xzp[0]) : 0) - 128;  // offset x zero point
   const uint32_t padb = static_cast<uint8_t>(static_cast<int8_t>(xz));

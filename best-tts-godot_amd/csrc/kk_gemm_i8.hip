@@ -71,9 +71,10 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int r = lane & 31, g = lane >> 5;
   const int wm = wv >> 1, wn = wv & 1;
-  const int64_t bz = blockIdx.z;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kTM;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * kTN;
+  const uint3 tile = xcd_tile();  // neighbouring column tiles on one XCD
+  const int64_t bz = tile.z;
+  const int64_t m0 = static_cast<int64_t>(tile.y) * kTM;
+  const int64_t n0 = static_cast<int64_t>(tile.x) * kTN;
   const int64_t M = G.M, N = G.N, K = G.K;
   const uint8_t* a = G.a + batch_offset(G.bm, 0, bz);
   const uint8_t* b = G.b + batch_offset(G.bm, 1, bz);

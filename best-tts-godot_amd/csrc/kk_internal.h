@@ -380,6 +380,19 @@ bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t 
                  const Dequant& dq, float* out, int64_t som, int64_t son, const BatchMap& bm,
                  int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, const int* only_if,
                  int* status);
+// XCD-aware block order: workgroup w runs on XCD w % 8, so XCD x is given
+// the contiguous run of tiles x q + min(x, r) .. (T = 8 q + r tiles, the
+// first r XCDs one more), x-fastest: neighbouring tiles, which share input
+// rows or halos, share an L2.  A bijection on the grid; the tile's (x, y, z).
+__device__ inline uint3 xcd_tile() {
+  const uint32_t gx = gridDim.x, gy = gridDim.y;
+  const uint32_t tiles = gx * gy * gridDim.z;
+  const uint32_t wid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  const uint32_t xcd = wid % 8u, q8 = tiles / 8u, r8 = tiles % 8u;
+  const uint32_t t = xcd * q8 + (xcd < r8 ? xcd : r8) + wid / 8u;
+  return make_uint3(t % gx, (t / gx) % gy, t / (gx * gy));
+}
+
 // A zero-point-only shift (scale 1) for the integer ops: per tensor, or per
 // element of `count` when the zero point has that many elements.
 int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* who);
