@@ -90,6 +90,9 @@ PROTOTYPES = {
     "kk_conv_integer_scaled_qbias": [_T] * 8 + [_i, _i, _i, _i, _i],
     "kk_conv_integer_scaled_add": [_T] * 8 + [_i, _i, _i, _i, _i],
     "kk_conv_integer_scaled_qbias_add": [_T] * 9 + [_i, _i, _i, _i, _i],
+    "kk_conv_integer_packed_bytes": [ctypes.c_int64] * 3 + [ctypes.POINTER(ctypes.c_int64)],
+    "kk_conv_integer_pack": [_T] * 3,
+    "kk_conv_integer_scaled_qbias_packed": [_T] * 10 + [_i] * 5,
     "kk_conv_integer_scaled_qbias_noalloc": [_T] * 8 + [_i, _i, _i, _i, _i],
     "kk_instance_norm_scale_shift": [_T, _T, _T, _T, _f, _i, _f],
     "kk_instance_norm_scale_shift_snake": [_T, _T, _T, _T, _T, _T, _f],

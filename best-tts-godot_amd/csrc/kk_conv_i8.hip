@@ -45,6 +45,19 @@ struct QBias {
   int32_t* ibias;
 };
 
+// The per-call bias quantisation of one channel: scale = sa * sw and
+// int32 bias = Cast(Floor(Div(bias, scale))), each operation rounded as its
+// node rounds it; the float -> int32 Cast as the device's Cast node does it
+// (truncation, INT64_MIN outside the int64 range, then the low 32 bits).
+__device__ inline int32_t qbias_channel(float sa, float sw, float b, float* scale) {
+  const float sc = sa * sw;
+  const float t = truncf(floorf(b / sc));
+  const int64_t v = (t >= -9.223372036854775808e18f && t < 9.223372036854775808e18f)
+                        ? static_cast<int64_t>(t) : INT64_MIN;
+  *scale = sc;
+  return static_cast<int32_t>(v);
+}
+
 // The offset weights (0 for padding rows/channels) in MFMA fragment order:
 // for row block mb = co / 128, step st = (ci / 64) Kw + tap, wave row wm =
 // (co % 128) / 64, fragment q = 2 ((ci % 64) / 32) + (co % 64) / 32 and lane
@@ -103,15 +116,9 @@ __global__ void __launch_bounds__(256) conv_i8_wprep(const void* __restrict__ w,
     if (live) z = (wzp ? static_cast<int>(load_as_i64(wzp, wzp_dt, wzp_n > 1 ? co : 0)) : 0) - off;
     wzo[co] = z;
     if (qb.scale && live) {
-      // the chain's operations, each rounded as its node rounds it; the
-      // float -> int32 Cast as the device's Cast node does it (truncation,
-      // INT64_MIN outside the int64 range, then the low 32 bits)
-      const float sc = qb.sa[0] * qb.sw[0];
-      const float t = truncf(floorf(qb.bias[co] / sc));
-      const int64_t v = (t >= -9.223372036854775808e18f && t < 9.223372036854775808e18f)
-                            ? static_cast<int64_t>(t) : INT64_MIN;
+      float sc;
+      qb.ibias[co] = qbias_channel(qb.sa[0], qb.sw[0], qb.bias[co], &sc);
       qb.scale[co] = sc;
-      qb.ibias[co] = static_cast<int32_t>(v);
     }
   }
 }
@@ -127,6 +134,9 @@ struct ConvI8Args {
   const int32_t* bias;  // [Cout] or NULL
   const float* scale;   // 1 or Cout values
   const float* resid;   // with outf: [N][Cout][Lout] added after the scale (the Add), or NULL
+  const float* qsa;     // with outf, packed weights: scale = qsa[0] * qsw[0] and the int32
+  const float* qsw;     // bias of channel co from the fp32 qbias[co] (qbias_channel), formed
+  const float* qbias;   // in the prologue instead of the weight preparation
   int64_t scale_n;
   int64_t Cout, Cin, CinP, Kw, s, d, L, p0, Lout, Kreal;
   int W4;               // time rows staged per block: the window plus alignment slack
@@ -185,7 +195,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
     float sc = 0.0f;
     if (co < A.Cout) {
       c = static_cast<int>(A.Kreal) * wz * xz - xz * A.wsum[co];
-      if (A.outf) {
+      if (A.outf && A.qsa) {
+        c += qbias_channel(A.qsa[0], A.qsw[0], A.qbias[co], &sc);
+      } else if (A.outf) {
         if (A.bias) c += A.bias[co];
         sc = A.scale[A.scale_n > 1 ? co : 0];
       }
@@ -559,21 +571,23 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
                      const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
                      bool outf, const kk_tensor* qb_sa = nullptr, const kk_tensor* qb_sw = nullptr,
                      const kk_tensor* qb_bias = nullptr, void* fixed_ws = nullptr,
-                     const kk_tensor* resid = nullptr) {
+                     const kk_tensor* resid = nullptr, const kk_tensor* packed = nullptr) {
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], Kw = w->shape[2];
   const int64_t Lout = out->shape[2];
   const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
   const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
   const ConvWs lay = conv_ws_layout(Cout, Cin, Kw);
-  void* ws = fixed_ws;
-  if (!ws) KK_TRY(kk_alloc(static_cast<size_t>(lay.total), &ws));
+  // packed weights (kk_conv_integer_pack) hold wT, wsum and wzo already
+  void* ws = packed ? packed->data : fixed_ws;
+  const bool own_ws = !ws;
+  if (own_ws) KK_TRY(kk_alloc(static_cast<size_t>(lay.total), &ws));
   char* base = static_cast<char*>(ws);
   int8_t* wT = reinterpret_cast<int8_t*>(base + lay.wT);
   int32_t* wsum = reinterpret_cast<int32_t*>(base + lay.wsum);
   int32_t* wzo = reinterpret_cast<int32_t*>(base + lay.wzo);
   QBias qb{};
-  if (qb_sa) {
+  if (qb_sa && !packed) {
     qb.sa = static_cast<const float*>(qb_sa->data);
     qb.sw = static_cast<const float*>(qb_sw->data);
     qb.bias = static_cast<const float*>(qb_bias->data);
@@ -581,16 +595,24 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     qb.ibias = reinterpret_cast<int32_t*>(base + lay.qb);
   }
   hipStream_t st = ctx().stream;
-  hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
-                     w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
-                     w_zp ? numel(w_zp) : 0, wT, wsum, wzo, Cout, Cin, Kw, CinP, qb);
-  int rc = check_launch("conv_i8_wprep");
+  int rc = KK_OK;
+  if (!packed) {
+    hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
+                       w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
+                       w_zp ? numel(w_zp) : 0, wT, wsum, wzo, Cout, Cin, Kw, CinP, qb);
+    rc = check_launch("conv_i8_wprep");
+  }
   if (rc == KK_OK) {
     ConvI8Args A{};
     A.wT = wT; A.wsum = wsum; A.wzo = wzo;
     A.x = static_cast<const uint8_t*>(x->data);
     A.xzp = x_zp ? static_cast<const uint8_t*>(x_zp->data) : nullptr;
-    if (outf && qb.scale) {
+    if (outf && packed && qb_sa) {
+      A.outf = static_cast<float*>(out->data);
+      A.qsa = static_cast<const float*>(qb_sa->data);
+      A.qsw = static_cast<const float*>(qb_sw->data);
+      A.qbias = static_cast<const float*>(qb_bias->data);
+    } else if (outf && qb.scale) {
       A.outf = static_cast<float*>(out->data);
       A.bias = qb.ibias;
       A.scale = qb.scale;
@@ -620,7 +642,7 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     }
     rc = check_launch("conv_i8_kernel");
   }
-  if (!fixed_ws) kk_free(ws);  // stream order keeps the workspace alive for the kernels
+  if (own_ws) kk_free(ws);  // stream order keeps the workspace alive for the kernels
   return rc;
 }
 
@@ -754,6 +776,70 @@ int kk_conv_integer_scaled_qbias_add(const kk_tensor* out, const kk_tensor* x, c
   if (empty) return KK_OK;
   return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
                           true, scale_a, scale_w, bias, nullptr, resid);
+}
+
+int kk_conv_integer_packed_bytes(int64_t cout, int64_t cin, int64_t k, int64_t* bytes) {
+  if (!bytes || cout <= 0 || cin <= 0 || k <= 0)
+    return set_error(KK_E_ARG, "kk_conv_integer_packed_bytes: positive sizes and an output");
+  *bytes = conv_ws_layout(cout, cin, k).qs;  // wT, wsum and wzo
+  return KK_OK;
+}
+
+// The packed weights' checks: uint8, contiguous, 256-byte aligned, sized
+// for w's shape.
+static int check_packed(const kk_tensor* packed, const kk_tensor* w, const char* who) {
+  KK_TRY(check_tensor(packed, "packed"));
+  const int64_t need = conv_ws_layout(w->shape[0], w->shape[1], w->shape[2]).qs;
+  if (packed->dtype != KK_U8 || !is_contiguous(packed) || numel(packed) != need ||
+      reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
+    return set_error(KK_E_ARG, "%s: packed must be %lld contiguous, 256-byte aligned uint8 bytes",
+                     who, (long long)need);
+  return KK_OK;
+}
+
+int kk_conv_integer_pack(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp) {
+  const char* who = "kk_conv_integer_pack";
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(w, "w"));
+  if (w->rank != 3 || !(w->dtype == KK_U8 || w->dtype == KK_I8) || !is_contiguous(w) ||
+      numel(w) == 0)
+    return set_error(KK_E_ARG, "%s: w must be a non-empty contiguous uint8/int8 [Cout, Cin, K]",
+                     who);
+  if (w_zp) {
+    KK_TRY(check_tensor(w_zp, "w_zp"));
+    if (!(w_zp->dtype == KK_U8 || w_zp->dtype == KK_I8 || w_zp->dtype == KK_I32) ||
+        numel(w_zp) != 1)
+      return set_error(KK_E_ARG, "%s: w_zp must be one uint8/int8/int32", who);
+  }
+  KK_TRY(check_packed(packed, w, who));
+  const int64_t Cout = w->shape[0], Cin = w->shape[1], Kw = w->shape[2];
+  const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
+  const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
+  const ConvWs lay = conv_ws_layout(Cout, Cin, Kw);
+  char* base = static_cast<char*>(packed->data);
+  hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, ctx().stream,
+                     w->data, w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
+                     w_zp ? numel(w_zp) : 0, reinterpret_cast<int8_t*>(base + lay.wT),
+                     reinterpret_cast<int32_t*>(base + lay.wsum),
+                     reinterpret_cast<int32_t*>(base + lay.wzo), Cout, Cin, Kw, CinP, QBias{});
+  return check_launch("conv_i8_wprep");
+}
+
+int kk_conv_integer_scaled_qbias_packed(const kk_tensor* out, const kk_tensor* x,
+                                        const kk_tensor* w, const kk_tensor* packed,
+                                        const kk_tensor* x_zp, const kk_tensor* w_zp,
+                                        const kk_tensor* bias, const kk_tensor* scale_a,
+                                        const kk_tensor* scale_w, const kk_tensor* resid,
+                                        int stride, int dilation, int pad0, int pad1, int group) {
+  const char* who = "kk_conv_integer_scaled_qbias_packed";
+  bool empty = false;
+  KK_TRY(check_qbias(out, x, w, x_zp, w_zp, bias, scale_a, scale_w, stride, dilation, pad0, pad1,
+                     group, who, &empty));
+  KK_TRY(check_packed(packed, w, who));
+  if (resid) KK_TRY(check_resid(out, resid, who));
+  if (empty) return KK_OK;
+  return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
+                          true, scale_a, scale_w, bias, nullptr, resid, packed);
 }
 
 int kk_conv_integer_scaled_qbias_noalloc(const kk_tensor* out, const kk_tensor* x,

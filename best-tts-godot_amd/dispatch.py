@@ -391,7 +391,8 @@ def dispatch(op, node_input, node_output, at, env):
                                             at.get("pads", [0, 0]),
                                             at.get("strides", [1])[0],
                                             at.get("dilations", [1])[0],
-                                            at.get("group", 1), resid=resid)
+                                            at.get("group", 1), resid=resid,
+                                            packed=env.get(at.get("packed")))
         if "resid" in at and resid is None:  # the Add it took in, after it
             out = ops.binary("Add", out, to_device(inp(at["resid"])))
     elif op == "QConvScaled":

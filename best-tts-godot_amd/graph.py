@@ -22,7 +22,7 @@ import os
 
 import numpy as np
 
-from . import audio
+from . import audio, ops
 from .dispatch import dispatch, to_device, to_host
 from .fuse import fuse as fuse_chains
 from .kpk import CODE_TO_NP, read_kpk
@@ -188,6 +188,7 @@ class PackedGraph:
         if fuse:
             keep = {self.output} | {str(p) for p in protect}
             self.nodes, self.groups = fuse_chains(nodes, self.weights, keep)
+            self._pack_conv_weights()
         else:
             self.nodes, self.groups = nodes, [[i] for i in range(len(nodes))]
         # Last use of every non-weight tensor (executor.gd:190-195).
@@ -200,6 +201,25 @@ class PackedGraph:
         self.frees = [[] for _ in self.nodes]  # names whose last use is node i
         for name, i in self.last_use.items():
             self.frees[i].append(name)
+
+    def _pack_conv_weights(self):
+        """Each quantised conv with its bias quantisation folded in whose
+        weight and weight zero point are constants gets its weights packed
+        once (ops.conv_integer_pack), under "<weight>#packed"; its node names
+        that in attribute "packed" and skips the per-call re-layout."""
+        packs = {}
+        for k, (op, ins, outs, at) in enumerate(self.nodes):
+            if op != "QConvScaled" or not at.get("bias_quant"):
+                continue
+            w, wz = ins[1], ins[3]
+            if w not in self.weights or (wz and wz not in self.weights):
+                continue
+            key = (w, wz)
+            if key not in packs:
+                packs[key] = f"{w}#{wz}#packed"
+                self.weights[packs[key]] = ops.conv_integer_pack(
+                    self.weights[w], self.weights[wz] if wz else None)
+            self.nodes[k] = (op, ins, outs, dict(at, packed=packs[key]))
 
     def run(self, input_ids, style, speed=1.0, keep=(), pcm16=False, notch=True, gain=1.0):
         """Returns the waveform on the host: float32 samples, or with

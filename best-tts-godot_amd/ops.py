@@ -280,15 +280,28 @@ def conv_integer_scaled(x, w, x_zp, w_zp, bias, scale, pads=(0, 0), stride=1, di
     return out
 
 
+def conv_integer_pack(w, w_zp=None):
+    """The packed form of a ConvInteger weight (uint8/int8 [Cout, Cin, K])
+    and its zero point, for conv_integer_scaled_qbias(packed=...): the
+    per-call weight re-layout done once (uint8 bytes on the device)."""
+    w = w.contiguous()
+    nbytes = ctypes.c_int64(0)
+    _lib.call("kk_conv_integer_packed_bytes", *[int(v) for v in w.shape], ctypes.byref(nbytes))
+    packed = DeviceTensor.empty((nbytes.value,), np.uint8)
+    _lib.call("kk_conv_integer_pack", packed.desc(), w.desc(), _d(w_zp))
+    return packed
+
+
 def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0, 0), stride=1,
-                              dilation=1, group=1, noalloc=False, resid=None):
+                              dilation=1, group=1, noalloc=False, resid=None, packed=None):
     """conv_integer_scaled with its int32 bias and scale formed in the same
     launch sequence: scale = scale_a * scale_w, bias_int32 =
     int32(floor(bias / scale)) (bias fp32 [Cout], the scales one value each).
     With `noalloc` the library allocates nothing for the call (its workspace
     is a fixed device array); the output is still allocated here.  With
     `resid` (fp32, the output's shape) that is added too: the residual Add
-    fused (not with `noalloc`)."""
+    fused (not with `noalloc`).  With `packed` (conv_integer_pack of this w
+    and w_zp) the weights are not re-laid for the call."""
     x = x.contiguous()
     w = w.contiguous()
     n, _, L = x.shape
@@ -298,7 +311,13 @@ def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0,
     args = [out.desc(), x.desc(), w.desc(), _d(x_zp), _d(w_zp), bias.contiguous().desc(),
             scale_a.contiguous().desc(), scale_w.contiguous().desc()]
     tail = (int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
-    if resid is not None:
+    if packed is not None:
+        if noalloc:
+            raise ValueError("conv_integer_scaled_qbias: packed with noalloc is not supported")
+        args.insert(3, packed.desc())
+        _lib.call("kk_conv_integer_scaled_qbias_packed", *args,
+                  None if resid is None else resid.contiguous().desc(), *tail)
+    elif resid is not None:
         if noalloc:
             raise ValueError("conv_integer_scaled_qbias: resid with noalloc is not supported")
         _lib.call("kk_conv_integer_scaled_qbias_add", *args, resid.contiguous().desc(), *tail)

@@ -298,6 +298,29 @@ int kk_conv_integer_scaled_qbias_add(const kk_tensor* out, const kk_tensor* x, c
                                      const kk_tensor* scale_w, const kk_tensor* resid, int stride,
                                      int dilation, int pad0, int pad1, int group);
 
+/* ConvInteger's weight re-layout (ref_runtime.py:130-134 reads w as it is;
+ * the int8 matrix cores take it offset to int8, in fragment order, with
+ * per-channel sums and zero points) done once for weights that do not change
+ * between calls, e.g. a graph's constants.  kk_conv_integer_packed_bytes
+ * gives the size of the packed form of a [cout, cin, k] weight;
+ * kk_conv_integer_pack writes it into `packed` (uint8, contiguous, 256-byte
+ * aligned, exactly that many bytes) from w (uint8/int8 [Cout, Cin, K]) and
+ * its zero point (NULL: 0). */
+int kk_conv_integer_packed_bytes(int64_t cout, int64_t cin, int64_t k, int64_t* bytes);
+int kk_conv_integer_pack(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp);
+/* kk_conv_integer_scaled_qbias (resid NULL) or kk_conv_integer_scaled_qbias_add
+ * (resid given) on weights packed by kk_conv_integer_pack from this w and
+ * w_zp: the same checks and bit-identical results, without the per-call
+ * re-layout (w and w_zp give the shapes and are not read; the caller keeps
+ * `packed` in step with them).  The per-call bias quantisation is formed
+ * per block with the same operations. */
+int kk_conv_integer_scaled_qbias_packed(const kk_tensor* out, const kk_tensor* x,
+                                        const kk_tensor* w, const kk_tensor* packed,
+                                        const kk_tensor* x_zp, const kk_tensor* w_zp,
+                                        const kk_tensor* bias, const kk_tensor* scale_a,
+                                        const kk_tensor* scale_w, const kk_tensor* resid,
+                                        int stride, int dilation, int pad0, int pad1, int group);
+
 /* kk_conv_integer_scaled_qbias without any allocation.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

@@ -11,7 +11,7 @@ max|ref| stays below 1e-4."""
 import numpy as np
 import pytest
 
-from conftest import assert_close, rng
+from conftest import assert_bitexact, assert_close, rng
 
 pytestmark = pytest.mark.gpu
 RTOL, FLOOR = 1e-4, 1e-5
@@ -620,3 +620,33 @@ def test_decoder_upsample_stage_free_running(gpu, oracle):
         return h
 
     assert_close(run(gpu), run(None), 1e-3, floor_rel=1e-4, what="decoder stage")
+
+
+@pytest.mark.parametrize("cin,cout,k,L,pad,dil,stride,wdt,wzp,resid", [
+    (128, 128, 11, 3001, 5, 1, 1, np.uint8, 129, False),
+    (100, 200, 3, 777, 3, 3, 1, np.int8, None, True),
+    (512, 256, 7, 1203, 9, 3, 1, np.uint8, 66, True),
+    (64, 40, 5, 500, 2, 1, 2, np.uint8, 0, False)])
+def test_conv_packed_weights(gpu, cin, cout, k, L, pad, dil, stride, wdt, wzp, resid):
+    """kk_conv_integer_scaled_qbias_packed: the weights packed once by
+    kk_conv_integer_pack, the bias quantisation formed in the conv's
+    prologue -- bit-identical to the per-call path (with and without the
+    residual Add), on two calls in a row with different activations."""
+    r = rng(41)
+    lo, hi = (0, 256) if wdt == np.uint8 else (-128, 128)
+    w = gpu.to_device(r.integers(lo, hi, (cout, cin, k)).astype(wdt))
+    wz = None if wzp is None else gpu.to_device(np.array(wzp, wdt))
+    bias = gpu.to_device(r.normal(0, 0.5, (cout,)).astype(np.float32))
+    sw = gpu.to_device(np.array(0.0037, np.float32))
+    packed = gpu.ops.conv_integer_pack(w, wz)
+    lout = (L + 2 * pad - dil * (k - 1) - 1) // stride + 1
+    for call in range(2):
+        x = gpu.to_device(r.integers(0, 256, (1, cin, L)).astype(np.uint8))
+        xz = gpu.to_device(np.array(100 + call, np.uint8))
+        sa = gpu.to_device(np.array(r.uniform(1e-3, 1e-2), np.float32))
+        res = gpu.to_device(r.normal(0, 1, (1, cout, lout)).astype(np.float32)) if resid else None
+        kw = dict(pads=(pad, pad), stride=stride, dilation=dil, resid=res)
+        want = gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, **kw).numpy()
+        got = gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, packed=packed,
+                                                **kw).numpy()
+        assert_bitexact(got, want, f"packed conv {cin}->{cout} k{k} call {call}")
