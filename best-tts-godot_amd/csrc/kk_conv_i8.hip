@@ -22,6 +22,9 @@
 // sum_ci b[t][ci] for the epilogue.
 #include <type_traits>
 
+#include <mutex>
+#include <unordered_map>
+
 #include "kk_internal.h"
 
 namespace kk {
@@ -597,7 +600,7 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
   hipStream_t st = ctx().stream;
   int rc = KK_OK;
   if (!packed) {
-    hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
+    KK_LAUNCH(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, st, w->data,
                        w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
                        w_zp ? numel(w_zp) : 0, wT, wsum, wzo, Cout, Cin, Kw, CinP, qb);
     rc = check_launch("conv_i8_wprep");
@@ -633,14 +636,17 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     A.W4 = static_cast<int>(conv_rows(tn, stride, dilation, Kw));
     const dim3 grid(static_cast<unsigned>(ceil_div(Lout, tn)),
                     static_cast<unsigned>(CoutP / kTileM), static_cast<unsigned>(N));
-    if (A.resid) {
-      if (tn == 128) hipLaunchKernelGGL((conv_i8_kernel<128, true>), grid, dim3(256), conv_lds(A.W4), st, A);
-      else hipLaunchKernelGGL((conv_i8_kernel<64, true>), grid, dim3(256), conv_lds(A.W4), st, A);
-    } else {
-      if (tn == 128) hipLaunchKernelGGL((conv_i8_kernel<128, false>), grid, dim3(256), conv_lds(A.W4), st, A);
-      else hipLaunchKernelGGL((conv_i8_kernel<64, false>), grid, dim3(256), conv_lds(A.W4), st, A);
+    rc = check_xcd_grid(grid, "ConvInteger");
+    if (rc == KK_OK) {
+      if (A.resid) {
+        if (tn == 128) KK_LAUNCH((conv_i8_kernel<128, true>), grid, dim3(256), conv_lds(A.W4), st, A);
+        else KK_LAUNCH((conv_i8_kernel<64, true>), grid, dim3(256), conv_lds(A.W4), st, A);
+      } else {
+        if (tn == 128) KK_LAUNCH((conv_i8_kernel<128, false>), grid, dim3(256), conv_lds(A.W4), st, A);
+        else KK_LAUNCH((conv_i8_kernel<64, false>), grid, dim3(256), conv_lds(A.W4), st, A);
+      }
+      rc = check_launch("conv_i8_kernel");
     }
-    rc = check_launch("conv_i8_kernel");
   }
   if (own_ws) kk_free(ws);  // stream order keeps the workspace alive for the kernels
   return rc;
@@ -747,6 +753,30 @@ static int check_qbias(const kk_tensor* out, const kk_tensor* x, const kk_tensor
   return KK_OK;
 }
 
+// What each packed buffer was made from (kk_conv_integer_pack), by its
+// device address: a call must pass the same weight tensor (address, shape,
+// dtype) and the same zero-point tensor (address, dtype) the pack read, so
+// a buffer packed for another weight or zero point is refused, not used.
+struct PackRecord {
+  const void* w;
+  int64_t cout, cin, k;
+  int w_dt;
+  const void* zp;
+  int zp_dt;
+};
+static std::mutex g_pack_mu;
+static std::unordered_map<const void*, PackRecord> g_packs;
+
+void kk::conv_i8_forget_pack(const void* p) {
+  std::lock_guard<std::mutex> lock(g_pack_mu);
+  g_packs.erase(p);
+}
+
+static PackRecord pack_record(const kk_tensor* w, const kk_tensor* w_zp) {
+  return PackRecord{w->data, w->shape[0], w->shape[1], w->shape[2], w->dtype,
+                    w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : -1};
+}
+
 extern "C" {
 
 int kk_conv_integer_scaled_qbias(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
@@ -786,14 +816,29 @@ int kk_conv_integer_packed_bytes(int64_t cout, int64_t cin, int64_t k, int64_t* 
 }
 
 // The packed weights' checks: uint8, contiguous, 256-byte aligned, sized
-// for w's shape.
-static int check_packed(const kk_tensor* packed, const kk_tensor* w, const char* who) {
+// for w's shape; with `made_from`, also that the pack was made from this w
+// and w_zp.
+static int check_packed(const kk_tensor* packed, const kk_tensor* w, const char* who,
+                        const kk_tensor* w_zp = nullptr, bool made_from = false) {
   KK_TRY(check_tensor(packed, "packed"));
   const int64_t need = conv_ws_layout(w->shape[0], w->shape[1], w->shape[2]).qs;
   if (packed->dtype != KK_U8 || !is_contiguous(packed) || numel(packed) != need ||
       reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
     return set_error(KK_E_ARG, "%s: packed must be %lld contiguous, 256-byte aligned uint8 bytes",
                      who, (long long)need);
+  if (made_from) {
+    const PackRecord want = pack_record(w, w_zp);
+    std::lock_guard<std::mutex> lock(g_pack_mu);
+    auto it = g_packs.find(packed->data);
+    if (it == g_packs.end())
+      return set_error(KK_E_ARG, "%s: packed was not made by kk_conv_integer_pack", who);
+    const PackRecord& r = it->second;
+    if (r.w != want.w || r.cout != want.cout || r.cin != want.cin || r.k != want.k ||
+        r.w_dt != want.w_dt)
+      return set_error(KK_E_ARG, "%s: packed was made from another weight tensor", who);
+    if (r.zp != want.zp || r.zp_dt != want.zp_dt)
+      return set_error(KK_E_ARG, "%s: packed was made with another weight zero point", who);
+  }
   return KK_OK;
 }
 
@@ -816,8 +861,12 @@ int kk_conv_integer_pack(const kk_tensor* packed, const kk_tensor* w, const kk_t
   const int64_t CinP = ceil_div(Cin, kCinAlign) * kCinAlign;
   const int64_t CoutP = ceil_div(Cout, kTileM) * kTileM;
   const ConvWs lay = conv_ws_layout(Cout, Cin, Kw);
+  {
+    std::lock_guard<std::mutex> lock(g_pack_mu);
+    g_packs[packed->data] = pack_record(w, w_zp);
+  }
   char* base = static_cast<char*>(packed->data);
-  hipLaunchKernelGGL(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, ctx().stream,
+  KK_LAUNCH(conv_i8_wprep, dim3(static_cast<unsigned>(CoutP)), dim3(256), 0, ctx().stream,
                      w->data, w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : 0,
                      w_zp ? numel(w_zp) : 0, reinterpret_cast<int8_t*>(base + lay.wT),
                      reinterpret_cast<int32_t*>(base + lay.wsum),
@@ -835,7 +884,7 @@ int kk_conv_integer_scaled_qbias_packed(const kk_tensor* out, const kk_tensor* x
   bool empty = false;
   KK_TRY(check_qbias(out, x, w, x_zp, w_zp, bias, scale_a, scale_w, stride, dilation, pad0, pad1,
                      group, who, &empty));
-  KK_TRY(check_packed(packed, w, who));
+  KK_TRY(check_packed(packed, w, who, w_zp, true));
   if (resid) KK_TRY(check_resid(out, resid, who));
   if (empty) return KK_OK;
   return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,

@@ -296,11 +296,12 @@ static int i8_launch(const I8Args& G, int64_t batch) {
     if (G.bm.st[1][d] % 4) bv = false;
   }
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(batch));
+  KK_TRY(check_xcd_grid(grid, "MatMulInteger"));
   hipStream_t st = ctx().stream;
-  if (av && bv) hipLaunchKernelGGL((i8_matmul_kernel<true, true>), grid, dim3(kThreads), 0, st, G);
-  else if (av) hipLaunchKernelGGL((i8_matmul_kernel<true, false>), grid, dim3(kThreads), 0, st, G);
-  else if (bv) hipLaunchKernelGGL((i8_matmul_kernel<false, true>), grid, dim3(kThreads), 0, st, G);
-  else hipLaunchKernelGGL((i8_matmul_kernel<false, false>), grid, dim3(kThreads), 0, st, G);
+  if (av && bv) KK_LAUNCH((i8_matmul_kernel<true, true>), grid, dim3(kThreads), 0, st, G);
+  else if (av) KK_LAUNCH((i8_matmul_kernel<true, false>), grid, dim3(kThreads), 0, st, G);
+  else if (bv) KK_LAUNCH((i8_matmul_kernel<false, true>), grid, dim3(kThreads), 0, st, G);
+  else KK_LAUNCH((i8_matmul_kernel<false, false>), grid, dim3(kThreads), 0, st, G);
   return check_launch("i8_matmul_kernel");
 }
 

@@ -134,6 +134,16 @@ def _decode_attrs(at):
     return attrs
 
 
+class NonFiniteError(RuntimeError):
+    """A strict run's first node with a non-finite float output: `node`
+    (index in the walk), `op`, `output` (tensor name) and `inputs` (name,
+    shape, dtype, (min, max)) of each of its inputs."""
+
+    def __init__(self, msg, node, op, output, inputs):
+        super().__init__(msg)
+        self.node, self.op, self.output, self.inputs = node, op, output, inputs
+
+
 class PackedGraph:
     """A packed graph with its weights resident on the device.
 
@@ -214,6 +224,16 @@ class PackedGraph:
             w, wz = ins[1], ins[3]
             if w not in self.weights or (wz and wz not in self.weights):
                 continue
+            if wz and not isinstance(self.weights[wz], DeviceTensor):
+                # an int32 zero point is kept on the host (integer constants
+                # of 4 bytes or more are); the pack and every call read one
+                # device copy of it (libkk checks that a call passes the
+                # weight and zero-point tensors its pack was made from)
+                dev = f"{wz}#dev"
+                if dev not in self.weights:
+                    self.weights[dev] = to_device(self.weights[wz])
+                ins = list(ins)
+                ins[3] = wz = dev
             key = (w, wz)
             if key not in packs:
                 packs[key] = f"{w}#{wz}#packed"
@@ -221,27 +241,72 @@ class PackedGraph:
                     self.weights[w], self.weights[wz] if wz else None)
             self.nodes[k] = (op, ins, outs, dict(at, packed=packs[key]))
 
-    def run(self, input_ids, style, speed=1.0, keep=(), pcm16=False, notch=True, gain=1.0):
+    def _check_finite(self, i, env):
+        """Strict mode (ref_runtime.py:404-418): raises at the first float
+        output of node i that holds a NaN or an infinity, naming the node
+        (and the original nodes it stands for) with the shape, dtype and
+        value range of each of its inputs."""
+        op, ins, outs, _at = self.nodes[i]
+        for o in outs:
+            v = env.get(o) if o else None
+            if v is None or np.dtype(v.dtype).kind != "f" or not int(np.prod(v.shape)):
+                continue
+            host = np.asarray(to_host(v))
+            if np.isfinite(host).all():
+                continue
+            bad = int((~np.isfinite(host)).sum())
+            described = []
+            for name in ins:
+                if not name or name not in env:
+                    continue
+                a = np.asarray(to_host(env[name]))
+                rng = None
+                if a.dtype.kind in "fiu" and a.size:
+                    af = a.astype(np.float64)
+                    rng = (float(np.nanmin(af)), float(np.nanmax(af))) if not np.isnan(af).all() \
+                        else (float("nan"), float("nan"))
+                described.append((name, tuple(a.shape), str(a.dtype), rng))
+            raise NonFiniteError(
+                f"non-finite output at node {i} {op} (original nodes {self.groups[i]}) -> {o} "
+                f"{tuple(v.shape)}: {bad} non-finite values\n  inputs: {described}",
+                node=i, op=op, output=o, inputs=described)
+
+    def run(self, input_ids, style, speed=1.0, keep=(), pcm16=False, notch=True, gain=1.0,
+            strict=False, max_nodes=None):
         """Returns the waveform on the host: float32 samples, or with
         `pcm16` the 16-bit PCM samples (int16) the reference's output stage
         makes of them on the device (audio.gd:59-106), through the notch
-        filter first unless `notch` is false."""
+        filter first unless `notch` is false.
+
+        Debugging aids: `strict` stops at the first node whose float output
+        is not finite and raises NonFiniteError naming it and its inputs'
+        ranges (ref_runtime.py:378-418; every float output is read back, so
+        it is slow); `max_nodes` runs only the first that many nodes of the
+        walk (executor.gd:67-72, 306-307) and returns None when the output
+        was not reached -- `keep` names the tensors to look at then, in
+        `last_env`."""
         env = dict(self.weights)
         env[self.inputs["input_ids"]] = np.asarray(input_ids, np.int64).reshape(1, -1)
         env[self.inputs["style"]] = to_device(np.asarray(style, np.float32).reshape(1, 256))
         env[self.inputs["speed"]] = to_device(np.asarray([speed], np.float32))
         keep = {str(k) for k in keep}
         frees = self.frees
-        for i, (op, ins, outs, at) in enumerate(self.nodes):
+        limit = len(self.nodes) if max_nodes is None or max_nodes < 0 else min(max_nodes, len(self.nodes))
+        for i in range(limit):
+            op, ins, outs, at = self.nodes[i]
             try:
                 dispatch(op, ins, outs, at, env)
             except Exception as exc:
                 raise RuntimeError(f"node {i} {op}: {exc}") from exc
+            if strict:
+                self._check_finite(i, env)
             for name in frees[i]:
                 if name not in keep:
                     env.pop(name, None)
-        out = env[self.output]
         self.last_env = {k: env[k] for k in keep if k in env}
+        if self.output not in env:
+            return None
+        out = env[self.output]
         if pcm16:
             taps = None
             if notch:
@@ -261,4 +326,4 @@ def synth_model(graph=None, seed=0):
 
 
 __all__ = ["load_graph", "structure_path", "synth_weights", "synth_model", "synth_inputs",
-           "PackedGraph", "DeviceTensor"]
+           "PackedGraph", "NonFiniteError", "DeviceTensor"]

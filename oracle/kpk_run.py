@@ -33,6 +33,16 @@ def run(graph, weights, input_ids, style, speed=1.0, max_nodes=None, capture=Non
     env[str(graph["inputs"]["style"])] = np.asarray(style, np.float32).reshape(1, 256)
     env[str(graph["inputs"]["speed"])] = np.asarray([speed], np.float32)
     ops = graph["ops"]
+    # Intermediates are dropped after their last reader (the captured ones,
+    # the weights and the output are kept), so that long utterances fit in
+    # host memory; the values computed are the same.
+    keep = {str(k) for k in weights} | {str(graph["output"])}
+    keep |= {str(t) for t in (capture or ())}
+    last = {}
+    for i, (_op, ins, _outs, _at, _pl) in enumerate(graph["nodes"]):
+        for t in ins:
+            if t >= 0:
+                last[str(t)] = i
     for i, (op_id, ins, outs, at, _place) in enumerate(graph["nodes"]):
         if max_nodes is not None and i >= max_nodes:
             break
@@ -41,6 +51,11 @@ def run(graph, weights, input_ids, style, speed=1.0, max_nodes=None, capture=Non
                              ["" if t < 0 else str(t) for t in outs], decode_attrs(at), env)
         except Exception as exc:
             raise RuntimeError(f"node {i} {ops[op_id]}: {exc}") from exc
+        if max_nodes is None:
+            for t in ins:
+                name = str(t)
+                if t >= 0 and last.get(name) == i and name not in keep:
+                    env.pop(name, None)
     out = env.get(str(graph["output"]))
     if capture is not None:
         return out, {t: env.get(str(t)) for t in capture}

@@ -1,6 +1,7 @@
-"""Writes graph_golden_t8.npz: checkpoints of the synthetic Kokoro graph (the
-packaged structure + seeded random learned weights, 8 phoneme ids, speed 1)
-computed by the CPU oracle (oracle/kpk_run.py).
+"""Writes graph_golden_t<N>.npz: checkpoints of the synthetic Kokoro graph
+(the packaged structure + seeded random learned weights, N phoneme ids
+(default 8; 128 for the graph the benchmark times), speed 1) computed by the
+CPU oracle (oracle/kpk_run.py).
 
 Checkpoints (tensor ids of the packed graph):
   2430  pre-round durations              (/encoder/Div_output_0)
@@ -12,7 +13,11 @@ Checkpoints (tensor ids of the packed graph):
   5038  conv_post output (log-magnitude and phase logits) -- first 1024 frames
   5092  the waveform, whole, as float16 (its values are within +-2: float16
         holds them to 2^-11 relative, far inside the waveform gate).
-Run from the repository root: python tests/golden/make_graph_golden.py
+With more than 8 ids the last frames of the three long checkpoints are kept
+too (t<id>_tail), so the end of the utterance is checked as well as its
+start.
+Run from the repository root: python tests/golden/make_graph_golden.py [N]
+(N = 128 takes several minutes of CPU time.)
 """
 import importlib
 import os
@@ -24,13 +29,18 @@ import numpy as np
 ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
 sys.path.insert(0, ROOT)
 
-N_IDS = 8
+N_IDS = int(sys.argv[1]) if len(sys.argv) > 1 else 8
 CHECK = [2430, 2432, 1165, 2892, 3037, 3304, 5038]
 HEAD = {3037: (1, 1024), 3304: (2, 16), 5038: (2, 1024)}  # tensor id: (time axis, frames kept)
 
 
 def head(v, axis, n):
     return np.ascontiguousarray(np.take(np.asarray(v), np.arange(min(n, v.shape[axis])), axis=axis))
+
+
+def tail(v, axis, n):
+    m = v.shape[axis]
+    return np.ascontiguousarray(np.take(np.asarray(v), np.arange(max(0, m - n), m), axis=axis))
 
 
 def main():
@@ -47,6 +57,8 @@ def main():
     for k in CHECK:
         v = np.asarray(cap[k])
         out[f"t{k}"] = head(v, *HEAD[k]) if k in HEAD else v
+        if k in HEAD and N_IDS > 8:
+            out[f"t{k}_tail"] = tail(v, *HEAD[k])
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), f"graph_golden_t{N_IDS}.npz")
     np.savez_compressed(path, **out)
     pre = np.asarray(cap[2430]).reshape(-1)

@@ -650,3 +650,30 @@ def test_conv_packed_weights(gpu, cin, cout, k, L, pad, dil, stride, wdt, wzp, r
         got = gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, packed=packed,
                                                 **kw).numpy()
         assert_bitexact(got, want, f"packed conv {cin}->{cout} k{k} call {call}")
+
+
+def test_conv_packed_refuses_another_weight(gpu):
+    """A packed buffer is used only with the weight and zero-point tensors it
+    was packed from: another weight of the same shape, or another zero point,
+    is refused with an error before any launch."""
+    r = rng(43)
+    w = gpu.to_device(r.integers(0, 256, (64, 64, 3)).astype(np.uint8))
+    w2 = gpu.to_device(r.integers(0, 256, (64, 64, 3)).astype(np.uint8))
+    wz = gpu.to_device(np.array(120, np.uint8))
+    wz2 = gpu.to_device(np.array(121, np.uint8))
+    packed = gpu.ops.conv_integer_pack(w, wz)
+    x = gpu.to_device(r.integers(0, 256, (1, 64, 300)).astype(np.uint8))
+    xz = gpu.to_device(np.array(100, np.uint8))
+    bias = gpu.to_device(r.normal(0, 0.5, (64,)).astype(np.float32))
+    sa = gpu.to_device(np.array(0.004, np.float32))
+    sw = gpu.to_device(np.array(0.003, np.float32))
+    kw = dict(pads=(1, 1), packed=packed)
+    ok = gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, **kw).numpy()
+    assert ok.shape == (1, 64, 300)
+    with pytest.raises(gpu._lib.KKError, match="another weight tensor"):
+        gpu.ops.conv_integer_scaled_qbias(x, w2, xz, wz, bias, sa, sw, **kw)
+    with pytest.raises(gpu._lib.KKError, match="another weight zero point"):
+        gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz2, bias, sa, sw, **kw)
+    with pytest.raises(gpu._lib.KKError, match="not made by kk_conv_integer_pack"):
+        other = gpu.DeviceTensor.empty(packed.shape, np.uint8)
+        gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, pads=(1, 1), packed=other)
