@@ -97,6 +97,17 @@ class Bench:
         self.call("kk_event_elapsed", 0, 1, ctypes.byref(ms))
         return ms.value / (reps * len(gids))
 
+    def graph_nodes(self, gid):
+        n = ctypes.c_int64()
+        self.call("kk_graph_nodes", gid, ctypes.byref(n))
+        return int(n.value)
+
+    def kernels_per_call(self, fn, i=0):
+        """Kernels one eager call of fn(i) launches (libkk's dispatch count)."""
+        before = self.kk.dispatch_count()
+        fn(i)
+        return self.kk.dispatch_count() - before
+
     def time_eager(self, fn, sets, reps):
         """Average ms per call of fn(i) for i in range(sets), called eagerly
         (for ops that draw scratch from the pool, which a graph recording
@@ -226,25 +237,26 @@ def run_gpu(args):
         op_ln(i)
         op_sm(i)
 
-    # One graph per input set (one step) and one graph for a whole rotation
-    # (nsets steps), so K steps cost K // nsets + K % nsets graph launches.
-    step_graphs = [B.graph(lambda i=i: step(i)) for i in range(nsets)]
-    rotation = B.graph(lambda: [step(i) for i in range(nsets)])
+    # The W warm-up steps and the K timed steps are each one recorded graph
+    # of exactly that many steps, walking the rotating input sets in turn, so
+    # the timed region is one graph launch whatever K is.
+    def steps_graph(k_steps, first=0):
+        return B.graph(lambda: [step((first + j) % nsets) for j in range(k_steps)])
 
-    def run_steps(k_steps):
-        for _ in range(k_steps // nsets):
-            B.call("kk_graph_launch", rotation)
-        for k in range(k_steps % nsets):
-            B.call("kk_graph_launch", step_graphs[k])
-
-    run_steps(args.warmup)
+    timed = steps_graph(args.steps, args.warmup)
+    if args.warmup > 0:
+        warm = steps_graph(args.warmup)
+        B.call("kk_graph_launch", warm)
+        kk.sync()
+        B.call("kk_graph_destroy", warm)
     kk.sync()
     B.call("kk_event_record", 2)
-    run_steps(args.steps)
+    B.call("kk_graph_launch", timed)
     B.call("kk_event_record", 3)
     kk.sync()
     ms = ctypes.c_float()
     B.call("kk_event_elapsed", 2, 3, ctypes.byref(ms))
+    B.call("kk_graph_destroy", timed)
     ms_per_step = ms.value / args.steps
     log(f"bench: step {ms_per_step * 1e3:.2f} us ({STEP_BYTES / ms_per_step / 1e6:.0f} GB/s)")
 
@@ -254,19 +266,23 @@ def run_gpu(args):
     def per_op(name, fn, nbytes=None, flops=None, reps=20, sets=nsets, eager=False, mfma=None):
         if eager:
             t_ms = B.time_eager(fn, sets, reps)
+            kernels = B.kernels_per_call(fn)
         else:  # one graph holding the op GRAPH_REPEAT times per rotating set
             # (each replay's own launch cost spread over as many calls as a
             # graph of a few ops would; the model graph holds thousands)
             gid = B.graph(lambda: [fn(i) for _ in range(GRAPH_REPEAT) for i in range(sets)])
             t_ms = B.time_graphs([gid], reps) / (sets * GRAPH_REPEAT)
+            kernels = B.graph_nodes(gid) / (sets * GRAPH_REPEAT)
             B.call("kk_graph_destroy", gid)
-        rec = {"us": round(t_ms * 1e3, 3)}
+        rec = {"us": round(t_ms * 1e3, 3), "kernels": kernels}
         if nbytes:
             gbs = nbytes / (t_ms * 1e-3) / 1e9
             rec.update(bytes=nbytes, gbps=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4))
         if flops:
             tf = flops / (t_ms * 1e-3) / 1e12
-            rec.update(flops=flops, tflops=round(tf, 2), frac_fp32=round(tf / FP32_PEAK_TFLOPS, 4))
+            rec.update(flops=flops, tflops=round(tf, 2))
+            if mfma != "i8":  # fp32-semantics work: its fraction of the fp32 peak
+                rec["frac_fp32"] = round(tf / FP32_PEAK_TFLOPS, 4)
             if mfma:  # the matrix-core type the kernel runs on, at its effective peak
                 kind, peak = MFMA_PEAKS[mfma]
                 rec.update(mfma=kind, mfma_peak_tflops=peak, frac_mfma=round(tf / peak, 4))
@@ -402,7 +418,7 @@ def run_gpu(args):
         "kk_conv_transpose1d", ot[i].desc(), xt[i].desc(), wt.desc(), sct.desc(), None, None, 10, 1,
         5, 5, 1, 0), flops=2 * 512 * 256 * 2400 * 20 // 10, sets=4, eager=True, mfma="f16x2")
 
-    # The decoder upsample stage as one chain (13 launches): int8
+    # The decoder upsample stage as one chain of 13 ops: int8
     # ConvTranspose1d 512->256 (k20, s10, p5) on [1,512,240], snake, AdaIN
     # (style [1,128], Linear 128->512), then two residual blocks AdaIN ->
     # snake -> int8 Conv1d 256->256 k3 (dilation 1, then 3) -> AdaIN -> snake
@@ -433,7 +449,7 @@ def run_gpu(args):
     flops4 = 2 * 512 * 256 * 2400 * 20 // 10 + 4 * 2 * 256 * 256 * 3 * 2400
     rec = per_op("decoder_upsample_stage_1x512x240", stage4, flops=flops4, sets=4, reps=10,
                  eager=True)
-    rec["launches"] = 13
+    rec["ops"] = 13
     rec["workload"] = ("int8 ConvT 512->256 k20 s10 + snake + AdaIN, then 2 residual blocks "
                        "(AdaIN, snake, int8 Conv1d 256 k3 d1/d3, AdaIN, snake, Conv1d k3, Add)")
 
@@ -469,16 +485,28 @@ def run_graph(n_ids, reps):
     g = kkg.load_graph()
     pg = kkg.PackedGraph(g, kkg.synth_weights(g, 0))
     ids, style, speed = kkg.synth_inputs(n_ids, 0)
-    pg.run(ids, style, speed, keep=[2432])  # warm-up: fills the buffer pool
+    first = pg.run(ids, style, speed, keep=[2432])  # warm-up: fills the buffer pool
     frames = int(np.asarray(kk.to_host(pg.last_env["2432"])).sum())
     kk.sync()
     walls = []
+    d0 = kk.dispatch_count()
     for _ in range(reps):
         t0 = time.perf_counter()
         wav = pg.run(ids, style, speed)
         walls.append(time.perf_counter() - t0)
+    dispatches = (kk.dispatch_count() - d0) // max(1, reps)
     wall = float(np.median(walls))
     audio = wav.size / 24000.0
+    # The timed output is checked: finite, 600 samples per predicted frame,
+    # not silent, and the same bits as the warm-up run.
+    if not np.isfinite(wav).all():
+        raise RuntimeError("kokoro graph: non-finite waveform")
+    if wav.size != 600 * frames:
+        raise RuntimeError(f"kokoro graph: {wav.size} samples for {frames} frames")
+    if not float(np.sqrt(np.mean(np.square(wav, dtype=np.float64)))) > 1e-3:
+        raise RuntimeError("kokoro graph: silent waveform")
+    if not np.array_equal(wav, first):
+        raise RuntimeError("kokoro graph: the timed run differs from the warm-up run")
     rec = {
         "audio_sec_per_wall_sec": round(audio / wall, 2),
         "wall_ms": round(wall * 1e3, 2),
@@ -489,6 +517,8 @@ def run_graph(n_ids, reps):
         "audio_sec": round(audio, 3),
         "nodes": len(g["nodes"]),
         "launch_nodes": len(pg.nodes),
+        "kernels_per_run": int(dispatches),
+        "checked": "finite, 600 samples per frame, not silent, bit-identical across runs",
         "peak_pool_bytes": kk.pool_stats()[2],
         "workload": (f"full Kokoro-82M-architecture graph ({len(g['nodes'])} nodes, "
                      f"{len(pg.nodes)} after chain fusion; int8 GEMM/conv + fp16 weights, "
@@ -497,6 +527,19 @@ def run_graph(n_ids, reps):
     }
     log(f"bench: kokoro graph {json.dumps(rec)}")
     return rec
+
+
+def blas_info():
+    """numpy's BLAS library, its version and thread count (threadpoolctl),
+    and OPENBLAS_NUM_THREADS as set in the environment."""
+    try:
+        from threadpoolctl import threadpool_info
+        libs = [f"{d.get('internal_api')} {d.get('version')} ({d.get('num_threads')} threads)"
+                for d in threadpool_info() if d.get("user_api") == "blas"]
+    except Exception:  # pragma: no cover - threadpoolctl is installed here
+        libs = []
+    return (f"BLAS: {', '.join(libs) or 'unknown'}; OPENBLAS_NUM_THREADS="
+            f"{os.environ.get('OPENBLAS_NUM_THREADS', 'unset')}")
 
 
 def run_graph_cpu(n_ids):
@@ -516,7 +559,8 @@ def run_graph_cpu(n_ids):
         "kind": "port",
         "sample": (f"numpy oracle whole-graph walk, {n_ids} ids ({len(ids)} tokens), "
                    f"{wav.size} samples in {wall:.1f} s; numpy ufuncs/einsum on 1 thread, "
-                   f"BLAS matmuls on up to the visible cores"),
+                   f"BLAS matmuls on up to the visible cores; numpy {np.__version__}; "
+                   f"{blas_info()}"),
     }
 
 
@@ -543,8 +587,9 @@ def run_cpu(seconds):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
+    blas = blas_info()
     if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
+        limiter.restore_original_limits()
     t = float(np.median(times))
     model = ""
     try:
@@ -562,7 +607,8 @@ def run_cpu(seconds):
         "sample": (f"numpy oracle, full step (AdaIN T=1200 and T=9600 with Linear, LayerNorm, "
                    f"Softmax) x{len(times)} runs, median {t * 1e3:.1f} ms/step; 1 thread "
                    f"(threadpoolctl); {model or platform.processor()}; "
-                   f"{len(os.sched_getaffinity(0))} cores visible; numpy {np.__version__}"),
+                   f"{len(os.sched_getaffinity(0))} cores visible; numpy {np.__version__}; "
+                   f"{blas} (limited to 1 thread for this sample)"),
     }
 
 

@@ -11,8 +11,9 @@ The directory name is not a Python identifier; import it with
 """
 from . import _lib  # noqa: F401
 from .dispatch import dispatch, to_device, to_host  # noqa: F401
-from .tensor import DeviceTensor, device_count, init, pool_stats, pool_trim, sync  # noqa: F401
+from .tensor import (DeviceTensor, device_count, dispatch_count, init, pool_stats,  # noqa: F401
+                     pool_trim, sync)
 from . import ops  # noqa: F401
 
 __all__ = ["dispatch", "to_device", "to_host", "DeviceTensor", "init", "sync",
-           "pool_stats", "pool_trim", "device_count", "ops"]
+           "pool_stats", "pool_trim", "device_count", "dispatch_count", "ops"]

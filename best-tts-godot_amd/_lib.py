@@ -110,6 +110,8 @@ PROTOTYPES = {
     "kk_graph_end": [ctypes.POINTER(_i)],
     "kk_graph_launch": [_i],
     "kk_graph_destroy": [_i],
+    "kk_graph_nodes": [_i, ctypes.POINTER(ctypes.c_int64)],
+    "kk_dispatch_count": [ctypes.POINTER(ctypes.c_uint64)],
 }
 
 _lib = None

@@ -172,10 +172,10 @@ static int launch_fir(const kk_tensor* x, const kk_tensor* taps, int center, flo
   const float* hp = static_cast<const float*>(taps->data);
   const int t = static_cast<int>(numel(taps));
   if (pcm)
-    hipLaunchKernelGGL(fir_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+    KK_LAUNCH(fir_kernel<true>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
                        ctx().stream, xp, n, hp, t, center, nullptr, pcm, gain);
   else
-    hipLaunchKernelGGL(fir_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
+    KK_LAUNCH(fir_kernel<false>, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0,
                        ctx().stream, xp, n, hp, t, center, y, nullptr, 0.0f);
   return check_launch("fir_kernel");
 }
@@ -203,7 +203,7 @@ int kk_pcm16(const kk_tensor* out_bytes, const kk_tensor* x, float gain) {
   KK_TRY(check_pcm_out(out_bytes, n, "kk_pcm16"));
   if (n == 0) return KK_OK;
   const unsigned g = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 8 * 256), 4096)));
-  hipLaunchKernelGGL(pcm16_kernel, dim3(g), dim3(256), 0, ctx().stream,
+  KK_LAUNCH(pcm16_kernel, dim3(g), dim3(256), 0, ctx().stream,
                      static_cast<const float*>(x->data), n, gain, static_cast<int16_t*>(out_bytes->data));
   return check_launch("pcm16_kernel");
 }

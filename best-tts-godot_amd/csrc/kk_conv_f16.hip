@@ -574,9 +574,9 @@ static bool ring_ok(const HArgs& a) {
 template <class T, typename TW>
 static void launch_t(const HArgs& a, const dim3& grid) {
   if (a.wt)
-    hipLaunchKernelGGL((convh_ring_kernel<T>), grid, dim3(kThreads), 0, ctx().stream, a);
+    KK_LAUNCH((convh_ring_kernel<T>), grid, dim3(kThreads), 0, ctx().stream, a);
   else
-    hipLaunchKernelGGL((convh_kernel<T, TW, false>), grid, dim3(kThreads), 0, ctx().stream, a);
+    KK_LAUNCH((convh_kernel<T, TW, false>), grid, dim3(kThreads), 0, ctx().stream, a);
 }
 
 // Split-K count for the ring kernel: enough splits that every CU gets two
@@ -610,7 +610,7 @@ static void launch(HArgs& a, int w_dt, int64_t batch, float* part, size_t part_b
   if (a.part) {
     const dim3 fg(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Lout, 256), 64)),
                   static_cast<unsigned>(std::min<int64_t>(a.Cout, 65535)), static_cast<unsigned>(batch));
-    hipLaunchKernelGGL(convh_splitk_finish, fg, dim3(256), 0, ctx().stream, a);
+    KK_LAUNCH(convh_splitk_finish, fg, dim3(256), 0, ctx().stream, a);
     a.part = nullptr;
     a.ksplit = 1;
   }
@@ -631,20 +631,20 @@ static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
     const dim3 g(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Kg, 256), 64)),
                  static_cast<unsigned>(std::min<int64_t>(a.Mp, 65535)));
     if (w->dtype == KK_F16)
-      hipLaunchKernelGGL(convh_weights<_Float16>, g, dim3(256), 0, ctx().stream, wt, a);
+      KK_LAUNCH(convh_weights<_Float16>, g, dim3(256), 0, ctx().stream, wt, a);
     else if (w->dtype == KK_I8)
-      hipLaunchKernelGGL(convh_weights<int8_t>, g, dim3(256), 0, ctx().stream, wt, a);
+      KK_LAUNCH(convh_weights<int8_t>, g, dim3(256), 0, ctx().stream, wt, a);
     else
-      hipLaunchKernelGGL(convh_weights<uint8_t>, g, dim3(256), 0, ctx().stream, wt, a);
+      KK_LAUNCH(convh_weights<uint8_t>, g, dim3(256), 0, ctx().stream, wt, a);
     a.wt = wt;
   } else {
-    hipLaunchKernelGGL(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, a.flag, a.xmax);
+    KK_LAUNCH(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, a.flag, a.xmax);
   }
   {
     const int64_t n = a.Cin * a.L * batch;
     const unsigned g = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256 * 16), 1024)));
     const int vec = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 ? 1 : 0;
-    hipLaunchKernelGGL(convh_absmax, dim3(g), dim3(256), 0, ctx().stream, a.x, n, vec, a.xmax);
+    KK_LAUNCH(convh_absmax, dim3(g), dim3(256), 0, ctx().stream, a.x, n, vec, a.xmax);
   }
   // split-K partial sums: the context scratch beside weights rearranged there
   float* part = nullptr;

@@ -441,7 +441,7 @@ static int launch_inner_op(const EwArgs& A, int vec, bool u32, int flat_kinds) {
   const int64_t items = A.n / vec;
   hipStream_t s = ctx().stream;
   if (flat_kinds >= 0) {
-    hipLaunchKernelGGL((ew_flat4<OP, NIN>), dim3(grid_for(A.n / 4)), dim3(256), 0, s, A,
+    KK_LAUNCH((ew_flat4<OP, NIN>), dim3(grid_for(A.n / 4)), dim3(256), 0, s, A,
                        flat_kinds);
     return check_launch("ew_flat4");
   }
@@ -451,17 +451,17 @@ static int launch_inner_op(const EwArgs& A, int vec, bool u32, int flat_kinds) {
     const int64_t gx = std::min<int64_t>(ceil_div(per_row, 256), 1 << 20);
     const int64_t gy = std::min<int64_t>(rows, 65535);
     const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
-    if (vec == 4) hipLaunchKernelGGL((ew_rows<OP, NIN, 4>), grid, dim3(256), 0, s, A);
-    else hipLaunchKernelGGL((ew_rows<OP, NIN, 1>), grid, dim3(256), 0, s, A);
+    if (vec == 4) KK_LAUNCH((ew_rows<OP, NIN, 4>), grid, dim3(256), 0, s, A);
+    else KK_LAUNCH((ew_rows<OP, NIN, 1>), grid, dim3(256), 0, s, A);
     return check_launch("ew_rows");
   }
   const int grid = grid_for(items);
   if (vec == 4) {
-    if (u32) hipLaunchKernelGGL((ew_inner<OP, NIN, 4, uint32_t>), dim3(grid), dim3(256), 0, s, A);
-    else hipLaunchKernelGGL((ew_inner<OP, NIN, 4, int64_t>), dim3(grid), dim3(256), 0, s, A);
+    if (u32) KK_LAUNCH((ew_inner<OP, NIN, 4, uint32_t>), dim3(grid), dim3(256), 0, s, A);
+    else KK_LAUNCH((ew_inner<OP, NIN, 4, int64_t>), dim3(grid), dim3(256), 0, s, A);
   } else {
-    if (u32) hipLaunchKernelGGL((ew_inner<OP, NIN, 1, uint32_t>), dim3(grid), dim3(256), 0, s, A);
-    else hipLaunchKernelGGL((ew_inner<OP, NIN, 1, int64_t>), dim3(grid), dim3(256), 0, s, A);
+    if (u32) KK_LAUNCH((ew_inner<OP, NIN, 1, uint32_t>), dim3(grid), dim3(256), 0, s, A);
+    else KK_LAUNCH((ew_inner<OP, NIN, 1, int64_t>), dim3(grid), dim3(256), 0, s, A);
   }
   return check_launch("ew_inner");
 }
@@ -573,7 +573,7 @@ static int run_elementwise(int op, const kk_tensor* out, const kk_tensor* const*
     }
     return launch_inner(A, nin, vec4 ? 4 : 1, fits_u32(p), kinds);
   }
-  hipLaunchKernelGGL(ew_generic, dim3(grid_for(p.n)), dim3(256), 0, ctx().stream, A, nin, mode);
+  KK_LAUNCH(ew_generic, dim3(grid_for(p.n)), dim3(256), 0, ctx().stream, A, nin, mode);
   return check_launch("ew_generic");
 }
 
@@ -597,6 +597,33 @@ __global__ void __launch_bounds__(256) gather_kernel(T* __restrict__ out, const 
     if (k < 0) k += dim;
     k = k < 0 ? 0 : (k >= dim ? dim - 1 : k);
     out[t] = data[(o * dim + k) * inner + i];
+  }
+}
+
+// A copy between two contiguous tensors of one dtype, 16-byte aligned: each
+// block moves a contiguous stretch of 256 * U 16-byte items, every thread
+// issuing its U non-temporal loads before its U stores (U items in flight a
+// lane; one item a lane leaves a wave waiting on a single round trip); the
+// last bytes % 16 are moved by block 0.
+template <int U>
+__global__ void __launch_bounds__(256) copy_flat16(float* __restrict__ out,
+                                                   const float* __restrict__ in, int64_t n16,
+                                                   int64_t tail_bytes) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (256 * U) + threadIdx.x;
+  float4 v[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int64_t i = base + j * 256;
+    if (i < n16) v[j] = ld_stream4(in + 4 * i);
+  }
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int64_t i = base + j * 256;
+    if (i < n16) st_stream4(out + 4 * i, v[j]);
+  }
+  if (blockIdx.x == 0 && threadIdx.x < tail_bytes) {
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(in + 4 * n16);
+    reinterpret_cast<uint8_t*>(out + 4 * n16)[threadIdx.x] = src[threadIdx.x];
   }
 }
 
@@ -663,8 +690,8 @@ static bool snake_rows_try(const kk_tensor* out, const kk_tensor* x, const kk_te
                  static_cast<int>(L / 4)};
   const int width = static_cast<int>(std::min<int64_t>(256, ceil_div(L / 4, 64) * 64));
   const dim3 grid(static_cast<unsigned>(ceil_div(L / 4, int64_t{width})), static_cast<unsigned>(rows));
-  if (recip) hipLaunchKernelGGL((snake_rows<true>), grid, dim3(width), 0, ctx().stream, S);
-  else hipLaunchKernelGGL((snake_rows<false>), grid, dim3(width), 0, ctx().stream, S);
+  if (recip) KK_LAUNCH((snake_rows<true>), grid, dim3(width), 0, ctx().stream, S);
+  else KK_LAUNCH((snake_rows<false>), grid, dim3(width), 0, ctx().stream, S);
   *status = check_launch("snake_rows");
   return true;
 }
@@ -790,6 +817,38 @@ int kk_dequantize(const kk_tensor* out, const kk_tensor* q, const kk_tensor* sca
 
 int kk_copy(const kk_tensor* out, const kk_tensor* x) {
   KK_TRY(check_tensor(x, "x"));
+  KK_TRY(check_tensor(out, "out"));
+  if (out->dtype == x->dtype && out->rank == x->rank && is_contiguous(out) &&
+      is_contiguous(x) && numel(out) == numel(x) && numel(x) > 0 &&
+      reinterpret_cast<uintptr_t>(out->data) % 16 == 0 &&
+      reinterpret_cast<uintptr_t>(x->data) % 16 == 0) {
+    bool same = true;
+    for (int d = 0; d < x->rank; ++d) same = same && out->shape[d] == x->shape[d];
+    if (same) {
+      KK_TRY(require_ready());
+      const int64_t bytes = numel(x) * dtype_size(x->dtype);
+      // Four items a lane between 16 and 64 MB, one elsewhere (measured on
+      // MI355X, eager launches over inputs rotating past the Infinity Cache:
+      // 4.9 MB 2.97 us with one item against 3.48 with four; 39 MB 7.11 us
+      // with four against 7.87; 73 MB 23.7 against 26.3; 220 MB 66.5 against
+      // 73.8).
+      const int U = bytes > (int64_t{16} << 20) && bytes < (int64_t{64} << 20) ? 4 : 1;
+      const int64_t n16 = bytes / 16;
+      const int64_t blocks = std::max<int64_t>(1, ceil_div(n16, 256 * U));
+      if (blocks >= (int64_t(1) << 31))
+        return set_error(KK_E_UNSUPPORTED, "kk_copy: %lld bytes exceed one launch",
+                         (long long)bytes);
+      float* o = static_cast<float*>(out->data);
+      const float* in = static_cast<const float*>(x->data);
+      if (U == 4)
+        KK_LAUNCH((copy_flat16<4>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, ctx().stream,
+                  o, in, n16, bytes - 16 * n16);
+      else
+        KK_LAUNCH((copy_flat16<1>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, ctx().stream,
+                  o, in, n16, bytes - 16 * n16);
+      return check_launch("copy_flat16");
+    }
+  }
   const kk_tensor* ins[1] = {x};
   const int mode = (is_float(out->dtype) || is_float(x->dtype)) ? MODE_FLOAT : MODE_INT;
   return run_elementwise(OPX_COPY, out, ins, 1, 0.0f, 0, mode);
@@ -825,7 +884,7 @@ int kk_fill(const kk_tensor* out, double value) {
     A.dims[d] = d < p.rank ? p.dims[d] : 1;
     A.st[0][d] = d < p.rank ? p.st[0][d] : 0;
   }
-  hipLaunchKernelGGL(fill_kernel, dim3(grid_for(p.n)), dim3(256), 0, ctx().stream, A, value);
+  KK_LAUNCH(fill_kernel, dim3(grid_for(p.n)), dim3(256), 0, ctx().stream, A, value);
   return check_launch("fill_kernel");
 }
 
@@ -864,22 +923,22 @@ int kk_gather(const kk_tensor* out, const kk_tensor* data, const kk_tensor* indi
   hipStream_t s = ctx().stream;
   switch (dtype_size(data->dtype)) {
     case 1:
-      hipLaunchKernelGGL(gather_kernel<uint8_t>, dim3(grid), dim3(256), 0, s,
+      KK_LAUNCH(gather_kernel<uint8_t>, dim3(grid), dim3(256), 0, s,
                          static_cast<uint8_t*>(out->data), static_cast<const uint8_t*>(data->data),
                          indices->data, indices->dtype, outer, dim, nidx, inner);
       break;
     case 2:
-      hipLaunchKernelGGL(gather_kernel<uint16_t>, dim3(grid), dim3(256), 0, s,
+      KK_LAUNCH(gather_kernel<uint16_t>, dim3(grid), dim3(256), 0, s,
                          static_cast<uint16_t*>(out->data), static_cast<const uint16_t*>(data->data),
                          indices->data, indices->dtype, outer, dim, nidx, inner);
       break;
     case 4:
-      hipLaunchKernelGGL(gather_kernel<uint32_t>, dim3(grid), dim3(256), 0, s,
+      KK_LAUNCH(gather_kernel<uint32_t>, dim3(grid), dim3(256), 0, s,
                          static_cast<uint32_t*>(out->data), static_cast<const uint32_t*>(data->data),
                          indices->data, indices->dtype, outer, dim, nidx, inner);
       break;
     default:
-      hipLaunchKernelGGL(gather_kernel<uint64_t>, dim3(grid), dim3(256), 0, s,
+      KK_LAUNCH(gather_kernel<uint64_t>, dim3(grid), dim3(256), 0, s,
                          static_cast<uint64_t*>(out->data), static_cast<const uint64_t*>(data->data),
                          indices->data, indices->dtype, outer, dim, nidx, inner);
   }

@@ -754,11 +754,11 @@ static int check_grid(const dim3& g, int64_t z) {
 #define KK_TILED(KERNEL, TS, GRID, ...)                                                       \
   do {                                                                                          \
     if ((TS) == TILE_L)                                                                         \
-      hipLaunchKernelGGL((KERNEL<CfgL, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
+      KK_LAUNCH((KERNEL<CfgL, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
     else if ((TS) == TILE_M)                                                                    \
-      hipLaunchKernelGGL((KERNEL<CfgM, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
+      KK_LAUNCH((KERNEL<CfgM, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
     else                                                                                        \
-      hipLaunchKernelGGL((KERNEL<CfgS, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
+      KK_LAUNCH((KERNEL<CfgS, __VA_ARGS__>), GRID, dim3(kNT), 0, ctx().stream, args); \
   } while (0)
 
 static bool aligned(const void* p, int bytes) {
@@ -792,7 +792,7 @@ static int launch_gemm(const GemmArgs& args, int64_t batch, bool weights_rounded
   if (args.N <= kSkinnyN && args.K <= kSkinnyK && args.M * batch >= 4096) {
     const int64_t rows = args.M * batch;
     const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(rows, 256), 1 << 16));
-    hipLaunchKernelGGL(gemm_skinny_kernel, dim3(grid), dim3(256), 0, ctx().stream, args, batch);
+    KK_LAUNCH(gemm_skinny_kernel, dim3(grid), dim3(256), 0, ctx().stream, args, batch);
     return check_launch("gemm_skinny_kernel");
   }
   // 8-bit and fp16 weights with fp32 activations: the bf16 matrix cores
@@ -861,7 +861,7 @@ static int launch_gemm(const GemmArgs& args, int64_t batch, bool weights_rounded
   KK_TRY(check_launch("gemm_kernel"));
   if (args.splits > 1) {
     const int64_t total = batch * args.M * args.N;
-    hipLaunchKernelGGL(gemm_splitk_reduce, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 4096))),
+    KK_LAUNCH(gemm_splitk_reduce, dim3(static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 4096))),
                        dim3(256), 0, ctx().stream, args, batch);
     KK_TRY(check_launch("gemm_splitk_reduce"));
   }
@@ -1037,7 +1037,7 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
   D.s = stride; D.d = dilation; D.p0 = pad0; D.group = group;
   const int64_t total = N * Cout * Lout;
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 1 << 20));
-  hipLaunchKernelGGL(conv1d_direct_kernel, dim3(grid), dim3(256), 0, ctx().stream, D);
+  KK_LAUNCH(conv1d_direct_kernel, dim3(grid), dim3(256), 0, ctx().stream, D);
   return check_launch("conv1d_direct_kernel");
 }
 
@@ -1090,11 +1090,11 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
     if (convh_run(out, x, w, dq, bias, true, stride, 1, pad0, args.nq, &hflag, &hws))
       args.only_if = hflag;
     if (ts == TILE_L)
-      hipLaunchKernelGGL(conv_transpose_kernel<CfgL>, grid, dim3(kNT), 0, ctx().stream, args);
+      KK_LAUNCH(conv_transpose_kernel<CfgL>, grid, dim3(kNT), 0, ctx().stream, args);
     else if (ts == TILE_M)
-      hipLaunchKernelGGL(conv_transpose_kernel<CfgM>, grid, dim3(kNT), 0, ctx().stream, args);
+      KK_LAUNCH(conv_transpose_kernel<CfgM>, grid, dim3(kNT), 0, ctx().stream, args);
     else
-      hipLaunchKernelGGL(conv_transpose_kernel<CfgS>, grid, dim3(kNT), 0, ctx().stream, args);
+      KK_LAUNCH(conv_transpose_kernel<CfgS>, grid, dim3(kNT), 0, ctx().stream, args);
     if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
     return check_launch("conv_transpose_kernel");
   }
@@ -1106,11 +1106,11 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
   const int64_t total = N * Cout * Lout;
   if (group == 1 && dilation == 1 && Cin * Cout * K <= kSmallTW) {
     const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 2048));
-    hipLaunchKernelGGL(conv_transpose_small_kernel, dim3(g), dim3(256), 0, ctx().stream, D);
+    KK_LAUNCH(conv_transpose_small_kernel, dim3(g), dim3(256), 0, ctx().stream, D);
     return check_launch("conv_transpose_small_kernel");
   }
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 1 << 20));
-  hipLaunchKernelGGL(conv_transpose_direct_kernel, dim3(grid), dim3(256), 0, ctx().stream, D);
+  KK_LAUNCH(conv_transpose_direct_kernel, dim3(grid), dim3(256), 0, ctx().stream, D);
   return check_launch("conv_transpose_direct_kernel");
 }
 

@@ -451,7 +451,7 @@ static bool gemm_fused_try(const float* a, int64_t a_si, const void* b, int b_dt
   const int shape = bt == 1 && mt * ceil_div(N, 64) >= cus ? 0 : 1;
 #endif
 #define KK_GFU_LAUNCH(SH)                                                                       \
-  hipLaunchKernelGGL((gemm_fused_kernel<SH>),                                                   \
+  KK_LAUNCH((gemm_fused_kernel<SH>),                                                   \
                      dim3(static_cast<unsigned>(ceil_div(N, SH::BN)), static_cast<unsigned>(mt)), \
                      dim3(SH::THREADS), 0, ctx().stream, g)
   using H4 = Shape<1, 4, 2>;

@@ -113,7 +113,7 @@ __global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __rest
 
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
                     uint8_t* zp_out, const int* only_if, int* clear) {
-  hipLaunchKernelGGL(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
+  KK_LAUNCH(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
                      scale_out, zp_out, only_if, clear);
   return check_launch("dql_fold");
 }
@@ -709,7 +709,7 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
   const int vec = (reinterpret_cast<uintptr_t>(x->data) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(y->data) % 4 == 0) ? 1 : 0;
   if (n <= kDqlSmall) {
-    hipLaunchKernelGGL(dql_small, dim3(1), dim3(kDqlSmallThreads), 0, ctx().stream,
+    KK_LAUNCH(dql_small, dim3(1), dim3(kDqlSmallThreads), 0, ctx().stream,
                        static_cast<const float*>(x->data), n, static_cast<float*>(scale->data),
                        static_cast<uint8_t*>(zp->data), static_cast<uint8_t*>(y->data), vec);
     return check_launch("dql_small");
@@ -717,18 +717,18 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
   void* part = nullptr;
   KK_TRY(kk_alloc(sizeof(float2) * (nblk + 1), &part));
   float2* pp = static_cast<float2*>(part);
-  hipLaunchKernelGGL(dql_minmax, dim3(nblk), dim3(256), 0, ctx().stream,
+  KK_LAUNCH(dql_minmax, dim3(nblk), dim3(256), 0, ctx().stream,
                      static_cast<const float*>(x->data), n, pp, vec);
   int rc = check_launch("dql_minmax");
   if (rc == KK_OK) {
-    hipLaunchKernelGGL(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, pp, nblk, pp + nblk,
+    KK_LAUNCH(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, pp, nblk, pp + nblk,
                        static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data),
                        static_cast<const int*>(nullptr), static_cast<int*>(nullptr));
     rc = check_launch("dql_fold");
   }
   if (rc == KK_OK) {
     const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 1024), 4096));
-    hipLaunchKernelGGL(dql_quantize, dim3(g), dim3(256), 0, ctx().stream,
+    KK_LAUNCH(dql_quantize, dim3(g), dim3(256), 0, ctx().stream,
                        static_cast<const float*>(x->data), n, pp + nblk,
                        static_cast<uint8_t*>(y->data), vec);
     rc = check_launch("dql_quantize");
@@ -832,7 +832,7 @@ int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const
     A.yh = yh ? static_cast<float*>(yh->data) : nullptr;
     A.yc = yc ? static_cast<float*>(yc->data) : nullptr;
     A.seq = seq; A.batch = batch; A.H = H; A.ndir = ndir;
-    hipLaunchKernelGGL(lstm_recurrence, dim3(static_cast<unsigned>(ndir * batch)),
+    KK_LAUNCH(lstm_recurrence, dim3(static_cast<unsigned>(ndir * batch)),
                        dim3(kLstmThreads), 0, ctx().stream, A);
     rc = check_launch("lstm_recurrence");
   }
@@ -864,7 +864,7 @@ int kk_stft(const kk_tensor* out, const kk_tensor* signal, const kk_tensor* wind
     return set_error(KK_E_UNSUPPORTED, "kk_stft: frame_length %lld too long (basis > 64 KB)",
                      (long long)frame_length);
   const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 1024));
-  hipLaunchKernelGGL(stft_kernel, dim3(blocks), dim3(256), lds, ctx().stream,
+  KK_LAUNCH(stft_kernel, dim3(blocks), dim3(256), lds, ctx().stream,
                      static_cast<float*>(out->data), static_cast<const float*>(signal->data),
                      window->data, window->dtype, batch, slen, nframes, static_cast<int>(nfreq),
                      static_cast<int>(frame_length), frame_step);
@@ -884,7 +884,7 @@ int kk_resize(const kk_tensor* out, const kk_tensor* x, int mode, double scale) 
     if (x->shape[i] != out->shape[i]) return set_error(KK_E_ARG, "kk_resize: leading axes differ");
   const int64_t rows = lin ? numel(x) / lin : 0;
   if (!rows || !lout) return KK_OK;
-  hipLaunchKernelGGL(resize_kernel, dim3(grid1d(rows * lout)), dim3(256), 0, ctx().stream,
+  KK_LAUNCH(resize_kernel, dim3(grid1d(rows * lout)), dim3(256), 0, ctx().stream,
                      static_cast<float*>(out->data), static_cast<const float*>(x->data), rows, lin,
                      lout, scale, mode);
   return check_launch("resize_kernel");
@@ -921,11 +921,11 @@ int kk_pad(const kk_tensor* out, const kk_tensor* x, const int64_t* pads, int mo
     const int64_t rows = P.n / lout;
     const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(lout, 256 * 4), 1 << 16)),
                     static_cast<unsigned>(std::min<int64_t>(rows, 65535)));
-    hipLaunchKernelGGL(pad_rows_kernel, grid, dim3(256), 0, ctx().stream,
+    KK_LAUNCH(pad_rows_kernel, grid, dim3(256), 0, ctx().stream,
                        static_cast<float*>(out->data), static_cast<const float*>(x->data), P, rows);
     return check_launch("pad_rows_kernel");
   }
-  hipLaunchKernelGGL(pad_kernel, dim3(grid1d(P.n)), dim3(256), 0, ctx().stream,
+  KK_LAUNCH(pad_kernel, dim3(grid1d(P.n)), dim3(256), 0, ctx().stream,
                      static_cast<float*>(out->data), static_cast<const float*>(x->data), P);
   return check_launch("pad_kernel");
 }
@@ -946,24 +946,24 @@ int kk_cumsum(const kk_tensor* out, const kk_tensor* x, int axis) {
   if (!numel(x)) return KK_OK;
   const dim3 g(grid1d(outer * inner));
   if (x->dtype == KK_F32 && dim <= kCumsumLds && outer * inner <= 0x7fffffff) {
-    hipLaunchKernelGGL(cumsum_lds_kernel, dim3(static_cast<unsigned>(outer * inner)), dim3(256), 0,
+    KK_LAUNCH(cumsum_lds_kernel, dim3(static_cast<unsigned>(outer * inner)), dim3(256), 0,
                        ctx().stream, static_cast<float*>(out->data), static_cast<const float*>(x->data),
                        dim, inner);
     return check_launch("cumsum_lds_kernel");
   }
   switch (x->dtype) {
     case KK_F32:
-      hipLaunchKernelGGL(cumsum_kernel<float>, g, dim3(256), 0, ctx().stream,
+      KK_LAUNCH(cumsum_kernel<float>, g, dim3(256), 0, ctx().stream,
                          static_cast<float*>(out->data), static_cast<const float*>(x->data), outer,
                          dim, inner);
       break;
     case KK_I64:
-      hipLaunchKernelGGL(cumsum_kernel<int64_t>, g, dim3(256), 0, ctx().stream,
+      KK_LAUNCH(cumsum_kernel<int64_t>, g, dim3(256), 0, ctx().stream,
                          static_cast<int64_t*>(out->data), static_cast<const int64_t*>(x->data),
                          outer, dim, inner);
       break;
     case KK_I32:
-      hipLaunchKernelGGL(cumsum_kernel<int32_t>, g, dim3(256), 0, ctx().stream,
+      KK_LAUNCH(cumsum_kernel<int32_t>, g, dim3(256), 0, ctx().stream,
                          static_cast<int32_t*>(out->data), static_cast<const int32_t*>(x->data),
                          outer, dim, inner);
       break;
@@ -992,7 +992,7 @@ int kk_scatter_nd(const kk_tensor* out, const kk_tensor* updates, const int64_t*
   KK_TRY(kk_alloc(sizeof(int64_t) * nidx, &dev));
   int rc = kk_upload(dev, offsets, sizeof(int64_t) * nidx);
   if (rc == KK_OK) {
-    hipLaunchKernelGGL(scatter_kernel, dim3(grid1d(nidx * inner)), dim3(256), 0, ctx().stream,
+    KK_LAUNCH(scatter_kernel, dim3(grid1d(nidx * inner)), dim3(256), 0, ctx().stream,
                        static_cast<uint8_t*>(out->data), static_cast<const uint8_t*>(updates->data),
                        static_cast<const int64_t*>(dev), nidx, inner, dtype_size(out->dtype));
     rc = check_launch("scatter_kernel");

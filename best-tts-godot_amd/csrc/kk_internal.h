@@ -31,6 +31,9 @@ struct Context {
   // before the next call's kernels run, and the buffer never moves while a
   // recorded graph may refer to it.
   void* scratch = nullptr;
+  // Kernels launched outside graph recording since kk_init (each replay of a
+  // recorded graph launches its kernels without passing through here).
+  uint64_t dispatches = 0;
 };
 constexpr size_t kScratchBytes = size_t{16} << 20;
 constexpr int kRowCounters = 65536;
@@ -54,9 +57,19 @@ __device__ __forceinline__ uint32_t dql_byte(float x, float sc, float z) {
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
                     uint8_t* zp_out, const int* only_if = nullptr, int* clear = nullptr);
 Context& ctx();
+// Every kernel launch of the library goes through KK_LAUNCH, which counts it
+// (kk_dispatch_count) unless a graph is being recorded.
+#define KK_LAUNCH(...)                                        \
+  do {                                                        \
+    if (!::kk::ctx().capturing) ++::kk::ctx().dispatches;     \
+    hipLaunchKernelGGL(__VA_ARGS__);                          \
+  } while (0)
 // Takes the device address of the allocation-free convolution's file-scope
 // scratch for `device` (current), once per device (kk_conv_i8.hip).
 int conv_i8_scratch_setup(int device);
+// Drops the record of what a packed ConvInteger weight buffer at `p` was
+// made from (kk_free calls it: the address may next hold anything).
+void conv_i8_forget_pack(const void* p);
 
 // Thread-local last error; set_error returns `code` so call sites can
 // `return set_error(KK_E_ARG, "...")`.
@@ -380,7 +393,8 @@ bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t 
                  const Dequant& dq, float* out, int64_t som, int64_t son, const BatchMap& bm,
                  int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, const int* only_if,
                  int* status);
-// XCD-aware block order: workgroup w runs on XCD w % 8, so XCD x is given
+// XCD-aware block order (this library is built for gfx950 alone, whose
+// parts have 8 XCDs): workgroup w runs on XCD w % 8, so XCD x is given
 // the contiguous run of tiles x q + min(x, r) .. (T = 8 q + r tiles, the
 // first r XCDs one more), x-fastest: neighbouring tiles, which share input
 // rows or halos, share an L2.  A bijection on the grid; the tile's (x, y, z).
@@ -391,6 +405,15 @@ __device__ inline uint3 xcd_tile() {
   const uint32_t xcd = wid % 8u, q8 = tiles / 8u, r8 = tiles % 8u;
   const uint32_t t = xcd * q8 + (xcd < r8 ? xcd : r8) + wid / 8u;
   return make_uint3(t % gx, (t / gx) % gy, t / (gx * gy));
+}
+// Host check for a grid whose kernel calls xcd_tile: its block count, and
+// so every linear block id, fits the 32-bit arithmetic above.
+inline int check_xcd_grid(const dim3& g, const char* who) {
+  const uint64_t n = uint64_t{g.x} * g.y * g.z;
+  if (n >= (uint64_t{1} << 32))
+    return set_error(KK_E_UNSUPPORTED, "%s: %llu blocks exceed the 32-bit tile order", who,
+                     static_cast<unsigned long long>(n));
+  return KK_OK;
 }
 
 // A zero-point-only shift (scale 1) for the integer ops: per tensor, or per

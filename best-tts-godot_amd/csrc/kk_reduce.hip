@@ -1842,33 +1842,33 @@ static unsigned row_threads(const RowShape& rs, int64_t rows) {
     if ((RS).group == 64) {                                                                    \
       if ((RS).vec == 4) {                                                                     \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<64, 4, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 1: KK_LAUNCH((KERNEL<64, 1, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: KK_LAUNCH((KERNEL<64, 2, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: KK_LAUNCH((KERNEL<64, 4, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       } else {                                                                                 \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<64, 1, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<64, 2, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<64, 4, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 1: KK_LAUNCH((KERNEL<64, 1, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: KK_LAUNCH((KERNEL<64, 2, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: KK_LAUNCH((KERNEL<64, 4, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       }                                                                                        \
     } else {                                                                                   \
       if ((RS).vec == 4) {                                                                     \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<256, 16, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 1: KK_LAUNCH((KERNEL<256, 1, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: KK_LAUNCH((KERNEL<256, 2, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 4: KK_LAUNCH((KERNEL<256, 4, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 8: KK_LAUNCH((KERNEL<256, 8, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: KK_LAUNCH((KERNEL<256, 16, 4>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       } else {                                                                                 \
         switch ((RS).nv) {                                                                     \
-          case 1: hipLaunchKernelGGL((KERNEL<256, 1, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 2: hipLaunchKernelGGL((KERNEL<256, 2, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 4: hipLaunchKernelGGL((KERNEL<256, 4, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          case 8: hipLaunchKernelGGL((KERNEL<256, 8, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
-          default: hipLaunchKernelGGL((KERNEL<256, 16, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 1: KK_LAUNCH((KERNEL<256, 1, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 2: KK_LAUNCH((KERNEL<256, 2, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 4: KK_LAUNCH((KERNEL<256, 4, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          case 8: KK_LAUNCH((KERNEL<256, 8, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
+          default: KK_LAUNCH((KERNEL<256, 16, 1>), _grid, dim3(_threads), 0, _s, __VA_ARGS__); break; \
         }                                                                                      \
       }                                                                                        \
     }                                                                                          \
@@ -1951,13 +1951,13 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
   NpTail tail;  // the rows' partial 8192-block, if any
   np_tail_plan(static_cast<int>(n % kNpBlock), &tail);
   if (n <= kNpLeaf) {
-    hipLaunchKernelGGL(np_leaf_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 256))),
+    KK_LAUNCH(np_leaf_rows_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 256))),
                        dim3(256), 0, st, out, x, rows, static_cast<int>(n), mean ? 1 : 0);
     return check_launch("np_leaf_rows_kernel");
   }
   if (n <= kNpRowMax) {
     Affine af{};
-    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
+    KK_LAUNCH(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(n), st, out, x, int64_t{1}, static_cast<int>(n), mean ? 1 : 0,
                        0.0f, af, vec ? 1 : 0, static_cast<float2*>(nullptr), static_cast<float2*>(nullptr),
                        tail);
@@ -1967,7 +1967,7 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
   const int64_t nblk = ceil_div(n, kNpBlock);
   void* part = nullptr;
   KK_TRY(kk_alloc(sizeof(float) * rows * nblk, &part));
-  hipLaunchKernelGGL(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
+  KK_LAUNCH(np_blocks_kernel, dim3(static_cast<unsigned>(nblk), static_cast<unsigned>(rows)),
                      dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
                      static_cast<int>(nblk), 0, static_cast<float2*>(nullptr), ctx().row_counters,
                      counter_stride(rows), out, mean ? 1 : 0, 0.0f, static_cast<float2*>(nullptr),
@@ -2005,8 +2005,8 @@ static int np_resident_launch(float* out, const float* x, int64_t rows, int64_t 
   hipStream_t st = ctx().stream;
 #define KK_RES_CASE(NBV)                                                                          \
   case NBV:                                                                                       \
-    if (out) hipLaunchKernelGGL((np_resident_kernel<NBV, 0>), grid, dim3(128 * NBV), lds, st, A); \
-    else hipLaunchKernelGGL((np_resident_kernel<NBV, 2>), grid, dim3(128 * NBV), lds, st, A);  \
+    if (out) KK_LAUNCH((np_resident_kernel<NBV, 0>), grid, dim3(128 * NBV), lds, st, A); \
+    else KK_LAUNCH((np_resident_kernel<NBV, 2>), grid, dim3(128 * NBV), lds, st, A);  \
     break;
   switch (nb) {
     KK_RES_CASE(1)
@@ -2032,7 +2032,7 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
   np_tail_plan(static_cast<int>(T % kNpBlock), &tail);
   const float* xp = static_cast<const float*>(x->data);
   if (T <= kNpRowMax) {
-    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
+    KK_LAUNCH(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(T), st, static_cast<float*>(out->data), xp, C,
                        static_cast<int>(T), 2, eps, af, vec_ok ? 1 : 0, static_cast<float2*>(nullptr),
                        static_cast<float2*>(nullptr), tail);
@@ -2054,7 +2054,7 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
   const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
   int rc = KK_OK;
   for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
-    hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
+    KK_LAUNCH(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                        static_cast<int>(nblk), pass, stats, ctx().row_counters,
                        counter_stride(rows), static_cast<float*>(nullptr), 0, eps,
                        static_cast<float2*>(nullptr), static_cast<float2*>(nullptr), int64_t{0},
@@ -2067,7 +2067,7 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
     const int64_t per_block = kRowBlock * (avec ? 4 : 1) * 8;
     const unsigned gx = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(
         ceil_div(T, per_block), 1 << 16)));
-    hipLaunchKernelGGL(instnorm_apply, dim3(gx, static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
+    KK_LAUNCH(instnorm_apply, dim3(gx, static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
                        st, static_cast<float*>(out->data), xp, static_cast<const float2*>(stats), C,
                        T, af, avec ? 1 : 0);
     rc = check_launch("instnorm_apply");
@@ -2133,7 +2133,7 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   const int64_t fgx = std::min<int64_t>(gx, std::max<int64_t>(1, ceil_div(2048, rows)));
   const dim3 fgrid(static_cast<unsigned>(fgx), static_cast<unsigned>(rows));
   auto quant = [&](const int* only_if, int* check) {
-    hipLaunchKernelGGL(instnorm_quant, only_if ? fgrid : qgrid, dim3(kRowBlock), 0, st,
+    KK_LAUNCH(instnorm_quant, only_if ? fgrid : qgrid, dim3(kRowBlock), 0, st,
                        static_cast<uint8_t*>(q->data),
                        xp, static_cast<const float2*>(stats), static_cast<const float2*>(params), C, T,
                        af, vec ? 1 : 0, only_if, check);
@@ -2141,7 +2141,7 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   };
   int rc = KK_OK;
   if (!long_rows) {
-    hipLaunchKernelGGL(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
+    KK_LAUNCH(np_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(kNpThreads),
                        np_row_lds(T), st, static_cast<float*>(nullptr), xp, C, static_cast<int>(T), 3,
                        eps, af, rows_vec ? 1 : 0, stats, mm, tail);
     rc = check_launch("np_rows_kernel");
@@ -2150,7 +2150,7 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   } else {
     const dim3 bgrid(static_cast<unsigned>(nblk), static_cast<unsigned>(rows));
     for (int pass = 0; pass < 2 && rc == KK_OK; ++pass) {
-      hipLaunchKernelGGL(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
+      KK_LAUNCH(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                          static_cast<int>(nblk), pass, stats, ctx().row_counters,
                          counter_stride(rows), static_cast<float*>(nullptr), 0, eps, xmm,
                          pass == 1 ? mm : static_cast<float2*>(nullptr), C, af, tail);
@@ -2160,7 +2160,7 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   if (rc == KK_OK) rc = launch_dql_fold(mm, static_cast<int>(rows), params, ysp, yzp, nullptr, flag);
   if (rc == KK_OK) rc = quant(nullptr, flag);
   if (rc == KK_OK && flag) {  // only if a y fell outside the bounds
-    hipLaunchKernelGGL(instnorm_minmax, fgrid, dim3(kRowBlock), 0, st, mm, xp,
+    KK_LAUNCH(instnorm_minmax, fgrid, dim3(kRowBlock), 0, st, mm, xp,
                        static_cast<const float2*>(stats), C, T, af, vec ? 1 : 0,
                        static_cast<const int*>(flag));
     rc = check_launch("instnorm_minmax");
@@ -2191,11 +2191,11 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
     const float* xp = static_cast<const float*>(x->data);
     hipStream_t st = ctx().stream;
     switch (nv) {
-      case 3: hipLaunchKernelGGL((instnorm_wide_kernel<8, 3>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
-      case 4: hipLaunchKernelGGL((instnorm_wide_kernel<8, 4>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
-      case 5: hipLaunchKernelGGL((instnorm_wide_kernel<8, 5>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
-      case 6: hipLaunchKernelGGL((instnorm_wide_kernel<8, 6>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
-      default: hipLaunchKernelGGL((instnorm_wide_kernel<8, 8>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      case 3: KK_LAUNCH((instnorm_wide_kernel<8, 3>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      case 4: KK_LAUNCH((instnorm_wide_kernel<8, 4>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      case 5: KK_LAUNCH((instnorm_wide_kernel<8, 5>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      case 6: KK_LAUNCH((instnorm_wide_kernel<8, 6>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
+      default: KK_LAUNCH((instnorm_wide_kernel<8, 8>), grid, dim3(512), 0, st, op, xp, C, T, it, eps, sa); break;
     }
     return check_launch("instnorm_wide_kernel");
   }
@@ -2211,10 +2211,10 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
     const int Ti = static_cast<int>(T);  // (T <= 2048 here)
     const float it = 1.0f / static_cast<float>(T);
     switch (nv) {
-      case 5: hipLaunchKernelGGL((adain_row_kernel<5>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
-      case 6: hipLaunchKernelGGL((adain_row_kernel<6>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
-      case 7: hipLaunchKernelGGL((adain_row_kernel<7>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
-      default: hipLaunchKernelGGL((adain_row_kernel<8>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+      case 5: KK_LAUNCH((adain_row_kernel<5>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+      case 6: KK_LAUNCH((adain_row_kernel<6>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+      case 7: KK_LAUNCH((adain_row_kernel<7>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
+      default: KK_LAUNCH((adain_row_kernel<8>), grid, dim3(64), 0, st, op, xp, C, Ti, it, eps, sa); break;
     }
     return check_launch("adain_row_kernel");
   }
@@ -2222,7 +2222,7 @@ static int instnorm_launch(const kk_tensor* out, const kk_tensor* x, float eps, 
     KK_ROW_DISPATCH(instnorm_kernel, rs, rows, static_cast<float*>(out->data),
                     static_cast<const float*>(x->data), rows, C, T, eps, af, sa);
   } else {
-    hipLaunchKernelGGL(instnorm_long_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
+    KK_LAUNCH(instnorm_long_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
                        ctx().stream, static_cast<float*>(out->data),
                        static_cast<const float*>(x->data), C, T, eps, af, sa);
   }
@@ -2431,10 +2431,10 @@ int kk_layernorm(const kk_tensor* out, const kk_tensor* x, const kk_tensor* skip
     hipStream_t st = ctx().stream;
 #define KK_LN_ROW(NVV)                                                                        \
   if (la.bias)                                                                                \
-    hipLaunchKernelGGL((layernorm_row_kernel<NVV, true>), grid, dim3(64), 0, st, op, xp, ci,  \
+    KK_LAUNCH((layernorm_row_kernel<NVV, true>), grid, dim3(64), 0, st, op, xp, ci,  \
                        ic, eps, la.scale, la.bias);                                           \
   else                                                                                        \
-    hipLaunchKernelGGL((layernorm_row_kernel<NVV, false>), grid, dim3(64), 0, st, op, xp, ci, \
+    KK_LAUNCH((layernorm_row_kernel<NVV, false>), grid, dim3(64), 0, st, op, xp, ci, \
                        ic, eps, la.scale, la.bias);
     switch (nv) {
       case 2: KK_LN_ROW(2) break;
@@ -2453,7 +2453,7 @@ int kk_layernorm(const kk_tensor* out, const kk_tensor* x, const kk_tensor* skip
     KK_ROW_DISPATCH(layernorm_kernel, rs, rows, static_cast<float*>(out->data),
                     static_cast<const float*>(x->data), rows, cols, eps, la);
   } else {
-    hipLaunchKernelGGL(layernorm_long_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
+    KK_LAUNCH(layernorm_long_kernel, dim3(static_cast<unsigned>(rows)), dim3(kRowBlock), 0,
                        ctx().stream, static_cast<float*>(out->data),
                        static_cast<const float*>(x->data), cols, eps, la);
   }
@@ -2482,7 +2482,7 @@ int kk_softmax(const kk_tensor* out, const kk_tensor* x, int axis) {
   }
   const int64_t cols = outer * inner;
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(cols, 256), 65535));
-  hipLaunchKernelGGL(softmax_cols_kernel, dim3(grid), dim3(256), 0, ctx().stream,
+  KK_LAUNCH(softmax_cols_kernel, dim3(grid), dim3(256), 0, ctx().stream,
                      static_cast<float*>(out->data), static_cast<const float*>(x->data), outer, dim,
                      inner);
   return check_launch("softmax_cols_kernel");
@@ -2540,7 +2540,7 @@ int kk_reduce(int op, const kk_tensor* out, const kk_tensor* x, uint32_t axes_ma
     return check_launch("reduce_rows_kernel");
   }
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(nout, 256), 65535));
-  hipLaunchKernelGGL(reduce_generic_kernel, dim3(grid), dim3(256), 0, ctx().stream,
+  KK_LAUNCH(reduce_generic_kernel, dim3(grid), dim3(256), 0, ctx().stream,
                      static_cast<float*>(out->data), static_cast<const float*>(x->data), R, op);
   return check_launch("reduce_generic_kernel");
 }

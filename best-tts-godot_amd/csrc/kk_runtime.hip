@@ -470,6 +470,7 @@ int kk_free(void* dptr) {
   // ordered before any later reuse, because every op runs on one stream.
   p.in_pool.insert(dptr);
   p.free_lists[it->second].push_back(dptr);
+  conv_i8_forget_pack(dptr);
   p.pooled_bytes += it->second;
   p.live_bytes -= it->second;
   return KK_OK;
@@ -520,7 +521,7 @@ int kk_upload(void* dst, const void* src, size_t bytes) {
     a.dst = static_cast<uint8_t*>(dst);
     a.n = static_cast<uint32_t>(bytes);
     std::memcpy(a.data, src, bytes);
-    hipLaunchKernelGGL(upload_small_kernel, dim3(1), dim3(256), 0, ctx().stream, a);
+    KK_LAUNCH(upload_small_kernel, dim3(1), dim3(256), 0, ctx().stream, a);
     return check_launch("upload_small_kernel");
   }
   if (bytes <= kStageBytes / 4) return stage_upload(dst, src, bytes);
@@ -584,6 +585,13 @@ int kk_graph_end(int* graph_id) {
     (void)hipGraphDestroy(s.graph);
     return check_hip(e, "hipGraphInstantiate");
   }
+  // Uploaded now, so that the first launch costs what later ones do.
+  e = hipGraphUpload(s.exec, ctx().stream);
+  if (e != hipSuccess) {
+    (void)hipGraphExecDestroy(s.exec);
+    (void)hipGraphDestroy(s.graph);
+    return check_hip(e, "hipGraphUpload");
+  }
   auto& g = graphs();
   for (size_t i = 0; i < g.size(); ++i)
     if (!g[i].exec) { g[i] = s; *graph_id = static_cast<int>(i); return KK_OK; }
@@ -612,6 +620,24 @@ int kk_graph_destroy(int graph_id) {
   (void)hipGraphExecDestroy(g[graph_id].exec);
   (void)hipGraphDestroy(g[graph_id].graph);
   g[graph_id] = GraphSlot();
+  return KK_OK;
+}
+
+int kk_graph_nodes(int graph_id, int64_t* nodes) {
+  KK_TRY(require_ready());
+  auto& g = graphs();
+  if (graph_id < 0 || graph_id >= static_cast<int>(g.size()) || !g[graph_id].exec || !nodes)
+    return set_error(KK_E_ARG, "kk_graph_nodes: no graph %d", graph_id);
+  size_t n = 0;
+  KK_HIP(hipGraphGetNodes(g[graph_id].graph, nullptr, &n));
+  *nodes = static_cast<int64_t>(n);
+  return KK_OK;
+}
+
+int kk_dispatch_count(uint64_t* dispatches) {
+  KK_TRY(require_ready());
+  if (!dispatches) return set_error(KK_E_ARG, "kk_dispatch_count: NULL output");
+  *dispatches = ctx().dispatches;
   return KK_OK;
 }
 

@@ -52,6 +52,13 @@ def pool_stats():
     return tuple(v.value for v in vals)
 
 
+def dispatch_count():
+    """Kernels launched by libkk since init, outside graph recording."""
+    n = ctypes.c_uint64(0)
+    _lib.call("kk_dispatch_count", ctypes.byref(n))
+    return n.value
+
+
 def pool_trim(budget_bytes=0):
     init()
     _lib.call("kk_pool_trim", int(budget_bytes))

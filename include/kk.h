@@ -312,8 +312,10 @@ int kk_conv_integer_pack(const kk_tensor* packed, const kk_tensor* w, const kk_t
  * (resid given) on weights packed by kk_conv_integer_pack from this w and
  * w_zp: the same checks and bit-identical results, without the per-call
  * re-layout (w and w_zp give the shapes and are not read; the caller keeps
- * `packed` in step with them).  The per-call bias quantisation is formed
- * per block with the same operations. */
+ * `packed` in step with their contents).  A `packed` buffer is refused
+ * (KK_E_ARG) unless the last kk_conv_integer_pack into it read this very w
+ * (address, shape, dtype) and w_zp (address, dtype).  The per-call bias
+ * quantisation is formed per block with the same operations. */
 int kk_conv_integer_scaled_qbias_packed(const kk_tensor* out, const kk_tensor* x,
                                         const kk_tensor* w, const kk_tensor* packed,
                                         const kk_tensor* x_zp, const kk_tensor* w_zp,
@@ -410,6 +412,15 @@ int kk_graph_begin(void);
 int kk_graph_end(int* graph_id);
 int kk_graph_launch(int graph_id);
 int kk_graph_destroy(int graph_id);
+/* Nodes of a recorded graph (every kernel an op recorded is one node). */
+int kk_graph_nodes(int graph_id, int64_t* nodes);
+
+/* ---------------------------------------------------------- dispatches
+ * Kernels the library has launched since kk_init, outside graph recording
+ * (a graph replay's kernels are not counted here) -- the counterpart of
+ * the reference executor's per-run dispatch count
+ * (addons/best-tts/runtime/executor.gd:65, 303, 356). */
+int kk_dispatch_count(uint64_t* dispatches);
 
 #ifdef __cplusplus
 }
