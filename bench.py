@@ -389,11 +389,17 @@ def run_gpu(args):
         sc = D(np.array(0.005, np.float32))
         lout = L + 2 * pad - dil * (k - 1)
         o = [kk.DeviceTensor.empty((1, cout, lout)) for _ in range(4)]
-        # eager: the fp16 matrix-core path rearranges the weights into a
-        # workspace, which graph capture does not allow
-        per_op(name, lambda i: B.call("kk_conv1d", o[i].desc(), x[i].desc(), wq.desc(), sc.desc(),
-                                      None, None, 1, dil, pad, pad, 1),
-               flops=2 * cout * cin * k * lout, sets=4, eager=True, mfma="f16x2")
+        # the constant weights laid out once for the matrix cores, as the
+        # graph does at load (kk_conv_pack); then one launch a call
+        pk = kk.ops.conv_pack(wq, None, False, 1)
+        rec = per_op(name, lambda i: B.call("kk_conv1d_packed", o[i].desc(), x[i].desc(), wq.desc(),
+                                            pk.desc(), sc.desc(), None, None, 1, dil, pad, pad),
+                     flops=2 * cout * cin * k * lout, sets=4, mfma="f16x2")
+        # the per-call form (kk_conv1d): the layout made for every call
+        fe = lambda i: B.call("kk_conv1d", o[i].desc(), x[i].desc(), wq.desc(), sc.desc(), None,
+                              None, 1, dil, pad, pad, 1)
+        rec["per_call_us"] = round(B.time_eager(fe, 4, 20) * 1e3, 3)
+        rec["per_call_kernels"] = B.kernels_per_call(fe)
 
     conv_case("conv_i8_512x512_k3_L2400", 512, 512, 3, 2400, 1, 1)
     conv_case("conv_i8_256x256_k3_d1_L2400", 256, 256, 3, 2400, 1, 1)
@@ -414,16 +420,20 @@ def run_gpu(args):
     wt = D(r.integers(-127, 128, (512, 256, 20)).astype(np.int8))
     sct = D(np.array(0.005, np.float32))
     ot = [kk.DeviceTensor.empty((1, 256, 2400)) for _ in range(4)]
-    per_op("convT_i8_512x256_k20_s10", lambda i: B.call(
-        "kk_conv_transpose1d", ot[i].desc(), xt[i].desc(), wt.desc(), sct.desc(), None, None, 10, 1,
-        5, 5, 1, 0), flops=2 * 512 * 256 * 2400 * 20 // 10, sets=4, eager=True, mfma="f16x2")
+    pkt = kk.ops.conv_pack(wt, None, True, 10)
+    rec = per_op("convT_i8_512x256_k20_s10", lambda i: B.call(
+        "kk_conv_transpose1d_packed", ot[i].desc(), xt[i].desc(), wt.desc(), pkt.desc(), sct.desc(),
+        None, None, 10, 5, 5, 0), flops=2 * 512 * 256 * 2400 * 20 // 10, sets=4, mfma="f16x2")
+    fe = lambda i: B.call("kk_conv_transpose1d", ot[i].desc(), xt[i].desc(), wt.desc(), sct.desc(),
+                          None, None, 10, 1, 5, 5, 1, 0)
+    rec["per_call_us"] = round(B.time_eager(fe, 4, 20) * 1e3, 3)
+    rec["per_call_kernels"] = B.kernels_per_call(fe)
 
     # The decoder upsample stage as one chain of 13 ops: int8
     # ConvTranspose1d 512->256 (k20, s10, p5) on [1,512,240], snake, AdaIN
     # (style [1,128], Linear 128->512), then two residual blocks AdaIN ->
     # snake -> int8 Conv1d 256->256 k3 (dilation 1, then 3) -> AdaIN -> snake
-    # -> int8 Conv1d k3 -> + input; per-tensor int8 scales.  Eager: the
-    # convolutions draw workspace from the pool.
+    # -> int8 Conv1d k3 -> + input; per-tensor int8 scales.
     qt4 = D(r.integers(-127, 128, (512, 256, 20)).astype(np.int8))
     st4 = D(np.array(r.uniform(1e-3, 1e-2), np.float32))
     sty4 = D(r.normal(0, 0.1, (1, 128)).astype(np.float32))
@@ -432,26 +442,61 @@ def run_gpu(args):
     cv4 = [(D(r.integers(-127, 128, (256, 256, 3)).astype(np.int8)),
             D(np.array(r.uniform(1e-3, 1e-2), np.float32))) for _ in range(4)]
     ops_ = kk.ops
+    # the constant conv weights laid out once, as a graph does at load
+    pq4 = ops_.conv_pack(qt4, None, True, 10)
+    pcv4 = [ops_.conv_pack(q, None, False, 1) for q, _s in cv4]
 
     def stage4(i):
-        h = ops_.conv_transpose1d(xt[i], qt4, None, (5, 5), 10, w_scale=st4)
+        h = ops_.conv_transpose1d(xt[i], qt4, None, (5, 5), 10, w_scale=st4, packed=pq4)
         h = ops_.adain(ops_.snake(h, al4[0]), sty4, fc4[0], None, 1e-5)
         for blk, dil in enumerate((1, 3)):
             y = ops_.snake(ops_.adain(h, sty4, fc4[1 + 2 * blk], None, 1e-5), al4[1 + 2 * blk])
             q, s = cv4[2 * blk]
-            y = ops_.conv1d(y, q, None, (dil, dil), 1, dil, w_scale=s)
+            y = ops_.conv1d(y, q, None, (dil, dil), 1, dil, w_scale=s, packed=pcv4[2 * blk])
             y = ops_.snake(ops_.adain(y, sty4, fc4[2 + 2 * blk], None, 1e-5), al4[2 + 2 * blk])
             q, s = cv4[2 * blk + 1]
-            y = ops_.conv1d(y, q, None, (1, 1), w_scale=s)
+            y = ops_.conv1d(y, q, None, (1, 1), w_scale=s, packed=pcv4[2 * blk + 1])
             h = ops_.binary("Add", h, y)
         return h
 
     flops4 = 2 * 512 * 256 * 2400 * 20 // 10 + 4 * 2 * 256 * 256 * 3 * 2400
-    rec = per_op("decoder_upsample_stage_1x512x240", stage4, flops=flops4, sets=4, reps=10,
-                 eager=True)
+    # Recorded: the same 13 launches over buffers allocated beforehand, one
+    # graph per rotating input set (device time, no host dispatch)
+    hb = [[kk.DeviceTensor.empty((1, 256, 2400)) for _ in range(12)] for _ in range(4)]
+
+    def stage4_rec(i):
+        t = hb[i]
+        c = lambda name, *a: B.call(name, *[v.desc() if isinstance(v, kk.DeviceTensor) else v
+                                             for v in a])
+        c("kk_conv_transpose1d_packed", t[0], xt[i], qt4, pq4, st4, None, None, 10, 5, 5, 0)
+        c("kk_snake", t[1], t[0], al4[0], None)
+        c("kk_adain", t[2], t[1], sty4, fc4[0], None, None, None, 1e-5)
+        h, k = t[2], 3
+        for blk, dil in enumerate((1, 3)):
+            c("kk_adain", t[k], h, sty4, fc4[1 + 2 * blk], None, None, None, 1e-5)
+            c("kk_snake", t[k + 1], t[k], al4[1 + 2 * blk], None)
+            q, s = cv4[2 * blk]
+            c("kk_conv1d_packed", t[k + 2], t[k + 1], q, pcv4[2 * blk], s, None, None, 1, dil, dil,
+              dil)
+            c("kk_adain", t[k], t[k + 2], sty4, fc4[2 + 2 * blk], None, None, None, 1e-5)
+            c("kk_snake", t[k + 1], t[k], al4[2 + 2 * blk], None)
+            q, s = cv4[2 * blk + 1]
+            c("kk_conv1d_packed", t[k + 2], t[k + 1], q, pcv4[2 * blk + 1], s, None, None, 1, 1, 1,
+              1)
+            c("kk_binary", opc["Add"], t[k + 3], h, t[k + 2])
+            h, k = t[k + 3], k + 4
+        return h
+
+    rec = per_op("decoder_upsample_stage_1x512x240", stage4_rec, flops=flops4, sets=4, reps=10)
     rec["ops"] = 13
     rec["workload"] = ("int8 ConvT 512->256 k20 s10 + snake + AdaIN, then 2 residual blocks "
-                       "(AdaIN, snake, int8 Conv1d 256 k3 d1/d3, AdaIN, snake, Conv1d k3, Add)")
+                       "(AdaIN, snake, int8 Conv1d 256 k3 d1/d3, AdaIN, snake, Conv1d k3, Add); "
+                       "weights packed at load")
+    got = hb[0][10].numpy()  # the second block's sum
+    want = stage4(0).numpy()  # the same chain through the op wrappers, eagerly
+    if not np.array_equal(got, want):
+        raise RuntimeError("bench: the recorded decoder stage differs from the eager one")
+    rec["eager_us"] = round(B.time_eager(stage4, 4, 10) * 1e3, 3)
 
     # The output stage at the 128-id waveform's length (~2.15M samples): the
     # 1023-tap notch FIR (fp32 FMAs: 2 * 1023 flops per sample), the PCM16

@@ -80,6 +80,11 @@ PROTOTYPES = {
     "kk_gemm": [_T, _T, _T, _T, _T, _f],
     "kk_conv1d": [_T, _T, _T, _T, _T, _T, _i, _i, _i, _i, _i],
     "kk_conv_transpose1d": [_T, _T, _T, _T, _T, _T, _i, _i, _i, _i, _i, _i],
+    "kk_conv_packed_bytes": [_i, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i,
+                             ctypes.POINTER(ctypes.c_int64)],
+    "kk_conv_pack": [_T, _T, _T, _i, _i],
+    "kk_conv1d_packed": [_T] * 7 + [_i, _i, _i, _i],
+    "kk_conv_transpose1d_packed": [_T] * 7 + [_i, _i, _i, _i],
     "kk_event_record": [_i],
     "kk_event_elapsed": [_i, _i, ctypes.POINTER(_f)],
     "kk_dynamic_quantize_linear": [_T, _T, _T, _T],

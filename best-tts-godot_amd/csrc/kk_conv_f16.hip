@@ -1,42 +1,61 @@
 // Conv1d and ConvTranspose1d with fp16 or 8-bit weights on the fp16 matrix
-// cores, fp32 results.
+// cores (v_mfma_f32_32x32x16_f16), fp32 results, in one launch.
 //
-// An fp16 weight is exact in fp16, and so is an 8-bit weight less its zero
-// point (|q - zp| <= 255); the 8-bit weights' scale, per tensor or per
-// output channel, multiplies the fp32 sum (sum (q - zp) s x = s sum (q - zp) x,
-// the same value up to fp32 rounding).  A first pass forms m = max |x| over
-// the input; every activation is then scaled by 2^k, the power of two that
-// puts m in [2^14, 2^15) (exact in fp32), and the scaled y = x 2^k is split
-// into hi = fp16(y) and lo = fp16(y - hi) (y - hi is exact in fp32).  For
-// |y| >= 2^-3 lo is a normal fp16 number and hi + lo equals y to within
-// 2^-22 |y|; below that (|x| < m 2^-17) the error is at most 2^-25 in
-// scaled units, m 2^-39 or less.  Every product w*hi and w*lo is exact in
-// fp32 (11 + 11 significant bits), v_mfma_f32_32x32x16_f16 accumulates them
-// in fp32, and the sum is scaled back by 2^-k (exact): the accuracy of fp32
-// products accumulated in fp32, at the fp16 matrix rate, whatever the
-// activations' magnitude.  A non-finite activation (m inf or NaN) sets a
-// flag instead; the fp32 kernels, launched after this one with that flag as
-// their condition, then compute the convolution.
+// Exact operands.  An fp16 weight is exact in fp16, and so is an 8-bit
+// weight less its zero point (|q - zp| <= 255); the 8-bit weights' scale,
+// per tensor or per output channel, multiplies the fp32 sum
+// (sum (q - zp) s x = s sum (q - zp) x up to fp32 rounding).  Every output
+// column (time step) scales its activations by its own power of two, 2^k,
+// chosen from the largest |x| its receptive field has shown so far: with m
+// that maximum, m 2^k first lies in [2^10, 2^11) (exact in fp32), and a
+// scaled y = x 2^k is split into hi = fp16(y) and lo = fp16(y - hi) (y - hi
+// is exact in fp32).  For |y| >= 2^-3 lo is a normal fp16 number and hi + lo
+// equals y to within 2^-22 |y|; below that the error is at most 2^-25 in
+// scaled units, m 2^-35 or less.  Every product w hi and w lo is exact in
+// fp32 (11 + 11 significant bits) and the matrix cores accumulate them in
+// fp32.  Only when a column's maximum grows past 2^15 in scaled units (a
+// value 16 to 32 times the first maximum) does its k fall afresh; its
+// accumulators (all in the lanes that hold that column) are then multiplied
+// by 2^(k_new - k_old), exact for a power of two.  The sums are scaled back
+// by 2^-k at the end.  A column whose receptive field holds an infinity or
+// a NaN is recomputed with scalar fp32 products and sums, which give numpy's
+// inf / NaN pattern.
 //
-// Both operations are one implicit GEMM with rows m = co*P + r (output
-// channel co, phase r < P):
-//   out[co, q*os + r + ophase0] = sum_kk Wt[m][kk] * x[ci, q*qs + t*tap_mul + tap_add]
-// with kk = t*Cin + ci (tap-major, so a K-step of 32 has one tap t).
-//   Conv1d (P = 1): t = the tap k, qs = stride, tap_mul = dilation,
-//     tap_add = -pad0, os = 1, ophase0 = 0; Wt[co][k*Cin + ci] = W[co][ci][k].
-//   ConvTranspose1d, P = stride phases (dilation 1): t = m, x[ci, q - m],
-//     qs = 1, tap_mul = -1, tap_add = 0, os = stride, ophase0 = -pad0;
-//     Wt[co*P + r][m*Cin + ci] = W[ci][co][r + stride*m] (0 past the kernel).
-//     A block's rows hold every phase of its output channels, so its
-//     stores fill whole lines of the interleaved output in its L2.
-// A call rearranges W into Wt (fp16, less the zero point) first, in the
-// library context's scratch (a pooled workspace when larger), so each K-step
-// loads its weight rows as vectors.  A Wt beyond the scratch while a graph
-// is being recorded (nothing may be allocated then) is not stored: the
-// kernel gathers the same fp16 values from W itself (slower, the same
-// results bit for bit).  The non-finite flag and m are slots of the library
-// context, cleared at the start of each call.
+// Both operations are one implicit GEMM with rows m = co P + r (output
+// channel co, phase r < P) and columns q, the reduction index k running over
+// (input channel ci, tap t') with TP in {2, 4, 8} taps a channel (T taps
+// used, the rest weigh 0):
+//   out[co, q os + r + oph] = sum_ci sum_t' Wv[m][ci][t'] x[ci, q qs + ta + t' tm]
+//   Conv1d (P = 1): t' = the tap, qs = stride, ta = -pad0, tm = dilation,
+//     os = 1, oph = 0, Wv[co][ci][t'] = W[co][ci][t'].
+//   ConvTranspose1d (dilation 1), P = stride phases, T = ceil(K / P) taps a
+//     phase, read in increasing position: x[ci, q - (T - 1) + t'] (qs = 1,
+//     ta = 1 - T, tm = 1), os = stride, oph = -pad0,
+//     Wv[co P + r][ci][t'] = W[ci][co][r + P (T - 1 - t')] (0 past K).
+// A 16-deep reduction slice s holds channels 16 s / TP .. + 16 / TP - 1, each
+// with its TP taps, so a lane's eight operand values of a slice are TP
+// consecutive taps of 8 / TP channels: for Conv1d with dilation 1 and for
+// ConvTranspose1d, consecutive x positions of each channel.
+//
+// Packed weights (kk_conv_pack, or per call into the context scratch): fp16
+// values (W less its zero point) in the matrix cores' operand order: the
+// 16-byte unit (mt KS + s) 64 + l holds lane l's operand of slice s for rows
+// 32 mt .. 32 mt + 31: row 32 mt + l % 32, k = 8 (l / 32) + 0..7 (KS slices;
+// zeros past M, past Cin and past T).
+//
+// A block owns 32 MI rows x 32 WN columns; its 4 waves are WN (columns) x
+// WK (reduction ranges).  A wave holds MI 32 x 32 accumulator tiles of its
+// 32 columns: lane (n, g) = (lane % 32, lane / 32) loads its column's eight
+// x values of a slice straight from memory (bounds-checked buffer loads: 0
+// outside the signal, past Cin and past T), the two lanes of a column agree
+// on its scale (one lane swap), and split, and the weights' operands come
+// as 1 KB fragments; both run three slices ahead in a register ring, with
+// no LDS and no barrier in the reduction loop.  The WK waves of a column
+// range add their unscaled partial tiles through LDS in wave order.
 #include <algorithm>
+#include <climits>
+#include <mutex>
+#include <unordered_map>
 
 #include "kk_internal.h"
 
@@ -44,671 +63,569 @@ namespace kk {
 namespace convh {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
-#ifndef KK_CONVH_BK
-#define KK_CONVH_BK 32
-#endif
-constexpr int kBK = KK_CONVH_BK;  // K-step (halves)
-constexpr int kPitch = kBK + 8;  // LDS row pitch (halves): 80 bytes
 constexpr int kThreads = 256;
 
-struct HArgs {
-  const _Float16* wt;  // [M][Kg] when rearranged, else NULL
-  const void* w;       // conv [Cout][Cin][Kw], transposed [Cin][Cout][Kw]
+// Taps a channel spans in the reduction order: T rounded up to 2, 4 or 8 (0:
+// more than 8 taps, which this path does not take).
+static int taps_padded(int64_t T) { return T <= 2 ? 2 : T <= 4 ? 4 : T <= 8 ? 8 : 0; }
+
+// The packed geometry: what a pack and a convolution must agree on.
+struct Geo {
   int transposed;
-  int64_t Kw, s;       // kernel taps, stride (the phase count P for transposed)
-  Dequant dq;          // 8-bit weights: zero point subtracted, scale applied to the sums
-  const float* x;      // [N, Cin, L]
-  float* out;          // [N, Cout, Lout]
-  const float* bias;   // [Cout] or NULL
-  int* flag;           // set: an activation is not finite
-  unsigned* xmax;      // bits of max |x| (a non-negative float, so ordered as unsigned)
-  int64_t Cin, L, M, Cout, Kg, Nq, Lout;
-  int64_t qs, tap_mul, tap_add, os, ophase0;
-  int P;
-  // split-K (ring kernel): blockIdx.z = batch * ksplit + split; each split
-  // sums its share of the K-steps into part[(b * ksplit + split) * M + m][q]
-  // (raw, in the activations' scaled units), NULL for the direct epilogue
-  int ksplit;
-  float* part;
-  int64_t Mp;  // rows of the rearranged weights: M rounded up to 128 (zeros past M)
+  int64_t Cin, Cout, Kw, P;  // P: phases (the stride) of a transposed conv, else 1
+  int64_t T, TP;             // taps a row reads; taps a channel spans (0: unsupported)
+  int64_t M, MT, KS;         // rows, 32-row tiles, 16-deep slices
+  int64_t bytes;             // packed size
 };
 
-// WAVES_M x (4 / WAVES_M) wavefronts, each owning WM_T x WN_T tiles of 32x32.
-template <int WAVES_M_, int WM_T_, int WN_T_>
-struct Tile {
-  static constexpr int WAVES_M = WAVES_M_, WM_T = WM_T_, WN_T = WN_T_;
-  static constexpr int WAVES_N = 4 / WAVES_M;
-  static constexpr int BM = WAVES_M * 32 * WM_T, BN = WAVES_N * 32 * WN_T;
-  // A staging: thread -> row t % BM, KPT consecutive k from KPT * (t / BM)
-  static constexpr int KPT = BM * kBK / kThreads;
-  static_assert(kThreads % BM == 0 && KPT % 4 == 0, "A staging shape");
-  // B staging: thread -> column n = t % BN, k pairs t / BN + j * (256 / BN)
-  static constexpr int KP_STEP = kThreads / BN;
-  static constexpr int B_PAIRS = (kBK / 2) / KP_STEP;
-  static_assert(kThreads % BN == 0 && (kBK / 2) % KP_STEP == 0, "B staging shape");
+static Geo geometry(bool transposed, int64_t Cin, int64_t Cout, int64_t Kw, int64_t stride) {
+  Geo g{};
+  g.transposed = transposed ? 1 : 0;
+  g.Cin = Cin; g.Cout = Cout; g.Kw = Kw;
+  g.P = transposed ? stride : 1;
+  g.T = transposed ? ceil_div(Kw, stride) : Kw;
+  g.TP = taps_padded(g.T);
+  g.M = g.P * Cout;
+  g.MT = ceil_div(g.M, 32);
+  g.KS = g.TP ? ceil_div(Cin * g.TP, 16) : 0;
+  g.bytes = g.MT * g.KS * 1024;
+  return g;
+}
+
+struct PackArgs {
+  uint4* wp;
+  const void* w;   // conv [Cout][Cin][Kw], transposed [Cin][Cout][Kw]
+  const void* zp;  // 8-bit weights' zero point (1 or Cout values) or NULL
+  int zp_dt;
+  int zp_stride;
+  int Cin, Cout, Kw, P, T, TP, M, KS;
+  int transposed;
+  int64_t units;
 };
 
-// The power of two k with m 2^k in [2^14, 2^15) for m = max |x| > 0 (0 for
-// m = 0), kept within [-120, 120] so that 2^k and 2^-k are normal floats.
-__device__ __forceinline__ int convh_scale_exp(unsigned mbits) {
-  if (mbits == 0) return 0;
-  const int e = static_cast<int>(mbits >> 23) - 127;  // floor(log2 m); -127 for subnormal m
-  return min(120, 14 - e);
-}
-
-// PRE: the weights come rearranged in A.wt; else gathered from A.w.
-template <class T, typename TW, bool PRE>
-__global__ void __launch_bounds__(kThreads) convh_kernel(HArgs A) {
-  __shared__ __align__(16) _Float16 As[2][T::BM * kPitch];
-  __shared__ __align__(16) _Float16 Bh[2][T::BN * kPitch];
-  __shared__ __align__(16) _Float16 Bl[2][T::BN * kPitch];
-  constexpr int WM_T = T::WM_T, WN_T = T::WN_T;
-  const unsigned mbits = *A.xmax;
-  if (mbits >= 0x7f800000u) {  // an infinite or NaN activation: the fp32 kernels compute it
-    if (threadIdx.x == 0) *A.flag = 1;  // every writer stores the same 1
-    return;
-  }
-  const int kexp = convh_scale_exp(mbits);
-  const float xscale = ldexpf(1.0f, kexp), unscale = ldexpf(1.0f, -kexp);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m_w = (wave / T::WAVES_N) * 32 * WM_T, n_w = (wave % T::WAVES_N) * 32 * WN_T;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * T::BN;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * T::BM;
-  const int64_t b = blockIdx.z;
-  const float* xb = A.x + b * A.Cin * A.L;
-  const int64_t nk = A.Kg / kBK;
-  const TW* w = static_cast<const TW*>(A.w);
-
-  // this thread's A row: m = co*P + r, and its weights' zero point
-  const int am = tid % T::BM, ak = T::KPT * (tid / T::BM);
-  const int64_t m_row = m0 + am;
-  const int64_t a_co = m_row / A.P, a_r = m_row - a_co * A.P;
-  const bool a_in = m_row < A.M;
-  const float a_zp = A.dq.zp && a_in ? load_as_f32(A.dq.zp, A.dq.zp_dt, a_co * A.dq.zp_stride) : 0.0f;
-  const int64_t cout = A.M / A.P;
-  // step between consecutive ci in W
-  const int64_t w_ci = A.transposed ? cout * A.Kw : A.Kw;
-
-  // staging registers
-  _Float16 av[T::KPT];
-  float bv[T::B_PAIRS][2];
-  const int bn = tid % T::BN;
-  const int64_t q = n0 + bn;
-  auto fetch = [&](int64_t k0) {
-    const int64_t t = k0 / A.Cin, ci0 = k0 - t * A.Cin;
-    if constexpr (PRE) {
-      typedef _Float16 h4v __attribute__((ext_vector_type(4)));
-#pragma unroll
-      for (int e = 0; e < T::KPT; e += 4) {
-        h4v v = {};
-        if (a_in) v = *reinterpret_cast<const h4v*>(A.wt + m_row * A.Kg + k0 + ak + e);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) av[e + u] = v[u];
-      }
-    } else {
-      // W[co][ci][t] (conv) or W[ci][co][r + s*t] (transposed, 0 past the kernel)
-      const int64_t tap = A.transposed ? a_r + A.s * t : t;
-      const bool tap_in = a_in && tap < A.Kw;
-      const int64_t wbase = A.transposed ? ((ci0 + ak) * cout + a_co) * A.Kw + tap
-                                         : (a_co * A.Cin + ci0 + ak) * A.Kw + tap;
-#pragma unroll
-      for (int e = 0; e < T::KPT; ++e) {
-        float v = 0.0f;
-        if (tap_in) v = static_cast<float>(w[wbase + e * w_ci]) - a_zp;
-        av[e] = static_cast<_Float16>(v);
-      }
-    }
-    const int64_t pos = q * A.qs + t * A.tap_mul + A.tap_add;
-    const bool in = q < A.Nq && pos >= 0 && pos < A.L;
-#pragma unroll
-    for (int j = 0; j < T::B_PAIRS; ++j) {
-      const int kp = tid / T::BN + j * T::KP_STEP;
-      const float* xr = xb + (ci0 + 2 * kp) * A.L + pos;
-      bv[j][0] = in ? xr[0] : 0.0f;
-      bv[j][1] = in ? xr[A.L] : 0.0f;
-    }
-  };
-  auto stash = [&](int buf) {
-#pragma unroll
-    for (int e = 0; e < T::KPT; e += 4) {
-      typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<h4*>(&As[buf][am * kPitch + ak + e]) =
-          h4{av[e], av[e + 1], av[e + 2], av[e + 3]};
-    }
-#pragma unroll
-    for (int j = 0; j < T::B_PAIRS; ++j) {
-      const int kp = tid / T::BN + j * T::KP_STEP;
-      h2 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float v = bv[j][e] * xscale;  // |v| < 2^15: exact
-        const _Float16 h = static_cast<_Float16>(v);
-        hi[e] = h;
-        lo[e] = static_cast<_Float16>(v - static_cast<float>(h));
-      }
-      *reinterpret_cast<h2*>(&Bh[buf][bn * kPitch + 2 * kp]) = hi;
-      *reinterpret_cast<h2*>(&Bl[buf][bn * kPitch + 2 * kp]) = lo;
-    }
-  };
-
-  f16v acc[WM_T][WN_T];
-#pragma unroll
-  for (int i = 0; i < WM_T; ++i)
-#pragma unroll
-    for (int j = 0; j < WN_T; ++j)
-#pragma unroll
-      for (int g = 0; g < 16; ++g) acc[i][j][g] = 0.0f;
-
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int buf = static_cast<int>(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) fetch((kt + 1) * kBK);
-#pragma unroll
-    for (int ks = 0; ks < kBK; ks += 16) {
-      const int kofs = ks + 8 * (lane >> 5);
-      h8 a[WM_T], bh[WN_T], bl[WN_T];
-#pragma unroll
-      for (int i = 0; i < WM_T; ++i)
-        a[i] = *reinterpret_cast<const h8*>(&As[buf][(m_w + 32 * i + (lane & 31)) * kPitch + kofs]);
-#pragma unroll
-      for (int j = 0; j < WN_T; ++j) {
-        bh[j] = *reinterpret_cast<const h8*>(&Bh[buf][(n_w + 32 * j + (lane & 31)) * kPitch + kofs]);
-        bl[j] = *reinterpret_cast<const h8*>(&Bl[buf][(n_w + 32 * j + (lane & 31)) * kPitch + kofs]);
-      }
-#pragma unroll
-      for (int i = 0; i < WM_T; ++i)
-#pragma unroll
-        for (int j = 0; j < WN_T; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], acc[i][j], 0, 0, 0);
-        }
-    }
-    if (more) stash(buf ^ 1);
-    __syncthreads();
-  }
-  // D(i, j) of a 32x32 tile: lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
-  float* ob = A.out + b * A.Cout * A.Lout;
-#pragma unroll
-  for (int i = 0; i < WM_T; ++i)
-#pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const int64_t m = m0 + m_w + 32 * i + 8 * (g / 4) + 4 * (lane >> 5) + (g % 4);
-      if (m >= A.M) continue;
-      const int64_t co = m / A.P, r = m - co * A.P;
-      const float bias = A.bias ? A.bias[co] : 0.0f;
-      const float sc = A.dq.scale ? load_as_f32(A.dq.scale, A.dq.scale_dt, co * A.dq.scale_stride)
-                                  : 1.0f;
-#pragma unroll
-      for (int j = 0; j < WN_T; ++j) {
-        const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
-        const float u = acc[i][j][g] * unscale;  // exact: a power of two
-        const float v = A.dq.scale ? u * sc : u;
-        const int64_t pos = qq * A.os + r + A.ophase0;
-        if (qq < A.Nq && pos >= 0 && pos < A.Lout) ob[co * A.Lout + pos] = A.bias ? v + bias : v;
-      }
-    }
-}
-
-// The same GEMM over rearranged weights with three K-steps of loads in
-// flight: step kt issues the loads of step kt + 3 into the register slot
-// that step kt's data has just left, computes step kt from LDS, then moves
-// step kt + 1's registers into the other LDS buffer.  With one step of
-// prefetch each of the 48 K-steps of Conv1d 512->512 k3 waited a whole
-// memory round trip (about one wave per SIMD to cover it).  Buffer loads
-// return zeros past the weight rows and, with the offset pushed out of
-// range, at padding and past the output positions, so every step issues
-// the same loads and the wait counts are exact; the last steps re-load
-// the final K-step (unused).  Needs M Kg 2 and Cin L 4 below 2^31.
-template <class T>
-__global__ void __launch_bounds__(kThreads) convh_ring_kernel(HArgs A) {
-  __shared__ __align__(16) _Float16 As[2][T::BM * kPitch];
-  __shared__ __align__(16) _Float16 Bh[2][T::BN * kPitch];
-  __shared__ __align__(16) _Float16 Bl[2][T::BN * kPitch];
-  constexpr int WM_T = T::WM_T, WN_T = T::WN_T, BP = T::B_PAIRS;
-  // A: a step's BM x 32 weight tile is BM * 4 16-byte pieces in a row;
-  // thread t takes pieces t and t + 256 (as many as there are)
-  constexpr int NPC = T::BM * 4, APT = (NPC + kThreads - 1) / kThreads;
-  const unsigned mbits = *A.xmax;
-  if (mbits >= 0x7f800000u) {  // an infinite or NaN activation: the fp32 kernels compute it
-    if (threadIdx.x == 0) *A.flag = 1;  // every writer stores the same 1
-    return;
-  }
-  const int kexp = convh_scale_exp(mbits);
-  const float xscale = ldexpf(1.0f, kexp), unscale = ldexpf(1.0f, -kexp);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m_w = (wave / T::WAVES_N) * 32 * WM_T, n_w = (wave % T::WAVES_N) * 32 * WN_T;
-  const uint3 tile = xcd_tile();  // neighbouring time tiles on one XCD
-  const int64_t n0 = static_cast<int64_t>(tile.x) * T::BN;
-  const int64_t m0 = static_cast<int64_t>(tile.y) * T::BM;
-  const int64_t b = tile.z / A.ksplit;
-  const int split = static_cast<int>(tile.z - b * A.ksplit);
-  const int nk_all = static_cast<int>(A.Kg / kBK);
-  const int kt0 = static_cast<int>(static_cast<int64_t>(nk_all) * split / A.ksplit);
-  const int nk = static_cast<int>(static_cast<int64_t>(nk_all) * (split + 1) / A.ksplit) - kt0;
-  const int Cin = static_cast<int>(A.Cin), L = static_cast<int>(A.L);
-  const auto wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(A.wt), 0,
-                                                     static_cast<int>(A.Kg * A.Mp * 2), 0x00020000);
-  const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A.x + b * A.Cin * A.L), 0,
-                                                     static_cast<int>(A.Cin * A.L * 4), 0x00020000);
-  const int bn = tid % T::BN;
-  const int64_t q = n0 + bn;
-  const int q_pos = static_cast<int>(q * A.qs + A.tap_add);
-  const bool q_in = q < A.Nq;
-  struct Slot {
-    uint4 a[APT];
-    float b[BP][2];
-  };
-  Slot ring[3];
-  // the next K-step to fetch (k0, its tap t and first channel ci0), moved
-  // on after each fetch and held at the split's last step (the final
-  // fetches repeat it): no division per step
-  int f_k0 = kt0 * kBK, f_t = f_k0 / Cin, f_ci0 = f_k0 - f_t * Cin;
-  const int k_last = (kt0 + nk - 1) * kBK;
-  auto fetch = [&](Slot& sl) {
-    const int k0 = f_k0, t = f_t, ci0 = f_ci0;
-    if (f_k0 < k_last) {
-      f_k0 += kBK;
-      f_ci0 += kBK;
-      if (f_ci0 >= Cin) {
-        f_ci0 -= Cin;
-        ++f_t;
-      }
-    }
-    // the step's weight tile: Wt rows m0 .. m0+BM-1 of step k0 / 32, one
-    // contiguous stretch (the old row-major Wt gave every lane of a load its
-    // own cache line)
-    const uint32_t ao = static_cast<uint32_t>(((k0 / kBK) * A.Mp + m0) * 64);
-#pragma unroll
-    for (int e = 0; e < APT; ++e) {
-      const int pc = tid + kThreads * e;
-      uint32_t off = pc < NPC ? ao + 16u * pc : 0x80000000u;
-      asm volatile("" : "+v"(off));
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
-      sl.a[e] = make_uint4(v[0], v[1], v[2], v[3]);
-    }
-    const int pos = q_pos + t * static_cast<int>(A.tap_mul);
-    const bool in = q_in && pos >= 0 && pos < L;
-#pragma unroll
-    for (int j = 0; j < BP; ++j) {
-      const int kp = tid / T::BN + j * T::KP_STEP;
-      uint32_t off = in ? static_cast<uint32_t>((ci0 + 2 * kp) * L + pos) * 4u : 0x80000000u;
-      // the offset held in a register: without it the compiler turned the
-      // select into a branch around each load, and the waits then covered
-      // every load in flight
-      asm volatile("" : "+v"(off));
-      sl.b[j][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, off, 0, 0));
-      // (past the buffer stays past it: its size is below 2^31)
-      sl.b[j][1] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, off + 4u * L, 0, 0));
-    }
-  };
-  auto stash = [&](const Slot& sl, int buf) {
-#pragma unroll
-    for (int e = 0; e < APT; ++e) {
-      const int pc = tid + kThreads * e;  // row pc / 4, halves 8 (pc % 4)
-      if (pc < NPC) *reinterpret_cast<uint4*>(&As[buf][(pc >> 2) * kPitch + 8 * (pc & 3)]) = sl.a[e];
-    }
-#pragma unroll
-    for (int j = 0; j < BP; ++j) {
-      const int kp = tid / T::BN + j * T::KP_STEP;
-      h2 hi, lo;
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float v = sl.b[j][e] * xscale;  // |v| < 2^15: exact
-        const _Float16 h = static_cast<_Float16>(v);
-        hi[e] = h;
-        lo[e] = static_cast<_Float16>(v - static_cast<float>(h));
-      }
-      *reinterpret_cast<h2*>(&Bh[buf][bn * kPitch + 2 * kp]) = hi;
-      *reinterpret_cast<h2*>(&Bl[buf][bn * kPitch + 2 * kp]) = lo;
-    }
-  };
-
-  f16v acc[WM_T][WN_T];
-#pragma unroll
-  for (int i = 0; i < WM_T; ++i)
-#pragma unroll
-    for (int j = 0; j < WN_T; ++j)
-#pragma unroll
-      for (int g = 0; g < 16; ++g) acc[i][j][g] = 0.0f;
-
-  fetch(ring[0]);
-  fetch(ring[1]);
-  fetch(ring[2]);
-  stash(ring[0], 0);
-  __syncthreads();
-  auto step = [&](auto sc, int kt) {
-    constexpr int S = decltype(sc)::value;  // kt % 3
-    fetch(ring[S]);  // step min(kt + 3, nk - 1)
-    const int buf = kt & 1;
-#pragma unroll
-    for (int ks = 0; ks < kBK; ks += 16) {
-      const int kofs = ks + 8 * (lane >> 5);
-      h8 a[WM_T], bh[WN_T], bl[WN_T];
-#pragma unroll
-      for (int i = 0; i < WM_T; ++i)
-        a[i] = *reinterpret_cast<const h8*>(&As[buf][(m_w + 32 * i + (lane & 31)) * kPitch + kofs]);
-#pragma unroll
-      for (int j = 0; j < WN_T; ++j) {
-        bh[j] = *reinterpret_cast<const h8*>(&Bh[buf][(n_w + 32 * j + (lane & 31)) * kPitch + kofs]);
-        bl[j] = *reinterpret_cast<const h8*>(&Bl[buf][(n_w + 32 * j + (lane & 31)) * kPitch + kofs]);
-      }
-#pragma unroll
-      for (int i = 0; i < WM_T; ++i)
-#pragma unroll
-        for (int j = 0; j < WN_T; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bh[j], acc[i][j], 0, 0, 0);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl[j], acc[i][j], 0, 0, 0);
-        }
-    }
-    if (kt + 1 < nk) stash(ring[(S + 1) % 3], buf ^ 1);
-    __syncthreads();
-  };
-  // whole rounds of three steps, then the rest: an early exit between the
-  // steps of a round put a wait for every load at the loop's head
-  const int nr = nk / 3;
-  for (int r = 0; r < nr; ++r) {
-    step(std::integral_constant<int, 0>{}, 3 * r);
-    step(std::integral_constant<int, 1>{}, 3 * r + 1);
-    step(std::integral_constant<int, 2>{}, 3 * r + 2);
-  }
-  if (3 * nr < nk) step(std::integral_constant<int, 0>{}, 3 * nr);
-  if (3 * nr + 1 < nk) step(std::integral_constant<int, 1>{}, 3 * nr + 1);
-
-  // D(i, j) of a 32x32 tile: lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
-  if (A.part) {  // this split's raw sums
-    float* pb = A.part + (b * A.ksplit + split) * A.M * A.Nq;
-#pragma unroll
-    for (int i = 0; i < WM_T; ++i)
-#pragma unroll
-      for (int g = 0; g < 16; ++g) {
-        const int64_t m = m0 + m_w + 32 * i + 8 * (g / 4) + 4 * (lane >> 5) + (g % 4);
-        if (m >= A.M) continue;
-#pragma unroll
-        for (int j = 0; j < WN_T; ++j) {
-          const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
-          if (qq < A.Nq) pb[m * A.Nq + qq] = acc[i][j][g];
-        }
-      }
-    return;
-  }
-  float* ob = A.out + b * A.Cout * A.Lout;
-#pragma unroll
-  for (int i = 0; i < WM_T; ++i)
-#pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const int64_t m = m0 + m_w + 32 * i + 8 * (g / 4) + 4 * (lane >> 5) + (g % 4);
-      if (m >= A.M) continue;
-      const int64_t co = m / A.P, r = m - co * A.P;
-      const float bias = A.bias ? A.bias[co] : 0.0f;
-      const float sc = A.dq.scale ? load_as_f32(A.dq.scale, A.dq.scale_dt, co * A.dq.scale_stride)
-                                  : 1.0f;
-#pragma unroll
-      for (int j = 0; j < WN_T; ++j) {
-        const int64_t qq = n0 + n_w + 32 * j + (lane & 31);
-        const float u = acc[i][j][g] * unscale;  // exact: a power of two
-        const float v = A.dq.scale ? u * sc : u;
-        const int64_t pos = qq * A.os + r + A.ophase0;
-        if (qq < A.Nq && pos >= 0 && pos < A.Lout) ob[co * A.Lout + pos] = A.bias ? v + bias : v;
-      }
-    }
-}
-
-// Split-K's finish: out[b, co, pos] = the splits' sums at (m, q) added in
-// split order, then the epilogue above, where pos - ophase0 = q P + r and
-// m = co P + r (P = os: one phase per output position).  A thread per
-// output position (blocks along the row on x, channels on y, batch on z),
-// so the stores run along each output row; 32-bit indexes (the host keeps
-// M Nq and Cout Lout below 2^31).  Nothing to do after a non-finite
-// activation (the fp32 kernels compute the convolution).
-__global__ void __launch_bounds__(256) convh_splitk_finish(HArgs A) {
-  const unsigned mbits = *A.xmax;
-  if (mbits >= 0x7f800000u) return;
-  const float unscale = ldexpf(1.0f, -convh_scale_exp(mbits));
-  const int P = A.P, Nq = static_cast<int>(A.Nq), Lout = static_cast<int>(A.Lout);
-  const int MN = static_cast<int>(A.M * A.Nq), ks = A.ksplit, ph0 = static_cast<int>(A.ophase0);
-  const int b = blockIdx.z;
-  for (int co = blockIdx.y; co < static_cast<int>(A.Cout); co += gridDim.y) {
-    const float bias = A.bias ? A.bias[co] : 0.0f;
-    const float sc = A.dq.scale ? load_as_f32(A.dq.scale, A.dq.scale_dt, co * A.dq.scale_stride)
-                                : 1.0f;
-    const float* pb = A.part + static_cast<int64_t>(b) * ks * MN;
-    float* orow = A.out + (static_cast<int64_t>(b) * A.Cout + co) * Lout;
-    for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < Lout; pos += gridDim.x * blockDim.x) {
-      const int u = pos - ph0;
-      if (u < 0) continue;
-      const int q = u / P, r = u - q * P;
-      if (q >= Nq) continue;
-      const int i = (co * P + r) * Nq + q;
-      float acc = pb[i];
-      for (int sp = 1; sp < ks; ++sp) acc += pb[sp * MN + i];
-      const float v0 = acc * unscale;  // exact: a power of two
-      const float v = A.dq.scale ? v0 * sc : v0;
-      orow[pos] = A.bias ? v + bias : v;
-    }
-  }
-}
-
-__global__ void convh_flag_clear(int* flag, unsigned* xmax) {
-  *flag = 0;
-  *xmax = 0u;
-}
-
-// *xmax = max(*xmax, bits of max |x|) over n floats: |x| is a non-negative
-// float (NaN above infinity), so its bits order as unsigned integers.
-// vec: x is 16-byte aligned.
-__global__ void __launch_bounds__(256) convh_absmax(const float* __restrict__ x, int64_t n, int vec,
-                                                    unsigned* xmax) {
-  __shared__ unsigned part[4];
-  unsigned m = 0;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  const int64_t t0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  int64_t done = 0;
-  if (vec) {
-    const float4* x4 = reinterpret_cast<const float4*>(x);
-    const int64_t n4 = n / 4;
-    for (int64_t i = t0; i < n4; i += stride) {
-      const float4 v = x4[i];
-      m = max(m, max(max(__float_as_uint(fabsf(v.x)), __float_as_uint(fabsf(v.y))),
-                     max(__float_as_uint(fabsf(v.z)), __float_as_uint(fabsf(v.w)))));
-    }
-    done = 4 * n4;
-  }
-  for (int64_t i = done + t0; i < n; i += stride) m = max(m, __float_as_uint(fabsf(x[i])));
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = max(m, static_cast<unsigned>(__shfl_xor(static_cast<int>(m), off, 64)));
-  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) atomicMax(xmax, max(max(part[0], part[1]), max(part[2], part[3])));
-}
-
-// Wt[kk / 32][m][kk % 32] (m = co*P + r, kk = t*Cin + ci; Mp rows a step,
-// zeros past M): the fp16 value the gathering kernel forms, W less the zero
-// point (0 past the kernel for transposed), stored step by step so that a
-// step's weight tile is one stretch.
-// Rows m on the grid's y axis, kk along x, 32-bit index arithmetic (the
-// host checks the weight count and M * Kg against 2^31): a flat 64-bit walk
-// with a division chain per element took 16.8 us for ConvTranspose1d
-// 512->256 k20's 2.6M values, this 14 us -- bound by the transposed
-// weights' reads, one cache line per element (a block per output channel
-// staging its weights through LDS measured slower, 23 us).
+// One 16-byte unit (eight fp16 values) a thread.
 template <typename TW>
-__global__ void __launch_bounds__(256) convh_weights(_Float16* __restrict__ wt, HArgs A) {
-  if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
-    *A.flag = 0;
-    *A.xmax = 0u;
-  }
+__global__ void __launch_bounds__(256) convh_pack(PackArgs A) {
+  const int64_t u = blockIdx.x * int64_t{256} + threadIdx.x;
+  if (u >= A.units) return;
+  const int l = static_cast<int>(u % 64);
+  const int s = static_cast<int>((u / 64) % A.KS);
+  const int mt = static_cast<int>(u / (int64_t{64} * A.KS));
+  const int m = 32 * mt + (l % 32), g = l / 32;
+  const int co = m / A.P, r = m - co * A.P;
   const TW* w = static_cast<const TW*>(A.w);
-  const int P = A.P, Kg = static_cast<int>(A.Kg), Cin = static_cast<int>(A.Cin);
-  const int Kw = static_cast<int>(A.Kw), s = static_cast<int>(A.s);
-  const int M = static_cast<int>(A.M), Mp = static_cast<int>(A.Mp), cout = M / P;
-  for (int m = blockIdx.y; m < Mp; m += gridDim.y) {
-    const int co = m / P, r = m - co * P;
-    const float zp = A.dq.zp && m < M ? load_as_f32(A.dq.zp, A.dq.zp_dt, co * A.dq.zp_stride) : 0.0f;
-    for (int kk = blockIdx.x * blockDim.x + threadIdx.x; kk < Kg; kk += gridDim.x * blockDim.x) {
-      const int t = kk / Cin, ci = kk - t * Cin;
-      const int tap = A.transposed ? r + s * t : t;
-      float v = 0.0f;
-      if (m < M && tap < Kw) {
-        const int idx = A.transposed ? (ci * cout + co) * Kw + tap : (co * Cin + ci) * Kw + tap;
-        v = static_cast<float>(w[idx]) - zp;
+  const float z = A.zp && m < A.M ? load_as_f32(A.zp, A.zp_dt, co * A.zp_stride) : 0.0f;
+  h8 v;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int k = 8 * g + e;
+    const int ci = s * (16 / A.TP) + k / A.TP, tp = k % A.TP;
+    const int tap = A.transposed ? r + A.P * (A.T - 1 - tp) : tp;
+    float f = 0.0f;
+    if (m < A.M && ci < A.Cin && tp < A.T && tap < A.Kw) {
+      const int64_t idx = A.transposed ? (static_cast<int64_t>(ci) * A.Cout + co) * A.Kw + tap
+                                       : (static_cast<int64_t>(co) * A.Cin + ci) * A.Kw + tap;
+      f = static_cast<float>(w[idx]) - z;
+    }
+    v[e] = static_cast<_Float16>(f);
+  }
+  *reinterpret_cast<h8*>(A.wp + u) = v;
+}
+
+struct CArgs {
+  const uint4* wp;     // packed weights
+  const float* x;      // [N][Cin][L]
+  float* out;          // [N][Cout][Lout]
+  const float* bias;   // [Cout] or NULL
+  const void* scale;   // 8-bit weights: 1 or Cout values; NULL for fp16 weights
+  int scale_dt, scale_stride;
+  int Cin, L, Cout, Lout, M, Nq, P, T, KS;
+  int qs, ta, tm;      // x position of (q, t'): q qs + ta + t' tm
+  int os, oph;         // output position of (q, r): q os + r + oph
+  int wbytes;          // packed bytes (below 2^31)
+};
+
+// The power of two k with m 2^k in [2^10, 2^11) for the bits of m = max |x|
+// > 0, kept within [-120, 120] so that 2^k and 2^-k are normal floats.
+__device__ __forceinline__ int scale_exp(unsigned mbits) {
+  const int e = static_cast<int>(mbits >> 23) - 127;  // floor(log2 m); -127 for subnormal m
+  return min(120, 10 - e);
+}
+
+template <int TP, int MI, int WK, int R>
+__global__ void __launch_bounds__(kThreads) convh_kernel(CArgs A) {
+  constexpr int WN = 4 / WK, CPL = 8 / TP, CPS = 16 / TP;
+  constexpr int BM = 32 * MI, BN = 32 * WN;
+  constexpr int RED = WK > 1 ? (WK - 1) * WN * MI * 16 * 64 : 1;
+  __shared__ float red[RED];       // [wk - 1][wn][register][lane]: the other waves' partials
+  __shared__ int red_bad[4 * 64];  // [wave][lane]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave % WN, wk = wave / WN;
+  const int ln = lane & 31, g = lane >> 5;
+  // row tiles fastest: the blocks of one column range share an XCD.  The
+  // tile is wave-uniform; readfirstlane says so to the compiler, which would
+  // otherwise build the activations' buffer resource in vector registers
+  // and wrap every load in a loop over its distinct values.
+  const uint3 tile = xcd_tile();
+  const int m0 = __builtin_amdgcn_readfirstlane(static_cast<int>(tile.x)) * BM;
+  const int n0 = __builtin_amdgcn_readfirstlane(static_cast<int>(tile.y)) * BN;
+  const int64_t b = __builtin_amdgcn_readfirstlane(static_cast<int>(tile.z));
+  const int Cin = A.Cin, L = A.L, KS = A.KS;
+  const int q = n0 + wn * 32 + ln;
+  const int s0 = static_cast<int>(static_cast<int64_t>(KS) * wk / WK);
+  const int ns = static_cast<int>(static_cast<int64_t>(KS) * (wk + 1) / WK) - s0;
+  const auto xrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A.x + b * Cin * L), 0,
+                                                     Cin * L * 4, 0x00020000);
+  const auto wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint4*>(A.wp), 0, A.wbytes,
+                                                     0x00020000);
+  // byte offsets of this lane's TP positions in a channel row; 0x7fffffff
+  // outside the signal, past the columns or past the T taps in use, and a
+  // channel's offset 0x80000000 past Cin: any sum with either is past the
+  // buffer (below 2^31 bytes), so the load returns 0, and no sum wraps
+  uint32_t po[TP];
+#pragma unroll
+  for (int t = 0; t < TP; ++t) {
+    const int p = q * A.qs + A.ta + t * A.tm;
+    po[t] = q < A.Nq && t < A.T && p >= 0 && p < L ? static_cast<uint32_t>(4 * p) : 0x7fffffffu;
+  }
+  const int row_bytes = 4 * L;
+  const uint32_t a_lane = static_cast<uint32_t>(((m0 / 32) * KS * 64 + lane) * 16);
+  // per-row epilogue constants (output row offset, phase offset, scale,
+  // bias), filled by the first BM threads; read after the block's barrier
+  __shared__ int4 rows[BM];
+  if (tid < BM) {
+    const int m = m0 + tid;
+    int4 rv = make_int4(-1, 0, __float_as_int(1.0f), 0);
+    if (m < A.M) {
+      const int co = m / A.P, r = m - co * A.P;
+      rv.x = co * A.Lout;
+      rv.y = r + A.oph;
+      if (A.scale) rv.z = __float_as_int(load_as_f32(A.scale, A.scale_dt, co * A.scale_stride));
+      if (A.bias) rv.w = __float_as_int(A.bias[co]);
+    }
+    rows[tid] = rv;
+  }
+  float bv[R][8];
+  uint4 av[R][MI];
+  // slice s's x values (channels s CPS + g CPL + c, each with its TP taps)
+  // and weight fragments; issued whatever s (a read past the buffers
+  // returns 0), so every slot's loads count the same for the waits
+  auto fetch = [&](int s, float (&v)[8], uint4 (&f)[MI]) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int ci = s * CPS + g * CPL + c;
+      const uint32_t cofs = ci < Cin ? static_cast<uint32_t>(ci * row_bytes) : 0x80000000u;
+#pragma unroll
+      for (int t = 0; t < TP; ++t) {
+        uint32_t off = cofs + po[t];
+        asm volatile("" : "+v"(off));  // an unconditional load
+        v[c * TP + t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, off, 0, 0));
       }
-      wt[(static_cast<int64_t>(kk / kBK) * Mp + m) * kBK + (kk % kBK)] = static_cast<_Float16>(v);
+    }
+    const uint32_t a_s = a_lane + static_cast<uint32_t>(s * 1024);
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      uint32_t off = a_s + static_cast<uint32_t>(mi * KS * 1024);
+      asm volatile("" : "+v"(off));
+      const auto r = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);
+      f[mi] = make_uint4(r[0], r[1], r[2], r[3]);
+    }
+  };
+
+  f16v acc[MI];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+  int kcur = 0, have = 0, bad = 0;
+  // one slice: the column's running scale, the split, the products
+  auto mma = [&](float (&v)[8], const uint4 (&f)[MI]) {
+    unsigned mx = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = max(mx, __float_as_uint(v[e]) & 0x7fffffffu);
+    const auto pr = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);  // the column's other lane
+    mx = max(static_cast<unsigned>(pr[0]), static_cast<unsigned>(pr[1]));
+    const bool nonfinite = mx >= 0x7f800000u;
+    if (nonfinite) {
+      bad = 1;  // recomputed in the epilogue; no products from this slice
+    } else if (mx != 0u) {
+      if (!have) {
+        kcur = scale_exp(mx);
+        have = 1;
+      } else if (static_cast<int>(mx >> 23) - 127 + kcur >= 15) {  // m 2^k >= 2^15
+        const int kc = scale_exp(mx);
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][r] = ldexpf(acc[i][r], kc - kcur);
+        kcur = kc;
+      }
+    }
+    const float xs = nonfinite ? 0.0f : ldexpf(1.0f, kcur);
+    h8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = v[e] * xs;  // |y| < 2^15: exact
+      const _Float16 hh = static_cast<_Float16>(y);
+      hi[e] = hh;
+      lo[e] = static_cast<_Float16>(y - static_cast<float>(hh));
+    }
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) {
+      const h8 a = __builtin_bit_cast(h8, f[mi]);
+      acc[mi] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, hi, acc[mi], 0, 0, 0);
+      acc[mi] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, lo, acc[mi], 0, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int u = 0; u < R; ++u) fetch(s0 + u, bv[u], av[u]);
+  // whole rounds of R slices (a slot's refill is issued whether or not its
+  // slice exists: a skipped refill leaves the waits at "all loads")
+  for (int i = 0; i < ns; i += R) {
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      if (i + u < ns) mma(bv[u], av[u]);
+      fetch(s0 + i + u + R, bv[u], av[u]);
+    }
+  }
+  const float uns = ldexpf(1.0f, -kcur);  // exact: a power of two
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] *= uns;
+  if constexpr (WK > 1) {
+    if (wk > 0) {
+      float* dst = red + ((wk - 1) * WN + wn) * MI * 16 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dst[(i * 16 + r) * 64] = acc[i][r];
+    }
+    red_bad[wave * 64 + lane] = bad;
+  }
+  __syncthreads();  // the partials and the row constants
+  if (wk > 0) return;
+  if constexpr (WK > 1) {
+#pragma unroll
+    for (int k = 1; k < WK; ++k) {  // in wave order
+      const float* src = red + ((k - 1) * WN + wn) * MI * 16 * 64 + lane;
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] += src[(i * 16 + r) * 64];
+      bad |= red_bad[(k * WN + wn) * 64 + lane];
+    }
+  }
+  // D(i, j) of a 32x32 tile: lane j + 32 ((i / 4) % 2), register (i / 8) 4 + i % 4.
+  // Stores through a buffer resource over this item's output: an offset
+  // past it (a row past M, a column past Nq, a position outside [0, Lout))
+  // drops the store.
+  const auto ors = __builtin_amdgcn_make_buffer_rsrc(A.out + b * A.Cout * A.Lout, 0,
+                                                     A.Cout * A.Lout * 4, 0x00020000);
+  const int qpos = q < A.Nq ? q * A.os : INT_MIN / 2;
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int rg = 0; rg < 16; ++rg) {
+      const int ml = 32 * mi + 8 * (rg / 4) + 4 * g + (rg % 4);
+      const int4 rv = rows[ml];
+      const int pos = qpos + rv.y;
+      const bool ok = rv.x >= 0 && pos >= 0 && pos < A.Lout;
+      uint32_t off = ok ? static_cast<uint32_t>(4 * (rv.x + pos)) : 0x80000000u;
+      const float u = acc[mi][rg] * __int_as_float(rv.z);  // the scale (1 for fp16 weights)
+      const float v = A.bias ? u + __int_as_float(rv.w) : u;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ors, off, 0, 0);
+    }
+  if (bad) {
+    // a column with an infinity or a NaN: scalar fp32 products and sums over
+    // the packed weights (fp16 -> fp32 exact) and the raw activations give
+    // numpy's inf / NaN pattern
+    const float* xb = A.x + b * Cin * L;
+    const _Float16* wh = reinterpret_cast<const _Float16*>(A.wp);
+    for (int i = 0; i < 16 * MI; ++i) {
+      const int ml = 32 * (i / 16) + 8 * ((i % 16) / 4) + 4 * g + (i % 4);
+      const int m = m0 + ml;
+      const int4 rv = rows[ml];
+      const int pos = qpos + rv.y;
+      if (m >= A.M || pos < 0 || pos >= A.Lout) continue;
+      float sum = 0.0f;
+      for (int ci = 0; ci < Cin; ++ci)
+        for (int t = 0; t < A.T; ++t) {
+          const int p = q * A.qs + A.ta + t * A.tm;
+          if (p < 0 || p >= L) continue;
+          const int k = (ci % CPS) * TP + t;
+          const int64_t unit = (static_cast<int64_t>(m / 32) * KS + ci / CPS) * 64 + (m % 32) + 32 * (k / 8);
+          sum = sum + static_cast<float>(wh[unit * 8 + k % 8]) * xb[static_cast<int64_t>(ci) * L + p];
+        }
+      const float u = A.scale ? sum * __int_as_float(rv.z) : sum;
+      A.out[b * A.Cout * A.Lout + rv.x + pos] = A.bias ? u + __int_as_float(rv.w) : u;
     }
   }
 }
 
-// The ring kernel's 32-bit buffer offsets: weights (step-major) and one
-// batch of activations below 2^31 bytes; else the gathering kernel runs.
-static bool ring_ok(const HArgs& a) {
-  return a.Kg * a.Mp * 2 < (int64_t{1} << 31) && a.Cin * a.L * 4 < (int64_t{1} << 31);
+// The launch shape: MI 32-row tiles a wave, WK waves a column range.
+struct Shape {
+  int mi, wk;
+};
+
+// 128 rows a wave when that still gives every SIMD a wave, else 64 (32 for
+// at most 32 rows); then as many waves on the reduction (1, 2 or 4) as it
+// takes to give every SIMD two waves, each at least three slices.
+static Shape pick_shape(const CArgs& a, int64_t batch) {
+  Shape s{};
+  const int64_t simds = 4 * (ctx().num_cus > 0 ? ctx().num_cus : 256);
+  const int64_t cols = batch * ceil_div(a.Nq, 32);
+  s.mi = a.M <= 32 ? 1 : (a.M > 64 && cols * ceil_div(a.M, 128) >= simds) ? 4 : 2;
+  const int64_t waves = cols * ceil_div(a.M, 32 * s.mi);
+  s.wk = waves >= 2 * simds ? 1 : waves * 2 >= 2 * simds ? 2 : 4;
+  while (s.wk > 1 && a.KS < 3 * s.wk) s.wk /= 2;
+  return s;
 }
 
-// Rearranged weights (a.wt) go to the ring kernel, else the kernel gathers
-// them from W.
-template <class T, typename TW>
-static void launch_t(const HArgs& a, const dim3& grid) {
-  if (a.wt)
-    KK_LAUNCH((convh_ring_kernel<T>), grid, dim3(kThreads), 0, ctx().stream, a);
-  else
-    KK_LAUNCH((convh_kernel<T, TW, false>), grid, dim3(kThreads), 0, ctx().stream, a);
+template <int TP, int MI, int WK>
+static int launch_shape(const CArgs& a, int64_t batch) {
+  constexpr int BM = 32 * MI, BN = 32 * (4 / WK);
+  constexpr int R = 3;  // slices in flight (six measured no faster at MI <= 2)
+  const dim3 grid(static_cast<unsigned>(ceil_div(a.M, BM)), static_cast<unsigned>(ceil_div(a.Nq, BN)),
+                  static_cast<unsigned>(batch));
+  KK_TRY(check_xcd_grid(grid, "convh_kernel"));
+  KK_LAUNCH((convh_kernel<TP, MI, WK, R>), grid, dim3(kThreads), 0, ctx().stream, a);
+  return check_launch("convh_kernel");
 }
 
-// Split-K count for the ring kernel: enough splits that every CU gets two
-// blocks, at most 4, at least 8 K-steps a split, and the partial sums
-// within `part_bytes` (the context scratch left beside the rearranged
-// weights); 1 when no CU is short.  The choice depends on sizes alone, so a
-// call recorded into a graph sums in the same order as the same call made
-// eagerly.
-template <class T>
-static int ksplit_for(const HArgs& a, int64_t batch, size_t part_bytes) {
-  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
-  const int64_t blocks = batch * ceil_div(a.Nq, T::BN) * ceil_div(a.M, T::BM);
-  if (!a.wt || blocks >= 2 * cus || a.M * a.Nq >= (int64_t{1} << 31) / 4 ||
-      a.Cout * a.Lout >= (int64_t{1} << 31))
-    return 1;
-  const int64_t nk = a.Kg / kBK;
-  const int64_t room = static_cast<int64_t>(part_bytes) / (4 * batch * a.M * a.Nq);
-  const int64_t s = std::min<int64_t>({4, ceil_div(2 * cus, blocks), nk / 8, room});
-  return static_cast<int>(std::max<int64_t>(1, s));
-}
-
-template <class T>
-static void launch(HArgs& a, int w_dt, int64_t batch, float* part, size_t part_bytes) {
-  a.ksplit = ksplit_for<T>(a, batch, part_bytes);
-  a.part = a.ksplit > 1 ? part : nullptr;
-  const dim3 grid(static_cast<unsigned>(ceil_div(a.Nq, T::BN)), static_cast<unsigned>(ceil_div(a.M, T::BM)),
-                  static_cast<unsigned>(batch * a.ksplit));
-  if (w_dt == KK_F16) launch_t<T, _Float16>(a, grid);
-  else if (w_dt == KK_I8) launch_t<T, int8_t>(a, grid);
-  else launch_t<T, uint8_t>(a, grid);
-  if (a.part) {
-    const dim3 fg(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Lout, 256), 64)),
-                  static_cast<unsigned>(std::min<int64_t>(a.Cout, 65535)), static_cast<unsigned>(batch));
-    KK_LAUNCH(convh_splitk_finish, fg, dim3(256), 0, ctx().stream, a);
-    a.part = nullptr;
-    a.ksplit = 1;
+template <int TP>
+static int launch_tp(const CArgs& a, const Shape& s, int64_t batch) {
+#define KK_CONVH_WK(MI)                                           \
+  switch (s.wk) {                                                 \
+    case 1: return launch_shape<TP, MI, 1>(a, batch);             \
+    case 2: return launch_shape<TP, MI, 2>(a, batch);             \
+    default: return launch_shape<TP, MI, 4>(a, batch);            \
   }
+  if (s.mi == 1) KK_CONVH_WK(1)
+  if (s.mi == 2) KK_CONVH_WK(2)
+  KK_CONVH_WK(4)
+#undef KK_CONVH_WK
 }
 
-// Rearranges the weights into the context scratch (or, larger, into a
-// pooled workspace unless a graph is being recorded; else the kernel
-// gathers them); launches the tile that suits M x Nq.
-static void run(HArgs& a, const kk_tensor* w, int64_t batch, void** ws) {
-  a.Mp = ceil_div(a.M, 128) * 128;
-  const size_t wt_bytes = static_cast<size_t>(a.Kg * a.Mp * 2);
-  void* wtp = nullptr;
-  if (!ring_ok(a)) wtp = nullptr;
-  else if (wt_bytes <= kScratchBytes) wtp = ctx().scratch;
-  else if (!ctx().capturing && kk_alloc(wt_bytes, ws) == KK_OK) wtp = *ws;
-  if (wtp) {
-    _Float16* wt = static_cast<_Float16*>(wtp);
-    const dim3 g(static_cast<unsigned>(std::min<int64_t>(ceil_div(a.Kg, 256), 64)),
-                 static_cast<unsigned>(std::min<int64_t>(a.Mp, 65535)));
-    if (w->dtype == KK_F16)
-      KK_LAUNCH(convh_weights<_Float16>, g, dim3(256), 0, ctx().stream, wt, a);
-    else if (w->dtype == KK_I8)
-      KK_LAUNCH(convh_weights<int8_t>, g, dim3(256), 0, ctx().stream, wt, a);
-    else
-      KK_LAUNCH(convh_weights<uint8_t>, g, dim3(256), 0, ctx().stream, wt, a);
-    a.wt = wt;
+static int launch(const CArgs& a, int tp, int64_t batch) {
+  const Shape s = pick_shape(a, batch);
+  if (tp == 2) return launch_tp<2>(a, s, batch);
+  if (tp == 4) return launch_tp<4>(a, s, batch);
+  return launch_tp<8>(a, s, batch);
+}
+
+// The pack of w (less its zero point) into `wp` (g.bytes, 16-byte aligned).
+static int pack(const Geo& g, void* wp, const kk_tensor* w, const Dequant& dq) {
+  PackArgs p{};
+  p.wp = static_cast<uint4*>(wp);
+  p.w = w->data;
+  p.zp = dq.zp;
+  p.zp_dt = dq.zp_dt;
+  p.zp_stride = static_cast<int>(dq.zp_stride);
+  p.Cin = static_cast<int>(g.Cin); p.Cout = static_cast<int>(g.Cout); p.Kw = static_cast<int>(g.Kw);
+  p.P = static_cast<int>(g.P); p.T = static_cast<int>(g.T); p.TP = static_cast<int>(g.TP);
+  p.M = static_cast<int>(g.M); p.KS = static_cast<int>(g.KS);
+  p.transposed = g.transposed;
+  p.units = g.bytes / 16;
+  const dim3 grid(static_cast<unsigned>(ceil_div(p.units, 256)));
+  if (w->dtype == KK_F16) KK_LAUNCH(convh_pack<_Float16>, grid, dim3(256), 0, ctx().stream, p);
+  else if (w->dtype == KK_I8) KK_LAUNCH(convh_pack<int8_t>, grid, dim3(256), 0, ctx().stream, p);
+  else KK_LAUNCH(convh_pack<uint8_t>, grid, dim3(256), 0, ctx().stream, p);
+  return check_launch("convh_pack");
+}
+
+// Weights the fp16 path takes: fp16 as they are; 8-bit less an 8-bit zero
+// point (the difference is an integer of at most 255: exact in fp16).
+static bool weights_ok(const kk_tensor* w, const Dequant& dq) {
+  const bool w16 = w->dtype == KK_F16 && !dq.active;
+  const bool w8 = (w->dtype == KK_I8 || w->dtype == KK_U8) &&
+                  (!dq.zp || dq.zp_dt == KK_I8 || dq.zp_dt == KK_U8);
+  return w16 || w8;
+}
+
+// The launch arguments of a call, or false when the fp16 path does not
+// apply (more than 8 taps, or sizes beyond its 32-bit offsets and grid).
+static bool make_args(CArgs* a, const Geo& g, const kk_tensor* out, const kk_tensor* x,
+                      const Dequant& dq, const kk_tensor* bias, int64_t stride, int64_t dilation,
+                      int64_t pad0, int64_t Nq) {
+  const int64_t N = x->shape[0], L = x->shape[2], Lout = out->shape[2];
+  if (!g.TP || x->dtype != KK_F32 || N > 65535 || g.Cin * L * 4 >= (int64_t{1} << 31) ||
+      g.Cout * Lout * 4 >= (int64_t{1} << 31) || g.bytes >= (int64_t{1} << 31) ||
+      (Nq + 1) * std::max<int64_t>(stride, 1) + g.TP * dilation + pad0 >= (int64_t{1} << 29) ||
+      (Nq + 1) * g.P + Lout + pad0 >= (int64_t{1} << 30) || g.M >= (int64_t{1} << 30))
+    return false;
+  *a = CArgs{};
+  a->x = static_cast<const float*>(x->data);
+  a->out = static_cast<float*>(out->data);
+  a->bias = bias ? static_cast<const float*>(bias->data) : nullptr;
+  a->scale = dq.scale;
+  a->scale_dt = dq.scale_dt;
+  a->scale_stride = static_cast<int>(dq.scale_stride);
+  a->Cin = static_cast<int>(g.Cin); a->L = static_cast<int>(L);
+  a->Cout = static_cast<int>(g.Cout); a->Lout = static_cast<int>(Lout);
+  a->M = static_cast<int>(g.M); a->Nq = static_cast<int>(Nq); a->P = static_cast<int>(g.P);
+  a->T = static_cast<int>(g.T); a->KS = static_cast<int>(g.KS);
+  if (g.transposed) {
+    a->qs = 1; a->ta = static_cast<int>(1 - g.T); a->tm = 1;
+    a->os = static_cast<int>(g.P); a->oph = static_cast<int>(-pad0);
   } else {
-    KK_LAUNCH(convh_flag_clear, dim3(1), dim3(1), 0, ctx().stream, a.flag, a.xmax);
+    a->qs = static_cast<int>(stride); a->ta = static_cast<int>(-pad0); a->tm = static_cast<int>(dilation);
+    a->os = 1; a->oph = 0;
   }
-  {
-    const int64_t n = a.Cin * a.L * batch;
-    const unsigned g = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256 * 16), 1024)));
-    const int vec = reinterpret_cast<uintptr_t>(a.x) % 16 == 0 ? 1 : 0;
-    KK_LAUNCH(convh_absmax, dim3(g), dim3(256), 0, ctx().stream, a.x, n, vec, a.xmax);
-  }
-  // split-K partial sums: the context scratch beside weights rearranged there
-  float* part = nullptr;
-  size_t part_bytes = 0;
-  if (wtp == ctx().scratch) {
-    const size_t off = (wt_bytes + 255) & ~size_t{255};
-    if (off < kScratchBytes) {
-      part = reinterpret_cast<float*>(static_cast<char*>(ctx().scratch) + off);
-      part_bytes = kScratchBytes - off;
-    }
-  }
-  // the largest tile that still gives every CU two blocks; 128 x 32 below that
-  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
-  if (a.M <= 32) launch<Tile<1, 1, 1>>(a, w->dtype, batch, part, part_bytes);
-  else if (a.M <= 64) launch<Tile<2, 1, 2>>(a, w->dtype, batch, part, part_bytes);
-  else if (batch * ceil_div(a.M, 128) * ceil_div(a.Nq, 128) >= 2 * cus)
-    launch<Tile<2, 2, 2>>(a, w->dtype, batch, part, part_bytes);
-  else launch<Tile<4, 1, 1>>(a, w->dtype, batch, part, part_bytes);
+  a->wbytes = static_cast<int>(g.bytes);
+  return true;
+}
+
+// What a packed buffer was made from (checked by every packed call).
+struct PackRecord {
+  const void* w;
+  int64_t d0, d1, d2;
+  int w_dt;
+  const void* zp;
+  int zp_dt;
+  int transposed;
+  int64_t stride;
+};
+static std::mutex g_pack_mu;
+static std::unordered_map<const void*, PackRecord> g_packs;
+
+static PackRecord record_of(const kk_tensor* w, const kk_tensor* w_zp, bool transposed, int64_t stride) {
+  return PackRecord{w->data, w->shape[0], w->shape[1], w->shape[2], w->dtype,
+                    w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : -1, transposed ? 1 : 0,
+                    transposed ? stride : 1};
 }
 
 }  // namespace convh
 
 using namespace convh;
 
-// Launches the fp16 matrix-core convolution when it applies and returns
-// true; *flag is then the condition for the caller's fp32 fallback, which
-// the caller launches next, and *ws a workspace to kk_free after that (or
-// NULL).  The flag is cleared at the start of each call (by the weight
-// rearrangement, or a one-thread kernel when there is none).
+void convh_forget_pack(const void* p) {
+  std::lock_guard<std::mutex> lock(g_pack_mu);
+  g_packs.erase(p);
+}
+
+// The fp16 matrix-core convolution of one call: true when it ran (its
+// status in *rc), false when it does not apply (the caller runs the fp32
+// kernels).  `packed` (checked by the caller) holds the weights laid out by
+// kk_conv_pack; without it they are laid out here, in the context scratch
+// (or a pooled workspace, freed after the launch in stream order).
 bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const Dequant& dq,
                const kk_tensor* bias, bool transposed, int64_t stride, int64_t dilation,
-               int64_t pad0, int64_t Nq, int** flag, void** ws) {
-  *ws = nullptr;
-  // fp16 weights as they are; 8-bit weights less an 8-bit zero point
-  const bool w16 = w->dtype == KK_F16 && !dq.active;
-  const bool w8 = (w->dtype == KK_I8 || w->dtype == KK_U8) &&
-                  (!dq.zp || dq.zp_dt == KK_I8 || dq.zp_dt == KK_U8);
-  if (!(w16 || w8) || x->dtype != KK_F32) return false;
-  const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
-  const int64_t Cout = out->shape[1], Lout = out->shape[2], Kw = w->shape[2];
-  if (Cin % kBK || (transposed && dilation != 1)) return false;
-  const int64_t taps = transposed ? ceil_div(Kw, stride) : Kw;
-  const int64_t P = transposed ? stride : 1;
-  const int64_t Kg = taps * Cin, M = P * Cout;
-  if (M * Nq * Kg < (int64_t{1} << 26) || N > 65535 || ceil_div(M, 32) > 65535 ||
-      ceil_div(Nq, 32) > 0x7fffffff || numel(w) > 0x7fffffff)
-    return false;
-  *flag = ctx().row_counters + kRowCounters + kFlagConvh;
-  HArgs a{};
-  a.w = w->data; a.transposed = transposed ? 1 : 0; a.Kw = Kw; a.s = stride; a.dq = dq;
-  a.x = static_cast<const float*>(x->data); a.out = static_cast<float*>(out->data);
-  a.bias = bias ? static_cast<const float*>(bias->data) : nullptr; a.flag = *flag;
-  a.xmax = reinterpret_cast<unsigned*>(ctx().row_counters + kRowCounters + kFlagConvhMax);
-  a.Cin = Cin; a.L = L; a.M = M; a.Cout = Cout; a.Kg = Kg; a.Nq = Nq; a.Lout = Lout;
-  a.P = static_cast<int>(P);
-  a.ksplit = 1;
-  if (transposed) {
-    a.qs = 1; a.tap_mul = -1; a.tap_add = 0; a.os = stride; a.ophase0 = -pad0;
+               int64_t pad0, int64_t Nq, const kk_tensor* packed, int* rc) {
+  *rc = KK_OK;
+  if (!weights_ok(w, dq) || (transposed && dilation != 1)) return false;
+  const int64_t Cin = x->shape[1];
+  const int64_t Cout = out->shape[1], Kw = w->shape[2];
+  const Geo g = geometry(transposed, Cin, Cout, Kw, stride);
+  // enough work for the matrix cores
+  if (Cin < 8 || g.M * Nq * g.T * Cin < (int64_t{1} << 24)) return false;
+  CArgs a;
+  if (!make_args(&a, g, out, x, dq, bias, stride, dilation, pad0, Nq)) return false;
+  if (packed) {
+    a.wp = static_cast<const uint4*>(packed->data);
   } else {
-    a.qs = stride; a.tap_mul = dilation; a.tap_add = -pad0; a.os = 1; a.ophase0 = 0;
+    void* wp = nullptr;
+    void* ws = nullptr;
+    if (g.bytes <= static_cast<int64_t>(kScratchBytes)) wp = ctx().scratch;
+    else if (!ctx().capturing && kk_alloc(static_cast<size_t>(g.bytes), &ws) == KK_OK) wp = ws;
+    if (!wp) return false;
+    *rc = pack(g, wp, w, dq);
+    if (*rc == KK_OK) {
+      a.wp = static_cast<const uint4*>(wp);
+      *rc = launch(a, static_cast<int>(g.TP), x->shape[0]);
+    }
+    if (ws) kk_free(ws);  // stream order keeps it alive for the kernels above
+    return true;
   }
-  run(a, w, N, ws);
+  *rc = launch(a, static_cast<int>(g.TP), x->shape[0]);
   return true;
 }
 
+// Checks a packed buffer against the call: its size and alignment, and that
+// the last kk_conv_pack into it read this w (and zero point) for this
+// geometry.
+int convh_check_packed(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp,
+                       bool transposed, int64_t stride, const char* who) {
+  KK_TRY(check_tensor(packed, "packed"));
+  const int64_t cin = transposed ? w->shape[0] : w->shape[1];
+  const int64_t cout = transposed ? w->shape[1] : w->shape[0];
+  const int64_t need = geometry(transposed, cin, cout, w->shape[2], stride).bytes;
+  if (packed->dtype != KK_U8 || !is_contiguous(packed) || numel(packed) != need ||
+      reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
+    return set_error(KK_E_ARG, "%s: packed must be %lld contiguous, 256-byte aligned uint8 bytes",
+                     who, (long long)need);
+  const PackRecord want = record_of(w, w_zp, transposed, stride);
+  std::lock_guard<std::mutex> lock(g_pack_mu);
+  auto it = g_packs.find(packed->data);
+  if (it == g_packs.end()) return set_error(KK_E_ARG, "%s: packed was not made by kk_conv_pack", who);
+  const PackRecord& r = it->second;
+  if (r.w != want.w || r.d0 != want.d0 || r.d1 != want.d1 || r.d2 != want.d2 || r.w_dt != want.w_dt)
+    return set_error(KK_E_ARG, "%s: packed was made from another weight tensor", who);
+  if (r.zp != want.zp || r.zp_dt != want.zp_dt)
+    return set_error(KK_E_ARG, "%s: packed was made with another weight zero point", who);
+  if (r.transposed != want.transposed || r.stride != want.stride)
+    return set_error(KK_E_ARG, "%s: packed was made for another %s", who,
+                     r.transposed != want.transposed ? "operation" : "stride");
+  return KK_OK;
+}
 
 }  // namespace kk
+
+using namespace kk;
+
+extern "C" {
+
+int kk_conv_packed_bytes(int transposed, int64_t cin, int64_t cout, int64_t k, int stride,
+                         int64_t* bytes) {
+  if (!bytes || cin <= 0 || cout <= 0 || k <= 0 || stride < 1)
+    return set_error(KK_E_ARG, "kk_conv_packed_bytes: positive sizes, stride and an output");
+  const Geo g = geometry(transposed != 0, cin, cout, k, stride);
+  if (!g.TP)
+    return set_error(KK_E_UNSUPPORTED, "kk_conv_packed_bytes: %lld taps a row (more than 8) are "
+                     "not packed", (long long)g.T);
+  *bytes = g.bytes;
+  return KK_OK;
+}
+
+int kk_conv_pack(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp,
+                 int transposed, int stride) {
+  const char* who = "kk_conv_pack";
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(w, "w"));
+  if (w->rank != 3 || !(w->dtype == KK_F16 || w->dtype == KK_I8 || w->dtype == KK_U8) ||
+      !is_contiguous(w) || numel(w) == 0 || stride < 1)
+    return set_error(KK_E_ARG,
+                     "%s: w must be a non-empty contiguous fp16/int8/uint8 tensor of rank 3 and "
+                     "stride >= 1", who);
+  const bool tr = transposed != 0;
+  const int64_t cin = tr ? w->shape[0] : w->shape[1];
+  const int64_t cout = tr ? w->shape[1] : w->shape[0];
+  Dequant dq;
+  if (w_zp) {
+    if (w->dtype == KK_F16) return set_error(KK_E_ARG, "%s: an fp16 weight takes no zero point", who);
+    KK_TRY(check_tensor(w_zp, "w_zp"));
+    if (!(w_zp->dtype == KK_I8 || w_zp->dtype == KK_U8))
+      return set_error(KK_E_ARG, "%s: w_zp must be int8/uint8", who);
+    KK_TRY(zp_shift(&dq, w_zp, cout, who));
+  }
+  const Geo g = geometry(tr, cin, cout, w->shape[2], stride);
+  if (!g.TP)
+    return set_error(KK_E_UNSUPPORTED, "%s: %lld taps a row (more than 8) are not packed", who,
+                     (long long)g.T);
+  if (g.bytes >= (int64_t{1} << 31))
+    return set_error(KK_E_UNSUPPORTED, "%s: %lld packed bytes exceed 2 GiB", who, (long long)g.bytes);
+  KK_TRY(check_tensor(packed, "packed"));
+  if (packed->dtype != KK_U8 || !is_contiguous(packed) || numel(packed) != g.bytes ||
+      reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
+    return set_error(KK_E_ARG, "%s: packed must be %lld contiguous, 256-byte aligned uint8 bytes",
+                     who, (long long)g.bytes);
+  {
+    std::lock_guard<std::mutex> lock(g_pack_mu);
+    g_packs[packed->data] = record_of(w, w_zp, tr, stride);
+  }
+  return pack(g, packed->data, w, dq);
+}
+
+}  // extern "C"

@@ -471,13 +471,11 @@ struct ConvArgs {
   const float* bias;   // [Cout] or NULL
   int64_t Cin, L, Kw, s, d, p0, Lout;
   int64_t M, K;        // Cout, Cin*Kw
-  const int* only_if;  // the launch does nothing unless *only_if is set (NULL: always runs)
 };
 
 // AK: 0 = quad loads of TW (K % 4 == 0), 1 = scalar gather.
 template <class C, int AK, typename TW>
 __global__ void __launch_bounds__(kNT) conv1d_kernel(ConvArgs A) {
-  if (A.only_if && *A.only_if == 0) return;
   const int64_t bz = blockIdx.z;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
   const int64_t n0 = static_cast<int64_t>(blockIdx.x) * C::BN;
@@ -533,12 +531,10 @@ struct ConvTArgs {
   float* out;          // [N, Cout, Lout]
   const float* bias;
   int64_t Cin, Cout, L, Kw, s, MR, p0, Lout, nq;
-  const int* only_if;  // the launch does nothing unless *only_if is set (NULL: always runs)
 };
 
 template <class C>
 __global__ void __launch_bounds__(kNT) conv_transpose_kernel(ConvTArgs A) {
-  if (A.only_if && *A.only_if == 0) return;
   const int64_t r = blockIdx.z % A.s;
   const int64_t bz = blockIdx.z / A.s;
   const int64_t m0 = static_cast<int64_t>(blockIdx.y) * C::BM;
@@ -948,11 +944,13 @@ int zp_shift(Dequant* d, const kk_tensor* zp, int64_t count, const char* who) {
   return KK_OK;
 }
 
-// fp16-weight convolutions on the fp16 matrix cores (kk_conv_f16.hip):
-// true when launched; *flag is then the condition for the fp32 fallback.
+// fp16 / 8-bit-weight convolutions on the fp16 matrix cores (kk_conv_f16.hip):
+// true when that path ran (its status in *rc), false when it does not apply.
 bool convh_run(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const Dequant& dq,
                const kk_tensor* bias, bool transposed, int64_t stride, int64_t dilation,
-               int64_t pad0, int64_t Nq, int** flag, void** ws);
+               int64_t pad0, int64_t Nq, const kk_tensor* packed, int* rc);
+int convh_check_packed(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp,
+                       bool transposed, int64_t stride, const char* who);
 
 int gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
          const kk_tensor* w_zp, float alpha, bool weights_rounded) {
@@ -979,28 +977,42 @@ int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const 
   return gemm(out, a, w, w_scale, w_zp, alpha, false);
 }
 
-int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* w_scale,
-              const kk_tensor* w_zp, const kk_tensor* bias, int stride, int dilation, int pad0,
-              int pad1, int group) {
-  KK_TRY(conv_common(out, x, w, bias, "kk_conv1d"));
+}  // extern "C"
+
+namespace kk {
+
+// Conv1d (ref_runtime.py:58-82, 101-103); `packed` (checked by the caller)
+// holds w laid out by kk_conv_pack, or NULL.
+static int conv1d_impl(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                       const kk_tensor* w_scale, const kk_tensor* w_zp, const kk_tensor* bias,
+                       int stride, int dilation, int pad0, int pad1, int group,
+                       const kk_tensor* packed, const char* who) {
+  KK_TRY(conv_common(out, x, w, bias, who));
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], cin_g = w->shape[1], K = w->shape[2];
   if (stride < 1 || dilation < 1 || pad0 < 0 || pad1 < 0 || group < 1)
-    return set_error(KK_E_ARG, "kk_conv1d: bad stride/dilation/pads/group");
+    return set_error(KK_E_ARG, "%s: bad stride/dilation/pads/group", who);
   if (Cin % group || Cout % group || cin_g * group != Cin)
-    return set_error(KK_E_ARG, "kk_conv1d: channels do not match group %d", group);
+    return set_error(KK_E_ARG, "%s: channels do not match group %d", who, group);
   const int64_t span = static_cast<int64_t>(dilation) * (K - 1) + 1;
   const int64_t Lp = L + pad0 + pad1;
   const int64_t Lout = Lp >= span ? (Lp - span) / stride + 1 : 0;
   if (out->shape[0] != N || out->shape[1] != Cout || out->shape[2] != Lout)
-    return set_error(KK_E_ARG, "kk_conv1d: out must be [%lld, %lld, %lld]", (long long)N,
+    return set_error(KK_E_ARG, "%s: out must be [%lld, %lld, %lld]", who, (long long)N,
                      (long long)Cout, (long long)Lout);
-  if (bias && numel(bias) != Cout) return set_error(KK_E_ARG, "kk_conv1d: bias needs Cout elements");
+  if (bias && numel(bias) != Cout) return set_error(KK_E_ARG, "%s: bias needs Cout elements", who);
   Dequant dq;
-  KK_TRY(make_dequant(&dq, w, w_scale, w_zp, Cout, "kk_conv1d"));
+  KK_TRY(make_dequant(&dq, w, w_scale, w_zp, Cout, who));
+  if (packed) {
+    if (group != 1) return set_error(KK_E_ARG, "%s: packed weights need group 1", who);
+    KK_TRY(convh_check_packed(packed, w, w_zp, false, stride, who));
+  }
   if (N * Cout * Lout == 0) return KK_OK;
   const float* bp = bias ? static_cast<const float*>(bias->data) : nullptr;
   if (group == 1) {
+    // fp16 / 8-bit weights: the fp16 matrix cores when they apply
+    int rc = KK_OK;
+    if (convh_run(out, x, w, dq, bias, false, stride, dilation, pad0, Lout, packed, &rc)) return rc;
     ConvArgs args{};
     args.w = w->data; args.w_dt = w->dtype; args.dq = dq;
     args.x = static_cast<const float*>(x->data);
@@ -1011,11 +1023,6 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
     const TileSize ts = pick_tile(Cout, Lout, N);
     const dim3 grid = grid_of(ts, Cout, Lout, N);
     KK_TRY(check_grid(grid, N));
-    // fp16 / 8-bit weights: the fp16 matrix cores, this fp32 kernel only if flagged
-    int* hflag = nullptr;
-    void* hws = nullptr;
-    if (convh_run(out, x, w, dq, bias, false, stride, dilation, pad0, Lout, &hflag, &hws))
-      args.only_if = hflag;
     const bool quad = (Cin * K) % 4 == 0 && aligned(w->data, 4 * dtype_size(w->dtype));
     if (!quad) {
       KK_TILED(conv1d_kernel, ts, grid, 1, float);
@@ -1027,7 +1034,6 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
         default: KK_TILED(conv1d_kernel, ts, grid, 0, uint8_t); break;
       }
     }
-    if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
     return check_launch("conv1d_kernel");
   }
   DirectArgs D{};
@@ -1041,61 +1047,65 @@ int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, cons
   return check_launch("conv1d_direct_kernel");
 }
 
-
-int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
-                        const kk_tensor* w_scale, const kk_tensor* w_zp, const kk_tensor* bias,
-                        int stride, int dilation, int pad0, int pad1, int group,
-                        int output_padding) {
-  KK_TRY(conv_common(out, x, w, bias, "kk_conv_transpose1d"));
+// ConvTranspose1d (ref_runtime.py:83-99); `packed` as for conv1d_impl.
+static int conv_transpose1d_impl(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                                 const kk_tensor* w_scale, const kk_tensor* w_zp,
+                                 const kk_tensor* bias, int stride, int dilation, int pad0,
+                                 int pad1, int group, int output_padding,
+                                 const kk_tensor* packed, const char* who) {
+  KK_TRY(conv_common(out, x, w, bias, who));
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t cout_g = w->shape[1], K = w->shape[2];
   if (stride < 1 || dilation < 1 || pad0 < 0 || pad1 < 0 || group < 1 || output_padding < 0)
-    return set_error(KK_E_ARG, "kk_conv_transpose1d: bad stride/dilation/pads/group");
+    return set_error(KK_E_ARG, "%s: bad stride/dilation/pads/group", who);
   if (w->shape[0] != Cin || Cin % group)
-    return set_error(KK_E_ARG, "kk_conv_transpose1d: w must be [Cin, Cout/group, K]");
+    return set_error(KK_E_ARG, "%s: w must be [Cin, Cout/group, K]", who);
   const int64_t Cout = cout_g * group;
   const int64_t lfull = (L - 1) * stride + static_cast<int64_t>(dilation) * (K - 1) + 1 + output_padding;
   const int64_t Lout = lfull - pad0 - pad1;
-  if (L < 1 || Lout < 0) return set_error(KK_E_ARG, "kk_conv_transpose1d: empty or negative output");
+  if (L < 1 || Lout < 0) return set_error(KK_E_ARG, "%s: empty or negative output", who);
   if (out->shape[0] != N || out->shape[1] != Cout || out->shape[2] != Lout)
-    return set_error(KK_E_ARG, "kk_conv_transpose1d: out must be [%lld, %lld, %lld]", (long long)N,
+    return set_error(KK_E_ARG, "%s: out must be [%lld, %lld, %lld]", who, (long long)N,
                      (long long)Cout, (long long)Lout);
   if (bias && numel(bias) != Cout)
-    return set_error(KK_E_ARG, "kk_conv_transpose1d: bias needs Cout elements");
+    return set_error(KK_E_ARG, "%s: bias needs Cout elements", who);
   Dequant dq;
-  KK_TRY(make_dequant(&dq, w, w_scale, w_zp, Cout, "kk_conv_transpose1d"));
+  KK_TRY(make_dequant(&dq, w, w_scale, w_zp, Cout, who));
+  if (packed) {
+    if (group != 1 || dilation != 1)
+      return set_error(KK_E_ARG, "%s: packed weights need group 1 and dilation 1", who);
+    KK_TRY(convh_check_packed(packed, w, w_zp, true, stride, who));
+  }
   if (N * Cout * Lout == 0) return KK_OK;
   const float* bp = bias ? static_cast<const float*>(bias->data) : nullptr;
   // A few output channels: the direct kernel (a thread per output, only the
   // taps that land on it); the tiles below would be mostly empty rows.
-  if (group == 1 && dilation == 1 && Cout > 4) {
+  if (group == 1 && dilation == 1 && (Cout > 4 || packed)) {
     // Phase decomposition: s sub-GEMMs of MR = ceil(K/s) taps each.  Output
     // position jo maps to j = jo + p0 = q*s + r; every q up to the last
     // needed j is enumerated (x reads are bounds-checked, so the
     // output_padding tail gets the bias alone).
+    const int64_t jmax = lfull - pad1 - 1;  // last needed uncropped position
+    const int64_t nq = jmax / stride + 1;
+    // fp16 / 8-bit weights: the fp16 matrix cores when they apply
+    int rc = KK_OK;
+    if (convh_run(out, x, w, dq, bias, true, stride, 1, pad0, nq, packed, &rc)) return rc;
     ConvTArgs args{};
     args.w = w->data; args.w_dt = w->dtype; args.dq = dq;
     args.x = static_cast<const float*>(x->data);
     args.out = static_cast<float*>(out->data); args.bias = bp;
     args.Cin = Cin; args.Cout = Cout; args.L = L; args.Kw = K; args.s = stride;
     args.MR = ceil_div(K, stride); args.p0 = pad0; args.Lout = Lout;
-    const int64_t jmax = lfull - pad1 - 1;  // last needed uncropped position
-    args.nq = jmax / stride + 1;
+    args.nq = nq;
     const TileSize ts = pick_tile(Cout, args.nq, N * stride);
     const dim3 grid = grid_of(ts, Cout, args.nq, N * stride);
     KK_TRY(check_grid(grid, N * stride));
-    // fp16 / 8-bit weights: the fp16 matrix cores, this fp32 kernel only if flagged
-    int* hflag = nullptr;
-    void* hws = nullptr;
-    if (convh_run(out, x, w, dq, bias, true, stride, 1, pad0, args.nq, &hflag, &hws))
-      args.only_if = hflag;
     if (ts == TILE_L)
       KK_LAUNCH(conv_transpose_kernel<CfgL>, grid, dim3(kNT), 0, ctx().stream, args);
     else if (ts == TILE_M)
       KK_LAUNCH(conv_transpose_kernel<CfgM>, grid, dim3(kNT), 0, ctx().stream, args);
     else
       KK_LAUNCH(conv_transpose_kernel<CfgS>, grid, dim3(kNT), 0, ctx().stream, args);
-    if (hws) kk_free(hws);  // stream order keeps it alive for the kernels above
     return check_launch("conv_transpose_kernel");
   }
   DirectArgs D{};
@@ -1112,6 +1122,42 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tenso
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(total, 256), 1 << 20));
   KK_LAUNCH(conv_transpose_direct_kernel, dim3(grid), dim3(256), 0, ctx().stream, D);
   return check_launch("conv_transpose_direct_kernel");
+}
+
+}  // namespace kk
+
+extern "C" {
+
+int kk_conv1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* w_scale,
+              const kk_tensor* w_zp, const kk_tensor* bias, int stride, int dilation, int pad0,
+              int pad1, int group) {
+  return conv1d_impl(out, x, w, w_scale, w_zp, bias, stride, dilation, pad0, pad1, group, nullptr,
+                     "kk_conv1d");
+}
+
+int kk_conv1d_packed(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                     const kk_tensor* packed, const kk_tensor* w_scale, const kk_tensor* w_zp,
+                     const kk_tensor* bias, int stride, int dilation, int pad0, int pad1) {
+  if (!packed) return set_error(KK_E_ARG, "kk_conv1d_packed: packed is required");
+  return conv1d_impl(out, x, w, w_scale, w_zp, bias, stride, dilation, pad0, pad1, 1, packed,
+                     "kk_conv1d_packed");
+}
+
+int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                        const kk_tensor* w_scale, const kk_tensor* w_zp, const kk_tensor* bias,
+                        int stride, int dilation, int pad0, int pad1, int group,
+                        int output_padding) {
+  return conv_transpose1d_impl(out, x, w, w_scale, w_zp, bias, stride, dilation, pad0, pad1, group,
+                               output_padding, nullptr, "kk_conv_transpose1d");
+}
+
+int kk_conv_transpose1d_packed(const kk_tensor* out, const kk_tensor* x, const kk_tensor* w,
+                               const kk_tensor* packed, const kk_tensor* w_scale,
+                               const kk_tensor* w_zp, const kk_tensor* bias, int stride, int pad0,
+                               int pad1, int output_padding) {
+  if (!packed) return set_error(KK_E_ARG, "kk_conv_transpose1d_packed: packed is required");
+  return conv_transpose1d_impl(out, x, w, w_scale, w_zp, bias, stride, 1, pad0, pad1, 1,
+                               output_padding, packed, "kk_conv_transpose1d_packed");
 }
 
 }  // extern "C"

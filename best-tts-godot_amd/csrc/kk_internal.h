@@ -38,8 +38,6 @@ struct Context {
 constexpr size_t kScratchBytes = size_t{16} << 20;
 constexpr int kRowCounters = 65536;
 constexpr int kFlagSlots = 64;
-constexpr int kFlagConvh = 0;     // fp16 matrix-core convolution: a non-finite activation
-constexpr int kFlagConvhMax = 1;  // fp16 matrix-core convolution: max |x| (float bits)
 
 // DynamicQuantizeLinear's byte of x with the scale rounded to fp32 and the
 // zero point as a float: clamp(rint(x / scale) + zp, 0, 255)
@@ -70,6 +68,8 @@ int conv_i8_scratch_setup(int device);
 // Drops the record of what a packed ConvInteger weight buffer at `p` was
 // made from (kk_free calls it: the address may next hold anything).
 void conv_i8_forget_pack(const void* p);
+// The same for a packed fp16 matrix-core convolution weight (kk_conv_f16.hip).
+void convh_forget_pack(const void* p);
 
 // Thread-local last error; set_error returns `code` so call sites can
 // `return set_error(KK_E_ARG, "...")`.

@@ -471,6 +471,7 @@ int kk_free(void* dptr) {
   p.in_pool.insert(dptr);
   p.free_lists[it->second].push_back(dptr);
   conv_i8_forget_pack(dptr);
+  convh_forget_pack(dptr);
   p.pooled_bytes += it->second;
   p.live_bytes -= it->second;
   return KK_OK;

@@ -318,14 +318,18 @@ def dispatch(op, node_input, node_output, at, env):
     elif op == "DequantizeLinear":
         out = ops.dequantize(to_device(x), to_device(y), to_device(inp(2)))
     elif op == "Conv":
+        # attribute "packed" (set by a graph at load): the name of this
+        # constant weight's kk_conv_pack layout in env
         out = ops.conv1d(_f32(to_device(x)), to_device(y), _f32(to_device(inp(2))),
                          at.get("pads", [0, 0]), at.get("strides", [1])[0],
-                         at.get("dilations", [1])[0], at.get("group", 1))
+                         at.get("dilations", [1])[0], at.get("group", 1),
+                         packed=env.get(at.get("packed")))
     elif op == "ConvTranspose":
         out = ops.conv_transpose1d(_f32(to_device(x)), to_device(y), _f32(to_device(inp(2))),
                                    at.get("pads", [0, 0]), at.get("strides", [1])[0],
                                    at.get("dilations", [1])[0], at.get("group", 1),
-                                   at.get("output_padding", [0])[0])
+                                   at.get("output_padding", [0])[0],
+                                   packed=env.get(at.get("packed")))
 
     elif op == "CumSum":
         out = ops.cumsum(_f32(to_device(x)), int(np.asarray(to_host(y)).item()))

@@ -216,9 +216,15 @@ class PackedGraph:
         """Each quantised conv with its bias quantisation folded in whose
         weight and weight zero point are constants gets its weights packed
         once (ops.conv_integer_pack), under "<weight>#packed"; its node names
-        that in attribute "packed" and skips the per-call re-layout."""
+        that in attribute "packed" and skips the per-call re-layout.  So does
+        each Conv / ConvTranspose with a constant fp16 weight that the fp16
+        matrix cores take (group 1, a transposed one with dilation 1, at
+        most 8 taps a row: ops.conv_pack)."""
         packs = {}
         for k, (op, ins, outs, at) in enumerate(self.nodes):
+            if op in ("Conv", "ConvTranspose"):
+                self._pack_fp16_conv(k, op, ins, outs, at, packs)
+                continue
             if op != "QConvScaled" or not at.get("bias_quant"):
                 continue
             w, wz = ins[1], ins[3]
@@ -240,6 +246,24 @@ class PackedGraph:
                 self.weights[packs[key]] = ops.conv_integer_pack(
                     self.weights[w], self.weights[wz] if wz else None)
             self.nodes[k] = (op, ins, outs, dict(at, packed=packs[key]))
+
+    def _pack_fp16_conv(self, k, op, ins, outs, at, packs):
+        w = ins[1] if len(ins) > 1 else ""
+        wt = self.weights.get(w)
+        if not isinstance(wt, DeviceTensor) or wt.dtype != np.float16 or wt.ndim != 3:
+            return
+        tr = op == "ConvTranspose"
+        stride = int(at.get("strides", [1])[0])
+        if int(at.get("group", 1)) != 1 or (tr and int(at.get("dilations", [1])[0]) != 1):
+            return
+        taps = -(-wt.shape[2] // stride) if tr else wt.shape[2]
+        if taps > 8:
+            return
+        key = (w, tr, stride if tr else 1)
+        if key not in packs:
+            packs[key] = f"{w}#{'t' if tr else 'c'}{key[2]}#packed"
+            self.weights[packs[key]] = ops.conv_pack(wt, None, tr, key[2])
+        self.nodes[k] = (op, ins, outs, dict(at, packed=packs[key]))
 
     def _check_finite(self, i, env):
         """Strict mode (ref_runtime.py:404-418): raises at the first float

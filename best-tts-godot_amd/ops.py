@@ -192,28 +192,62 @@ def matmul(a, w, w_scale=None, w_zp=None, alpha=1.0):
 
 
 def conv1d(x, w, bias=None, pads=(0, 0), stride=1, dilation=1, group=1,
-           w_scale=None, w_zp=None):
+           w_scale=None, w_zp=None, packed=None):
+    """Conv1d; with `packed` (conv_pack(w, w_zp) of this very w) the
+    weights are not laid out for the call."""
     x = x.contiguous()
+    w = w.contiguous()
     n, _, L = x.shape
     cout, _, k = w.shape
     lout = (L + pads[0] + pads[1] - dilation * (k - 1) - 1) // stride + 1
     out = DeviceTensor.empty((n, cout, max(lout, 0)), np.float32)
-    _lib.call("kk_conv1d", out.desc(), x.desc(), w.contiguous().desc(), _d(w_scale), _d(w_zp),
+    if packed is not None:
+        if group != 1:
+            raise ValueError("conv1d: packed weights need group 1")
+        _lib.call("kk_conv1d_packed", out.desc(), x.desc(), w.desc(), packed.desc(), _d(w_scale),
+                  _d(w_zp), _d(bias), int(stride), int(dilation), int(pads[0]), int(pads[1]))
+        return out
+    _lib.call("kk_conv1d", out.desc(), x.desc(), w.desc(), _d(w_scale), _d(w_zp),
               _d(bias), int(stride), int(dilation), int(pads[0]), int(pads[1]), int(group))
     return out
 
 
 def conv_transpose1d(x, w, bias=None, pads=(0, 0), stride=1, dilation=1, group=1,
-                     output_padding=0, w_scale=None, w_zp=None):
+                     output_padding=0, w_scale=None, w_zp=None, packed=None):
+    """ConvTranspose1d; with `packed` (conv_pack(w, w_zp, True, stride) of
+    this very w) the weights are not laid out for the call."""
     x = x.contiguous()
+    w = w.contiguous()
     n, _, L = x.shape
     _, cout_g, k = w.shape
     lfull = (L - 1) * stride + dilation * (k - 1) + 1 + output_padding
     out = DeviceTensor.empty((n, cout_g * group, lfull - pads[0] - pads[1]), np.float32)
-    _lib.call("kk_conv_transpose1d", out.desc(), x.desc(), w.contiguous().desc(), _d(w_scale),
+    if packed is not None:
+        if group != 1 or dilation != 1:
+            raise ValueError("conv_transpose1d: packed weights need group 1 and dilation 1")
+        _lib.call("kk_conv_transpose1d_packed", out.desc(), x.desc(), w.desc(), packed.desc(),
+                  _d(w_scale), _d(w_zp), _d(bias), int(stride), int(pads[0]), int(pads[1]),
+                  int(output_padding))
+        return out
+    _lib.call("kk_conv_transpose1d", out.desc(), x.desc(), w.desc(), _d(w_scale),
               _d(w_zp), _d(bias), int(stride), int(dilation), int(pads[0]), int(pads[1]),
               int(group), int(output_padding))
     return out
+
+
+def conv_pack(w, w_zp=None, transposed=False, stride=1):
+    """The packed form of a constant Conv (transposed=False, any stride) or
+    ConvTranspose (transposed=True, this stride) weight: fp16, or int8/uint8
+    with its int8/uint8 zero point, laid out once for the fp16 matrix cores
+    (uint8 bytes on the device), for conv1d / conv_transpose1d(packed=...)."""
+    w = w.contiguous()
+    cin, cout = (w.shape[0], w.shape[1]) if transposed else (w.shape[1], w.shape[0])
+    nbytes = ctypes.c_int64(0)
+    _lib.call("kk_conv_packed_bytes", int(bool(transposed)), int(cin), int(cout), int(w.shape[2]),
+              int(stride), ctypes.byref(nbytes))
+    packed = DeviceTensor.empty((nbytes.value,), np.uint8)
+    _lib.call("kk_conv_pack", packed.desc(), w.desc(), _d(w_zp), int(bool(transposed)), int(stride))
+    return packed
 
 
 # ------------------------------------------------- quantized integer path

@@ -228,6 +228,37 @@ int kk_conv_transpose1d(const kk_tensor* out, const kk_tensor* x,
                         const kk_tensor* w_zp, const kk_tensor* bias,
                         int stride, int dilation, int pad0, int pad1,
                         int group, int output_padding);
+/* Constant Conv / ConvTranspose weights laid out once for the fp16 matrix
+ * cores: the same convolutions as kk_conv1d / kk_conv_transpose1d (the
+ * Conv :637-640 and ConvTranspose :646-651 branches over op_conv1d,
+ * ref_runtime.py:58-103), whose weights the reference dequantizes on every
+ * call.  A graph whose weights do not change between calls packs them at
+ * load (fp16, or int8/uint8 less its per-tensor or per-channel int8/uint8
+ * zero point; group 1).  kk_conv_packed_bytes gives the size of the pack
+ * (transposed: ConvTranspose1d with this stride; else Conv1d, any stride);
+ * kk_conv_pack writes it into `packed` (uint8, contiguous, 256-byte aligned,
+ * that many bytes). */
+int kk_conv_packed_bytes(int transposed, int64_t cin, int64_t cout, int64_t k,
+                         int stride, int64_t* bytes);
+int kk_conv_pack(const kk_tensor* packed, const kk_tensor* w,
+                 const kk_tensor* w_zp, int transposed, int stride);
+/* kk_conv1d (group 1) and kk_conv_transpose1d (group 1, dilation 1) on
+ * weights packed by kk_conv_pack; w (the tensor the pack was made from,
+ * with the same zero point) gives the shapes, and the call fails (KK_E_ARG)
+ * unless the last kk_conv_pack into `packed` read this very w for this
+ * operation and stride.  Shapes the matrix cores do not take run the fp32
+ * kernels on w itself. */
+int kk_conv1d_packed(const kk_tensor* out, const kk_tensor* x,
+                     const kk_tensor* w, const kk_tensor* packed,
+                     const kk_tensor* w_scale, const kk_tensor* w_zp,
+                     const kk_tensor* bias, int stride, int dilation,
+                     int pad0, int pad1);
+int kk_conv_transpose1d_packed(const kk_tensor* out, const kk_tensor* x,
+                               const kk_tensor* w, const kk_tensor* packed,
+                               const kk_tensor* w_scale,
+                               const kk_tensor* w_zp, const kk_tensor* bias,
+                               int stride, int pad0, int pad1,
+                               int output_padding);
 
 /* --------------------------------------------- quantized integer path
  * DynamicQuantizeLinear (ref_runtime.py:106-116): y = clip(rint(x / scale)

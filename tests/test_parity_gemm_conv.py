@@ -459,9 +459,10 @@ def test_fp16_weight_conv_large_activations(gpu, oracle):
 
 @pytest.mark.parametrize("bad", [np.inf, -np.inf, np.nan])
 def test_fp16_weight_conv_nonfinite_falls_back(gpu, oracle, bad):
-    """A non-finite activation sends the whole convolution to the fp32
-    kernels (launched after the matrix-core pass, run only if flagged), which
-    propagate it as numpy does; the next call runs on the matrix cores again."""
+    """A non-finite activation sends each block whose input window holds it
+    to scalar fp32 products and sums (inside the same launch), which
+    propagate it as numpy does; the other blocks, and the next call, run on
+    the matrix cores."""
     r = rng(11)
     x = r.normal(0, 1, (1, 256, 2000)).astype(np.float32)
     x[0, 5, 123] = bad
@@ -677,3 +678,80 @@ def test_conv_packed_refuses_another_weight(gpu):
     with pytest.raises(gpu._lib.KKError, match="not made by kk_conv_integer_pack"):
         other = gpu.DeviceTensor.empty(packed.shape, np.uint8)
         gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, pads=(1, 1), packed=other)
+
+
+@pytest.mark.parametrize("case", F16MC)
+def test_fp16_weight_conv_packed(gpu, oracle, case):
+    """kk_conv1d_packed / kk_conv_transpose1d_packed: the weights laid out
+    once by kk_conv_pack give the per-call path's bits (the same kernel on
+    the same layout) on two calls in a row with different activations, each
+    within the oracle's bar."""
+    kind, n, cin, cout, k, L, p0, p1, s, d, op, wdt = case
+    r = rng(44)
+    shape = (cin, cout, k) if kind == "convT" else (cout, cin, k)
+    bshape = (1, cout, 1) if kind == "convT" else (cout, 1, 1)
+    sc = zp = None
+    if wdt == "f16":
+        w = r.normal(0, 0.05, shape).astype(np.float16)
+        wdeq = w
+    elif wdt == "i8":
+        w, sc = int8_weight(r, shape)
+        wdeq = oracle.dequantize(w, sc)
+    else:
+        w = r.integers(0, 256, shape).astype(np.uint8)
+        sc = r.uniform(1e-4, 1e-3, cout).astype(np.float32)
+        zp = r.integers(100, 156, cout).astype(np.uint8)
+        wdeq = oracle.dequantize(w, sc.reshape(bshape), zp.reshape(bshape))
+    dv = gpu.to_device
+    wd = dv(w)
+    kw = dict(w_scale=dv(np.asarray(sc)) if sc is not None else None,
+              w_zp=dv(zp) if zp is not None else None)
+    packed = gpu.ops.conv_pack(wd, kw["w_zp"], kind == "convT", s)
+    for call in range(2):
+        x = r.normal(0, 1 + call, (n, cin, L)).astype(np.float32)
+        b = r.normal(0, 0.1, cout).astype(np.float32)
+        if kind == "convT":
+            args = (dv(x), wd, dv(b), (p0, p1), s, d, 1, op)
+            want = gpu.ops.conv_transpose1d(*args, **kw).numpy()
+            got = gpu.ops.conv_transpose1d(*args, packed=packed, **kw).numpy()
+            ref = oracle.conv_transpose1d(x, wdeq, b, (p0, p1), s, d, 1, op)
+        else:
+            args = (dv(x), wd, dv(b), (p0, p1), s, d)
+            want = gpu.ops.conv1d(*args, **kw).numpy()
+            got = gpu.ops.conv1d(*args, packed=packed, **kw).numpy()
+            ref = oracle.conv1d(x, wdeq, b, (p0, p1), s, d)
+        assert_bitexact(got, want, f"packed {wdt}-weight {case} call {call}")
+        check(got, ref, f"packed {wdt}-weight {case} call {call}")
+
+
+def test_fp16_weight_conv_packed_refuses_mismatch(gpu):
+    """A packed Conv / ConvTranspose weight is used only with the tensor, zero
+    point, operation and stride it was packed for."""
+    r = rng(45)
+    dv = gpu.to_device
+    w = dv(r.integers(0, 256, (256, 128, 12)).astype(np.uint8))
+    w2 = dv(r.integers(0, 256, (256, 128, 12)).astype(np.uint8))
+    wz, wz2 = dv(np.array(120, np.uint8)), dv(np.array(121, np.uint8))
+    sc = dv(np.array(0.002, np.float32))
+    x = dv(r.normal(0, 1, (1, 256, 600)).astype(np.float32))
+    packed = gpu.ops.conv_pack(w, wz, True, 6)
+    ok = gpu.ops.conv_transpose1d(x, w, None, (3, 3), 6, w_scale=sc, w_zp=wz, packed=packed)
+    assert ok.shape == (1, 128, 3600)
+    E = gpu._lib.KKError
+    with pytest.raises(E, match="another weight tensor"):
+        gpu.ops.conv_transpose1d(x, w2, None, (3, 3), 6, w_scale=sc, w_zp=wz, packed=packed)
+    with pytest.raises(E, match="another weight zero point"):
+        gpu.ops.conv_transpose1d(x, w, None, (3, 3), 6, w_scale=sc, w_zp=wz2, packed=packed)
+    with pytest.raises(E, match="another stride|packed must be"):
+        gpu.ops.conv_transpose1d(x, w, None, (3, 3), 4, w_scale=sc, w_zp=wz, packed=packed)
+    with pytest.raises(E, match="not made by kk_conv_pack"):
+        gpu.ops.conv_transpose1d(x, w, None, (3, 3), 6, w_scale=sc, w_zp=wz,
+                                 packed=gpu.DeviceTensor.empty(packed.shape, np.uint8))
+    wc = dv(r.normal(0, 0.05, (128, 128, 3)).astype(np.float16))
+    pc = gpu.ops.conv_pack(wc, None, False, 1)
+    xc = dv(r.normal(0, 1, (1, 128, 900)).astype(np.float32))
+    gpu.ops.conv1d(xc, wc, None, (1, 1), packed=pc)
+    wt = dv(r.normal(0, 0.05, (128, 128, 3)).astype(np.float16))
+    pt = gpu.ops.conv_pack(wt, None, True, 1)  # the same size as pc, packed for ConvTranspose
+    with pytest.raises(E, match="another operation"):
+        gpu.ops.conv1d(xc, wt, None, (1, 1), packed=pt)
