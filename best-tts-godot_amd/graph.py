@@ -296,7 +296,7 @@ class PackedGraph:
                 node=i, op=op, output=o, inputs=described)
 
     def run(self, input_ids, style, speed=1.0, keep=(), pcm16=False, notch=True, gain=1.0,
-            strict=False, max_nodes=None):
+            strict=False, max_nodes=None, start=0, inject=None):
         """Returns the waveform on the host: float32 samples, or with
         `pcm16` the 16-bit PCM samples (int16) the reference's output stage
         makes of them on the device (audio.gd:59-106), through the notch
@@ -308,15 +308,20 @@ class PackedGraph:
         it is slow); `max_nodes` runs only the first that many nodes of the
         walk (executor.gd:67-72, 306-307) and returns None when the output
         was not reached -- `keep` names the tensors to look at then, in
-        `last_env`."""
+        `last_env`; `start` skips the walk's first nodes, whose outputs the
+        rest reads from `inject` ({tensor id: array}, floats placed on the
+        device), to run a part of the graph from given values."""
         env = dict(self.weights)
         env[self.inputs["input_ids"]] = np.asarray(input_ids, np.int64).reshape(1, -1)
         env[self.inputs["style"]] = to_device(np.asarray(style, np.float32).reshape(1, 256))
         env[self.inputs["speed"]] = to_device(np.asarray([speed], np.float32))
+        for name, v in (inject or {}).items():
+            v = np.asarray(v)
+            env[str(name)] = to_device(v) if v.dtype.kind == "f" else v
         keep = {str(k) for k in keep}
         frees = self.frees
         limit = len(self.nodes) if max_nodes is None or max_nodes < 0 else min(max_nodes, len(self.nodes))
-        for i in range(limit):
+        for i in range(start, limit):
             op, ins, outs, at = self.nodes[i]
             try:
                 dispatch(op, ins, outs, at, env)

@@ -15,9 +15,12 @@ Checkpoints (tensor ids of the packed graph):
         holds them to 2^-11 relative, far inside the waveform gate).
 With more than 8 ids the last frames of the three long checkpoints are kept
 too (t<id>_tail), so the end of the utterance is checked as well as its
-start.
+start, and so is every tensor the rest of the graph reads from the part up
+to the durations (b<id>: the text encoder's output, the prosody features,
+the rounded durations and the style projections, 0.8 MB at 128 ids), from
+which a test runs the decoder part on its own.
 Run from the repository root: python tests/golden/make_graph_golden.py [N]
-(N = 128 takes several minutes of CPU time.)
+(N = 128 takes about 22 minutes of CPU time on 2.7 GHz Xeon cores.)
 """
 import importlib
 import os
@@ -43,14 +46,28 @@ def tail(v, axis, n):
     return np.ascontiguousarray(np.take(np.asarray(v), np.arange(max(0, m - n), m), axis=axis))
 
 
+def boundary(g, weights):
+    """Non-weight tensors made up to the node that writes the rounded
+    durations (2432) and read after it."""
+    idx = next(i for i, n in enumerate(g["nodes"]) if 2432 in n[2])
+    made = {int(v) for v in g["inputs"].values()}
+    for n in g["nodes"][:idx + 1]:
+        made |= {t for t in n[2] if t >= 0}
+    read = set()
+    for n in g["nodes"][idx + 1:]:
+        read |= {t for t in n[1] if t >= 0}
+    return sorted((made & read) - {int(k) for k in weights})
+
+
 def main():
     from oracle import kpk_run
     kkg = importlib.import_module("best-tts-godot_amd.graph")
     g = kkg.load_graph()
     w = kkg.synth_weights(g, 0)
     ids, style, speed = kkg.synth_inputs(N_IDS, 0)
+    bnd = boundary(g, w) if N_IDS > 8 else []
     t = time.time()
-    wav, cap = kpk_run.run(g, w, ids, style, speed, capture=CHECK)
+    wav, cap = kpk_run.run(g, w, ids, style, speed, capture=CHECK + bnd)
     print(f"oracle graph: {time.time() - t:.1f} s, waveform {wav.shape}")
     out = {"ids": ids, "style": style, "wave_len": np.array(wav.size),
            "wave_f16": np.asarray(wav, np.float32).reshape(-1).astype(np.float16)}
@@ -59,6 +76,8 @@ def main():
         out[f"t{k}"] = head(v, *HEAD[k]) if k in HEAD else v
         if k in HEAD and N_IDS > 8:
             out[f"t{k}_tail"] = tail(v, *HEAD[k])
+    for k in bnd:
+        out[f"b{k}"] = np.asarray(cap[k])
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), f"graph_golden_t{N_IDS}.npz")
     np.savez_compressed(path, **out)
     pre = np.asarray(cap[2430]).reshape(-1)
