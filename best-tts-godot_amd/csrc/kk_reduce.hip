@@ -1066,6 +1066,12 @@ struct NpTail {
   uint8_t ca[kTailMax], cb[kTailMax];
   uint8_t lev_end[kNpDepth];
 };
+// lo, n, ca and cb as 32-bit words (np_resident_kernel copies them as such)
+constexpr int kPlanWords = 5 * kTailMax / 4;
+static_assert(offsetof(NpTail, lo) % 4 == 0 && offsetof(NpTail, n) == offsetof(NpTail, lo) + 2 * kTailMax &&
+                  offsetof(NpTail, ca) == offsetof(NpTail, n) + kTailMax &&
+                  offsetof(NpTail, cb) == offsetof(NpTail, ca) + kTailMax && (5 * kTailMax) % 4 == 0,
+              "the plan's arrays are contiguous 32-bit words");
 
 // The plan in LDS (its lane-indexed reads would otherwise be memory loads)
 // and the partial block's node values.
@@ -1430,6 +1436,7 @@ struct ResArgs {
   int64_t C, T;
   float eps;
   int stage_off;  // floats from the LDS base to the waves' stages
+  int delay;      // MODE 0: the delayed half's wait, in 100 MHz clock ticks (0: none)
   Affine af;
   NpTail tail;
 };
@@ -1466,11 +1473,25 @@ __global__ void __launch_bounds__(128 * NB) np_resident_kernel(ResArgs A) {
   __shared__ float tv[2 * kTailMax];
   __shared__ float2 wmm[NT / 64];
   __shared__ float bc[4];
-  __shared__ uint16_t p_lo[kTailMax];
-  __shared__ uint8_t p_n[kTailMax], p_ca[kTailMax], p_cb[kTailMax];
+  // the tree plan (lo, n, ca, cb as laid out in NpTail)
+  __shared__ uint32_t plan_w[kPlanWords];
+  const uint16_t* const p_lo = reinterpret_cast<const uint16_t*>(plan_w);
+  const uint8_t* const p_n = reinterpret_cast<const uint8_t*>(plan_w) + 2 * kTailMax;
+  const uint8_t* const p_ca = p_n + kTailMax;
+  const uint8_t* const p_cb = p_ca + kTailMax;
   float* const res_tail = res_lds;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int64_t row = blockIdx.x;
+  // MODE 0 with one block per CU: each block loads its row, reduces it and
+  // stores it, so with every block in step HBM idles while they reduce and
+  // no store overlaps a load.  Alternate groups of eight blocks (one a
+  // XCD) start their loads A.delay ticks later -- about what the other
+  // half's loads take -- so their loads overlap the first half's
+  // statistics and stores.  The wait ends on the clock alone.
+  if (MODE == 0 && A.delay && ((blockIdx.x >> 3) & 1)) {
+    const uint64_t until = __builtin_amdgcn_s_memrealtime() + static_cast<uint64_t>(A.delay);
+    while (__builtin_amdgcn_s_memrealtime() < until) __builtin_amdgcn_s_sleep(4);
+  }
   const float* xr = A.x + row * A.T;
   const int m = A.tail.m, nleaf = A.tail.nleaf;
   // the partial block (buffer loads: past m they return zeros), the tree
@@ -1484,16 +1505,14 @@ __global__ void __launch_bounds__(128 * NB) np_resident_kernel(ResArgs A) {
         kk_f4v, __builtin_amdgcn_raw_buffer_load_b128(rsrc, 16 * (t + i * NT), 0, 0));
     u[i] = make_float4(r.x, r.y, r.z, r.w);
   }
-  if (w == NT / 64 - 1) {
+  if (t == NT - 64) {
     // the tree plan into LDS (its lane-indexed reads would otherwise be
-    // memory loads each time), by one wave before its row loads: a wait
-    // for the plan after them would wait for them all
-    for (int i = lane; i < kTailMax; i += 64) {
-      p_lo[i] = A.tail.lo[i];
-      p_n[i] = A.tail.n[i];
-      p_ca[i] = A.tail.ca[i];
-      p_cb[i] = A.tail.cb[i];
-    }
+    // memory loads each time), one lane: uniform reads of the kernel
+    // argument are scalar loads, which wait on their own counter and not on
+    // the row's loads
+    const uint32_t* const src = reinterpret_cast<const uint32_t*>(A.tail.lo);
+#pragma unroll
+    for (int q = 0; q < kPlanWords; ++q) plan_w[q] = src[q];
   }
   // (the partial block's loads stay ahead of the row's, so that waiting for
   // them leaves those in flight)
@@ -1995,6 +2014,14 @@ static int np_resident_launch(float* out, const float* x, int64_t rows, int64_t 
   A.T = T;
   A.eps = eps;
   A.af = af;
+  // the delayed half (rows of one wave of blocks, at most one a CU; with
+  // more rows than CUs later blocks start staggered anyway): the other
+  // half's bytes at 6.1 TB/s (what one block a row reads at when no block
+  // stores), in ticks of the 100 MHz clock (s_memrealtime)
+  const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  if (out && 4 * rows >= 3 * cus && rows <= cus)
+    A.delay = static_cast<int>(0.5 * static_cast<double>(rows * T) * 4.0 / 6.1e12 * 1e8);
+
   const int nb = static_cast<int>(T / kNpBlock);
   np_tail_plan(static_cast<int>(T - nb * kNpBlock), &A.tail);
   // the partial block, then 8 leaves of 136 floats a wave
