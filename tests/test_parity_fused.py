@@ -254,8 +254,13 @@ def norm_chain(affine, leaky):
                                               (40, 15004, False, True),
                                               # longer rows (statistics passes): a
                                               # partial last block of 1696, the
-                                              # decoder's 430800, a 6-element one
+                                              # decoder's 430800 (2 and 128 rows),
+                                              # nine whole blocks and no partial one,
+                                              # sixteen, 63 of them and 100 elements,
+                                              # a 6-element one
                                               (4, 100000, True, False), (2, 430800, True, True),
+                                              (128, 430800, True, False), (40, 73728, False, False),
+                                              (6, 131072, True, True), (2, 516196, True, False),
                                               (3, 81926, False, False)])
 def test_instance_norm_chain(gpu, oracle, C, T, affine, leaky):
     r = rng(22)
@@ -426,6 +431,7 @@ def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leak
                                       (16, 15004, "leaky"),
                                       # longer rows (statistics passes)
                                       (4, 100000, "snake"), (2, 430800, "leaky"),
+                                      (128, 430800, "leaky"), (40, 73732, "snake"),
                                       (3, 81926, "affine")])
 def test_instance_norm_quant_chain(gpu, oracle, C, T, kind):
     """The InstanceNorm chain (plain, affine, + LeakyRelu, + snake) -> Cast
