@@ -225,8 +225,8 @@ __global__ void __launch_bounds__(kDqlSmallThreads) dql_small(const float* __res
 // The per-step product h @ (q - zp) runs on the int8 matrix cores, exactly
 // in integers: h is scaled by a power of two (chosen from max|h0| for the
 // first step, 2^30 after it, since |h| = |o tanh(c)| <= 1 from then on),
-// rounded, and split into four signed base-256 digits,
-// which are four rows of the A operand of v_mfma_i32_16x16x64_i8; R's raw
+// rounded, and split into four signed base-256 digits, which are rows of
+// the 2-of-4 sparse A operand of v_smfmac_i32_16x16x128_i8 (below); R's raw
 // int8 values are the B operand and stay in registers for all steps (each
 // wave owns four 16-column tiles: 64 VGPRs).  The four digit sums of a
 // column recombine exactly in int64 (< 2^45), the zero point comes out
@@ -242,6 +242,7 @@ constexpr int kLstmMaxH = kLstmThreads / 4;
 // outputs of a chunk leave in one store per thread.
 constexpr int kLstmChunk = 4;
 typedef int lstm_v4i __attribute__((ext_vector_type(4)));
+typedef int lstm_v8i __attribute__((ext_vector_type(8)));
 
 struct LstmArgs {
   const float* xw;       // [ndir][seq * batch][4H] x @ deq(W) + (wb + rb)
@@ -269,11 +270,34 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// The gate activations within a few ulp: sigmoid(x) = 1 / (1 + e) for
+// x >= 0, e / (1 + e) below, with e = exp(-|x|) on the hardware exp2
+// (kk_exp_neg) and the hardware reciprocal; tanh(x) = (1 - e) / (1 + e) with
+// e = exp(-2|x|) and x's sign, or for |x| < 1/16 (where 1 - e cancels) its
+// Taylor series to x^7, whose next term is below 2^-30 |x|.
+__device__ __forceinline__ float lstm_sigmoid(float x) {
+  const float e = kk_exp_neg(-fabsf(x));
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);
+  return x >= 0.0f ? r : e * r;
+}
+__device__ __forceinline__ float lstm_tanh(float x) {
+  const float a = fabsf(x);
+  const float e = kk_exp_neg(-2.0f * a);
+  const float big = __builtin_copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
+  const float x2 = x * x;
+  float p = __builtin_fmaf(-17.0f / 315.0f, x2, 2.0f / 15.0f);
+  p = __builtin_fmaf(p, x2, -1.0f / 3.0f);
+  const float small = __builtin_fmaf(x * x2, p, x);
+  return a < 0.0625f ? small : big;
+}
+
 __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
   // R's staging area at set-up, then the double buffer of input projections
   // [2][kLstmChunk][4H] floats (both 32 KiB)
   __shared__ __align__(16) unsigned char big[32 * kLstmThreads];
-  __shared__ __align__(16) int8_t hd[4][kLstmMaxH];  // digits of the scaled h
+  // digits of the scaled h: hd[i][p] holds digit i of the units k with
+  // (k / 2) % 2 == p, at (k / 4) * 2 + k % 2 (the sparse A operand's order)
+  __shared__ __align__(16) int8_t hd[4][2][kLstmMaxH / 2];
   __shared__ float gs[kLstmThreads];
   __shared__ float hring[kLstmChunk][kLstmMaxH];     // this chunk's h, for ys
   __shared__ float wmax[kLstmMaxH / 64];
@@ -284,15 +308,23 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
   const int64_t d = blockIdx.x / A.batch, b = blockIdx.x % A.batch;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar addresses
-  const float rs = load_as_f32(A.r_scale, A.r_scale_dt, A.r_scale_n > 1 ? d : 0);
-  const long long rz =
+  // block-uniform: held in scalar registers (a vector register would be
+  // spilled, and its reload would sit in every step)
+  const float rs = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(
+      int, load_as_f32(A.r_scale, A.r_scale_dt, A.r_scale_n > 1 ? d : 0))));
+  long long rz =
       A.r_zp ? static_cast<long long>(load_as_i64(A.r_zp, A.r_zp_dt, A.r_zp_n > 1 ? d : 0)) : 0;
+  rz = static_cast<long long>(
+      (static_cast<unsigned long long>(static_cast<unsigned>(
+           __builtin_amdgcn_readfirstlane(static_cast<int>(rz >> 32))))
+       << 32) |
+      static_cast<unsigned>(__builtin_amdgcn_readfirstlane(static_cast<int>(rz))));
   const int8_t* R = A.r + d * static_cast<int64_t>(H) * G4;
   const float* xw = A.xw + d * A.seq * A.batch * G4;
   // B fragments: wave wv owns columns [64 wv, 64 wv + 64), four tiles of
   // 16; lane (n, g) = (lane % 16, lane / 16) holds R[ks*64 + 16g + e][col].
   // R arrives through LDS in 32-row chunks (coalesced 4-byte loads).
-  lstm_v4i bf[4][4];
+  lstm_v8i bf[4][2];  // [tile][k-step of 128]: the 64-row k-steps 2 kk and 2 kk + 1 side by side
 #pragma unroll
   for (int chunk = 0; chunk < kLstmMaxH / 32; ++chunk) {
     __syncthreads();
@@ -321,7 +353,8 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
             word |= static_cast<uint32_t>(static_cast<uint8_t>(rbuf[r0 + 4 * q + e][j])) << (8 * e);
           w[q] = static_cast<int>(word);
         }
-        bf[ct][ks] = lstm_v4i{w[0], w[1], w[2], w[3]};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) bf[ct][ks >> 1][4 * (ks & 1) + q] = w[q];
       }
     }
   }
@@ -373,7 +406,7 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
   {
     int ex = 0;
     (void)frexpf(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])), &ex);
-    shift = 30 - ex;
+    shift = __builtin_amdgcn_readfirstlane(30 - ex);
   }
   float4 pf = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   if (seq > 0) {
@@ -387,7 +420,7 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) asm volatile("" : "+v"(bf[ct][ks]));
+      for (int kk = 0; kk < 2; ++kk) asm volatile("" : "+v"(bf[ct][kk]));
     // (b) scale, round and split h into digits (and, with a zero point, the
     // integer sum of the scaled h).  h * 2^shift is exact in fp32 and below
     // 2^30 in magnitude, so it rounds to an int exactly.
@@ -397,7 +430,7 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int dg = ((v + 128) & 255) - 128;
-        hd[i][tid] = static_cast<int8_t>(dg);
+        hd[i][(tid >> 1) & 1][((tid >> 2) << 1) | (tid & 1)] = static_cast<int8_t>(dg);
         v = (v - dg) >> 8;
       }
       if (rz != 0) {
@@ -410,36 +443,59 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
     lds_barrier();
     if (s == 0 && step > 0) flush_chunk(kc - 1);  // hring is rewritten after the next barrier
     const long long hsum = rz != 0 ? (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]) : 0;
-    // (c) gates.  A row i carries digit i % 4 (rows 4q .. 4q+3 repeat the
-    // four digits), so tile ct's digit sums for its column n land in every
-    // lane group q: lane n + 16q, registers 0..3.  Lane l takes tile l / 16,
-    // i.e. column 64 wv + l, and applies that gate's activation itself.
+    // (c) gates, on the sparse int8 matrix cores: v_smfmac_i32_16x16x128_i8
+    // takes A as 2-of-4 structured (per group of four k, two values and
+    // their positions) against a dense 128-k slice of R, twice the k of the
+    // dense 16x16x64 for the same issue cost.  A row r (r % 8 = 2 i + p)
+    // holds digit i of h at the k pairs of parity p ((k / 2) % 2 == p), the
+    // other pair zero; rows 8..15 repeat 0..7.  Lane l of A (row l % 16, k
+    // group l / 16 of 32) reads its sixteen values contiguously from hd[i][p];
+    // R's fragments are the dense ones of k-steps 2 kk and 2 kk + 1 side by
+    // side (the sparse B operand's k order).  Tile ct's lane group q then
+    // holds rows 4q .. 4q+3: digits 0 and 1 (even q) or 2 and 3 (odd q), each
+    // as its two parities.  Lane l takes tile l / 16, i.e. column 64 wv + l;
+    // the other half of its column's digit sums comes from lane l ^ 16
+    // (v_permlane16_swap), and the four recombine exactly in int64.
     lstm_v4i acc[4] = {};
+    {
+      const int idx = (lane & 1) ? static_cast<int>(0xEEEEEEEEu) : 0x44444444;  // positions (2, 3) / (0, 1)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const lstm_v4i a = *reinterpret_cast<const lstm_v4i*>(&hd[lane & 3][ks * 64 + 16 * (lane >> 4)]);
+      for (int kk = 0; kk < 2; ++kk) {
+        const lstm_v4i a =
+            *reinterpret_cast<const lstm_v4i*>(&hd[(lane >> 1) & 3][lane & 1][64 * kk + 16 * (lane >> 4)]);
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        acc[ct] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bf[ct][ks], acc[ct], 0, 0, 0);
+        for (int ct = 0; ct < 4; ++ct) {
+          acc[ct] = __builtin_amdgcn_smfmac_i32_16x16x128_i8(a, bf[ct][kk], acc[ct], idx, 0, 0);
+        }
+      }
     }
     {
       const int q = lane >> 4;
-      const lstm_v4i r = q == 0 ? acc[0] : (q == 1 ? acc[1] : (q == 2 ? acc[2] : acc[3]));
+      // two digit sums (each over both parities) recombined: |.| < 2^22 + 2^30
+      int fa[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) fa[ct] = (acc[ct][0] + acc[ct][1]) + ((acc[ct][2] + acc[ct][3]) << 8);
+      const int own = q == 0 ? fa[0] : (q == 1 ? fa[1] : (q == 2 ? fa[2] : fa[3]));
+      const int send = q == 0 ? fa[1] : (q == 1 ? fa[0] : (q == 2 ? fa[3] : fa[2]));
+      // each lane keeps its own value in one of the two results and gets its
+      // partner's in the other
+      const auto pr = __builtin_amdgcn_permlane16_swap(send, send, false, false);
+      const int recv = static_cast<int>(static_cast<unsigned>(pr[0]) + static_cast<unsigned>(pr[1]) -
+                                        static_cast<unsigned>(send));
+      const int lo = (q & 1) ? recv : own, hi = (q & 1) ? own : recv;
       const int j = 64 * wv + lane;
-      if (j < G4) {
-        const long long dot = static_cast<long long>(r[0]) + (static_cast<long long>(r[1]) << 8) +
-                              (static_cast<long long>(r[2]) << 16) +
-                              (static_cast<long long>(r[3]) << 24);
+        if (j < G4) {
+        const long long dot = static_cast<long long>(lo) + (static_cast<long long>(hi) << 16);
         const float hr = static_cast<float>(ldexp(static_cast<double>(dot - rz * hsum), -shift));
         const float pre = xs[((kc & 1) * kLstmChunk + s) * G4 + j] + hr * rs;  // (xw + (wb + rb)) + h @ deq(R)
-        gs[j] = j < 3 * H ? 1.0f / (1.0f + expf(-pre)) : tanhf(pre);  // i, o, f: sigmoid; c: tanh
+        gs[j] = j < 3 * H ? lstm_sigmoid(pre) : lstm_tanh(pre);  // i, o, f: sigmoid; c: tanh
       }
     }
     lds_barrier();
     // (d) cell update of unit tid
     if (tid < H) {
       c = gs[2 * H + tid] * c + gs[tid] * gs[3 * H + tid];
-      h = gs[H + tid] * tanhf(c);
+      h = gs[H + tid] * lstm_tanh(c);
       hring[s][tid] = h;
     }
     // Chunk kc + 1 goes into the buffer chunk kc - 1 used (its last reader
