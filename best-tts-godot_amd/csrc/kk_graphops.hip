@@ -425,14 +425,15 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
     // integer sum of the scaled h).  h * 2^shift is exact in fp32 and below
     // 2^30 in magnitude, so it rounds to an int exactly.
     if (tid < kLstmMaxH) {
-      int v = tid < H ? static_cast<int>(rintf(ldexpf(h, shift))) : 0;
-      const int v0 = v;
+      const int v0 = tid < H ? static_cast<int>(rintf(ldexpf(h, shift))) : 0;
+      // the balanced digits d_i in [-128, 127] with v0 = sum d_i 256^i: as
+      // |v0| < 2^30, w = v0 + 0x80808080 lies in [0, 2^32) and its bytes are
+      // d_i + 128 (the carries ripple in the addition), so the bytes of
+      // w ^ 0x80808080 are the d_i as int8
+      const uint32_t dd = (static_cast<uint32_t>(v0) + 0x80808080u) ^ 0x80808080u;
+      const int hp = (tid >> 1) & 1, hpos = ((tid >> 2) << 1) | (tid & 1);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int dg = ((v + 128) & 255) - 128;
-        hd[i][(tid >> 1) & 1][((tid >> 2) << 1) | (tid & 1)] = static_cast<int8_t>(dg);
-        v = (v - dg) >> 8;
-      }
+      for (int i = 0; i < 4; ++i) hd[i][hp][hpos] = static_cast<int8_t>(dd >> (8 * i));
       if (rz != 0) {
         long long sum = v0;
 #pragma unroll
