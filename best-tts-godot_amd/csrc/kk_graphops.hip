@@ -270,27 +270,6 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// The gate activations within a few ulp: sigmoid(x) = 1 / (1 + e) for
-// x >= 0, e / (1 + e) below, with e = exp(-|x|) on the hardware exp2
-// (kk_exp_neg) and the hardware reciprocal; tanh(x) = (1 - e) / (1 + e) with
-// e = exp(-2|x|) and x's sign, or for |x| < 1/16 (where 1 - e cancels) its
-// Taylor series to x^7, whose next term is below 2^-30 |x|.
-__device__ __forceinline__ float lstm_sigmoid(float x) {
-  const float e = kk_exp_neg(-fabsf(x));
-  const float r = __builtin_amdgcn_rcpf(1.0f + e);
-  return x >= 0.0f ? r : e * r;
-}
-__device__ __forceinline__ float lstm_tanh(float x) {
-  const float a = fabsf(x);
-  const float e = kk_exp_neg(-2.0f * a);
-  const float big = __builtin_copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
-  const float x2 = x * x;
-  float p = __builtin_fmaf(-17.0f / 315.0f, x2, 2.0f / 15.0f);
-  p = __builtin_fmaf(p, x2, -1.0f / 3.0f);
-  const float small = __builtin_fmaf(x * x2, p, x);
-  return a < 0.0625f ? small : big;
-}
-
 __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
   // R's staging area at set-up, then the double buffer of input projections
   // [2][kLstmChunk][4H] floats (both 32 KiB)
@@ -489,14 +468,17 @@ __global__ void __launch_bounds__(kLstmThreads) lstm_recurrence(LstmArgs A) {
         const long long dot = static_cast<long long>(lo) + (static_cast<long long>(hi) << 16);
         const float hr = static_cast<float>(ldexp(static_cast<double>(dot - rz * hsum), -shift));
         const float pre = xs[((kc & 1) * kLstmChunk + s) * G4 + j] + hr * rs;  // (xw + (wb + rb)) + h @ deq(R)
-        gs[j] = j < 3 * H ? lstm_sigmoid(pre) : lstm_tanh(pre);  // i, o, f: sigmoid; c: tanh
+        // (libm's expf and tanhf and the IEEE division: the 84-second
+        // utterance's F0 curve feeds a running phase, whose end moves
+        // visibly with a few-ulp change here)
+        gs[j] = j < 3 * H ? 1.0f / (1.0f + expf(-pre)) : tanhf(pre);  // i, o, f: sigmoid; c: tanh
       }
     }
     lds_barrier();
     // (d) cell update of unit tid
     if (tid < H) {
       c = gs[2 * H + tid] * c + gs[tid] * gs[3 * H + tid];
-      h = gs[H + tid] * lstm_tanh(c);
+      h = gs[H + tid] * tanhf(c);
       hring[s][tid] = h;
     }
     // Chunk kc + 1 goes into the buffer chunk kc - 1 used (its last reader
