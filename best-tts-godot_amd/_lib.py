@@ -78,6 +78,9 @@ PROTOTYPES = {
     "kk_layernorm": [_T, _T, _T, _T, _T, _T, _i, _f],
     "kk_softmax": [_T, _T, _i],
     "kk_gemm": [_T, _T, _T, _T, _T, _f],
+    "kk_gemm_packed_bytes": [ctypes.c_int64, ctypes.c_int64, _i, ctypes.POINTER(ctypes.c_int64)],
+    "kk_gemm_pack": [_T, _T, _T],
+    "kk_gemm_packed": [_T] * 6 + [_f],
     "kk_conv1d": [_T, _T, _T, _T, _T, _T, _i, _i, _i, _i, _i],
     "kk_conv_transpose1d": [_T, _T, _T, _T, _T, _T, _i, _i, _i, _i, _i, _i],
     "kk_conv_packed_bytes": [_i, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, _i,

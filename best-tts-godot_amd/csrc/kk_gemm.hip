@@ -375,6 +375,7 @@ struct GemmArgs {
   // and gemm_splitk_reduce forms out
   int splits;
   float* part;
+  const void* bpack;   // B packed by kk_gemm_pack (the bf16 matrix-core path), or NULL
 };
 
 // A kinds: 0 = K-contiguous quads of TA, 1 = scalar gather.
@@ -797,7 +798,7 @@ static int launch_gemm(const GemmArgs& args, int64_t batch, bool weights_rounded
     int st = KK_OK;
     if (gemm_dq_try(static_cast<const float*>(args.a), args.a_si, args.b, args.b_dt, args.b_si,
                     args.dq, args.out, args.som, args.son, args.bm, args.M, args.N, args.K, batch,
-                    args.alpha, args.only_if, &st))
+                    args.alpha, args.only_if, args.bpack, &st))
       return st;
   }
   const TileSize ts = pick_tile(args.M, args.N, batch);
@@ -953,13 +954,18 @@ int convh_check_packed(const kk_tensor* packed, const kk_tensor* w, const kk_ten
                        bool transposed, int64_t stride, const char* who);
 
 int gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
-         const kk_tensor* w_zp, float alpha, bool weights_rounded) {
+         const kk_tensor* w_zp, float alpha, bool weights_rounded, const kk_tensor* packed) {
+  const char* who = packed ? "kk_gemm_packed" : "kk_gemm";
   GemmArgs G{};
   int64_t batch = 0;
-  KK_TRY(setup_gemm(&G, out, a, w, &batch, "kk_gemm"));
-  if (!is_float(a->dtype)) return set_error(KK_E_ARG, "kk_gemm: a must be f32/f16");
-  if (out->dtype != KK_F32) return set_error(KK_E_ARG, "kk_gemm: out must be fp32");
-  KK_TRY(make_dequant(&G.dq, w, w_scale, w_zp, G.N, "kk_gemm"));
+  KK_TRY(setup_gemm(&G, out, a, w, &batch, who));
+  if (!is_float(a->dtype)) return set_error(KK_E_ARG, "%s: a must be f32/f16", who);
+  if (out->dtype != KK_F32) return set_error(KK_E_ARG, "%s: out must be fp32", who);
+  KK_TRY(make_dequant(&G.dq, w, w_scale, w_zp, G.N, who));
+  if (packed) {
+    KK_TRY(gemm_check_packed(packed, w, w_zp, who));
+    G.bpack = packed->data;
+  }
   G.alpha = alpha;
   if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
   if (G.K == 0) return kk_fill(out, 0.0);
@@ -974,7 +980,14 @@ extern "C" {
 
 int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
             const kk_tensor* w_zp, float alpha) {
-  return gemm(out, a, w, w_scale, w_zp, alpha, false);
+  return gemm(out, a, w, w_scale, w_zp, alpha, false, nullptr);
+}
+
+int kk_gemm_packed(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w,
+                   const kk_tensor* packed, const kk_tensor* w_scale, const kk_tensor* w_zp,
+                   float alpha) {
+  KK_TRY(check_tensor(w, "w"));
+  return gemm(out, a, w, w_scale, w_zp, alpha, false, packed);
 }
 
 }  // extern "C"

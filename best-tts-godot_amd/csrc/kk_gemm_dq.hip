@@ -56,11 +56,20 @@
 // about 3.5 VALU instructions a value (the loop is VALU-bound) and gave way
 // to the accumulator test.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 #include "kk_internal.h"
 
 namespace kk {
+// Bytes of a [K, N] weight packed by kk_gemm_pack: per 32-column tile, per
+// 32-wide K-step, per half-step, one 1 KB matrix-core fragment per bf16
+// part (8-bit weights: q - z, one part; fp16: two parts).
+int64_t gemm_packed_size(int64_t K, int64_t N, int w_dt) {
+  return ceil_div(N, 32) * ceil_div(K, 32) * 2 * (w_dt == KK_F16 ? 2 : 1) * 1024;
+}
+
 namespace gfu {
 
 // The upper halves of lo and hi as two packed bf16 (lo first).
@@ -82,19 +91,26 @@ typedef short s4v __attribute__((ext_vector_type(4)));
 // distinct banks), B rows of 32 / 96 bytes (8-bit, two 16-lane groups of
 // transposing reads over 8 rows cover the 64 banks once) or 64 bytes (fp16,
 // 4 rows).
-template <int NT_, int KS_, int BT_>
+template <int NT_, int KS_, int BT_, bool PB_ = false>
 struct Shape {
   static constexpr int NT = NT_, KS = KS_, BT = BT_;
+  // PB: B packed by kk_gemm_pack, read straight into registers as
+  // matrix-core operands (PARTS bf16 fragments a tile and half-step)
+  static constexpr bool PB = PB_;
+  static constexpr int PARTS = BT;
   static constexpr int BN = 32 * NT, THREADS = 64 * KS;
   static constexpr int A_PITCH = 144;
   static constexpr int B_ROW = BN * BT;  // bytes of one k row of the B tile
   static constexpr int B_PITCH = BT == 1 ? (NT == 2 ? 96 : 32) : 64;
   static constexpr int B_CH = B_ROW / 16;          // 16-byte chunks per B row
   static constexpr int B_LOADS = 32 * B_CH / 64;   // 16-byte B loads per lane per K-step
-  static constexpr int LOADS = 4 + B_LOADS;
-  static constexpr int STAGE = 32 * A_PITCH + 32 * B_PITCH;  // one wave's staging bytes
+  static constexpr int LOADS = 4 + (PB ? NT * 2 * PARTS : B_LOADS);
+  static constexpr int STAGE = 32 * A_PITCH + (PB ? 0 : 32 * B_PITCH);  // one wave's staging bytes
   static constexpr int RED = KS * NT * 16 * 64 * 4;          // the partial tiles
-  static constexpr int LDS = KS * STAGE > RED ? KS * STAGE : RED;
+  // PB: the partial tiles beside the staging (no barrier before they are
+  // written); else in the staging's place
+  static constexpr int RED_OFF = PB ? KS * STAGE : 0;
+  static constexpr int LDS = PB ? KS * STAGE + RED : (KS * STAGE > RED ? KS * STAGE : RED);
   static constexpr int RING = KS == 8 ? 2 : 3;  // (two waves per SIMD share the registers)
   static constexpr int SHARE = NT * 16 / KS;
   static constexpr int B_ROWS_PER_LOAD = 64 / B_CH;  // B rows one 16-byte load per lane covers
@@ -117,6 +133,8 @@ struct Args {
   int64_t som, son;
   int64_t M, N, K;
   float alpha;
+  const void* bp;     // B packed by kk_gemm_pack (PB kernels)
+  uint32_t bp_bytes;
 };
 
 __device__ __forceinline__ float zero_point(const Args& G, int64_t n) {
@@ -185,14 +203,30 @@ __global__ void __launch_bounds__(S::THREADS) gemm_fused_kernel(Args G) {
 
   unsigned char* st = lds + wave * S::STAGE;
   u4 ring[R][L];
+  // packed B: fragment ((tile * nk + s) * 2 + h) * PARTS + part, 1 KB each,
+  // lane l's 16 bytes at 16 l
+  const __amdgpu_buffer_rsrc_t rbp =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(G.bp), 0, static_cast<int>(G.bp_bytes), 0x00020000);
+  const int bp_off = static_cast<int>((n0 / 32) * nk * 2 * S::PARTS * 1024 + 16 * lane);
   auto fetch = [&](int sl, int s) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       ring[sl][i] = __builtin_amdgcn_raw_buffer_load_b128(ra, a_off + (s * a_step + i * a_grp), 0, 0);
+    if constexpr (S::PB) {
 #pragma unroll
-    for (int i = 0; i < S::B_LOADS; ++i)
-      ring[sl][4 + i] =
-          __builtin_amdgcn_raw_buffer_load_b128(rb, b_off + (s * b_step + i * b_grp), 0, 0);
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int pt = 0; pt < S::PARTS; ++pt)
+            ring[sl][4 + (t * 2 + h) * S::PARTS + pt] = __builtin_amdgcn_raw_buffer_load_b128(
+                rbp, bp_off + ((((t * nk + s) * 2 + h) * S::PARTS + pt) * 1024), 0, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < S::B_LOADS; ++i)
+        ring[sl][4 + i] =
+            __builtin_amdgcn_raw_buffer_load_b128(rb, b_off + (s * b_step + i * b_grp), 0, 0);
+    }
   };
 
   // per-lane constants of the operand reads and conversions
@@ -230,9 +264,11 @@ __global__ void __launch_bounds__(S::THREADS) gemm_fused_kernel(Args G) {
     // stage this step's raw operands in the wave's region
 #pragma unroll
     for (int i = 0; i < 4; ++i) *reinterpret_cast<u4*>(st + a_st + 8 * S::A_PITCH * i) = ring[u][i];
+    if constexpr (!S::PB) {
 #pragma unroll
-    for (int i = 0; i < S::B_LOADS; ++i)
-      *reinterpret_cast<u4*>(st + b_st + S::B_ROWS_PER_LOAD * S::B_PITCH * i) = ring[u][4 + i];
+      for (int i = 0; i < S::B_LOADS; ++i)
+        *reinterpret_cast<u4*>(st + b_st + S::B_ROWS_PER_LOAD * S::B_PITCH * i) = ring[u][4 + i];
+    }
     // read them back as operands
     float av[2][8];
 #pragma unroll
@@ -248,6 +284,7 @@ __global__ void __launch_bounds__(S::THREADS) gemm_fused_kernel(Args G) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
+        if constexpr (S::PB) continue;
         if (BT == 1) {
           const i2v w = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
               reinterpret_cast<KK_LDS i2v*>(sb + b_rd[t][h][0]));
@@ -304,7 +341,21 @@ __global__ void __launch_bounds__(S::THREADS) gemm_fused_kernel(Args G) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        if (BT == 1) {
+        if constexpr (S::PB) {
+          const bf8 b0 = __builtin_bit_cast(bf8, ring[u][4 + (t * 2 + h) * S::PARTS]);
+          if constexpr (BT == 1) {
+#pragma unroll
+            for (int pa = 0; pa < 3; ++pa)
+              acc[t][h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[pa][h], b0, acc[t][h], 0, 0, 0);
+          } else {
+            const bf8 b1 = __builtin_bit_cast(bf8, ring[u][4 + (t * 2 + h) * S::PARTS + 1]);
+#pragma unroll
+            for (int pa = 0; pa < 3; ++pa) {
+              acc[t][h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[pa][h], b0, acc[t][h], 0, 0, 0);
+              acc[t][h] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ap[pa][h], b1, acc[t][h], 0, 0, 0);
+            }
+          }
+        } else if (BT == 1) {
           unsigned pb[4];
 #pragma unroll
           for (int d = 0; d < 2; ++d) {
@@ -379,6 +430,55 @@ __global__ void __launch_bounds__(S::THREADS) gemm_fused_kernel(Args G) {
     Unroll<0, R>::run(step_last, s0, s1);
   }
 
+  if constexpr (S::PB) {
+    float sc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int64_t n = n0 + 32 * t + (lane & 31);
+      sc[t] = G.scale && n < G.N ? load_as_f32(G.scale, G.scale_dt, n * G.scale_stride) : 1.0f;
+    }
+    // the partial tiles, summed in wave order; a NaN in any partial makes
+    // its sum NaN, so the test runs on the sums (four a lane) rather than
+    // on the accumulators (64 a lane)
+    float* red = reinterpret_cast<float*>(lds + S::RED_OFF);  // [wave][tile][register][lane]
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) red[((wave * NT + t) * 16 + q) * 64 + lane] = acc[t][0][q] + acc[t][1][q];
+    __syncthreads();
+    float v[S::SHARE];
+    bool vbad = false;
+#pragma unroll
+    for (int i = 0; i < S::SHARE; ++i) {
+      const int e = wave * S::SHARE + i, t = e / 16, q = e % 16;
+      v[i] = red[(t * 16 + q) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < KS; ++w) v[i] += red[((w * NT + t) * 16 + q) * 64 + lane];
+      vbad |= __builtin_isnan(v[i]);
+    }
+    const int vwave_bad = __any(vbad);  // (all lanes active: the vote covers the whole wave)
+    if (lane == 0) bad_w[wave] = vwave_bad;
+    __syncthreads();
+    bool vany_bad = false;
+#pragma unroll
+    for (int w = 0; w < KS; ++w) vany_bad |= bad_w[w] != 0;
+    if (vany_bad) {
+      exact_tile<S>(G, m0, n0);
+      return;
+    }
+    // D(i, j) of a 32x32 tile: lane j + 32 * ((i / 4) % 2), register (i / 8) * 4 + i % 4
+#pragma unroll
+    for (int i = 0; i < S::SHARE; ++i) {
+      const int e = wave * S::SHARE + i, t = e / 16, q = e % 16;
+      const int64_t n = n0 + 32 * t + (lane & 31);
+      const int64_t m = m0 + 8 * (q / 4) + 4 * (lane >> 5) + (q % 4);
+      if (m >= G.M || n >= G.N) continue;
+      float o = v[i] * sc[t];
+      if (G.alpha != 1.0f) o *= G.alpha;
+      G.out[m * G.som + n * G.son] = o;
+    }
+    return;
+  }
   bool bad = false;  // a NaN in this lane's accumulators (see the top of the section)
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -425,13 +525,104 @@ __global__ void __launch_bounds__(S::THREADS) gemm_fused_kernel(Args G) {
   }
 }
 
+struct PackArgs {
+  const void* w;     // [K, N], rows w_si apart
+  int w_dt;
+  int64_t w_si;
+  const void* zp;    // 8-bit zero point (per tensor or per column) or NULL
+  int64_t zp_stride;
+  int64_t K, N;
+  int nk, parts;
+  int64_t total;     // 16-byte units
+  u4* out;
+};
+
+// One lane of one fragment per thread: fragment ((tile * nk + s) * 2 + h) *
+// parts + part, lane l = (n, g) = (l % 32, l / 32) holding the weights of
+// column 32 tile + n at k = 32 s + 16 g + 8 h + e, e = 0..7 -- the k order the
+// kernel's staged activations take -- as bf16: q - z for 8-bit weights
+// (exact), the two parts b0 + b1 of an fp16 weight.
+__global__ void __launch_bounds__(256) gemm_pack_kernel(PackArgs P) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (u >= P.total) return;
+  const int lane = static_cast<int>(u % 64);
+  int64_t r = u / 64;
+  const int pt = static_cast<int>(r % P.parts);
+  r /= P.parts;
+  const int h = static_cast<int>(r % 2);
+  r /= 2;
+  const int s = static_cast<int>(r % P.nk);
+  const int64_t tile = r / P.nk;
+  const int64_t n = 32 * tile + (lane & 31);
+  const int g = lane >> 5;
+  unsigned f[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t k = 32 * static_cast<int64_t>(s) + 16 * g + 8 * h + e;
+    float v = 0.0f;
+    if (k < P.K && n < P.N) {
+      if (P.w_dt == KK_F16) {
+        const float x = static_cast<float>(static_cast<const _Float16*>(P.w)[k * P.w_si + n]);
+        const float x0 = __uint_as_float(__float_as_uint(x) & 0xffff0000u);
+        v = pt == 0 ? x0 : x - x0;
+      } else {
+        const uint8_t qb = static_cast<const uint8_t*>(P.w)[k * P.w_si + n];
+        const uint8_t zb = P.zp ? static_cast<const uint8_t*>(P.zp)[n * P.zp_stride] : 0;
+        v = P.w_dt == KK_I8 ? static_cast<float>(static_cast<int8_t>(qb)) - static_cast<float>(static_cast<int8_t>(zb))
+                            : static_cast<float>(qb) - static_cast<float>(zb);
+      }
+    }
+    f[e] = __float_as_uint(v);
+  }
+  P.out[u] = u4{pack_hi(f[0], f[1]), pack_hi(f[2], f[3]), pack_hi(f[4], f[5]), pack_hi(f[6], f[7])};
+}
+
+// What a packed buffer was made from (checked by every packed call).
+struct PackRecord {
+  const void* w;
+  int64_t K, N;
+  int w_dt;
+  const void* zp;
+  int zp_dt;
+};
+static std::mutex g_pack_mu;
+static std::unordered_map<const void*, PackRecord> g_packs;
+
 }  // namespace gfu
+
+void gemm_forget_pack(const void* p) {
+  std::lock_guard<std::mutex> lock(gfu::g_pack_mu);
+  gfu::g_packs.erase(p);
+}
+
+// Checks a packed buffer against a call's [K, N] weight w and zero point:
+// its size and alignment, and that the last kk_gemm_pack into it read this
+// very w and zero point.
+int gemm_check_packed(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp,
+                      const char* who) {
+  KK_TRY(check_tensor(packed, "packed"));
+  if (w->rank != 2) return set_error(KK_E_ARG, "%s: a packed weight is [K, N]", who);
+  const int64_t need = gemm_packed_size(w->shape[0], w->shape[1], w->dtype);
+  if (packed->dtype != KK_U8 || !is_contiguous(packed) || numel(packed) != need ||
+      reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
+    return set_error(KK_E_ARG, "%s: packed must be %lld contiguous, 256-byte aligned uint8 bytes",
+                     who, (long long)need);
+  std::lock_guard<std::mutex> lock(gfu::g_pack_mu);
+  auto it = gfu::g_packs.find(packed->data);
+  if (it == gfu::g_packs.end()) return set_error(KK_E_ARG, "%s: packed was not made by kk_gemm_pack", who);
+  const gfu::PackRecord& r = it->second;
+  if (r.w != w->data || r.K != w->shape[0] || r.N != w->shape[1] || r.w_dt != w->dtype)
+    return set_error(KK_E_ARG, "%s: packed was made from another weight tensor", who);
+  if (r.zp != (w_zp ? w_zp->data : nullptr) || r.zp_dt != (w_zp ? w_zp->dtype : -1))
+    return set_error(KK_E_ARG, "%s: packed was made with another weight zero point", who);
+  return KK_OK;
+}
 
 // Launches the kernel when B's rows are 16-byte aligned and every offset a
 // load forms is below 2^31; false, launching nothing, otherwise.
 static bool gemm_fused_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t b_si,
                            const Dequant& dq, float* out, int64_t som, int64_t son, int64_t Mt,
-                           int64_t N, int64_t K, float alpha, int* status) {
+                           int64_t N, int64_t K, float alpha, const void* bpack, int* status) {
   using namespace gfu;
   const int bt = b_dt == KK_F16 ? 2 : 1;
   if ((reinterpret_cast<uintptr_t>(b) & 15) || (b_si * bt) % 16) return false;
@@ -440,9 +631,12 @@ static bool gemm_fused_try(const float* a, int64_t a_si, const void* b, int b_dt
   const int64_t a_reach = (ceil_div(Mt, 32) * 32 * a_si + ceil_div(K, 32) * 32) * 4;
   const int64_t b_reach = (ceil_div(K, 32) * 32 * b_si + ceil_div(N, 64) * 64) * bt;
   if (a_reach >= (int64_t{1} << 31) || b_reach >= (int64_t{1} << 31)) return false;
+  const int64_t bp_bytes = gemm_packed_size(K, N, b_dt);
+  if (bpack && bp_bytes >= (int64_t{1} << 31)) return false;
   const Args g{a, b, static_cast<uint32_t>(a_bytes), static_cast<uint32_t>(b_bytes), a_si, b_si,
                b_dt, bt == 1 ? dq.zp : nullptr, dq.zp_stride, bt == 1 ? dq.scale : nullptr,
-               dq.scale_dt, dq.scale_stride, out, som, son, Mt, N, K, alpha};
+               dq.scale_dt, dq.scale_stride, out, som, son, Mt, N, K, alpha, bpack,
+               static_cast<uint32_t>(bpack ? bp_bytes : 0)};
   const int64_t cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
   const int64_t mt = ceil_div(Mt, 32);
 #ifdef KK_GFU_SHAPE
@@ -460,7 +654,14 @@ static bool gemm_fused_try(const float* a, int64_t a_si, const void* b, int b_dt
   using Q32x8 = Shape<1, 8, 1>;
   using Q32x4 = Shape<1, 4, 1>;
   using Q64x4 = Shape<2, 4, 1>;
-  if (bt == 2) {
+  using PH8 = Shape<1, 8, 2, true>;
+  using PQ64x8 = Shape<2, 8, 1, true>;
+  using PQ32x8 = Shape<1, 8, 1, true>;
+  if (bpack) {
+    if (bt == 2) KK_GFU_LAUNCH(PH8);
+    else if (shape == 0) KK_GFU_LAUNCH(PQ64x8);
+    else KK_GFU_LAUNCH(PQ32x8);
+  } else if (bt == 2) {
     if (shape == 2) KK_GFU_LAUNCH(H4);
     else KK_GFU_LAUNCH(H8);
   } else {
@@ -484,7 +685,7 @@ static bool gemm_fused_try(const float* a, int64_t a_si, const void* b, int b_dt
 bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t b_si,
                  const Dequant& dq, float* out, int64_t som, int64_t son, const BatchMap& bm,
                  int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, const int* only_if,
-                 int* status) {
+                 const void* bpack, int* status) {
   *status = KK_OK;
   if (only_if) return false;
   if (b_dt == KK_F16) {
@@ -504,7 +705,65 @@ bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t 
   }
   const int64_t Mt = M * batch;  // A and out as [batch * M] rows
   if (ceil_div(Mt, 32) > 65535 || ceil_div(N, 32) > (int64_t{1} << 30)) return false;
-  return gemm_fused_try(a, a_si, b, b_dt, b_si, dq, out, som, son, Mt, N, K, alpha, status);
+  return gemm_fused_try(a, a_si, b, b_dt, b_si, dq, out, som, son, Mt, N, K, alpha, bpack, status);
 }
 
 }  // namespace kk
+
+using namespace kk;
+
+extern "C" {
+
+int kk_gemm_packed_bytes(int64_t k, int64_t n, int w_dtype, int64_t* bytes) {
+  if (!bytes || k <= 0 || n <= 0)
+    return set_error(KK_E_ARG, "kk_gemm_packed_bytes: positive sizes and an output");
+  if (!(w_dtype == KK_F16 || w_dtype == KK_I8 || w_dtype == KK_U8))
+    return set_error(KK_E_ARG, "kk_gemm_packed_bytes: int8, uint8 or fp16 weights");
+  *bytes = gemm_packed_size(k, n, w_dtype);
+  return KK_OK;
+}
+
+int kk_gemm_pack(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp) {
+  const char* who = "kk_gemm_pack";
+  KK_TRY(require_ready());
+  KK_TRY(check_tensor(w, "w"));
+  if (w->rank != 2 || !(w->dtype == KK_F16 || w->dtype == KK_I8 || w->dtype == KK_U8) ||
+      w->strides[1] != 1 || numel(w) == 0)
+    return set_error(KK_E_ARG, "%s: w must be a non-empty fp16/int8/uint8 [K, N] with N contiguous",
+                     who);
+  const int64_t K = w->shape[0], N = w->shape[1];
+  int64_t zp_stride = 0;
+  if (w_zp) {
+    if (w->dtype == KK_F16) return set_error(KK_E_ARG, "%s: an fp16 weight takes no zero point", who);
+    KK_TRY(check_tensor(w_zp, "w_zp"));
+    if (w_zp->dtype != w->dtype)
+      return set_error(KK_E_ARG, "%s: w_zp must have w's type", who);
+    const int64_t nz = numel(w_zp);
+    if (nz == N && nz > 1) {
+      zp_stride = w_zp->rank ? w_zp->strides[w_zp->rank - 1] : 0;
+    } else if (nz != 1) {
+      return set_error(KK_E_ARG, "%s: w_zp must be per tensor or per column", who);
+    }
+  }
+  const int64_t bytes = gemm_packed_size(K, N, w->dtype);
+  if (bytes >= (int64_t{1} << 31))
+    return set_error(KK_E_UNSUPPORTED, "%s: %lld packed bytes exceed 2 GiB", who, (long long)bytes);
+  KK_TRY(check_tensor(packed, "packed"));
+  if (packed->dtype != KK_U8 || !is_contiguous(packed) || numel(packed) != bytes ||
+      reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
+    return set_error(KK_E_ARG, "%s: packed must be %lld contiguous, 256-byte aligned uint8 bytes",
+                     who, (long long)bytes);
+  {
+    std::lock_guard<std::mutex> lock(gfu::g_pack_mu);
+    gfu::g_packs[packed->data] =
+        gfu::PackRecord{w->data, K, N, w->dtype, w_zp ? w_zp->data : nullptr, w_zp ? w_zp->dtype : -1};
+  }
+  gfu::PackArgs P{w->data, w->dtype, w->strides[0], w_zp ? w_zp->data : nullptr, zp_stride, K, N,
+                  static_cast<int>(ceil_div(K, 32)), w->dtype == KK_F16 ? 2 : 1, bytes / 16,
+                  static_cast<gfu::u4*>(packed->data)};
+  KK_LAUNCH(gfu::gemm_pack_kernel, dim3(static_cast<unsigned>(ceil_div(P.total, 256))), dim3(256), 0,
+            ctx().stream, P);
+  return check_launch("gemm_pack_kernel");
+}
+
+}  // extern "C"

@@ -70,6 +70,7 @@ int conv_i8_scratch_setup(int device);
 void conv_i8_forget_pack(const void* p);
 // The same for a packed fp16 matrix-core convolution weight (kk_conv_f16.hip).
 void convh_forget_pack(const void* p);
+void gemm_forget_pack(const void* p);
 
 // Thread-local last error; set_error returns `code` so call sites can
 // `return set_error(KK_E_ARG, "...")`.
@@ -383,8 +384,11 @@ int matmul_shape(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, B
                  int64_t* M, int64_t* N, int64_t* K, int64_t* batch, const char* who);
 // kk_gemm; weights_rounded keeps numpy's rounding of each dequantised weight
 // (the fp32 matrix cores) where a caller's result feeds a recurrence.
+// `packed` (checked here): w laid out by kk_gemm_pack, used where the bf16
+// matrix-core path takes the call (the same results as without it).
 int gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_tensor* w_scale,
-         const kk_tensor* w_zp, float alpha, bool weights_rounded);
+         const kk_tensor* w_zp, float alpha, bool weights_rounded,
+         const kk_tensor* packed = nullptr);
 // out = A @ dequant(B) on the bf16 matrix cores (kk_gemm_dq.hip) when the
 // operands fit: fp32 A with K contiguous, int8/uint8 B (zero point of the
 // same type) or fp16 B with N contiguous.  Returns false, launching nothing,
@@ -392,7 +396,13 @@ int gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w, const kk_
 bool gemm_dq_try(const float* a, int64_t a_si, const void* b, int b_dt, int64_t b_si,
                  const Dequant& dq, float* out, int64_t som, int64_t son, const BatchMap& bm,
                  int64_t M, int64_t N, int64_t K, int64_t batch, float alpha, const int* only_if,
-                 int* status);
+                 const void* bpack, int* status);
+// kk_gemm_pack's layout: its size, the check of a packed buffer against a
+// call, and the registry entry dropped when the buffer is freed.
+int64_t gemm_packed_size(int64_t K, int64_t N, int w_dt);
+int gemm_check_packed(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp,
+                      const char* who);
+void gemm_forget_pack(const void* p);
 // XCD-aware block order (this library is built for gfx950 alone, whose
 // parts have 8 XCDs): workgroup w runs on XCD w % 8, so XCD x is given
 // the contiguous run of tiles x q + min(x, r) .. (T = 8 q + r tiles, the

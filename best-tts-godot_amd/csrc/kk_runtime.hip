@@ -472,6 +472,7 @@ int kk_free(void* dptr) {
   p.free_lists[it->second].push_back(dptr);
   conv_i8_forget_pack(dptr);
   convh_forget_pack(dptr);
+  gemm_forget_pack(dptr);
   p.pooled_bytes += it->second;
   p.live_bytes -= it->second;
   return KK_OK;

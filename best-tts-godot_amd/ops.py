@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 
 from . import _lib
-from .tensor import DeviceTensor
+from .tensor import NP_TO_CODE, DeviceTensor
 
 
 def _d(t):
@@ -174,8 +174,10 @@ def softmax(x, axis=-1):
 
 
 # ----------------------------------------------------------- contractions
-def matmul(a, w, w_scale=None, w_zp=None, alpha=1.0):
-    """numpy matmul (1-D operands promoted and the added axis dropped)."""
+def matmul(a, w, w_scale=None, w_zp=None, alpha=1.0, packed=None):
+    """numpy matmul (1-D operands promoted and the added axis dropped); with
+    `packed` (gemm_pack(w, w_zp) of this very 2-D w) the weights are not
+    converted for the call."""
     squeeze = []
     if a.ndim == 1:
         a = a.expand_dims(0)
@@ -185,7 +187,11 @@ def matmul(a, w, w_scale=None, w_zp=None, alpha=1.0):
         squeeze.append(-1)
     batch = broadcast_shape(a.shape[:-2], w.shape[:-2])
     out = DeviceTensor.empty(batch + (a.shape[-2], w.shape[-1]), np.float32)
-    _lib.call("kk_gemm", out.desc(), a.desc(), w.desc(), _d(w_scale), _d(w_zp), float(alpha))
+    if packed is not None:
+        _lib.call("kk_gemm_packed", out.desc(), a.desc(), w.desc(), packed.desc(), _d(w_scale),
+                  _d(w_zp), float(alpha))
+    else:
+        _lib.call("kk_gemm", out.desc(), a.desc(), w.desc(), _d(w_scale), _d(w_zp), float(alpha))
     if squeeze:
         out = out.squeeze([out.ndim + s for s in squeeze])
     return out
@@ -233,6 +239,18 @@ def conv_transpose1d(x, w, bias=None, pads=(0, 0), stride=1, dilation=1, group=1
               _d(w_zp), _d(bias), int(stride), int(dilation), int(pads[0]), int(pads[1]),
               int(group), int(output_padding))
     return out
+
+
+def gemm_pack(w, w_zp=None):
+    """The packed form of a constant [K, N] MatMul weight (fp16, or int8/uint8
+    with its zero point of the same type) as the bf16 matrix cores' operands
+    (uint8 bytes on the device), for matmul(packed=...)."""
+    nbytes = ctypes.c_int64(0)
+    _lib.call("kk_gemm_packed_bytes", int(w.shape[0]), int(w.shape[1]), int(NP_TO_CODE[w.dtype]),
+              ctypes.byref(nbytes))
+    packed = DeviceTensor.empty((nbytes.value,), np.uint8)
+    _lib.call("kk_gemm_pack", packed.desc(), w.desc(), _d(w_zp))
+    return packed
 
 
 def conv_pack(w, w_zp=None, transposed=False, stride=1):

@@ -214,6 +214,23 @@ int kk_softmax(const kk_tensor* out, const kk_tensor* x, int axis);
  * and f16 w take no scale.  Accumulation is fp32. */
 int kk_gemm(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w,
             const kk_tensor* w_scale, const kk_tensor* w_zp, float alpha);
+/* Packed weights for kk_gemm: the weight side of MatMul on a DequantizeLinear
+ * output or an fp16 weight (ref_runtime.py:614-615, 631-636), which the
+ * reference dequantizes on every call.  A graph whose weights do not change
+ * packs them at load: w [K, N] (N contiguous) fp16, or int8/uint8 less its
+ * per-tensor or per-column zero point of the same type, as the bf16
+ * matrix-core operands.  kk_gemm_packed_bytes gives the pack's size;
+ * kk_gemm_pack writes it into `packed` (uint8, contiguous, 256-byte
+ * aligned, that many bytes).  kk_gemm_packed is kk_gemm on a pack, with the
+ * same results: w (the tensor the pack was made from, with the same zero
+ * point) gives the shapes, and the call fails (KK_E_ARG) unless the last
+ * kk_gemm_pack into `packed` read this very w and zero point.  Calls the
+ * bf16 matrix cores do not take run kk_gemm's other kernels on w itself. */
+int kk_gemm_packed_bytes(int64_t k, int64_t n, int w_dtype, int64_t* bytes);
+int kk_gemm_pack(const kk_tensor* packed, const kk_tensor* w, const kk_tensor* w_zp);
+int kk_gemm_packed(const kk_tensor* out, const kk_tensor* a, const kk_tensor* w,
+                   const kk_tensor* packed, const kk_tensor* w_scale,
+                   const kk_tensor* w_zp, float alpha);
 /* Conv1d: op_conv1d forward (ref_runtime.py:58-82, 101-103).  x [N,Cin,L],
  * w [Cout, Cin/group, K] (f32/f16, or int8/uint8 dequantized with a
  * per-tensor or per-output-channel scale/zp), bias [Cout] or NULL. */

@@ -755,3 +755,71 @@ def test_fp16_weight_conv_packed_refuses_mismatch(gpu):
     pt = gpu.ops.conv_pack(wt, None, True, 1)  # the same size as pc, packed for ConvTranspose
     with pytest.raises(E, match="another operation"):
         gpu.ops.conv1d(xc, wt, None, (1, 1), packed=pt)
+
+
+# ------------------------------------------- packed dequant-GEMM weights
+GEMM_PACKED = [  # (batch, m, k, n, weight kind, zero point)
+    ((), 256, 768, 2048, "i8", None),      # the dequant GEMM configs (64-wide column tiles)
+    ((), 256, 2048, 768, "i8", None),      # (32-wide)
+    ((), 256, 768, 768, "f16", None),      # fp16 weights, two bf16 parts
+    ((), 130, 100, 70, "u8", "col"),       # ragged K and N, per-column uint8 zero point
+    ((), 37, 96, 333, "i8", "tensor"),     # a nonzero per-tensor int8 zero point
+    ((2,), 64, 96, 80, "f16", None),       # batched activations, one weight
+    ((), 50, 45, 40, "i8", None),          # K % 4 != 0: the fp32 kernels, w itself
+]
+
+
+@pytest.mark.parametrize("case", GEMM_PACKED, ids=[f"{c[4]}-{c[1]}x{c[2]}x{c[3]}" for c in GEMM_PACKED])
+def test_gemm_packed(gpu, oracle, case):
+    """kk_gemm_packed: the weights packed once by kk_gemm_pack give kk_gemm's
+    bits (the same kernel on the same operand values) on two calls in a row
+    with different activations, each within the oracle's bar."""
+    batch, m, k, n, wdt, zpk = case
+    r = rng(46)
+    dv = gpu.to_device
+    sc = zp = None
+    if wdt == "f16":
+        w = r.normal(0, 0.05, (k, n)).astype(np.float16)
+        wdeq = w
+    elif wdt == "i8":
+        w, s = int8_weight(r, (k, n))
+        sc = np.array(s, np.float32)
+        zp = np.array(r.integers(-20, 20), np.int8) if zpk == "tensor" else None
+        wdeq = oracle.dequantize(w, sc, zp)
+    else:
+        w = r.integers(0, 256, (k, n)).astype(np.uint8)
+        sc = r.uniform(1e-4, 1e-3, n).astype(np.float32)
+        zp = r.integers(100, 156, n).astype(np.uint8)
+        wdeq = oracle.dequantize(w, sc, zp)
+    wd = dv(w)
+    kw = dict(w_scale=dv(sc) if sc is not None else None, w_zp=dv(zp) if zp is not None else None)
+    packed = gpu.ops.gemm_pack(wd, kw["w_zp"])
+    for call in range(2):
+        a = r.normal(0, 1 + call, batch + (m, k)).astype(np.float32)
+        want = gpu.ops.matmul(dv(a), wd, **kw).numpy()
+        got = gpu.ops.matmul(dv(a), wd, packed=packed, **kw).numpy()
+        assert_bitexact(got, want, f"packed {case} call {call}")
+        check(got, oracle.matmul(a, wdeq), f"packed {case} call {call}")
+
+
+def test_gemm_packed_refuses_mismatch(gpu):
+    """A packed MatMul weight is used only with the tensor and zero point it
+    was packed from."""
+    r = rng(47)
+    dv = gpu.to_device
+    w = dv(r.integers(0, 256, (256, 512)).astype(np.uint8))
+    w2 = dv(r.integers(0, 256, (256, 512)).astype(np.uint8))
+    wz, wz2 = dv(np.array(120, np.uint8)), dv(np.array(121, np.uint8))
+    sc = dv(np.array(0.002, np.float32))
+    a = dv(r.normal(0, 1, (64, 256)).astype(np.float32))
+    packed = gpu.ops.gemm_pack(w, wz)
+    assert gpu.ops.matmul(a, w, sc, wz, packed=packed).shape == (64, 512)
+    E = gpu._lib.KKError
+    with pytest.raises(E, match="another weight tensor"):
+        gpu.ops.matmul(a, w2, sc, wz, packed=packed)
+    with pytest.raises(E, match="another weight zero point"):
+        gpu.ops.matmul(a, w, sc, wz2, packed=packed)
+    with pytest.raises(E, match="not made by kk_gemm_pack"):
+        gpu.ops.matmul(a, w, sc, wz, packed=gpu.DeviceTensor.empty(packed.shape, np.uint8))
+    with pytest.raises(E, match="packed must be"):
+        gpu.ops.matmul(a, w, sc, wz, packed=gpu.DeviceTensor.empty((packed.shape[0] // 2,), np.uint8))
