@@ -78,9 +78,22 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
   const int64_t M = G.M, N = G.N, K = G.K;
   const uint8_t* a = G.a + batch_offset(G.bm, 0, bz);
   const uint8_t* b = G.b + batch_offset(G.bm, 1, bz);
+  // The vector paths read through buffer resources based at this block's
+  // first row of A and first column of B (the host keeps each span below
+  // 2^31 bytes).  An offset at or past the span reads zeros, so the bounds
+  // become a select on the offset: a guarded load would be a branch with a
+  // wait of its own, and the K-step's loads would go out one at a time.
+  const int64_t a_rows = M - m0 < kTM ? M - m0 : kTM;
+  const uint32_t a_span = static_cast<uint32_t>((a_rows - 1) * G.a_si + K);
+  const uint32_t b_span = static_cast<uint32_t>((K - 1) * G.b_si + (N - n0));
+  const auto a_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a + m0 * G.a_si), 0,
+                                                      static_cast<int>(a_span), 0x00020000);
+  const auto b_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(b + n0), 0,
+                                                      static_cast<int>(b_span), 0x00020000);
 
   // A pieces: two per thread, row i >> 3, 16 bytes at k 16 (i & 7)
   v4i ra[2];
+  uint32_t fa[2] = {0u, 0u};  // the flip of a vector piece, applied as it is stashed
   auto fetch_a = [&](int64_t k0) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -88,10 +101,10 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
       const int64_t m = m0 + row, k = k0 + kc;
       v4i v = {0, 0, 0, 0};  // padding holds a' = 0
       if (AV) {
-        if (m < M && k < K) {
-          v = *reinterpret_cast<const v4i*>(a + m * G.a_si + k);
-          v ^= static_cast<int>(G.a_flip);
-        }
+        const bool in = m < M && k < K;
+        const uint32_t off = in ? static_cast<uint32_t>(row * G.a_si + k) : a_span;
+        v = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(a_rs, off, 0, 0));
+        fa[j] = in ? G.a_flip : 0u;
       } else {
         uint32_t w[4] = {0, 0, 0, 0};
         if (m < M) {
@@ -111,11 +124,13 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int i = tid + kThreads * j;
-      *reinterpret_cast<v4i*>(&As[buf][(i >> 3) * kPitch + 16 * (i & 7)]) = ra[j];
+      *reinterpret_cast<v4i*>(&As[buf][(i >> 3) * kPitch + 16 * (i & 7)]) =
+          ra[j] ^ static_cast<int>(fa[j]);
     }
   };
   // B items: two per thread, rows k 4 (i >> 4) .. +3 x columns 4 (i & 15) .. +3
   uint32_t rb[2][4];
+  uint32_t fb[2][4] = {};  // as fa
   auto fetch_b = [&](int64_t k0) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -125,10 +140,13 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
       for (int q = 0; q < 4; ++q) {
         const int64_t k = k0 + 4 * kg + q;
         uint32_t v = 0;  // padding holds b' = 0
-        if (k < K) {
-          if (BV) {
-            if (n < N) v = *reinterpret_cast<const uint32_t*>(b + k * G.b_si + n) ^ G.b_flip;
-          } else {
+        if (BV) {
+          const bool in = k < K && n < N;
+          const uint32_t off = in ? static_cast<uint32_t>(k * G.b_si + 4 * ng) : b_span;
+          v = __builtin_amdgcn_raw_buffer_load_b32(b_rs, off, 0, 0);
+          fb[j][q] = in ? G.b_flip : 0u;
+        } else if (k < K) {
+          {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               if (n + e < N)
@@ -144,7 +162,9 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int i = tid + kThreads * j, kg = i >> 4, ng = i & 15;
-      const uint32_t* d = rb[j];
+      uint32_t d[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d[q] = rb[j][q] ^ fb[j][q];
       // 4 x 4 byte transpose (v_perm: bytes 0-3 from the second operand, 4-7
       // from the first): word e = column 4ng + e at rows 4kg .. 4kg + 3
       const uint32_t t01l = __builtin_amdgcn_perm(d[1], d[0], 0x05010400u);
@@ -295,6 +315,10 @@ static int i8_launch(const I8Args& G, int64_t batch) {
     if (G.bm.st[0][d] % 16) av = false;
     if (G.bm.st[1][d] % 4) bv = false;
   }
+  // the buffer spans of one block's rows of A and of B's K rows
+  const int64_t kSpanMax = (int64_t{1} << 31) - 256;
+  if ((std::min<int64_t>(G.M, kTM) - 1) * G.a_si + G.K > kSpanMax) av = false;
+  if ((G.K - 1) * G.b_si + G.N > kSpanMax) bv = false;
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(batch));
   KK_TRY(check_xcd_grid(grid, "MatMulInteger"));
   hipStream_t st = ctx().stream;
