@@ -115,6 +115,8 @@ PROTOTYPES = {
     "kk_pcm16": [_T, _T, _f],
     "kk_fir_pcm16": [_T, _T, _T, _i, _f],
     "kk_graph_begin": [],
+    "kk_graph_begin_arena": [_sz],
+    "kk_graph_abort": [],
     "kk_graph_end": [ctypes.POINTER(_i)],
     "kk_graph_launch": [_i],
     "kk_graph_destroy": [_i],

@@ -235,6 +235,71 @@ static void pool_release_all() {
   p.live_bytes = p.pooled_bytes = 0;
 }
 
+// ---------------------------------------------------------- graph arenas
+// Device memory owned by a graph recorded with kk_graph_begin_arena.  While
+// it is recorded, kk_alloc hands out the arena's blocks (the pool's buckets,
+// a free list per bucket, so that a block freed by one op is reused by a
+// later one exactly as it would be in the pool: the recorded kernels run in
+// recording order), and a pool buffer freed by an op is held by the graph
+// instead of returning to the pool, since every replay reads it again.
+// Arena blocks are released only with the graph (kk_free of one is then a
+// no-op); held buffers go back to the pool at the same time.
+struct Arena {
+  char* base = nullptr;
+  size_t bytes = 0, top = 0;
+  std::unordered_map<void*, size_t> size_of;  // every block handed out -> bucket
+  std::unordered_map<size_t, std::vector<void*>> free_lists;
+  std::vector<void*> held;  // pool buffers freed while recording
+  bool owns(const void* p) const {
+    const char* c = static_cast<const char*>(p);
+    return c >= base && c < base + bytes;
+  }
+};
+static Arena* g_rec_arena = nullptr;   // the arena of the graph being recorded
+static Arena* g_dead_arena = nullptr;  // a recording kk_graph_end could not make a graph of
+
+static int arena_alloc(Arena& a, size_t nbytes, void** dptr) {
+  const size_t size = bucket_size(nbytes);
+  auto it = a.free_lists.find(size);
+  if (it != a.free_lists.end() && !it->second.empty()) {
+    *dptr = it->second.back();
+    it->second.pop_back();
+    return KK_OK;
+  }
+  if (a.top + size > a.bytes)
+    return set_error(KK_E_NOMEM, "graph arena exhausted: %zu of %zu bytes in use, %zu more asked",
+                     a.top, a.bytes, size);
+  void* q = a.base + a.top;
+  a.top += size;
+  a.size_of[q] = size;
+  *dptr = q;
+  return KK_OK;
+}
+
+// Releases an arena whose graph has gone (or was never made): its blocks,
+// and its held buffers back to the pool.  The stream must not be running
+// work that reads them.
+static void arena_release(Arena* a) {
+  if (!a) return;
+  Pool& p = pool();
+  {
+    std::lock_guard<std::mutex> lk(p.mu);
+    for (void* q : a->held) {
+      auto it = p.live.find(q);
+      if (it == p.live.end() || p.in_pool.count(q)) continue;
+      conv_i8_forget_pack(q);
+      convh_forget_pack(q);
+      gemm_forget_pack(q);
+      p.in_pool.insert(q);
+      p.free_lists[it->second].push_back(q);
+      p.pooled_bytes += it->second;
+      p.live_bytes -= it->second;
+    }
+  }
+  if (a->base) (void)hipFree(a->base);
+  delete a;
+}
+
 // ---------------------------------------------------------------- uploads
 // kk_upload never waits for the stream.  Up to kUploadArgBytes travel inside
 // the arguments of a one-block copy kernel (kernel arguments are captured at
@@ -323,10 +388,20 @@ static bool g_event_made[KK_MAX_EVENTS];
 struct GraphSlot {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  Arena* arena = nullptr;
 };
 static std::vector<GraphSlot>& graphs() {
   static std::vector<GraphSlot>* g = new std::vector<GraphSlot>();
   return *g;
+}
+
+// The arena (of the graph being recorded or of a recorded one) holding p.
+static Arena* arena_of(const void* p) {
+  if (g_rec_arena && g_rec_arena->owns(p)) return g_rec_arena;
+  if (g_dead_arena && g_dead_arena->owns(p)) return g_dead_arena;
+  for (auto& s : graphs())
+    if (s.arena && s.arena->owns(p)) return s.arena;
+  return nullptr;
 }
 
 static int not_capturing(const char* who) {
@@ -339,8 +414,29 @@ static void destroy_graphs() {
   for (auto& s : graphs()) {
     if (s.exec) (void)hipGraphExecDestroy(s.exec);
     if (s.graph) (void)hipGraphDestroy(s.graph);
+    arena_release(s.arena);
     s = GraphSlot();
   }
+}
+
+// Ends a recording that will not become a graph.
+static void abandon_recording() {
+  Context& c = ctx();
+  if (!c.capturing) return;
+  hipGraph_t g = nullptr;
+  (void)hipStreamEndCapture(c.stream, &g);
+  if (g) (void)hipGraphDestroy(g);
+  (void)hipGetLastError();
+  c.capturing = false;
+  arena_release(g_rec_arena);  // nothing recorded into it has run
+  g_rec_arena = nullptr;
+}
+
+// kk_graph_end's failures keep the recording's arena (the caller may still
+// hold its blocks) until kk_graph_abort.
+static void keep_dead_arena(Arena* a) {
+  arena_release(g_dead_arena);
+  g_dead_arena = a;
 }
 
 }  // namespace kk
@@ -388,14 +484,11 @@ int kk_init(int device) {
 int kk_shutdown(void) {
   Context& c = ctx();
   if (!c.ready) return KK_OK;
-  if (c.capturing) {
-    hipGraph_t g = nullptr;
-    (void)hipStreamEndCapture(c.stream, &g);
-    if (g) (void)hipGraphDestroy(g);
-    c.capturing = false;
-  }
+  abandon_recording();
   (void)hipStreamSynchronize(c.stream);
   destroy_graphs();
+  arena_release(g_dead_arena);
+  g_dead_arena = nullptr;
   pool_release_all();
   staging_release();
   if (c.row_counters) { (void)hipFree(c.row_counters); c.row_counters = nullptr; }
@@ -418,8 +511,13 @@ int kk_sync(void) {
 
 int kk_alloc(size_t bytes, void** dptr) {
   KK_TRY(require_ready());
-  KK_TRY(not_capturing("kk_alloc"));
   if (!dptr) return set_error(KK_E_ARG, "dptr is NULL");
+  if (ctx().capturing) {
+    if (!g_rec_arena)
+      return set_error(KK_E_STATE, "kk_alloc is not allowed while a graph is being recorded "
+                                   "without an arena (kk_graph_begin_arena)");
+    return arena_alloc(*g_rec_arena, bytes, dptr);
+  }
   const size_t size = bucket_size(bytes);
   Pool& p = pool();
   std::lock_guard<std::mutex> lk(p.mu);
@@ -459,6 +557,14 @@ int kk_alloc(size_t bytes, void** dptr) {
 int kk_free(void* dptr) {
   if (!dptr) return KK_OK;
   KK_TRY(require_ready());
+  if (Arena* a = arena_of(dptr)) {
+    if (a != g_rec_arena) return KK_OK;  // a recorded graph's: released with it
+    auto sz = a->size_of.find(dptr);
+    if (sz == a->size_of.end())
+      return set_error(KK_E_STATE, "kk_free: %p is not a block of the graph arena", dptr);
+    a->free_lists[sz->second].push_back(dptr);
+    return KK_OK;
+  }
   Pool& p = pool();
   std::lock_guard<std::mutex> lk(p.mu);
   auto it = p.live.find(dptr);
@@ -466,6 +572,13 @@ int kk_free(void* dptr) {
     return set_error(KK_E_STATE, "kk_free: %p was not allocated by kk_alloc", dptr);
   if (p.in_pool.count(dptr))
     return set_error(KK_E_STATE, "kk_free: %p freed twice", dptr);
+  if (g_rec_arena) {
+    // read again by every replay of the graph being recorded
+    for (void* q : g_rec_arena->held)
+      if (q == dptr) return set_error(KK_E_STATE, "kk_free: %p freed twice", dptr);
+    g_rec_arena->held.push_back(dptr);
+    return KK_OK;
+  }
   // Work already enqueued on the stream that reads this buffer stays
   // ordered before any later reuse, because every op runs on one stream.
   p.in_pool.insert(dptr);
@@ -513,9 +626,25 @@ int kk_pool_trim(size_t budget_bytes) {
 
 int kk_upload(void* dst, const void* src, size_t bytes) {
   KK_TRY(require_ready());
-  KK_TRY(not_capturing("kk_upload"));
+  if (ctx().capturing && !g_rec_arena)
+    return set_error(KK_E_STATE, "kk_upload is not allowed while a graph is being recorded "
+                                 "without an arena (kk_graph_begin_arena)");
   if (!bytes) return KK_OK;
   if (!dst || !src) return set_error(KK_E_ARG, "kk_upload: NULL pointer");
+  if (ctx().capturing) {
+    // Recorded with an arena: the bytes become arguments of copy kernels in
+    // the graph (a host staging buffer would be read again, changed, by
+    // every replay), kUploadArgBytes a kernel.
+    for (size_t at = 0; at < bytes; at += kUploadArgBytes) {
+      UploadArgs a;
+      a.dst = static_cast<uint8_t*>(dst) + at;
+      a.n = static_cast<uint32_t>(std::min(kUploadArgBytes, bytes - at));
+      std::memcpy(a.data, static_cast<const uint8_t*>(src) + at, a.n);
+      KK_LAUNCH(upload_small_kernel, dim3(1), dim3(256), 0, ctx().stream, a);
+      KK_TRY(check_launch("upload_small_kernel"));
+    }
+    return KK_OK;
+  }
   // The host buffer belongs to the caller, who may release it on return: its
   // bytes are captured (kernel arguments or the staging ring) before that.
   if (bytes <= kUploadArgBytes) {
@@ -575,16 +704,63 @@ int kk_graph_begin(void) {
   return KK_OK;
 }
 
+int kk_graph_begin_arena(size_t arena_bytes) {
+  KK_TRY(require_ready());
+  KK_TRY(not_capturing("kk_graph_begin_arena"));
+  if (arena_bytes == 0) return set_error(KK_E_ARG, "kk_graph_begin_arena: empty arena");
+  Arena* a = new Arena();
+  a->bytes = (arena_bytes + 255) & ~size_t(255);
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&a->base), a->bytes);
+  if (e != hipSuccess) {
+    delete a;
+    (void)hipGetLastError();
+    return set_error(KK_E_NOMEM, "kk_graph_begin_arena: hipMalloc(%zu) failed: %s", arena_bytes,
+                     hipGetErrorString(e));
+  }
+  e = hipStreamBeginCapture(ctx().stream, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) {
+    arena_release(a);
+    return check_hip(e, "hipStreamBeginCapture");
+  }
+  g_rec_arena = a;
+  ctx().capturing = true;
+  return KK_OK;
+}
+
+int kk_graph_abort(void) {
+  KK_TRY(require_ready());
+  if (ctx().capturing) {
+    abandon_recording();
+  } else if (g_dead_arena) {
+    arena_release(g_dead_arena);
+    g_dead_arena = nullptr;
+  } else {
+    return set_error(KK_E_STATE, "kk_graph_abort without a recording");
+  }
+  return KK_OK;
+}
+
 int kk_graph_end(int* graph_id) {
   KK_TRY(require_ready());
   if (!ctx().capturing) return set_error(KK_E_STATE, "kk_graph_end without kk_graph_begin");
-  if (!graph_id) return set_error(KK_E_ARG, "graph_id is NULL");
+  if (!graph_id) {
+    abandon_recording();
+    return set_error(KK_E_ARG, "graph_id is NULL");
+  }
   ctx().capturing = false;
   GraphSlot s;
-  KK_HIP(hipStreamEndCapture(ctx().stream, &s.graph));
-  hipError_t e = hipGraphInstantiate(&s.exec, s.graph, nullptr, nullptr, 0);
+  s.arena = g_rec_arena;
+  g_rec_arena = nullptr;
+  hipError_t e = hipStreamEndCapture(ctx().stream, &s.graph);
+  if (e != hipSuccess) {
+    if (s.graph) (void)hipGraphDestroy(s.graph);
+    keep_dead_arena(s.arena);
+    return check_hip(e, "hipStreamEndCapture");
+  }
+  e = hipGraphInstantiate(&s.exec, s.graph, nullptr, nullptr, 0);
   if (e != hipSuccess) {
     (void)hipGraphDestroy(s.graph);
+    keep_dead_arena(s.arena);
     return check_hip(e, "hipGraphInstantiate");
   }
   // Uploaded now, so that the first launch costs what later ones do.
@@ -592,6 +768,7 @@ int kk_graph_end(int* graph_id) {
   if (e != hipSuccess) {
     (void)hipGraphExecDestroy(s.exec);
     (void)hipGraphDestroy(s.graph);
+    keep_dead_arena(s.arena);
     return check_hip(e, "hipGraphUpload");
   }
   auto& g = graphs();
@@ -621,6 +798,7 @@ int kk_graph_destroy(int graph_id) {
   KK_HIP(hipStreamSynchronize(ctx().stream));
   (void)hipGraphExecDestroy(g[graph_id].exec);
   (void)hipGraphDestroy(g[graph_id].graph);
+  arena_release(g[graph_id].arena);
   g[graph_id] = GraphSlot();
   return KK_OK;
 }

@@ -16,17 +16,20 @@ weights of the same dtype, shape and scale, which together give the full
 Kokoro-82M-architecture graph with random-init weights (int8/uint8 for the
 quantized contractions, fp16 elsewhere); `synth_model` packs the two.
 """
+import collections
+import ctypes
 import gzip
 import json
 import os
 
 import numpy as np
 
-from . import audio, ops
+from . import _lib, audio, ops
+from . import tensor as _tensor
 from .dispatch import dispatch, to_device, to_host
 from .fuse import fuse as fuse_chains
 from .kpk import CODE_TO_NP, read_kpk
-from .tensor import DeviceTensor
+from .tensor import DeviceTensor, pool_stats
 
 DATA = os.path.join(os.path.dirname(os.path.abspath(__file__)), "data")
 
@@ -144,21 +147,50 @@ class NonFiniteError(RuntimeError):
         self.node, self.op, self.output, self.inputs = node, op, output, inputs
 
 
+class _TextPart:
+    """The nodes a run walks before its first read of device data -- the
+    text encoder, the predictors and the durations, whose shapes follow from
+    the token count alone -- recorded for one token count as one HIP graph
+    that owns its intermediates (kk_graph_begin_arena)."""
+
+    __slots__ = ("end", "arena", "gid", "inputs", "env", "checks", "error")
+
+    def __init__(self):
+        self.end = None     # nodes [0, end) are recorded
+        self.arena = 0      # arena bytes to record with
+        self.gid = None     # the recorded graph
+        self.inputs = None  # device input_ids, style, speed the graph reads
+        self.env = None     # the tensors live after node end - 1
+        self.checks = ()    # (node, axis, extent) of the Gathers indexed by input_ids
+        self.error = None   # why this token count is walked without recording
+
+
 class PackedGraph:
     """A packed graph with its weights resident on the device.
 
     With `fuse` (the default) the quantised-conv tails, InstanceNorm chains
     and snake chains run as single kernels; `groups[k]` lists the original
     node indices that node k stands for.  Tensors in `protect` stay
-    readable after a run (they are never fused away)."""
+    readable after a run (they are never fused away).
+
+    With `record` (the default) the part of a run that precedes its first
+    read of device data is recorded as a HIP graph on the second run of a
+    token count and replayed from the third on, from device copies of the
+    inputs: the same kernels with the same arguments, without walking those
+    nodes on the host.  The first run of a token count finds where that part
+    ends; up to `RECORD_KEEP` token counts keep their graphs."""
+
+    RECORD_KEEP = 4
 
     @classmethod
-    def from_kpk(cls, path, fuse=True, protect=()):
+    def from_kpk(cls, path, fuse=True, protect=(), record=True):
         """The model in the KPK1 file at `path` (tools/kpk_runtime.py:27-50)."""
         desc, weights = read_kpk(path)
-        return cls(desc, weights, fuse=fuse, protect=protect)
+        return cls(desc, weights, fuse=fuse, protect=protect, record=record)
 
-    def __init__(self, graph, weights, fuse=True, protect=()):
+    def __init__(self, graph, weights, fuse=True, protect=(), record=True):
+        self.record = record
+        self._parts = collections.OrderedDict()  # token count -> _TextPart
         self.graph = graph
         self._notch = None  # the notch filter's taps on the device, made on first use
         self.ops = graph["ops"]
@@ -295,6 +327,147 @@ class PackedGraph:
                 f"{tuple(v.shape)}: {bad} non-finite values\n  inputs: {described}",
                 node=i, op=op, output=o, inputs=described)
 
+    def _walk(self, env, lo, hi, keep, strict, probe=None):
+        """Runs nodes [lo, hi) on `env`, dropping each tensor after its last
+        use.  With `probe` (a _TextPart of this token count), also finds the
+        first node that reads device data and the most pool memory the nodes
+        before it hold at once."""
+        frees = self.frees
+        base = peak = pool_stats()[0] if probe is not None else 0
+        for i in range(lo, hi):
+            op, ins, outs, at = self.nodes[i]
+            if probe is not None:
+                seen = _tensor._state["downloads"]
+            try:
+                dispatch(op, ins, outs, at, env)
+            except Exception as exc:
+                raise RuntimeError(f"node {i} {op}: {exc}") from exc
+            if probe is not None:
+                if _tensor._state["downloads"] != seen:
+                    self._measured(probe, i, peak - base)
+                    probe = None
+                else:
+                    peak = max(peak, pool_stats()[0])
+            if strict:
+                self._check_finite(i, env)
+            for name in frees[i]:
+                if name not in keep:
+                    env.pop(name, None)
+        if probe is not None:
+            self._measured(probe, hi, peak - base)
+
+    # ------------------------------------------------ recorded text parts
+    def _part(self, n_ids):
+        part = self._parts.get(n_ids)
+        if part is not None:
+            self._parts.move_to_end(n_ids)
+            return part
+        while len(self._parts) >= self.RECORD_KEEP:
+            self._drop(self._parts.popitem(last=False)[1])
+        part = self._parts[n_ids] = _TextPart()
+        return part
+
+    def _measured(self, part, end, need):
+        """Nodes [0, end) read no device data and held at most `need` bytes
+        of the pool at once: record them in an arena of three times that (its
+        buckets are not shared between sizes) and some slack.  The Gathers
+        that index a weight with input_ids are checked on the host, as the
+        walk checks host indices (a recorded gather clamps them)."""
+        part.end = end
+        part.arena = 3 * int(need) + (16 << 20)
+        if end == 0:
+            part.error = "the first node reads device data"
+            return
+        name = self.inputs["input_ids"]
+        checks = []
+        for i in range(end):
+            op, ins, _outs, at = self.nodes[i]
+            if name not in ins:
+                continue
+            data = self.weights.get(ins[0]) if op == "Gather" and ins.index(name) == 1 else None
+            if op == "Shape":
+                continue
+            if data is None:
+                part.error = f"node {i} {op} reads input_ids"
+                return
+            axis = int(at.get("axis", 0)) % len(data.shape)
+            checks.append((i, axis, int(data.shape[axis])))
+        part.checks = tuple(checks)
+
+    def _record(self, part, env, ids, style, speed):
+        """Walks nodes [0, part.end) into a graph with device inputs and
+        launches it.  Returns part.end, or None when the walk could not be
+        recorded (part.error says why; `env` then holds the weights only)."""
+        names = self.inputs
+        inputs = (DeviceTensor.from_numpy(ids), to_device(style), to_device(speed))
+        env[names["input_ids"]], env[names["style"]], env[names["speed"]] = inputs
+        failed = None
+        _lib.call("kk_graph_begin_arena", part.arena)
+        try:
+            self._walk(env, 0, part.end, set(), False)
+        except Exception as exc:  # recorded nothing that will run: walk it instead
+            failed = f"{type(exc).__name__}: {exc}"
+        gid = ctypes.c_int(-1)
+        if failed is None:
+            try:
+                _lib.call("kk_graph_end", ctypes.byref(gid))
+            except Exception as exc:
+                failed = f"{type(exc).__name__}: {exc}"
+        if failed is not None:
+            # nothing may refer to the arena's blocks when it is released
+            env.clear()
+            env.update(self.weights)
+            _lib.call("kk_graph_abort")
+            part.error = failed
+            return None
+        part.gid = gid.value
+        part.inputs = inputs
+        part.env = {k: v for k, v in env.items() if k not in self.weights}
+        _lib.call("kk_graph_launch", part.gid)
+        return part.end
+
+    def _replay(self, part, env, ids, style, speed):
+        for i, axis, n in part.checks:
+            if ids.size and (int(ids.min()) < -n or int(ids.max()) >= n):
+                raise RuntimeError(
+                    f"node {i} Gather: index out of bounds for axis {axis} with size {n}")
+        for t, a in zip(part.inputs, (ids, style, speed)):
+            _lib.call("kk_upload", ctypes.c_void_p(t.ptr), a.ctypes.data_as(ctypes.c_void_p),
+                      a.nbytes)
+        _lib.call("kk_graph_launch", part.gid)
+        env.update(part.env)
+        return part.end
+
+    def _drop(self, part):
+        gid, part.gid = part.gid, None
+        part.env = part.inputs = None  # (before the graph's arena goes)
+        if gid is not None and _lib._lib is not None:
+            _lib.call("kk_graph_destroy", gid)
+
+    def release_recordings(self):
+        """Destroys the recorded text parts and frees their memory."""
+        while self._parts:
+            self._drop(self._parts.popitem()[1])
+
+    def recorded(self, n_ids):
+        """(recorded nodes, graph kernel nodes, arena bytes, error) of the
+        text part for `n_ids` token ids, or None before its first run."""
+        part = self._parts.get(n_ids)
+        if part is None:
+            return None
+        kernels = None
+        if part.gid is not None:
+            n = ctypes.c_int64(0)
+            _lib.call("kk_graph_nodes", part.gid, ctypes.byref(n))
+            kernels = n.value
+        return part.end, kernels, part.arena, part.error
+
+    def __del__(self):
+        try:
+            self.release_recordings()
+        except Exception:  # interpreter shutdown: the process frees it
+            pass
+
     def run(self, input_ids, style, speed=1.0, keep=(), pcm16=False, notch=True, gain=1.0,
             strict=False, max_nodes=None, start=0, inject=None):
         """Returns the waveform on the host: float32 samples, or with
@@ -311,27 +484,31 @@ class PackedGraph:
         `last_env`; `start` skips the walk's first nodes, whose outputs the
         rest reads from `inject` ({tensor id: array}, floats placed on the
         device), to run a part of the graph from given values."""
-        env = dict(self.weights)
-        env[self.inputs["input_ids"]] = np.asarray(input_ids, np.int64).reshape(1, -1)
-        env[self.inputs["style"]] = to_device(np.asarray(style, np.float32).reshape(1, 256))
-        env[self.inputs["speed"]] = to_device(np.asarray([speed], np.float32))
-        for name, v in (inject or {}).items():
-            v = np.asarray(v)
-            env[str(name)] = to_device(v) if v.dtype.kind == "f" else v
+        ids = np.ascontiguousarray(np.asarray(input_ids, np.int64).reshape(1, -1))
+        style = np.ascontiguousarray(np.asarray(style, np.float32).reshape(1, 256))
+        speed = np.asarray([speed], np.float32)
         keep = {str(k) for k in keep}
-        frees = self.frees
         limit = len(self.nodes) if max_nodes is None or max_nodes < 0 else min(max_nodes, len(self.nodes))
-        for i in range(start, limit):
-            op, ins, outs, at = self.nodes[i]
-            try:
-                dispatch(op, ins, outs, at, env)
-            except Exception as exc:
-                raise RuntimeError(f"node {i} {op}: {exc}") from exc
-            if strict:
-                self._check_finite(i, env)
-            for name in frees[i]:
-                if name not in keep:
-                    env.pop(name, None)
+        part = None
+        if self.record and start == 0 and not inject and not keep and not strict \
+                and limit == len(self.nodes):
+            part = self._part(ids.shape[1])
+        env = dict(self.weights)
+        first = None
+        if part is not None and part.gid is not None:
+            first = self._replay(part, env, ids, style, speed)
+        elif part is not None and part.end is not None and part.error is None:
+            first = self._record(part, env, ids, style, speed)
+        if first is None:
+            env[self.inputs["input_ids"]] = ids
+            env[self.inputs["style"]] = to_device(style)
+            env[self.inputs["speed"]] = to_device(speed)
+            for name, v in (inject or {}).items():
+                v = np.asarray(v)
+                env[str(name)] = to_device(v) if v.dtype.kind == "f" else v
+            first = start
+        probe = part if part is not None and part.end is None else None
+        self._walk(env, first, limit, keep, strict, probe)
         self.last_env = {k: env[k] for k in keep if k in env}
         if self.output not in env:
             return None

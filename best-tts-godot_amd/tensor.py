@@ -23,7 +23,7 @@ NP_TO_CODE = {
 }
 CODE_TO_NP = {v: k for k, v in NP_TO_CODE.items()}
 
-_state = {"device": None}
+_state = {"device": None, "downloads": 0}  # downloads: DeviceTensor.numpy calls so far
 
 
 def init(device=0):
@@ -226,6 +226,7 @@ class DeviceTensor:
 
     def numpy(self):
         """Download (waits for all enqueued work)."""
+        _state["downloads"] += 1
         src = self.contiguous()
         host = np.empty(self.shape, dtype=self.dtype)
         if host.nbytes:

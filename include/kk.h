@@ -457,6 +457,23 @@ int kk_event_elapsed(int start_slot, int stop_slot, float* ms);
  * buffer a graph touches must exist before kk_graph_begin and stay
  * allocated while the graph may be launched. */
 int kk_graph_begin(void);
+/* Records as kk_graph_begin does, into a graph that owns `arena_bytes` of
+ * device memory: while recording, kk_alloc hands out the arena's blocks
+ * (bucketed, a block freed by one op is reused by a later one), kk_upload
+ * records its bytes as arguments of copy kernels (the host buffer may change
+ * after the call), and a pool buffer freed by an op is held by the graph,
+ * whose replays read it again.  The arena's blocks and the held buffers go
+ * back with kk_graph_destroy (kk_free of an arena block is a no-op until
+ * then); kk_alloc fails with KK_E_NOMEM when the arena is used up.  This
+ * lets a walk of graph nodes that allocates its intermediates, the text
+ * part of a run, be recorded as it runs and replayed for the next input of
+ * the same length (executor.gd:306-331 walks the nodes on every run). */
+int kk_graph_begin_arena(size_t arena_bytes);
+/* Ends a recording without making a graph, or follows a kk_graph_end that
+ * failed on an arena recording (which keeps the arena, since the caller may
+ * still hold its blocks): the arena and the held buffers are released
+ * (nothing recorded has run). */
+int kk_graph_abort(void);
 int kk_graph_end(int* graph_id);
 int kk_graph_launch(int graph_id);
 int kk_graph_destroy(int graph_id);
