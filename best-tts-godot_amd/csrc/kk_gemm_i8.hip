@@ -14,7 +14,9 @@
 // whenever it fits int32 (always for K <= 33025: |a - az|, |b - bz| <= 255).
 //
 // Block: 64 x 64 outputs, 4 waves as 2 x 2, each a 32 x 32 MFMA tile; K-steps
-// of 128.  A [M, K] is staged row-major (K contiguous, 16-byte loads); B
+// of 256 (the graph's K of 768 and 2048 in 3 and 8 steps: at its M of 130
+// a launch has a few dozen blocks, each waiting out one round trip a step).
+// A [M, K] is staged row-major (K contiguous, 16-byte loads); B
 // [K, N] arrives N-contiguous and is transposed on the way into LDS (a
 // thread loads four rows of four columns, one dword each, and swaps the 4 x 4
 // bytes with v_perm), so both MFMA operand fragments -- 16 consecutive k of
@@ -32,9 +34,12 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int kTM = 64, kTN = 64;  // outputs per block
-constexpr int kTK = 128;           // K-step (bytes of one row)
+constexpr int kTK = 256;           // K-step (bytes of one row)
 constexpr int kPitch = kTK + 16;   // LDS row pitch: 16-byte pad staggers the banks
 constexpr int kThreads = 256;
+constexpr int kAPieces = kTM * kTK / 16 / kThreads;         // 16-byte A pieces a thread
+constexpr int kBItems = (kTK / 4) * (kTN / 4) / kThreads;   // 4 x 4-byte B items a thread
+constexpr int kRowPieces = kTK / 16;
 
 struct I8Args {
   const uint8_t* a;     // bytes of A [.., M, K]
@@ -91,13 +96,13 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
   const auto b_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(b + n0), 0,
                                                       static_cast<int>(b_span), 0x00020000);
 
-  // A pieces: two per thread, row i >> 3, 16 bytes at k 16 (i & 7)
-  v4i ra[2];
-  uint32_t fa[2] = {0u, 0u};  // the flip of a vector piece, applied as it is stashed
+  // A pieces: kAPieces a thread, row i / kRowPieces, 16 bytes at k 16 (i % kRowPieces)
+  v4i ra[kAPieces];
+  uint32_t fa[kAPieces] = {};  // the flip of a vector piece, applied as it is stashed
   auto fetch_a = [&](int64_t k0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int i = tid + kThreads * j, row = i >> 3, kc = 16 * (i & 7);
+    for (int j = 0; j < kAPieces; ++j) {
+      const int i = tid + kThreads * j, row = i / kRowPieces, kc = 16 * (i % kRowPieces);
       const int64_t m = m0 + row, k = k0 + kc;
       v4i v = {0, 0, 0, 0};  // padding holds a' = 0
       if (AV) {
@@ -122,18 +127,18 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
   };
   auto stash_a = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kAPieces; ++j) {
       const int i = tid + kThreads * j;
-      *reinterpret_cast<v4i*>(&As[buf][(i >> 3) * kPitch + 16 * (i & 7)]) =
+      *reinterpret_cast<v4i*>(&As[buf][(i / kRowPieces) * kPitch + 16 * (i % kRowPieces)]) =
           ra[j] ^ static_cast<int>(fa[j]);
     }
   };
-  // B items: two per thread, rows k 4 (i >> 4) .. +3 x columns 4 (i & 15) .. +3
-  uint32_t rb[2][4];
-  uint32_t fb[2][4] = {};  // as fa
+  // B items: kBItems a thread, rows k 4 (i >> 4) .. +3 x columns 4 (i & 15) .. +3
+  uint32_t rb[kBItems][4];
+  uint32_t fb[kBItems][4] = {};  // as fa
   auto fetch_b = [&](int64_t k0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kBItems; ++j) {
       const int i = tid + kThreads * j, kg = i >> 4, ng = i & 15;
       const int64_t n = n0 + 4 * ng;
 #pragma unroll
@@ -160,7 +165,7 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
   };
   auto stash_b = [&](int buf) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < kBItems; ++j) {
       const int i = tid + kThreads * j, kg = i >> 4, ng = i & 15;
       uint32_t d[4];
 #pragma unroll

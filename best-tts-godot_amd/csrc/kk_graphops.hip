@@ -9,47 +9,13 @@
 namespace kk {
 
 // --------------------------------------------------- DynamicQuantizeLinear
-// Stage 1: per-block min/max.  Stage 2: every block folds the partials,
-// derives scale and zero point in double exactly as the reference does
-// (ref_runtime.py:106-116), and quantises its share.
-// Both stages stream x as float4 (non-temporal) when it is 16-byte aligned;
-// the quantised bytes leave four at a time.
+// Stage 1: per-block (min, max), the last block to finish folding them and
+// deriving scale and zero point in double exactly as the reference does
+// (ref_runtime.py:106-116).  Stage 2: the bytes.  Both stages read x as
+// float4 when it is 16-byte aligned (stage 1 with cached loads, which stage
+// 2 finds in the L2 for the graph's activations); the quantised bytes leave
+// four at a time.
 constexpr int kDqlBlocks = 2048;
-
-__global__ void __launch_bounds__(256) dql_minmax(const float* __restrict__ x, int64_t n,
-                                                   float2* __restrict__ part, int vec) {
-  __shared__ float smin[4], smax[4];
-  float lo = INFINITY, hi = -INFINITY;
-  const int64_t tid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  const int64_t nthreads = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  int64_t head = 0;
-  if (vec) {
-    const int64_t n4 = n / 4;
-    for (int64_t i = tid; i < n4; i += nthreads) {
-      const float4 v = ld_stream4(x + 4 * i);
-      lo = fminf(lo, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
-      hi = fmaxf(hi, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
-    }
-    head = 4 * n4;
-  }
-  for (int64_t i = head + tid; i < n; i += nthreads) {
-    const float v = x[i];
-    lo = fminf(lo, v);
-    hi = fmaxf(hi, v);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    lo = fminf(lo, __shfl_xor(lo, off, 64));
-    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
-  }
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  if (lane == 0) { smin[w] = lo; smax[w] = hi; }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    part[blockIdx.x] = make_float2(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
-                                   fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])));
-  }
-}
 
 // Scale and zero point from the (min, max) of x, in double exactly as the
 // reference does; returns (scale, zero point) as floats (x / scale runs in
@@ -111,6 +77,88 @@ __global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __rest
 }
 
 
+// Stage 1 with the fold in its last block: every block stores its (min,
+// max) at the device-coherent level and counts itself in; the block that
+// counts last folds the npart partials (min and max do not depend on the
+// order) into params[0] and the outputs through dql_params, and resets the
+// count.  Saves dql_fold's launch and needs no allocation (the partials and
+// params sit in the context's scratch, the count in its row counters).
+__global__ void __launch_bounds__(256) dql_minmax_last(const float* __restrict__ x, int64_t n,
+                                                        float2* __restrict__ part, int* cnt,
+                                                        float2* __restrict__ params,
+                                                        float* __restrict__ scale_out,
+                                                        uint8_t* __restrict__ zp_out, int vec) {
+  __shared__ float smin[4], smax[4];
+  __shared__ int last_s;
+  float lo = INFINITY, hi = -INFINITY;
+  const int64_t tid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  const int64_t nthreads = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  int64_t head = 0;
+  if (vec) {
+    const int64_t n4 = n / 4;
+    for (int64_t i = tid; i < n4; i += nthreads) {
+      const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);  // read again by stage 2
+      lo = fminf(lo, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
+      hi = fmaxf(hi, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+    }
+    head = 4 * n4;
+  }
+  for (int64_t i = head + tid; i < n; i += nthreads) {
+    const float v = x[i];
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) { smin[w] = lo; smax[w] = hi; }
+  __syncthreads();
+  const int npart = static_cast<int>(gridDim.x);
+  if (threadIdx.x == 0) {
+    const float2 p = make_float2(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
+                                 fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])));
+    // the partial has landed at the device-coherent level before the count
+    // moves (an agent-scope store, then vmcnt(0); the compiler fence keeps
+    // the two accesses in order)
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(part) + blockIdx.x,
+                       __builtin_bit_cast(uint64_t, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    last_s = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == npart - 1;
+  }
+  __syncthreads();
+  if (!last_s) return;
+  // the last block: an agent-scope acquire orders its reads of the other
+  // blocks' partials after the count it saw
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  lo = INFINITY;
+  hi = -INFINITY;
+  for (int i = threadIdx.x; i < npart; i += blockDim.x) {
+    const float2 q = __builtin_bit_cast(
+        float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(part) + i, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT));
+    lo = fminf(lo, q.x);
+    hi = fmaxf(hi, q.y);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, off, 64));
+    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+  }
+  __syncthreads();  // (the shared partials above have been read)
+  if (lane == 0) { smin[w] = lo; smax[w] = hi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    params[0] = dql_params(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
+                           fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])), scale_out,
+                           zp_out);
+    __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
                     uint8_t* zp_out, const int* only_if, int* clear) {
   KK_LAUNCH(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
@@ -140,11 +188,11 @@ __global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x,
 
 // Inputs up to kDqlSmall elements: one block of 1024 threads takes the
 // (min, max), the scale and zero point and the bytes in one launch (the
-// same values as the three-kernel path: min and max do not depend on the
-// order, and the parameters come from dql_params).  Saves two launches and
-// the partials' allocation for the many small activations of the text
-// encoder and the predictors.
-constexpr int64_t kDqlSmall = 131072;
+// same values as the two-launch path: min and max do not depend on the
+// order, and the parameters come from dql_params).  Above that one CU's
+// share of the bandwidth costs more than the second launch (99840 values:
+// 17 us in one block).
+constexpr int64_t kDqlSmall = 16384;
 constexpr int kDqlSmallThreads = 1024;
 
 __global__ void __launch_bounds__(kDqlSmallThreads) dql_small(const float* __restrict__ x, int64_t n,
@@ -753,28 +801,19 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
                        static_cast<uint8_t*>(zp->data), static_cast<uint8_t*>(y->data), vec);
     return check_launch("dql_small");
   }
-  void* part = nullptr;
-  KK_TRY(kk_alloc(sizeof(float2) * (nblk + 1), &part));
-  float2* pp = static_cast<float2*>(part);
-  KK_LAUNCH(dql_minmax, dim3(nblk), dim3(256), 0, ctx().stream,
-                     static_cast<const float*>(x->data), n, pp, vec);
-  int rc = check_launch("dql_minmax");
-  if (rc == KK_OK) {
-    KK_LAUNCH(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, pp, nblk, pp + nblk,
-                       static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data),
-                       static_cast<const int*>(nullptr), static_cast<int*>(nullptr));
-    rc = check_launch("dql_fold");
-  }
-  if (rc == KK_OK) {
-    const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 1024), 4096));
-    KK_LAUNCH(dql_quantize, dim3(g), dim3(256), 0, ctx().stream,
-                       static_cast<const float*>(x->data), n, pp + nblk,
-                       static_cast<uint8_t*>(y->data), vec);
-    rc = check_launch("dql_quantize");
-  }
-  // Stream order keeps the partials alive until the three kernels have read them.
-  kk_free(part);
-  return rc;
+  // partials and params in the context's scratch, the arrival count in its
+  // first row counter (zero between launches: the last block resets it)
+  static_assert(sizeof(float2) * (kDqlBlocks + 1) <= kScratchBytes, "DQL partials");
+  float2* pp = static_cast<float2*>(ctx().scratch);
+  KK_LAUNCH(dql_minmax_last, dim3(nblk), dim3(256), 0, ctx().stream,
+                     static_cast<const float*>(x->data), n, pp, ctx().row_counters, pp + nblk,
+                     static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data), vec);
+  KK_TRY(check_launch("dql_minmax_last"));
+  const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 1024), 4096));
+  KK_LAUNCH(dql_quantize, dim3(g), dim3(256), 0, ctx().stream,
+                     static_cast<const float*>(x->data), n, pp + nblk,
+                     static_cast<uint8_t*>(y->data), vec);
+  return check_launch("dql_quantize");
 }
 
 int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const kk_tensor* x,

@@ -46,10 +46,13 @@ def onode(oracle, op, inputs, attrs=None, nout=1):
 
 
 @pytest.mark.parametrize("case", ["normal", "positive", "negative", "zeros", "big", "odd_small",
-                                  "just_over"])
+                                  "just_over", "one_block_max", "two_launch_min", "ragged"])
 def test_dynamic_quantize_linear(gpu, oracle, case):
-    """Inputs up to 131072 elements take the one-block kernel, larger ones
-    the three-kernel path; both against the oracle, bit for bit."""
+    """Inputs up to 16384 elements take the one-block kernel, larger ones
+    the two launches (many blocks' (min, max), the last block folding them;
+    then the bytes); both against the oracle, bit for bit, the two-launch
+    cases one after another (each leaves its arrival count at zero for the
+    next)."""
     r = rng(1)
     x = {"normal": r.normal(0, 1, (1, 130, 768)),
          "positive": r.uniform(0.5, 3, (4, 1000)),
@@ -57,7 +60,10 @@ def test_dynamic_quantize_linear(gpu, oracle, case):
          "zeros": np.zeros((3, 7)),
          "big": r.normal(0, 50, (1, 512, 2400)),
          "odd_small": r.normal(0.3, 2, (1, 3, 43689)),
-         "just_over": r.normal(-0.2, 1, (2, 65537))}[case].astype(np.float32)
+         "just_over": r.normal(-0.2, 1, (2, 65537)),
+         "one_block_max": r.normal(0, 1, (4, 4096)),
+         "two_launch_min": r.normal(0, 1, (1, 16385)),
+         "ragged": r.normal(1, 3, (7, 3001))}[case].astype(np.float32)
     y, s, z = node(gpu, "DynamicQuantizeLinear", [x], nout=3)
     yo, so, zo = onode(oracle, "DynamicQuantizeLinear", [x], nout=3)
     assert_bitexact(np.asarray(s, np.float32).reshape(()), np.asarray(so, np.float32), "scale")
