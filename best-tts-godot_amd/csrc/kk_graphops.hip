@@ -9,13 +9,13 @@
 namespace kk {
 
 // --------------------------------------------------- DynamicQuantizeLinear
-// Stage 1: per-block (min, max), the last block to finish folding them and
-// deriving scale and zero point in double exactly as the reference does
-// (ref_runtime.py:106-116).  Stage 2: the bytes.  Both stages read x as
-// float4 when it is 16-byte aligned (stage 1 with cached loads, which stage
-// 2 finds in the L2 for the graph's activations); the quantised bytes leave
-// four at a time.
-constexpr int kDqlBlocks = 2048;
+// Stage 1: per-block (min, max) partials.  Stage 2: every block folds them,
+// derives scale and zero point in double exactly as the reference does
+// (ref_runtime.py:106-116) and writes its share of the bytes.  Both stages
+// read x as float4 when it is 16-byte aligned (stage 1 with cached loads,
+// which stage 2 finds in the L2 for the graph's activations); the quantised
+// bytes leave four at a time.
+constexpr int kDqlBlocks = 256;  // stage-1 blocks at most (one partial a thread of a stage-2 block)
 
 // Scale and zero point from the (min, max) of x, in double exactly as the
 // reference does; returns (scale, zero point) as floats (x / scale runs in
@@ -77,29 +77,35 @@ __global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __rest
 }
 
 
-// Stage 1 with the fold in its last block: every block stores its (min,
-// max) at the device-coherent level and counts itself in; the block that
-// counts last folds the npart partials (min and max do not depend on the
-// order) into params[0] and the outputs through dql_params, and resets the
-// count.  Saves dql_fold's launch and needs no allocation (the partials and
-// params sit in the context's scratch, the count in its row counters).
-__global__ void __launch_bounds__(256) dql_minmax_last(const float* __restrict__ x, int64_t n,
-                                                        float2* __restrict__ part, int* cnt,
-                                                        float2* __restrict__ params,
-                                                        float* __restrict__ scale_out,
-                                                        uint8_t* __restrict__ zp_out, int vec) {
+// Stage 1: at most kDqlBlocks blocks each take the (min, max) of their
+// grid-stride share, four float4 loads in flight a thread, and store it.
+// No block waits for another and none counts in (a count that every block
+// of a large grid increments serialises on its one address: 2048 blocks
+// took 40 us): the stage-2 blocks fold the partials themselves.
+__global__ void __launch_bounds__(256) dql_minmax_part(const float* __restrict__ x, int64_t n,
+                                                        float2* __restrict__ part, int vec) {
   __shared__ float smin[4], smax[4];
-  __shared__ int last_s;
   float lo = INFINITY, hi = -INFINITY;
   const int64_t tid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   const int64_t nthreads = static_cast<int64_t>(gridDim.x) * blockDim.x;
   int64_t head = 0;
   if (vec) {
+    constexpr int kU = 4;
     const int64_t n4 = n / 4;
-    for (int64_t i = tid; i < n4; i += nthreads) {
-      const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);  // read again by stage 2
-      lo = fminf(lo, fminf(fminf(v.x, v.y), fminf(v.z, v.w)));
-      hi = fmaxf(hi, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+    const float x0 = x[0];  // (past the end a slot holds x[0], which moves neither extreme)
+    for (int64_t i0 = tid; i0 < n4; i0 += nthreads * kU) {
+      float4 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int64_t i = i0 + u * nthreads;
+        v[u] = i < n4 ? *reinterpret_cast<const float4*>(x + 4 * i)  // read again by stage 2
+                      : make_float4(x0, x0, x0, x0);
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        lo = fminf(lo, fminf(fminf(v[u].x, v[u].y), fminf(v[u].z, v[u].w)));
+        hi = fmaxf(hi, fmaxf(fmaxf(v[u].x, v[u].y), fmaxf(v[u].z, v[u].w)));
+      }
     }
     head = 4 * n4;
   }
@@ -116,61 +122,47 @@ __global__ void __launch_bounds__(256) dql_minmax_last(const float* __restrict__
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 0) { smin[w] = lo; smax[w] = hi; }
   __syncthreads();
-  const int npart = static_cast<int>(gridDim.x);
-  if (threadIdx.x == 0) {
-    const float2 p = make_float2(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
-                                 fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])));
-    // the partial has landed at the device-coherent level before the count
-    // moves (an agent-scope store, then vmcnt(0); the compiler fence keeps
-    // the two accesses in order)
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(part) + blockIdx.x,
-                       __builtin_bit_cast(uint64_t, p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    last_s = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == npart - 1;
-  }
-  __syncthreads();
-  if (!last_s) return;
-  // the last block: an agent-scope acquire orders its reads of the other
-  // blocks' partials after the count it saw
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  lo = INFINITY;
-  hi = -INFINITY;
-  for (int i = threadIdx.x; i < npart; i += blockDim.x) {
-    const float2 q = __builtin_bit_cast(
-        float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(part) + i, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT));
-    lo = fminf(lo, q.x);
-    hi = fmaxf(hi, q.y);
+  if (threadIdx.x == 0)
+    part[blockIdx.x] = make_float2(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
+                                   fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])));
+}
+
+// Stage 2: every block folds the npart (<= 256) partials (min and max do
+// not depend on the order, so every block finds the same scale and zero
+// point; block 0 stores them) and quantises its grid-stride share.
+__global__ void __launch_bounds__(256) dql_quantize_fold(const float* __restrict__ x, int64_t n,
+                                                          const float2* __restrict__ part, int npart,
+                                                          float* __restrict__ scale_out,
+                                                          uint8_t* __restrict__ zp_out,
+                                                          uint8_t* __restrict__ y, int vec) {
+  __shared__ float smin[4], smax[4];
+  __shared__ float2 pz_s;
+  float lo = INFINITY, hi = -INFINITY;
+  if (static_cast<int>(threadIdx.x) < npart) {
+    const float2 q = part[threadIdx.x];
+    lo = q.x;
+    hi = q.y;
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     lo = fminf(lo, __shfl_xor(lo, off, 64));
     hi = fmaxf(hi, __shfl_xor(hi, off, 64));
   }
-  __syncthreads();  // (the shared partials above have been read)
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   if (lane == 0) { smin[w] = lo; smax[w] = hi; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    params[0] = dql_params(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
-                           fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])), scale_out,
-                           zp_out);
-    __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float sc;
+    uint8_t zq;
+    pz_s = dql_params(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
+                      fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])), &sc, &zq);
+    if (blockIdx.x == 0) {
+      *scale_out = sc;
+      *zp_out = zq;
+    }
   }
-}
-
-int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
-                    uint8_t* zp_out, const int* only_if, int* clear) {
-  KK_LAUNCH(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
-                     scale_out, zp_out, only_if, clear);
-  return check_launch("dql_fold");
-}
-
-__global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x, int64_t n,
-                                                     const float2* __restrict__ params,
-                                                     uint8_t* __restrict__ y, int vec) {
-  const float2 pz = params[0];
-  const float sc = pz.x, z = pz.y;
+  __syncthreads();
+  const float sc = pz_s.x, z = pz_s.y;
   const KkDivisor dsc = kk_divisor(sc);
   const int64_t tid = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   const int64_t nthreads = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -184,6 +176,13 @@ __global__ void __launch_bounds__(256) dql_quantize(const float* __restrict__ x,
     head = 4 * n4;
   }
   for (int64_t i = head + tid; i < n; i += nthreads) y[i] = static_cast<uint8_t>(dql_byte(x[i], sc, z));
+}
+
+int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
+                    uint8_t* zp_out, const int* only_if, int* clear) {
+  KK_LAUNCH(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
+                     scale_out, zp_out, only_if, clear);
+  return check_launch("dql_fold");
 }
 
 // Inputs up to kDqlSmall elements: one block of 1024 threads takes the
@@ -792,7 +791,7 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
     return set_error(KK_E_ARG, "kk_dynamic_quantize_linear: scale is one fp32, zp one uint8");
   const int64_t n = numel(x);
   if (n == 0) return set_error(KK_E_ARG, "kk_dynamic_quantize_linear: empty input");
-  const int nblk = static_cast<int>(std::min<int64_t>(kDqlBlocks, ceil_div(n, 1024)));
+  const int nblk = static_cast<int>(std::min<int64_t>(kDqlBlocks, ceil_div(n, 4096)));
   const int vec = (reinterpret_cast<uintptr_t>(x->data) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(y->data) % 4 == 0) ? 1 : 0;
   if (n <= kDqlSmall) {
@@ -801,19 +800,18 @@ int kk_dynamic_quantize_linear(const kk_tensor* y, const kk_tensor* scale, const
                        static_cast<uint8_t*>(zp->data), static_cast<uint8_t*>(y->data), vec);
     return check_launch("dql_small");
   }
-  // partials and params in the context's scratch, the arrival count in its
-  // first row counter (zero between launches: the last block resets it)
-  static_assert(sizeof(float2) * (kDqlBlocks + 1) <= kScratchBytes, "DQL partials");
+  // the partials in the context's scratch
+  static_assert(sizeof(float2) * kDqlBlocks <= kScratchBytes, "DQL partials");
   float2* pp = static_cast<float2*>(ctx().scratch);
-  KK_LAUNCH(dql_minmax_last, dim3(nblk), dim3(256), 0, ctx().stream,
-                     static_cast<const float*>(x->data), n, pp, ctx().row_counters, pp + nblk,
-                     static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data), vec);
-  KK_TRY(check_launch("dql_minmax_last"));
+  KK_LAUNCH(dql_minmax_part, dim3(nblk), dim3(256), 0, ctx().stream,
+                     static_cast<const float*>(x->data), n, pp, vec);
+  KK_TRY(check_launch("dql_minmax_part"));
   const unsigned g = static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 1024), 4096));
-  KK_LAUNCH(dql_quantize, dim3(g), dim3(256), 0, ctx().stream,
-                     static_cast<const float*>(x->data), n, pp + nblk,
+  KK_LAUNCH(dql_quantize_fold, dim3(g), dim3(256), 0, ctx().stream,
+                     static_cast<const float*>(x->data), n, static_cast<const float2*>(pp), nblk,
+                     static_cast<float*>(scale->data), static_cast<uint8_t*>(zp->data),
                      static_cast<uint8_t*>(y->data), vec);
-  return check_launch("dql_quantize");
+  return check_launch("dql_quantize_fold");
 }
 
 int kk_lstm(const kk_tensor* ys, const kk_tensor* yh, const kk_tensor* yc, const kk_tensor* x,
