@@ -17,22 +17,6 @@ namespace kk {
 // bytes leave four at a time.
 constexpr int kDqlBlocks = 256;  // stage-1 blocks at most (one partial a thread of a stage-2 block)
 
-// Scale and zero point from the (min, max) of x, in double exactly as the
-// reference does; returns (scale, zero point) as floats (x / scale runs in
-// float32 against the scale rounded to float32) and stores the outputs.
-__device__ float2 dql_params(float fmn, float fmx, float* scale_out, uint8_t* zp_out) {
-  const double mn = fmn;
-  const double mx = fmx;
-  const double dlo = mn < 0.0 ? mn : 0.0;
-  const double dhi = mx > 0.0 ? mx : 0.0;
-  double scale = (dhi - dlo) / 255.0;
-  if (scale == 0.0) scale = 1.0;
-  double zp = rint(0.0 - dlo / scale);
-  zp = zp < 0.0 ? 0.0 : (zp > 255.0 ? 255.0 : zp);
-  *scale_out = static_cast<float>(scale);
-  *zp_out = static_cast<uint8_t>(zp);
-  return make_float2(static_cast<float>(scale), static_cast<float>(zp));
-}
 
 // One block folds the partials and derives scale and zero point in double
 // exactly as the reference does; params = (scale, zero point) as floats.

@@ -48,6 +48,23 @@ __device__ __forceinline__ uint32_t dql_byte(float x, float sc, float z) {
   return static_cast<uint32_t>(v);
 }
 
+// Scale and zero point from the (min, max) of x, in double exactly as the
+// reference does; returns (scale, zero point) as floats (x / scale runs in
+// float32 against the scale rounded to float32) and stores the outputs.
+__device__ inline float2 dql_params(float fmn, float fmx, float* scale_out, uint8_t* zp_out) {
+  const double mn = fmn;
+  const double mx = fmx;
+  const double dlo = mn < 0.0 ? mn : 0.0;
+  const double dhi = mx > 0.0 ? mx : 0.0;
+  double scale = (dhi - dlo) / 255.0;
+  if (scale == 0.0) scale = 1.0;
+  double zp = rint(0.0 - dlo / scale);
+  zp = zp < 0.0 ? 0.0 : (zp > 255.0 ? 255.0 : zp);
+  *scale_out = static_cast<float>(scale);
+  *zp_out = static_cast<uint8_t>(zp);
+  return make_float2(static_cast<float>(scale), static_cast<float>(zp));
+}
+
 // Folds npart (min, max) partials and derives DynamicQuantizeLinear's scale
 // and zero point: params[0] = (scale, zp) as floats, *scale_out, *zp_out.
 // With only_if, the launch does nothing unless *only_if is set; with clear,

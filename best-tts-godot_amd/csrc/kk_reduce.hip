@@ -554,13 +554,15 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
 // The normalised results y = affine((x - mean) / den) of long rows, not
 // stored: block (bx, row) writes the (min, max) of its share to
 // mm[row * gridDim.x + bx] (the first half of DynamicQuantizeLinear).
+// only_if: the launch does nothing unless *only_if == epoch.
 __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict__ mm,
                                                              const float* __restrict__ x,
                                                              const float2* __restrict__ stats,
                                                              int64_t C, int64_t T, Affine af,
                                                              int vec,
-                                                             const int* __restrict__ only_if) {
-  if (only_if && *only_if == 0) return;
+                                                             const int* __restrict__ only_if,
+                                                             int epoch) {
+  if (only_if && *only_if != epoch) return;
   __shared__ float2 wmm[kRowBlock / 64];
   const int64_t row = blockIdx.y;
   const int64_t c = row % C;
@@ -607,24 +609,69 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict_
   }
 }
 
-// y recomputed exactly as above, then DynamicQuantizeLinear's byte with
-// params[0] = (scale, zero point): the float y never reaches memory.
-// only_if: the launch does nothing unless *only_if is set.  check: any y
-// outside params[1] = (min, max) sets *check.
+// y recomputed exactly as above, then DynamicQuantizeLinear's byte: the
+// float y never reaches memory.  The scale and zero point come from the
+// npart (min, max) partials in mm, which every block folds (min and max do
+// not depend on the order, so every block finds the same; block (0, 0)
+// stores them: no fold launch), or with mm NULL from params[0] (dql_fold's
+// launch, for more partials than a block folds).  only_if: the launch does
+// nothing unless *only_if == epoch.  check: a y outside the folded (min,
+// max) (params[1] with mm NULL) sets *check = epoch -- a value no earlier
+// call leaves there, so nothing has to clear it first.
 __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict__ q,
                                                             const float* __restrict__ x,
                                                             const float2* __restrict__ stats,
                                                             const float2* __restrict__ params,
+                                                            const float2* __restrict__ mm, int npart,
+                                                            float* __restrict__ ysp,
+                                                            uint8_t* __restrict__ yzp,
                                                             int64_t C, int64_t T, Affine af,
                                                             int vec, const int* __restrict__ only_if,
-                                                            int* __restrict__ check) {
-  if (only_if && *only_if == 0) return;
+                                                            int* __restrict__ check, int epoch) {
+  if (only_if && *only_if != epoch) return;
+  __shared__ float2 wmm[kRowBlock / 64];
+  __shared__ float4 pl;  // scale, zero point, and the (min, max) of y
+  if (mm) {
+    float lo = INFINITY, hi = -INFINITY;
+    for (int i = threadIdx.x; i < npart; i += kRowBlock) {
+      const float2 p = mm[i];
+      lo = fminf(lo, p.x);
+      hi = fmaxf(hi, p.y);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lo = fminf(lo, __shfl_xor(lo, off, 64));
+      hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+    }
+    if ((threadIdx.x & 63) == 0) wmm[threadIdx.x >> 6] = make_float2(lo, hi);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < kRowBlock / 64; ++w) {
+        lo = fminf(lo, wmm[w].x);
+        hi = fmaxf(hi, wmm[w].y);
+      }
+      float sc;
+      uint8_t zq;
+      const float2 pz = dql_params(lo, hi, &sc, &zq);
+      if (blockIdx.x == 0 && blockIdx.y == 0) {
+        *ysp = sc;
+        *yzp = zq;
+      }
+      pl = make_float4(pz.x, pz.y, lo, hi);
+    }
+  } else if (threadIdx.x == 0) {
+    const float2 p0 = params[0];
+    const float2 p1 = check ? params[1] : make_float2(-INFINITY, INFINITY);
+    pl = make_float4(p0.x, p0.y, p1.x, p1.y);
+  }
+  __syncthreads();
   const int64_t row = blockIdx.y;
   const int64_t c = row % C;
   const RowAffine ra = row_affine(af, C, c, 0.0f, 0.0f);
-  const float2 st = stats[row], pz = params[0];
+  const float4 P = pl;
+  const float2 st = stats[row], pz = make_float2(P.x, P.y);
   const KkDivisor dden = kk_divisor(st.y), dsc = kk_divisor(pz.x);
-  const float2 lim = check ? params[1] : make_float2(-INFINITY, INFINITY);
+  const float2 lim = make_float2(P.z, P.w);
   const float* xr = x + row * T;
   uint8_t* qr = q + row * T;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -659,7 +706,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
       qr[i] = static_cast<uint8_t>(dql_byte(y, pz.x, pz.y));
     }
   }
-  if (check && out) *check = 1;  // every writer stores the same 1
+  if (check && out) *check = epoch;  // every writer stores the same value
 }
 
 // -------------------------------------------------------------- LayerNorm
@@ -2116,6 +2163,14 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
 // checks every y against the bounds and, if one falls outside, flags it;
 // three more launches that do nothing unless flagged then take the exact
 // (min, max) of y, the scale and zero point again, and the bytes again.
+// A value per InstanceNormQuant call for its out-of-bounds flag, never 0
+// (wraps after 2^31 - 1 calls).
+static int next_epoch() {
+  static uint32_t n = 0;
+  n = n % 0x7ffffffeu + 1u;
+  return static_cast<int>(n);
+}
+
 static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, const kk_tensor* y_zp,
                               const kk_tensor* x, float eps, const Affine& af) {
   hipStream_t st = ctx().stream;
@@ -2159,11 +2214,17 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   // an unflagged one ends at once; their loops stride over the rows
   const int64_t fgx = std::min<int64_t>(gx, std::max<int64_t>(1, ceil_div(2048, rows)));
   const dim3 fgrid(static_cast<unsigned>(fgx), static_cast<unsigned>(rows));
-  auto quant = [&](const int* only_if, int* check) {
+  // Up to 2048 rows every quantising block folds the (min, max) partials
+  // itself (rows, or rows * fgx < 4096 on the fallback); beyond, a dql_fold
+  // launch folds them into params.
+  const bool fold_in = rows <= 2048;
+  const int epoch = next_epoch();
+  auto quant = [&](const int* only_if, int* check, int64_t npart) {
     KK_LAUNCH(instnorm_quant, only_if ? fgrid : qgrid, dim3(kRowBlock), 0, st,
-                       static_cast<uint8_t*>(q->data),
-                       xp, static_cast<const float2*>(stats), static_cast<const float2*>(params), C, T,
-                       af, vec ? 1 : 0, only_if, check);
+                       static_cast<uint8_t*>(q->data), xp, static_cast<const float2*>(stats),
+                       static_cast<const float2*>(params),
+                       fold_in ? static_cast<const float2*>(mm) : nullptr, static_cast<int>(npart),
+                       ysp, yzp, C, T, af, vec ? 1 : 0, only_if, check, epoch);
     return check_launch("instnorm_quant");
   };
   int rc = KK_OK;
@@ -2184,16 +2245,19 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
       rc = check_launch("np_blocks_kernel");
     }
   }
-  if (rc == KK_OK) rc = launch_dql_fold(mm, static_cast<int>(rows), params, ysp, yzp, nullptr, flag);
-  if (rc == KK_OK) rc = quant(nullptr, flag);
+  // (dql_fold with clear zeroes the flag; folded in, the flag is compared
+  // with this call's epoch instead)
+  if (rc == KK_OK && !fold_in)
+    rc = launch_dql_fold(mm, static_cast<int>(rows), params, ysp, yzp, nullptr, flag);
+  if (rc == KK_OK) rc = quant(nullptr, flag, rows);
   if (rc == KK_OK && flag) {  // only if a y fell outside the bounds
     KK_LAUNCH(instnorm_minmax, fgrid, dim3(kRowBlock), 0, st, mm, xp,
                        static_cast<const float2*>(stats), C, T, af, vec ? 1 : 0,
-                       static_cast<const int*>(flag));
+                       static_cast<const int*>(flag), epoch);
     rc = check_launch("instnorm_minmax");
-    if (rc == KK_OK)
+    if (rc == KK_OK && !fold_in)
       rc = launch_dql_fold(mm, static_cast<int>(rows * fgx), params, ysp, yzp, flag, nullptr);
-    if (rc == KK_OK) rc = quant(flag, nullptr);
+    if (rc == KK_OK) rc = quant(flag, nullptr, rows * fgx);
   }
   kk_free(ws);  // stream order keeps it alive for the kernels above
   return rc;

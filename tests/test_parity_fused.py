@@ -391,7 +391,12 @@ def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
                                               # rows held in registers (the decoder's
                                               # [1,256,71800]; a 4-element last block)
                                               (256, 71800, 1.0, None), (256, 71800, None, 0.2),
-                                              (16, 65540, 5.0, None)])
+                                              (16, 65540, 5.0, None),
+                                              # up to 2048 rows every quantising block
+                                              # folds the rows' partials; beyond, a fold
+                                              # launch does (with the fallback, both ways)
+                                              (2048, 64, 5.0, None), (2100, 40, 5.0, None),
+                                              (2100, 40, None, 0.2)])
 def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leaky):
     """InstanceNormQuant gives the same bytes, scale and zero point as the
     device's own unfused chain: the float result stored, then
