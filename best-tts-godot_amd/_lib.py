@@ -93,6 +93,10 @@ PROTOTYPES = {
     "kk_dynamic_quantize_linear": [_T, _T, _T, _T],
     "kk_matmul_integer": [_T, _T, _T, _T, _T],
     "kk_matmul_integer_scaled": [_T, _T, _T, _T, _T, _T, _T, _T],
+    "kk_matmul_integer_packed": [_T, _T, _T, _T, _T, _T],
+    "kk_matmul_integer_scaled_packed": [_T, _T, _T, _T, _T, _T, _T, _T, _T],
+    "kk_matmul_integer_pack_bytes": [_T, ctypes.POINTER(_sz)],
+    "kk_matmul_integer_pack": [_T, _T],
     "kk_conv_integer": [_T, _T, _T, _T, _T, _i, _i, _i, _i, _i],
     "kk_conv_integer_scaled": [_T] * 7 + [_i, _i, _i, _i, _i],
     "kk_conv_integer_scaled_qbias": [_T] * 8 + [_i, _i, _i, _i, _i],

@@ -23,7 +23,9 @@
 // one row or column -- are single 16-byte LDS reads.  The next K-step is
 // loaded into registers while this one is multiplied.  The fused
 // Cast -> Mul(scale) (-> Add(bias)) tail of the graph runs in the epilogue.
+#include <mutex>
 #include <type_traits>
+#include <unordered_map>
 
 #include "kk_internal.h"
 
@@ -64,6 +66,10 @@ struct I8Args {
   int64_t cs2_n;
   const float* cb;
   int64_t cb_n;
+  // packed B (i8_packed_kernel): fragments, column sums of b', k-steps
+  const uint8_t* bp;
+  const int32_t* colsum;
+  int nS;
 };
 
 // AV: A rows 16-byte loadable (K % 16 == 0, aligned); BV: B rows dword
@@ -268,8 +274,194 @@ __global__ void __launch_bounds__(kThreads) i8_matmul_kernel(I8Args G) {
   }
 }
 
+// ------------------------------------------------------- packed weights
+// kk_matmul_integer_pack lays a constant [K, N] B out as the MFMA takes it:
+// for column tile t (32 columns) and k-step s (32 k), 64 lanes x 16 bytes,
+// lane (n, g) holding b'[32 s + 16 g + e][32 t + n] for e = 0..15 (zeros past
+// K and N; b' = b for int8, b - 128 for uint8), tiles t-major so that one
+// tile's k-steps are contiguous; then the N column sums of b' (int32,
+// modulo 2^32).  A wave loads a fragment with one 16-byte load a lane,
+// straight into registers: no LDS stage, no transpose, and the column sums
+// are not recomputed per call.
+inline int64_t pack_frag_bytes(int64_t K, int64_t N) {
+  return ceil_div(N, 32) * ceil_div(K, 32) * 1024;
+}
+
+__global__ void __launch_bounds__(256) i8_pack_kernel(uint4* __restrict__ dst,
+                                                      const uint8_t* __restrict__ b, int64_t b_si,
+                                                      int64_t b_sj, int64_t K, int64_t N, int nS,
+                                                      uint32_t flip, int64_t pieces) {
+  for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < pieces;
+       idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int lane = static_cast<int>(idx % 64);
+    const int64_t ts = idx / 64, st = ts % nS, t = ts / nS;
+    const int64_t n = 32 * t + (lane & 31), k0 = 32 * st + 16 * (lane >> 5);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    if (n < N) {
+      for (int e = 0; e < 16; ++e)
+        if (k0 + e < K)
+          w[e >> 2] |= ((static_cast<uint32_t>(b[(k0 + e) * b_si + n * b_sj]) ^ flip) & 0xffu)
+                       << (8 * (e & 3));
+    }
+    dst[idx] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+__global__ void __launch_bounds__(256) i8_colsum_kernel(int32_t* __restrict__ cs,
+                                                        const uint8_t* __restrict__ b, int64_t b_si,
+                                                        int64_t b_sj, int64_t K, int64_t N,
+                                                        uint32_t flip) {
+  const int64_t n = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
+  if (n >= N) return;
+  uint32_t sum = 0;
+  for (int64_t k = 0; k < K; ++k)
+    sum += static_cast<uint32_t>(static_cast<int32_t>(
+        static_cast<int8_t>((static_cast<uint32_t>(b[k * b_si + n * b_sj]) ^ flip) & 0xffu)));
+  cs[n] = static_cast<int32_t>(sum);
+}
+
+// MatMulInteger on packed B, one 32 x 32 output tile a block: the four
+// waves split the k-steps, each loading its share of A (one 16-byte piece a
+// lane: row lane % 32, k 16 (lane / 32) of the step, out of range reading
+// zeros) and of the packed B, SPW steps in flight before it multiplies, and
+// summing its rows of a' on the side (v_dot4 with ones); waves 1-3 hand
+// their accumulators and row sums to wave 0 through LDS, which corrects for
+// the zero points as i8_matmul_kernel does and runs the epilogue.  A and
+// the output are contiguous, their batch dimensions folded into the rows
+// (B is one [K, N] matrix).
+template <int SPW>
+__global__ void __launch_bounds__(kThreads) i8_packed_kernel(I8Args G) {
+  __shared__ int red[3][16][64];
+  __shared__ int rsum[4][32];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int r = lane & 31, g = lane >> 5;
+  const int64_t t = blockIdx.x, m0 = static_cast<int64_t>(blockIdx.y) * 32;
+  const int64_t M = G.M, N = G.N, K = G.K;
+  const int nS = G.nS;
+  const int64_t a_rows = M - m0 < 32 ? M - m0 : 32;
+  const uint32_t a_span = static_cast<uint32_t>((a_rows - 1) * G.a_si + K);
+  const auto a_rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(G.a + m0 * G.a_si), 0,
+                                                      static_cast<int>(a_span), 0x00020000);
+  const uint32_t b_span = static_cast<uint32_t>(nS) * 1024u;
+  const auto b_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(G.bp + t * static_cast<int64_t>(nS) * 1024), 0, static_cast<int>(b_span),
+      0x00020000);
+  const int per = (nS + 3) / 4;
+  const int s0 = w * per, s1 = s0 + per < nS ? s0 + per : nS;
+  const bool row_in = r < a_rows;
+  v16i acc = {};
+  int rs = 0;
+  const uint32_t a_row = static_cast<uint32_t>(r * G.a_si) + 16u * g;
+  const uint32_t kg = 16u * g;
+  const uint32_t K32 = static_cast<uint32_t>(K);
+  for (int c = s0; c < s1; c += SPW) {
+    v4i av[SPW], bv[SPW];
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) {
+      const int st = c + u;
+      const bool in = st < s1 && row_in && 32u * st + kg < K32;
+      av[u] = __builtin_bit_cast(
+          v4i, __builtin_amdgcn_raw_buffer_load_b128(a_rs, in ? a_row + 32u * st : a_span, 0, 0));
+      bv[u] = __builtin_bit_cast(
+          v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                   b_rs, st < s1 ? static_cast<uint32_t>(st * 64 + lane) * 16u : b_span, 0, 0));
+    }
+#pragma unroll
+    for (int u = 0; u < SPW; ++u) {
+      const int st = c + u;
+      const bool in = st < s1 && row_in && 32u * st + kg < K32;
+      const v4i a2 = av[u] ^ static_cast<int>(in ? G.a_flip : 0u);
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a2, bv[u], acc, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) rs = __builtin_amdgcn_sdot4(a2[q], 0x01010101, rs, false);
+    }
+  }
+  rs += __shfl_xor(rs, 32, 64);  // the row's two k halves
+  if (g == 0) rsum[w][r] = rs;
+  if (w > 0) {
+#pragma unroll
+    for (int reg = 0; reg < 16; ++reg) red[w - 1][reg][lane] = acc[reg];
+  }
+  __syncthreads();
+  if (w > 0) return;
+#pragma unroll
+  for (int reg = 0; reg < 16; ++reg)
+    acc[reg] = static_cast<int>(static_cast<uint32_t>(acc[reg]) +
+                                static_cast<uint32_t>(red[0][reg][lane]) +
+                                static_cast<uint32_t>(red[1][reg][lane]) +
+                                static_cast<uint32_t>(red[2][reg][lane]));
+  const int64_t n = 32 * t + r;  // this lane's column
+  if (n >= N) return;
+  const int azo = (G.azp ? static_cast<int>(load_as_i64(G.azp, G.azp_dt, 0)) : 0) -
+                  (G.a_flip ? 128 : 0);
+  const int bzo = (G.bzp ? static_cast<int>(load_as_i64(G.bzp, G.bzp_dt, n * G.bzp_stride)) : 0) -
+                  (G.b_flip ? 128 : 0);
+  const uint32_t uaz = static_cast<uint32_t>(azo), ubz = static_cast<uint32_t>(bzo);
+  const uint32_t colterm = static_cast<uint32_t>(K) * uaz * ubz -
+                           uaz * static_cast<uint32_t>(G.colsum[n]);
+  float sc = 0.0f, bias = 0.0f;
+  if (G.out_f) {
+    sc = G.cs[G.cs_n > 1 ? n : 0];
+    if (G.cs2) sc = sc * G.cs2[G.cs2_n > 1 ? n : 0];
+    if (G.cb) bias = G.cb[G.cb_n > 1 ? n : 0];
+  }
+#pragma unroll
+  for (int reg = 0; reg < 16; ++reg) {
+    const int il = 8 * (reg / 4) + 4 * g + (reg % 4);
+    if (il >= a_rows) continue;
+    const uint32_t rsm = static_cast<uint32_t>(rsum[0][il]) + static_cast<uint32_t>(rsum[1][il]) +
+                         static_cast<uint32_t>(rsum[2][il]) + static_cast<uint32_t>(rsum[3][il]);
+    const int v = static_cast<int>(static_cast<uint32_t>(acc[reg]) - ubz * rsm + colterm);
+    const int64_t o = (m0 + il) * G.som + n;
+    if (G.out_f) {
+      float y = static_cast<float>(v) * sc;
+      if (G.cb) y = y + bias;
+      G.out_f[o] = y;
+    } else {
+      G.out_i[o] = v;
+    }
+  }
+}
+
+struct I8PackRecord {
+  const void* b;
+  int64_t K, N;
+  int b_dt;
+};
+static std::mutex g_i8_pack_mu;
+static std::unordered_map<const void*, I8PackRecord> g_i8_packs;
+
 }  // namespace i8gemm
 using namespace i8gemm;
+
+void i8_forget_pack(const void* p) {
+  std::lock_guard<std::mutex> lock(g_i8_pack_mu);
+  g_i8_packs.erase(p);
+}
+
+static int64_t i8_packed_size(int64_t K, int64_t N) {
+  return pack_frag_bytes(K, N) + ceil_div(4 * N, 256) * 256;
+}
+
+// Checks a packed buffer against a call's [K, N] B: size, alignment, and
+// that the last kk_matmul_integer_pack into it read this very B.
+static int i8_check_packed(const kk_tensor* packed, const kk_tensor* b, const char* who) {
+  KK_TRY(check_tensor(packed, "packed"));
+  if (b->rank != 2) return set_error(KK_E_ARG, "%s: a packed B is [K, N]", who);
+  const int64_t need = i8_packed_size(b->shape[0], b->shape[1]);
+  if (packed->dtype != KK_U8 || !is_contiguous(packed) || numel(packed) != need ||
+      reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
+    return set_error(KK_E_ARG, "%s: packed must be %lld contiguous, 256-byte aligned uint8 bytes",
+                     who, (long long)need);
+  std::lock_guard<std::mutex> lock(g_i8_pack_mu);
+  auto it = g_i8_packs.find(packed->data);
+  if (it == g_i8_packs.end())
+    return set_error(KK_E_ARG, "%s: packed was not made by kk_matmul_integer_pack", who);
+  const I8PackRecord& rec = it->second;
+  if (rec.b != b->data || rec.K != b->shape[0] || rec.N != b->shape[1] || rec.b_dt != b->dtype)
+    return set_error(KK_E_ARG, "%s: packed was made from another B", who);
+  return KK_OK;
+}
 
 static bool aligned_to(const void* p, int bytes) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
@@ -334,6 +526,40 @@ static int i8_launch(const I8Args& G, int64_t batch) {
   return check_launch("i8_matmul_kernel");
 }
 
+// Launches i8_packed_kernel when A and the output are contiguous (their
+// batch dimensions folded into the rows), A's rows are 16-byte loadable
+// and every offset stays below 2^31; false, launching nothing, otherwise
+// (the caller then runs i8_matmul_kernel on b itself).
+static bool i8_packed_try(I8Args* G, const kk_tensor* out, const kk_tensor* a,
+                          const kk_tensor* packed) {
+  const int64_t K = G->K, N = G->N;
+  if (!is_contiguous(a) || !is_contiguous(out) || K % 16 != 0 || !aligned_to(a->data, 16))
+    return false;
+  const int64_t rows = numel(a) / K;
+  const int64_t nS = ceil_div(K, 32), gy = ceil_div(rows, 32), gx = ceil_div(N, 32);
+  if (32 * K > (int64_t{1} << 31) - 256 || nS * 1024 > (int64_t{1} << 31) - 256 || gy > 65535 ||
+      gx > 0x7fffffff)
+    return false;
+  G->M = rows;
+  G->a_si = K;
+  G->som = N;
+  G->son = 1;
+  G->bp = static_cast<const uint8_t*>(packed->data);
+  G->colsum = reinterpret_cast<const int32_t*>(G->bp + pack_frag_bytes(K, N));
+  G->nS = static_cast<int>(nS);
+  const int per = static_cast<int>((nS + 3) / 4);
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  hipStream_t st = ctx().stream;
+  if (per <= 1) KK_LAUNCH((i8_packed_kernel<1>), grid, dim3(kThreads), 0, st, *G);
+  else if (per <= 2) KK_LAUNCH((i8_packed_kernel<2>), grid, dim3(kThreads), 0, st, *G);
+  else if (per <= 4) KK_LAUNCH((i8_packed_kernel<4>), grid, dim3(kThreads), 0, st, *G);
+  else if (per <= 6) KK_LAUNCH((i8_packed_kernel<6>), grid, dim3(kThreads), 0, st, *G);
+  else if (per <= 8) KK_LAUNCH((i8_packed_kernel<8>), grid, dim3(kThreads), 0, st, *G);
+  else if (per <= 12) KK_LAUNCH((i8_packed_kernel<12>), grid, dim3(kThreads), 0, st, *G);
+  else KK_LAUNCH((i8_packed_kernel<16>), grid, dim3(kThreads), 0, st, *G);
+  return true;
+}
+
 }  // namespace kk
 
 using namespace kk;
@@ -342,21 +568,38 @@ extern "C" {
 
 int kk_matmul_integer(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
                       const kk_tensor* a_zp, const kk_tensor* b_zp) {
+  return kk_matmul_integer_packed(out, a, b, nullptr, a_zp, b_zp);
+}
+
+int kk_matmul_integer_packed(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
+                             const kk_tensor* packed, const kk_tensor* a_zp,
+                             const kk_tensor* b_zp) {
+  const char* who = packed ? "kk_matmul_integer_packed" : "kk_matmul_integer";
   I8Args G;
   int64_t batch = 0;
-  KK_TRY(i8_setup(&G, &batch, out, a, b, a_zp, b_zp, KK_I32, "kk_matmul_integer"));
+  KK_TRY(i8_setup(&G, &batch, out, a, b, a_zp, b_zp, KK_I32, who));
+  if (packed) KK_TRY(i8_check_packed(packed, b, who));
   if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
   if (G.K == 0) return kk_fill(out, 0.0);
+  if (packed && i8_packed_try(&G, out, a, packed)) return check_launch("i8_packed_kernel");
   return i8_launch(G, batch);
 }
 
 int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
                              const kk_tensor* a_zp, const kk_tensor* b_zp, const kk_tensor* scale,
                              const kk_tensor* scale2, const kk_tensor* bias) {
-  const char* who = "kk_matmul_integer_scaled";
+  return kk_matmul_integer_scaled_packed(out, a, b, nullptr, a_zp, b_zp, scale, scale2, bias);
+}
+
+int kk_matmul_integer_scaled_packed(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
+                                    const kk_tensor* packed, const kk_tensor* a_zp,
+                                    const kk_tensor* b_zp, const kk_tensor* scale,
+                                    const kk_tensor* scale2, const kk_tensor* bias) {
+  const char* who = packed ? "kk_matmul_integer_scaled_packed" : "kk_matmul_integer_scaled";
   I8Args G;
   int64_t batch = 0;
   KK_TRY(i8_setup(&G, &batch, out, a, b, a_zp, b_zp, KK_F32, who));
+  if (packed) KK_TRY(i8_check_packed(packed, b, who));
   // scale and bias: one value or one per output column, contiguous fp32
   auto per_col = [&](const kk_tensor* t, const char* what, const float** p, int64_t* n) -> int {
     KK_TRY(check_tensor(t, what));
@@ -376,7 +619,51 @@ int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_
   if (bias) KK_TRY(per_col(bias, "bias", &G.cb, &G.cb_n));
   if (G.M == 0 || G.N == 0 || batch == 0) return KK_OK;
   if (G.K == 0) return set_error(KK_E_UNSUPPORTED, "%s: K = 0", who);
+  if (packed && i8_packed_try(&G, out, a, packed)) return check_launch("i8_packed_kernel");
   return i8_launch(G, batch);
+}
+
+int kk_matmul_integer_pack_bytes(const kk_tensor* b, size_t* bytes) {
+  KK_TRY(check_tensor(b, "b"));
+  if (!bytes) return set_error(KK_E_ARG, "kk_matmul_integer_pack_bytes: bytes is NULL");
+  if (b->rank != 2 || !(b->dtype == KK_U8 || b->dtype == KK_I8) || b->shape[0] == 0 ||
+      b->shape[1] == 0)
+    return set_error(KK_E_ARG, "kk_matmul_integer_pack_bytes: b must be a non-empty [K, N] "
+                               "int8/uint8 matrix");
+  *bytes = static_cast<size_t>(i8_packed_size(b->shape[0], b->shape[1]));
+  return KK_OK;
+}
+
+int kk_matmul_integer_pack(const kk_tensor* packed, const kk_tensor* b) {
+  const char* who = "kk_matmul_integer_pack";
+  KK_TRY(require_ready());
+  size_t bytes = 0;
+  KK_TRY(kk_matmul_integer_pack_bytes(b, &bytes));
+  KK_TRY(check_tensor(packed, "packed"));
+  if (packed->dtype != KK_U8 || !is_contiguous(packed) ||
+      numel(packed) != static_cast<int64_t>(bytes) ||
+      reinterpret_cast<uintptr_t>(packed->data) % 256 != 0)
+    return set_error(KK_E_ARG, "%s: packed must be %zu contiguous, 256-byte aligned uint8 bytes",
+                     who, bytes);
+  const int64_t K = b->shape[0], N = b->shape[1];
+  const int64_t nS = ceil_div(K, 32);
+  if (nS > (int64_t{1} << 21))
+    return set_error(KK_E_UNSUPPORTED, "%s: K = %lld too large", who, (long long)K);
+  const uint32_t flip = b->dtype == KK_U8 ? 0x80u : 0u;
+  const int64_t frag = pack_frag_bytes(K, N), pieces = frag / 16;
+  uint8_t* dst = static_cast<uint8_t*>(packed->data);
+  const uint8_t* src = static_cast<const uint8_t*>(b->data);
+  hipStream_t st = ctx().stream;
+  const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(pieces, 256), 65536));
+  KK_LAUNCH(i8_pack_kernel, dim3(grid), dim3(256), 0, st, reinterpret_cast<uint4*>(dst), src,
+            b->strides[0], b->strides[1], K, N, static_cast<int>(nS), flip, pieces);
+  KK_TRY(check_launch("i8_pack_kernel"));
+  KK_LAUNCH(i8_colsum_kernel, dim3(static_cast<unsigned>(ceil_div(N, 256))), dim3(256), 0, st,
+            reinterpret_cast<int32_t*>(dst + frag), src, b->strides[0], b->strides[1], K, N, flip);
+  KK_TRY(check_launch("i8_colsum_kernel"));
+  std::lock_guard<std::mutex> lock(g_i8_pack_mu);
+  g_i8_packs[packed->data] = I8PackRecord{b->data, K, N, b->dtype};
+  return KK_OK;
 }
 
 }  // extern "C"

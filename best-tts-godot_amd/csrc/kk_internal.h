@@ -88,6 +88,9 @@ void conv_i8_forget_pack(const void* p);
 // The same for a packed fp16 matrix-core convolution weight (kk_conv_f16.hip).
 void convh_forget_pack(const void* p);
 void gemm_forget_pack(const void* p);
+// Drops the record of what a packed MatMulInteger B at `p` was made from
+// (kk_free calls it).
+void i8_forget_pack(const void* p);
 
 // Thread-local last error; set_error returns `code` so call sites can
 // `return set_error(KK_E_ARG, "...")`.

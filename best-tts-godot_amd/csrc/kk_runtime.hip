@@ -290,6 +290,7 @@ static void arena_release(Arena* a) {
       conv_i8_forget_pack(q);
       convh_forget_pack(q);
       gemm_forget_pack(q);
+      i8_forget_pack(q);
       p.in_pool.insert(q);
       p.free_lists[it->second].push_back(q);
       p.pooled_bytes += it->second;
@@ -586,6 +587,7 @@ int kk_free(void* dptr) {
   conv_i8_forget_pack(dptr);
   convh_forget_pack(dptr);
   gemm_forget_pack(dptr);
+  i8_forget_pack(dptr);
   p.pooled_bytes += it->second;
   p.live_bytes -= it->second;
   return KK_OK;

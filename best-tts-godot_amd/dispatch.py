@@ -433,13 +433,16 @@ def dispatch(op, node_input, node_output, at, env):
                 scale, scale2 = ops.binary("Mul", scale, scale2), None
         else:
             scale = _f32(to_device(inp(4)))
+        # attribute "packed" (set by a graph at load): the name of this
+        # constant B's kk_matmul_integer_pack layout in env
+        packed = env.get(at.get("packed"))
         if a.shape[-1] and per_col(scale) and per_col(bias):
-            out = ops.matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias, scale2)
+            out = ops.matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias, scale2, packed=packed)
         else:
             if scale2 is not None:
                 scale = ops.binary("Mul", scale, scale2)
-            out = ops.binary("Mul", ops.matmul_integer(a, b, a_zp, b_zp).astype(np.float32),
-                             scale)
+            out = ops.binary("Mul", ops.matmul_integer(a, b, a_zp, b_zp, packed=packed)
+                             .astype(np.float32), scale)
             if bias is not None:
                 out = ops.binary("Add", out, bias)
     elif op == "InstanceNormScaleShift":

@@ -245,7 +245,10 @@ class PackedGraph:
             self.frees[i].append(name)
 
     def _pack_conv_weights(self):
-        """Each quantised conv with its bias quantisation folded in whose
+        """Each fused quantised Linear (QMatMulScaled) with a constant 2-D B
+        gets B packed once (ops.matmul_integer_pack), under
+        "<B>#i8packed", named in its node's attribute "packed".  Each
+        quantised conv with its bias quantisation folded in whose
         weight and weight zero point are constants gets its weights packed
         once (ops.conv_integer_pack), under "<weight>#packed"; its node names
         that in attribute "packed" and skips the per-call re-layout.  So does
@@ -256,6 +259,17 @@ class PackedGraph:
         for k, (op, ins, outs, at) in enumerate(self.nodes):
             if op in ("Conv", "ConvTranspose"):
                 self._pack_fp16_conv(k, op, ins, outs, at, packs)
+                continue
+            if op == "QMatMulScaled":
+                # a constant 2-D B: packed once for the int8 matrix cores
+                # (ops.matmul_integer_pack)
+                bt = self.weights.get(ins[1])
+                if isinstance(bt, DeviceTensor) and bt.ndim == 2 and bt.dtype in (np.int8, np.uint8):
+                    key = (ins[1], "i8")
+                    if key not in packs:
+                        packs[key] = f"{ins[1]}#i8packed"
+                        self.weights[packs[key]] = ops.matmul_integer_pack(bt)
+                    self.nodes[k] = (op, ins, outs, dict(at, packed=packs[key]))
                 continue
             if op != "QConvScaled" or not at.get("bias_quant"):
                 continue

@@ -279,23 +279,44 @@ def dynamic_quantize_linear(x):
     return y, scale, zp
 
 
-def matmul_integer(a, b, a_zp=None, b_zp=None):
+def matmul_integer_pack(b):
+    """The packed form of a constant [K, N] int8/uint8 MatMulInteger B for
+    the int8 matrix cores (uint8 bytes on the device), for
+    matmul_integer(packed=...) and matmul_integer_scaled(packed=...)."""
+    nbytes = ctypes.c_size_t(0)
+    _lib.call("kk_matmul_integer_pack_bytes", b.desc(), ctypes.byref(nbytes))
+    packed = DeviceTensor.empty((nbytes.value,), np.uint8)
+    _lib.call("kk_matmul_integer_pack", packed.desc(), b.desc())
+    return packed
+
+
+def matmul_integer(a, b, a_zp=None, b_zp=None, packed=None):
     batch = broadcast_shape(a.shape[:-2], b.shape[:-2])
     out = DeviceTensor.empty(batch + (a.shape[-2], b.shape[-1]), np.int32)
-    _lib.call("kk_matmul_integer", out.desc(), a.desc(), b.desc(), _d(a_zp), _d(b_zp))
+    if packed is None:
+        _lib.call("kk_matmul_integer", out.desc(), a.desc(), b.desc(), _d(a_zp), _d(b_zp))
+    else:
+        _lib.call("kk_matmul_integer_packed", out.desc(), a.desc(), b.desc(), packed.desc(),
+                  _d(a_zp), _d(b_zp))
     return out
 
 
-def matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias=None, scale2=None):
+def matmul_integer_scaled(a, b, a_zp, b_zp, scale, bias=None, scale2=None, packed=None):
     """MatMulInteger -> Cast(float) -> Mul(scale) (-> Add(bias)) in one
     launch, the scale optionally the product scale * scale2 (rounded once,
     as a Mul node forms it); each holds 1 or N (the output's columns)
-    values."""
+    values.  `packed`: b's matmul_integer_pack."""
     batch = broadcast_shape(a.shape[:-2], b.shape[:-2])
     out = DeviceTensor.empty(batch + (a.shape[-2], b.shape[-1]), np.float32)
-    _lib.call("kk_matmul_integer_scaled", out.desc(), a.desc(), b.desc(), _d(a_zp), _d(b_zp),
-              scale.contiguous().desc(), _d(None if scale2 is None else scale2.contiguous()),
-              _d(None if bias is None else bias.contiguous()))
+    sc = scale.contiguous().desc()
+    s2 = _d(None if scale2 is None else scale2.contiguous())
+    bi = _d(None if bias is None else bias.contiguous())
+    if packed is None:
+        _lib.call("kk_matmul_integer_scaled", out.desc(), a.desc(), b.desc(), _d(a_zp), _d(b_zp),
+                  sc, s2, bi)
+    else:
+        _lib.call("kk_matmul_integer_scaled_packed", out.desc(), a.desc(), b.desc(), packed.desc(),
+                  _d(a_zp), _d(b_zp), sc, s2, bi)
     return out
 
 

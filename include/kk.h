@@ -302,6 +302,28 @@ int kk_matmul_integer_scaled(const kk_tensor* out, const kk_tensor* a, const kk_
                              const kk_tensor* a_zp, const kk_tensor* b_zp,
                              const kk_tensor* scale, const kk_tensor* scale2,
                              const kk_tensor* bias);
+/* A constant [K, N] B of MatMulInteger laid out once for the int8 matrix
+ * cores: the reference's op_matmul_integer (ref_runtime.py:119-127) reads
+ * b as it is on every call; a graph whose weights do not change between
+ * calls packs them at load.  kk_matmul_integer_pack_bytes gives the size of
+ * the uint8 buffer (256-byte aligned) kk_matmul_integer_pack fills from b
+ * (int8 or uint8): the fragments of every 32-column, 32-k tile in the
+ * matrix cores' lane order, then the int32 column sums. */
+int kk_matmul_integer_pack_bytes(const kk_tensor* b, size_t* bytes);
+int kk_matmul_integer_pack(const kk_tensor* packed, const kk_tensor* b);
+/* kk_matmul_integer and kk_matmul_integer_scaled on a packed B: the same
+ * results bit for bit, in one launch of a kernel that loads the packed
+ * fragments straight into registers.  b is the tensor the pack was made
+ * from (KK_E_ARG otherwise); where A or out is not contiguous, or K is not
+ * a multiple of 16, the call runs the unpacked kernel on b. */
+int kk_matmul_integer_packed(const kk_tensor* out, const kk_tensor* a, const kk_tensor* b,
+                             const kk_tensor* packed, const kk_tensor* a_zp,
+                             const kk_tensor* b_zp);
+int kk_matmul_integer_scaled_packed(const kk_tensor* out, const kk_tensor* a,
+                                    const kk_tensor* b, const kk_tensor* packed,
+                                    const kk_tensor* a_zp, const kk_tensor* b_zp,
+                                    const kk_tensor* scale, const kk_tensor* scale2,
+                                    const kk_tensor* bias);
 /* ConvInteger (ref_runtime.py:130-134): int32 conv of (x - x_zp) with
  * (w - w_zp); x uint8 [N, Cin, L], w uint8/int8 [Cout, Cin, K]; padding
  * reads 0 after the zero-point shift. */

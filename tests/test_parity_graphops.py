@@ -176,6 +176,90 @@ def test_matmul_integer_variants(gpu, oracle, case):
     assert_bitexact(got, want, f"MatMulInteger {case}")
 
 
+PACKED_CASES = {
+    # (M, K, N, a dtype, b dtype, zero points): the text encoder's ALBERT
+    # shapes, the predictors' style Linear (M = 1), the duration projection
+    # (N = 50), partial tiles, both byte types
+    "albert_qkv": (130, 768, 768, np.uint8, np.int8, "col"),
+    "ffn_up": (130, 768, 2048, np.uint8, np.int8, "col"),
+    "ffn_down": (130, 2048, 768, np.uint8, np.int8, "col"),
+    "gemv": (1, 128, 1024, np.uint8, np.int8, "tensor"),
+    "n50": (10, 512, 50, np.uint8, np.int8, "col"),
+    "tails": (33, 48, 33, np.uint8, np.uint8, "tensor"),
+    "i8_i8": (65, 512, 68, np.int8, np.int8, "col"),
+    "no_zp": (7, 32, 50, np.uint8, np.int8, None),
+    "k_odd": (9, 37, 40, np.uint8, np.int8, "col"),  # K % 16: the unpacked kernel on b
+}
+
+
+@pytest.mark.parametrize("case", list(PACKED_CASES) + ["batch", "strided_a", "wraps_mod_2_32"])
+def test_matmul_integer_packed(gpu, case):
+    """kk_matmul_integer_pack'ed B: kk_matmul_integer_packed and
+    kk_matmul_integer_scaled_packed give the unpacked kernels' bits (and
+    int64 brute force's, wrapped to int32), one launch of the packed kernel
+    where A and out are contiguous and K % 16 == 0, the unpacked kernel on b
+    otherwise (a strided A, K = 37)."""
+    r = rng(27)
+    ops, D = gpu.ops, gpu.to_device
+    if case in PACKED_CASES:
+        m, k, n, adt, bdt, zps = PACKED_CASES[case]
+        lo = -128 if adt == np.int8 else 0
+        a = r.integers(lo, lo + 256, (1, m, k)).astype(adt)
+        lo = -128 if bdt == np.int8 else 0
+        b = r.integers(lo, lo + 256, (k, n)).astype(bdt)
+        azp = None if zps is None else np.asarray(r.integers(0, 256) if adt == np.uint8
+                                                  else r.integers(-128, 128), adt)
+        bzp = (None if zps is None else
+               np.asarray(r.integers(-4, 5, n if zps == "col" else ()), bdt) if bdt == np.int8
+               else np.asarray(r.integers(120, 136, n if zps == "col" else ()), bdt))
+        da = D(a)
+    elif case == "batch":
+        a = r.integers(0, 256, (2, 3, 40, 96)).astype(np.uint8)
+        b = r.integers(-128, 128, (96, 72)).astype(np.int8)
+        azp, bzp = np.uint8(9), r.integers(-5, 6, 72).astype(np.int8)
+        da = D(a)
+    elif case == "strided_a":
+        a_full = r.integers(0, 256, (64, 256)).astype(np.uint8)
+        a = a_full[:, ::2]
+        b = r.integers(-128, 128, (128, 100)).astype(np.int8)
+        azp, bzp = np.uint8(1), None
+        da = D(a_full).slice_axis(1, 0, 256, 2)
+    else:
+        a = np.full((1, 4, 40000), 255, np.uint8)
+        b = np.full((40000, 8), 127, np.int8)
+        azp, bzp = np.uint8(0), np.full(8, -128, np.int8)
+        da = D(a)
+    db = D(np.ascontiguousarray(b))
+    dazp = None if azp is None else D(np.asarray(azp))
+    dbzp = None if bzp is None else D(np.asarray(bzp))
+    packed = ops.matmul_integer_pack(db)
+    want = gpu.to_host(ops.matmul_integer(da, db, dazp, dbzp))
+    got = gpu.to_host(ops.matmul_integer(da, db, dazp, dbzp, packed=packed))
+    assert_bitexact(got, want, f"packed MatMulInteger {case}")
+    if a.ndim == 2 or a.shape[0] == 1 and a.ndim == 3:
+        brute = brute_matmul_integer(a.reshape(a.shape[-2:]), b, azp, bzp)
+        assert_bitexact(np.asarray(want).reshape(brute.shape), brute, f"unpacked vs brute {case}")
+    n = b.shape[1]
+    scale = D(r.uniform(1e-4, 1e-3, (n,)).astype(np.float32))
+    scale2 = D(np.asarray([0.02], np.float32))
+    bias = D(r.normal(0, 1, (n,)).astype(np.float32))
+    want = gpu.to_host(ops.matmul_integer_scaled(da, db, dazp, dbzp, scale, bias, scale2))
+    got = gpu.to_host(ops.matmul_integer_scaled(da, db, dazp, dbzp, scale, bias, scale2,
+                                                packed=packed))
+    assert_bitexact(got, want, f"packed scaled MatMulInteger {case}")
+
+
+def test_matmul_integer_packed_refuses_mismatch(gpu):
+    r = rng(28)
+    ops, D = gpu.ops, gpu.to_device
+    b1 = D(r.integers(-128, 128, (64, 32)).astype(np.int8))
+    b2 = D(r.integers(-128, 128, (64, 32)).astype(np.int8))
+    a = D(r.integers(0, 256, (1, 5, 64)).astype(np.uint8))
+    packed = ops.matmul_integer_pack(b1)
+    with pytest.raises(Exception, match="another B"):
+        ops.matmul_integer(a, b2, None, None, packed=packed)
+
+
 @pytest.mark.parametrize("cin,cout,k,L,pad,dil", [(512, 512, 3, 240, 1, 1), (1090, 1024, 3, 40, 1, 1),
                                                   (256, 256, 7, 300, 9, 3), (1, 1, 3, 50, 1, 1),
                                                   (22, 128, 1, 480, 0, 1)])
