@@ -535,19 +535,22 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
   const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
   if (vec) {
     const RowSplit rsp = row_split(row, T);
+    // (cached loads: the statistics pass before this one read the row, and
+    // part of it is still in the last-level cache -- a second read of a
+    // 208 MB tensor runs at 6.3 TB/s, 5.6 with non-temporal loads)
     for (int64_t k = i0; k < rsp.nv; k += stride) {
       const int64_t i = rsp.hh + 4 * k;
-      const float4 v = ld_stream4(xr + i);
+      const float4 v = *reinterpret_cast<const float4*>(xr + i);
       const float4 q = kk_div4(make_float4(v.x - st.x, v.y - st.x, v.z - st.x, v.w - st.x), dden);
       st_stream4(orow + i, make_float4(apply_affine(q.x, ra, af), apply_affine(q.y, ra, af),
                                        apply_affine(q.z, ra, af), apply_affine(q.w, ra, af)));
     }
     int64_t i;
     if (rsp.edge(i))
-      st_stream(orow + i, apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af));
+      st_stream(orow + i, apply_affine((xr[i] - st.x) / st.y, ra, af));
   } else {
     for (int64_t i = i0; i < T; i += stride)
-      st_stream(orow + i, apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af));
+      st_stream(orow + i, apply_affine((xr[i] - st.x) / st.y, ra, af));
   }
 }
 
@@ -681,7 +684,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
     const RowSplit rsp = row_split(row, T);
     for (int64_t k = i0; k < rsp.nv; k += stride) {
       const int64_t i = rsp.hh + 4 * k;
-      const float4 v = ld_stream4(xr + i);
+      const float4 v = *reinterpret_cast<const float4*>(xr + i);  // cached: as instnorm_apply
       const float4 q = kk_div4(make_float4(v.x - st.x, v.y - st.x, v.z - st.x, v.w - st.x), dden);
       const float y0 = apply_affine(q.x, ra, af);
       const float y1 = apply_affine(q.y, ra, af);
@@ -695,13 +698,13 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
     }
     int64_t i;
     if (rsp.edge(i)) {
-      const float y = apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af);
+      const float y = apply_affine((xr[i] - st.x) / st.y, ra, af);
       out |= y < lim.x || y > lim.y;
       qr[i] = static_cast<uint8_t>(dql_byte(y, pz.x, pz.y));
     }
   } else {
     for (int64_t i = i0; i < T; i += stride) {
-      const float y = apply_affine((ld_stream(xr + i) - st.x) / st.y, ra, af);
+      const float y = apply_affine((xr[i] - st.x) / st.y, ra, af);
       out |= y < lim.x || y > lim.y;
       qr[i] = static_cast<uint8_t>(dql_byte(y, pz.x, pz.y));
     }
