@@ -105,10 +105,12 @@ PROTOTYPES = {
     "kk_conv_integer_packed_bytes": [ctypes.c_int64] * 3 + [ctypes.POINTER(ctypes.c_int64)],
     "kk_conv_integer_pack": [_T] * 3,
     "kk_conv_integer_scaled_qbias_packed": [_T] * 10 + [_i] * 5,
+    "kk_conv_integer_scaled_qbias_packed_leaves": [_T] * 11 + [_i] * 5,
     "kk_conv_integer_scaled_qbias_noalloc": [_T] * 8 + [_i, _i, _i, _i, _i],
     "kk_instance_norm_scale_shift": [_T, _T, _T, _T, _f, _i, _f],
     "kk_instance_norm_scale_shift_snake": [_T, _T, _T, _T, _T, _T, _f],
     "kk_instance_norm_quant": [_T, _T, _T, _T, _T, _T, _T, _T, _f, _i, _f],
+    "kk_instance_norm_quant_leaves": [_T, _T, _T, _T, _T, _T, _T, _T, _f, _i, _f, _T],
     "kk_lstm": [_T] * 13 + [_i, _i],
     "kk_stft": [_T, _T, _T, ctypes.c_int64, ctypes.c_int64, _i],
     "kk_resize": [_T, _T, _i, _d],

@@ -36,6 +36,14 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 constexpr int kTileM = 128;  // output channels per block (2 waves x 64)
 constexpr int kCinAlign = 64;   // channels per chunk: two 32-deep MFMA steps
 constexpr int kRowPitch = 80;   // LDS bytes per 64-channel row (16-byte pad: staggered banks)
+constexpr int kLeafPitch = 136; // LDS floats per output row in the leaf sums' transpose
+
+// LDS of a block: the staged rows and their channel sums, the per-channel
+// epilogue constants; with leaf sums, then the 64-row transpose area.
+__host__ __device__ constexpr int conv_leaf_off(int rows) {
+  return (rows * (kRowPitch + 4) + 2 * kTileM * 4 + 15) & ~15;
+}
+constexpr int kLeafBytes = 64 * kLeafPitch * 4;
 
 // The graph's per-call bias quantisation ahead of a quantised conv:
 // scale = Mul(sa, sw), bias_int32 = Cast(Floor(Div(bias, scale))); sa and sw
@@ -144,6 +152,11 @@ struct ConvI8Args {
   int64_t Cout, Cin, CinP, Kw, s, d, L, p0, Lout, Kreal;
   int W4;               // time rows staged per block: the window plus alignment slack
   int aligned;          // rows start 4-byte aligned (L % 4 == 0): dword loads
+  // with outf and 128-step tiles: leaf[(n Cout + co) nleaf + t] = the sum of
+  // the block's 128 outputs of row co at steps 128 t .. 128 t + 127 in
+  // numpy's order, for t < nleaf (the leaves of the rows' whole 8192-blocks)
+  float* leaf;
+  int64_t nleaf;
 };
 
 // Block: 128 output channels x TN output steps, 4 waves as 2 (channels) x
@@ -376,14 +389,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
       RES ? const_cast<float*>(A.resid) + b * A.Cout * A.Lout : nullptr, 0,
       RES ? static_cast<int>(A.Cout * A.Lout * 4) : 0, 0x00020000);
   const uint32_t r_off = static_cast<uint32_t>(4 * (m0 * A.Lout + nb)) + lane_off;
+  // This block's outputs are one numpy leaf of each of its rows (the
+  // InstanceNorm that reads them sums its rows in numpy's pairwise order,
+  // 8192-blocks of 64 leaves of 128 elements): its sum is formed here, in
+  // that order, from the values as stored -- accumulator k of 8 sums the
+  // elements 8 m + k, m = 0..15, one after another; then ((a0 + a1) + (a2 +
+  // a3)) + ((a4 + a5) + (a6 + a7)).  A half (mi) of the tile, 64 rows x 128
+  // steps, goes through LDS (kLeafPitch floats a row: the two rows a store
+  // instruction writes fall 32 banks apart), where four threads a row each
+  // sum two accumulators from their own addresses and two shuffles form the
+  // tree.
+  const bool leafy = TN == 128 && A.leaf && static_cast<int64_t>(tile.x) < A.nleaf;
+  float* const lt = reinterpret_cast<float*>(conv_lds + conv_leaf_off(A.W4));  // [64][kLeafPitch]
   auto epilogue = [&](auto full_tile) {
     constexpr bool kFull = decltype(full_tile)::value;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
-      // the residual of this half of the lane's outputs, all loads issued
-      // before the first store (a load after a store to a possibly aliasing
-      // address would wait for it: one memory round trip per element)
-      float rv[16][NI];
+      // the stored values (for the leaf sums), and before them the residual
+      // of this half of the lane's outputs, all its loads issued before the
+      // first store (a load after a store to a possibly aliasing address
+      // would wait for it: one memory round trip per element)
+      float yv[16][NI];
       if constexpr (RES) {
 #pragma unroll
         for (int reg = 0; reg < 16; ++reg) {
@@ -391,7 +417,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
           const uint32_t roff = r_off + static_cast<uint32_t>(cr) * lout4;
 #pragma unroll
           for (int ni = 0; ni < NI; ++ni)
-            rv[reg][ni] = __builtin_bit_cast(
+            yv[reg][ni] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(rrs, roff + 128u * ni, 0, 0));
         }
       }
@@ -409,12 +435,40 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) c
           const int v = acc[mi][ni][reg] + c - zS[ni];
           char* dst = ob + (roff + 128u * ni);
           if constexpr (RES) {
-            *reinterpret_cast<float*>(dst) = static_cast<float>(v) * sc + rv[reg][ni];
+            yv[reg][ni] = static_cast<float>(v) * sc + yv[reg][ni];
+            *reinterpret_cast<float*>(dst) = yv[reg][ni];
           } else if (A.outf) {
-            *reinterpret_cast<float*>(dst) = static_cast<float>(v) * sc;
+            yv[reg][ni] = static_cast<float>(v) * sc;
+            *reinterpret_cast<float*>(dst) = yv[reg][ni];
           } else {
             *reinterpret_cast<int*>(dst) = v;
           }
+        }
+      }
+      if constexpr (TN == 128) {
+        if (leafy) {  // block-uniform: every wave meets the barriers
+#pragma unroll
+          for (int reg = 0; reg < 16; ++reg) {
+            const int rl = wm * 32 + 8 * (reg / 4) + 4 * g + (reg % 4);
+#pragma unroll
+            for (int ni = 0; ni < NI; ++ni)
+              lt[rl * kLeafPitch + wn * 64 + 32 * ni + r] = yv[reg][ni];
+          }
+          __syncthreads();
+          const int rl = tid >> 2, q = tid & 3;  // row rl, accumulators 2q and 2q + 1
+          const float* src = lt + rl * kLeafPitch + 2 * q;
+          float a0 = src[0], a1 = src[1];
+#pragma unroll
+          for (int m = 1; m < 16; ++m) {
+            a0 = a0 + src[8 * m];
+            a1 = a1 + src[8 * m + 1];
+          }
+          float p = a0 + a1;
+          p = p + __shfl_xor(p, 1, 64);
+          p = p + __shfl_xor(p, 2, 64);
+          const int cl = (rl >> 5) * 64 + 32 * mi + (rl & 31);
+          if (q == 0 && cl < c_rem) A.leaf[(b * A.Cout + m0 + cl) * A.nleaf + tile.x] = p;
+          if (mi == 0) __syncthreads();  // (the next half reuses the area)
         }
       }
     }
@@ -574,7 +628,8 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
                      const kk_tensor* scale, int stride, int dilation, int pad0, int pad1,
                      bool outf, const kk_tensor* qb_sa = nullptr, const kk_tensor* qb_sw = nullptr,
                      const kk_tensor* qb_bias = nullptr, void* fixed_ws = nullptr,
-                     const kk_tensor* resid = nullptr, const kk_tensor* packed = nullptr) {
+                     const kk_tensor* resid = nullptr, const kk_tensor* packed = nullptr,
+                     const kk_tensor* leaves = nullptr) {
   const int64_t N = x->shape[0], Cin = x->shape[1], L = x->shape[2];
   const int64_t Cout = w->shape[0], Kw = w->shape[2];
   const int64_t Lout = out->shape[2];
@@ -632,18 +687,25 @@ static int conv_integer_run(const kk_tensor* out, const kk_tensor* x, const kk_t
     A.L = L; A.p0 = pad0; A.Lout = Lout; A.Kreal = Cin * Kw;
     A.resid = resid ? static_cast<const float*>(resid->data) : nullptr;
     A.aligned = (L % 4 == 0) && (reinterpret_cast<uintptr_t>(x->data) % 4 == 0);
-    const int tn = conv_launch_tile(stride, dilation, Kw, N, CoutP, Lout);
+    // leaf sums need the 128-step tiles (checked to fit by the caller)
+    const int tn = leaves ? 128 : conv_launch_tile(stride, dilation, Kw, N, CoutP, Lout);
+    if (leaves) {
+      A.leaf = static_cast<float*>(leaves->data);
+      A.nleaf = (Lout / 8192) * 64;
+    }
     A.W4 = static_cast<int>(conv_rows(tn, stride, dilation, Kw));
     const dim3 grid(static_cast<unsigned>(ceil_div(Lout, tn)),
                     static_cast<unsigned>(CoutP / kTileM), static_cast<unsigned>(N));
     rc = check_xcd_grid(grid, "ConvInteger");
     if (rc == KK_OK) {
+      const size_t lds = A.leaf ? static_cast<size_t>(conv_leaf_off(A.W4) + kLeafBytes)
+                                : conv_lds(A.W4);
       if (A.resid) {
-        if (tn == 128) KK_LAUNCH((conv_i8_kernel<128, true>), grid, dim3(256), conv_lds(A.W4), st, A);
-        else KK_LAUNCH((conv_i8_kernel<64, true>), grid, dim3(256), conv_lds(A.W4), st, A);
+        if (tn == 128) KK_LAUNCH((conv_i8_kernel<128, true>), grid, dim3(256), lds, st, A);
+        else KK_LAUNCH((conv_i8_kernel<64, true>), grid, dim3(256), lds, st, A);
       } else {
-        if (tn == 128) KK_LAUNCH((conv_i8_kernel<128, false>), grid, dim3(256), conv_lds(A.W4), st, A);
-        else KK_LAUNCH((conv_i8_kernel<64, false>), grid, dim3(256), conv_lds(A.W4), st, A);
+        if (tn == 128) KK_LAUNCH((conv_i8_kernel<128, false>), grid, dim3(256), lds, st, A);
+        else KK_LAUNCH((conv_i8_kernel<64, false>), grid, dim3(256), lds, st, A);
       }
       rc = check_launch("conv_i8_kernel");
     }
@@ -889,6 +951,38 @@ int kk_conv_integer_scaled_qbias_packed(const kk_tensor* out, const kk_tensor* x
   if (empty) return KK_OK;
   return conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
                           true, scale_a, scale_w, bias, nullptr, resid, packed);
+}
+
+int kk_conv_integer_scaled_qbias_packed_leaves(
+    const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* packed,
+    const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias, const kk_tensor* scale_a,
+    const kk_tensor* scale_w, const kk_tensor* resid, const kk_tensor* leaves, int stride,
+    int dilation, int pad0, int pad1, int group) {
+  const char* who = "kk_conv_integer_scaled_qbias_packed_leaves";
+  bool empty = false;
+  KK_TRY(check_qbias(out, x, w, x_zp, w_zp, bias, scale_a, scale_w, stride, dilation, pad0, pad1,
+                     group, who, &empty));
+  KK_TRY(check_packed(packed, w, who, w_zp, true));
+  if (resid) KK_TRY(check_resid(out, resid, who));
+  if (leaves) {
+    KK_TRY(check_tensor(leaves, "leaves"));
+    const int64_t rows = out->shape[0] * out->shape[1], Lout = out->shape[2];
+    const int64_t nleaf = (Lout / 8192) * 64;
+    if (nleaf == 0)
+      return set_error(KK_E_ARG, "%s: rows of %lld steps hold no whole 8192-block", who,
+                       (long long)Lout);
+    if (leaves->dtype != KK_F32 || !is_contiguous(leaves) || numel(leaves) != rows * nleaf)
+      return set_error(KK_E_ARG, "%s: leaves must be %lld contiguous fp32 values", who,
+                       (long long)(rows * nleaf));
+    if (conv_leaf_off(static_cast<int>(conv_rows(128, stride, dilation, w->shape[2]))) +
+            kLeafBytes > 65536)
+      return set_error(KK_E_UNSUPPORTED, "%s: the 128-step tile's window does not fit LDS", who);
+  }
+  if (empty) return KK_OK;
+  KK_TRY(conv_integer_run(out, x, w, x_zp, w_zp, nullptr, nullptr, stride, dilation, pad0, pad1,
+                          true, scale_a, scale_w, bias, nullptr, resid, packed, leaves));
+  if (leaves) leaf_record(leaves->data, out->data, out->shape[0] * out->shape[1], out->shape[2]);
+  return KK_OK;
 }
 
 int kk_conv_integer_scaled_qbias_noalloc(const kk_tensor* out, const kk_tensor* x,

@@ -88,6 +88,10 @@ void conv_i8_forget_pack(const void* p);
 // The same for a packed fp16 matrix-core convolution weight (kk_conv_f16.hip).
 void convh_forget_pack(const void* p);
 void gemm_forget_pack(const void* p);
+// Leaf sums a convolution formed of its [rows, T] fp32 output x, for the
+// InstanceNorm that reads x (kk_free forgets the record of either buffer).
+void leaf_record(const void* leaf, const void* x, int64_t rows, int64_t T);
+bool leaf_matches(const void* leaf, const void* x, int64_t rows, int64_t T);
 // Drops the record of what a packed MatMulInteger B at `p` was made from
 // (kk_free calls it).
 void i8_forget_pack(const void* p);

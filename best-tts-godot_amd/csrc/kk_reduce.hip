@@ -1307,7 +1307,7 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     float* __restrict__ part, const float* __restrict__ x, int64_t T, int nblk, int mode,
     float2* __restrict__ stats, int* __restrict__ cnt, int cstride, float* __restrict__ red_out,
     int red_mean, float eps, float2* __restrict__ xmm, float2* __restrict__ mm, int64_t C,
-    Affine af, NpTail tail) {
+    Affine af, NpTail tail, const float* __restrict__ leaves, int64_t nleaf) {
   __shared__ NpScratch S;
   const int64_t row = blockIdx.y;
   cnt += row * cstride;  // counters spaced apart: the rows' atomics do not share a line
@@ -1321,8 +1321,26 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     return d * d;
   };
   const float* xb = x + row * T + lo;
+  // xmm: the (min, max) of x of each block, formed in the second pass (the
+  // first may take its sums from leaves and not read x) and read by that
+  // pass's last block of the row: stored and loaded at the device-coherent
+  // level, as the partials are
+  const bool want_xmm = xmm && mode == 1;
   float s;
-  if (m == kNpBlock) {
+  if (m == kNpBlock && leaves && mode == 0) {
+    // the 64 leaf sums of this block, formed by the producer of x in the
+    // same order (kk_conv_integer_scaled_qbias_packed_leaves): the balanced
+    // tree of the full-block path below
+    if (threadIdx.x >= 64) return;
+    float r = leaves[row * nleaf + static_cast<int64_t>(b) * 64 + threadIdx.x];
+    r += __shfl_xor(r, 1, 64);
+    r += __shfl_xor(r, 2, 64);
+    r += __shfl_xor(r, 4, 64);
+    r += __shfl_xor(r, 8, 64);
+    r += __shfl_xor(r, 16, 64);
+    r += __shfl_xor(r, 32, 64);
+    s = r;
+  } else if (m == kNpBlock) {
     // A whole block straight from memory into the summation order: lane j
     // of leaf q (eight lanes per 128-element leaf) holds elements
     // q*128 + 8k + j, k = 0..15, its accumulator's terms in order.  (Staging
@@ -1341,7 +1359,7 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     r += __shfl_xor(r, 16, 64);
     r += __shfl_xor(r, 32, 64);
     if ((threadIdx.x & 63) == 0) S.wave[threadIdx.x >> 6] = r;
-    if (xmm) {
+    if (want_xmm) {
       float lo = v[0], hi = v[0];
 #pragma unroll
       for (int k = 1; k < kNpLeaf / 8; ++k) {
@@ -1408,7 +1426,7 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
         tv[leaf] = res;
       }
     }
-    if (xmm) np_wave_minmax(lo_x, hi_x, S);
+    if (want_xmm) np_wave_minmax(lo_x, hi_x, S);
     __syncthreads();
     if (threadIdx.x >= 64) return;
     for (int l = 0; l < tail.nlev; ++l) {  // wave 0: the tree, a level at a time
@@ -1419,13 +1437,15 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     }
     s = tv[tail.nnode ? tail.nleaf + tail.nnode - 1 : 0];
   }
-  if (xmm && threadIdx.x == 0) {
+  if (want_xmm && threadIdx.x == 0) {
     float lo = S.wmin[0], hi = S.wmax[0];
     for (int w = 1; w < kNpThreads / 64; ++w) {
       lo = fminf(lo, S.wmin[w]);
       hi = fmaxf(hi, S.wmax[w]);
     }
-    xmm[row * nblk + b] = make_float2(lo, hi);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(xmm) + row * nblk + b,
+                       __builtin_bit_cast(uint64_t, make_float2(lo, hi)), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
   }
   // wave 0: the partial goes to the device-coherent level (an agent-scope
   // store writes through this XCD's L2) and has landed before the count
@@ -1446,10 +1466,12 @@ __global__ void __launch_bounds__(kNpThreads) np_blocks_kernel(
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     const float acc = np_fold(part + row * nblk, nblk);
     const float n = static_cast<float>(T);
-    if (mode == 1 && mm) {  // the row's (xmin, xmax), written by the mode-0 launch
+    if (mode == 1 && mm) {  // the row's (xmin, xmax), from its blocks' xmm
       float lo = INFINITY, hi = -INFINITY;
       for (int i = threadIdx.x; i < nblk; i += 64) {
-        const float2 p = xmm[row * nblk + i];
+        const float2 p = __builtin_bit_cast(
+            float2, __hip_atomic_load(reinterpret_cast<const uint64_t*>(xmm) + row * nblk + i,
+                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
         lo = fminf(lo, p.x);
         hi = fmaxf(hi, p.y);
       }
@@ -2040,7 +2062,8 @@ static int np_reduce_rows(float* out, const float* x, int64_t rows, int64_t n, b
                      dim3(kNpThreads), 0, st, static_cast<float*>(part), x, n,
                      static_cast<int>(nblk), 0, static_cast<float2*>(nullptr), ctx().row_counters,
                      counter_stride(rows), out, mean ? 1 : 0, 0.0f, static_cast<float2*>(nullptr),
-                     static_cast<float2*>(nullptr), int64_t{0}, Affine{}, tail);
+                     static_cast<float2*>(nullptr), int64_t{0}, Affine{}, tail,
+                     static_cast<const float*>(nullptr), int64_t{0});
   const int rc = check_launch("np_blocks_kernel");
   kk_free(part);  // stream order keeps it alive for the kernel
   return rc;
@@ -2135,7 +2158,7 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
                        static_cast<int>(nblk), pass, stats, ctx().row_counters,
                        counter_stride(rows), static_cast<float*>(nullptr), 0, eps,
                        static_cast<float2*>(nullptr), static_cast<float2*>(nullptr), int64_t{0},
-                       Affine{}, tail);
+                       Affine{}, tail, static_cast<const float*>(nullptr), int64_t{0});
     rc = check_launch("np_blocks_kernel");
   }
   if (rc == KK_OK) {
@@ -2175,7 +2198,8 @@ static int next_epoch() {
 }
 
 static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, const kk_tensor* y_zp,
-                              const kk_tensor* x, float eps, const Affine& af) {
+                              const kk_tensor* x, float eps, const Affine& af,
+                              const float* leaves = nullptr) {
   hipStream_t st = ctx().stream;
   const int64_t T = x->shape[x->rank - 1];
   const int64_t C = x->shape[x->rank - 2];
@@ -2244,7 +2268,8 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
       KK_LAUNCH(np_blocks_kernel, bgrid, dim3(kNpThreads), 0, st, part, xp, T,
                          static_cast<int>(nblk), pass, stats, ctx().row_counters,
                          counter_stride(rows), static_cast<float*>(nullptr), 0, eps, xmm,
-                         pass == 1 ? mm : static_cast<float2*>(nullptr), C, af, tail);
+                         pass == 1 ? mm : static_cast<float2*>(nullptr), C, af, tail, leaves,
+                         (T / kNpBlock) * 64);
       rc = check_launch("np_blocks_kernel");
     }
   }
@@ -2336,7 +2361,8 @@ static int instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
                                      const kk_tensor* scale, const kk_tensor* shift,
                                      const kk_tensor* snake_a, const kk_tensor* snake_r, float eps,
                                      int leaky, float alpha, const kk_tensor* y_scale = nullptr,
-                                     const kk_tensor* y_zp = nullptr) {
+                                     const kk_tensor* y_zp = nullptr,
+                                     const kk_tensor* leaves = nullptr) {
   KK_TRY(require_ready());
   KK_TRY(check_f32_contig(x, "x"));
   KK_TRY(check_tensor(out, "out"));
@@ -2382,7 +2408,14 @@ static int instance_norm_scale_shift(const kk_tensor* out, const kk_tensor* x,
   }
   if (y_scale) {
     if (numel(x) == 0) return set_error(KK_E_ARG, "instance norm quant: empty input");
-    return instnorm_quant_run(out, y_scale, y_zp, x, eps, af);
+    const float* lv = nullptr;
+    if (leaves) {
+      const int64_t T = x->shape[x->rank - 1], rows = numel(x) / T;
+      if (!leaf_matches(leaves->data, x->data, rows, T))
+        return set_error(KK_E_ARG, "kk_instance_norm_quant_leaves: leaves were not formed from x");
+      lv = static_cast<const float*>(leaves->data);
+    }
+    return instnorm_quant_run(out, y_scale, y_zp, x, eps, af, lv);
   }
   StyleArgs sa{};
   return instnorm_launch(out, x, eps, af, sa);
@@ -2432,6 +2465,21 @@ int kk_instance_norm_quant(const kk_tensor* y, const kk_tensor* y_scale, const k
   if (!y_scale || !y_zp) return set_error(KK_E_ARG, "kk_instance_norm_quant: scale/zero point outputs");
   return instance_norm_scale_shift(y, x, scale, shift, alpha, recip, eps, leaky, leaky_alpha,
                                    y_scale, y_zp);
+}
+
+int kk_instance_norm_quant_leaves(const kk_tensor* y, const kk_tensor* y_scale,
+                                  const kk_tensor* y_zp, const kk_tensor* x,
+                                  const kk_tensor* scale, const kk_tensor* shift,
+                                  const kk_tensor* alpha, const kk_tensor* recip, float eps,
+                                  int leaky, float leaky_alpha, const kk_tensor* leaves) {
+  if ((alpha == nullptr) != (recip == nullptr))
+    return set_error(KK_E_ARG, "kk_instance_norm_quant_leaves: snake needs both alpha and recip");
+  if (alpha && leaky)
+    return set_error(KK_E_UNSUPPORTED, "kk_instance_norm_quant_leaves: LeakyRelu and snake together");
+  if (!y_scale || !y_zp)
+    return set_error(KK_E_ARG, "kk_instance_norm_quant_leaves: scale/zero point outputs");
+  return instance_norm_scale_shift(y, x, scale, shift, alpha, recip, eps, leaky, leaky_alpha,
+                                   y_scale, y_zp, leaves);
 }
 
 int kk_instance_norm_scale_shift_snake(const kk_tensor* out, const kk_tensor* x,

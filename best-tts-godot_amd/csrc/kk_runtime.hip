@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstring>
+#include <iterator>
 #include <mutex>
 #include <unordered_map>
 #include <unordered_set>
@@ -235,6 +236,52 @@ static void pool_release_all() {
   p.live_bytes = p.pooled_bytes = 0;
 }
 
+// ------------------------------------------------------------ leaf sums
+// Which tensor a convolution's leaf sums were formed from (an InstanceNorm
+// takes them only for that tensor); forgotten when either buffer is freed.
+struct LeafRec {
+  const void* x;
+  int64_t rows, T;
+};
+static std::mutex g_leaf_mu;
+static std::unordered_map<const void*, LeafRec>& leaf_recs() {
+  static auto* m = new std::unordered_map<const void*, LeafRec>();
+  return *m;
+}
+
+void leaf_record(const void* leaf, const void* x, int64_t rows, int64_t T) {
+  std::lock_guard<std::mutex> lk(g_leaf_mu);
+  leaf_recs()[leaf] = LeafRec{x, rows, T};
+}
+
+bool leaf_matches(const void* leaf, const void* x, int64_t rows, int64_t T) {
+  std::lock_guard<std::mutex> lk(g_leaf_mu);
+  auto it = leaf_recs().find(leaf);
+  return it != leaf_recs().end() && it->second.x == x && it->second.rows == rows &&
+         it->second.T == T;
+}
+
+static void leaf_forget(const void* p) {
+  std::lock_guard<std::mutex> lk(g_leaf_mu);
+  auto& m = leaf_recs();
+  if (m.empty()) return;
+  m.erase(p);
+  for (auto it = m.begin(); it != m.end();)
+    it = it->second.x == p ? m.erase(it) : std::next(it);
+}
+
+// Every record whose leaf buffer or x lies in [base, base + bytes).
+static void leaf_forget_range(const char* base, size_t bytes) {
+  std::lock_guard<std::mutex> lk(g_leaf_mu);
+  auto& m = leaf_recs();
+  auto in = [base, bytes](const void* q) {
+    const char* c = static_cast<const char*>(q);
+    return c >= base && c < base + bytes;
+  };
+  for (auto it = m.begin(); it != m.end();)
+    it = in(it->first) || in(it->second.x) ? m.erase(it) : std::next(it);
+}
+
 // ---------------------------------------------------------- graph arenas
 // Device memory owned by a graph recorded with kk_graph_begin_arena.  While
 // it is recorded, kk_alloc hands out the arena's blocks (the pool's buckets,
@@ -297,7 +344,10 @@ static void arena_release(Arena* a) {
       p.live_bytes -= it->second;
     }
   }
-  if (a->base) (void)hipFree(a->base);
+  if (a->base) {
+    leaf_forget_range(a->base, a->bytes);
+    (void)hipFree(a->base);
+  }
   delete a;
 }
 
@@ -558,6 +608,7 @@ int kk_alloc(size_t bytes, void** dptr) {
 int kk_free(void* dptr) {
   if (!dptr) return KK_OK;
   KK_TRY(require_ready());
+  leaf_forget(dptr);
   if (Arena* a = arena_of(dptr)) {
     if (a != g_rec_arena) return KK_OK;  // a recorded graph's: released with it
     auto sz = a->size_of.find(dptr);

@@ -37,6 +37,11 @@ _HOST_MOVE_OPS = {
     "Shape", "Reshape", "Unsqueeze", "Squeeze", "Concat", "Slice", "Gather",
     "Cast", "Transpose", "Expand", "Split",
 }
+# The shortest conv output whose InstanceNorm takes the block-wise
+# statistics (rows of nine 8192-blocks or more; shorter rows are held on
+# chip, read once): only there do leaf sums save a pass.
+_LEAF_MIN_STEPS = 9 * 8192
+
 _HOST_INT_OPS = {
     "Equal", "Where", "Greater", "Less", "GreaterOrEqual", "And", "Add", "Sub", "Mul",
     "Div", "CumSum",
@@ -389,14 +394,23 @@ def dispatch(op, node_input, node_output, at, env):
         # scale_a * scale_w, int32 bias = Cast(Floor(Div(bias, scale))).
         x, y = to_device(x), to_device(y)
         resid = _qconv_resid(at, inp, x, y)
+        packed = env.get(at.get("packed"))
+        # a second output: the leaf sums of the result for the InstanceNorm
+        # that reads it, where its rows take the block-wise statistics
+        # (at least nine 8192-blocks; none otherwise)
+        pads, st, dil = at.get("pads", [0, 0]), at.get("strides", [1])[0], at.get("dilations", [1])[0]
+        lout = (x.shape[2] + pads[0] + pads[1] - dil * (y.shape[2] - 1) - 1) // st + 1
+        leafy = (len(node_output) > 1 and node_output[1] and packed is not None and
+                 ("resid" not in at or resid is not None) and lout >= _LEAF_MIN_STEPS)
         out = ops.conv_integer_scaled_qbias(x, y, to_device(inp(2)),
                                             to_device(inp(3)), _f32(to_device(inp(8))),
                                             _f32(to_device(inp(6))), _f32(to_device(inp(7))),
-                                            at.get("pads", [0, 0]),
-                                            at.get("strides", [1])[0],
-                                            at.get("dilations", [1])[0],
-                                            at.get("group", 1), resid=resid,
-                                            packed=env.get(at.get("packed")))
+                                            pads, st, dil, at.get("group", 1), resid=resid,
+                                            packed=packed, leaves=leafy)
+        if leafy:
+            out, env[node_output[1]] = out
+        elif len(node_output) > 1 and node_output[1]:
+            env[node_output[1]] = None
         if "resid" in at and resid is None:  # the Add it took in, after it
             out = ops.binary("Add", out, to_device(inp(at["resid"])))
     elif op == "QConvScaled":
@@ -470,7 +484,10 @@ def dispatch(op, node_input, node_output, at, env):
         a = _f32(to_device(a)) if a is not None else None
         rc = _f32(to_device(rc)) if rc is not None else None
         if all(_per_channel(t, xd) for t in (sc, sh, a, rc)):
-            res = ops.instance_norm_quant(xd, sc, sh, a, rc, at["epsilon"], at.get("leaky_alpha"))
+            # input 5: x's leaf sums from the conv that produced it, or None
+            res = ops.instance_norm_quant(xd, sc, sh, a, rc, at["epsilon"], at.get("leaky_alpha"),
+                                          leaves=env.get(node_input[5]) if len(node_input) > 5
+                                          and node_input[5] and xd is x else None)
         else:  # an operand not per channel: the chains one after the other
             yv = _norm_chain(xd, sc, sh, at["epsilon"], None if a is not None else
                              at.get("leaky_alpha"))

@@ -97,7 +97,32 @@ def fuse(nodes, weights, protect=()):
     out, groups = _merge_norm_snake(out, groups, protect)
     out, groups = _merge_norm_quant(out, groups, protect)
     out, groups = _merge_qconv_bias(out, groups, weights, protect)
-    return _merge_qconv_add(out, groups, protect)
+    out, groups = _merge_qconv_add(out, groups, protect)
+    return _link_conv_leaves(out), groups
+
+
+def _link_conv_leaves(out):
+    """An InstanceNormQuant whose x a quantised conv (with its bias
+    quantisation folded in) produces takes that conv's leaf sums of x: the
+    conv node gains a second output "<x>#leaves", the norm node a sixth
+    input of that name (the dispatch forms the sums only for packed weights
+    and rows long enough for the block-wise statistics, and the norm reads
+    x again where there are none)."""
+    producer = {}
+    for k, (op, _ins, outs, at) in enumerate(out):
+        if op == "QConvScaled" and at.get("bias_quant") and outs and outs[0]:
+            producer[outs[0]] = k
+    linked = list(out)
+    for k, (op, ins, outs, at) in enumerate(out):
+        if op != "InstanceNormQuant" or ins[0] not in producer:
+            continue
+        c = producer[ins[0]]
+        name = f"{ins[0]}#leaves"
+        c_op, c_ins, c_outs, c_at = linked[c]
+        if len(c_outs) < 2:
+            linked[c] = (c_op, c_ins, [c_outs[0], name], c_at)
+        linked[k] = (op, list(ins[:5]) + [""] * (5 - len(ins[:5])) + [name], outs, at)
+    return linked
 
 
 def _merge_qconv_add(out, groups, protect):

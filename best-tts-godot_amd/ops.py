@@ -366,7 +366,8 @@ def conv_integer_pack(w, w_zp=None):
 
 
 def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0, 0), stride=1,
-                              dilation=1, group=1, noalloc=False, resid=None, packed=None):
+                              dilation=1, group=1, noalloc=False, resid=None, packed=None,
+                              leaves=False):
     """conv_integer_scaled with its int32 bias and scale formed in the same
     launch sequence: scale = scale_a * scale_w, bias_int32 =
     int32(floor(bias / scale)) (bias fp32 [Cout], the scales one value each).
@@ -374,7 +375,9 @@ def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0,
     is a fixed device array); the output is still allocated here.  With
     `resid` (fp32, the output's shape) that is added too: the residual Add
     fused (not with `noalloc`).  With `packed` (conv_integer_pack of this w
-    and w_zp) the weights are not re-laid for the call."""
+    and w_zp) the weights are not re-laid for the call; with `leaves` too
+    (and an output of at least 8192 steps) the result is (out, leaf sums of
+    out for instance_norm_quant(leaves=...))."""
     x = x.contiguous()
     w = w.contiguous()
     n, _, L = x.shape
@@ -388,8 +391,12 @@ def conv_integer_scaled_qbias(x, w, x_zp, w_zp, bias, scale_a, scale_w, pads=(0,
         if noalloc:
             raise ValueError("conv_integer_scaled_qbias: packed with noalloc is not supported")
         args.insert(3, packed.desc())
-        _lib.call("kk_conv_integer_scaled_qbias_packed", *args,
-                  None if resid is None else resid.contiguous().desc(), *tail)
+        rd = None if resid is None else resid.contiguous().desc()
+        if leaves:
+            lv = DeviceTensor.empty((n * cout, (lout // 8192) * 64), np.float32)
+            _lib.call("kk_conv_integer_scaled_qbias_packed_leaves", *args, rd, lv.desc(), *tail)
+            return out, lv
+        _lib.call("kk_conv_integer_scaled_qbias_packed", *args, rd, *tail)
     elif resid is not None:
         if noalloc:
             raise ValueError("conv_integer_scaled_qbias: resid with noalloc is not supported")
@@ -425,20 +432,25 @@ def instance_norm_scale_shift_snake(x, scale, shift, alpha, recip, eps=1e-5):
 
 
 def instance_norm_quant(x, scale=None, shift=None, alpha=None, recip=None, eps=1e-5,
-                        leaky_alpha=None):
+                        leaky_alpha=None, leaves=None):
     """The instance norm chain (affine, then LeakyRelu or snake) and the
     DynamicQuantizeLinear of its result: (y uint8, scale fp32 [], zero point
-    uint8 []), the float result never stored."""
+    uint8 []), the float result never stored.  `leaves`: x's leaf sums from
+    the convolution that produced it (conv_integer_scaled_qbias(leaves=True))."""
     x = x.contiguous()
     y = DeviceTensor.empty(x.shape, np.uint8)
     ys = DeviceTensor.empty((), np.float32)
     yz = DeviceTensor.empty((), np.uint8)
-    _lib.call("kk_instance_norm_quant", y.desc(), ys.desc(), yz.desc(), x.desc(),
-              _d(scale.contiguous() if scale is not None else None),
-              _d(shift.contiguous() if shift is not None else None),
-              _d(alpha.contiguous() if alpha is not None else None),
-              _d(recip.contiguous() if recip is not None else None), float(eps),
-              0 if leaky_alpha is None else 1, 0.0 if leaky_alpha is None else float(leaky_alpha))
+    args = [y.desc(), ys.desc(), yz.desc(), x.desc(),
+            _d(scale.contiguous() if scale is not None else None),
+            _d(shift.contiguous() if shift is not None else None),
+            _d(alpha.contiguous() if alpha is not None else None),
+            _d(recip.contiguous() if recip is not None else None), float(eps),
+            0 if leaky_alpha is None else 1, 0.0 if leaky_alpha is None else float(leaky_alpha)]
+    if leaves is None:
+        _lib.call("kk_instance_norm_quant", *args)
+    else:
+        _lib.call("kk_instance_norm_quant_leaves", *args, leaves.desc())
     return y, ys, yz
 
 

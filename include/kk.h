@@ -187,6 +187,16 @@ int kk_instance_norm_quant(const kk_tensor* y, const kk_tensor* y_scale,
                            const kk_tensor* scale, const kk_tensor* shift,
                            const kk_tensor* alpha, const kk_tensor* recip, float eps,
                            int leaky, float leaky_alpha);
+/* kk_instance_norm_quant with x's leaf sums from the convolution that
+ * produced it (kk_conv_integer_scaled_qbias_packed_leaves; KK_E_ARG if they
+ * were formed from another tensor): rows long enough for the block-wise
+ * statistics take their means from the leaves instead of a pass over x
+ * (the same bits: the same sums in the same order). */
+int kk_instance_norm_quant_leaves(const kk_tensor* y, const kk_tensor* y_scale,
+                                  const kk_tensor* y_zero_point, const kk_tensor* x,
+                                  const kk_tensor* scale, const kk_tensor* shift,
+                                  const kk_tensor* alpha, const kk_tensor* recip, float eps,
+                                  int leaky, float leaky_alpha, const kk_tensor* leaves);
 /* AdaIN with the style Linear fused: h = style . W + b with W [S, 2C]
  * (any strides), then kk_instance_norm_affine on x [N,C,T].  bias may be
  * NULL.  W may be f32, f16 or int8/uint8 with w_scale/w_zp (per tensor or
@@ -392,6 +402,18 @@ int kk_conv_integer_scaled_qbias_packed(const kk_tensor* out, const kk_tensor* x
                                         const kk_tensor* bias, const kk_tensor* scale_a,
                                         const kk_tensor* scale_w, const kk_tensor* resid,
                                         int stride, int dilation, int pad0, int pad1, int group);
+/* kk_conv_integer_scaled_qbias_packed that also forms, for the InstanceNorm
+ * that reads its output, the output's numpy-order leaf sums (no counterpart
+ * in the reference, whose InstanceNorm chain re-reads the conv output:
+ * ref_runtime.py:446-459 ReduceMean): leaves fp32 contiguous [N * Cout,
+ * (Lout / 8192) * 64], leaf t of a row = np.add.reduce of its elements
+ * 128 t .. 128 t + 127 (8 accumulators of 16 terms in order, then their
+ * balanced tree), for the rows' whole 8192-blocks.  Lout >= 8192. */
+int kk_conv_integer_scaled_qbias_packed_leaves(
+    const kk_tensor* out, const kk_tensor* x, const kk_tensor* w, const kk_tensor* packed,
+    const kk_tensor* x_zp, const kk_tensor* w_zp, const kk_tensor* bias, const kk_tensor* scale_a,
+    const kk_tensor* scale_w, const kk_tensor* resid, const kk_tensor* leaves, int stride,
+    int dilation, int pad0, int pad1, int group);
 
 /* kk_conv_integer_scaled_qbias without any allocation.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code

@@ -215,13 +215,16 @@ def test_every_node_teacher_forced(gpu, oracle, n_ids, speed):
             for n in gins:
                 if not n or n in genv:
                     continue
+                if n.endswith("#leaves"):  # a conv's leaf sums: none at these lengths
+                    genv[n] = None
+                    continue
                 if n in pg.weights:
                     genv[n] = pg.weights[n]
                 else:
                     genv[n] = gpu.to_device(np.asarray(oenv[n])) if on_device[n] else oenv[n]
             gpu.dispatch(gop, gins, gouts, gat, genv)
             for o in gouts:
-                if not o:
+                if not o or o.endswith("#leaves"):
                     continue
                 on_device[o] = isinstance(genv[o], gpu.DeviceTensor)
                 msg = _node_close(gpu.to_host(genv[o]), oenv[o],
@@ -232,7 +235,7 @@ def test_every_node_teacher_forced(gpu, oracle, n_ids, speed):
         for n in ins:
             if n and last.get(n) == i and n not in pg.weights:
                 oenv.pop(n, None)
-    assert counted == sum(1 for n in pg.nodes for o in n[2] if o)
+    assert counted == sum(1 for n in pg.nodes for o in n[2] if o and not o.endswith("#leaves"))
     if n_ids == 8:
         assert longest > 16384, longest  # the long-row paths ran
     assert not failures, f"{len(failures)} node outputs differ:\n" + "\n".join(failures[:20])

@@ -653,6 +653,80 @@ def test_conv_packed_weights(gpu, cin, cout, k, L, pad, dil, stride, wdt, wzp, r
         assert_bitexact(got, want, f"packed conv {cin}->{cout} k{k} call {call}")
 
 
+@pytest.mark.parametrize("cin,cout,k,L,pad,dil,resid", [
+    (64, 64, 3, 20000, 1, 1, False),      # two whole 8192-blocks and a tail
+    (128, 130, 7, 17000, 9, 3, True),     # a second, partial channel block; the residual
+    (96, 128, 11, 16400, 25, 5, False)])
+def test_conv_leaf_sums(gpu, cin, cout, k, L, pad, dil, resid):
+    """kk_conv_integer_scaled_qbias_packed_leaves: the output bit-identical to
+    the packed conv's, and leaf t of each row -- the sum of its elements
+    128 t .. 128 t + 127 -- equal to numpy's np.add.reduce of that slice
+    (eight accumulators of sixteen terms, then their tree) for every leaf of
+    the rows' whole 8192-blocks."""
+    r = rng(45)
+    w = gpu.to_device(r.integers(0, 256, (cout, cin, k)).astype(np.uint8))
+    wz = gpu.to_device(np.array(128, np.uint8))
+    bias = gpu.to_device(r.normal(0, 0.5, (cout,)).astype(np.float32))
+    sw = gpu.to_device(np.array(0.0037, np.float32))
+    sa = gpu.to_device(np.array(0.0051, np.float32))
+    packed = gpu.ops.conv_integer_pack(w, wz)
+    x = gpu.to_device(r.integers(0, 256, (1, cin, L)).astype(np.uint8))
+    xz = gpu.to_device(np.array(117, np.uint8))
+    lout = L + 2 * pad - dil * (k - 1)
+    res = gpu.to_device(r.normal(0, 1, (1, cout, lout)).astype(np.float32)) if resid else None
+    kw = dict(pads=(pad, pad), dilation=dil, resid=res, packed=packed)
+    want = gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, **kw).numpy()
+    out, leaves = gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, leaves=True, **kw)
+    got = out.numpy()
+    assert_bitexact(got, want, f"conv with leaf sums {cin}->{cout} k{k}")
+    lv = leaves.numpy()
+    nleaf = (lout // 8192) * 64
+    assert lv.shape == (cout, nleaf)
+    ref = np.add.reduce(got[0, :, :nleaf * 128].reshape(cout, nleaf, 128), axis=2)
+    # (np.add.reduce over the last axis of a [.., 128] view sums each row of
+    # 128 contiguous values with numpy's pairwise loop, as the oracle's
+    # ReduceMean does)
+    for t in (0, 1, nleaf - 1):
+        assert_bitexact(np.float32(np.add.reduce(got[0, 0, 128 * t:128 * t + 128])), ref[0, t],
+                        "numpy leaf order")
+    assert_bitexact(lv, ref.astype(np.float32), f"leaf sums {cin}->{cout} k{k}")
+
+
+@pytest.mark.parametrize("kind", ["leaky", "snake", "affine"])
+def test_instance_norm_quant_with_leaf_sums(gpu, kind):
+    """kk_instance_norm_quant_leaves on a conv's output with that conv's leaf
+    sums: the same bytes, scale and zero point as without them, on rows
+    long enough for the block-wise statistics (100,000 steps: twelve whole
+    8192-blocks and a tail).  Leaf sums formed from another tensor are
+    refused."""
+    r = rng(46)
+    cin, cout, L = 32, 48, 100000
+    w = gpu.to_device(r.integers(0, 256, (cout, cin, 3)).astype(np.uint8))
+    wz = gpu.to_device(np.array(128, np.uint8))
+    bias = gpu.to_device(r.normal(0, 0.5, (cout,)).astype(np.float32))
+    sw = gpu.to_device(np.array(0.004, np.float32))
+    sa = gpu.to_device(np.array(0.006, np.float32))
+    packed = gpu.ops.conv_integer_pack(w, wz)
+    x = gpu.to_device(r.integers(0, 256, (1, cin, L)).astype(np.uint8))
+    xz = gpu.to_device(np.array(100, np.uint8))
+    y, leaves = gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, pads=(1, 1),
+                                                  packed=packed, leaves=True)
+    D = gpu.to_device
+    g = D((1 + 0.1 * r.normal(0, 1, (1, cout, 1))).astype(np.float32))
+    b = D((0.1 * r.normal(0, 1, (1, cout, 1))).astype(np.float32))
+    a = D(r.uniform(0.5, 2, (1, cout, 1)).astype(np.float32))
+    rc = D((1.0 / r.uniform(0.5, 2, (1, cout, 1))).astype(np.float32))
+    args = {"leaky": dict(leaky_alpha=0.2), "snake": dict(alpha=a, recip=rc),
+            "affine": {}}[kind]
+    want = gpu.ops.instance_norm_quant(y, g, b, eps=1e-5, **args)
+    got = gpu.ops.instance_norm_quant(y, g, b, eps=1e-5, leaves=leaves, **args)
+    for gt, wt, what in zip(got, want, ("bytes", "scale", "zero point")):
+        assert_bitexact(gpu.to_host(gt), gpu.to_host(wt), f"{kind} {what}")
+    other = y.astype(np.float32)  # same values, another buffer
+    with pytest.raises(gpu._lib.KKError, match="not formed from x"):
+        gpu.ops.instance_norm_quant(other, g, b, eps=1e-5, leaves=leaves, **args)
+
+
 def test_conv_packed_refuses_another_weight(gpu):
     """A packed buffer is used only with the weight and zero-point tensors it
     was packed from: another weight of the same shape, or another zero point,
