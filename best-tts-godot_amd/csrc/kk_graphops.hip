@@ -22,16 +22,17 @@ constexpr int kDqlBlocks = 256;  // stage-1 blocks at most (one partial a thread
 // exactly as the reference does; params = (scale, zero point) as floats.
 constexpr int kDqlFoldThreads = 1024;
 
-// only_if: the launch does nothing unless *only_if is set.  clear: also
-// keeps the folded (min, max) in params[1] and zeroes *clear, the flag a
-// later pass sets when one of its values falls outside that range.
+// only_if: the launch does nothing unless *only_if == epoch (the value a
+// pass of the same call stores there).  clear: also keeps the folded (min,
+// max) in params[1] and zeroes *clear, the flag a later pass sets (to
+// epoch) when one of its values falls outside that range.
 __global__ void __launch_bounds__(kDqlFoldThreads) dql_fold(const float2* __restrict__ part,
                                                             int npart, float2* __restrict__ params,
                                                             float* __restrict__ scale_out,
                                                             uint8_t* __restrict__ zp_out,
                                                             const int* __restrict__ only_if,
-                                                            int* __restrict__ clear) {
-  if (only_if && *only_if == 0) return;
+                                                            int* __restrict__ clear, int epoch) {
+  if (only_if && *only_if != epoch) return;
   __shared__ float smin[kDqlFoldThreads / 64], smax[kDqlFoldThreads / 64];
   float lo = INFINITY, hi = -INFINITY;
   for (int i = threadIdx.x; i < npart; i += blockDim.x) {
@@ -163,9 +164,9 @@ __global__ void __launch_bounds__(256) dql_quantize_fold(const float* __restrict
 }
 
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
-                    uint8_t* zp_out, const int* only_if, int* clear) {
+                    uint8_t* zp_out, const int* only_if, int* clear, int epoch) {
   KK_LAUNCH(dql_fold, dim3(1), dim3(kDqlFoldThreads), 0, ctx().stream, part, npart, params,
-                     scale_out, zp_out, only_if, clear);
+                     scale_out, zp_out, only_if, clear, epoch);
   return check_launch("dql_fold");
 }
 

@@ -67,10 +67,11 @@ __device__ inline float2 dql_params(float fmn, float fmx, float* scale_out, uint
 
 // Folds npart (min, max) partials and derives DynamicQuantizeLinear's scale
 // and zero point: params[0] = (scale, zp) as floats, *scale_out, *zp_out.
-// With only_if, the launch does nothing unless *only_if is set; with clear,
-// params[1] = the folded (min, max) and *clear = 0.
+// With only_if, the launch does nothing unless *only_if == epoch; with
+// clear, params[1] = the folded (min, max) and *clear = 0.
 int launch_dql_fold(const float2* part, int npart, float2* params, float* scale_out,
-                    uint8_t* zp_out, const int* only_if = nullptr, int* clear = nullptr);
+                    uint8_t* zp_out, const int* only_if = nullptr, int* clear = nullptr,
+                    int epoch = 0);
 Context& ctx();
 // Every kernel launch of the library goes through KK_LAUNCH, which counts it
 // (kk_dispatch_count) unless a graph is being recorded.

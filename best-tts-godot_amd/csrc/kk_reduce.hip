@@ -554,64 +554,6 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_apply(float* __restrict__ 
   }
 }
 
-// The normalised results y = affine((x - mean) / den) of long rows, not
-// stored: block (bx, row) writes the (min, max) of its share to
-// mm[row * gridDim.x + bx] (the first half of DynamicQuantizeLinear).
-// only_if: the launch does nothing unless *only_if == epoch.
-__global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict__ mm,
-                                                             const float* __restrict__ x,
-                                                             const float2* __restrict__ stats,
-                                                             int64_t C, int64_t T, Affine af,
-                                                             int vec,
-                                                             const int* __restrict__ only_if,
-                                                             int epoch) {
-  if (only_if && *only_if != epoch) return;
-  __shared__ float2 wmm[kRowBlock / 64];
-  const int64_t row = blockIdx.y;
-  const int64_t c = row % C;
-  const RowAffine ra = row_affine(af, C, c, 0.0f, 0.0f);
-  const float2 st = stats[row];
-  const KkDivisor dden = kk_divisor(st.y);
-  const float* xr = x + row * T;
-  float lo = INFINITY, hi = -INFINITY;
-  auto take_y = [&](float y) {
-    lo = fminf(lo, y);
-    hi = fmaxf(hi, y);
-  };
-  auto take = [&](float v) { take_y(apply_affine(kk_div(v - st.x, dden), ra, af)); };
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  if (vec) {
-    const RowSplit rsp = row_split(row, T);
-    for (int64_t k = i0; k < rsp.nv; k += stride) {
-      const float4 v = *reinterpret_cast<const float4*>(xr + rsp.hh + 4 * k);  // read again next
-      const float4 q = kk_div4(make_float4(v.x - st.x, v.y - st.x, v.z - st.x, v.w - st.x), dden);
-      take_y(apply_affine(q.x, ra, af));
-      take_y(apply_affine(q.y, ra, af));
-      take_y(apply_affine(q.z, ra, af));
-      take_y(apply_affine(q.w, ra, af));
-    }
-    int64_t i;
-    if (rsp.edge(i)) take(xr[i]);
-  } else {
-    for (int64_t i = i0; i < T; i += stride) take(xr[i]);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    lo = fminf(lo, __shfl_xor(lo, off, 64));
-    hi = fmaxf(hi, __shfl_xor(hi, off, 64));
-  }
-  if ((threadIdx.x & 63) == 0) wmm[threadIdx.x >> 6] = make_float2(lo, hi);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int w = 1; w < kRowBlock / 64; ++w) {
-      lo = fminf(lo, wmm[w].x);
-      hi = fmaxf(hi, wmm[w].y);
-    }
-    mm[row * gridDim.x + blockIdx.x] = make_float2(lo, hi);
-  }
-}
-
 // y recomputed exactly as above, then DynamicQuantizeLinear's byte: the
 // float y never reaches memory.  The scale and zero point come from the
 // npart (min, max) partials in mm, which every block folds (min and max do
@@ -620,7 +562,9 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_minmax(float2* __restrict_
 // launch, for more partials than a block folds).  only_if: the launch does
 // nothing unless *only_if == epoch.  check: a y outside the folded (min,
 // max) (params[1] with mm NULL) sets *check = epoch -- a value no earlier
-// call leaves there, so nothing has to clear it first.
+// call leaves there, so nothing has to clear it first.  bmm: every block
+// also stores the exact (min, max) of its y in bmm[row * gridDim.x +
+// blockIdx.x], the partials a flagged call folds before quantising again.
 __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict__ q,
                                                             const float* __restrict__ x,
                                                             const float2* __restrict__ stats,
@@ -630,7 +574,8 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
                                                             uint8_t* __restrict__ yzp,
                                                             int64_t C, int64_t T, Affine af,
                                                             int vec, const int* __restrict__ only_if,
-                                                            int* __restrict__ check, int epoch) {
+                                                            int* __restrict__ check, int epoch,
+                                                            float2* __restrict__ bmm) {
   if (only_if && *only_if != epoch) return;
   __shared__ float2 wmm[kRowBlock / 64];
   __shared__ float4 pl;  // scale, zero point, and the (min, max) of y
@@ -679,7 +624,7 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
   uint8_t* qr = q + row * T;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
   const int64_t i0 = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  bool out = false;
+  float lo = INFINITY, hi = -INFINITY;  // this thread's (min, max) of y
   if (vec) {
     const RowSplit rsp = row_split(row, T);
     for (int64_t k = i0; k < rsp.nv; k += stride) {
@@ -690,7 +635,8 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
       const float y1 = apply_affine(q.y, ra, af);
       const float y2 = apply_affine(q.z, ra, af);
       const float y3 = apply_affine(q.w, ra, af);
-      out |= fminf(fminf(y0, y1), fminf(y2, y3)) < lim.x || fmaxf(fmaxf(y0, y1), fmaxf(y2, y3)) > lim.y;
+      lo = fminf(lo, fminf(fminf(y0, y1), fminf(y2, y3)));
+      hi = fmaxf(hi, fmaxf(fmaxf(y0, y1), fmaxf(y2, y3)));
       const uint32_t w = dql_bytes4(make_float4(y0, y1, y2, y3), dsc, pz.y);
       // an ordinary store: the convolution that reads the bytes next finds
       // them in the last-level cache
@@ -699,17 +645,35 @@ __global__ void __launch_bounds__(kRowBlock) instnorm_quant(uint8_t* __restrict_
     int64_t i;
     if (rsp.edge(i)) {
       const float y = apply_affine((xr[i] - st.x) / st.y, ra, af);
-      out |= y < lim.x || y > lim.y;
+      lo = fminf(lo, y);
+      hi = fmaxf(hi, y);
       qr[i] = static_cast<uint8_t>(dql_byte(y, pz.x, pz.y));
     }
   } else {
     for (int64_t i = i0; i < T; i += stride) {
       const float y = apply_affine((xr[i] - st.x) / st.y, ra, af);
-      out |= y < lim.x || y > lim.y;
+      lo = fminf(lo, y);
+      hi = fmaxf(hi, y);
       qr[i] = static_cast<uint8_t>(dql_byte(y, pz.x, pz.y));
     }
   }
-  if (check && out) *check = epoch;  // every writer stores the same value
+  if (check && (lo < lim.x || hi > lim.y)) *check = epoch;  // every writer stores the same value
+  if (bmm) {  // (uniform: every thread of the block takes the barrier)
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lo = fminf(lo, __shfl_xor(lo, off, 64));
+      hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+    }
+    if ((threadIdx.x & 63) == 0) wmm[threadIdx.x >> 6] = make_float2(lo, hi);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      for (int w = 1; w < kRowBlock / 64; ++w) {
+        lo = fminf(lo, wmm[w].x);
+        hi = fmaxf(hi, wmm[w].y);
+      }
+      bmm[row * gridDim.x + blockIdx.x] = make_float2(lo, hi);
+    }
+  }
 }
 
 // -------------------------------------------------------------- LayerNorm
@@ -2186,9 +2150,10 @@ static int instnorm_np(const kk_tensor* out, const kk_tensor* x, int64_t rows, i
 // 1 + sin(2 a y) >= 0), so y at those two points bounds the row and the
 // extremes over all rows give the quantiser's scale and zero point.  Where
 // rounding could break that (the snake: sin's last bit), the quantising pass
-// checks every y against the bounds and, if one falls outside, flags it;
-// three more launches that do nothing unless flagged then take the exact
-// (min, max) of y, the scale and zero point again, and the bytes again.
+// checks every y against the bounds and, if one falls outside, flags it,
+// and each of its blocks leaves the exact (min, max) of its y; two more
+// launches that do nothing unless flagged then fold those partials into
+// the scale and zero point again and write the bytes again.
 // A value per InstanceNormQuant call for its out-of-bounds flag, never 0
 // (wraps after 2^31 - 1 calls).
 static int next_epoch() {
@@ -2219,12 +2184,14 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   // y is monotonic in x with exact floats: no snake, and a LeakyRelu slope >= 0
   const bool exact_bounds = !af.snake_a && (!af.leaky || af.alpha >= 0.0f);
   const int64_t nblk = long_rows ? ceil_div(T, kNpBlock) : 0;
-  const int64_t nmm = long_rows && !exact_bounds ? std::max(rows, rows * gx) : rows;
-  if (nmm > 0x7fffffff) return set_error(KK_E_UNSUPPORTED, "instance norm: too many partials");
+  // the quantising pass's per-block (min, max) of y, kept for the fallback
+  const int64_t nbmm = long_rows && !exact_bounds ? rows * gx : 0;
+  if (nbmm > 0x7fffffff) return set_error(KK_E_UNSUPPORTED, "instance norm: too many partials");
   auto up = [](int64_t b) { return ceil_div(b, 256) * 256; };
-  const int64_t o_stats = 0, o_mm = up(8 * rows), o_par = o_mm + up(8 * nmm);
+  const int64_t o_stats = 0, o_mm = up(8 * rows), o_par = o_mm + up(8 * rows);
   const int64_t o_part = o_par + 256, o_xmm = o_part + up(4 * rows * nblk + 4);
-  const int64_t o_flag = o_xmm + up(8 * rows * nblk + 8), total = o_flag + 256;
+  const int64_t o_flag = o_xmm + up(8 * rows * nblk + 8), o_bmm = o_flag + 256;
+  const int64_t total = o_bmm + up(8 * nbmm);
   void* ws = nullptr;
   KK_TRY(kk_alloc(static_cast<size_t>(total), &ws));
   char* base = static_cast<char*>(ws);
@@ -2234,24 +2201,24 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   float* part = reinterpret_cast<float*>(base + o_part);
   float2* xmm = reinterpret_cast<float2*>(base + o_xmm);
   int* flag = long_rows && !exact_bounds ? reinterpret_cast<int*>(base + o_flag) : nullptr;
+  float2* bmm = flag ? reinterpret_cast<float2*>(base + o_bmm) : nullptr;
   float* ysp = static_cast<float*>(y_scale->data);
   uint8_t* yzp = static_cast<uint8_t*>(y_zp->data);
   const dim3 qgrid(static_cast<unsigned>(gx), static_cast<unsigned>(rows));
-  // the fallback launches (rarely flagged) take about 2048 blocks, so that
-  // an unflagged one ends at once; their loops stride over the rows
+  // the fallback quantising launch (rarely flagged) takes about 2048
+  // blocks, so that an unflagged one ends at once; its loops stride over
+  // the rows
   const int64_t fgx = std::min<int64_t>(gx, std::max<int64_t>(1, ceil_div(2048, rows)));
   const dim3 fgrid(static_cast<unsigned>(fgx), static_cast<unsigned>(rows));
-  // Up to 2048 rows every quantising block folds the (min, max) partials
-  // itself (rows, or rows * fgx < 4096 on the fallback); beyond, a dql_fold
-  // launch folds them into params.
+  // Up to 2048 rows every quantising block folds the rows' (min, max)
+  // partials itself; beyond, a dql_fold launch folds them into params.
   const bool fold_in = rows <= 2048;
   const int epoch = next_epoch();
-  auto quant = [&](const int* only_if, int* check, int64_t npart) {
+  auto quant = [&](const int* only_if, int* check, const float2* fold) {
     KK_LAUNCH(instnorm_quant, only_if ? fgrid : qgrid, dim3(kRowBlock), 0, st,
                        static_cast<uint8_t*>(q->data), xp, static_cast<const float2*>(stats),
-                       static_cast<const float2*>(params),
-                       fold_in ? static_cast<const float2*>(mm) : nullptr, static_cast<int>(npart),
-                       ysp, yzp, C, T, af, vec ? 1 : 0, only_if, check, epoch);
+                       static_cast<const float2*>(params), fold, static_cast<int>(rows), ysp,
+                       yzp, C, T, af, vec ? 1 : 0, only_if, check, epoch, check ? bmm : nullptr);
     return check_launch("instnorm_quant");
   };
   int rc = KK_OK;
@@ -2277,15 +2244,11 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   // with this call's epoch instead)
   if (rc == KK_OK && !fold_in)
     rc = launch_dql_fold(mm, static_cast<int>(rows), params, ysp, yzp, nullptr, flag);
-  if (rc == KK_OK) rc = quant(nullptr, flag, rows);
-  if (rc == KK_OK && flag) {  // only if a y fell outside the bounds
-    KK_LAUNCH(instnorm_minmax, fgrid, dim3(kRowBlock), 0, st, mm, xp,
-                       static_cast<const float2*>(stats), C, T, af, vec ? 1 : 0,
-                       static_cast<const int*>(flag), epoch);
-    rc = check_launch("instnorm_minmax");
-    if (rc == KK_OK && !fold_in)
-      rc = launch_dql_fold(mm, static_cast<int>(rows * fgx), params, ysp, yzp, flag, nullptr);
-    if (rc == KK_OK) rc = quant(flag, nullptr, rows * fgx);
+  if (rc == KK_OK) rc = quant(nullptr, flag, fold_in ? mm : nullptr);
+  if (rc == KK_OK && flag) {  // only if a y fell outside the bounds: the
+    // exact (min, max) from that pass's block partials, and the bytes again
+    rc = launch_dql_fold(bmm, static_cast<int>(nbmm), params, ysp, yzp, flag, nullptr, epoch);
+    if (rc == KK_OK) rc = quant(flag, nullptr, nullptr);
   }
   kk_free(ws);  // stream order keeps it alive for the kernels above
   return rc;
