@@ -725,6 +725,18 @@ def test_instance_norm_quant_with_leaf_sums(gpu, kind):
     other = y.astype(np.float32)  # same values, another buffer
     with pytest.raises(gpu._lib.KKError, match="not formed from x"):
         gpu.ops.instance_norm_quant(other, g, b, eps=1e-5, leaves=leaves, **args)
+    # freeing x forgets its leaf sums: a tensor that the pool hands the same
+    # address next is refused with them
+    addr = y.ptr
+    del y, got, want
+    gpu.sync()
+    again = [gpu.ops.conv_integer_scaled_qbias(x, w, xz, wz, bias, sa, sw, pads=(1, 1),
+                                               packed=packed) for _ in range(4)]
+    reused = [t for t in again if t.ptr == addr]
+    assert reused, "the pool did not hand out the freed address again"
+    for t in reused:
+        with pytest.raises(gpu._lib.KKError, match="not formed from x"):
+            gpu.ops.instance_norm_quant(t, g, b, eps=1e-5, leaves=leaves, **args)
 
 
 def test_conv_packed_refuses_another_weight(gpu):
