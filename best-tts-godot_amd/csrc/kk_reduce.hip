@@ -2214,10 +2214,10 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   // partials itself; beyond, a dql_fold launch folds them into params.
   const bool fold_in = rows <= 2048;
   const int epoch = next_epoch();
-  auto quant = [&](const int* only_if, int* check, const float2* fold) {
+  auto quant = [&](const int* only_if, int* check, const float2* fold, int64_t npart) {
     KK_LAUNCH(instnorm_quant, only_if ? fgrid : qgrid, dim3(kRowBlock), 0, st,
                        static_cast<uint8_t*>(q->data), xp, static_cast<const float2*>(stats),
-                       static_cast<const float2*>(params), fold, static_cast<int>(rows), ysp,
+                       static_cast<const float2*>(params), fold, static_cast<int>(npart), ysp,
                        yzp, C, T, af, vec ? 1 : 0, only_if, check, epoch, check ? bmm : nullptr);
     return check_launch("instnorm_quant");
   };
@@ -2244,11 +2244,18 @@ static int instnorm_quant_run(const kk_tensor* q, const kk_tensor* y_scale, cons
   // with this call's epoch instead)
   if (rc == KK_OK && !fold_in)
     rc = launch_dql_fold(mm, static_cast<int>(rows), params, ysp, yzp, nullptr, flag);
-  if (rc == KK_OK) rc = quant(nullptr, flag, fold_in ? mm : nullptr);
+  if (rc == KK_OK) rc = quant(nullptr, flag, fold_in ? mm : nullptr, rows);
   if (rc == KK_OK && flag) {  // only if a y fell outside the bounds: the
-    // exact (min, max) from that pass's block partials, and the bytes again
-    rc = launch_dql_fold(bmm, static_cast<int>(nbmm), params, ysp, yzp, flag, nullptr, epoch);
-    if (rc == KK_OK) rc = quant(flag, nullptr, nullptr);
+    // exact (min, max) from that pass's block partials, and the bytes again;
+    // up to 16384 partials (the 128-id graph's [1,128,405840]: 6400) every
+    // block of the second quantising pass folds them itself, so an
+    // unflagged call adds one launch that ends at once, not two
+    if (nbmm <= 16384) {
+      rc = quant(flag, nullptr, bmm, nbmm);
+    } else {
+      rc = launch_dql_fold(bmm, static_cast<int>(nbmm), params, ysp, yzp, flag, nullptr, epoch);
+      if (rc == KK_OK) rc = quant(flag, nullptr, nullptr, rows);
+    }
   }
   kk_free(ws);  // stream order keeps it alive for the kernels above
   return rc;

@@ -396,7 +396,10 @@ def test_instance_norm_snake_chain(gpu, oracle, C, T, affine):
                                               # folds the rows' partials; beyond, a fold
                                               # launch does (with the fallback, both ways)
                                               (2048, 64, 5.0, None), (2100, 40, 5.0, None),
-                                              (2100, 40, None, 0.2)])
+                                              (2100, 40, None, 0.2),
+                                              # the fallback's partials (rows x 4 blocks)
+                                              # beyond one block's fold: a fold launch
+                                              (4200, 24580, 5.0, None)])
 def test_instance_norm_quant_matches_unfused_device_path(gpu, C, T, rc_mul, leaky):
     """InstanceNormQuant gives the same bytes, scale and zero point as the
     device's own unfused chain: the float result stored, then
